@@ -1,0 +1,133 @@
+/*
+ * stacr_amd.h -- C ABI of the MI355X-native STAC-R save / weight-gradient path.
+ *
+ * Plain C types only: device pointers are `void*`, sizes are int64_t, the HIP stream is passed
+ * as `void*` (a hipStream_t, or NULL for the default stream).  The library never allocates:
+ * every output and the workspace are supplied by the caller (query the workspace size first).
+ * Every entry point returns STACR_OK or an error code; stacr_last_error() gives a thread-local
+ * message for the last failure on the calling thread.  Launches are asynchronous on `stream`;
+ * no entry point synchronises the device or reads device memory back to the host.
+ *
+ * Reference interfaces replaced (Manar-Hamed/STAC-R, stacr 0.2.0):
+ *   stacr_residual_plan      k rules of stacr/layers.py:25-27,33,51-53
+ *   stacr_save               STACRFunction.forward compression, stacr/layers.py:135-148
+ *                            (coeff = X.Q, _select_residual :16-41/:44-102, quantize_values
+ *                            stacr/quant.py:49-65)
+ *   stacr_weight_grad        STACRFunction.backward grad_weight / grad_bias,
+ *                            stacr/layers.py:172-198
+ */
+#ifndef STACR_AMD_H
+#define STACR_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define STACR_ABI_VERSION 1
+
+/* element types of activations, gradients, coefficients, basis and outputs */
+#define STACR_DTYPE_F32 0
+#define STACR_DTYPE_BF16 1
+#define STACR_DTYPE_F16 2
+
+/* residual selection modes (stacr/layers.py:13; "topk" is an alias of "chunk_topk") */
+#define STACR_MODE_CHUNK_TOPK 0
+#define STACR_MODE_GLOBAL_TOPK 1
+
+/* status codes */
+#define STACR_OK 0
+#define STACR_ERR_INVALID 1     /* bad argument (shape, dtype, null pointer, size) */
+#define STACR_ERR_UNSUPPORTED 2 /* valid for the reference but outside this library's limits */
+#define STACR_ERR_WORKSPACE 3   /* workspace smaller than the queried size */
+#define STACR_ERR_HIP 4         /* a HIP runtime call failed */
+
+/* Largest padded rank the kernels are built for (ranks 1..32 are accepted). */
+#define STACR_MAX_RANK 32
+
+int stacr_abi_version(void);
+
+/* Thread-local description of the last error returned on this thread ("" if none). */
+const char *stacr_last_error(void);
+
+/*
+ * Residual entry counts for a (rows x feats) activation (stacr/layers.py:25-27,33,51-53):
+ *   *k_total  = round_half_even(budget * rows * feats)   (0 means "no residual is saved")
+ *   *k_saved  = number of entries stacr_save writes: k_total for global_topk; for chunk_topk the
+ *               sum over chunks of max(1, min(n_c, round(budget * n_c))), trimmed to k_total.
+ * Also reports whether flat indices need int64 (*index_bytes = 8 when rows*feats >= 2^31-1,
+ * stacr/layers.py:41,54).
+ */
+int stacr_residual_plan(int64_t rows, int64_t feats, int mode, double budget, int64_t chunk_rows,
+                        int64_t *k_total, int64_t *k_saved, int *index_bytes);
+
+/* Workspace bytes stacr_save needs for this problem. */
+int stacr_save_workspace_bytes(int64_t rows, int64_t feats, int rank, int dtype, int mode,
+                               double budget, int64_t chunk_rows, int bits, size_t *bytes);
+
+/*
+ * One streaming save of the activation X (rows x feats, row-major, `dtype`):
+ *   coeff (rows x rank, dtype)   = X . Q, fp32 accumulation, rounded once to dtype
+ *   residual r = X - coeff . Q^T (fp32), selected by |r| per chunk_topk / global_topk with the
+ *   reference's k rules; ties at the cut go to the lowest flat index; output is in ascending
+ *   flat-index order:
+ *   idx   (k_saved, int32 or int64 per index_bytes) = row * feats + col
+ *   data  bits 8: int8 q; bits 4: uint8 packed nibbles (ceil(k/2) bytes, even entry low);
+ *         bits 0: values in `dtype`
+ *   scale (1 fp32) = max(amax / qmax, FLT_MIN), or 1 for bits 0
+ * q is the basis already cast to `dtype` (feats x rank, row-major), as the reference saves it.
+ * budget <= 0 or k_total == 0: only coeff is written (idx/data/scale may be NULL).
+ * Requires rows*feats < 2^32 and 1 <= rank <= STACR_MAX_RANK.
+ */
+int stacr_save(const void *x, const void *q, int dtype, int64_t rows, int64_t feats, int rank,
+               int mode, double budget, int64_t chunk_rows, int bits, void *coeff, void *idx,
+               int index_bytes, void *data, float *scale, void *workspace,
+               size_t workspace_bytes, void *stream);
+
+/*
+ * Selection and quantization only, on caller-supplied coefficients (rows x rank, dtype):
+ * the reference's _select_residual(x, coeff, basis, ...) followed by quantize_values
+ * (stacr/layers.py:44-102,148).  Same residual arithmetic, rules and outputs as stacr_save;
+ * use stacr_save_workspace_bytes for the workspace size.
+ */
+int stacr_select_residual(const void *x, const void *coeff, const void *q, int dtype, int64_t rows,
+                          int64_t feats, int rank, int mode, double budget, int64_t chunk_rows,
+                          int bits, void *idx, int index_bytes, void *data, float *scale,
+                          void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * quantize_values (stacr/quant.py:49-65) for bits 4 or 8 on n values of `dtype`:
+ * scale = max(max|v| / qmax, FLT_MIN) (fp32), q = round_half_even(v / scale) clamped to
+ * [-qmax-1, qmax]; bits 8 writes n int8, bits 4 writes ceil(n/2) packed bytes (even entry in the
+ * low nibble).  Needs 4 workspace bytes.  (bits 0 is a passthrough and needs no kernel.)
+ */
+int stacr_quantize_values(const void *values, int dtype, int64_t n, int bits, void *data, float *scale,
+                          void *workspace, size_t workspace_bytes, void *stream);
+
+/* Workspace bytes stacr_weight_grad needs for this problem. */
+int stacr_weight_grad_workspace_bytes(int64_t rows, int64_t d_out, int64_t d_in, int rank,
+                                      int64_t nnz, size_t *bytes);
+
+/*
+ * Weight gradient from the saved factors (stacr/layers.py:172-198):
+ *   dW = (G^T . coeff) . Q^T + G^T . R_s        fp32 accumulation, rounded once to dw_dtype
+ *   dbias = sum over rows of G                  (optional; dbias may be NULL)
+ * g: rows x d_out (dtype); coeff: rows x rank (dtype); q: d_in x rank (dtype).
+ * Sparse residual: idx (nnz, ascending flat indices row*d_in+col, int32 or int64 per
+ * index_bytes), data/scale/bits as written by stacr_save; for bits 0 `data` holds values of
+ * val_dtype.  nnz may be 0 (low-rank only; idx/data/scale may then be NULL).
+ * transposed = 0: dW is d_out x d_in (nn.Linear); 1: d_in x d_out (Transformers Conv1D).
+ */
+int stacr_weight_grad(const void *g, int dtype, int64_t rows, int64_t d_out, const void *coeff,
+                      const void *q, int64_t d_in, int rank, const void *idx, int index_bytes,
+                      const void *data, const float *scale, int bits, int val_dtype, int64_t nnz,
+                      int transposed, void *dw, int dw_dtype, void *dbias, int dbias_dtype,
+                      void *workspace, size_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STACR_AMD_H */

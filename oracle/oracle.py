@@ -1,0 +1,202 @@
+"""Python face of the CPU oracle (test infrastructure only).
+
+Only tests/, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import this
+module.  It is the checker and the timed CPU baseline, never part of the product path.
+
+The integer/byte work (k rules, exact selection, quantization, nibble packing) and the fp64
+weight gradient live in ``stacr_oracle.c`` (each function there cites the reference line it
+restates).  This module adds the numpy pieces: dtype rounding, the fp64 projection
+(stacr/layers.py:135-137), dequantization (stacr/quant.py:17-21,40-46) and a composed save.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
+
+MODE_CHUNK, MODE_GLOBAL = 0, 1
+MODES = {"chunk_topk": MODE_CHUNK, "topk": MODE_CHUNK, "global_topk": MODE_GLOBAL}
+
+_lib = None
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        i64, f64, i32 = ctypes.c_int64, ctypes.c_double, ctypes.c_int
+        P = ctypes.c_void_p
+        L.orc_py_round.argtypes, L.orc_py_round.restype = [f64], i64
+        L.orc_chunk_k.argtypes, L.orc_chunk_k.restype = [i64, f64], i64
+        L.orc_residual_plan.argtypes = [i64, i64, i32, f64, i64, P, P]
+        L.orc_residual_f32.argtypes = [P, P, P, i64, i64, i32, P]
+        L.orc_select.argtypes, L.orc_select.restype = [P, i64, i64, i32, f64, i64, P, P], i64
+        L.orc_sorted_keys.argtypes = [P, i64, P]
+        L.orc_quantize.argtypes = [P, i64, i32, P, P]
+        L.orc_pack_int4.argtypes = [P, i64, P]
+        L.orc_weight_grad.argtypes = [P, i64, i64, P, P, i64, i32, P, P, i64, P, P]
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# ---------------------------------------------------------------- k rules
+def py_round(v: float) -> int:
+    return int(lib().orc_py_round(float(v)))
+
+
+def chunk_k(n: int, budget: float) -> int:
+    return int(lib().orc_chunk_k(int(n), float(budget)))
+
+
+def residual_plan(rows: int, feats: int, mode: str, budget: float, chunk_rows: int):
+    """(k_total, sum of per-chunk k) following stacr/layers.py:16-41,44-54."""
+    kt, ks = ctypes.c_int64(), ctypes.c_int64()
+    lib().orc_residual_plan(int(rows), int(feats), MODES[mode], float(budget), int(chunk_rows),
+                            ctypes.byref(kt), ctypes.byref(ks))
+    return int(kt.value), int(ks.value)
+
+
+# ---------------------------------------------------------------- dtype helpers
+def round_to(a: np.ndarray, dtype: str) -> np.ndarray:
+    """Round fp32 values to bf16 / fp16 (nearest-even) and return them as fp32."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    if dtype in ("f32", "float32"):
+        return a.copy()
+    if dtype in ("f16", "float16"):
+        return a.astype(np.float16).astype(np.float32)
+    if dtype in ("bf16", "bfloat16"):
+        u = a.view(np.uint32).astype(np.uint64)
+        nan = np.isnan(a)
+        r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+        out = r.view(np.float32).copy()
+        out[nan] = np.nan
+        return out
+    raise ValueError(dtype)
+
+
+def project_f64(x: np.ndarray, q: np.ndarray) -> np.ndarray:
+    """C = X Q in fp64 (stacr/layers.py:137 before its final rounding)."""
+    return np.asarray(x, np.float64) @ np.asarray(q, np.float64)
+
+
+# ---------------------------------------------------------------- residual + selection
+def residual_f32(x: np.ndarray, c: np.ndarray, q: np.ndarray) -> np.ndarray:
+    x, c, q = _c(x, np.float32), _c(c, np.float32), _c(q, np.float32)
+    rows, d = x.shape
+    r = q.shape[1]
+    out = np.empty_like(x)
+    lib().orc_residual_f32(_ptr(x), _ptr(c), _ptr(q), rows, d, r, _ptr(out))
+    return out
+
+
+def select(resid: np.ndarray, mode: str, budget: float, chunk_rows: int):
+    """Exact selection with the lowest-index tie rule; (idx int64 ascending, values fp32)."""
+    resid = _c(resid, np.float32)
+    rows, d = resid.shape
+    if rows * d >= 2**32:
+        raise ValueError("oracle selection supports fewer than 2^32 elements")
+    kt, ks = residual_plan(rows, d, mode, budget, chunk_rows)
+    idx = np.empty(max(ks, 1), np.int64)
+    val = np.empty(max(ks, 1), np.float32)
+    n = lib().orc_select(_ptr(resid), rows, d, MODES[mode], float(budget), int(chunk_rows),
+                         _ptr(idx), _ptr(val))
+    return idx[:n].copy(), val[:n].copy()
+
+
+def sorted_keys(resid: np.ndarray) -> np.ndarray:
+    flat = _c(resid, np.float32).reshape(-1)
+    out = np.empty(flat.size, np.uint64)
+    lib().orc_sorted_keys(_ptr(flat), flat.size, _ptr(out))
+    return out
+
+
+# ---------------------------------------------------------------- quantization
+def quantize(vals: np.ndarray, bits: int):
+    """stacr/quant.py:49-65 -> (q int8 before packing, scale fp32)."""
+    vals = _c(vals, np.float32).reshape(-1)
+    q = np.zeros(vals.size, np.int8)
+    scale = np.zeros(1, np.float32)
+    lib().orc_quantize(_ptr(vals), vals.size, int(bits), _ptr(q), _ptr(scale))
+    return q, np.float32(scale[0])
+
+
+def pack_int4(q: np.ndarray) -> np.ndarray:
+    q = _c(q, np.int8).reshape(-1)
+    out = np.zeros((q.size + 1) // 2, np.uint8)
+    lib().orc_pack_int4(_ptr(q), q.size, _ptr(out))
+    return out
+
+
+def unpack_int4(packed: np.ndarray, length: int) -> np.ndarray:
+    """stacr/quant.py:40-46."""
+    p = np.asarray(packed, np.uint8)
+    lo = (p & 0x0F).astype(np.int8)
+    hi = ((p >> 4) & 0x0F).astype(np.int8)
+    lo = np.where(lo > 7, lo - 16, lo).astype(np.int8)
+    hi = np.where(hi > 7, hi - 16, hi).astype(np.int8)
+    return np.stack([lo, hi], axis=1).reshape(-1)[:length]
+
+
+def dequantize(data: np.ndarray, scale: float, bits: int, length: int) -> np.ndarray:
+    """stacr/quant.py:17-21 with dtype fp32: data.to(f32) * scale.to(f32)."""
+    if bits == 4:
+        data = unpack_int4(data, length)
+    if bits == 0:
+        return np.asarray(data, np.float32).copy()
+    return (np.asarray(data, np.float32) * np.float32(scale)).astype(np.float32)
+
+
+# ---------------------------------------------------------------- weight gradient
+def weight_grad(g, c, q, idx, vals, d_in: int):
+    """fp64 dW (d_out x d_in) and dbias following stacr/layers.py:172-198."""
+    g, c, q = _c(g, np.float32), _c(c, np.float32), _c(q, np.float32)
+    idx, vals = _c(idx, np.int64).reshape(-1), _c(vals, np.float32).reshape(-1)
+    n, d_out = g.shape
+    r = c.shape[1]
+    dw = np.empty((d_out, d_in), np.float64)
+    db = np.empty(d_out, np.float64)
+    lib().orc_weight_grad(_ptr(g), n, d_out, _ptr(c), _ptr(q), d_in, r, _ptr(idx), _ptr(vals),
+                          idx.size, _ptr(dw), _ptr(db))
+    return dw, db
+
+
+# ---------------------------------------------------------------- composed save (CPU baseline)
+def save(x: np.ndarray, q: np.ndarray, dtype: str, mode: str, budget: float, chunk_rows: int,
+         bits: int, coeff: np.ndarray | None = None):
+    """The whole save step on the CPU, in the HIP path's arithmetic.
+
+    ``coeff`` (already rounded to ``dtype``) may be supplied so that selection is compared on the
+    identical residual; otherwise it is the fp64 projection rounded to ``dtype``.
+    Returns (coeff, idx, q_or_values, scale).
+    """
+    xr = round_to(x, dtype)
+    qr = round_to(q, dtype)
+    if coeff is None:
+        coeff = round_to(project_f64(xr, qr).astype(np.float32), dtype)
+    resid = residual_f32(xr, coeff, qr)
+    idx, val = select(resid, mode, budget, chunk_rows)
+    val = round_to(val, dtype)
+    if bits == 0:
+        return coeff, idx, val, np.float32(1.0)
+    qv, scale = quantize(val, bits)
+    return coeff, idx, (pack_int4(qv) if bits == 4 else qv), scale

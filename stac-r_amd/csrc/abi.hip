@@ -1,0 +1,269 @@
+// C ABI entry points: argument validation, the reference's k rules, error reporting.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "internal.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+// Python's round() of a double: nearest integer, ties to even (stacr/layers.py:25,33,51).
+int64_t py_round(double v) { return (int64_t)nearbyint(v); }
+
+// stacr/layers.py:33: k = max(1, min(n, round(budget * n)))
+int64_t chunk_k(int64_t n, double budget)
+{
+    int64_t k = py_round(budget * (double)n);
+    if (k > n) k = n;
+    return k < 1 ? 1 : k;
+}
+
+bool valid_dtype(int dt) { return dt == STACR_DTYPE_F32 || dt == STACR_DTYPE_BF16 || dt == STACR_DTYPE_F16; }
+
+struct KPlan {
+    int64_t k_total = 0, k_full = 0, k_last = 0, k_sum = 0, k_saved = 0, chunk_rows = 1;
+};
+
+// k rules: stacr/layers.py:25-27 (chunk_topk total), :33 (per chunk), :38-40 (trim), :51-53 (global)
+int plan_k(int64_t rows, int64_t feats, int mode, double budget, int64_t chunk_rows, KPlan *p)
+{
+    if (rows < 0 || feats < 0) return stacr_fail(STACR_ERR_INVALID, "negative shape (%lld x %lld)", (long long)rows, (long long)feats);
+    if (mode != STACR_MODE_CHUNK_TOPK && mode != STACR_MODE_GLOBAL_TOPK)
+        return stacr_fail(STACR_ERR_INVALID, "unknown residual mode %d", mode);
+    if (!(budget >= 0.0 && budget <= 1.0)) return stacr_fail(STACR_ERR_INVALID, "budget %g outside [0, 1]", budget);
+    if (mode == STACR_MODE_CHUNK_TOPK && chunk_rows < 1)
+        return stacr_fail(STACR_ERR_INVALID, "chunk_rows must be positive");
+    *p = KPlan{};
+    const int64_t total = rows * feats;
+    if (total == 0 || budget <= 0.0) return STACR_OK;
+    p->k_total = py_round(budget * (double)total);
+    if (p->k_total <= 0) { p->k_total = 0; return STACR_OK; }
+    if (mode == STACR_MODE_GLOBAL_TOPK) {
+        p->chunk_rows = rows;
+        p->k_full = p->k_last = p->k_sum = p->k_saved = p->k_total;
+        return STACR_OK;
+    }
+    const int64_t cr = chunk_rows < rows ? chunk_rows : rows;
+    const int64_t n_chunks = (rows + cr - 1) / cr;
+    const int64_t last_rows = rows - (n_chunks - 1) * cr;
+    p->chunk_rows = cr;
+    p->k_full = chunk_k(cr * feats, budget);
+    p->k_last = chunk_k(last_rows * feats, budget);
+    p->k_sum = (n_chunks - 1) * p->k_full + p->k_last;
+    p->k_saved = p->k_sum > p->k_total ? p->k_total : p->k_sum;
+    return STACR_OK;
+}
+
+}  // namespace
+
+int stacr_fail(int code, const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int stacr_hip_check(hipError_t err, const char *what)
+{
+    if (err == hipSuccess) return STACR_OK;
+    return stacr_fail(STACR_ERR_HIP, "%s: %s", what, hipGetErrorString(err));
+}
+
+extern "C" {
+
+int stacr_abi_version(void) { return STACR_ABI_VERSION; }
+
+const char *stacr_last_error(void) { return g_err; }
+
+int stacr_residual_plan(int64_t rows, int64_t feats, int mode, double budget, int64_t chunk_rows,
+                        int64_t *k_total, int64_t *k_saved, int *index_bytes)
+{
+    KPlan p;
+    const int rc = plan_k(rows, feats, mode, budget, chunk_rows, &p);
+    if (rc) return rc;
+    if (k_total) *k_total = p.k_total;
+    if (k_saved) *k_saved = p.k_saved;
+    if (index_bytes) *index_bytes = rows * feats < 2147483647LL ? 4 : 8;  // stacr/layers.py:41
+    return STACR_OK;
+}
+
+static int fill_save_args(int64_t rows, int64_t feats, int rank, int dtype, int mode, double budget,
+                          int64_t chunk_rows, int bits, StacrSaveArgs *a)
+{
+    if (!valid_dtype(dtype)) return stacr_fail(STACR_ERR_INVALID, "unsupported activation dtype code %d", dtype);
+    if (rank < 1 || rank > STACR_MAX_RANK)
+        return stacr_fail(STACR_ERR_UNSUPPORTED, "rank %d outside 1..%d", rank, STACR_MAX_RANK);
+    if (bits != 0 && bits != 4 && bits != 8) return stacr_fail(STACR_ERR_INVALID, "residual_bits must be 0, 4, or 8");
+    KPlan p;
+    const int rc = plan_k(rows, feats, mode, budget, chunk_rows, &p);
+    if (rc) return rc;
+    if ((uint64_t)rows * (uint64_t)feats >= (1ull << 32))
+        return stacr_fail(STACR_ERR_UNSUPPORTED, "rows*feats = %lld exceeds 2^32 elements",
+                          (long long)(rows * feats));
+    *a = StacrSaveArgs{};
+    a->dtype = dtype;
+    a->rows = rows;
+    a->feats = feats;
+    a->rank = rank;
+    a->mode = mode;
+    a->chunk_rows = p.chunk_rows;
+    a->k_total = p.k_total;
+    a->k_full = p.k_full;
+    a->k_last = p.k_last;
+    a->k_sum = p.k_sum;
+    a->bits = bits;
+    return STACR_OK;
+}
+
+int stacr_save_workspace_bytes(int64_t rows, int64_t feats, int rank, int dtype, int mode, double budget,
+                               int64_t chunk_rows, int bits, size_t *bytes)
+{
+    if (!bytes) return stacr_fail(STACR_ERR_INVALID, "bytes is NULL");
+    StacrSaveArgs a;
+    const int rc = fill_save_args(rows, feats, rank, dtype, mode, budget, chunk_rows, bits, &a);
+    if (rc) return rc;
+    *bytes = rows * feats ? stacr_save_ws_layout(a, nullptr) : 0;
+    return STACR_OK;
+}
+
+int stacr_save(const void *x, const void *q, int dtype, int64_t rows, int64_t feats, int rank, int mode,
+               double budget, int64_t chunk_rows, int bits, void *coeff, void *idx, int index_bytes, void *data,
+               float *scale, void *workspace, size_t workspace_bytes, void *stream)
+{
+    StacrSaveArgs a;
+    int rc = fill_save_args(rows, feats, rank, dtype, mode, budget, chunk_rows, bits, &a);
+    if (rc) return rc;
+    if (rows * feats == 0) return STACR_OK;
+    if (!x || !q || !coeff) return stacr_fail(STACR_ERR_INVALID, "stacr_save: x, q and coeff must be non-NULL");
+    if (a.k_total > 0) {
+        if (!idx || !data || !scale) return stacr_fail(STACR_ERR_INVALID, "stacr_save: idx, data, scale must be non-NULL");
+        const int want = rows * feats < 2147483647LL ? 4 : 8;
+        if (index_bytes != want)
+            return stacr_fail(STACR_ERR_INVALID, "stacr_save: index_bytes must be %d for %lld elements", want,
+                              (long long)(rows * feats));
+    }
+    if (!workspace) return stacr_fail(STACR_ERR_INVALID, "stacr_save: workspace is NULL");
+    a.x = x;
+    a.q = q;
+    a.coeff = coeff;
+    a.idx = idx;
+    a.index_bytes = index_bytes;
+    a.data = data;
+    a.scale = scale;
+    a.workspace = workspace;
+    a.workspace_bytes = workspace_bytes;
+    a.stream = static_cast<hipStream_t>(stream);
+    return stacr_save_launch(a);
+}
+
+int stacr_select_residual(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t feats,
+                          int rank, int mode, double budget, int64_t chunk_rows, int bits, void *idx,
+                          int index_bytes, void *data, float *scale, void *workspace, size_t workspace_bytes,
+                          void *stream)
+{
+    StacrSaveArgs a;
+    int rc = fill_save_args(rows, feats, rank, dtype, mode, budget, chunk_rows, bits, &a);
+    if (rc) return rc;
+    if (rows * feats == 0 || a.k_total == 0) return STACR_OK;
+    if (!x || !q || !coeff || !idx || !data || !scale || !workspace)
+        return stacr_fail(STACR_ERR_INVALID, "stacr_select_residual: NULL pointer argument");
+    const int want = rows * feats < 2147483647LL ? 4 : 8;
+    if (index_bytes != want)
+        return stacr_fail(STACR_ERR_INVALID, "stacr_select_residual: index_bytes must be %d", want);
+    a.x = x;
+    a.q = q;
+    a.coeff_in = coeff;
+    a.coeff = nullptr;
+    a.idx = idx;
+    a.index_bytes = index_bytes;
+    a.data = data;
+    a.scale = scale;
+    a.workspace = workspace;
+    a.workspace_bytes = workspace_bytes;
+    a.stream = static_cast<hipStream_t>(stream);
+    return stacr_save_launch(a);
+}
+
+int stacr_quantize_values(const void *values, int dtype, int64_t n, int bits, void *data, float *scale,
+                          void *workspace, size_t workspace_bytes, void *stream)
+{
+    if (!valid_dtype(dtype)) return stacr_fail(STACR_ERR_INVALID, "unsupported value dtype code %d", dtype);
+    if (bits != 4 && bits != 8) return stacr_fail(STACR_ERR_INVALID, "stacr_quantize_values: bits must be 4 or 8");
+    if (n < 0) return stacr_fail(STACR_ERR_INVALID, "negative length");
+    if (n == 0) return STACR_OK;
+    if (!values || !data || !scale || !workspace) return stacr_fail(STACR_ERR_INVALID, "NULL pointer argument");
+    if (workspace_bytes < 4) return stacr_fail(STACR_ERR_WORKSPACE, "stacr_quantize_values needs 4 workspace bytes");
+    return stacr_quantize_launch(values, dtype, n, bits, data, scale, workspace, static_cast<hipStream_t>(stream));
+}
+
+static int fill_grad_args(int64_t rows, int64_t d_out, int64_t d_in, int rank, int64_t nnz, StacrGradArgs *a)
+{
+    if (rows < 0 || d_out < 0 || d_in < 0 || nnz < 0) return stacr_fail(STACR_ERR_INVALID, "negative size");
+    if (rank < 1 || rank > STACR_MAX_RANK)
+        return stacr_fail(STACR_ERR_UNSUPPORTED, "rank %d outside 1..%d", rank, STACR_MAX_RANK);
+    if (nnz > rows * d_in) return stacr_fail(STACR_ERR_INVALID, "nnz exceeds rows*d_in");
+    if (nnz >= (1ll << 31)) return stacr_fail(STACR_ERR_UNSUPPORTED, "nnz %lld >= 2^31", (long long)nnz);
+    *a = StacrGradArgs{};
+    a->rows = rows;
+    a->d_out = d_out;
+    a->d_in = d_in;
+    a->rank = rank;
+    a->nnz = nnz;
+    return STACR_OK;
+}
+
+int stacr_weight_grad_workspace_bytes(int64_t rows, int64_t d_out, int64_t d_in, int rank, int64_t nnz, size_t *bytes)
+{
+    if (!bytes) return stacr_fail(STACR_ERR_INVALID, "bytes is NULL");
+    StacrGradArgs a;
+    const int rc = fill_grad_args(rows, d_out, d_in, rank, nnz, &a);
+    if (rc) return rc;
+    *bytes = stacr_grad_ws_layout(a, nullptr);
+    return STACR_OK;
+}
+
+int stacr_weight_grad(const void *g, int dtype, int64_t rows, int64_t d_out, const void *coeff, const void *q,
+                      int64_t d_in, int rank, const void *idx, int index_bytes, const void *data, const float *scale,
+                      int bits, int val_dtype, int64_t nnz, int transposed, void *dw, int dw_dtype, void *dbias,
+                      int dbias_dtype, void *workspace, size_t workspace_bytes, void *stream)
+{
+    StacrGradArgs a;
+    int rc = fill_grad_args(rows, d_out, d_in, rank, nnz, &a);
+    if (rc) return rc;
+    if (!valid_dtype(dtype) || !valid_dtype(dw_dtype) || (dbias && !valid_dtype(dbias_dtype)))
+        return stacr_fail(STACR_ERR_INVALID, "unsupported dtype code");
+    if (bits != 0 && bits != 4 && bits != 8) return stacr_fail(STACR_ERR_INVALID, "residual_bits must be 0, 4, or 8");
+    if (nnz > 0) {
+        if (!idx || !data || (bits && !scale)) return stacr_fail(STACR_ERR_INVALID, "sparse residual pointers are NULL");
+        if (index_bytes != 4 && index_bytes != 8) return stacr_fail(STACR_ERR_INVALID, "index_bytes must be 4 or 8");
+        if (bits == 0 && !valid_dtype(val_dtype)) return stacr_fail(STACR_ERR_INVALID, "bad value dtype");
+    }
+    if (d_out * d_in == 0) return STACR_OK;
+    if (!dw || !q || (rows > 0 && (!g || !coeff)) || !workspace)
+        return stacr_fail(STACR_ERR_INVALID, "stacr_weight_grad: NULL pointer argument");
+    a.g = g;
+    a.dtype = dtype;
+    a.coeff = coeff;
+    a.q = q;
+    a.idx = idx;
+    a.index_bytes = index_bytes;
+    a.data = data;
+    a.scale = scale;
+    a.bits = bits;
+    a.val_dtype = val_dtype;
+    a.transposed = transposed ? 1 : 0;
+    a.dw = dw;
+    a.dw_dtype = dw_dtype;
+    a.dbias = dbias;
+    a.dbias_dtype = dbias_dtype;
+    a.workspace = workspace;
+    a.workspace_bytes = workspace_bytes;
+    a.stream = static_cast<hipStream_t>(stream);
+    return stacr_grad_launch(a);
+}
+
+}  // extern "C"

@@ -1,0 +1,224 @@
+// Internal device helpers and launcher declarations shared by the HIP translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "stacr_amd.h"
+
+namespace stacr {
+
+// host-side min/max (the HIP headers' min/max are device functions)
+template <typename T> inline T hmin(T a, T b) { return a < b ? a : b; }
+template <typename T> inline T hmax(T a, T b) { return a < b ? b : a; }
+
+constexpr int kBlock = 256;             // threads per workgroup (4 wave64)
+constexpr int kWaves = kBlock / 64;
+constexpr int kBins = 2048;             // histogram bins of the first two radix digits
+// 31-bit magnitude key = fp32 bits of |r|; digits: [30:20] (11 b), [19:9] (11 b), [8:0] (9 b)
+constexpr int kDigitShift[3] = {20, 9, 0};
+constexpr int kDigitBins[3] = {2048, 2048, 512};
+constexpr int kListBlock = 4096;        // list entries per workgroup in the trim pass
+
+// ------------------------------------------------------------------ element types
+__device__ __forceinline__ float bf16_bits_to_f(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ uint32_t f_to_bf16_bits(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;  // quiet NaN
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;                              // nearest-even
+}
+__device__ __forceinline__ float f16_bits_to_f(uint32_t v)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)v);
+}
+__device__ __forceinline__ uint32_t f_to_f16_bits(float f)
+{
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+template <int DT> struct Act;
+template <> struct Act<STACR_DTYPE_F32> {
+    using T = float;
+    static constexpr int kVec = 4;  // elements per 16-byte load
+    static __device__ __forceinline__ float ld(T v) { return v; }
+    static __device__ __forceinline__ T st(float f) { return f; }
+    static __device__ __forceinline__ float rnd(float f) { return f; }
+};
+template <> struct Act<STACR_DTYPE_BF16> {
+    using T = uint16_t;
+    static constexpr int kVec = 8;
+    static __device__ __forceinline__ float ld(T v) { return bf16_bits_to_f(v); }
+    static __device__ __forceinline__ T st(float f) { return (T)f_to_bf16_bits(f); }
+    static __device__ __forceinline__ float rnd(float f) { return bf16_bits_to_f(f_to_bf16_bits(f)); }
+};
+template <> struct Act<STACR_DTYPE_F16> {
+    using T = uint16_t;
+    static constexpr int kVec = 8;
+    static __device__ __forceinline__ float ld(T v) { return f16_bits_to_f(v); }
+    static __device__ __forceinline__ T st(float f) { return (T)f_to_f16_bits(f); }
+    static __device__ __forceinline__ float rnd(float f) { return f16_bits_to_f(f_to_f16_bits(f)); }
+};
+
+// V consecutive elements starting at p, widened to fp32 (16-byte load when V == kVec).
+template <int DT, int V>
+__device__ __forceinline__ void load_vec(const typename Act<DT>::T *__restrict__ p, float (&x)[V])
+{
+    using A = Act<DT>;
+    if constexpr (V == 1) {
+        x[0] = A::ld(p[0]);
+    } else if constexpr (sizeof(typename A::T) == 4) {
+        static_assert(V == 4, "fp32 vector width is 4");
+        const float4 v = *reinterpret_cast<const float4 *>(p);
+        x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+    } else {
+        static_assert(V == 8, "16-bit vector width is 8");
+        const uint4 v = *reinterpret_cast<const uint4 *>(p);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            x[2 * k] = A::ld((typename A::T)(w[k] & 0xffffu));
+            x[2 * k + 1] = A::ld((typename A::T)(w[k] >> 16));
+        }
+    }
+}
+
+__device__ __forceinline__ float load_any(const void *p, int dt, int64_t i)
+{
+    if (dt == STACR_DTYPE_F32) return static_cast<const float *>(p)[i];
+    const uint16_t v = static_cast<const uint16_t *>(p)[i];
+    return dt == STACR_DTYPE_BF16 ? bf16_bits_to_f(v) : f16_bits_to_f(v);
+}
+
+__device__ __forceinline__ void store_any(void *p, int dt, int64_t i, float f)
+{
+    if (dt == STACR_DTYPE_F32) {
+        static_cast<float *>(p)[i] = f;
+    } else {
+        static_cast<uint16_t *>(p)[i] =
+            (uint16_t)(dt == STACR_DTYPE_BF16 ? f_to_bf16_bits(f) : f_to_f16_bits(f));
+    }
+}
+
+// ------------------------------------------------------------------ block primitives
+// Exclusive prefix sum over the 256 threads of a workgroup; *total receives the sum.
+// Every thread must call it (it contains __syncthreads).
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *s_tot, uint32_t *total)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    if (lane == 63) s_tot[wave] = x;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        const uint32_t t = s_tot[w];
+        before += w < wave ? t : 0u;
+        all += t;
+    }
+    __syncthreads();
+    *total = all;
+    return before + x - v;
+}
+
+__device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t *s_tot)
+{
+    uint32_t total;
+    block_exclusive_scan(v, s_tot, &total);
+    return total;
+}
+
+// ------------------------------------------------------------------ save geometry
+// A workgroup owns `rows_per_wg` consecutive rows inside one selection chunk.  Inside it, the
+// 256 threads form rpi = 256 / L row slots of L threads; each thread walks `mv` vectors of V
+// elements per row at columns (m * L + u) * V.  Either rpi == 1 or mv == 1, so visiting the
+// vectors in m-major, thread-minor order enumerates elements in ascending flat index.
+struct SaveGeom {
+    int64_t rows, d;
+    int64_t chunk_rows;     // rows per selection chunk (global_topk: all rows)
+    int64_t n_chunks;
+    int64_t rows_per_wg;
+    int64_t wgs_per_chunk;  // uniform; trailing workgroups of the last chunk may be empty
+    int L, log2L, rpi, mv;
+    int rank;
+};
+
+// Per-chunk selection state after each radix level: prefix of the key found so far and the
+// number of elements still to take from inside that prefix.
+struct SelState {
+    uint32_t prefix;
+    uint32_t need;
+};
+
+struct WgCount {
+    uint32_t gt;  // elements with key > threshold
+    uint32_t eq;  // elements with key == threshold
+};
+
+struct WgOffset {
+    uint32_t off;   // first output position of the workgroup
+    uint32_t take;  // ties (key == threshold) it keeps, lowest flat index first
+};
+
+}  // namespace stacr
+
+// ------------------------------------------------------------------ error reporting
+int stacr_fail(int code, const char *fmt, ...);
+int stacr_hip_check(hipError_t err, const char *what);
+
+// ------------------------------------------------------------------ launchers (save.hip)
+struct StacrSaveArgs {
+    const void *x;
+    const void *q;
+    int dtype;
+    int64_t rows, feats;
+    int rank;
+    int mode;
+    int64_t chunk_rows;  // effective (global_topk: rows)
+    int64_t k_total, k_full, k_last, k_sum;
+    int bits;
+    const void *coeff_in;  // non-NULL: use these coefficients instead of projecting X
+    void *coeff, *idx;
+    int index_bytes;
+    void *data;
+    float *scale;
+    void *workspace;
+    size_t workspace_bytes;
+    hipStream_t stream;
+};
+size_t stacr_save_ws_layout(const StacrSaveArgs &a, size_t *offsets);
+int stacr_save_launch(const StacrSaveArgs &a);
+int stacr_quantize_launch(const void *v, int dtype, int64_t n, int bits, void *data, float *scale, void *workspace,
+                          hipStream_t s);
+
+// ------------------------------------------------------------------ launchers (weight_grad.hip)
+struct StacrGradArgs {
+    const void *g;
+    int dtype;
+    int64_t rows, d_out;
+    const void *coeff, *q;
+    int64_t d_in;
+    int rank;
+    const void *idx;
+    int index_bytes;
+    const void *data;
+    const float *scale;
+    int bits, val_dtype;
+    int64_t nnz;
+    int transposed;
+    void *dw;
+    int dw_dtype;
+    void *dbias;
+    int dbias_dtype;
+    void *workspace;
+    size_t workspace_bytes;
+    hipStream_t stream;
+};
+size_t stacr_grad_ws_layout(const StacrGradArgs &a, size_t *offsets);
+int stacr_grad_launch(const StacrGradArgs &a);

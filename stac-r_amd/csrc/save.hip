@@ -1,0 +1,812 @@
+// Save path: coefficients, exact residual top-k selection, ordered compaction, quantization.
+//
+// Restates stacr/layers.py:135-148 (coeff = X.Q, _select_residual, quantize_values) as a chain
+// of streaming passes over X:
+//   proj_hist     X -> coeff (rounded to the activation dtype), residual r = X - coeff.Q^T in
+//                 fp32, per-chunk histogram of the top 11 bits of |r|, global max |r|
+//   select_step   per chunk: which histogram bin holds the k-th largest key
+//   refine_hist   recompute r; histogram of the next key digit inside the chosen prefix (x2)
+//   count/offsets exact 31-bit threshold known: per-workgroup survivor counts -> output offsets
+//   emit          recompute r; ordered compaction in ascending flat index; quantize and write
+// chunk_topk's trim to k_total (stacr/layers.py:38-40) reruns the radix select over the emitted
+// list.  Ties at the threshold go to the lowest flat index.
+#include <float.h>
+
+#include "internal.h"
+
+using namespace stacr;
+
+namespace {
+
+__device__ __forceinline__ void wg_rows(const SaveGeom &g, int64_t wg, int64_t &chunk, int64_t &row0,
+                                        int64_t &row_end)
+{
+    chunk = wg / g.wgs_per_chunk;
+    const int64_t local = wg - chunk * g.wgs_per_chunk;
+    const int64_t cstart = chunk * g.chunk_rows;
+    const int64_t cend = min(cstart + g.chunk_rows, g.rows);
+    row0 = cstart + local * g.rows_per_wg;
+    row_end = min(row0 + g.rows_per_wg, cend);
+}
+
+// Sum R partial values over the L threads of a row slot; every thread of the slot receives the
+// identical total (the xor butterfly adds commuted pairs, the cross-wave sum has a fixed order).
+template <int R>
+__device__ __forceinline__ void row_reduce(float (&acc)[R], int L, float *s_red)
+{
+    const int w = L < 64 ? L : 64;
+    for (int off = w >> 1; off > 0; off >>= 1) {
+#pragma unroll
+        for (int j = 0; j < R; ++j) acc[j] += __shfl_xor(acc[j], off, 64);
+    }
+    if (L > 64) {
+        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        if (lane == 0) {
+#pragma unroll
+            for (int j = 0; j < R; ++j) s_red[wave * R + j] = acc[j];
+        }
+        __syncthreads();
+        const int per = L >> 6, first = (wave / per) * per;
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            float s = 0.f;
+            for (int k = 0; k < per; ++k) s += s_red[(first + k) * R + j];
+            acc[j] = s;
+        }
+        __syncthreads();
+    }
+}
+
+// Basis columns of one vector, either cached in registers or read from the padded fp32 copy.
+template <int R, int V, bool QREG>
+struct QCols {
+    float q[QREG ? V : 1][QREG ? R : 1];
+    __device__ __forceinline__ void init(const float *__restrict__ qp, int64_t col, int64_t d)
+    {
+        if constexpr (QREG) {
+#pragma unroll
+            for (int e = 0; e < V; ++e)
+#pragma unroll
+                for (int j = 0; j < R; ++j)
+                    q[e][j] = (col + e < d) ? qp[(col + e) * R + j] : 0.f;
+        }
+    }
+    __device__ __forceinline__ float get(const float *__restrict__ qp, int64_t col, int e, int j) const
+    {
+        if constexpr (QREG) return q[e][j];
+        else return qp[(col + e) * R + j];
+    }
+};
+
+// r = x - sum_j c_j q_j as an fp32 fused multiply-add chain, j ascending (the oracle's order).
+template <int R, int V, bool QREG>
+__device__ __forceinline__ void residuals(const float (&xv)[V], const float (&c)[R],
+                                          const QCols<R, V, QREG> &qc, const float *__restrict__ qp,
+                                          int64_t col, float (&r)[V])
+{
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+        float acc = xv[e];
+#pragma unroll
+        for (int j = 0; j < R; ++j) acc = fmaf(-c[j], qc.get(qp, col, e, j), acc);
+        r[e] = acc;
+    }
+}
+
+template <int DT, int R>
+__device__ __forceinline__ void load_coeff(const typename Act<DT>::T *__restrict__ coeff, int64_t row,
+                                           int rank, bool active, float (&c)[R])
+{
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+        c[j] = (active && j < rank) ? Act<DT>::ld(coeff[row * rank + j]) : 0.f;
+}
+
+struct OutSpec {
+    void *idx;
+    int idx64;
+    void *data;   // int8 (bits 8), int8 staging (bits 4), activation dtype (bits 0)
+    int bits;
+    uint32_t *list_rbits;  // trim path: chunk survivors as (fp32 bits, flat index)
+    uint32_t *list_idx;
+};
+
+__device__ __forceinline__ float quant_scale(uint32_t maxkey, int bits, float amax_rounded)
+{
+    (void)maxkey;
+    const float qmax = bits == 4 ? 7.f : 127.f;
+    float s = __fdiv_rn(amax_rounded, qmax);
+    return s < FLT_MIN ? FLT_MIN : s;  // NaN propagates (comparison is false)
+}
+
+__device__ __forceinline__ int8_t quantize_one(float v, float scale, int bits)
+{
+    const float qmax = bits == 4 ? 7.f : 127.f;
+    float t = rintf(__fdiv_rn(v, scale));  // round half to even, as torch.round
+    t = fminf(fmaxf(t, -qmax - 1.f), qmax);
+    return (int8_t)(int)t;
+}
+
+template <int DT>
+__device__ __forceinline__ void write_entry(const OutSpec &o, uint32_t pos, uint32_t flat, float r, float scale)
+{
+    if (o.idx64) static_cast<int64_t *>(o.idx)[pos] = (int64_t)flat;
+    else static_cast<int32_t *>(o.idx)[pos] = (int32_t)flat;
+    const float v = Act<DT>::rnd(r);
+    if (o.bits == 0) static_cast<typename Act<DT>::T *>(o.data)[pos] = Act<DT>::st(v);
+    else static_cast<int8_t *>(o.data)[pos] = quantize_one(v, scale, o.bits);
+}
+
+// ------------------------------------------------------------------ kernels
+__global__ void k_zero_u32(uint32_t *p, int64_t n)
+{
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+template <int DT>
+__global__ void k_pad_basis(const typename Act<DT>::T *__restrict__ q, int64_t d, int rank, int R, float *__restrict__ qp)
+{
+    const int64_t n = d * R;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = i / R;
+        const int j = (int)(i - row * R);
+        qp[i] = j < rank ? Act<DT>::ld(q[row * rank + j]) : 0.f;
+    }
+}
+
+// Pass 1: coefficients, first-digit histogram, max key.
+template <int DT, int R, int V, bool QREG>
+__global__ __launch_bounds__(kBlock) void k_proj_hist(SaveGeom g, const typename Act<DT>::T *__restrict__ x,
+                                                      const float *__restrict__ qp,
+                                                      typename Act<DT>::T *__restrict__ coeff,
+                                                      uint32_t *__restrict__ hist, uint32_t *__restrict__ maxkey,
+                                                      int do_hist, const typename Act<DT>::T *__restrict__ coeff_in)
+{
+    using A = Act<DT>;
+    __shared__ uint32_t s_hist[kBins];
+    __shared__ float s_red[kWaves * R];
+    for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
+
+    int64_t chunk, row0, row_end;
+    wg_rows(g, blockIdx.x, chunk, row0, row_end);
+    const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
+    QCols<R, V, QREG> qc;
+    qc.init(qp, (int64_t)u * V, g.d);
+    uint32_t kmax = 0u;
+    __syncthreads();
+
+    for (int64_t base = row0; base < row_end; base += g.rpi) {
+        const int64_t row = base + slot;
+        const bool active = row < row_end;
+        const typename A::T *xr = x + row * g.d;
+        float xkeep[V];
+        float c[R];
+        if (coeff_in) {
+            // coefficients supplied by the caller (selection on a given projection)
+            load_coeff<DT, R>(coeff_in, row, g.rank, active, c);
+        } else {
+            float acc[R];
+#pragma unroll
+            for (int j = 0; j < R; ++j) acc[j] = 0.f;
+            for (int m = 0; m < g.mv; ++m) {
+                const int64_t col = ((int64_t)m * g.L + u) * V;
+                if (active && col < g.d) {
+                    float xv[V];
+                    load_vec<DT, V>(xr + col, xv);
+#pragma unroll
+                    for (int e = 0; e < V; ++e) {
+                        xkeep[e] = xv[e];
+#pragma unroll
+                        for (int j = 0; j < R; ++j) acc[j] = fmaf(xv[e], qc.get(qp, col, e, j), acc[j]);
+                    }
+                }
+            }
+            row_reduce<R>(acc, g.L, s_red);
+#pragma unroll
+            for (int j = 0; j < R; ++j) c[j] = j < g.rank ? A::rnd(acc[j]) : 0.f;
+            if (active && u == 0)
+                for (int j = 0; j < g.rank; ++j) coeff[row * g.rank + j] = A::st(c[j]);
+        }
+        if (!do_hist) continue;
+        for (int m = 0; m < g.mv; ++m) {
+            const int64_t col = ((int64_t)m * g.L + u) * V;
+            if (active && col < g.d) {
+                float xv[V], r[V];
+                if (QREG && !coeff_in) {
+#pragma unroll
+                    for (int e = 0; e < V; ++e) xv[e] = xkeep[e];
+                } else {
+                    load_vec<DT, V>(xr + col, xv);
+                }
+                residuals<R, V, QREG>(xv, c, qc, qp, col, r);
+#pragma unroll
+                for (int e = 0; e < V; ++e) {
+                    const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
+                    atomicAdd(&s_hist[key >> kDigitShift[0]], 1u);
+                    kmax = max(kmax, key);
+                }
+            }
+        }
+    }
+    if (!do_hist) return;
+    __syncthreads();
+    uint32_t *gh = hist + (chunk * 3 + 0) * kBins;
+    for (int b = threadIdx.x; b < kBins; b += kBlock)
+        if (s_hist[b]) atomicAdd(&gh[b], s_hist[b]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, off, 64));
+    if ((threadIdx.x & 63) == 0 && kmax) atomicMax(maxkey, kmax);
+}
+
+// Passes 2 and 3: histogram of digit `lvl` among keys matching the chunk's prefix so far.
+template <int DT, int R, int V, bool QREG>
+__global__ __launch_bounds__(kBlock) void k_refine_hist(SaveGeom g, int lvl, const typename Act<DT>::T *__restrict__ x,
+                                                        const float *__restrict__ qp,
+                                                        const typename Act<DT>::T *__restrict__ coeff,
+                                                        uint32_t *__restrict__ hist, const SelState *__restrict__ state)
+{
+    __shared__ uint32_t s_hist[kBins];
+    for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
+    int64_t chunk, row0, row_end;
+    wg_rows(g, blockIdx.x, chunk, row0, row_end);
+    const uint32_t prefix = state[chunk * 3 + lvl - 1].prefix;
+    const int match_shift = kDigitShift[lvl - 1], dshift = kDigitShift[lvl];
+    const uint32_t dmask = (uint32_t)kDigitBins[lvl] - 1u;
+    const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
+    QCols<R, V, QREG> qc;
+    qc.init(qp, (int64_t)u * V, g.d);
+    __syncthreads();
+    for (int64_t base = row0; base < row_end; base += g.rpi) {
+        const int64_t row = base + slot;
+        const bool active = row < row_end;
+        float c[R];
+        load_coeff<DT, R>(coeff, row, g.rank, active, c);
+        for (int m = 0; m < g.mv; ++m) {
+            const int64_t col = ((int64_t)m * g.L + u) * V;
+            if (active && col < g.d) {
+                float xv[V], r[V];
+                load_vec<DT, V>(x + row * g.d + col, xv);
+                residuals<R, V, QREG>(xv, c, qc, qp, col, r);
+#pragma unroll
+                for (int e = 0; e < V; ++e) {
+                    const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
+                    if ((key >> match_shift) == prefix) atomicAdd(&s_hist[(key >> dshift) & dmask], 1u);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    uint32_t *gh = hist + (chunk * 3 + lvl) * kBins;
+    for (int b = threadIdx.x; b < kDigitBins[lvl]; b += kBlock)
+        if (s_hist[b]) atomicAdd(&gh[b], s_hist[b]);
+}
+
+// One radix level per chunk: find the bin holding the need-th largest key.
+// hist_stride/state_base let the same kernel serve the per-chunk pass and the trim pass.
+__global__ __launch_bounds__(kBlock) void k_select_step(int lvl, const uint32_t *__restrict__ hist,
+                                                        SelState *__restrict__ state, int64_t n_chunks,
+                                                        uint32_t k_full, uint32_t k_last)
+{
+    __shared__ uint32_t s_tot[kWaves];
+    const int64_t chunk = blockIdx.x;
+    uint32_t need, prefix;
+    if (lvl == 0) {
+        need = chunk == n_chunks - 1 ? k_last : k_full;
+        prefix = 0u;
+    } else {
+        const SelState s = state[chunk * 3 + lvl - 1];
+        need = s.need;
+        prefix = s.prefix;
+    }
+    const int nb = kDigitBins[lvl];
+    const int per = nb / kBlock;
+    const int bits = lvl == 2 ? 9 : 11;
+    const uint32_t *h = hist + (chunk * 3 + lvl) * kBins;
+    // thread t looks at the bins of owner 255 - t so that the exclusive scan counts the bins above
+    const int owner = kBlock - 1 - threadIdx.x;
+    uint32_t local = 0u;
+    for (int i = 0; i < per; ++i) local += h[owner * per + i];
+    uint32_t total;
+    const uint32_t above = block_exclusive_scan(local, s_tot, &total);
+    if (threadIdx.x == 0) state[chunk * 3 + lvl] = SelState{prefix << bits, need};
+    __syncthreads();
+    if (above < need && above + local >= need) {
+        uint32_t run = above;
+        for (int i = per - 1; i >= 0; --i) {
+            const int b = owner * per + i;
+            if (run + h[b] >= need) {
+                state[chunk * 3 + lvl] = SelState{(prefix << bits) | (uint32_t)b, need - run};
+                break;
+            }
+            run += h[b];
+        }
+    }
+}
+
+template <int DT, int R, int V, bool QREG>
+__global__ __launch_bounds__(kBlock) void k_count(SaveGeom g, const typename Act<DT>::T *__restrict__ x,
+                                                  const float *__restrict__ qp,
+                                                  const typename Act<DT>::T *__restrict__ coeff,
+                                                  const SelState *__restrict__ state, WgCount *__restrict__ counts)
+{
+    __shared__ uint32_t s_tot[kWaves];
+    int64_t chunk, row0, row_end;
+    wg_rows(g, blockIdx.x, chunk, row0, row_end);
+    const uint32_t T = state[chunk * 3 + 2].prefix;
+    const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
+    QCols<R, V, QREG> qc;
+    qc.init(qp, (int64_t)u * V, g.d);
+    uint32_t gt = 0u, eq = 0u;
+    for (int64_t base = row0; base < row_end; base += g.rpi) {
+        const int64_t row = base + slot;
+        const bool active = row < row_end;
+        float c[R];
+        load_coeff<DT, R>(coeff, row, g.rank, active, c);
+        for (int m = 0; m < g.mv; ++m) {
+            const int64_t col = ((int64_t)m * g.L + u) * V;
+            if (active && col < g.d) {
+                float xv[V], r[V];
+                load_vec<DT, V>(x + row * g.d + col, xv);
+                residuals<R, V, QREG>(xv, c, qc, qp, col, r);
+#pragma unroll
+                for (int e = 0; e < V; ++e) {
+                    const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
+                    gt += key > T;
+                    eq += key == T;
+                }
+            }
+        }
+    }
+    const uint32_t tg = block_sum(gt, s_tot);
+    const uint32_t te = block_sum(eq, s_tot);
+    if (threadIdx.x == 0) counts[blockIdx.x] = WgCount{tg, te};
+}
+
+// Output offsets: per chunk, scan the workgroups in order; ties are handed out first come.
+__global__ __launch_bounds__(kBlock) void k_offsets(const WgCount *__restrict__ counts, WgOffset *__restrict__ offs,
+                                                    const SelState *__restrict__ state, int64_t wgs_per_chunk,
+                                                    uint32_t chunk_k)
+{
+    __shared__ uint32_t s_tot[kWaves];
+    const int64_t chunk = blockIdx.x;
+    const uint32_t need_eq = state[chunk * 3 + 2].need;
+    const uint32_t base = (uint32_t)chunk * chunk_k;
+    uint32_t carry_eq = 0u, carry_sel = 0u;
+    for (int64_t w0 = 0; w0 < wgs_per_chunk; w0 += kBlock) {
+        const int64_t w = w0 + threadIdx.x;
+        const WgCount c = w < wgs_per_chunk ? counts[chunk * wgs_per_chunk + w] : WgCount{0u, 0u};
+        uint32_t tot_eq, tot_sel;
+        const uint32_t eq_before = carry_eq + block_exclusive_scan(c.eq, s_tot, &tot_eq);
+        const uint32_t take = eq_before >= need_eq ? 0u : min(c.eq, need_eq - eq_before);
+        const uint32_t sel = c.gt + take;
+        const uint32_t sel_before = carry_sel + block_exclusive_scan(sel, s_tot, &tot_sel);
+        if (w < wgs_per_chunk) offs[chunk * wgs_per_chunk + w] = WgOffset{base + sel_before, take};
+        carry_eq += tot_eq;
+        carry_sel += tot_sel;
+    }
+}
+
+template <int DT, int R, int V, bool QREG>
+__global__ __launch_bounds__(kBlock) void k_emit(SaveGeom g, const typename Act<DT>::T *__restrict__ x,
+                                                 const float *__restrict__ qp,
+                                                 const typename Act<DT>::T *__restrict__ coeff,
+                                                 const SelState *__restrict__ state, const WgOffset *__restrict__ offs,
+                                                 const uint32_t *__restrict__ maxkey, OutSpec o, float *scale_out,
+                                                 int to_list)
+{
+    __shared__ uint32_t s_tot[kWaves];
+    int64_t chunk, row0, row_end;
+    wg_rows(g, blockIdx.x, chunk, row0, row_end);
+    const uint32_t T = state[chunk * 3 + 2].prefix;
+    const WgOffset wo = offs[blockIdx.x];
+    const float amax = Act<DT>::rnd(__uint_as_float(*maxkey));
+    const float scale = o.bits ? quant_scale(*maxkey, o.bits, amax) : 1.f;
+    if (!to_list && blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
+    const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
+    QCols<R, V, QREG> qc;
+    qc.init(qp, (int64_t)u * V, g.d);
+    uint32_t cur_gt = 0u, cur_eq = 0u;
+    for (int64_t base = row0; base < row_end; base += g.rpi) {
+        const int64_t row = base + slot;
+        const bool active = row < row_end;
+        float c[R];
+        load_coeff<DT, R>(coeff, row, g.rank, active, c);
+        for (int m = 0; m < g.mv; ++m) {
+            const int64_t col = ((int64_t)m * g.L + u) * V;
+            const bool live = active && col < g.d;
+            float r[V];
+            uint32_t ngt = 0u, neq = 0u;
+            if (live) {
+                float xv[V];
+                load_vec<DT, V>(x + row * g.d + col, xv);
+                residuals<R, V, QREG>(xv, c, qc, qp, col, r);
+#pragma unroll
+                for (int e = 0; e < V; ++e) {
+                    const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
+                    ngt += key > T;
+                    neq += key == T;
+                }
+            }
+            uint32_t tot;
+            const uint32_t ex = block_exclusive_scan(ngt | (neq << 16), s_tot, &tot);
+            if (live && (ngt | neq)) {
+                uint32_t gb = cur_gt + (ex & 0xffffu), eb = cur_eq + (ex >> 16);
+#pragma unroll
+                for (int e = 0; e < V; ++e) {
+                    const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
+                    const bool is_gt = key > T, is_eq = key == T;
+                    if (is_gt || (is_eq && eb < wo.take)) {
+                        const uint32_t pos = wo.off + gb + min(eb, wo.take);
+                        const uint32_t flat = (uint32_t)(row * g.d + col + e);
+                        if (to_list) {
+                            o.list_rbits[pos] = __float_as_uint(r[e]);
+                            o.list_idx[pos] = flat;
+                        } else {
+                            write_entry<DT>(o, pos, flat, r[e], scale);
+                        }
+                    }
+                    gb += is_gt;
+                    eb += is_eq;
+                }
+            }
+            cur_gt += tot & 0xffffu;
+            cur_eq += tot >> 16;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ trim pass over the list
+__global__ __launch_bounds__(kBlock) void k_list_hist(int lvl, const uint32_t *__restrict__ rbits, int64_t n,
+                                                      uint32_t *__restrict__ hist, const SelState *__restrict__ state)
+{
+    __shared__ uint32_t s_hist[kBins];
+    for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
+    __syncthreads();
+    const uint32_t prefix = lvl ? state[lvl - 1].prefix : 0u;
+    const int match_shift = lvl ? kDigitShift[lvl - 1] : 31, dshift = kDigitShift[lvl];
+    const uint32_t dmask = (uint32_t)kDigitBins[lvl] - 1u;
+    const int64_t start = (int64_t)blockIdx.x * kListBlock + threadIdx.x * (kListBlock / kBlock);
+    for (int k = 0; k < kListBlock / kBlock; ++k) {
+        const int64_t i = start + k;
+        if (i >= n) break;
+        const uint32_t key = rbits[i] & 0x7fffffffu;
+        if ((key >> match_shift) == prefix) atomicAdd(&s_hist[(key >> dshift) & dmask], 1u);
+    }
+    __syncthreads();
+    uint32_t *gh = hist + lvl * kBins;
+    for (int b = threadIdx.x; b < kDigitBins[lvl]; b += kBlock)
+        if (s_hist[b]) atomicAdd(&gh[b], s_hist[b]);
+}
+
+__global__ __launch_bounds__(kBlock) void k_list_count(const uint32_t *__restrict__ rbits, int64_t n,
+                                                       const SelState *__restrict__ state, WgCount *__restrict__ counts)
+{
+    __shared__ uint32_t s_tot[kWaves];
+    const uint32_t T = state[2].prefix;
+    const int64_t start = (int64_t)blockIdx.x * kListBlock + threadIdx.x * (kListBlock / kBlock);
+    uint32_t gt = 0u, eq = 0u;
+    for (int k = 0; k < kListBlock / kBlock; ++k) {
+        const int64_t i = start + k;
+        if (i >= n) break;
+        const uint32_t key = rbits[i] & 0x7fffffffu;
+        gt += key > T;
+        eq += key == T;
+    }
+    const uint32_t tg = block_sum(gt, s_tot);
+    const uint32_t te = block_sum(eq, s_tot);
+    if (threadIdx.x == 0) counts[blockIdx.x] = WgCount{tg, te};
+}
+
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_list_emit(const uint32_t *__restrict__ rbits, const uint32_t *__restrict__ lidx,
+                                                      int64_t n, const SelState *__restrict__ state,
+                                                      const WgOffset *__restrict__ offs,
+                                                      const uint32_t *__restrict__ maxkey, OutSpec o, float *scale_out)
+{
+    __shared__ uint32_t s_tot[kWaves];
+    const uint32_t T = state[2].prefix;
+    const WgOffset wo = offs[blockIdx.x];
+    const float amax = Act<DT>::rnd(__uint_as_float(*maxkey));
+    const float scale = o.bits ? quant_scale(*maxkey, o.bits, amax) : 1.f;
+    if (blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
+    constexpr int per = kListBlock / kBlock;
+    const int64_t start = (int64_t)blockIdx.x * kListBlock + threadIdx.x * per;
+    uint32_t ngt = 0u, neq = 0u;
+    for (int k = 0; k < per; ++k) {
+        const int64_t i = start + k;
+        if (i >= n) break;
+        const uint32_t key = rbits[i] & 0x7fffffffu;
+        ngt += key > T;
+        neq += key == T;
+    }
+    uint32_t tot;
+    const uint32_t ex = block_exclusive_scan(ngt | (neq << 16), s_tot, &tot);
+    uint32_t gb = ex & 0xffffu, eb = ex >> 16;
+    for (int k = 0; k < per; ++k) {
+        const int64_t i = start + k;
+        if (i >= n) break;
+        const uint32_t rb = rbits[i];
+        const uint32_t key = rb & 0x7fffffffu;
+        const bool is_gt = key > T, is_eq = key == T;
+        if (is_gt || (is_eq && eb < wo.take)) {
+            const uint32_t pos = wo.off + gb + min(eb, wo.take);
+            write_entry<DT>(o, pos, lidx[i], __uint_as_float(rb), scale);
+        }
+        gb += is_gt;
+        eb += is_eq;
+    }
+}
+
+__global__ void k_pack_int4(const int8_t *__restrict__ q, int64_t n, uint8_t *__restrict__ out)
+{
+    const int64_t m = (n + 1) / 2;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < m; i += (int64_t)gridDim.x * blockDim.x) {
+        const uint32_t lo = (uint32_t)q[2 * i] & 0xfu;
+        const uint32_t hi = 2 * i + 1 < n ? ((uint32_t)q[2 * i + 1] & 0xfu) : 0u;
+        out[i] = (uint8_t)(lo | (hi << 4));
+    }
+}
+
+// ------------------------------------------------------------------ standalone quantizer
+// quantize_values (stacr/quant.py:49-65) on a value vector: max |v| then the symmetric rounding.
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_absmax(const typename Act<DT>::T *__restrict__ v, int64_t n,
+                                                   uint32_t *__restrict__ maxkey)
+{
+    uint32_t m = 0u;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
+        m = max(m, __float_as_uint(Act<DT>::ld(v[i])) & 0x7fffffffu);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
+    if ((threadIdx.x & 63) == 0 && m) atomicMax(maxkey, m);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_quantize(const typename Act<DT>::T *__restrict__ v, int64_t n, int bits,
+                                                     const uint32_t *__restrict__ maxkey, void *__restrict__ data,
+                                                     float *__restrict__ scale_out)
+{
+    const float scale = quant_scale(*maxkey, bits, __uint_as_float(*maxkey));
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
+    if (bits == 8) {
+        for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
+            static_cast<int8_t *>(data)[i] = quantize_one(Act<DT>::ld(v[i]), scale, 8);
+    } else {
+        const int64_t nb = (n + 1) / 2;
+        for (int64_t b = (int64_t)blockIdx.x * kBlock + threadIdx.x; b < nb; b += (int64_t)gridDim.x * kBlock) {
+            const uint32_t lo = (uint32_t)quantize_one(Act<DT>::ld(v[2 * b]), scale, 4) & 0xfu;
+            const uint32_t hi = 2 * b + 1 < n ? ((uint32_t)quantize_one(Act<DT>::ld(v[2 * b + 1]), scale, 4) & 0xfu) : 0u;
+            static_cast<uint8_t *>(data)[b] = (uint8_t)(lo | (hi << 4));
+        }
+    }
+}
+
+// ------------------------------------------------------------------ host side
+int next_pow2(int64_t v)
+{
+    int p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+int ilog2(int v)
+{
+    int l = 0;
+    while ((1 << l) < v) ++l;
+    return l;
+}
+
+int pad_rank(int rank) { return rank <= 4 ? 4 : rank <= 8 ? 8 : rank <= 16 ? 16 : 32; }
+
+int grid_for(int64_t n) { return (int)hmin<int64_t>(4096, hmax<int64_t>(1, (n + kBlock - 1) / kBlock)); }
+
+struct Plan {
+    SaveGeom g;
+    int V, R;
+    bool qreg;
+    int64_t n_wgs;
+    bool trim;
+    int64_t n_list_blocks;
+};
+
+Plan make_plan(const StacrSaveArgs &a)
+{
+    Plan p{};
+    const int vec = a.dtype == STACR_DTYPE_F32 ? 4 : 8;
+    const bool aligned = ((uintptr_t)a.x % 16) == 0;
+    p.V = (a.feats % vec == 0 && aligned) ? vec : 1;
+    p.R = pad_rank(a.rank);
+    SaveGeom &g = p.g;
+    g.rows = a.rows;
+    g.d = a.feats;
+    g.rank = a.rank;
+    const int64_t vecs = (a.feats + p.V - 1) / p.V;
+    g.L = (int)hmin<int64_t>(kBlock, hmax<int64_t>(16, next_pow2(vecs)));
+    g.log2L = ilog2(g.L);
+    g.rpi = kBlock / g.L;
+    g.mv = (int)((vecs + g.L - 1) / g.L);
+    g.chunk_rows = a.mode == STACR_MODE_GLOBAL_TOPK ? a.rows : min(a.chunk_rows, a.rows);
+    if (g.chunk_rows < 1) g.chunk_rows = 1;
+    g.n_chunks = (a.rows + g.chunk_rows - 1) / g.chunk_rows;
+    int64_t target = hmax<int64_t>(1, 16384 / hmax<int64_t>(1, a.feats));
+    int64_t rpw = 1;
+    while (rpw * 2 <= target) rpw *= 2;
+    if (a.mode != STACR_MODE_GLOBAL_TOPK)
+        while (rpw > 1 && g.chunk_rows % rpw) rpw >>= 1;
+    g.rows_per_wg = rpw;
+    g.wgs_per_chunk = (g.chunk_rows + rpw - 1) / rpw;
+    p.n_wgs = g.n_chunks * g.wgs_per_chunk;
+    p.qreg = g.mv == 1 && p.V * p.R <= 128;
+    p.trim = a.k_sum > a.k_total;
+    p.n_list_blocks = (a.k_sum + kListBlock - 1) / kListBlock;
+    return p;
+}
+
+template <typename T> T *carve(char *base, size_t off) { return reinterpret_cast<T *>(base + off); }
+
+enum { WS_QP, WS_HIST, WS_STATE, WS_MAXKEY, WS_COUNTS, WS_OFFS, WS_LRBITS, WS_LIDX, WS_THIST, WS_TSTATE,
+       WS_LCOUNTS, WS_LOFFS, WS_Q4, WS_N };
+
+size_t layout(const StacrSaveArgs &a, const Plan &p, size_t *off)
+{
+    size_t cur = 0;
+    auto take = [&](int slot, size_t bytes) { off[slot] = cur; cur += (bytes + 255) & ~(size_t)255; };
+    take(WS_QP, (size_t)a.feats * p.R * sizeof(float));
+    take(WS_HIST, (size_t)p.g.n_chunks * 3 * kBins * sizeof(uint32_t));
+    take(WS_MAXKEY, sizeof(uint32_t));
+    take(WS_STATE, (size_t)p.g.n_chunks * 3 * sizeof(SelState));
+    take(WS_COUNTS, (size_t)p.n_wgs * sizeof(WgCount));
+    take(WS_OFFS, (size_t)p.n_wgs * sizeof(WgOffset));
+    const size_t nl = p.trim ? (size_t)a.k_sum : 0, nb = p.trim ? (size_t)p.n_list_blocks : 0;
+    take(WS_LRBITS, nl * sizeof(uint32_t));
+    take(WS_LIDX, nl * sizeof(uint32_t));
+    take(WS_THIST, p.trim ? 3 * kBins * sizeof(uint32_t) : 0);
+    take(WS_TSTATE, p.trim ? 3 * sizeof(SelState) : 0);
+    take(WS_LCOUNTS, nb * sizeof(WgCount));
+    take(WS_LOFFS, nb * sizeof(WgOffset));
+    take(WS_Q4, a.bits == 4 ? (size_t)a.k_total : 0);
+    return cur;
+}
+
+template <int DT, int R, int V, bool QREG>
+int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *off)
+{
+    using T = typename Act<DT>::T;
+    hipStream_t s = a.stream;
+    const T *x = static_cast<const T *>(a.x);
+    T *coeff_out = static_cast<T *>(a.coeff);
+    const T *coeff_in = static_cast<const T *>(a.coeff_in);
+    const T *coeff = coeff_in ? coeff_in : coeff_out;
+    float *qp = carve<float>(ws, off[WS_QP]);
+    uint32_t *hist = carve<uint32_t>(ws, off[WS_HIST]);
+    uint32_t *maxkey = carve<uint32_t>(ws, off[WS_MAXKEY]);
+    SelState *state = carve<SelState>(ws, off[WS_STATE]);
+    WgCount *counts = carve<WgCount>(ws, off[WS_COUNTS]);
+    WgOffset *offs = carve<WgOffset>(ws, off[WS_OFFS]);
+    const bool resid = a.k_total > 0;
+    const int nwg = (int)p.n_wgs;
+
+    k_pad_basis<DT><<<grid_for(a.feats * R), kBlock, 0, s>>>(static_cast<const T *>(a.q), a.feats, a.rank, R, qp);
+    if (resid) {
+        // histogram and max key are contiguous in the layout: one clear
+        k_zero_u32<<<grid_for((int64_t)p.g.n_chunks * 3 * kBins + 64), kBlock, 0, s>>>(
+            hist, (int64_t)((off[WS_MAXKEY] + sizeof(uint32_t) - off[WS_HIST]) / sizeof(uint32_t)));
+    }
+    if (!coeff_in || resid)
+        k_proj_hist<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in);
+    if (!resid) return stacr_hip_check(hipGetLastError(), "save kernels");
+
+    const int nch = (int)p.g.n_chunks;
+    const uint32_t kf = (uint32_t)a.k_full, kl = (uint32_t)a.k_last;
+    k_select_step<<<nch, kBlock, 0, s>>>(0, hist, state, p.g.n_chunks, kf, kl);
+    for (int lvl = 1; lvl < 3; ++lvl) {
+        k_refine_hist<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, lvl, x, qp, coeff, hist, state);
+        k_select_step<<<nch, kBlock, 0, s>>>(lvl, hist, state, p.g.n_chunks, kf, kl);
+    }
+    k_count<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, counts);
+    k_offsets<<<nch, kBlock, 0, s>>>(counts, offs, state, p.g.wgs_per_chunk, kf);
+
+    OutSpec o{};
+    o.idx = a.idx;
+    o.idx64 = a.index_bytes == 8;
+    o.bits = a.bits;
+    o.data = a.bits == 4 ? (void *)carve<int8_t>(ws, off[WS_Q4]) : a.data;
+    uint32_t *lrb = carve<uint32_t>(ws, off[WS_LRBITS]);
+    uint32_t *lix = carve<uint32_t>(ws, off[WS_LIDX]);
+    o.list_rbits = lrb;
+    o.list_idx = lix;
+    k_emit<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, offs, maxkey, o, a.scale, p.trim ? 1 : 0);
+
+    if (p.trim) {
+        uint32_t *thist = carve<uint32_t>(ws, off[WS_THIST]);
+        SelState *tstate = carve<SelState>(ws, off[WS_TSTATE]);
+        WgCount *lcounts = carve<WgCount>(ws, off[WS_LCOUNTS]);
+        WgOffset *loffs = carve<WgOffset>(ws, off[WS_LOFFS]);
+        const int nlb = (int)p.n_list_blocks;
+        const uint32_t kt = (uint32_t)a.k_total;
+        k_zero_u32<<<grid_for(3 * kBins), kBlock, 0, s>>>(thist, 3 * kBins);
+        for (int lvl = 0; lvl < 3; ++lvl) {
+            k_list_hist<<<nlb, kBlock, 0, s>>>(lvl, lrb, a.k_sum, thist, tstate);
+            k_select_step<<<1, kBlock, 0, s>>>(lvl, thist, tstate, 1, kt, kt);
+        }
+        k_list_count<<<nlb, kBlock, 0, s>>>(lrb, a.k_sum, tstate, lcounts);
+        k_offsets<<<1, kBlock, 0, s>>>(lcounts, loffs, tstate, p.n_list_blocks, kt);
+        k_list_emit<DT><<<nlb, kBlock, 0, s>>>(lrb, lix, a.k_sum, tstate, loffs, maxkey, o, a.scale);
+    }
+    if (a.bits == 4)
+        k_pack_int4<<<grid_for((a.k_total + 1) / 2), kBlock, 0, s>>>(carve<int8_t>(ws, off[WS_Q4]), a.k_total,
+                                                                   static_cast<uint8_t *>(a.data));
+    return stacr_hip_check(hipGetLastError(), "save kernels");
+}
+
+template <int DT, int R>
+int dispatch_vq(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *off)
+{
+    constexpr int VEC = Act<DT>::kVec;
+    if (p.V == VEC) {
+        if (p.qreg) return launch_typed<DT, R, VEC, true>(a, p, ws, off);
+        return launch_typed<DT, R, VEC, false>(a, p, ws, off);
+    }
+    if (p.qreg) return launch_typed<DT, R, 1, true>(a, p, ws, off);
+    return launch_typed<DT, R, 1, false>(a, p, ws, off);
+}
+
+template <int DT>
+int dispatch_r(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *off)
+{
+    switch (p.R) {
+    case 4: return dispatch_vq<DT, 4>(a, p, ws, off);
+    case 8: return dispatch_vq<DT, 8>(a, p, ws, off);
+    case 16: return dispatch_vq<DT, 16>(a, p, ws, off);
+    default: return dispatch_vq<DT, 32>(a, p, ws, off);
+    }
+}
+
+}  // namespace
+
+size_t stacr_save_ws_layout(const StacrSaveArgs &a, size_t *offsets)
+{
+    const Plan p = make_plan(a);
+    size_t tmp[WS_N];
+    return layout(a, p, offsets ? offsets : tmp);
+}
+
+int stacr_save_launch(const StacrSaveArgs &a)
+{
+    const Plan p = make_plan(a);
+    size_t off[WS_N];
+    const size_t need = layout(a, p, off);
+    if (a.workspace_bytes < need)
+        return stacr_fail(STACR_ERR_WORKSPACE, "stacr_save: workspace has %zu bytes, needs %zu", a.workspace_bytes, need);
+    if (p.n_wgs > INT32_MAX)
+        return stacr_fail(STACR_ERR_UNSUPPORTED, "stacr_save: too many workgroups");
+    char *ws = static_cast<char *>(a.workspace);
+    switch (a.dtype) {
+    case STACR_DTYPE_F32: return dispatch_r<STACR_DTYPE_F32>(a, p, ws, off);
+    case STACR_DTYPE_BF16: return dispatch_r<STACR_DTYPE_BF16>(a, p, ws, off);
+    default: return dispatch_r<STACR_DTYPE_F16>(a, p, ws, off);
+    }
+}
+
+template <int DT>
+static int quantize_typed(const void *v, int64_t n, int bits, void *data, float *scale, uint32_t *maxkey, hipStream_t s)
+{
+    using T = typename Act<DT>::T;
+    k_zero_u32<<<1, kBlock, 0, s>>>(maxkey, 1);
+    k_absmax<DT><<<grid_for(n), kBlock, 0, s>>>(static_cast<const T *>(v), n, maxkey);
+    k_quantize<DT><<<grid_for(bits == 4 ? (n + 1) / 2 : n), kBlock, 0, s>>>(static_cast<const T *>(v), n, bits, maxkey,
+                                                                          data, scale);
+    return stacr_hip_check(hipGetLastError(), "quantize kernels");
+}
+
+int stacr_quantize_launch(const void *v, int dtype, int64_t n, int bits, void *data, float *scale, void *workspace,
+                          hipStream_t s)
+{
+    uint32_t *maxkey = static_cast<uint32_t *>(workspace);
+    switch (dtype) {
+    case STACR_DTYPE_F32: return quantize_typed<STACR_DTYPE_F32>(v, n, bits, data, scale, maxkey, s);
+    case STACR_DTYPE_BF16: return quantize_typed<STACR_DTYPE_BF16>(v, n, bits, data, scale, maxkey, s);
+    default: return quantize_typed<STACR_DTYPE_F16>(v, n, bits, data, scale, maxkey, s);
+    }
+}

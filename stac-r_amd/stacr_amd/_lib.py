@@ -1,0 +1,77 @@
+"""Loads libstacr_amd.so (the HIP kernels behind the C ABI in include/stacr_amd.h).
+
+torch is imported first so that the library binds to the HIP runtime torch already loaded
+(both carry the SONAME libamdhip64.so.7); streams and device pointers are then shared.
+There is no fallback: if the library is missing, every compute entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must be loaded before the HIP library)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libstacr_amd.so")
+
+STACR_OK = 0
+STACR_ERR_INVALID = 1
+STACR_ERR_UNSUPPORTED = 2
+STACR_ERR_WORKSPACE = 3
+STACR_ERR_HIP = 4
+
+DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
+MODE_CHUNK_TOPK, MODE_GLOBAL_TOPK = 0, 1
+MAX_RANK = 32
+
+# Every symbol declared in include/stacr_amd.h, with its ctypes signature.
+_i64, _i32, _f64, _p, _sz = ctypes.c_int64, ctypes.c_int, ctypes.c_double, ctypes.c_void_p, ctypes.c_size_t
+_P64, _PSZ, _PI32 = ctypes.POINTER(_i64), ctypes.POINTER(_sz), ctypes.POINTER(_i32)
+SIGNATURES = {
+    "stacr_abi_version": ([], _i32),
+    "stacr_last_error": ([], ctypes.c_char_p),
+    "stacr_residual_plan": ([_i64, _i64, _i32, _f64, _i64, _P64, _P64, _PI32], _i32),
+    "stacr_save_workspace_bytes": ([_i64, _i64, _i32, _i32, _i32, _f64, _i64, _i32, _PSZ], _i32),
+    "stacr_save": ([_p, _p, _i32, _i64, _i64, _i32, _i32, _f64, _i64, _i32, _p, _p, _i32, _p, _p, _p, _sz, _p],
+                   _i32),
+    "stacr_select_residual": ([_p, _p, _p, _i32, _i64, _i64, _i32, _i32, _f64, _i64, _i32, _p, _i32, _p, _p, _p,
+                               _sz, _p], _i32),
+    "stacr_quantize_values": ([_p, _i32, _i64, _i32, _p, _p, _p, _sz, _p], _i32),
+    "stacr_weight_grad_workspace_bytes": ([_i64, _i64, _i64, _i32, _i64, _PSZ], _i32),
+    "stacr_weight_grad": ([_p, _i32, _i64, _i64, _p, _p, _i64, _i32, _p, _i32, _p, _p, _i32, _i32, _i64, _i32, _p,
+                           _i32, _p, _i32, _p, _sz, _p], _i32),
+}
+
+_lib = None
+
+
+class StacrLibraryError(RuntimeError):
+    pass
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library; raises if it has not been built (python stac-r_amd/build.py)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise StacrLibraryError(
+                f"{LIB_PATH} is missing: build the HIP library first (python stac-r_amd/build.py)"
+            )
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes, fn.restype = args, res
+        if lib.stacr_abi_version() != 1:
+            raise StacrLibraryError("libstacr_amd.so ABI version mismatch")
+        _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc == STACR_OK:
+        return
+    msg = load().stacr_last_error().decode(errors="replace")
+    if rc == STACR_ERR_INVALID:
+        raise ValueError(f"{what}: {msg}")
+    if rc == STACR_ERR_UNSUPPORTED:
+        raise NotImplementedError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg}")

@@ -1,0 +1,156 @@
+"""Tensor-level calls into the HIP library (PyTorch supplies device memory and the stream).
+
+Every function here requires ROCm GPU tensors and raises otherwise: the save and weight-gradient
+arithmetic has no CPU implementation in this package.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+DTYPE_CODES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16}
+MODE_CODES = {"chunk_topk": _lib.MODE_CHUNK_TOPK, "topk": _lib.MODE_CHUNK_TOPK,
+              "global_topk": _lib.MODE_GLOBAL_TOPK}
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return DTYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"stacr_amd supports float32, bfloat16 and float16 tensors, got {dtype}") from None
+
+
+def require_gpu(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(
+            f"stacr_amd: {name} must be a ROCm GPU tensor; the save/backward path runs only in the "
+            f"HIP kernels (got device {t.device})"
+        )
+
+
+def _ptr(t: torch.Tensor | None):
+    return ctypes.c_void_p(t.data_ptr() if t is not None and t.numel() else None)
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def residual_plan(rows: int, feats: int, mode: str, budget: float, chunk_rows: int):
+    """(k_total, k_saved, index_bytes) per the reference's k rules (stacr/layers.py:25-27,33,51-53)."""
+    if mode not in MODE_CODES:
+        raise ValueError(f"residual_mode {mode!r} has no HIP selection kernel")
+    kt, ks, ib = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int()
+    L = _lib.load()
+    _lib.check(L.stacr_residual_plan(int(rows), int(feats), MODE_CODES[mode], float(budget), int(chunk_rows),
+                                     ctypes.byref(kt), ctypes.byref(ks), ctypes.byref(ib)), "stacr_residual_plan")
+    return int(kt.value), int(ks.value), int(ib.value)
+
+
+def _outputs(k: int, bits: int, dtype: torch.dtype, index_bytes: int, device):
+    idx = torch.empty(k, dtype=torch.int32 if index_bytes == 4 else torch.int64, device=device)
+    if bits == 8:
+        data = torch.empty(k, dtype=torch.int8, device=device)
+    elif bits == 4:
+        data = torch.empty((k + 1) // 2, dtype=torch.uint8, device=device)
+    else:
+        data = torch.empty(k, dtype=dtype, device=device)
+    scale = torch.empty((), dtype=torch.float32, device=device)
+    return idx, data, scale
+
+
+def save(x2d: torch.Tensor, q: torch.Tensor, *, mode: str, budget: float, chunk_rows: int, bits: int,
+         coeff: torch.Tensor | None = None):
+    """One save pass.  Returns (coeff, idx, data, scale); the last three are None without residual.
+
+    x2d: rows x feats activation (cast to the compute dtype), q: feats x rank basis in that dtype.
+    With ``coeff`` given, only selection and quantization run (stacr_select_residual).
+    """
+    require_gpu(x2d, "activation")
+    x2d = x2d.contiguous()
+    q = q.contiguous()
+    if q.dtype != x2d.dtype:
+        raise TypeError("basis must be cast to the activation dtype")
+    rows, feats = x2d.shape
+    rank = q.shape[1]
+    dt = dtype_code(x2d.dtype)
+    k_total, k_saved, ib = residual_plan(rows, feats, mode, budget, chunk_rows)
+    device = x2d.device
+    L = _lib.load()
+    ws_bytes = ctypes.c_size_t()
+    _lib.check(L.stacr_save_workspace_bytes(rows, feats, rank, dt, MODE_CODES[mode], float(budget),
+                                            int(chunk_rows), int(bits), ctypes.byref(ws_bytes)), "stacr_save")
+    ws = torch.empty(max(1, ws_bytes.value), dtype=torch.uint8, device=device)
+    stream = _stream(device)
+    if k_total > 0:
+        idx, data, scale = _outputs(k_saved, bits, x2d.dtype, ib, device)
+    else:
+        idx = data = scale = None
+    if coeff is None:
+        coeff = torch.empty(rows, rank, dtype=x2d.dtype, device=device)
+        _lib.check(L.stacr_save(_ptr(x2d), _ptr(q), dt, rows, feats, rank, MODE_CODES[mode], float(budget),
+                                int(chunk_rows), int(bits), _ptr(coeff), _ptr(idx), ib, _ptr(data), _ptr(scale),
+                                _ptr(ws), ws_bytes.value, stream), "stacr_save")
+    else:
+        coeff = coeff.contiguous()
+        if k_total > 0:
+            _lib.check(L.stacr_select_residual(_ptr(x2d), _ptr(coeff), _ptr(q), dt, rows, feats, rank,
+                                               MODE_CODES[mode], float(budget), int(chunk_rows), int(bits),
+                                               _ptr(idx), ib, _ptr(data), _ptr(scale), _ptr(ws), ws_bytes.value,
+                                               stream), "stacr_select_residual")
+    return coeff, idx, data, scale
+
+
+def quantize(values: torch.Tensor, bits: int):
+    """(data, scale) of quantize_values for bits 4/8 (stacr/quant.py:49-65)."""
+    require_gpu(values, "values")
+    flat = values.reshape(-1).contiguous()
+    n = flat.numel()
+    data = torch.empty(n if bits == 8 else (n + 1) // 2, dtype=torch.int8 if bits == 8 else torch.uint8,
+                       device=flat.device)
+    scale = torch.empty((), dtype=torch.float32, device=flat.device)
+    ws = torch.empty(4, dtype=torch.uint8, device=flat.device)
+    L = _lib.load()
+    _lib.check(L.stacr_quantize_values(_ptr(flat), dtype_code(flat.dtype), n, int(bits), _ptr(data), _ptr(scale),
+                                       _ptr(ws), 4, _stream(flat.device)), "stacr_quantize_values")
+    return data, scale
+
+
+def weight_grad(g2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, residual, bits: int, transposed: bool,
+                out_dtype: torch.dtype, bias_dtype: torch.dtype | None = None):
+    """dW (and dbias when bias_dtype is given) from the saved factors (stacr/layers.py:172-198).
+
+    ``residual`` is None or (idx, data, scale); ``coeff`` and ``q`` are cast to G's dtype first, as
+    the reference does.  dW is d_out x d_in, or d_in x d_out when ``transposed``.
+    """
+    require_gpu(g2d, "grad_output")
+    g2d = g2d.contiguous()
+    rows, d_out = g2d.shape
+    d_in, rank = q.shape
+    dt = dtype_code(g2d.dtype)
+    coeff = coeff.to(g2d.dtype).contiguous()
+    q = q.to(g2d.dtype).contiguous()
+    device = g2d.device
+    if residual is not None and residual[0].numel():
+        idx, data, scale = residual
+        nnz = idx.numel()
+        ib = idx.element_size()
+        vdt = dtype_code(data.dtype) if bits == 0 else 0
+    else:
+        idx = data = scale = None
+        nnz, ib, vdt = 0, 4, 0
+    dw = torch.empty((d_in, d_out) if transposed else (d_out, d_in), dtype=out_dtype, device=device)
+    db = torch.empty(d_out, dtype=bias_dtype, device=device) if bias_dtype is not None else None
+    L = _lib.load()
+    ws_bytes = ctypes.c_size_t()
+    _lib.check(L.stacr_weight_grad_workspace_bytes(rows, d_out, d_in, rank, nnz, ctypes.byref(ws_bytes)),
+               "stacr_weight_grad")
+    ws = torch.empty(max(1, ws_bytes.value), dtype=torch.uint8, device=device)
+    _lib.check(L.stacr_weight_grad(_ptr(g2d), dt, rows, d_out, _ptr(coeff), _ptr(q), d_in, rank, _ptr(idx), ib,
+                                   _ptr(data), _ptr(scale), int(bits), vdt, nnz, 1 if transposed else 0, _ptr(dw),
+                                   dtype_code(out_dtype), _ptr(db), dtype_code(bias_dtype) if db is not None else 0,
+                                   _ptr(ws), ws_bytes.value, _stream(device)), "stacr_weight_grad")
+    return dw, db
