@@ -1,0 +1,227 @@
+#!/usr/bin/env python3
+"""STACRLinear save + backward throughput on one MI355X (the north-star layer).
+
+Workload (c_fc layer): GPT-2-medium MLP c_fc as a Transformers Conv1D,
+N = 8 x 1024 = 8192 tokens, d_in 1024 -> d_out 4096, bf16, rank 8, residual_budget 0.005,
+residual_mode global_topk, int8 residual values, fused bias gradient.  Synthetic inputs with the
+configs' generator (low-rank + noise + 0.1% x20 outliers, per-channel log-normal scale), resident
+in HBM before timing.
+
+One step = stacr_save (coefficients, exact global top-k selection, quantization) + stacr_weight_grad
+(dW = (G^T C) Q^T + G^T R_s and dbias).  The dense Y = X W^T and grad_input = G W GEMMs are not part
+of the STAC-R path and are not timed.  Steps are replayed from a HIP graph captured once (the
+eager time is reported beside it).  Prints one JSON line.
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "stac-r_amd"), os.path.join(ROOT, "tests")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "STACRLinear save+bwd tokens/s (d=1024→4096 bf16) and % of HBM BW roofline"
+HBM_PEAK_GBS = 8000.0
+
+# workload
+N, D_IN, D_OUT, RANK = 8192, 1024, 4096, 8
+BUDGET, MODE, CHUNK, BITS = 0.005, "global_topk", 512, 8
+S_ACT = 2  # bf16 bytes
+
+
+def algorithmic_bytes(k: int) -> dict:
+    """Byte model per layer-step: U fp32, idx int32, int8 value + 4 B scale."""
+    save = N * D_IN * S_ACT + 4 * D_IN * RANK + N * RANK * S_ACT + 5 * k + 4
+    bwd = N * D_OUT * S_ACT + N * RANK * S_ACT + 5 * k + 4 + 4 * D_IN * RANK + D_OUT * D_IN * S_ACT
+    # minimal bytes each kernel's own job needs (reads of its inputs, writes of its outputs)
+    per_kernel = {
+        "k_proj_hist": N * D_IN * S_ACT + N * RANK * S_ACT,
+        "k_refine_hist": N * D_IN * S_ACT + N * RANK * S_ACT,
+        "k_count": N * D_IN * S_ACT + N * RANK * S_ACT,
+        "k_emit": N * D_IN * S_ACT + N * RANK * S_ACT + 5 * k,
+        "k_lowrank": N * D_OUT * S_ACT + N * RANK * S_ACT,
+        "k_sparse": N * D_OUT * S_ACT + 8 * k,
+        "k_expand": D_OUT * D_IN * S_ACT + D_OUT * (RANK + 1) * 4 + D_IN * RANK * 4,
+        "k_csr_rows": 5 * k + 12 * k,
+    }
+    return {"save": save, "bwd": bwd, "total": save + bwd, "per_kernel": per_kernel}
+
+
+def cpu_baseline(x, q, g, budget_s: float = 12.0, max_steps: int = 6) -> dict:
+    """The oracle (a CPU restatement of the reference path) on the same workload, one thread."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import oracle as orc
+
+    xf = x.float().cpu().numpy()
+    qf = q.float().cpu().numpy()
+    gf = g.float().cpu().numpy()
+    times = []
+    with threadpool_limits(1):
+        while len(times) < max_steps and sum(times) < budget_s:
+            t0 = time.perf_counter()
+            coeff, idx, data, scale = orc.save(xf, qf, "bf16", MODE, BUDGET, CHUNK, BITS)
+            vals = orc.dequantize(data, scale, BITS, idx.size)
+            orc.weight_grad(gf, coeff, qf, idx, vals, D_IN)
+            times.append(time.perf_counter() - t0)
+    per_step = float(np.median(times))
+    return {
+        "value": N / per_step,
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"full c_fc layer-step (save + dW + dbias, {N} tokens), {len(times)} steps, median "
+                  f"{per_step * 1e3:.0f} ms/step; oracle/stacr_oracle.c + numpy fp64 projection, 1 thread",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of graph replay")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from gpu_cases import make_activation, make_basis, make_grad
+    from stacr_amd import _lib, kernels
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    x = make_activation(N, D_IN, lognormal=True).to(dev, torch.bfloat16)
+    q = make_basis(D_IN, RANK).to(dev, torch.bfloat16)
+    g = make_grad(N, D_OUT).to(dev, torch.bfloat16)
+    k_total, k_saved, _ = kernels.residual_plan(N, D_IN, MODE, BUDGET, CHUNK)
+
+    def step():
+        coeff, idx, data, scale = kernels.save(x, q, mode=MODE, budget=BUDGET, chunk_rows=CHUNK, bits=BITS)
+        dw, db = kernels.weight_grad(g, coeff, q, (idx, data, scale), BITS, True, torch.bfloat16, torch.bfloat16)
+        return coeff, idx, data, scale, dw, db
+
+    print(f"[bench] workload ready: k={k_saved}", file=sys.stderr, flush=True)
+    ref = step()
+    torch.cuda.synchronize()
+
+    # eager timing
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    print(f"[bench] eager {eager_ms:.4f} ms/step", file=sys.stderr, flush=True)
+
+    # graph replay: capture once, check replays against the eager result, then time
+    graph_ms, graph_note = None, None
+    if not args.no_graph:
+        try:
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                step()
+            torch.cuda.current_stream().wait_stream(s)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                outs = step()
+            for _ in range(3):
+                graph.replay()
+                torch.cuda.synchronize()
+                step()  # interleaved eager work between replays
+                torch.cuda.synchronize()
+                for a, b in zip(outs, ref):
+                    if not torch.equal(a, b):
+                        raise RuntimeError("graph replay differs from the eager result")
+            for _ in range(args.warmup):
+                graph.replay()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                graph.replay()
+            torch.cuda.synchronize()
+            graph_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+            print(f"[bench] graph {graph_ms:.4f} ms/step", file=sys.stderr, flush=True)
+        except Exception as exc:  # graph capture unavailable: report eager
+            graph_note = f"graph replay unavailable ({exc}); value is eager"
+            print(f"[bench] {graph_note}", file=sys.stderr, flush=True)
+    ms = graph_ms if graph_ms is not None else eager_ms
+
+    # per-kernel durations (HIP events around each launch, device kept busy ahead of each)
+    prof_steps = 20
+    with _lib.KernelTimer(max_launches=prof_steps * 64) as timer:
+        for _ in range(prof_steps):
+            step()
+    kern = {name: {"avg_us": tot / max(cnt, 1) * 1e3, "per_step_us": tot / prof_steps * 1e3,
+                   "launches_per_step": cnt / prof_steps}
+            for name, (tot, cnt) in timer.results.items()}
+    dominant = max(kern, key=lambda n: kern[n]["per_step_us"])
+    ab = algorithmic_bytes(k_saved)
+    dom_bytes = ab["per_kernel"].get(dominant)
+    avg_s = kern[dominant]["avg_us"] * 1e-6
+    achieved = dom_bytes / avg_s / 1e9 if dom_bytes else None
+    print(f"[bench] kernels: " + ", ".join(f"{n}={v['per_step_us']:.1f}us" for n, v in kern.items()),
+          file=sys.stderr, flush=True)
+
+    path_gbs = ab["total"] / (ms * 1e-3) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": N / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "cfg3 c_fc: STACRLinear save+bwd, Conv1D 1024->4096, N=8192 tokens, bf16, r=8, "
+                        "budget 0.005 global_topk, int8 residual, fused dbias",
+            "tokens": N, "d_in": D_IN, "d_out": D_OUT, "rank": RANK, "k": k_saved,
+            "timing": "hip graph replay" if graph_ms is not None else "eager",
+        },
+        "pct_hbm_roofline": 100.0 * path_gbs / HBM_PEAK_GBS,
+        "path_algorithmic_bytes": ab["total"],
+        "eager_ms_per_step": eager_ms,
+        "roofline": {
+            "kernel": dominant,
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS if achieved else None,
+            "traffic": None,
+            "algorithmic_bytes_per_launch": dom_bytes,
+            "avg_launch_us": kern[dominant]["avg_us"],
+        },
+        "kernels_us_per_step": {n: round(v["per_step_us"], 3) for n, v in kern.items()},
+    }
+    if graph_note:
+        out["note"] = graph_note
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
+        out["cpu_baseline"] = cpu_baseline(x, q, g)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

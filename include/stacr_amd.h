@@ -126,6 +126,17 @@ int stacr_weight_grad(const void *g, int dtype, int64_t rows, int64_t d_out, con
                       int transposed, void *dw, int dw_dtype, void *dbias, int dbias_dtype,
                       void *workspace, size_t workspace_bytes, void *stream);
 
+/*
+ * Kernel timing (benchmarking aid; no counterpart in the reference).  Between begin and end,
+ * every kernel this library launches is bracketed by HIP events on its stream, preceded by a
+ * `sleep_us` device-side sleep so host enqueue gaps are not measured (up to max_launches
+ * launches are recorded).  end synchronises the recorded events and returns, per kernel name in
+ * first-launch order, the summed milliseconds and launch count (names: 64-byte slots).
+ * Single-threaded use only; do not enable during stream capture.
+ */
+int stacr_profile_begin(int max_launches, double sleep_us);
+int stacr_profile_end(int max_kernels, char *names, double *total_ms, int *launches, int *n_kernels);
+
 #ifdef __cplusplus
 }
 #endif

@@ -172,6 +172,21 @@ struct WgOffset {
 int stacr_fail(int code, const char *fmt, ...);
 int stacr_hip_check(hipError_t err, const char *what);
 
+// ------------------------------------------------------------------ timing hook (profile.hip)
+bool stacr_prof_on();
+void stacr_prof_before(hipStream_t s);
+void stacr_prof_after(const char *name, hipStream_t s);
+
+// Every kernel launch goes through here so the optional timing hook can bracket it.
+template <typename F>
+inline void stacr_launch(const char *name, hipStream_t s, F &&launch)
+{
+    const bool timed = stacr_prof_on();
+    if (timed) stacr_prof_before(s);
+    launch();
+    if (timed) stacr_prof_after(name, s);
+}
+
 // ------------------------------------------------------------------ launchers (save.hip)
 struct StacrSaveArgs {
     const void *x;

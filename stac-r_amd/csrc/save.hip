@@ -109,6 +109,7 @@ struct OutSpec {
     int bits;
     uint32_t *list_rbits;  // trim path: chunk survivors as (fp32 bits, flat index)
     uint32_t *list_idx;
+    uint32_t cap;          // entries the destination holds; positions at or past it are dropped
 };
 
 __device__ __forceinline__ float quant_scale(uint32_t maxkey, int bits, float amax_rounded)
@@ -439,7 +440,9 @@ __global__ __launch_bounds__(kBlock) void k_emit(SaveGeom g, const typename Act<
                     if (is_gt || (is_eq && eb < wo.take)) {
                         const uint32_t pos = wo.off + gb + min(eb, wo.take);
                         const uint32_t flat = (uint32_t)(row * g.d + col + e);
-                        if (to_list) {
+                        if (pos >= o.cap) {
+                            // unreachable when the counts are consistent; never write out of bounds
+                        } else if (to_list) {
                             o.list_rbits[pos] = __float_as_uint(r[e]);
                             o.list_idx[pos] = flat;
                         } else {
@@ -531,7 +534,7 @@ __global__ __launch_bounds__(kBlock) void k_list_emit(const uint32_t *__restrict
         const bool is_gt = key > T, is_eq = key == T;
         if (is_gt || (is_eq && eb < wo.take)) {
             const uint32_t pos = wo.off + gb + min(eb, wo.take);
-            write_entry<DT>(o, pos, lidx[i], __uint_as_float(rb), scale);
+            if (pos < o.cap) write_entry<DT>(o, pos, lidx[i], __uint_as_float(rb), scale);
         }
         gb += is_gt;
         eb += is_eq;
@@ -687,25 +690,25 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     const bool resid = a.k_total > 0;
     const int nwg = (int)p.n_wgs;
 
-    k_pad_basis<DT><<<grid_for(a.feats * R), kBlock, 0, s>>>(static_cast<const T *>(a.q), a.feats, a.rank, R, qp);
+    stacr_launch("k_pad_basis", s, [&] { k_pad_basis<DT><<<grid_for(a.feats * R), kBlock, 0, s>>>(static_cast<const T *>(a.q), a.feats, a.rank, R, qp); });
     if (resid) {
         // histogram and max key are contiguous in the layout: one clear
-        k_zero_u32<<<grid_for((int64_t)p.g.n_chunks * 3 * kBins + 64), kBlock, 0, s>>>(
-            hist, (int64_t)((off[WS_MAXKEY] + sizeof(uint32_t) - off[WS_HIST]) / sizeof(uint32_t)));
+        stacr_launch("k_zero_u32", s, [&] { k_zero_u32<<<grid_for((int64_t)p.g.n_chunks * 3 * kBins + 64), kBlock, 0, s>>>(
+            hist, (int64_t)((off[WS_MAXKEY] + sizeof(uint32_t) - off[WS_HIST]) / sizeof(uint32_t))); });
     }
     if (!coeff_in || resid)
-        k_proj_hist<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in);
+        stacr_launch("k_proj_hist", s, [&] { k_proj_hist<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in); });
     if (!resid) return stacr_hip_check(hipGetLastError(), "save kernels");
 
     const int nch = (int)p.g.n_chunks;
     const uint32_t kf = (uint32_t)a.k_full, kl = (uint32_t)a.k_last;
-    k_select_step<<<nch, kBlock, 0, s>>>(0, hist, state, p.g.n_chunks, kf, kl);
+    stacr_launch("k_select_step", s, [&] { k_select_step<<<nch, kBlock, 0, s>>>(0, hist, state, p.g.n_chunks, kf, kl); });
     for (int lvl = 1; lvl < 3; ++lvl) {
-        k_refine_hist<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, lvl, x, qp, coeff, hist, state);
-        k_select_step<<<nch, kBlock, 0, s>>>(lvl, hist, state, p.g.n_chunks, kf, kl);
+        stacr_launch("k_refine_hist", s, [&] { k_refine_hist<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, lvl, x, qp, coeff, hist, state); });
+        stacr_launch("k_select_step", s, [&] { k_select_step<<<nch, kBlock, 0, s>>>(lvl, hist, state, p.g.n_chunks, kf, kl); });
     }
-    k_count<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, counts);
-    k_offsets<<<nch, kBlock, 0, s>>>(counts, offs, state, p.g.wgs_per_chunk, kf);
+    stacr_launch("k_count", s, [&] { k_count<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, counts); });
+    stacr_launch("k_offsets", s, [&] { k_offsets<<<nch, kBlock, 0, s>>>(counts, offs, state, p.g.wgs_per_chunk, kf); });
 
     OutSpec o{};
     o.idx = a.idx;
@@ -716,7 +719,8 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     uint32_t *lix = carve<uint32_t>(ws, off[WS_LIDX]);
     o.list_rbits = lrb;
     o.list_idx = lix;
-    k_emit<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, offs, maxkey, o, a.scale, p.trim ? 1 : 0);
+    o.cap = (uint32_t)(p.trim ? a.k_sum : a.k_total);
+    stacr_launch("k_emit", s, [&] { k_emit<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, offs, maxkey, o, a.scale, p.trim ? 1 : 0); });
 
     if (p.trim) {
         uint32_t *thist = carve<uint32_t>(ws, off[WS_THIST]);
@@ -725,18 +729,19 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
         WgOffset *loffs = carve<WgOffset>(ws, off[WS_LOFFS]);
         const int nlb = (int)p.n_list_blocks;
         const uint32_t kt = (uint32_t)a.k_total;
-        k_zero_u32<<<grid_for(3 * kBins), kBlock, 0, s>>>(thist, 3 * kBins);
+        stacr_launch("k_zero_u32", s, [&] { k_zero_u32<<<grid_for(3 * kBins), kBlock, 0, s>>>(thist, 3 * kBins); });
         for (int lvl = 0; lvl < 3; ++lvl) {
-            k_list_hist<<<nlb, kBlock, 0, s>>>(lvl, lrb, a.k_sum, thist, tstate);
-            k_select_step<<<1, kBlock, 0, s>>>(lvl, thist, tstate, 1, kt, kt);
+            stacr_launch("k_list_hist", s, [&] { k_list_hist<<<nlb, kBlock, 0, s>>>(lvl, lrb, a.k_sum, thist, tstate); });
+            stacr_launch("k_select_step", s, [&] { k_select_step<<<1, kBlock, 0, s>>>(lvl, thist, tstate, 1, kt, kt); });
         }
-        k_list_count<<<nlb, kBlock, 0, s>>>(lrb, a.k_sum, tstate, lcounts);
-        k_offsets<<<1, kBlock, 0, s>>>(lcounts, loffs, tstate, p.n_list_blocks, kt);
-        k_list_emit<DT><<<nlb, kBlock, 0, s>>>(lrb, lix, a.k_sum, tstate, loffs, maxkey, o, a.scale);
+        stacr_launch("k_list_count", s, [&] { k_list_count<<<nlb, kBlock, 0, s>>>(lrb, a.k_sum, tstate, lcounts); });
+        stacr_launch("k_offsets", s, [&] { k_offsets<<<1, kBlock, 0, s>>>(lcounts, loffs, tstate, p.n_list_blocks, kt); });
+        o.cap = (uint32_t)a.k_total;
+        stacr_launch("k_list_emit", s, [&] { k_list_emit<DT><<<nlb, kBlock, 0, s>>>(lrb, lix, a.k_sum, tstate, loffs, maxkey, o, a.scale); });
     }
     if (a.bits == 4)
-        k_pack_int4<<<grid_for((a.k_total + 1) / 2), kBlock, 0, s>>>(carve<int8_t>(ws, off[WS_Q4]), a.k_total,
-                                                                   static_cast<uint8_t *>(a.data));
+        stacr_launch("k_pack_int4", s, [&] { k_pack_int4<<<grid_for((a.k_total + 1) / 2), kBlock, 0, s>>>(carve<int8_t>(ws, off[WS_Q4]), a.k_total,
+                                                                   static_cast<uint8_t *>(a.data)); });
     return stacr_hip_check(hipGetLastError(), "save kernels");
 }
 
@@ -793,10 +798,10 @@ template <int DT>
 static int quantize_typed(const void *v, int64_t n, int bits, void *data, float *scale, uint32_t *maxkey, hipStream_t s)
 {
     using T = typename Act<DT>::T;
-    k_zero_u32<<<1, kBlock, 0, s>>>(maxkey, 1);
-    k_absmax<DT><<<grid_for(n), kBlock, 0, s>>>(static_cast<const T *>(v), n, maxkey);
-    k_quantize<DT><<<grid_for(bits == 4 ? (n + 1) / 2 : n), kBlock, 0, s>>>(static_cast<const T *>(v), n, bits, maxkey,
-                                                                          data, scale);
+    stacr_launch("k_zero_u32", s, [&] { k_zero_u32<<<1, kBlock, 0, s>>>(maxkey, 1); });
+    stacr_launch("k_absmax", s, [&] { k_absmax<DT><<<grid_for(n), kBlock, 0, s>>>(static_cast<const T *>(v), n, maxkey); });
+    stacr_launch("k_quantize", s, [&] { k_quantize<DT><<<grid_for(bits == 4 ? (n + 1) / 2 : n), kBlock, 0, s>>>(static_cast<const T *>(v), n, bits, maxkey,
+                                                                          data, scale); });
     return stacr_hip_check(hipGetLastError(), "quantize kernels");
 }
 

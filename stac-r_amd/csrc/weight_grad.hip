@@ -32,7 +32,8 @@ __global__ void k_csr_rows(const void *__restrict__ idx, int64_t nnz, int64_t d_
         return IDX64 ? static_cast<const int64_t *>(idx)[k] : (int64_t) static_cast<const int32_t *>(idx)[k];
     };
     const int64_t f = flat_at(e);
-    const int64_t t = f / d_in;
+    // an index outside rows x d_in maps past the last row and touches no row offset
+    const int64_t t = (f < 0 || f >= rows * d_in) ? rows : f / d_in;
     col[e] = (uint32_t)(f - t * d_in);
     float v;
     if (bits == 8) {
@@ -46,10 +47,14 @@ __global__ void k_csr_rows(const void *__restrict__ idx, int64_t nnz, int64_t d_
         v = load_any(data, val_dt, e);
     }
     val[e] = v;
-    const int64_t tprev = e ? flat_at(e - 1) / d_in : -1;
-    for (int64_t tt = tprev + 1; tt <= t; ++tt) rowptr[tt] = (uint32_t)e;
+    int64_t tprev = -1;
+    if (e) {
+        const int64_t fp = flat_at(e - 1);
+        tprev = (fp < 0 || fp >= rows * d_in) ? rows : fp / d_in;
+    }
+    for (int64_t tt = tprev + 1; tt <= t && tt < rows; ++tt) rowptr[tt] = (uint32_t)e;
     if (e == nnz - 1)
-        for (int64_t tt = t + 1; tt <= rows; ++tt) rowptr[tt] = (uint32_t)nnz;
+        for (int64_t tt = t < rows ? t + 1 : rows; tt <= rows; ++tt) rowptr[tt] = (uint32_t)nnz;
 }
 
 // Partial M[j][o] = sum over a token split of G[t][o] * C[t][j]; row j == R holds sum G[t][o].
@@ -99,11 +104,13 @@ __global__ void k_reduce_m(const float *__restrict__ mpart, int64_t n_splits, in
     }
 }
 
-// Sparse term for one (64 x kSparseI) tile of dW, accumulated in LDS.  Waves take tokens in
-// turn; an LDS float atomic add resolves two waves updating the same entry.
+// Sparse term for one (64 x kSparseI) tile of dW, accumulated in LDS.  Each wave owns a quarter
+// of the tile's input features and walks every token in order, so each accumulator has a single
+// writer and a fixed summation order (deterministic results, no atomics).
 template <int DT>
 __global__ __launch_bounds__(kBlock) void k_sparse(const typename Act<DT>::T *__restrict__ g, int64_t rows,
-                                                   int64_t d_out, int64_t d_in, const uint32_t *__restrict__ rowptr,
+                                                   int64_t d_out, int64_t d_in, uint32_t nnz,
+                                                   const uint32_t *__restrict__ rowptr,
                                                    const uint32_t *__restrict__ col, const float *__restrict__ val,
                                                    float *__restrict__ s_out, int transposed)
 {
@@ -116,17 +123,22 @@ __global__ __launch_bounds__(kBlock) void k_sparse(const typename Act<DT>::T *__
     const uint32_t i1 = min<uint32_t>(i0 + kSparseI, (uint32_t)d_in);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr uint32_t span = (kSparseI + kWaves - 1) / kWaves;
+    const uint32_t w_lo = min<uint32_t>(i0 + wave * span, i1);
+    const uint32_t w_hi = min<uint32_t>(w_lo + span, i1);
     const int64_t o = o0 + lane;
-    for (int64_t t = wave; t < rows; t += kWaves) {
-        uint32_t e = rowptr[t];
-        const uint32_t e1 = rowptr[t + 1];
-        while (e < e1 && col[e] < i0) ++e;
-        if (e >= e1 || col[e] >= i1) continue;
+    for (int64_t t = 0; t < rows && w_lo < w_hi; ++t) {
+        // clamped so that inconsistent offsets (unsorted indices) cannot read past the arrays
+        const uint32_t e1 = min(rowptr[t + 1], nnz);
+        uint32_t e = min(rowptr[t], e1);
+        while (e < e1 && col[e] < w_lo) ++e;
+        if (e >= e1 || col[e] >= w_hi) continue;
         const float gv = o < d_out ? A::ld(g[t * d_out + o]) : 0.f;
         for (; e < e1; ++e) {
             const uint32_t c = col[e];
-            if (c >= i1) break;
-            atomicAdd(&acc[(c - i0) * kLdsPitch + lane], val[e] * gv);
+            if (c >= w_hi) break;
+            float *a = &acc[(c - i0) * kLdsPitch + lane];
+            *a = *a + val[e] * gv;
         }
     }
     __syncthreads();
@@ -231,14 +243,14 @@ int launch_grad(const StacrGradArgs &a, const GPlan &p, char *ws, const size_t *
     float *mpart = reinterpret_cast<float *>(ws + off[GW_MPART]);
     float *m = reinterpret_cast<float *>(ws + off[GW_M]);
     float *sbuf = nullptr;
-    k_pad_basis_g<DT><<<grid_for(a.d_in * R), kBlock, 0, s>>>(static_cast<const T *>(a.q), a.d_in, a.rank, R, qp);
+    stacr_launch("k_pad_basis_g", s, [&] { k_pad_basis_g<DT><<<grid_for(a.d_in * R), kBlock, 0, s>>>(static_cast<const T *>(a.q), a.d_in, a.rank, R, qp); });
     if (a.rows > 0) {
         dim3 grid((unsigned)p.o_blocks, (unsigned)p.n_splits);
-        k_lowrank<DT, R><<<grid, kBlock, 0, s>>>(static_cast<const T *>(a.g), a.rows, a.d_out,
-                                                 static_cast<const T *>(a.coeff), a.rank, p.tokens_per_split, mpart);
-        k_reduce_m<<<grid_for((R + 1) * a.d_out), kBlock, 0, s>>>(mpart, p.n_splits, (int64_t)(R + 1) * a.d_out, m);
+        stacr_launch("k_lowrank", s, [&] { k_lowrank<DT, R><<<grid, kBlock, 0, s>>>(static_cast<const T *>(a.g), a.rows, a.d_out,
+                                                 static_cast<const T *>(a.coeff), a.rank, p.tokens_per_split, mpart); });
+        stacr_launch("k_reduce_m", s, [&] { k_reduce_m<<<grid_for((R + 1) * a.d_out), kBlock, 0, s>>>(mpart, p.n_splits, (int64_t)(R + 1) * a.d_out, m); });
     } else {
-        k_reduce_m<<<grid_for((R + 1) * a.d_out), kBlock, 0, s>>>(mpart, 0, (int64_t)(R + 1) * a.d_out, m);
+        stacr_launch("k_reduce_m", s, [&] { k_reduce_m<<<grid_for((R + 1) * a.d_out), kBlock, 0, s>>>(mpart, 0, (int64_t)(R + 1) * a.d_out, m); });
     }
     if (a.nnz > 0) {
         uint32_t *rowptr = reinterpret_cast<uint32_t *>(ws + off[GW_ROWPTR]);
@@ -247,17 +259,18 @@ int launch_grad(const StacrGradArgs &a, const GPlan &p, char *ws, const size_t *
         sbuf = reinterpret_cast<float *>(ws + off[GW_S]);
         const int cg = (int)((a.nnz + kBlock - 1) / kBlock);
         if (a.index_bytes == 8)
-            k_csr_rows<1><<<cg, kBlock, 0, s>>>(a.idx, a.nnz, a.d_in, a.rows, a.data, a.scale, a.bits, a.val_dtype,
-                                               rowptr, col, val);
+            stacr_launch("k_csr_rows", s, [&] { k_csr_rows<1><<<cg, kBlock, 0, s>>>(a.idx, a.nnz, a.d_in, a.rows, a.data, a.scale, a.bits, a.val_dtype,
+                                               rowptr, col, val); });
         else
-            k_csr_rows<0><<<cg, kBlock, 0, s>>>(a.idx, a.nnz, a.d_in, a.rows, a.data, a.scale, a.bits, a.val_dtype,
-                                               rowptr, col, val);
+            stacr_launch("k_csr_rows", s, [&] { k_csr_rows<0><<<cg, kBlock, 0, s>>>(a.idx, a.nnz, a.d_in, a.rows, a.data, a.scale, a.bits, a.val_dtype,
+                                               rowptr, col, val); });
         dim3 grid((unsigned)((a.d_out + kSparseO - 1) / kSparseO), (unsigned)((a.d_in + kSparseI - 1) / kSparseI));
-        k_sparse<DT><<<grid, kBlock, 0, s>>>(static_cast<const T *>(a.g), a.rows, a.d_out, a.d_in, rowptr, col, val,
-                                             sbuf, a.transposed);
+        stacr_launch("k_sparse", s, [&] { k_sparse<DT><<<grid, kBlock, 0, s>>>(static_cast<const T *>(a.g), a.rows, a.d_out, a.d_in, (uint32_t)a.nnz,
+                                             rowptr, col, val,
+                                             sbuf, a.transposed); });
     }
-    k_expand<R><<<grid_for(a.d_out * a.d_in), kBlock, 0, s>>>(m, qp, sbuf, a.d_out, a.d_in, a.transposed, a.dw,
-                                                             a.dw_dtype, a.dbias, a.dbias_dtype);
+    stacr_launch("k_expand", s, [&] { k_expand<R><<<grid_for(a.d_out * a.d_in), kBlock, 0, s>>>(m, qp, sbuf, a.d_out, a.d_in, a.transposed, a.dw,
+                                                             a.dw_dtype, a.dbias, a.dbias_dtype); });
     return stacr_hip_check(hipGetLastError(), "weight_grad kernels");
 }
 

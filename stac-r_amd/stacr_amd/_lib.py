@@ -36,6 +36,8 @@ SIGNATURES = {
     "stacr_select_residual": ([_p, _p, _p, _i32, _i64, _i64, _i32, _i32, _f64, _i64, _i32, _p, _i32, _p, _p, _p,
                                _sz, _p], _i32),
     "stacr_quantize_values": ([_p, _i32, _i64, _i32, _p, _p, _p, _sz, _p], _i32),
+    "stacr_profile_begin": ([_i32, _f64], _i32),
+    "stacr_profile_end": ([_i32, _p, _p, _p, _p], _i32),
     "stacr_weight_grad_workspace_bytes": ([_i64, _i64, _i64, _i32, _i64, _PSZ], _i32),
     "stacr_weight_grad": ([_p, _i32, _i64, _i64, _p, _p, _i64, _i32, _p, _i32, _p, _p, _i32, _i32, _i64, _i32, _p,
                            _i32, _p, _i32, _p, _sz, _p], _i32),
@@ -64,6 +66,33 @@ def load() -> ctypes.CDLL:
             raise StacrLibraryError("libstacr_amd.so ABI version mismatch")
         _lib = lib
     return _lib
+
+
+class KernelTimer:
+    """Context manager around stacr_profile_begin/end: per-kernel (total ms, launches)."""
+
+    def __init__(self, max_launches: int = 4096, sleep_us: float = 20.0):
+        self.max_launches, self.sleep_us = int(max_launches), float(sleep_us)
+        self.results: dict[str, tuple[float, int]] = {}
+
+    def __enter__(self):
+        check(load().stacr_profile_begin(self.max_launches, self.sleep_us), "stacr_profile_begin")
+        return self
+
+    def __exit__(self, *exc):
+        cap = 64
+        names = ctypes.create_string_buffer(64 * cap)
+        ms = (ctypes.c_double * cap)()
+        cnt = (ctypes.c_int * cap)()
+        n = ctypes.c_int()
+        check(load().stacr_profile_end(cap, ctypes.cast(names, ctypes.c_void_p), ctypes.cast(ms, ctypes.c_void_p),
+                                       ctypes.cast(cnt, ctypes.c_void_p), ctypes.cast(ctypes.byref(n), ctypes.c_void_p)),
+              "stacr_profile_end")
+        raw = names.raw
+        for i in range(n.value):
+            name = raw[64 * i: 64 * (i + 1)].split(b"\0", 1)[0].decode()
+            self.results[name] = (ms[i], cnt[i])
+        return False
 
 
 def check(rc: int, what: str) -> None:

@@ -1,0 +1,482 @@
+"""Parity of the HIP save / weight-gradient path against the CPU oracle (needs an MI355X).
+
+Bars:
+  * coefficients: rel-L2 against the fp64 projection of the same (dtype-rounded) operands,
+    <= 1e-5 in fp32 and <= 2e-2 in bf16/fp16;
+  * selected indices, int8 / packed int4 bytes, bits-0 values and the fp32 scale: bit-exact
+    against the oracle run on the kernel's own coefficients (identical residual arithmetic);
+  * dW / dbias: rel-L2 against the fp64 oracle, <= 1e-5 (fp32) and <= 2e-2 (bf16/fp16).
+All calls go through the C ABI (stacr_amd.kernels / the drop-in layer).
+"""
+import numpy as np
+import pytest
+import torch
+
+from gpu_cases import make_activation, make_basis, make_grad
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+DT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+TOL = {"f32": 1e-5, "bf16": 2e-2, "f16": 2e-2}
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU visible")
+    return torch.device("cuda:0")
+
+
+def rel_l2(a, b) -> float:
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def announce(*parts):
+    print("CASE", *parts, flush=True)
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+def run_and_check_save(dev, rows, d, rank, dtype, mode, budget, chunk, bits, lognormal=False, seed=1234):
+    from stacr_amd import kernels
+
+    announce("save", rows, d, rank, dtype, mode, budget, chunk, bits)
+    x = make_activation(rows, d, lognormal=lognormal, seed=seed)
+    q = make_basis(d, rank)
+    xd, qd = x.to(dev, DT[dtype]), q.to(dev, DT[dtype])
+    coeff, idx, data, scale = kernels.save(xd, qd, mode=mode, budget=budget, chunk_rows=chunk, bits=bits)
+    torch.cuda.synchronize()
+    xf, qf, cf = _np(xd), _np(qd), _np(coeff)
+    assert coeff.shape == (rows, rank) and coeff.dtype == DT[dtype]
+    assert rel_l2(cf, orc.project_f64(xf, qf)) <= TOL[dtype]
+    omode = "chunk_topk" if mode == "topk" else mode
+    _, oidx, odata, oscale = orc.save(xf, qf, dtype, omode, budget, chunk, bits, coeff=cf)
+    if oidx.size == 0:
+        assert idx is None
+        return
+    assert idx.dtype == torch.int32
+    assert np.array_equal(idx.cpu().numpy().astype(np.int64), oidx)
+    if bits == 0:
+        assert data.dtype == DT[dtype]
+        assert np.array_equal(_np(data), odata)
+        assert scale.item() == 1.0
+    else:
+        assert np.array_equal(data.cpu().numpy().view(np.int8 if bits == 8 else np.uint8), odata)
+        assert np.float32(scale.item()) == oscale
+    return idx, data, scale, coeff, xd, qd
+
+
+SAVE_CASES = [
+    # name: rows, d, rank, dtype, mode, budget, chunk_rows, bits, lognormal
+    ("cfg1_fp32_chunk", 4096, 768, 8, "f32", "chunk_topk", 0.005, 512, 8, False),
+    ("cfg3_cfc_bf16_global", 8192, 1024, 8, "bf16", "global_topk", 0.005, 512, 8, True),
+    ("cfg3_cproj_bf16_global", 2048, 4096, 8, "bf16", "global_topk", 0.005, 512, 8, True),
+    ("cfg4_shape_bf16_chunk", 1024, 8192, 16, "bf16", "chunk_topk", 0.005, 512, 8, False),
+    ("chunk_trim_bf16", 1536, 4096, 8, "bf16", "chunk_topk", 0.005, 512, 8, False),
+    ("chunk_trim_small", 37, 24, 4, "f32", "chunk_topk", 0.05, 8, 8, False),
+    ("f16_scalar_path_int4", 300, 20, 3, "f16", "chunk_topk", 0.1, 64, 4, False),
+    ("bf16_bits0_global", 1000, 96, 5, "bf16", "global_topk", 0.02, 512, 0, False),
+    ("ref_tiny_bits0", 5, 16, 4, "f32", "chunk_topk", 0.25, 2, 0, False),
+    ("ref_tiny_bits4", 5, 16, 4, "f32", "chunk_topk", 0.25, 2, 4, False),
+    ("ref_tiny_global", 5, 16, 4, "f32", "global_topk", 0.25, 2, 8, False),
+    ("fp32_odd_width", 64, 30, 2, "f32", "topk", 0.1, 16, 8, False),
+    ("fp32_wide_rows", 64, 8192, 16, "f32", "global_topk", 0.01, 512, 8, False),
+    ("bf16_rank32", 512, 256, 32, "bf16", "chunk_topk", 0.01, 128, 8, False),
+    ("fp32_rank1", 256, 64, 1, "f32", "global_topk", 0.05, 512, 8, False),
+    ("partial_last_chunk", 1000, 128, 8, "bf16", "chunk_topk", 0.01, 300, 8, False),
+    ("no_residual_budget", 64, 64, 4, "f32", "chunk_topk", 0.0, 16, 8, False),
+]
+
+
+@pytest.mark.parametrize("case", SAVE_CASES, ids=[c[0] for c in SAVE_CASES])
+def test_save_matches_oracle(dev, case):
+    run_and_check_save(dev, *case[1:])
+
+
+def test_save_is_deterministic(dev):
+    from stacr_amd import kernels
+
+    announce("determinism")
+    x = make_activation(4096, 1024).to(dev, torch.bfloat16)
+    q = make_basis(1024, 8).to(dev, torch.bfloat16)
+    a = kernels.save(x, q, mode="global_topk", budget=0.005, chunk_rows=512, bits=8)
+    b = kernels.save(x, q, mode="global_topk", budget=0.005, chunk_rows=512, bits=8)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+
+
+# ------------------------------------------------------------------ reference known answers on the GPU
+def test_global_topk_vs_chunk_known_answer(dev):
+    """Reference tests/test_integration.py:106-114 through _select_residual."""
+    from stacr_amd.layers import _select_residual
+
+    announce("kat global vs chunk")
+    x = torch.tensor([[100.0, 90.0, 80.0, 70.0], [4.0, 3.0, 2.0, 1.0]], device=dev)
+    q, c = torch.zeros(4, 1, device=dev), torch.zeros(2, 1, device=dev)
+    i, v = _select_residual(x, c, q, 0.5, 1, "global_topk", 2, 0.1)
+    assert set(i.tolist()) == {0, 1, 2, 3}
+    assert set(v.tolist()) == {100.0, 90.0, 80.0, 70.0}
+    local, _ = _select_residual(x, c, q, 0.5, 1, "chunk_topk", 2, 0.1)
+    assert set(local.tolist()) == {0, 1, 4, 5}
+
+
+def test_ties_take_lowest_flat_index(dev):
+    from stacr_amd.layers import _select_residual
+
+    announce("ties")
+    x = torch.ones(4, 8, device=dev)
+    x[:, ::2] *= -1.0
+    q, c = torch.zeros(8, 1, device=dev), torch.zeros(4, 1, device=dev)
+    i, _ = _select_residual(x, c, q, 0.25, 512, "global_topk")
+    assert i.tolist() == list(range(8))
+    i, _ = _select_residual(x, c, q, 0.25, 2, "chunk_topk")
+    assert i.tolist() == [0, 1, 2, 3, 16, 17, 18, 19]
+
+
+def test_exact_span_gives_zero_residual_lowest_indices(dev):
+    """X exactly in the span of a unit-vector basis: every residual is 0, all keys tie."""
+    from stacr_amd import kernels
+
+    announce("zero residual")
+    d, rank, rows = 64, 4, 32
+    q = torch.zeros(d, rank)
+    q[[3, 9, 17, 31], [0, 1, 2, 3]] = 1.0
+    c = torch.randint(-5, 5, (rows, rank)).float()
+    x = (c @ q.t()).to(dev)
+    coeff, idx, data, scale = kernels.save(x, q.to(dev), mode="global_topk", budget=0.05, chunk_rows=512, bits=8)
+    k = orc.residual_plan(rows, d, "global_topk", 0.05, 512)[0]
+    assert torch.equal(coeff.cpu(), c)
+    assert idx.tolist() == list(range(k))
+    assert not data.any() and scale.item() == np.float32(np.finfo(np.float32).tiny)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+def test_quantize_values_known_answers(dev, dtype):
+    import stacr_amd
+
+    announce("quantize", dtype)
+    v = torch.tensor([0.0, 1e-6, -1e-6], dtype=DT[dtype], device=dev)
+    p = stacr_amd.quantize_values(v, 8)
+    assert p.scale.dtype == torch.float32 and p.scale.item() > 0
+    assert torch.allclose(p.dequantize(torch.float32), v.float(), atol=1e-8)
+    s = 2.0**-7
+    v = torch.tensor([127, 0.5, 1.5, 2.5, -3.5, -127, 64.25], device=dev) * s
+    p = stacr_amd.quantize_values(v, 8)
+    assert p.scale.item() == s and p.data.tolist() == [127, 0, 2, 2, -4, -127, 64]
+    p = stacr_amd.quantize_values(torch.tensor([7, -7, 0.5, 1.5, 2.5], device=dev) * 0.125, 4)
+    assert p.scale.item() == 0.125 and p.data.tolist() == [0x97, 0x20, 0x02]
+    rnd = torch.randn(1001, generator=torch.Generator().manual_seed(3)).to(dev, DT[dtype])
+    for bits in (4, 8):
+        p = stacr_amd.quantize_values(rnd, bits)
+        oq, oscale = orc.quantize(_np(rnd), bits)
+        got = p.data.cpu().numpy()
+        want = oq if bits == 8 else orc.pack_int4(oq)
+        assert np.array_equal(got.view(np.int8) if bits == 8 else got, want)
+        assert np.float32(p.scale.item()) == oscale
+
+
+# ------------------------------------------------------------------ weight gradient
+GRAD_CASES = [
+    # name: rows, d_in, d_out, rank, dtype, transposed, bits, mode, budget
+    ("cfg1_fp32", 4096, 768, 3072, 8, "f32", False, 8, "chunk_topk", 0.005),
+    ("cfg3_cfc_bf16_conv1d", 2048, 1024, 4096, 8, "bf16", True, 8, "global_topk", 0.005),
+    ("cfg3_cproj_bf16_conv1d", 1024, 4096, 1024, 8, "bf16", True, 8, "global_topk", 0.005),
+    ("fp32_bits0", 512, 256, 384, 4, "f32", False, 0, "chunk_topk", 0.02),
+    ("f16_bits4_rank3", 300, 40, 70, 3, "f16", False, 4, "chunk_topk", 0.1),
+    ("fp32_lowrank_only", 256, 128, 96, 8, "f32", True, 8, "chunk_topk", 0.0),
+    ("bf16_rank16", 1024, 2048, 512, 16, "bf16", False, 8, "chunk_topk", 0.005),
+]
+
+
+@pytest.mark.parametrize("case", GRAD_CASES, ids=[c[0] for c in GRAD_CASES])
+def test_weight_grad_matches_oracle(dev, case):
+    from stacr_amd import kernels
+
+    _, rows, d_in, d_out, rank, dtype, transposed, bits, mode, budget = case
+    announce("grad", *case)
+    x = make_activation(rows, d_in).to(dev, DT[dtype])
+    q = make_basis(d_in, rank).to(dev, DT[dtype])
+    g = make_grad(rows, d_out).to(dev, DT[dtype])
+    coeff, idx, data, scale = kernels.save(x, q, mode=mode, budget=budget, chunk_rows=512, bits=bits)
+    residual = None if idx is None else (idx, data, scale)
+    dw, db = kernels.weight_grad(g, coeff, q, residual, bits, transposed, DT[dtype], DT[dtype])
+    torch.cuda.synchronize()
+    if idx is None:
+        oidx, ovals = np.zeros(0, np.int64), np.zeros(0, np.float32)
+    else:
+        oidx = idx.cpu().numpy().astype(np.int64)
+        raw = data.cpu().numpy()
+        if bits == 0:
+            ovals = _np(data)
+        else:
+            ovals = orc.dequantize(raw.view(np.int8) if bits == 8 else raw, np.float32(scale.item()), bits, oidx.size)
+    odw, odb = orc.weight_grad(_np(g), _np(coeff), _np(q), oidx, ovals, d_in)
+    got = _np(dw)
+    assert got.shape == ((d_in, d_out) if transposed else (d_out, d_in))
+    assert rel_l2(got.T if transposed else got, odw) <= TOL[dtype]
+    assert rel_l2(_np(db), odb) <= TOL[dtype]
+
+
+def test_weight_grad_int64_indices(dev):
+    """The backward accepts int64 flat indices (used when rows*d >= 2^31-1)."""
+    from stacr_amd import kernels
+
+    announce("int64 indices")
+    rows, d_in, d_out, rank = 256, 64, 48, 4
+    x = make_activation(rows, d_in).to(dev)
+    q = make_basis(d_in, rank).to(dev)
+    g = make_grad(rows, d_out).to(dev)
+    coeff, idx, data, scale = kernels.save(x, q, mode="chunk_topk", budget=0.05, chunk_rows=64, bits=8)
+    a, _ = kernels.weight_grad(g, coeff, q, (idx, data, scale), 8, False, torch.float32)
+    b, _ = kernels.weight_grad(g, coeff, q, (idx.long(), data, scale), 8, False, torch.float32)
+    assert torch.equal(a, b)
+
+
+# ------------------------------------------------------------------ the drop-in layer on the GPU
+def _lowrank(rows, feats, rank, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(rows, rank, generator=g) @ torch.randn(rank, feats, generator=g) / rank**0.5
+
+
+def test_layer_input_gradient_and_forward_are_native(dev):
+    from stacr_amd import STACRLinear
+
+    announce("layer native grads")
+    torch.manual_seed(0)
+    w = torch.nn.Parameter((torch.randn(64, 256) * 0.05).to(dev))
+    b = torch.nn.Parameter(torch.randn(64, device=dev))
+    layer = STACRLinear(w, b, rank=8, residual_budget=0.005)
+    x = _lowrank(128, 256, 12).to(dev).requires_grad_(True)
+    y = layer(x)
+    g = torch.randn_like(y)
+    y.backward(g)
+    x2 = x.detach().clone().requires_grad_(True)
+    w2, b2 = w.detach().clone().requires_grad_(True), b.detach().clone().requires_grad_(True)
+    y2 = torch.nn.functional.linear(x2, w2, b2)
+    y2.backward(g)
+    assert torch.equal(y, y2)
+    assert torch.equal(x.grad, x2.grad)
+    assert torch.equal(b.grad, b2.grad)
+
+
+def test_layer_weight_gradient_matches_factor_identity(dev):
+    """Reference tests/test_layers.py:49-69 (brute-force top-k, bits 0)."""
+    from stacr_amd import STACRLinear
+
+    announce("layer factor identity")
+    torch.manual_seed(0)
+    rows, feats, out_f = 128, 256, 64
+    w = torch.nn.Parameter((torch.randn(out_f, feats) * 0.05).to(dev))
+    layer = STACRLinear(w, None, rank=8, residual_budget=0.01, residual_bits=0)
+    x = _lowrank(rows, feats, 12)
+    y = layer(x.to(dev))
+    g = torch.randn_like(y)
+    y.backward(g)
+    q = layer.basis.float().cpu()
+    coeff = x @ q
+    recon = coeff @ q.t()
+    resid = x - recon
+    k = max(1, int(round(0.01 * resid.numel())))
+    _, top = torch.topk(resid.reshape(-1).abs(), k)
+    sparse = torch.zeros_like(resid).reshape(-1)
+    sparse[top] = resid.reshape(-1)[top]
+    expected = g.cpu().t() @ (recon + sparse.reshape_as(resid))
+    assert torch.allclose(w.grad.cpu(), expected, atol=1e-3)
+
+
+@pytest.mark.parametrize("mode", ["chunk_topk", "global_topk", "none"])
+@pytest.mark.parametrize("bits", [0, 4, 8])
+def test_all_selectors_contract_from_the_saved_factors(dev, mode, bits):
+    """Reference tests/test_integration.py:120-143: dW equals G^T (C Q^T + R_s) rebuilt from the
+    saved tensors."""
+    from stacr_amd import STACRLinear
+    from stacr_amd.quant import QuantizedValues
+
+    announce("selectors contract", mode, bits)
+    torch.manual_seed(4)
+    layer = STACRLinear.from_linear(torch.nn.Linear(16, 7).to(dev), rank=4, residual_budget=0.25, residual_bits=bits,
+                                    residual_mode=mode, chunk_rows=2, residual_block_size=4)
+    out = layer(torch.randn(5, 16, device=dev))
+    coeff, _, q, *sparse = out.grad_fn.saved_tensors
+    recon = coeff @ q.T
+    if sparse:
+        indices, data, scale = sparse
+        vals = QuantizedValues(data, scale, bits, indices.numel()).dequantize(recon.dtype)
+        recon.reshape(-1)[indices.long()] += vals
+    g = torch.randn_like(out)
+    out.backward(g)
+    assert torch.allclose(layer.weight.grad, g.T @ recon, atol=2e-5, rtol=1e-5)
+
+
+def test_turbo_drops_the_residual_channel(dev):
+    from stacr_amd import STACRLinear
+
+    announce("turbo")
+    w = torch.nn.Parameter((torch.randn(64, 256) * 0.05).to(dev))
+    layer = STACRLinear(w, None, rank=8, residual_budget=0.01, turbo_after_step=2)
+    x = _lowrank(64, 256, 8).to(dev)
+    layer.set_step(0)
+    out = layer(x)
+    assert len(out.grad_fn.saved_tensors) == 6 and out.grad_fn.has_residual
+    layer.set_step(5)
+    out = layer(x)
+    assert len(out.grad_fn.saved_tensors) == 3 and not out.grad_fn.has_residual
+    out.square().sum().backward()
+    assert torch.isfinite(w.grad).all() and w.grad.abs().sum() > 0
+
+
+def test_backward_never_stores_the_dense_activation(dev):
+    from stacr_amd import STACRLinear
+
+    announce("no dense save")
+    rows, feats = 256, 512
+    w = torch.nn.Parameter((torch.randn(128, feats) * 0.05).to(dev))
+    layer = STACRLinear(w, None, rank=8, residual_budget=0.005)
+    out = layer(_lowrank(rows, feats, 16).to(dev))
+    for t in out.grad_fn.saved_tensors:
+        assert t.numel() < rows * feats
+
+
+def test_outstanding_forwards_keep_their_basis_versions(dev):
+    from stacr_amd import STACRLinear
+
+    announce("basis versions")
+    layer = STACRLinear.from_linear(torch.nn.Linear(16, 7).to(dev), rank=4, residual_budget=0)
+    x = torch.randn(5, 16, device=dev, requires_grad=True)
+    a = layer(x)
+    saved = a.grad_fn.saved_tensors[2].clone()
+    first = layer.basis
+    layer.set_step(1)
+    b = layer(x * 3)
+    assert layer.basis is not first
+    assert torch.equal(saved, first)
+    (a.square().sum() + b.square().sum()).backward()
+    assert torch.isfinite(layer.weight.grad).all() and torch.isfinite(x.grad).all()
+
+
+@pytest.mark.parametrize("use_reentrant", [False, True])
+def test_checkpoint_replay_matches_direct_gradient(dev, use_reentrant):
+    import copy
+
+    from torch.utils.checkpoint import checkpoint
+
+    from stacr_amd import STACRLinear
+
+    announce("checkpoint replay", use_reentrant)
+    direct = STACRLinear.from_linear(torch.nn.Linear(16, 7).to(dev), rank=4, residual_budget=0.2)
+    replay = copy.deepcopy(direct)
+    x = torch.randn(5, 16, device=dev, requires_grad=True)
+    y = x.detach().clone().requires_grad_(True)
+    direct(x).square().sum().backward()
+    checkpoint(replay, y, use_reentrant=use_reentrant).square().sum().backward()
+    assert torch.allclose(replay.weight.grad, direct.weight.grad)
+    assert torch.allclose(y.grad, x.grad)
+    assert torch.equal(replay.basis, direct.basis)
+
+
+def test_state_dict_resumes_basis_and_step(dev):
+    from stacr_amd import STACRLinear
+
+    announce("state dict resume")
+    torch.manual_seed(1)
+    lin = torch.nn.Linear(16, 7).to(dev)
+    original = STACRLinear.from_linear(lin, rank=4, residual_budget=0)
+    original.set_step(9)
+    original(torch.randn(5, 16, device=dev)).sum().backward()
+    restored = STACRLinear.from_linear(torch.nn.Linear(16, 7).to(dev), rank=4, residual_budget=0)
+    restored.load_state_dict(original.state_dict())
+    assert restored.step == 9 and bool(restored.basis_ready)
+    assert torch.equal(restored.basis, original.basis)
+    x = torch.randn(5, 16, device=dev)
+    for layer in (original, restored):
+        layer.zero_grad()
+        layer.set_step(10)
+        layer(x).sum().backward()
+    assert torch.equal(restored.basis, original.basis)
+
+
+@pytest.mark.parametrize("transposed", [False, True])
+def test_autocast_forward_input_and_bias_gradient_match_native(dev, transposed):
+    """Reference tests/test_integration.py:83-103 under bf16 autocast on the GPU."""
+    from stacr_amd import STACRLinear
+
+    announce("autocast", transposed)
+    torch.manual_seed(14)
+    w = torch.nn.Parameter(torch.randn((16, 7) if transposed else (7, 16), device=dev))
+    b = torch.nn.Parameter(torch.randn(7, device=dev))
+    layer = STACRLinear(w, b, rank=4, transposed=transposed)
+    x = torch.randn(3, 2, 16, device=dev, requires_grad=True)
+    xr = x.detach().clone().requires_grad_(True)
+    wr, br = w.detach().clone().requires_grad_(True), b.detach().clone().requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        actual = layer(x)
+        expected = (torch.addmm(br, xr.reshape(-1, 16), wr).reshape(3, 2, 7) if transposed
+                    else torch.nn.functional.linear(xr, wr, br))
+    assert torch.equal(actual, expected)
+    g = torch.randn_like(actual)
+    actual.backward(g)
+    expected.backward(g)
+    assert torch.equal(x.grad, xr.grad)
+    assert torch.equal(b.grad, br.grad)
+    assert w.grad.dtype == w.dtype and w.grad.shape == w.shape
+
+
+def test_stored_bytes_equals_saved_inventory_under_autocast(dev):
+    """Reference tests/test_memory.py:366-388 for the top-k selectors."""
+    from stacr_amd import STACRLinear
+
+    for mode in ("chunk_topk", "global_topk"):
+        announce("inventory", mode)
+        layer = STACRLinear.from_linear(torch.nn.Linear(16, 7).to(dev), rank=4, residual_mode=mode, chunk_rows=1,
+                                        residual_block_size=4, residual_budget=0.17)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            output = layer(torch.randn(5, 16, device=dev))
+        coeff, weight, basis, indices, values, scale = output.grad_fn.saved_tensors
+        inventory = sum(t.numel() * t.element_size() for t in (coeff, basis, indices, values, scale))
+        estimate = layer.stored_bytes(5, value_bytes=2)
+        assert estimate["residual_count"] == indices.numel()
+        assert estimate["total"] == inventory + layer.basis.numel() * layer.basis.element_size()
+
+
+@pytest.mark.parametrize("full", [False, True], ids=["turbo_default", "full_explicit"])
+def test_turbo_step_50_freezes_basis_and_drops_residual(dev, full):
+    """Reference tests/test_surgery.py:79-141 on the GPU."""
+    from stacr_amd import apply_stacr, set_step
+
+    announce("turbo step 50", full)
+    torch.manual_seed(19)
+    model = torch.nn.Sequential(torch.nn.Linear(12, 7, bias=False)).to(dev)
+    weight = model[0].weight
+    options = {"turbo_after_step": None} if full else {}
+    layers = apply_stacr(model, surface="all", min_features=1, rank=3, residual_budget=0.25, update_interval=1,
+                         oja_lr=0.2, **options)
+    layer = layers[0]
+    set_step(layers, 48)
+    model(torch.randn(32, 12, device=dev)).sum().backward()
+    initialized = layer.basis.detach().clone()
+    set_step(layers, 49)
+    model.zero_grad(set_to_none=True)
+    before = model(torch.randn(32, 12, device=dev))
+    assert before.grad_fn.has_residual
+    assert not torch.equal(layer.basis, initialized)
+    before.sum().backward()
+    step49 = layer.basis.detach().clone()
+    set_step(layers, 50)
+    model.zero_grad(set_to_none=True)
+    x = torch.randn(32, 12, device=dev, requires_grad=True)
+    upstream = torch.randn(32, 7, device=dev)
+    out = model(x)
+    assert out.grad_fn.has_residual is full
+    if not full:
+        torch.testing.assert_close(layer.basis, step49, rtol=0, atol=0)
+    torch.testing.assert_close(out, x @ weight.t())
+    out.backward(upstream)
+    torch.testing.assert_close(x.grad, upstream @ weight)
+    if not full:
+        low = (x.detach() @ step49) @ step49.t()
+        torch.testing.assert_close(weight.grad, upstream.t() @ low)
