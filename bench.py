@@ -46,10 +46,8 @@ def algorithmic_bytes(k: int) -> dict:
         "k_refine_hist": N * D_IN * S_ACT + N * RANK * S_ACT,
         "k_count": N * D_IN * S_ACT + N * RANK * S_ACT,
         "k_emit": N * D_IN * S_ACT + N * RANK * S_ACT + 5 * k,
-        "k_lowrank": N * D_OUT * S_ACT + N * RANK * S_ACT,
-        "k_sparse": N * D_OUT * S_ACT + 8 * k,
-        "k_expand": D_OUT * D_IN * S_ACT + D_OUT * (RANK + 1) * 4 + D_IN * RANK * 4,
-        "k_csr_rows": 5 * k + 12 * k,
+        "k_dw_fused": bwd,
+        "k_rowptr": 4 * k + 4 * (N + 1),
     }
     return {"save": save, "bwd": bwd, "total": save + bwd, "per_kernel": per_kernel}
 
@@ -145,8 +143,12 @@ def main() -> int:
                 torch.cuda.synchronize()
                 step()  # interleaved eager work between replays
                 torch.cuda.synchronize()
-                for a, b in zip(outs, ref):
+                # save outputs are deterministic; dW/dbias sum the sparse term with LDS atomics
+                for a, b in zip(outs[:4], ref[:4]):
                     if not torch.equal(a, b):
+                        raise RuntimeError("graph replay differs from the eager result")
+                for a, b in zip(outs[4:], ref[4:]):
+                    if ((a.float() - b.float()).norm() / b.float().norm()).item() > 1e-3:
                         raise RuntimeError("graph replay differs from the eager result")
             for _ in range(args.warmup):
                 graph.replay()

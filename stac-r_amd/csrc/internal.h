@@ -102,10 +102,12 @@ __device__ __forceinline__ void store_any(void *p, int dt, int64_t i, float f)
 }
 
 // ------------------------------------------------------------------ block primitives
-// Exclusive prefix sum over the 256 threads of a workgroup; *total receives the sum.
-// Every thread must call it (it contains __syncthreads).
+// Exclusive prefix sum over the NT threads of a workgroup (NT a multiple of 64); *total receives
+// the sum.  s_tot needs NT / 64 entries.  Every thread must call it (it contains __syncthreads).
+template <int NT = kBlock>
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *s_tot, uint32_t *total)
 {
+    constexpr int NWAVE = NT / 64;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     uint32_t x = v;
 #pragma unroll
@@ -117,7 +119,7 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *s
     __syncthreads();
     uint32_t before = 0, all = 0;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < NWAVE; ++w) {
         const uint32_t t = s_tot[w];
         before += w < wave ? t : 0u;
         all += t;
@@ -127,10 +129,11 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *s
     return before + x - v;
 }
 
+template <int NT = kBlock>
 __device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t *s_tot)
 {
     uint32_t total;
-    block_exclusive_scan(v, s_tot, &total);
+    block_exclusive_scan<NT>(v, s_tot, &total);
     return total;
 }
 

@@ -74,7 +74,7 @@ def test_workspace_queries_and_error_paths():
     assert L.stacr_save_workspace_bytes(8192, 1024, 8, 1, 1, 0.005, 512, 8, ctypes.byref(b)) == 0
     assert b.value > 0
     assert L.stacr_weight_grad_workspace_bytes(8192, 4096, 1024, 8, 41943, ctypes.byref(b)) == 0
-    assert b.value >= 4096 * 1024 * 4
+    assert b.value >= (8192 + 1) * 4  # per-row residual offsets
     # rank outside the supported range -> UNSUPPORTED with a message
     assert L.stacr_save_workspace_bytes(64, 64, 33, 1, 0, 0.1, 16, 8, ctypes.byref(b)) == 2
     assert b"rank" in L.stacr_last_error()

@@ -234,7 +234,8 @@ def test_weight_grad_int64_indices(dev):
     coeff, idx, data, scale = kernels.save(x, q, mode="chunk_topk", budget=0.05, chunk_rows=64, bits=8)
     a, _ = kernels.weight_grad(g, coeff, q, (idx, data, scale), 8, False, torch.float32)
     b, _ = kernels.weight_grad(g, coeff, q, (idx.long(), data, scale), 8, False, torch.float32)
-    assert torch.equal(a, b)
+    # the sparse term is summed with LDS float atomics, so the order (last bits) may differ
+    assert rel_l2(_np(a), _np(b)) <= 1e-6
 
 
 # ------------------------------------------------------------------ the drop-in layer on the GPU
