@@ -3,31 +3,43 @@
 // Restates stacr/layers.py:172-198.  Accumulation is fp32 and dW is rounded once to the weight
 // dtype (the reference rounds the d_out x r product and the low-rank term to G's dtype before
 // adding its fp32 sparse correction; one rounding at the end is the more accurate of the two).
-// Residual values are dequantized exactly as QuantizedValues.dequantize(fp32) does
-// (stacr/quant.py:17-21,40-46): float(q) * scale in fp32.
+// Residual codes are dequantized as QuantizedValues.dequantize(fp32) does (stacr/quant.py:17-21,
+// 40-46): products use the exact integer code and the per-tensor fp32 scale multiplies each
+// piece's sum when it is added to the accumulator.
 //
-// Two launches:
+// Three launches:
 //   k_rowptr   ascending flat indices -> first residual entry of every token row (CSR offsets)
-//   k_dw_fused one streaming pass over G.  A workgroup owns 16 output features (one "o-slab") and
-//              a slab of at most 1024 input features; it reads G[:, o-slab] once, row block by
-//              row block, and
+//   k_dw_plan  for every block of TB token rows and every input-feature part: the block's residual
+//              entries bucketed by input feature (in rounds of <= kRoundCap entries), cut into
+//              pieces of <= kPiece entries.  Done once and shared by all output slabs.
+//   k_dw_fused one streaming pass over G.  A workgroup owns 16 output features (an "o-slab") and
+//              one part of <= 1024 input features.  Per block of token rows it
 //                * accumulates M = G^T [C | 1] in registers (packed bf16/fp16 dot products, or
 //                  fp32 FMAs), which also yields dbias;
-//                * adds v * G[t, o] into an LDS accumulator S[i][o] for every residual entry
-//                  (t, i, v) of its rows (LDS float atomics);
-//              then reduces M across its threads and writes dW = M Q^T + S for its tile.
+//                * sums every residual piece v * G[t, o-slab] in registers and adds it to an LDS
+//                  accumulator S[i][o] (the pieces of one feature in piece order);
+//              then reduces M over its threads and writes dW = M Q^T + S for its tile.
+// Inside a piece, entries follow the bucket order of their round, which LDS integer atomics fill
+// in arrival order: the last bits of the sparse term may differ from run to run.
 #include "internal.h"
 
 using namespace stacr;
 
 namespace {
 
-constexpr int kOSlab = 16;         // output features per workgroup
-constexpr int kAccPitch = 17;      // LDS row pitch of the accumulator: odd, so random rows hit
-                                   // different banks (a pitch of 16 maps every row to 2 banks)
-constexpr int kMaxISlab = 1024;    // input features per workgroup: 1024 x 17 fp32 = 68 KiB of LDS
-constexpr int kBwdThreads = 512;   // 8 waves
-constexpr int kPiece = 32;         // residual entries per register-accumulated piece
+constexpr int kOSlab = 16;          // output features per workgroup
+constexpr int kAccPitch = 17;       // LDS row pitch of S: odd, so random rows spread over banks
+constexpr int kMaxISlab = 1024;     // input features per part: 1024 x 17 fp32 = 68 KiB of LDS
+constexpr int kBwdThreads = 512;    // 8 waves
+constexpr int kPiece = 32;          // residual entries per register-accumulated piece
+constexpr int kRoundCap = 4096;     // residual entries bucketed per round
+constexpr int kTaskCap = kMaxISlab + kRoundCap / kPiece;  // pieces of one round (bound)
+constexpr int kHeavyCap = kRoundCap / (kPiece + 1) + 1;   // features cut into > 1 piece (bound)
+constexpr int kSlotCap = 2 * kRoundCap / kPiece;          // partial sums of those pieces (bound)
+constexpr uint32_t kDirect = 0xffffu;                     // task slot: add straight into S
+constexpr int kEntPT = kRoundCap / kBwdThreads;                      // staged entries per thread
+constexpr int kTaskPT = (kTaskCap + kBwdThreads - 1) / kBwdThreads;  // staged pieces per thread
+static_assert(kHeavyCap <= kBwdThreads, "one heavy record per thread");
 
 template <int DT, int R>
 struct GradCfg {
@@ -35,16 +47,12 @@ struct GradCfg {
     static constexpr bool k16 = sizeof(T) == 2;
     // output features per thread: keeps the M accumulator at <= 72 fp32 registers
     static constexpr int OT = k16 ? (R <= 8 ? 8 : (R == 16 ? 4 : 2)) : (R <= 16 ? 4 : 2);
-    static constexpr int OG = kOSlab / OT;          // threads sharing one token row
-    static constexpr int TP = kBwdThreads / OG;     // token pairs per block
-    static constexpr int TB = 2 * TP;               // token rows per block
-    static constexpr int VB = OT * (int)sizeof(T);  // bytes per thread per row
-    static constexpr int NV = OT * (R + 1);         // accumulator values per thread
-    // residual entries prefetched per thread and bucketed in LDS per round (8 B per entry for
-    // fp32 G, 4 B packed otherwise); pieces of features split over several pieces per round
-    static constexpr int EPT = k16 ? 8 : 4;
-    static constexpr int ENT_CAP = EPT * kBwdThreads;
-    static constexpr int HEAVY = 2 * ENT_CAP / kPiece;
+    static constexpr int OG = kOSlab / OT;             // threads sharing one token row
+    static constexpr int TP = kBwdThreads / OG;        // token-row pairs per block
+    static constexpr int TB = 2 * TP;                  // token rows per block
+    static constexpr int VB = OT * (int)sizeof(T);     // G bytes per thread per row
+    static constexpr int NV = OT * (R + 1);            // accumulator values per thread
+    static constexpr int CW = R * (int)sizeof(T) / 4;  // 32-bit words of one (padded) C row
 };
 
 template <int B> struct Vec;
@@ -53,14 +61,9 @@ template <> struct Vec<8> { using type = uint2; static constexpr int n = 2; };
 template <> struct Vec<16> { using type = uint4; static constexpr int n = 4; };
 
 template <int B>
-__device__ __forceinline__ void load_words(const void *p, bool ok, uint32_t (&w)[Vec<B>::n])
+__device__ __forceinline__ void load_words(const void *p, uint32_t *w)
 {
     using V = typename Vec<B>::type;
-    if (!ok) {
-#pragma unroll
-        for (int k = 0; k < Vec<B>::n; ++k) w[k] = 0u;
-        return;
-    }
     const V v = *reinterpret_cast<const V *>(p);
     if constexpr (B == 4) {
         w[0] = v;
@@ -72,7 +75,7 @@ __device__ __forceinline__ void load_words(const void *p, bool ok, uint32_t (&w)
 }
 
 // OT consecutive elements of one G row as 32-bit words (zero outside the row / matrix).  The
-// 16-byte vector load is used when the whole vector is in range and aligned.
+// vector load is used when the whole vector is in range and aligned.
 template <int DT, int VB>
 __device__ __forceinline__ void load_g(const typename Act<DT>::T *row, int64_t ob, int64_t d_out, bool row_ok,
                                        bool vec_ok, uint32_t (&w)[Vec<VB>::n])
@@ -80,7 +83,7 @@ __device__ __forceinline__ void load_g(const typename Act<DT>::T *row, int64_t o
     using T = typename Act<DT>::T;
     constexpr int OT = VB / (int)sizeof(T);
     if (row_ok && vec_ok && ob + OT <= d_out) {
-        load_words<VB>(row + ob, true, w);
+        load_words<VB>(row + ob, w);
         return;
     }
 #pragma unroll
@@ -115,20 +118,18 @@ __device__ __forceinline__ int64_t flat_at(const void *idx, int64_t k)
     return IDX64 ? static_cast<const int64_t *>(idx)[k] : (int64_t) static_cast<const int32_t *>(idx)[k];
 }
 
-__device__ __forceinline__ float dequant(const void *data, const float *scale, int bits, int val_dt, int64_t e)
+// off / d for off < 2^25: a float reciprocal, then an exact one-step correction
+__device__ __forceinline__ uint32_t div_small(uint32_t off, uint32_t d, float inv_d)
 {
-    if (bits == 8) return (float)static_cast<const int8_t *>(data)[e] * scale[0];
-    if (bits == 4) {
-        const uint32_t byte = static_cast<const uint8_t *>(data)[e >> 1];
-        int n = (int)((e & 1) ? (byte >> 4) : (byte & 0xfu));
-        n = n > 7 ? n - 16 : n;
-        return (float)n * scale[0];
-    }
-    return load_any(data, val_dt, e);
+    uint32_t q = (uint32_t)((float)off * inv_d);
+    if (q * d > off) --q;
+    else if ((q + 1) * d <= off) ++q;
+    return q;
 }
 
 // rowptr[t] = first entry whose flat index is >= t * d_in (t = 0..rows).  Indices are ascending
-// (stacr_save writes them so); an index outside rows x d_in maps past the last row.
+// (stacr_save writes them so); entries with an index outside rows x d_in count as row `rows` and
+// so fall outside every block.
 template <int IDX64>
 __global__ void k_rowptr(const void *__restrict__ idx, int64_t nnz, int64_t d_in, int64_t rows,
                          uint32_t *__restrict__ rowptr)
@@ -143,23 +144,208 @@ __global__ void k_rowptr(const void *__restrict__ idx, int64_t nnz, int64_t d_in
         const int64_t fp = flat_at<IDX64>(idx, e - 1);
         tprev = (fp < 0 || fp >= lim) ? rows : fp / d_in;
     }
-    for (int64_t tt = tprev + 1; tt <= t && tt < rows; ++tt) rowptr[tt] = (uint32_t)e;
+    for (int64_t tt = tprev + 1; tt <= t; ++tt) rowptr[tt] = (uint32_t)e;
     if (e == nnz - 1)
-        for (int64_t tt = t < rows ? t + 1 : rows; tt <= rows; ++tt) rowptr[tt] = (uint32_t)nnz;
+        for (int64_t tt = t + 1; tt <= rows; ++tt) rowptr[tt] = (uint32_t)nnz;
 }
 
+// ------------------------------------------------------------------ the plan
+// One round of one (block, part): its bucketed entries, pieces and heavy records all start at
+// plan slot `base` (a part's entries of a round occupy a private slot range; it never has more
+// pieces or heavy records than entries).
+struct RoundHdr {
+    uint32_t base;
+    uint32_t n_ent;
+    uint32_t n_task;
+    uint32_t n_heavy;
+};
+
+struct BlockHdr {
+    RoundHdr r0;           // the block's first round (all zero when the block has no entries)
+    uint32_t first_round;  // global index of that round
+    uint32_t n_rounds;
+    uint32_t pad[2];
+};
+
+struct PlanArgs {
+    const void *idx;
+    const void *data;
+    int bits, val_dt, g_dt;
+    int64_t nnz, rows, d_in;
+    int64_t n_parts, i_span;
+    int tb;                  // token rows per block
+    uint32_t max_rounds;     // rounds the header array holds
+    const uint32_t *rowptr;
+    uint32_t *ent;           // [nnz] t_local << 16 | 16-bit value code, or t_local (fp32 G)
+    float *val;              // [nnz] fp32 values (fp32 G only)
+    uint2 *task;             // [nnz] {feature | slot << 16, entry offset << 6 | entries}
+    uint2 *heavy;            // [nnz] {feature | first slot << 16, pieces}
+    RoundHdr *rhdr;          // [global round][part]
+    BlockHdr *bhdr;          // [block][part]
+};
+
+// The product operand of entry e: the integer code (exact in bf16/fp16) for bits 4/8, the stored
+// value for bits 0; as G's 16-bit code, or fp32 bits for fp32 G.
+__device__ __forceinline__ uint32_t entry_value(const PlanArgs &a, int64_t e)
+{
+    float v;
+    if (a.bits == 8) {
+        v = (float)static_cast<const int8_t *>(a.data)[e];
+    } else if (a.bits == 4) {
+        const uint32_t byte = static_cast<const uint8_t *>(a.data)[e >> 1];
+        const int n = (int)((e & 1) ? (byte >> 4) : (byte & 0xfu));
+        v = (float)(n > 7 ? n - 16 : n);
+    } else {
+        v = load_any(a.data, a.val_dt, e);
+    }
+    if (a.g_dt == STACR_DTYPE_BF16) return f_to_bf16_bits(v);
+    if (a.g_dt == STACR_DTYPE_F16) return f_to_f16_bits(v);
+    return __float_as_uint(v);
+}
+
+template <int IDX64>
+__global__ __launch_bounds__(kBwdThreads) void k_dw_plan(PlanArgs a)
+{
+    __shared__ uint32_t cnt[kMaxISlab], ccur[kMaxISlab];
+    __shared__ uint32_t cstart[kMaxISlab], tstart[kMaxISlab], hstart[kMaxISlab], hidx[kMaxISlab];
+    __shared__ uint32_t s_tot[kBwdThreads / 64];
+    __shared__ uint32_t s_first;
+    const int64_t b = blockIdx.x, p = blockIdx.y;
+    const int64_t t0 = b * a.tb, t1 = min(t0 + a.tb, a.rows);
+    const int64_t i0 = p * a.i_span;
+    const int ni = (int)(min(i0 + a.i_span, a.d_in) - i0);
+    const int64_t span = (t1 - t0) * a.d_in;  // flat offsets of the block's rows
+    const uint32_t d_in = (uint32_t)a.d_in;
+    const float inv_d = 1.f / (float)a.d_in;
+    // entry range of a block; the clamps keep indices that are not ascending inside the arrays
+    const uint32_t nnz = (uint32_t)a.nnz;
+    auto range = [&](int64_t bb, uint32_t &x0, uint32_t &x1) {
+        x0 = min(a.rowptr[bb * a.tb], nnz);
+        x1 = max(x0, min(a.rowptr[min((bb + 1) * a.tb, a.rows)], nnz));
+    };
+    uint32_t e0, e1;
+    range(b, e0, e1);
+    uint32_t n_rounds = (e1 - e0 + kRoundCap - 1) / kRoundCap;
+    if (threadIdx.x < 64) {  // rounds of the blocks before this one
+        uint32_t r = 0;
+        for (int64_t bb = threadIdx.x; bb < b; bb += 64) {
+            uint32_t x0, x1;
+            range(bb, x0, x1);
+            r += (x1 - x0 + kRoundCap - 1) / kRoundCap;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) r += __shfl_xor(r, off, 64);
+        if (threadIdx.x == 0) s_first = r;
+    }
+    __syncthreads();
+    const uint32_t first = s_first;
+    if (first + n_rounds > a.max_rounds) n_rounds = 0;  // only for indices that are not ascending
+    if (threadIdx.x == 0 && n_rounds == 0)
+        a.bhdr[b * a.n_parts + p] = BlockHdr{RoundHdr{0u, 0u, 0u, 0u}, first, 0u, {0u, 0u}};
+    for (uint32_t j = 0; j < n_rounds; ++j) {
+        const uint32_t c0 = e0 + j * kRoundCap, c1 = min(c0 + (uint32_t)kRoundCap, e1);
+        for (int c = threadIdx.x; c < ni; c += kBwdThreads) {
+            cnt[c] = 0u;
+            ccur[c] = 0u;
+        }
+        __syncthreads();
+        uint32_t col[kEntPT], tl[kEntPT];
+        uint32_t before = 0;
+#pragma unroll
+        for (int k = 0; k < kEntPT; ++k) {
+            col[k] = 0xffffffffu;
+            tl[k] = 0u;
+            const uint32_t e = c0 + threadIdx.x + k * kBwdThreads;
+            const int64_t off64 = e < c1 ? flat_at<IDX64>(a.idx, e) - t0 * a.d_in : -1;
+            if (off64 >= 0 && off64 < span) {
+                const uint32_t off = (uint32_t)off64;  // < 2^25: tb <= 512 rows of < 65536 features
+                const uint32_t t = div_small(off, d_in, inv_d);
+                const int64_t c = (int64_t)(off - t * d_in);
+                const int64_t part = c / a.i_span;
+                before += part < p;
+                if (part == p) {
+                    col[k] = (uint32_t)(c - i0);
+                    tl[k] = t;
+                    atomicAdd(&cnt[col[k]], 1u);
+                }
+            }
+        }
+        uint32_t n_before;
+        block_exclusive_scan<kBwdThreads>(before, s_tot, &n_before);  // also orders the counts
+        const uint32_t base = c0 + n_before;
+        // prefix sums over the features (two per thread): bucket starts, piece starts, partial-sum
+        // slots and heavy-record positions
+        {
+            const int f0 = 2 * threadIdx.x;
+            const uint32_t n0 = f0 < ni ? cnt[f0] : 0u, n1 = f0 + 1 < ni ? cnt[f0 + 1] : 0u;
+            const uint32_t p0 = (n0 + kPiece - 1) / kPiece, p1 = (n1 + kPiece - 1) / kPiece;
+            const uint32_t h0 = p0 > 1 ? p0 : 0u, h1 = p1 > 1 ? p1 : 0u;
+            const uint32_t x0 = p0 > 1, x1 = p1 > 1;
+            uint32_t tot_e, tot_p, tot_h, tot_x;
+            const uint32_t se = block_exclusive_scan<kBwdThreads>(n0 + n1, s_tot, &tot_e);
+            const uint32_t sp = block_exclusive_scan<kBwdThreads>(p0 + p1, s_tot, &tot_p);
+            const uint32_t sh = block_exclusive_scan<kBwdThreads>(h0 + h1, s_tot, &tot_h);
+            const uint32_t sx = block_exclusive_scan<kBwdThreads>(x0 + x1, s_tot, &tot_x);
+            if (f0 < ni) {
+                cstart[f0] = se; tstart[f0] = sp; hstart[f0] = sh; hidx[f0] = sx;
+            }
+            if (f0 + 1 < ni) {
+                cstart[f0 + 1] = se + n0; tstart[f0 + 1] = sp + p0; hstart[f0 + 1] = sh + h0; hidx[f0 + 1] = sx + x0;
+            }
+            if (threadIdx.x == 0) {
+                const RoundHdr h{base, tot_e, tot_p, tot_x};
+                a.rhdr[(int64_t)(first + j) * a.n_parts + p] = h;
+                if (j == 0) a.bhdr[b * a.n_parts + p] = BlockHdr{h, first, n_rounds, {0u, 0u}};
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kEntPT; ++k) {
+            if (col[k] != 0xffffffffu) {
+                const uint32_t e = c0 + threadIdx.x + k * kBwdThreads;
+                const uint32_t pos = base + cstart[col[k]] + atomicAdd(&ccur[col[k]], 1u);
+                const uint32_t v = entry_value(a, e);
+                if (a.g_dt == STACR_DTYPE_F32) {
+                    a.ent[pos] = tl[k];
+                    a.val[pos] = __uint_as_float(v);
+                } else {
+                    a.ent[pos] = (tl[k] << 16) | (v & 0xffffu);
+                }
+            }
+        }
+        for (int c = threadIdx.x; c < ni; c += kBwdThreads) {
+            const uint32_t n = cnt[c];
+            const uint32_t npc = (n + kPiece - 1) / kPiece;
+            for (uint32_t pc = 0; pc < npc; ++pc) {
+                const uint32_t slot = npc > 1 ? hstart[c] + pc : kDirect;
+                const uint32_t len = min((uint32_t)kPiece, n - pc * kPiece);
+                a.task[base + tstart[c] + pc] =
+                    make_uint2((uint32_t)c | (slot << 16), ((cstart[c] + pc * kPiece) << 6) | len);
+            }
+            if (npc > 1) a.heavy[base + hidx[c]] = make_uint2((uint32_t)c | (hstart[c] << 16), npc);
+        }
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------------ the streaming pass
 struct FusedArgs {
     const void *g, *coeff, *q;
     int64_t rows, d_out, d_in;
     int rank;
-    const void *idx;
-    const void *data;
     const float *scale;
-    int bits, val_dt;
+    int bits;
     int64_t nnz;
-    const uint32_t *rowptr;
+    const uint32_t *ent;
+    const float *val;
+    const uint2 *task;
+    const uint2 *heavy;
+    const RoundHdr *rhdr;
+    const BlockHdr *bhdr;
     int64_t n_slabs, n_parts, i_span;  // i_span: input features per part (<= kMaxISlab)
-    int vec_ok;                        // G rows are 16-byte aligned for whole-vector loads
+    int vec_ok;                        // G rows allow whole-vector loads
+    int c_vec;                         // C rows are exactly R wide and aligned for vector loads
+    int out_vec_ok;                    // dW rows are 16-byte aligned (Conv1D layout stores)
     int transposed;
     void *dw;
     int dw_dt;
@@ -167,48 +353,54 @@ struct FusedArgs {
     int db_dt;
 };
 
-
-// Shared-memory carve-up of k_dw_fused (byte offsets; sized for the widest configuration).
+// Shared-memory carve-up of k_dw_fused (byte offsets).
 template <int DT, int R>
 struct FusedLds {
     using C = GradCfg<DT, R>;
     using T = typename C::T;
-    static constexpr bool k16 = C::k16;
-    static constexpr size_t s_acc = 0;                                            // [1024][kAccPitch] f32
-    static constexpr size_t s_gtile = s_acc + (size_t)kMaxISlab * kAccPitch * 4;  // [TB][16] T
-    static constexpr size_t s_ctile = s_gtile + (size_t)C::TB * kOSlab * sizeof(T);  // [TB][R] T
-    static constexpr size_t s_ent = s_ctile + (((size_t)C::TB * R * sizeof(T) + 15) & ~(size_t)15);
-    static constexpr size_t ent_bytes = k16 ? 4 : 8;                              // packed (t, v)
-    static constexpr size_t s_cols = s_ent + (size_t)C::ENT_CAP * ent_bytes;      // 5 x [1025] u32
-    static constexpr size_t s_scr = s_cols + (size_t)5 * (kMaxISlab + 1) * 4;     // [HEAVY][16] f32
-    static constexpr size_t end = s_scr + (size_t)C::HEAVY * kOSlab * 4;
+    static constexpr size_t s_acc = 0;                                               // [1024][17] f32
+    static constexpr size_t s_gtile = s_acc + (size_t)kMaxISlab * kAccPitch * 4;     // [TB][16] T
+    static constexpr size_t s_ent = s_gtile + (size_t)C::TB * kOSlab * sizeof(T);    // [kRoundCap]
+    static constexpr size_t s_val = s_ent + (size_t)kRoundCap * 4;                   // fp32 G only
+    static constexpr size_t s_task = s_val + (C::k16 ? 0 : (size_t)kRoundCap * 4);   // [kTaskCap]
+    static constexpr size_t s_heavy = s_task + (size_t)kTaskCap * 8;                 // [kHeavyCap]
+    static constexpr size_t s_slot = s_heavy + (size_t)kHeavyCap * 8;                // [kSlotCap][16]
+    static constexpr size_t end = s_slot + (size_t)kSlotCap * kOSlab * 4;
+    static constexpr int HALF = (C::NV + 1) / 2;
+    static constexpr size_t red_end = s_gtile + ((size_t)kBwdThreads * HALF + (size_t)8 * C::OG * HALF +
+                                                 (size_t)kOSlab * (R + 1)) * 4;
+    static constexpr size_t bytes = end > red_end ? end : red_end;
 };
 
-template <int DT, int R, int IDX64>
+// A round's plan data held in registers between its load and its copy into LDS.
+template <bool K16>
+struct Staged {
+    uint32_t ent[kEntPT];
+    float val[K16 ? 1 : kEntPT];
+    uint2 task[kTaskPT];
+    uint2 heavy;
+};
+
+template <int DT, int R>
 __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
 {
     using C = GradCfg<DT, R>;
     using T = typename C::T;
     using L = FusedLds<DT, R>;
-    constexpr int OT = C::OT, OG = C::OG, TP = C::TP, TB = C::TB, VB = C::VB, NW = Vec<C::VB>::n;
-    constexpr int CPT = (TB * R + kBwdThreads - 1) / kBwdThreads;  // C elements staged per thread
-    constexpr int EPT = C::EPT, kEntCap = C::ENT_CAP;
-    constexpr int NGRP = kBwdThreads / OG;                          // piece groups per pass
+    constexpr int OT = C::OT, OG = C::OG, TB = C::TB, VB = C::VB, NW = Vec<C::VB>::n, CW = C::CW;
+    constexpr int NGRP = kBwdThreads / OG;  // piece groups working at once
+    constexpr bool K16 = C::k16;
 
     extern __shared__ float lds[];
     char *base = reinterpret_cast<char *>(lds);
-    float *acc = reinterpret_cast<float *>(base + L::s_acc);       // residual accumulator S[i][o]
-    T *gtile = reinterpret_cast<T *>(base + L::s_gtile);            // G rows of the current block
-    T *ctile = reinterpret_cast<T *>(base + L::s_ctile);            // C rows of the current block
-    uint32_t *ent = reinterpret_cast<uint32_t *>(base + L::s_ent);  // bucketed entries
-    uint32_t *cnt = reinterpret_cast<uint32_t *>(base + L::s_cols); // per column: entries,
-    uint32_t *cstart = cnt + (kMaxISlab + 1);                       //   first bucket slot,
-    uint32_t *ccur = cstart + (kMaxISlab + 1);                      //   placement cursor,
-    uint32_t *tstart = ccur + (kMaxISlab + 1);                      //   first piece,
-    uint32_t *hstart = tstart + (kMaxISlab + 1);                    //   first heavy-scratch slot
-    float *scr = reinterpret_cast<float *>(base + L::s_scr);        // partials of split columns
-    float *mred = reinterpret_cast<float *>(base + L::s_gtile);     // reused after the stream
-    __shared__ uint32_t s_tot[kBwdThreads / 64];
+    float *acc = reinterpret_cast<float *>(base + L::s_acc);
+    T *gtile = reinterpret_cast<T *>(base + L::s_gtile);
+    uint32_t *l_ent = reinterpret_cast<uint32_t *>(base + L::s_ent);
+    float *l_val = reinterpret_cast<float *>(base + L::s_val);
+    uint2 *l_task = reinterpret_cast<uint2 *>(base + L::s_task);
+    uint2 *l_heavy = reinterpret_cast<uint2 *>(base + L::s_heavy);
+    float *l_slot = reinterpret_cast<float *>(base + L::s_slot);
+    float *mred = reinterpret_cast<float *>(base + L::s_gtile);  // reused after the stream
 
     // workgroup -> (o-slab, part); consecutive logical ids land on the same XCD (ids are dealt
     // round-robin over 8 XCDs), so the parts of a slab and neighbouring slabs share an L2
@@ -218,19 +410,16 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
     const int64_t slab = lid / a.n_parts, part = lid - slab * a.n_parts;
     const int64_t o0 = slab * kOSlab;
     const int64_t i0 = part * a.i_span;
-    const int64_t i1 = min(i0 + a.i_span, a.d_in);
-    const int ni = (int)(i1 - i0);
+    const int ni = (int)(min(i0 + a.i_span, a.d_in) - i0);
 
     const int og = threadIdx.x % OG, tp = threadIdx.x / OG;
-    const int64_t ob = o0 + og * OT;                      // first output feature of this thread
-    const bool o_ok = ob < a.d_out;                       // thread owns at least one output feature
+    const int64_t ob = o0 + og * OT;
+    const bool o_ok = ob < a.d_out;
     const bool vec_ok = a.vec_ok != 0;
     const T *g = static_cast<const T *>(a.g);
     const T *coeff = static_cast<const T *>(a.coeff);
     const bool sparse = a.nnz > 0;
-    const float qscale = (sparse && a.bits) ? a.scale[0] : 1.f;  // residual codes are scaled at flush
-    const uint32_t d_in = (uint32_t)a.d_in;
-    const float inv_d = 1.f / (float)a.d_in;
+    const float qscale = (sparse && a.bits) ? a.scale[0] : 1.f;
 
     for (int i = threadIdx.x; i < ni * kAccPitch; i += kBwdThreads) acc[i] = 0.f;
 
@@ -240,146 +429,90 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
 #pragma unroll
         for (int j = 0; j <= R; ++j) m[o][j] = 0.f;
 
-    // ---- everything a block needs is loaded one block ahead into registers
-    uint32_t wa[NW], wb[NW];          // G rows t and t+1 (this thread's output features)
-    T cpre[CPT];                      // C elements of the block (cooperative)
-    uint32_t pf_off[EPT];             // residual entries: flat offset from the block start
-    uint32_t pf_val[EPT];             //   value bits (G's 16-bit type, or fp32 for fp32 G)
-    uint32_t pf_e0 = 0, pf_e1 = 0;    // entry range of the block
-    // residual entries [lo, hi) (at most kEntCap) into pf_off / pf_val
-    auto load_entries = [&](uint32_t lo, uint32_t hi, int64_t tb0) {
-        const int64_t fbase = tb0 * a.d_in;
+    auto load_c = [&](int64_t t, uint32_t (&x)[CW]) {
 #pragma unroll
-        for (int k = 0; k < EPT; ++k) {
-            const uint32_t e = lo + threadIdx.x + k * kBwdThreads;
-            if (e < hi) {
-                pf_off[k] = (uint32_t)(flat_at<IDX64>(a.idx, e) - fbase);
-                if (a.bits == 8 || a.bits == 4) {
-                    int qv;
-                    if (a.bits == 8) {
-                        qv = static_cast<const int8_t *>(a.data)[e];
-                    } else {
-                        const uint32_t byte = static_cast<const uint8_t *>(a.data)[e >> 1];
-                        qv = (int)((e & 1) ? (byte >> 4) : (byte & 0xfu));
-                        qv = qv > 7 ? qv - 16 : qv;
-                    }
-                    pf_val[k] = C::k16 ? (uint32_t)Act<DT>::st((float)qv) : __float_as_uint((float)qv);
+        for (int k = 0; k < CW; ++k) x[k] = 0u;
+        if (t >= a.rows) return;
+        if (a.c_vec) {
+            const char *p = reinterpret_cast<const char *>(coeff + t * R);
+            if constexpr (CW % 4 == 0) {
+#pragma unroll
+                for (int k = 0; k < CW / 4; ++k) load_words<16>(p + 16 * k, x + 4 * k);
+            } else {
+                load_words<8>(p, x);
+            }
+            return;
+        }
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            if (j < a.rank) {
+                if constexpr (K16) {
+                    x[j / 2] |= (uint32_t)coeff[t * a.rank + j] << (16 * (j & 1));
                 } else {
-                    const float v = load_any(a.data, a.val_dt, e);
-                    pf_val[k] = C::k16 ? (uint32_t)Act<DT>::st(v) : __float_as_uint(v);
+                    x[j] = __float_as_uint(coeff[t * a.rank + j]);
                 }
             }
-        }
-    };
-    auto prefetch_entries = [&](int64_t blk) {
-        const int64_t tb0 = blk * TB;
-        pf_e0 = a.rowptr[min(tb0, a.rows)];
-        pf_e1 = a.rowptr[min(tb0 + TB, a.rows)];
-        const uint32_t hi = pf_e1 - pf_e0 > (uint32_t)kEntCap ? pf_e0 + kEntCap : pf_e1;
-        load_entries(pf_e0, hi, tb0);
-    };
-    auto prefetch_gc = [&](int64_t blk) {
-        const int64_t tb0 = blk * TB, t = tb0 + 2 * tp;
-        load_g<DT, VB>(g + t * a.d_out, ob, a.d_out, o_ok && t < a.rows, vec_ok, wa);
-        load_g<DT, VB>(g + (t + 1) * a.d_out, ob, a.d_out, o_ok && t + 1 < a.rows, vec_ok, wb);
-#pragma unroll
-        for (int c = 0; c < CPT; ++c) {
-            const int el = threadIdx.x + c * kBwdThreads;
-            const int r = el / R, j = el - (el / R) * R;
-            const int64_t row = tb0 + r;
-            cpre[c] = (el < TB * R && j < a.rank && row < a.rows) ? coeff[row * a.rank + j] : (T)0;
         }
     };
 
-    // One round: bucket the staged entries [lo, hi) of this block by input feature, cut every
-    // feature's run into pieces of <= kPiece entries, accumulate each piece in registers, and add
-    // it into S (directly when the feature has one piece; through the scratch otherwise).
-    auto scatter_round = [&](uint32_t lo, uint32_t hi) {
-        for (int c = threadIdx.x; c <= ni; c += kBwdThreads) {
-            cnt[c] = 0u;
-            ccur[c] = 0u;
-        }
-        __syncthreads();
-        uint32_t mycol[EPT];
+    // G and C rows of the next block, one block ahead
+    uint32_t wa[NW], wb[NW], xa[CW], xb[CW];
+    auto prefetch = [&](int64_t blk) {
+        const int64_t t = blk * TB + 2 * tp;
+        load_g<DT, VB>(g + t * a.d_out, ob, a.d_out, o_ok && t < a.rows, vec_ok, wa);
+        load_g<DT, VB>(g + (t + 1) * a.d_out, ob, a.d_out, o_ok && t + 1 < a.rows, vec_ok, wb);
+        load_c(t, xa);
+        load_c(t + 1, xb);
+    };
+
+    // plan data of a round: global -> registers -> LDS (round sizes are bounded by the planner;
+    // the clamps only keep a malformed plan inside the buffers)
+    auto load_stage = [&](Staged<K16> &st, const RoundHdr &h) {
+        const uint32_t ne = min(h.n_ent, (uint32_t)kRoundCap), nt = min(h.n_task, (uint32_t)kTaskCap);
 #pragma unroll
-        for (int k = 0; k < EPT; ++k) {
-            mycol[k] = 0xffffffffu;
-            const uint32_t e = lo + threadIdx.x + k * kBwdThreads;
-            if (e < hi) {
-                const uint32_t off = pf_off[k];
-                uint32_t tl = (uint32_t)((float)off * inv_d);  // off / d_in, corrected below
-                if (tl * d_in > off) --tl;
-                else if ((tl + 1) * d_in <= off) ++tl;
-                const int64_t col = (int64_t)(off - tl * d_in) - i0;
-                if (tl < (uint32_t)TB && col >= 0 && col < ni) {
-                    mycol[k] = (uint32_t)col;
-                    pf_off[k] = tl;  // keep the block-local row for placement
-                    atomicAdd(&cnt[col], 1u);
-                }
-            }
+        for (int k = 0; k < kEntPT; ++k) {
+            const uint32_t e = threadIdx.x + k * kBwdThreads;
+            st.ent[k] = e < ne ? a.ent[h.base + e] : 0u;
+            if constexpr (!K16) st.val[k] = e < ne ? a.val[h.base + e] : 0.f;
         }
-        __syncthreads();
-        // prefix sums over features: bucket starts, piece starts, heavy-scratch starts
-        {
-            const int c0 = 2 * threadIdx.x;  // ni <= 1024: two features per thread
-            const uint32_t n0 = c0 < ni ? cnt[c0] : 0u, n1 = c0 + 1 < ni ? cnt[c0 + 1] : 0u;
-            const uint32_t p0 = (n0 + kPiece - 1) / kPiece, p1 = (n1 + kPiece - 1) / kPiece;
-            const uint32_t h0 = p0 > 1 ? p0 : 0u, h1 = p1 > 1 ? p1 : 0u;
-            uint32_t tot;
-            const uint32_t se = block_exclusive_scan<kBwdThreads>(n0 + n1, s_tot, &tot);
-            const uint32_t sp = block_exclusive_scan<kBwdThreads>(p0 + p1, s_tot, &tot);
-            const uint32_t n_pieces = tot;
-            const uint32_t sh = block_exclusive_scan<kBwdThreads>(h0 + h1, s_tot, &tot);
-            if (c0 < ni) {
-                cstart[c0] = se;
-                tstart[c0] = sp;
-                hstart[c0] = sh;
-            }
-            if (c0 + 1 < ni) {
-                cstart[c0 + 1] = se + n0;
-                tstart[c0 + 1] = sp + p0;
-                hstart[c0 + 1] = sh + h0;
-            }
-            if (threadIdx.x == 0) tstart[ni] = n_pieces;
-        }
-        __syncthreads();
 #pragma unroll
-        for (int k = 0; k < EPT; ++k) {
-            if (mycol[k] != 0xffffffffu) {
-                const uint32_t pos = cstart[mycol[k]] + atomicAdd(&ccur[mycol[k]], 1u);
-                if constexpr (C::k16) {
-                    ent[pos] = (pf_off[k] << 16) | (pf_val[k] & 0xffffu);
-                } else {
-                    ent[2 * pos] = pf_off[k];
-                    ent[2 * pos + 1] = pf_val[k];
-                }
-            }
+        for (int k = 0; k < kTaskPT; ++k) {
+            const uint32_t e = threadIdx.x + k * kBwdThreads;
+            st.task[k] = e < nt ? a.task[h.base + e] : make_uint2(0u, 0u);
         }
-        __syncthreads();
-        const uint32_t n_pieces = tstart[ni];
+        st.heavy = threadIdx.x < min(h.n_heavy, (uint32_t)kHeavyCap) ? a.heavy[h.base + threadIdx.x]
+                                                                     : make_uint2(0u, 0u);
+    };
+    auto store_stage = [&](const Staged<K16> &st) {
+#pragma unroll
+        for (int k = 0; k < kEntPT; ++k) {
+            l_ent[threadIdx.x + k * kBwdThreads] = st.ent[k];
+            if constexpr (!K16) l_val[threadIdx.x + k * kBwdThreads] = st.val[k];
+        }
+#pragma unroll
+        for (int k = 0; k < kTaskPT; ++k)
+            if (threadIdx.x + k * kBwdThreads < kTaskCap) l_task[threadIdx.x + k * kBwdThreads] = st.task[k];
+        if (threadIdx.x < kHeavyCap) l_heavy[threadIdx.x] = st.heavy;
+    };
+
+    // sum the round's pieces (staged in LDS; the G tile complete) into S
+    auto run_round = [&](const RoundHdr &h) {
+        const uint32_t nt = min(h.n_task, (uint32_t)kTaskCap), nh = min(h.n_heavy, (uint32_t)kHeavyCap);
         if (o_ok) {
-            const int grp = threadIdx.x / OG;
-            for (uint32_t task = grp; task < n_pieces; task += NGRP) {
-                int lo_c = 0, hi_c = ni;  // feature c with tstart[c] <= task < tstart[c + 1]
-                while (hi_c - lo_c > 1) {
-                    const int mid = (lo_c + hi_c) >> 1;
-                    if (tstart[mid] <= task) lo_c = mid;
-                    else hi_c = mid;
-                }
-                const int c = lo_c;
-                const uint32_t piece = task - tstart[c];
-                const uint32_t n = cnt[c];
-                const uint32_t e_lo = cstart[c] + piece * kPiece;
-                const uint32_t e_hi = cstart[c] + min(n, (piece + 1) * kPiece);
+            for (uint32_t tk = threadIdx.x / OG; tk < nt; tk += NGRP) {
+                const uint2 td = l_task[tk];
+                const uint32_t c = td.x & 0xffffu, slot = td.x >> 16;
+                const uint32_t e_lo = min(td.y >> 6, (uint32_t)kRoundCap);
+                const uint32_t e_hi = min(e_lo + (td.y & 63u), (uint32_t)kRoundCap);
                 float pacc[OT];
 #pragma unroll
                 for (int o = 0; o < OT; ++o) pacc[o] = 0.f;
                 for (uint32_t e = e_lo; e < e_hi; ++e) {
-                    if constexpr (C::k16) {
-                        const uint32_t wv = ent[e];
-                        const uint32_t tl = wv >> 16;
+                    const uint32_t wv = l_ent[e];
+                    if constexpr (K16) {
+                        const uint32_t *src =
+                            reinterpret_cast<const uint32_t *>(gtile + ((wv >> 16) % TB) * kOSlab + og * OT);
                         uint32_t gw[NW];
-                        const uint32_t *src = reinterpret_cast<const uint32_t *>(gtile + tl * kOSlab + og * OT);
 #pragma unroll
                         for (int k = 0; k < NW; ++k) gw[k] = src[k];
                         const uint32_t vlo = wv & 0xffffu, vhi = wv << 16;  // (v, 0) and (0, v)
@@ -389,82 +522,88 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
                             pacc[2 * k + 1] = dot2<DT>(gw[k], vhi, pacc[2 * k + 1]);
                         }
                     } else {
-                        const uint32_t tl = ent[2 * e];
-                        const float v = __uint_as_float(ent[2 * e + 1]);
-                        const float *src = reinterpret_cast<const float *>(gtile) + tl * kOSlab + og * OT;
+                        const float v = l_val[e];
+                        const float *src = reinterpret_cast<const float *>(gtile) + (wv % TB) * kOSlab + og * OT;
 #pragma unroll
                         for (int o = 0; o < OT; ++o) pacc[o] = fmaf(src[o], v, pacc[o]);
                     }
                 }
-                const uint32_t npc = (n + kPiece - 1) / kPiece;
-                if (npc == 1) {
+                if (c >= (uint32_t)ni) continue;
+                if (slot == kDirect) {
                     float *dst = acc + c * kAccPitch + og * OT;
 #pragma unroll
                     for (int o = 0; o < OT; ++o) dst[o] += pacc[o] * qscale;
-                } else {
-                    float *dst = scr + (hstart[c] + piece) * kOSlab + og * OT;
+                } else if (slot < (uint32_t)kSlotCap) {
+                    float *dst = l_slot + slot * kOSlab + og * OT;
 #pragma unroll
                     for (int o = 0; o < OT; ++o) dst[o] = pacc[o];
                 }
             }
         }
         __syncthreads();
-        // features split into several pieces: add their partials in piece order
-        for (int w = threadIdx.x; w < ni * kOSlab; w += kBwdThreads) {
-            const int c = w / kOSlab, o = w - c * kOSlab;
-            const uint32_t npc = (cnt[c] + kPiece - 1) / kPiece;
-            if (npc > 1 && o0 + o < a.d_out) {
+        // features cut into several pieces: their partial sums added in piece order
+        for (uint32_t w = threadIdx.x; w < nh * kOSlab; w += kBwdThreads) {
+            const uint2 hd = l_heavy[w / kOSlab];
+            const uint32_t o = w % kOSlab, c = hd.x & 0xffffu, s0 = hd.x >> 16;
+            if (o0 + o < a.d_out && c < (uint32_t)ni && s0 + hd.y <= (uint32_t)kSlotCap) {
                 float s = 0.f;
-                for (uint32_t p = 0; p < npc; ++p) s += scr[(hstart[c] + p) * kOSlab + o];
+                for (uint32_t pc = 0; pc < hd.y; ++pc) s += l_slot[(s0 + pc) * kOSlab + o];
                 acc[c * kAccPitch + o] += s * qscale;
             }
         }
+        __syncthreads();
     };
 
     const int64_t n_blocks = (a.rows + TB - 1) / TB;
+    const BlockHdr zero_hdr{};
+    BlockHdr bh_next = zero_hdr, bh_after = zero_hdr;
+    Staged<K16> st;
     if (n_blocks > 0) {
-        prefetch_gc(0);
-        if (sparse) prefetch_entries(0);
+        prefetch(0);
+        if (sparse) {
+            bh_next = a.bhdr[part];
+            load_stage(st, bh_next.r0);
+            if (n_blocks > 1) bh_after = a.bhdr[a.n_parts + part];
+        }
     }
     for (int64_t blk = 0; blk < n_blocks; ++blk) {
-        const int64_t t0 = blk * TB;
-        uint32_t ca[NW], cb[NW];
+        uint32_t ca[NW], cb[NW], ya[CW], yb[CW];
 #pragma unroll
         for (int k = 0; k < NW; ++k) { ca[k] = wa[k]; cb[k] = wb[k]; }
-        const uint32_t e0 = pf_e0, e1 = pf_e1;
-        __syncthreads();  // previous block's LDS tiles fully consumed
 #pragma unroll
-        for (int c = 0; c < CPT; ++c) {
-            const int el = threadIdx.x + c * kBwdThreads;
-            if (el < TB * R) ctile[el] = cpre[c];
-        }
-        {   // G rows of the block for the residual pieces
-            uint32_t *ga_dst = reinterpret_cast<uint32_t *>(gtile + (2 * tp) * kOSlab + og * OT);
-            uint32_t *gb_dst = reinterpret_cast<uint32_t *>(gtile + (2 * tp + 1) * kOSlab + og * OT);
+        for (int k = 0; k < CW; ++k) { ya[k] = xa[k]; yb[k] = xb[k]; }
+        const BlockHdr bh = bh_next;
+        if (sparse) {  // this block's G rows and first round of plan data into LDS
+            uint32_t *da = reinterpret_cast<uint32_t *>(gtile + (2 * tp) * kOSlab + og * OT);
+            uint32_t *db = reinterpret_cast<uint32_t *>(gtile + (2 * tp + 1) * kOSlab + og * OT);
 #pragma unroll
             for (int k = 0; k < NW; ++k) {
-                ga_dst[k] = ca[k];
-                gb_dst[k] = cb[k];
+                da[k] = ca[k];
+                db[k] = cb[k];
+            }
+            if (bh.n_rounds) store_stage(st);
+        }
+        if (blk + 1 < n_blocks) {  // the next block's loads overlap this block's arithmetic
+            prefetch(blk + 1);
+            if (sparse) {
+                bh_next = bh_after;
+                if (bh_next.n_rounds) load_stage(st, bh_next.r0);
+                if (blk + 2 < n_blocks) bh_after = a.bhdr[(blk + 2) * a.n_parts + part];
             }
         }
-        __syncthreads();
-        if (blk + 1 < n_blocks) prefetch_gc(blk + 1);  // overlaps with this block's arithmetic
         // ---- low rank: m[o][j] += G[t][o] C[t][j] + G[t+1][o] C[t+1][j];  m[o][R] += G[t][o] + G[t+1][o]
-        if constexpr (C::k16) {
+        if constexpr (K16) {
             uint32_t pr[OT];  // (G[t][o], G[t+1][o]) pairs
 #pragma unroll
             for (int k = 0; k < NW; ++k) {
                 pr[2 * k] = __builtin_amdgcn_perm(cb[k], ca[k], 0x05040100u);
                 pr[2 * k + 1] = __builtin_amdgcn_perm(cb[k], ca[k], 0x07060302u);
             }
-            const uint32_t *rowa = reinterpret_cast<const uint32_t *>(ctile + (2 * tp) * R);
-            const uint32_t *rowb = reinterpret_cast<const uint32_t *>(ctile + (2 * tp + 1) * R);
             uint32_t cv[R];  // (C[t][j], C[t+1][j]) pairs
 #pragma unroll
-            for (int k = 0; k < R / 2; ++k) {
-                const uint32_t xa = rowa[k], xb = rowb[k];
-                cv[2 * k] = __builtin_amdgcn_perm(xb, xa, 0x05040100u);
-                cv[2 * k + 1] = __builtin_amdgcn_perm(xb, xa, 0x07060302u);
+            for (int k = 0; k < CW; ++k) {
+                cv[2 * k] = __builtin_amdgcn_perm(yb[k], ya[k], 0x05040100u);
+                cv[2 * k + 1] = __builtin_amdgcn_perm(yb[k], ya[k], 0x07060302u);
             }
             const uint32_t ones = DT == STACR_DTYPE_BF16 ? 0x3f803f80u : 0x3c003c00u;
 #pragma unroll
@@ -474,43 +613,38 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
                 m[o][R] = dot2<DT>(pr[o], ones, m[o][R]);
             }
         } else {
-            float ga[OT], gb[OT];
-#pragma unroll
-            for (int k = 0; k < NW; ++k) {
-                ga[k] = __uint_as_float(ca[k]);
-                gb[k] = __uint_as_float(cb[k]);
-            }
-            const float *cpa = reinterpret_cast<const float *>(ctile) + (2 * tp) * R;
-            const float *cpb = cpa + R;
 #pragma unroll
             for (int j = 0; j < R; ++j) {
-                const float c0 = cpa[j], c1 = cpb[j];
+                const float c0 = __uint_as_float(ya[j]), c1 = __uint_as_float(yb[j]);
 #pragma unroll
-                for (int o = 0; o < OT; ++o) m[o][j] = fmaf(gb[o], c1, fmaf(ga[o], c0, m[o][j]));
+                for (int o = 0; o < OT; ++o)
+                    m[o][j] = fmaf(__uint_as_float(cb[o]), c1, fmaf(__uint_as_float(ca[o]), c0, m[o][j]));
             }
 #pragma unroll
-            for (int o = 0; o < OT; ++o) m[o][R] += ga[o] + gb[o];
+            for (int o = 0; o < OT; ++o) m[o][R] += __uint_as_float(ca[o]) + __uint_as_float(cb[o]);
         }
-        if (!sparse) continue;
-        // ---- residual entries of the block: first round from the prefetched registers; blocks
-        // with more than kEntCap entries continue with synchronously loaded rounds
-        const uint32_t hi0 = e1 - e0 > (uint32_t)kEntCap ? e0 + kEntCap : e1;
-        scatter_round(e0, hi0);
-        for (uint32_t lo = hi0; lo < e1; lo += kEntCap) {
-            const uint32_t hi = e1 - lo > (uint32_t)kEntCap ? lo + kEntCap : e1;
-            load_entries(lo, hi, t0);
-            scatter_round(lo, hi);
+        if (!sparse || bh.n_rounds == 0) continue;
+        __syncthreads();  // G tile and first round staged
+        run_round(bh.r0);
+        for (uint32_t j = 1; j < bh.n_rounds; ++j) {  // blocks with more than kRoundCap entries
+            const RoundHdr h = a.rhdr[(int64_t)(bh.first_round + j) * a.n_parts + part];
+            Staged<K16> tmp;
+            load_stage(tmp, h);
+            store_stage(tmp);
+            __syncthreads();
+            run_round(h);
         }
-        if (blk + 1 < n_blocks) prefetch_entries(blk + 1);
+        // (run_round ends with a barrier, so the next block may overwrite the tile and stage)
     }
     __syncthreads();
 
     // ---- reduce m over the TP threads that share an output group, in a fixed order.
     // Two halves of the per-thread values in turn: every thread parks its half in LDS, 8 threads
     // per output sum TP/8 rows each, one thread per output adds the 8 partial sums.
-    constexpr int HALF = (C::NV + 1) / 2;
-    float *psum = mred + kBwdThreads * HALF;       // [8][OG * HALF]
-    float *mfin = psum + 8 * OG * HALF;            // final M: [kOSlab][R + 1]
+    constexpr int HALF = L::HALF;
+    constexpr int TP = C::TP;
+    float *psum = mred + kBwdThreads * HALF;  // [8][OG * HALF]
+    float *mfin = psum + 8 * OG * HALF;       // final M: [kOSlab][R + 1]
     for (int h = 0; h < 2; ++h) {
         const int v0 = h * HALF, v1 = min(C::NV, v0 + HALF);
 #pragma unroll
@@ -536,21 +670,42 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
     }
 
     // ---- epilogue: dW tile = M Q^T + S, one rounding to the weight dtype; dbias from M[:, R].
-    // A thread takes whole input features i (its Q row stays in registers) and all 16 outputs.
+    // A thread takes whole input features i (its Q row in registers) and all 16 outputs.
     const T *q = static_cast<const T *>(a.q);
+    const bool vec_out = a.transposed && a.out_vec_ok && o0 + kOSlab <= a.d_out;
     for (int ii = threadIdx.x; ii < ni; ii += kBwdThreads) {
         const int64_t i = i0 + ii;
         float qr[R];
 #pragma unroll
         for (int j = 0; j < R; ++j) qr[j] = j < a.rank ? Act<DT>::ld(q[i * a.rank + j]) : 0.f;
+        float out[kOSlab];
 #pragma unroll
         for (int oo = 0; oo < kOSlab; ++oo) {
-            const int64_t o = o0 + oo;
-            if (o >= a.d_out) break;
             float s = acc[ii * kAccPitch + oo];
 #pragma unroll
             for (int j = 0; j < R; ++j) s = fmaf(mfin[oo * (R + 1) + j], qr[j], s);
-            store_any(a.dw, a.dw_dt, a.transposed ? i * a.d_out + o : o * a.d_in + i, s);
+            out[oo] = s;
+        }
+        if (vec_out && a.dw_dt != STACR_DTYPE_F32) {
+            // Conv1D layout [d_in, d_out]: the slab's 16 outputs of feature i are 32 contiguous bytes
+            const bool bf = a.dw_dt == STACR_DTYPE_BF16;
+            uint32_t wv[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                wv[k] = bf ? (f_to_bf16_bits(out[2 * k]) | (f_to_bf16_bits(out[2 * k + 1]) << 16))
+                           : (f_to_f16_bits(out[2 * k]) | (f_to_f16_bits(out[2 * k + 1]) << 16));
+            uint4 *dst = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.dw) + i * a.d_out + o0);
+            dst[0] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+            dst[1] = make_uint4(wv[4], wv[5], wv[6], wv[7]);
+        } else if (vec_out) {
+            float4 *dst = reinterpret_cast<float4 *>(static_cast<float *>(a.dw) + i * a.d_out + o0);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) dst[k] = make_float4(out[4 * k], out[4 * k + 1], out[4 * k + 2], out[4 * k + 3]);
+        } else {
+#pragma unroll
+            for (int oo = 0; oo < kOSlab; ++oo)
+                if (o0 + oo < a.d_out)
+                    store_any(a.dw, a.dw_dt, a.transposed ? i * a.d_out + o0 + oo : (o0 + oo) * a.d_in + i, out[oo]);
         }
     }
     if (a.dbias && part == 0)
@@ -558,23 +713,22 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
             if (o0 + oo < a.d_out) store_any(a.dbias, a.db_dt, o0 + oo, mfin[oo * (R + 1) + R]);
 }
 
-template <int DT, int R>
-constexpr size_t fused_lds_bytes()
-{
-    using C = GradCfg<DT, R>;
-    using L = FusedLds<DT, R>;
-    constexpr int HALF = (C::NV + 1) / 2;
-    constexpr size_t red = L::s_gtile + ((size_t)kBwdThreads * HALF + (size_t)8 * C::OG * HALF + (size_t)kOSlab * (R + 1)) * 4;
-    return L::end > red ? L::end : red;
-}
-
 int pad_rank(int rank) { return rank <= 4 ? 4 : rank <= 8 ? 8 : rank <= 16 ? 16 : 32; }
 
-enum { GW_ROWPTR, GW_N };
+int block_rows(int dt, int R)
+{
+    if (dt == STACR_DTYPE_F32)
+        return R <= 4 ? GradCfg<0, 4>::TB : R <= 8 ? GradCfg<0, 8>::TB : R <= 16 ? GradCfg<0, 16>::TB
+                                                                                   : GradCfg<0, 32>::TB;
+    return R <= 4 ? GradCfg<1, 4>::TB : R <= 8 ? GradCfg<1, 8>::TB : R <= 16 ? GradCfg<1, 16>::TB
+                                                                             : GradCfg<1, 32>::TB;
+}
+
+enum { GW_ROWPTR, GW_ENT, GW_VAL, GW_TASK, GW_HEAVY, GW_RHDR, GW_BHDR, GW_N };
 
 struct GPlan {
-    int R;
-    int64_t n_slabs, n_parts, i_span;
+    int R, tb;
+    int64_t n_slabs, n_parts, i_span, n_blocks, max_rounds;
 };
 
 GPlan make_gplan(const StacrGradArgs &a)
@@ -584,15 +738,25 @@ GPlan make_gplan(const StacrGradArgs &a)
     p.n_slabs = (a.d_out + kOSlab - 1) / kOSlab;
     p.n_parts = hmax<int64_t>(1, (a.d_in + kMaxISlab - 1) / kMaxISlab);
     p.i_span = (a.d_in + p.n_parts - 1) / p.n_parts;
+    p.tb = block_rows(a.dtype, p.R);
+    p.n_blocks = (a.rows + p.tb - 1) / p.tb;
+    p.max_rounds = a.nnz / kRoundCap + p.n_blocks + 1;  // sum over blocks of ceil(entries / cap)
     return p;
 }
 
 size_t glayout(const StacrGradArgs &a, const GPlan &p, size_t *off)
 {
-    (void)p;
     size_t cur = 0;
     auto take = [&](int slot, size_t bytes) { off[slot] = cur; cur += (bytes + 255) & ~(size_t)255; };
-    take(GW_ROWPTR, a.nnz > 0 ? (size_t)(a.rows + 1) * sizeof(uint32_t) : 0);
+    const bool sp = a.nnz > 0;
+    const size_t n = sp ? (size_t)a.nnz : 0;
+    take(GW_ROWPTR, sp ? (size_t)(a.rows + 1) * 4 : 0);
+    take(GW_ENT, n * 4);
+    take(GW_VAL, a.dtype == STACR_DTYPE_F32 ? n * 4 : 0);
+    take(GW_TASK, n * 8);
+    take(GW_HEAVY, n * 8);
+    take(GW_RHDR, sp ? (size_t)p.max_rounds * p.n_parts * sizeof(RoundHdr) : 0);
+    take(GW_BHDR, sp ? (size_t)p.n_blocks * p.n_parts * sizeof(BlockHdr) : 0);
     return cur;
 }
 
@@ -611,9 +775,9 @@ template <int DT, int R>
 int launch_grad(const StacrGradArgs &a, const GPlan &p, char *ws, const size_t *off)
 {
     using Cfg = GradCfg<DT, R>;
+    using L = FusedLds<DT, R>;
     hipStream_t s = a.stream;
     FusedArgs f{};
-    f.vec_ok = (a.d_out * (int64_t)sizeof(typename Cfg::T)) % Cfg::VB == 0 && (uintptr_t)a.g % Cfg::VB == 0;
     f.g = a.g;
     f.coeff = a.coeff;
     f.q = a.q;
@@ -621,39 +785,66 @@ int launch_grad(const StacrGradArgs &a, const GPlan &p, char *ws, const size_t *
     f.d_out = a.d_out;
     f.d_in = a.d_in;
     f.rank = a.rank;
-    f.idx = a.idx;
-    f.data = a.data;
     f.scale = a.scale;
     f.bits = a.bits;
-    f.val_dt = a.val_dtype;
-    f.nnz = a.nnz;
+    f.nnz = a.rows > 0 ? a.nnz : 0;
     f.n_slabs = p.n_slabs;
     f.n_parts = p.n_parts;
     f.i_span = p.i_span;
+    f.vec_ok = (a.d_out * (int64_t)sizeof(typename Cfg::T)) % Cfg::VB == 0 && (uintptr_t)a.g % Cfg::VB == 0;
+    const int c_align = Cfg::CW * 4 >= 16 ? 16 : Cfg::CW * 4;
+    f.c_vec = a.rank == R && (uintptr_t)a.coeff % c_align == 0;
+    const int wb = a.dw_dtype == STACR_DTYPE_F32 ? 4 : 2;
+    f.out_vec_ok = (a.d_out * wb) % 16 == 0 && (uintptr_t)a.dw % 16 == 0;
     f.transposed = a.transposed;
     f.dw = a.dw;
     f.dw_dt = a.dw_dtype;
     f.dbias = a.dbias;
     f.db_dt = a.dbias_dtype;
-    if (a.nnz > 0) {
+    if (f.nnz > 0) {
         uint32_t *rowptr = reinterpret_cast<uint32_t *>(ws + off[GW_ROWPTR]);
-        f.rowptr = rowptr;
         const int cg = (int)((a.nnz + kBlock - 1) / kBlock);
         if (a.index_bytes == 8)
             stacr_launch("k_rowptr", s, [&] { k_rowptr<1><<<cg, kBlock, 0, s>>>(a.idx, a.nnz, a.d_in, a.rows, rowptr); });
         else
             stacr_launch("k_rowptr", s, [&] { k_rowptr<0><<<cg, kBlock, 0, s>>>(a.idx, a.nnz, a.d_in, a.rows, rowptr); });
+        PlanArgs pa{};
+        pa.idx = a.idx;
+        pa.data = a.data;
+        pa.bits = a.bits;
+        pa.val_dt = a.val_dtype;
+        pa.g_dt = a.dtype;
+        pa.nnz = a.nnz;
+        pa.rows = a.rows;
+        pa.d_in = a.d_in;
+        pa.n_parts = p.n_parts;
+        pa.i_span = p.i_span;
+        pa.tb = p.tb;
+        pa.max_rounds = (uint32_t)p.max_rounds;
+        pa.rowptr = rowptr;
+        pa.ent = reinterpret_cast<uint32_t *>(ws + off[GW_ENT]);
+        pa.val = reinterpret_cast<float *>(ws + off[GW_VAL]);
+        pa.task = reinterpret_cast<uint2 *>(ws + off[GW_TASK]);
+        pa.heavy = reinterpret_cast<uint2 *>(ws + off[GW_HEAVY]);
+        pa.rhdr = reinterpret_cast<RoundHdr *>(ws + off[GW_RHDR]);
+        pa.bhdr = reinterpret_cast<BlockHdr *>(ws + off[GW_BHDR]);
+        const dim3 pg((unsigned)p.n_blocks, (unsigned)p.n_parts);
+        if (a.index_bytes == 8)
+            stacr_launch("k_dw_plan", s, [&] { k_dw_plan<1><<<pg, kBwdThreads, 0, s>>>(pa); });
+        else
+            stacr_launch("k_dw_plan", s, [&] { k_dw_plan<0><<<pg, kBwdThreads, 0, s>>>(pa); });
+        f.ent = pa.ent;
+        f.val = pa.val;
+        f.task = pa.task;
+        f.heavy = pa.heavy;
+        f.rhdr = pa.rhdr;
+        f.bhdr = pa.bhdr;
     }
-    constexpr size_t lds = fused_lds_bytes<DT, R>();
+    constexpr size_t lds = L::bytes;
     static_assert(lds <= 160 * 1024, "LDS budget");
     const unsigned nwg = (unsigned)(p.n_slabs * p.n_parts);
-    if (a.index_bytes == 8) {
-        raise_lds_limit(k_dw_fused<DT, R, 1>, lds);
-        stacr_launch("k_dw_fused", s, [&] { k_dw_fused<DT, R, 1><<<nwg, kBwdThreads, lds, s>>>(f); });
-    } else {
-        raise_lds_limit(k_dw_fused<DT, R, 0>, lds);
-        stacr_launch("k_dw_fused", s, [&] { k_dw_fused<DT, R, 0><<<nwg, kBwdThreads, lds, s>>>(f); });
-    }
+    raise_lds_limit(k_dw_fused<DT, R>, lds);
+    stacr_launch("k_dw_fused", s, [&] { k_dw_fused<DT, R><<<nwg, kBwdThreads, lds, s>>>(f); });
     return stacr_hip_check(hipGetLastError(), "weight_grad kernels");
 }
 
@@ -685,6 +876,8 @@ int stacr_grad_launch(const StacrGradArgs &a)
     if (a.workspace_bytes < need)
         return stacr_fail(STACR_ERR_WORKSPACE, "stacr_weight_grad: workspace has %zu bytes, needs %zu",
                           a.workspace_bytes, need);
+    if (a.d_in >= 65536)
+        return stacr_fail(STACR_ERR_UNSUPPORTED, "stacr_weight_grad: d_in must be below 65536");
     char *ws = static_cast<char *>(a.workspace);
     switch (a.dtype) {
     case STACR_DTYPE_F32: return grad_dispatch<STACR_DTYPE_F32>(a, p, ws, off);
