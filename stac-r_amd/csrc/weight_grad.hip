@@ -5,22 +5,25 @@
 // adding its fp32 sparse correction; one rounding at the end is the more accurate of the two).
 // Residual codes are dequantized as QuantizedValues.dequantize(fp32) does (stacr/quant.py:17-21,
 // 40-46): products use the exact integer code and the per-tensor fp32 scale multiplies each
-// piece's sum when it is added to the accumulator.
+// segment's sum when it is added to the accumulator.
 //
 // Three launches:
 //   k_rowptr   ascending flat indices -> first residual entry of every token row (CSR offsets)
 //   k_dw_plan  for every block of TB token rows and every input-feature part: the block's residual
-//              entries bucketed by input feature (in rounds of <= kRoundCap entries), cut into
-//              pieces of <= kPiece entries.  Done once and shared by all output slabs.
+//              entries bucketed by input feature (in rounds of <= 4096 entries) and cut into equal
+//              runs of P entries, one run per thread of the streaming kernel, plus the list of
+//              features whose entries cross a run boundary.  Done once, shared by all o-slabs.
 //   k_dw_fused one streaming pass over G.  A workgroup owns 16 output features (an "o-slab") and
 //              one part of <= 1024 input features.  Per block of token rows it
 //                * accumulates M = G^T [C | 1] in registers (packed bf16/fp16 dot products, or
 //                  fp32 FMAs), which also yields dbias;
-//                * sums every residual piece v * G[t, o-slab] in registers and adds it to an LDS
-//                  accumulator S[i][o] (the pieces of one feature in piece order);
+//                * walks its run of bucketed entries, summing v * G[t, o-slab] per feature in
+//                  registers, and adds each feature's sum into an LDS accumulator S[i][o]; a sum
+//                  that continues a feature from the previous run goes to a slot instead, and the
+//                  slots are added (in run order) after a barrier;
 //              then reduces M over its threads and writes dW = M Q^T + S for its tile.
-// Inside a piece, entries follow the bucket order of their round, which LDS integer atomics fill
-// in arrival order: the last bits of the sparse term may differ from run to run.
+// Within a feature, entries follow the bucket order, which LDS integer atomics fill in arrival
+// order: the last bits of the sparse term may differ from run to run.
 #include "internal.h"
 
 using namespace stacr;
@@ -28,18 +31,29 @@ using namespace stacr;
 namespace {
 
 constexpr int kOSlab = 16;          // output features per workgroup
-constexpr int kAccPitch = 17;       // LDS row pitch of S: odd, so random rows spread over banks
-constexpr int kMaxISlab = 1024;     // input features per part: 1024 x 17 fp32 = 68 KiB of LDS
+constexpr int kMaxISlab = 1024;     // input features per part: S = 1024 x 16 fp32 = 64 KiB of LDS
 constexpr int kBwdThreads = 512;    // 8 waves
-constexpr int kPiece = 32;          // residual entries per register-accumulated piece
-constexpr int kRoundCap = 4096;     // residual entries bucketed per round
-constexpr int kTaskCap = kMaxISlab + kRoundCap / kPiece;  // pieces of one round (bound)
-constexpr int kHeavyCap = kRoundCap / (kPiece + 1) + 1;   // features cut into > 1 piece (bound)
-constexpr int kSlotCap = 2 * kRoundCap / kPiece;          // partial sums of those pieces (bound)
-constexpr uint32_t kDirect = 0xffffu;                     // task slot: add straight into S
-constexpr int kEntPT = kRoundCap / kBwdThreads;                      // staged entries per thread
+constexpr int kRoundMax = 4096;     // residual entries bucketed per round (16-bit G; 2048 for fp32)
+constexpr int kMinPiece = 8;        // shortest piece (entries)
+constexpr int kMaxGroups = 256;     // piece groups of the widest configuration
+// A round's n entries are cut into pieces of P = clamp(ceil(n / groups), kMinPiece, 255) entries:
+// a feature with <= P entries is one piece, a longer ("heavy") one ceil(count / P) pieces.  Heavy
+// features hold > P entries each, so there are < n / P <= groups of them, and their pieces number
+// < 2 n / P <= 2 groups.  Pieces in all: < 2 groups + the features of the part.
+constexpr int kSlotCap = 2 * kMaxGroups;                  // partial sums of heavy pieces
+constexpr int kHeavyCap = kMaxGroups;                     // heavy features per round
+constexpr int kTaskCap = kMaxISlab + kSlotCap;            // pieces per round
+constexpr uint32_t kDirect = 0xffffu;                     // piece slot: add straight into S
 constexpr int kTaskPT = (kTaskCap + kBwdThreads - 1) / kBwdThreads;  // staged pieces per thread
 static_assert(kHeavyCap <= kBwdThreads, "one heavy record per thread");
+
+// S row i holds the 16 outputs as four 16-byte chunks; chunk q sits at position q ^ (i & 3), which
+// spreads rows over the LDS banks while keeping every chunk 16-byte aligned.
+constexpr int kAccPitch = kOSlab;
+__device__ __forceinline__ int s_index(int i, int o)
+{
+    return i * kOSlab + ((((o >> 2) ^ i) & 3) << 2) + (o & 3);
+}
 
 template <int DT, int R>
 struct GradCfg {
@@ -53,6 +67,11 @@ struct GradCfg {
     static constexpr int VB = OT * (int)sizeof(T);     // G bytes per thread per row
     static constexpr int NV = OT * (R + 1);            // accumulator values per thread
     static constexpr int CW = R * (int)sizeof(T) / 4;  // 32-bit words of one (padded) C row
+    static constexpr int NGRP = kBwdThreads / OG;      // piece groups (OG threads each)
+    static constexpr int ROUND = k16 ? kRoundMax : kRoundMax / 2;  // entries per round
+    static constexpr int EPT = ROUND / kBwdThreads;    // staged entries per thread
+    static constexpr int PD = 1;                       // blocks of C rows / plan data loaded ahead
+    static constexpr int GD = R <= 8 ? 2 : 1;          // blocks of G rows loaded ahead
 };
 
 template <int B> struct Vec;
@@ -151,8 +170,8 @@ __global__ void k_rowptr(const void *__restrict__ idx, int64_t nnz, int64_t d_in
 
 // ------------------------------------------------------------------ the plan
 // One round of one (block, part): its bucketed entries, pieces and heavy records all start at
-// plan slot `base` (a part's entries of a round occupy a private slot range; it never has more
-// pieces or heavy records than entries).
+// plan slot `base` (a part's entries of a round occupy a private slot range, and it never has
+// more pieces or heavy records than entries).
 struct RoundHdr {
     uint32_t base;
     uint32_t n_ent;
@@ -174,11 +193,13 @@ struct PlanArgs {
     int64_t nnz, rows, d_in;
     int64_t n_parts, i_span;
     int tb;                  // token rows per block
+    uint32_t round_cap;      // entries per round (<= kRoundMax)
+    uint32_t groups;         // piece groups of the streaming kernel
     uint32_t max_rounds;     // rounds the header array holds
     const uint32_t *rowptr;
-    uint32_t *ent;           // [nnz] t_local << 16 | 16-bit value code, or t_local (fp32 G)
-    float *val;              // [nnz] fp32 values (fp32 G only)
-    uint2 *task;             // [nnz] {feature | slot << 16, entry offset << 6 | entries}
+    void *ent;               // [nnz] 16-bit G: t_local << 16 | value code (uint32);
+                             //       fp32 G: {t_local, value bits} (uint2)
+    uint2 *task;             // [nnz] {feature | slot << 16, entry offset << 8 | entries}
     uint2 *heavy;            // [nnz] {feature | first slot << 16, pieces}
     RoundHdr *rhdr;          // [global round][part]
     BlockHdr *bhdr;          // [block][part]
@@ -207,7 +228,7 @@ template <int IDX64>
 __global__ __launch_bounds__(kBwdThreads) void k_dw_plan(PlanArgs a)
 {
     __shared__ uint32_t cnt[kMaxISlab], ccur[kMaxISlab];
-    __shared__ uint32_t cstart[kMaxISlab], tstart[kMaxISlab], hstart[kMaxISlab], hidx[kMaxISlab];
+    __shared__ uint32_t cstart[kMaxISlab], lstart[kMaxISlab], hstart[kMaxISlab], hidx[kMaxISlab];
     __shared__ uint32_t s_tot[kBwdThreads / 64];
     __shared__ uint32_t s_first;
     const int64_t b = blockIdx.x, p = blockIdx.y;
@@ -225,13 +246,14 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_plan(PlanArgs a)
     };
     uint32_t e0, e1;
     range(b, e0, e1);
-    uint32_t n_rounds = (e1 - e0 + kRoundCap - 1) / kRoundCap;
+    const uint32_t cap = a.round_cap;
+    uint32_t n_rounds = (e1 - e0 + cap - 1) / cap;
     if (threadIdx.x < 64) {  // rounds of the blocks before this one
         uint32_t r = 0;
         for (int64_t bb = threadIdx.x; bb < b; bb += 64) {
             uint32_t x0, x1;
             range(bb, x0, x1);
-            r += (x1 - x0 + kRoundCap - 1) / kRoundCap;
+            r += (x1 - x0 + cap - 1) / cap;
         }
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) r += __shfl_xor(r, off, 64);
@@ -242,17 +264,19 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_plan(PlanArgs a)
     if (first + n_rounds > a.max_rounds) n_rounds = 0;  // only for indices that are not ascending
     if (threadIdx.x == 0 && n_rounds == 0)
         a.bhdr[b * a.n_parts + p] = BlockHdr{RoundHdr{0u, 0u, 0u, 0u}, first, 0u, {0u, 0u}};
+    const bool f32 = a.g_dt == STACR_DTYPE_F32;
     for (uint32_t j = 0; j < n_rounds; ++j) {
-        const uint32_t c0 = e0 + j * kRoundCap, c1 = min(c0 + (uint32_t)kRoundCap, e1);
+        const uint32_t c0 = e0 + j * cap, c1 = min(c0 + cap, e1);
         for (int c = threadIdx.x; c < ni; c += kBwdThreads) {
             cnt[c] = 0u;
             ccur[c] = 0u;
         }
         __syncthreads();
-        uint32_t col[kEntPT], tl[kEntPT];
+        constexpr int EPT = kRoundMax / kBwdThreads;
+        uint32_t col[EPT], tl[EPT];
         uint32_t before = 0;
 #pragma unroll
-        for (int k = 0; k < kEntPT; ++k) {
+        for (int k = 0; k < EPT; ++k) {
             col[k] = 0xffffffffu;
             tl[k] = 0u;
             const uint32_t e = c0 + threadIdx.x + k * kBwdThreads;
@@ -273,56 +297,60 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_plan(PlanArgs a)
         uint32_t n_before;
         block_exclusive_scan<kBwdThreads>(before, s_tot, &n_before);  // also orders the counts
         const uint32_t base = c0 + n_before;
-        // prefix sums over the features (two per thread): bucket starts, piece starts, partial-sum
-        // slots and heavy-record positions
+        // prefix sums over the features (two per thread): bucket starts; then, with the piece
+        // length fixed by the part's entry count, heavy-piece starts (= partial-sum slots), light
+        // piece positions and heavy-record positions.  Heavy pieces come first in the piece list,
+        // so the longest work starts first.
+        uint32_t piece;
         {
             const int f0 = 2 * threadIdx.x;
             const uint32_t n0 = f0 < ni ? cnt[f0] : 0u, n1 = f0 + 1 < ni ? cnt[f0 + 1] : 0u;
-            const uint32_t p0 = (n0 + kPiece - 1) / kPiece, p1 = (n1 + kPiece - 1) / kPiece;
-            const uint32_t h0 = p0 > 1 ? p0 : 0u, h1 = p1 > 1 ? p1 : 0u;
-            const uint32_t x0 = p0 > 1, x1 = p1 > 1;
-            uint32_t tot_e, tot_p, tot_h, tot_x;
+            uint32_t tot_e, tot_h, tot_l, tot_x;
             const uint32_t se = block_exclusive_scan<kBwdThreads>(n0 + n1, s_tot, &tot_e);
-            const uint32_t sp = block_exclusive_scan<kBwdThreads>(p0 + p1, s_tot, &tot_p);
+            piece = min(max((tot_e + a.groups - 1) / a.groups, (uint32_t)kMinPiece), 255u);
+            const uint32_t p0 = (n0 + piece - 1) / piece, p1 = (n1 + piece - 1) / piece;
+            const uint32_t h0 = p0 > 1 ? p0 : 0u, h1 = p1 > 1 ? p1 : 0u;
+            const uint32_t l0 = p0 == 1, l1 = p1 == 1;
             const uint32_t sh = block_exclusive_scan<kBwdThreads>(h0 + h1, s_tot, &tot_h);
-            const uint32_t sx = block_exclusive_scan<kBwdThreads>(x0 + x1, s_tot, &tot_x);
+            const uint32_t sl = block_exclusive_scan<kBwdThreads>(l0 + l1, s_tot, &tot_l);
+            const uint32_t sx = block_exclusive_scan<kBwdThreads>((p0 > 1) + (p1 > 1), s_tot, &tot_x);
             if (f0 < ni) {
-                cstart[f0] = se; tstart[f0] = sp; hstart[f0] = sh; hidx[f0] = sx;
+                cstart[f0] = se; hstart[f0] = sh; lstart[f0] = tot_h + sl; hidx[f0] = sx;
             }
             if (f0 + 1 < ni) {
-                cstart[f0 + 1] = se + n0; tstart[f0 + 1] = sp + p0; hstart[f0 + 1] = sh + h0; hidx[f0 + 1] = sx + x0;
+                cstart[f0 + 1] = se + n0; hstart[f0 + 1] = sh + h0; lstart[f0 + 1] = tot_h + sl + l0;
+                hidx[f0 + 1] = sx + (p0 > 1);
             }
             if (threadIdx.x == 0) {
-                const RoundHdr h{base, tot_e, tot_p, tot_x};
+                const RoundHdr h{base, tot_e, tot_h + tot_l, tot_x};
                 a.rhdr[(int64_t)(first + j) * a.n_parts + p] = h;
                 if (j == 0) a.bhdr[b * a.n_parts + p] = BlockHdr{h, first, n_rounds, {0u, 0u}};
             }
         }
         __syncthreads();
 #pragma unroll
-        for (int k = 0; k < kEntPT; ++k) {
+        for (int k = 0; k < EPT; ++k) {
             if (col[k] != 0xffffffffu) {
                 const uint32_t e = c0 + threadIdx.x + k * kBwdThreads;
                 const uint32_t pos = base + cstart[col[k]] + atomicAdd(&ccur[col[k]], 1u);
                 const uint32_t v = entry_value(a, e);
-                if (a.g_dt == STACR_DTYPE_F32) {
-                    a.ent[pos] = tl[k];
-                    a.val[pos] = __uint_as_float(v);
-                } else {
-                    a.ent[pos] = (tl[k] << 16) | (v & 0xffffu);
-                }
+                if (f32)
+                    static_cast<uint2 *>(a.ent)[pos] = make_uint2(tl[k], v);
+                else
+                    static_cast<uint32_t *>(a.ent)[pos] = (tl[k] << 16) | (v & 0xffffu);
             }
         }
         for (int c = threadIdx.x; c < ni; c += kBwdThreads) {
             const uint32_t n = cnt[c];
-            const uint32_t npc = (n + kPiece - 1) / kPiece;
+            const uint32_t npc = (n + piece - 1) / piece;
+            if (npc == 1) a.task[base + lstart[c]] = make_uint2((uint32_t)c | (kDirect << 16), (cstart[c] << 8) | n);
+            if (npc < 2) continue;
             for (uint32_t pc = 0; pc < npc; ++pc) {
-                const uint32_t slot = npc > 1 ? hstart[c] + pc : kDirect;
-                const uint32_t len = min((uint32_t)kPiece, n - pc * kPiece);
-                a.task[base + tstart[c] + pc] =
-                    make_uint2((uint32_t)c | (slot << 16), ((cstart[c] + pc * kPiece) << 6) | len);
+                const uint32_t len = min(piece, n - pc * piece);
+                a.task[base + hstart[c] + pc] =
+                    make_uint2((uint32_t)c | ((hstart[c] + pc) << 16), ((cstart[c] + pc * piece) << 8) | len);
             }
-            if (npc > 1) a.heavy[base + hidx[c]] = make_uint2((uint32_t)c | (hstart[c] << 16), npc);
+            a.heavy[base + hidx[c]] = make_uint2((uint32_t)c | (hstart[c] << 16), npc);
         }
         __syncthreads();
     }
@@ -336,8 +364,7 @@ struct FusedArgs {
     const float *scale;
     int bits;
     int64_t nnz;
-    const uint32_t *ent;
-    const float *val;
+    const void *ent;
     const uint2 *task;
     const uint2 *heavy;
     const RoundHdr *rhdr;
@@ -358,11 +385,11 @@ template <int DT, int R>
 struct FusedLds {
     using C = GradCfg<DT, R>;
     using T = typename C::T;
-    static constexpr size_t s_acc = 0;                                               // [1024][17] f32
-    static constexpr size_t s_gtile = s_acc + (size_t)kMaxISlab * kAccPitch * 4;     // [TB][16] T
-    static constexpr size_t s_ent = s_gtile + (size_t)C::TB * kOSlab * sizeof(T);    // [kRoundCap]
-    static constexpr size_t s_val = s_ent + (size_t)kRoundCap * 4;                   // fp32 G only
-    static constexpr size_t s_task = s_val + (C::k16 ? 0 : (size_t)kRoundCap * 4);   // [kTaskCap]
+    static constexpr size_t ent_bytes = C::k16 ? 4 : 8;
+    static constexpr size_t s_acc = 0;                                               // [1024][16] f32
+    static constexpr size_t s_gtile = s_acc + (size_t)kMaxISlab * kAccPitch * 4;     // [TB + 1][16] T
+    static constexpr size_t s_ent = s_gtile + (size_t)(C::TB + 1) * kOSlab * sizeof(T);  // [ROUND]
+    static constexpr size_t s_task = s_ent + (size_t)C::ROUND * ent_bytes;           // [kTaskCap]
     static constexpr size_t s_heavy = s_task + (size_t)kTaskCap * 8;                 // [kHeavyCap]
     static constexpr size_t s_slot = s_heavy + (size_t)kHeavyCap * 8;                // [kSlotCap][16]
     static constexpr size_t end = s_slot + (size_t)kSlotCap * kOSlab * 4;
@@ -373,10 +400,9 @@ struct FusedLds {
 };
 
 // A round's plan data held in registers between its load and its copy into LDS.
-template <bool K16>
+template <typename E, int EPT>
 struct Staged {
-    uint32_t ent[kEntPT];
-    float val[K16 ? 1 : kEntPT];
+    E ent[EPT];
     uint2 task[kTaskPT];
     uint2 heavy;
 };
@@ -388,15 +414,17 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
     using T = typename C::T;
     using L = FusedLds<DT, R>;
     constexpr int OT = C::OT, OG = C::OG, TB = C::TB, VB = C::VB, NW = Vec<C::VB>::n, CW = C::CW;
-    constexpr int NGRP = kBwdThreads / OG;  // piece groups working at once
+    constexpr int ROUND = C::ROUND, EPT = C::EPT;
     constexpr bool K16 = C::k16;
+    using E = typename std::conditional<K16, uint32_t, uint2>::type;  // plan entry
+    using Stage = Staged<E, EPT>;
+    constexpr int NGRP = C::NGRP;
 
     extern __shared__ float lds[];
     char *base = reinterpret_cast<char *>(lds);
     float *acc = reinterpret_cast<float *>(base + L::s_acc);
     T *gtile = reinterpret_cast<T *>(base + L::s_gtile);
-    uint32_t *l_ent = reinterpret_cast<uint32_t *>(base + L::s_ent);
-    float *l_val = reinterpret_cast<float *>(base + L::s_val);
+    E *l_ent = reinterpret_cast<E *>(base + L::s_ent);
     uint2 *l_task = reinterpret_cast<uint2 *>(base + L::s_task);
     uint2 *l_heavy = reinterpret_cast<uint2 *>(base + L::s_heavy);
     float *l_slot = reinterpret_cast<float *>(base + L::s_slot);
@@ -422,6 +450,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
     const float qscale = (sparse && a.bits) ? a.scale[0] : 1.f;
 
     for (int i = threadIdx.x; i < ni * kAccPitch; i += kBwdThreads) acc[i] = 0.f;
+    for (int i = threadIdx.x; i < kOSlab; i += kBwdThreads) gtile[TB * kOSlab + i] = T{};  // zero row
 
     float m[OT][R + 1];
 #pragma unroll
@@ -455,25 +484,31 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
         }
     };
 
-    // G and C rows of the next block, one block ahead
-    uint32_t wa[NW], wb[NW], xa[CW], xb[CW];
-    auto prefetch = [&](int64_t blk) {
+    // What a block needs is loaded ahead into register rings (slot d of a ring holds block
+    // blk + d at the top of iteration blk): G rows GD blocks ahead, C rows and the block's first
+    // plan round PD blocks ahead; the block headers that locate those rounds two further blocks.
+    constexpr int PD = C::PD, GD = C::GD;
+    uint32_t wq[GD][2][NW], xq[PD][2][CW];
+    auto load_grows = [&](int64_t blk, uint32_t (&w)[2][NW]) {
         const int64_t t = blk * TB + 2 * tp;
-        load_g<DT, VB>(g + t * a.d_out, ob, a.d_out, o_ok && t < a.rows, vec_ok, wa);
-        load_g<DT, VB>(g + (t + 1) * a.d_out, ob, a.d_out, o_ok && t + 1 < a.rows, vec_ok, wb);
-        load_c(t, xa);
-        load_c(t + 1, xb);
+        load_g<DT, VB>(g + t * a.d_out, ob, a.d_out, o_ok && t < a.rows, vec_ok, w[0]);
+        load_g<DT, VB>(g + (t + 1) * a.d_out, ob, a.d_out, o_ok && t + 1 < a.rows, vec_ok, w[1]);
+    };
+    auto load_crows = [&](int64_t blk, uint32_t (&x)[2][CW]) {
+        const int64_t t = blk * TB + 2 * tp;
+        load_c(t, x[0]);
+        load_c(t + 1, x[1]);
     };
 
     // plan data of a round: global -> registers -> LDS (round sizes are bounded by the planner;
     // the clamps only keep a malformed plan inside the buffers)
-    auto load_stage = [&](Staged<K16> &st, const RoundHdr &h) {
-        const uint32_t ne = min(h.n_ent, (uint32_t)kRoundCap), nt = min(h.n_task, (uint32_t)kTaskCap);
+    auto load_stage = [&](Stage &st, const RoundHdr &h) {
+        const uint32_t ne = min(h.n_ent, (uint32_t)ROUND), nt = min(h.n_task, (uint32_t)kTaskCap);
+        const E *ge = static_cast<const E *>(a.ent) + h.base;
 #pragma unroll
-        for (int k = 0; k < kEntPT; ++k) {
+        for (int k = 0; k < EPT; ++k) {
             const uint32_t e = threadIdx.x + k * kBwdThreads;
-            st.ent[k] = e < ne ? a.ent[h.base + e] : 0u;
-            if constexpr (!K16) st.val[k] = e < ne ? a.val[h.base + e] : 0.f;
+            st.ent[k] = e < ne ? ge[e] : E{};
         }
 #pragma unroll
         for (int k = 0; k < kTaskPT; ++k) {
@@ -483,61 +518,95 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
         st.heavy = threadIdx.x < min(h.n_heavy, (uint32_t)kHeavyCap) ? a.heavy[h.base + threadIdx.x]
                                                                      : make_uint2(0u, 0u);
     };
-    auto store_stage = [&](const Staged<K16> &st) {
+    auto store_stage = [&](const Stage &st) {
 #pragma unroll
-        for (int k = 0; k < kEntPT; ++k) {
-            l_ent[threadIdx.x + k * kBwdThreads] = st.ent[k];
-            if constexpr (!K16) l_val[threadIdx.x + k * kBwdThreads] = st.val[k];
-        }
+        for (int k = 0; k < EPT; ++k) l_ent[threadIdx.x + k * kBwdThreads] = st.ent[k];
 #pragma unroll
         for (int k = 0; k < kTaskPT; ++k)
             if (threadIdx.x + k * kBwdThreads < kTaskCap) l_task[threadIdx.x + k * kBwdThreads] = st.task[k];
         if (threadIdx.x < kHeavyCap) l_heavy[threadIdx.x] = st.heavy;
     };
 
-    // sum the round's pieces (staged in LDS; the G tile complete) into S
+    // One piece's entries [e_lo, e_lo + n) accumulated into pa (this thread's OT outputs).  Four
+    // entries per batch with no branch inside a batch, so their loads issue together; entries past
+    // the piece are redirected to the all-zero G row TB with a zero value, which adds exactly 0.
+    auto piece_batch = [&](uint32_t e, uint32_t e_lo, uint32_t n, float (&pa)[OT]) {
+        const uint32_t last = e_lo + (n ? n - 1 : 0u);
+        E w[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const E x = l_ent[min(e + u, last) % ROUND];
+            const bool valid = e + u < e_lo + n;
+            if constexpr (K16) w[u] = valid ? x : (uint32_t)TB << 16;
+            else w[u] = valid ? x : make_uint2((uint32_t)TB, 0u);
+        }
+        uint32_t gw[4][NW];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            uint32_t row;
+            if constexpr (K16) row = w[u] >> 16;
+            else row = w[u].x;
+            load_words<VB>(gtile + min(row, (uint32_t)TB) * kOSlab + og * OT, gw[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if constexpr (K16) {
+                const uint32_t vlo = w[u] & 0xffffu, vhi = w[u] << 16;  // (v, 0) and (0, v)
+#pragma unroll
+                for (int k = 0; k < NW; ++k) {
+                    pa[2 * k] = dot2<DT>(gw[u][k], vlo, pa[2 * k]);
+                    pa[2 * k + 1] = dot2<DT>(gw[u][k], vhi, pa[2 * k + 1]);
+                }
+            } else {
+                const float v = __uint_as_float(w[u].y);
+#pragma unroll
+                for (int o = 0; o < OT; ++o) pa[o] = fmaf(__uint_as_float(gw[u][o]), v, pa[o]);
+            }
+        }
+    };
+    // A piece's sum: added (scaled) into S, or parked in its slot when the feature has several.
+    auto flush = [&](uint2 td, const float (&pa)[OT]) {
+        const uint32_t c = td.x & 0xffffu, slot = td.x >> 16;
+        if (c >= (uint32_t)ni) return;
+        if (slot == kDirect) {
+            if constexpr (OT >= 4) {
+#pragma unroll
+                for (int q4 = 0; q4 < OT / 4; ++q4) {
+                    float4 *dst = reinterpret_cast<float4 *>(acc + s_index((int)c, og * OT + 4 * q4));
+                    float4 v = *dst;
+                    v.x = fmaf(pa[4 * q4], qscale, v.x);
+                    v.y = fmaf(pa[4 * q4 + 1], qscale, v.y);
+                    v.z = fmaf(pa[4 * q4 + 2], qscale, v.z);
+                    v.w = fmaf(pa[4 * q4 + 3], qscale, v.w);
+                    *dst = v;
+                }
+            } else {
+#pragma unroll
+                for (int o = 0; o < OT; ++o) {
+                    float *dst = acc + s_index((int)c, og * OT + o);
+                    *dst = fmaf(pa[o], qscale, *dst);
+                }
+            }
+        } else if (slot < (uint32_t)kSlotCap) {
+            float *dst = l_slot + slot * kOSlab + og * OT;
+#pragma unroll
+            for (int o = 0; o < OT; ++o) dst[o] = pa[o];
+        }
+    };
+
+    // Sum the round's pieces (staged in LDS, the G tile complete) into S.  Group g (OG threads)
+    // takes pieces g, g + NGRP, g + 2 NGRP, ...
     auto run_round = [&](const RoundHdr &h) {
         const uint32_t nt = min(h.n_task, (uint32_t)kTaskCap), nh = min(h.n_heavy, (uint32_t)kHeavyCap);
         if (o_ok) {
             for (uint32_t tk = threadIdx.x / OG; tk < nt; tk += NGRP) {
                 const uint2 td = l_task[tk];
-                const uint32_t c = td.x & 0xffffu, slot = td.x >> 16;
-                const uint32_t e_lo = min(td.y >> 6, (uint32_t)kRoundCap);
-                const uint32_t e_hi = min(e_lo + (td.y & 63u), (uint32_t)kRoundCap);
-                float pacc[OT];
+                const uint32_t lo = td.y >> 8, n = td.y & 255u;
+                float pa[OT];
 #pragma unroll
-                for (int o = 0; o < OT; ++o) pacc[o] = 0.f;
-                for (uint32_t e = e_lo; e < e_hi; ++e) {
-                    const uint32_t wv = l_ent[e];
-                    if constexpr (K16) {
-                        const uint32_t *src =
-                            reinterpret_cast<const uint32_t *>(gtile + ((wv >> 16) % TB) * kOSlab + og * OT);
-                        uint32_t gw[NW];
-#pragma unroll
-                        for (int k = 0; k < NW; ++k) gw[k] = src[k];
-                        const uint32_t vlo = wv & 0xffffu, vhi = wv << 16;  // (v, 0) and (0, v)
-#pragma unroll
-                        for (int k = 0; k < NW; ++k) {
-                            pacc[2 * k] = dot2<DT>(gw[k], vlo, pacc[2 * k]);
-                            pacc[2 * k + 1] = dot2<DT>(gw[k], vhi, pacc[2 * k + 1]);
-                        }
-                    } else {
-                        const float v = l_val[e];
-                        const float *src = reinterpret_cast<const float *>(gtile) + (wv % TB) * kOSlab + og * OT;
-#pragma unroll
-                        for (int o = 0; o < OT; ++o) pacc[o] = fmaf(src[o], v, pacc[o]);
-                    }
-                }
-                if (c >= (uint32_t)ni) continue;
-                if (slot == kDirect) {
-                    float *dst = acc + c * kAccPitch + og * OT;
-#pragma unroll
-                    for (int o = 0; o < OT; ++o) dst[o] += pacc[o] * qscale;
-                } else if (slot < (uint32_t)kSlotCap) {
-                    float *dst = l_slot + slot * kOSlab + og * OT;
-#pragma unroll
-                    for (int o = 0; o < OT; ++o) dst[o] = pacc[o];
-                }
+                for (int o = 0; o < OT; ++o) pa[o] = 0.f;
+                for (uint32_t k = 0; k < n; k += 4) piece_batch(lo + k, lo, n, pa);
+                flush(td, pa);
             }
         }
         __syncthreads();
@@ -545,34 +614,46 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
         for (uint32_t w = threadIdx.x; w < nh * kOSlab; w += kBwdThreads) {
             const uint2 hd = l_heavy[w / kOSlab];
             const uint32_t o = w % kOSlab, c = hd.x & 0xffffu, s0 = hd.x >> 16;
-            if (o0 + o < a.d_out && c < (uint32_t)ni && s0 + hd.y <= (uint32_t)kSlotCap) {
-                float s = 0.f;
-                for (uint32_t pc = 0; pc < hd.y; ++pc) s += l_slot[(s0 + pc) * kOSlab + o];
-                acc[c * kAccPitch + o] += s * qscale;
+            if (c < (uint32_t)ni && s0 + hd.y <= (uint32_t)kSlotCap) {
+                // eight interleaved partial sums (independent loads), combined in a fixed order
+                float s8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                uint32_t k = 0;
+                for (; k + 8 <= hd.y; k += 8) {
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) s8[u] += l_slot[(s0 + k + u) * kOSlab + o];
+                }
+                for (; k < hd.y; ++k) s8[0] += l_slot[(s0 + k) * kOSlab + o];
+                const float sum = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
+                acc[s_index((int)c, (int)o)] += sum * qscale;
             }
         }
         __syncthreads();
     };
 
     const int64_t n_blocks = (a.rows + TB - 1) / TB;
-    const BlockHdr zero_hdr{};
-    BlockHdr bh_next = zero_hdr, bh_after = zero_hdr;
-    Staged<K16> st;
-    if (n_blocks > 0) {
-        prefetch(0);
-        if (sparse) {
-            bh_next = a.bhdr[part];
-            load_stage(st, bh_next.r0);
-            if (n_blocks > 1) bh_after = a.bhdr[a.n_parts + part];
-        }
-    }
+    auto load_hdr = [&](int64_t blk) {
+        BlockHdr h{};
+        if (sparse && blk < n_blocks) h = a.bhdr[blk * a.n_parts + part];
+        return h;
+    };
+    BlockHdr hq[PD + 2];
+    Stage sq[PD];
+#pragma unroll
+    for (int d = 0; d < GD; ++d) load_grows(d, wq[d]);  // rows past the matrix load as zero
+#pragma unroll
+    for (int d = 0; d < PD; ++d) load_crows(d, xq[d]);
+#pragma unroll
+    for (int d = 0; d < PD + 2; ++d) hq[d] = load_hdr(d);
+#pragma unroll
+    for (int d = 0; d < PD; ++d)
+        if (hq[d].n_rounds) load_stage(sq[d], hq[d].r0);
     for (int64_t blk = 0; blk < n_blocks; ++blk) {
         uint32_t ca[NW], cb[NW], ya[CW], yb[CW];
 #pragma unroll
-        for (int k = 0; k < NW; ++k) { ca[k] = wa[k]; cb[k] = wb[k]; }
+        for (int k = 0; k < NW; ++k) { ca[k] = wq[0][0][k]; cb[k] = wq[0][1][k]; }
 #pragma unroll
-        for (int k = 0; k < CW; ++k) { ya[k] = xa[k]; yb[k] = xb[k]; }
-        const BlockHdr bh = bh_next;
+        for (int k = 0; k < CW; ++k) { ya[k] = xq[0][0][k]; yb[k] = xq[0][1][k]; }
+        const BlockHdr bh = hq[0];
         if (sparse) {  // this block's G rows and first round of plan data into LDS
             uint32_t *da = reinterpret_cast<uint32_t *>(gtile + (2 * tp) * kOSlab + og * OT);
             uint32_t *db = reinterpret_cast<uint32_t *>(gtile + (2 * tp + 1) * kOSlab + og * OT);
@@ -581,16 +662,27 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
                 da[k] = ca[k];
                 db[k] = cb[k];
             }
-            if (bh.n_rounds) store_stage(st);
+            if (bh.n_rounds) store_stage(sq[0]);
         }
-        if (blk + 1 < n_blocks) {  // the next block's loads overlap this block's arithmetic
-            prefetch(blk + 1);
-            if (sparse) {
-                bh_next = bh_after;
-                if (bh_next.n_rounds) load_stage(st, bh_next.r0);
-                if (blk + 2 < n_blocks) bh_after = a.bhdr[(blk + 2) * a.n_parts + part];
-            }
+        // advance the rings; block blk + PD's loads overlap the arithmetic of this block
+#pragma unroll
+        for (int d = 0; d + 1 < GD; ++d)
+#pragma unroll
+            for (int k = 0; k < NW; ++k) { wq[d][0][k] = wq[d + 1][0][k]; wq[d][1][k] = wq[d + 1][1][k]; }
+#pragma unroll
+        for (int d = 0; d + 1 < PD; ++d) {
+#pragma unroll
+            for (int k = 0; k < CW; ++k) { xq[d][0][k] = xq[d + 1][0][k]; xq[d][1][k] = xq[d + 1][1][k]; }
+            sq[d] = sq[d + 1];
         }
+#pragma unroll
+        for (int d = 0; d + 1 < PD + 2; ++d) hq[d] = hq[d + 1];
+        if (blk + GD < n_blocks) load_grows(blk + GD, wq[GD - 1]);
+        if (blk + PD < n_blocks) {
+            load_crows(blk + PD, xq[PD - 1]);
+            if (hq[PD - 1].n_rounds) load_stage(sq[PD - 1], hq[PD - 1].r0);
+        }
+        hq[PD + 1] = load_hdr(blk + PD + 2);
         // ---- low rank: m[o][j] += G[t][o] C[t][j] + G[t+1][o] C[t+1][j];  m[o][R] += G[t][o] + G[t+1][o]
         if constexpr (K16) {
             uint32_t pr[OT];  // (G[t][o], G[t+1][o]) pairs
@@ -626,9 +718,9 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
         if (!sparse || bh.n_rounds == 0) continue;
         __syncthreads();  // G tile and first round staged
         run_round(bh.r0);
-        for (uint32_t j = 1; j < bh.n_rounds; ++j) {  // blocks with more than kRoundCap entries
+        for (uint32_t j = 1; j < bh.n_rounds; ++j) {  // blocks with more than ROUND entries
             const RoundHdr h = a.rhdr[(int64_t)(bh.first_round + j) * a.n_parts + part];
-            Staged<K16> tmp;
+            Stage tmp;
             load_stage(tmp, h);
             store_stage(tmp);
             __syncthreads();
@@ -681,7 +773,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
         float out[kOSlab];
 #pragma unroll
         for (int oo = 0; oo < kOSlab; ++oo) {
-            float s = acc[ii * kAccPitch + oo];
+            float s = acc[s_index(ii, oo)];
 #pragma unroll
             for (int j = 0; j < R; ++j) s = fmaf(mfin[oo * (R + 1) + j], qr[j], s);
             out[oo] = s;
@@ -715,19 +807,24 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
 
 int pad_rank(int rank) { return rank <= 4 ? 4 : rank <= 8 ? 8 : rank <= 16 ? 16 : 32; }
 
-int block_rows(int dt, int R)
+struct CfgInfo {
+    int tb, round;
+};
+template <int DT, int R> constexpr CfgInfo cfg_info()
+{
+    return CfgInfo{GradCfg<DT, R>::TB, GradCfg<DT, R>::ROUND};
+}
+CfgInfo block_geometry(int dt, int R)
 {
     if (dt == STACR_DTYPE_F32)
-        return R <= 4 ? GradCfg<0, 4>::TB : R <= 8 ? GradCfg<0, 8>::TB : R <= 16 ? GradCfg<0, 16>::TB
-                                                                                   : GradCfg<0, 32>::TB;
-    return R <= 4 ? GradCfg<1, 4>::TB : R <= 8 ? GradCfg<1, 8>::TB : R <= 16 ? GradCfg<1, 16>::TB
-                                                                             : GradCfg<1, 32>::TB;
+        return R <= 4 ? cfg_info<0, 4>() : R <= 8 ? cfg_info<0, 8>() : R <= 16 ? cfg_info<0, 16>() : cfg_info<0, 32>();
+    return R <= 4 ? cfg_info<1, 4>() : R <= 8 ? cfg_info<1, 8>() : R <= 16 ? cfg_info<1, 16>() : cfg_info<1, 32>();
 }
 
-enum { GW_ROWPTR, GW_ENT, GW_VAL, GW_TASK, GW_HEAVY, GW_RHDR, GW_BHDR, GW_N };
+enum { GW_ROWPTR, GW_ENT, GW_TASK, GW_HEAVY, GW_RHDR, GW_BHDR, GW_N };
 
 struct GPlan {
-    int R, tb;
+    int R, tb, round_cap;
     int64_t n_slabs, n_parts, i_span, n_blocks, max_rounds;
 };
 
@@ -738,9 +835,11 @@ GPlan make_gplan(const StacrGradArgs &a)
     p.n_slabs = (a.d_out + kOSlab - 1) / kOSlab;
     p.n_parts = hmax<int64_t>(1, (a.d_in + kMaxISlab - 1) / kMaxISlab);
     p.i_span = (a.d_in + p.n_parts - 1) / p.n_parts;
-    p.tb = block_rows(a.dtype, p.R);
+    const CfgInfo ci = block_geometry(a.dtype, p.R);
+    p.tb = ci.tb;
+    p.round_cap = ci.round;
     p.n_blocks = (a.rows + p.tb - 1) / p.tb;
-    p.max_rounds = a.nnz / kRoundCap + p.n_blocks + 1;  // sum over blocks of ceil(entries / cap)
+    p.max_rounds = a.nnz / p.round_cap + p.n_blocks + 1;  // sum over blocks of ceil(entries / cap)
     return p;
 }
 
@@ -751,8 +850,7 @@ size_t glayout(const StacrGradArgs &a, const GPlan &p, size_t *off)
     const bool sp = a.nnz > 0;
     const size_t n = sp ? (size_t)a.nnz : 0;
     take(GW_ROWPTR, sp ? (size_t)(a.rows + 1) * 4 : 0);
-    take(GW_ENT, n * 4);
-    take(GW_VAL, a.dtype == STACR_DTYPE_F32 ? n * 4 : 0);
+    take(GW_ENT, n * 8);
     take(GW_TASK, n * 8);
     take(GW_HEAVY, n * 8);
     take(GW_RHDR, sp ? (size_t)p.max_rounds * p.n_parts * sizeof(RoundHdr) : 0);
@@ -820,10 +918,11 @@ int launch_grad(const StacrGradArgs &a, const GPlan &p, char *ws, const size_t *
         pa.n_parts = p.n_parts;
         pa.i_span = p.i_span;
         pa.tb = p.tb;
+        pa.round_cap = (uint32_t)p.round_cap;
         pa.max_rounds = (uint32_t)p.max_rounds;
         pa.rowptr = rowptr;
-        pa.ent = reinterpret_cast<uint32_t *>(ws + off[GW_ENT]);
-        pa.val = reinterpret_cast<float *>(ws + off[GW_VAL]);
+        pa.groups = (uint32_t)Cfg::NGRP;
+        pa.ent = ws + off[GW_ENT];
         pa.task = reinterpret_cast<uint2 *>(ws + off[GW_TASK]);
         pa.heavy = reinterpret_cast<uint2 *>(ws + off[GW_HEAVY]);
         pa.rhdr = reinterpret_cast<RoundHdr *>(ws + off[GW_RHDR]);
@@ -834,7 +933,6 @@ int launch_grad(const StacrGradArgs &a, const GPlan &p, char *ws, const size_t *
         else
             stacr_launch("k_dw_plan", s, [&] { k_dw_plan<0><<<pg, kBwdThreads, 0, s>>>(pa); });
         f.ent = pa.ent;
-        f.val = pa.val;
         f.task = pa.task;
         f.heavy = pa.heavy;
         f.rhdr = pa.rhdr;
