@@ -64,6 +64,18 @@ struct QCols {
     __device__ __forceinline__ void init(const float *__restrict__ qp, int64_t col, int64_t d)
     {
         if constexpr (QREG) {
+            if (col + V <= d) {  // V * R contiguous floats, 16-byte aligned: vector loads, no branches
+                const float4 *src = reinterpret_cast<const float4 *>(qp + col * R);
+#pragma unroll
+                for (int k = 0; k < V * R / 4; ++k) {
+                    const float4 v = src[k];
+                    q[(4 * k) / R][(4 * k) % R] = v.x;
+                    q[(4 * k + 1) / R][(4 * k + 1) % R] = v.y;
+                    q[(4 * k + 2) / R][(4 * k + 2) % R] = v.z;
+                    q[(4 * k + 3) / R][(4 * k + 3) % R] = v.w;
+                }
+                return;
+            }
 #pragma unroll
             for (int e = 0; e < V; ++e)
 #pragma unroll
@@ -459,6 +471,416 @@ __global__ __launch_bounds__(kBlock) void k_emit(SaveGeom g, const typename Act<
     }
 }
 
+// ------------------------------------------------------------------ batched fast path
+// Rows of d <= 256 * V features whose vectors are aligned: every thread holds one V-wide vector
+// of a row and the basis rows of its V columns in registers; L = 64 * W threads (W waves) share a
+// row and 256 / L row slots run side by side.  A batch is NB = 64 / R iterations of the slots, and
+// everything a batch needs (NB vectors of X per thread, NB coefficient rows) is loaded before any
+// of it is used, so a batch costs one memory round trip and at most two barriers.
+template <int R> struct Batch {
+    static constexpr int NB = 64 / R;  // iterations per batch: NB * R = 64 values per row slot
+};
+
+// Raw V-wide vector of X (one 16-byte load), zero when the row is outside the workgroup's range.
+template <int DT, int V>
+__device__ __forceinline__ uint4 load_raw(const typename Act<DT>::T *__restrict__ p, bool ok)
+{
+    static_assert(V * sizeof(typename Act<DT>::T) == 16, "fast path uses 16-byte vectors");
+    return ok ? *reinterpret_cast<const uint4 *>(p) : make_uint4(0u, 0u, 0u, 0u);
+}
+
+template <int DT, int V>
+__device__ __forceinline__ void unpack_raw(const uint4 &w, float (&x)[V])
+{
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+    if constexpr (V == 4) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = __uint_as_float(u[e]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = Act<DT>::ld((typename Act<DT>::T)((u[e / 2] >> (16 * (e & 1))) & 0xffffu));
+    }
+}
+
+// Sum 64 values (v = i * R + j) over the 64 lanes of a wave: six halving exchanges leave lane l
+// with the wave's total of value l.
+__device__ __forceinline__ float wave_reduce_scatter64(float (&a)[64])
+{
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int st = 0; st < 6; ++st) {
+        const int o = 32 >> st, half = 32 >> st;
+        const bool upper = (lane & o) != 0;
+        // both halves cross (the select then picks between computed sums, never between array
+        // elements, which keeps a[] in registers)
+#pragma unroll
+        for (int k = 0; k < half; ++k) {
+            const float lo = a[k] + __shfl_xor(a[k], o, 64);
+            const float hi = a[k + half] + __shfl_xor(a[k + half], o, 64);
+            a[k] = upper ? hi : lo;
+        }
+    }
+    return a[0];
+}
+
+// Coefficients of the NB rows of a batch for this thread's slot, as the activation dtype rounds
+// them.  Pass 1 computes them (acc holds the thread's partial sums, flattened i * R + j) and
+// writes them to `coeff`; the later passes load them.  s_c holds [slot][64] floats.
+template <int DT, int R>
+__device__ __forceinline__ void batch_coeff_from_acc(float (&acc)[64], int W, int slot, float *s_part, float *s_c,
+                                                     const int64_t (&rows)[Batch<R>::NB], int64_t row_end, int rank,
+                                                     typename Act<DT>::T *__restrict__ coeff, float (&c)[64])
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float part = wave_reduce_scatter64(acc);
+    if (W > 1) s_part[wave * 64 + lane] = part;
+    __syncthreads();
+    const int w0 = slot * W;  // first wave of the slot
+    if (wave == w0) {
+        float tot = part;
+        for (int w = 1; w < W; ++w) tot += s_part[(w0 + w) * 64 + lane];
+        const float cv = Act<DT>::rnd(tot);
+        s_c[slot * 64 + lane] = cv;
+        const int i = lane / R, j = lane % R;
+        if (j < rank && rows[i] < row_end) coeff[rows[i] * rank + j] = Act<DT>::st(cv);
+    }
+    __syncthreads();
+    const float4 *src = reinterpret_cast<const float4 *>(s_c + slot * 64);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const float4 v = src[k];
+        c[4 * k] = v.x; c[4 * k + 1] = v.y; c[4 * k + 2] = v.z; c[4 * k + 3] = v.w;
+    }
+}
+
+template <int DT, int R>
+__device__ __forceinline__ void batch_coeff_load(const typename Act<DT>::T *__restrict__ coeff, int rank,
+                                                 const int64_t (&rows)[Batch<R>::NB], int64_t row_end, bool vec,
+                                                 float (&c)[64])
+{
+    constexpr int NB = Batch<R>::NB;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const bool ok = rows[i] < row_end;
+        if (vec && sizeof(typename Act<DT>::T) * R % 16 == 0) {  // rank == R, 16-byte aligned rows
+            constexpr int NW = (int)(sizeof(typename Act<DT>::T) * R / 16) > 0 ? (int)(sizeof(typename Act<DT>::T) * R / 16) : 1;
+            const uint4 *src = reinterpret_cast<const uint4 *>(coeff + rows[i] * R);
+#pragma unroll
+            for (int k = 0; k < NW; ++k) {
+                const uint4 w = ok ? src[k] : make_uint4(0u, 0u, 0u, 0u);
+                if constexpr (sizeof(typename Act<DT>::T) == 4) {
+                    c[i * R + 4 * k] = __uint_as_float(w.x); c[i * R + 4 * k + 1] = __uint_as_float(w.y);
+                    c[i * R + 4 * k + 2] = __uint_as_float(w.z); c[i * R + 4 * k + 3] = __uint_as_float(w.w);
+                } else {
+                    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        c[i * R + 8 * k + e] = Act<DT>::ld((typename Act<DT>::T)((u[e / 2] >> (16 * (e & 1))) & 0xffffu));
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < R; ++j) c[i * R + j] = (ok && j < rank) ? Act<DT>::ld(coeff[rows[i] * rank + j]) : 0.f;
+        }
+    }
+}
+
+// Residual keys of one vector: r = x - sum_j c_j q_j (fp32 fma chain, j ascending), |r| bits.
+template <int R, int V>
+__device__ __forceinline__ void batch_residual(const float (&xv)[V], const float *c, const float (&q)[V][R],
+                                               float (&r)[V])
+{
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+        float acc = xv[e];
+#pragma unroll
+        for (int j = 0; j < R; ++j) acc = fmaf(-c[j], q[e][j], acc);
+        r[e] = acc;
+    }
+}
+
+struct FastGeom {
+    int W;       // waves per row slot
+    int c_vec;   // coefficient rows are exactly R wide and 16-byte aligned
+};
+
+// The rows of batch `base` for this thread: base + i * rpi + slot.
+template <int R>
+__device__ __forceinline__ void batch_rows(const SaveGeom &g, int64_t base, int slot, int64_t (&rows)[Batch<R>::NB])
+{
+#pragma unroll
+    for (int i = 0; i < Batch<R>::NB; ++i) rows[i] = base + (int64_t)i * g.rpi + slot;
+}
+
+// Pass 1 (batched): coefficients, first-digit histogram, max key.
+template <int DT, int R, int V>
+__global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg, const typename Act<DT>::T *__restrict__ x,
+                                                        const float *__restrict__ qp, typename Act<DT>::T *__restrict__ coeff,
+                                                        uint32_t *__restrict__ hist, uint32_t *__restrict__ maxkey,
+                                                        int do_hist, const typename Act<DT>::T *__restrict__ coeff_in)
+{
+    constexpr int NB = Batch<R>::NB;
+    __shared__ uint32_t s_hist[kBins];
+    __shared__ __align__(16) float s_part[kWaves * 64];
+    __shared__ __align__(16) float s_c[kWaves * 64];
+    for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
+    int64_t chunk, row0, row_end;
+    wg_rows(g, blockIdx.x, chunk, row0, row_end);
+    const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
+    const int64_t col = (int64_t)u * V;
+    const bool col_ok = col < g.d;
+    QCols<R, V, true> qc;
+    qc.init(qp, col, g.d);
+    uint32_t kmax = 0u;
+    __syncthreads();
+    for (int64_t base = row0; base < row_end; base += (int64_t)NB * g.rpi) {
+        int64_t rows[NB];
+        batch_rows<R>(g, base, slot, rows);
+        uint4 raw[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) raw[i] = load_raw<DT, V>(x + rows[i] * g.d + col, col_ok && rows[i] < row_end);
+        float c[64];
+        if (coeff_in) {
+            batch_coeff_load<DT, R>(coeff_in, g.rank, rows, row_end, fg.c_vec != 0, c);
+        } else {
+            float acc[64];
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                float xv[V];
+                unpack_raw<DT, V>(raw[i], xv);
+#pragma unroll
+                for (int j = 0; j < R; ++j) {
+                    float s = 0.f;
+#pragma unroll
+                    for (int e = 0; e < V; ++e) s = fmaf(xv[e], qc.q[e][j], s);
+                    acc[i * R + j] = s;
+                }
+            }
+            batch_coeff_from_acc<DT, R>(acc, fg.W, slot, s_part, s_c, rows, row_end, g.rank, coeff, c);
+        }
+        if (!do_hist) continue;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            if (!(col_ok && rows[i] < row_end)) continue;
+            float xv[V], r[V];
+            unpack_raw<DT, V>(raw[i], xv);
+            batch_residual<R, V>(xv, c + i * R, qc.q, r);
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
+                atomicAdd(&s_hist[key >> kDigitShift[0]], 1u);
+                kmax = max(kmax, key);
+            }
+        }
+    }
+    if (!do_hist) return;
+    __syncthreads();
+    uint32_t *gh = hist + (chunk * 3 + 0) * kBins;
+    for (int b = threadIdx.x; b < kBins; b += kBlock)
+        if (s_hist[b]) atomicAdd(&gh[b], s_hist[b]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, off, 64));
+    if ((threadIdx.x & 63) == 0 && kmax) atomicMax(maxkey, kmax);
+}
+
+// Passes 2 and 3 (batched): histogram of digit `lvl` among keys matching the prefix so far.
+template <int DT, int R, int V>
+__global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom fg, int lvl,
+                                                          const typename Act<DT>::T *__restrict__ x,
+                                                          const float *__restrict__ qp,
+                                                          const typename Act<DT>::T *__restrict__ coeff,
+                                                          uint32_t *__restrict__ hist, const SelState *__restrict__ state)
+{
+    constexpr int NB = Batch<R>::NB;
+    __shared__ uint32_t s_hist[kBins];
+    for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
+    int64_t chunk, row0, row_end;
+    wg_rows(g, blockIdx.x, chunk, row0, row_end);
+    const uint32_t prefix = state[chunk * 3 + lvl - 1].prefix;
+    const int match_shift = kDigitShift[lvl - 1], dshift = kDigitShift[lvl];
+    const uint32_t dmask = (uint32_t)kDigitBins[lvl] - 1u;
+    const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
+    const int64_t col = (int64_t)u * V;
+    const bool col_ok = col < g.d;
+    QCols<R, V, true> qc;
+    qc.init(qp, col, g.d);
+    __syncthreads();
+    for (int64_t base = row0; base < row_end; base += (int64_t)NB * g.rpi) {
+        int64_t rows[NB];
+        batch_rows<R>(g, base, slot, rows);
+        uint4 raw[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) raw[i] = load_raw<DT, V>(x + rows[i] * g.d + col, col_ok && rows[i] < row_end);
+        float c[64];
+        batch_coeff_load<DT, R>(coeff, g.rank, rows, row_end, fg.c_vec != 0, c);
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            if (!(col_ok && rows[i] < row_end)) continue;
+            float xv[V], r[V];
+            unpack_raw<DT, V>(raw[i], xv);
+            batch_residual<R, V>(xv, c + i * R, qc.q, r);
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
+                if ((key >> match_shift) == prefix) atomicAdd(&s_hist[(key >> dshift) & dmask], 1u);
+            }
+        }
+    }
+    __syncthreads();
+    uint32_t *gh = hist + (chunk * 3 + lvl) * kBins;
+    for (int b = threadIdx.x; b < kDigitBins[lvl]; b += kBlock)
+        if (s_hist[b]) atomicAdd(&gh[b], s_hist[b]);
+}
+
+// Survivor counts (batched).
+template <int DT, int R, int V>
+__global__ __launch_bounds__(kBlock) void k_count_b(SaveGeom g, FastGeom fg, const typename Act<DT>::T *__restrict__ x,
+                                                    const float *__restrict__ qp,
+                                                    const typename Act<DT>::T *__restrict__ coeff,
+                                                    const SelState *__restrict__ state, WgCount *__restrict__ counts)
+{
+    constexpr int NB = Batch<R>::NB;
+    __shared__ uint32_t s_tot[kWaves];
+    int64_t chunk, row0, row_end;
+    wg_rows(g, blockIdx.x, chunk, row0, row_end);
+    const uint32_t T = state[chunk * 3 + 2].prefix;
+    const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
+    const int64_t col = (int64_t)u * V;
+    const bool col_ok = col < g.d;
+    QCols<R, V, true> qc;
+    qc.init(qp, col, g.d);
+    uint32_t gt = 0u, eq = 0u;
+    for (int64_t base = row0; base < row_end; base += (int64_t)NB * g.rpi) {
+        int64_t rows[NB];
+        batch_rows<R>(g, base, slot, rows);
+        uint4 raw[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) raw[i] = load_raw<DT, V>(x + rows[i] * g.d + col, col_ok && rows[i] < row_end);
+        float c[64];
+        batch_coeff_load<DT, R>(coeff, g.rank, rows, row_end, fg.c_vec != 0, c);
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            if (!(col_ok && rows[i] < row_end)) continue;
+            float xv[V], r[V];
+            unpack_raw<DT, V>(raw[i], xv);
+            batch_residual<R, V>(xv, c + i * R, qc.q, r);
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
+                gt += key > T;
+                eq += key == T;
+            }
+        }
+    }
+    const uint32_t tg = block_sum(gt, s_tot);
+    const uint32_t te = block_sum(eq, s_tot);
+    if (threadIdx.x == 0) counts[blockIdx.x] = WgCount{tg, te};
+}
+
+// Ordered compaction (batched).  Elements are enumerated as (iteration, slot, thread, element),
+// which is ascending flat index: one multi-value block scan per batch gives every thread the
+// number of survivors (gt in the low half, ties in the high half) before each of its vectors.
+template <int DT, int R, int V>
+__global__ __launch_bounds__(kBlock) void k_emit_b(SaveGeom g, FastGeom fg, const typename Act<DT>::T *__restrict__ x,
+                                                   const float *__restrict__ qp,
+                                                   const typename Act<DT>::T *__restrict__ coeff,
+                                                   const SelState *__restrict__ state, const WgOffset *__restrict__ offs,
+                                                   const uint32_t *__restrict__ maxkey, OutSpec o, float *scale_out,
+                                                   int to_list)
+{
+    constexpr int NB = Batch<R>::NB;
+    __shared__ uint32_t s_wt[kWaves * NB];
+    int64_t chunk, row0, row_end;
+    wg_rows(g, blockIdx.x, chunk, row0, row_end);
+    const uint32_t T = state[chunk * 3 + 2].prefix;
+    const WgOffset wo = offs[blockIdx.x];
+    const float amax = Act<DT>::rnd(__uint_as_float(*maxkey));
+    const float scale = o.bits ? quant_scale(*maxkey, o.bits, amax) : 1.f;
+    if (!to_list && blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
+    const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t col = (int64_t)u * V;
+    const bool col_ok = col < g.d;
+    QCols<R, V, true> qc;
+    qc.init(qp, col, g.d);
+    uint32_t carry = 0u;  // survivors (gt | eq << 16) of the workgroup's earlier batches
+    for (int64_t base = row0; base < row_end; base += (int64_t)NB * g.rpi) {
+        int64_t rows[NB];
+        batch_rows<R>(g, base, slot, rows);
+        uint4 raw[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) raw[i] = load_raw<DT, V>(x + rows[i] * g.d + col, col_ok && rows[i] < row_end);
+        float c[64];
+        batch_coeff_load<DT, R>(coeff, g.rank, rows, row_end, fg.c_vec != 0, c);
+        float r[NB][V];
+        uint32_t cnt[NB], incl[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            cnt[i] = 0u;
+            const bool live = col_ok && rows[i] < row_end;
+            float xv[V];
+            unpack_raw<DT, V>(raw[i], xv);
+            batch_residual<R, V>(xv, c + i * R, qc.q, r[i]);
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const uint32_t key = __float_as_uint(r[i][e]) & 0x7fffffffu;
+                cnt[i] += live ? ((key > T) ? 1u : (key == T ? 0x10000u : 0u)) : 0u;
+            }
+            incl[i] = cnt[i];
+        }
+        // inclusive scans over the wave's lanes, one per iteration
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const uint32_t y = __shfl_up(incl[i], off, 64);
+                if (lane >= off) incl[i] += y;
+            }
+        }
+        if (lane == 63)
+#pragma unroll
+            for (int i = 0; i < NB; ++i) s_wt[wave * NB + i] = incl[i];
+        __syncthreads();
+        uint32_t before_iter = carry;  // survivors of the batch's earlier iterations (all waves)
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            uint32_t waves_before = 0u, iter_total = 0u;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const uint32_t t = s_wt[w * NB + i];
+                waves_before += w < wave ? t : 0u;
+                iter_total += t;
+            }
+            const uint32_t ex = before_iter + waves_before + incl[i] - cnt[i];
+            if (cnt[i]) {
+                uint32_t gb = ex & 0xffffu, eb = ex >> 16;
+#pragma unroll
+                for (int e = 0; e < V; ++e) {
+                    const uint32_t key = __float_as_uint(r[i][e]) & 0x7fffffffu;
+                    const bool is_gt = key > T, is_eq = key == T;
+                    if (is_gt || (is_eq && eb < wo.take)) {
+                        const uint32_t pos = wo.off + gb + min(eb, wo.take);
+                        const uint32_t flat = (uint32_t)(rows[i] * g.d + col + e);
+                        if (pos >= o.cap) {
+                            // unreachable when the counts are consistent; never write out of bounds
+                        } else if (to_list) {
+                            o.list_rbits[pos] = __float_as_uint(r[i][e]);
+                            o.list_idx[pos] = flat;
+                        } else {
+                            write_entry<DT>(o, pos, flat, r[i][e], scale);
+                        }
+                    }
+                    gb += is_gt;
+                    eb += is_eq;
+                }
+            }
+            before_iter += iter_total;
+        }
+        carry = before_iter;
+        __syncthreads();  // s_wt is rewritten by the next batch
+    }
+}
+
 // ------------------------------------------------------------------ trim pass over the list
 __global__ __launch_bounds__(kBlock) void k_list_hist(int lvl, const uint32_t *__restrict__ rbits, int64_t n,
                                                       uint32_t *__restrict__ hist, const SelState *__restrict__ state)
@@ -696,18 +1118,35 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
         stacr_launch("k_zero_u32", s, [&] { k_zero_u32<<<grid_for((int64_t)p.g.n_chunks * 3 * kBins + 64), kBlock, 0, s>>>(
             hist, (int64_t)((off[WS_MAXKEY] + sizeof(uint32_t) - off[WS_HIST]) / sizeof(uint32_t))); });
     }
-    if (!coeff_in || resid)
-        stacr_launch("k_proj_hist", s, [&] { k_proj_hist<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in); });
+    // batched fast path: one aligned vector per thread per row, basis columns in registers
+    constexpr bool kFastOk = QREG && V == Act<DT>::kVec && V * R <= 64;
+    const bool fast = kFastOk && p.g.mv == 1 && p.g.L >= 64;
+    FastGeom fg{p.g.L / 64, a.rank == R && ((uintptr_t)coeff % 16) == 0};
+    if (!coeff_in || resid) {
+        if constexpr (kFastOk) {
+            if (fast) {
+                stacr_launch("k_proj_hist", s, [&] { k_proj_hist_b<DT, R, V><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in); });
+            }
+        }
+        if (!fast)
+            stacr_launch("k_proj_hist", s, [&] { k_proj_hist<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in); });
+    }
     if (!resid) return stacr_hip_check(hipGetLastError(), "save kernels");
 
     const int nch = (int)p.g.n_chunks;
     const uint32_t kf = (uint32_t)a.k_full, kl = (uint32_t)a.k_last;
     stacr_launch("k_select_step", s, [&] { k_select_step<<<nch, kBlock, 0, s>>>(0, hist, state, p.g.n_chunks, kf, kl); });
     for (int lvl = 1; lvl < 3; ++lvl) {
-        stacr_launch("k_refine_hist", s, [&] { k_refine_hist<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, lvl, x, qp, coeff, hist, state); });
+        if constexpr (kFastOk) {
+            if (fast) stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, x, qp, coeff, hist, state); });
+        }
+        if (!fast) stacr_launch("k_refine_hist", s, [&] { k_refine_hist<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, lvl, x, qp, coeff, hist, state); });
         stacr_launch("k_select_step", s, [&] { k_select_step<<<nch, kBlock, 0, s>>>(lvl, hist, state, p.g.n_chunks, kf, kl); });
     }
-    stacr_launch("k_count", s, [&] { k_count<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, counts); });
+    if constexpr (kFastOk) {
+        if (fast) stacr_launch("k_count", s, [&] { k_count_b<DT, R, V><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, counts); });
+    }
+    if (!fast) stacr_launch("k_count", s, [&] { k_count<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, counts); });
     stacr_launch("k_offsets", s, [&] { k_offsets<<<nch, kBlock, 0, s>>>(counts, offs, state, p.g.wgs_per_chunk, kf); });
 
     OutSpec o{};
@@ -720,7 +1159,10 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     o.list_rbits = lrb;
     o.list_idx = lix;
     o.cap = (uint32_t)(p.trim ? a.k_sum : a.k_total);
-    stacr_launch("k_emit", s, [&] { k_emit<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, offs, maxkey, o, a.scale, p.trim ? 1 : 0); });
+    if constexpr (kFastOk) {
+        if (fast) stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, offs, maxkey, o, a.scale, p.trim ? 1 : 0); });
+    }
+    if (!fast) stacr_launch("k_emit", s, [&] { k_emit<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, offs, maxkey, o, a.scale, p.trim ? 1 : 0); });
 
     if (p.trim) {
         uint32_t *thist = carve<uint32_t>(ws, off[WS_THIST]);
