@@ -52,6 +52,18 @@ def algorithmic_bytes(k: int) -> dict:
     return {"save": save, "bwd": bwd, "total": save + bwd, "per_kernel": per_kernel}
 
 
+def recorded_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` as the committed counter summary records them (rocprofv3
+    FETCH_SIZE + WRITE_SIZE, calibrated against a plain copy), or None when none is recorded."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_cfg3_c_fc_hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith(f"traffic_bytes {kernel}:"):
+            return int(line.split(":")[1])
+    return None
+
+
 def cpu_baseline(x, q, g, budget_s: float = 12.0, max_steps: int = 6) -> dict:
     """The oracle (a CPU restatement of the reference path) on the same workload, one thread."""
     import numpy as np
@@ -210,7 +222,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS if achieved else None,
-            "traffic": None,
+            "traffic": recorded_traffic(dominant),
             "algorithmic_bytes_per_launch": dom_bytes,
             "avg_launch_us": kern[dominant]["avg_us"],
         },
