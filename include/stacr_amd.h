@@ -15,6 +15,9 @@
  *                            stacr/quant.py:49-65)
  *   stacr_weight_grad        STACRFunction.backward grad_weight / grad_bias,
  *                            stacr/layers.py:172-198
+ *   stacr_adaptive_*         adaptive engine save and quantizers, stacr/adaptive.py:44-159,
+ *                            1333-1572,1943-2108
+ *   stacr_csr_* / stacr_delta_*   index codecs, stacr/index_compression.py:193-345
  */
 #ifndef STACR_AMD_H
 #define STACR_AMD_H
@@ -125,6 +128,82 @@ int stacr_weight_grad(const void *g, int dtype, int64_t rows, int64_t d_out, con
                       const void *data, const float *scale, int bits, int val_dtype, int64_t nnz,
                       int transposed, void *dw, int dw_dtype, void *dbias, int dbias_dtype,
                       void *workspace, size_t workspace_bytes, void *stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Adaptive engine (stacr/adaptive.py, stacr/index_compression.py)
+ * ---------------------------------------------------------------------------------------- */
+
+/* Scale record written by stacr_adaptive_quantize (16 bytes, device memory): a double holding
+ * the scale's value and an int32 naming the dtype the reference keeps it in: the input dtype,
+ * STACR_DTYPE_F32 when a 16-bit scale underflowed to 0 and the reference redid the
+ * quantization in fp32, or STACR_SCALE_F64 when an fp32 scale underflowed. */
+#define STACR_SCALE_F64 3
+
+/*
+ * Residual entry counts of the adaptive engine's "topk" mode (stacr/adaptive.py:1357-1365,
+ * 1492,1524-1530): k = floor(rows*feats*budget) (0: no residual), chunk = min(chunk_rows, rows),
+ * per-chunk k = max(1, ceil(k*chunk/rows)) capped at the chunk's element count; the union is cut
+ * to k when larger.  *k_saved is the number of entries stacr_adaptive_save writes; *index_bytes
+ * is 2 below 32768 elements, 4 up to 2^31, else 8 (_choose_index_dtype, :138-159).
+ */
+int stacr_adaptive_residual_plan(int64_t rows, int64_t feats, double budget, int64_t chunk_rows,
+                                 int64_t *k, int64_t *k_saved, int *index_bytes);
+
+int stacr_adaptive_save_workspace_bytes(int64_t rows, int64_t feats, int rank, int dtype, double budget,
+                                        int64_t chunk_rows, size_t *bytes);
+
+/*
+ * Adaptive-engine STAC-R save (stacr/adaptive.py:1333-1572, residual_mode "topk", standard
+ * chunked top-k): coeff = X.Q rounded once to dtype (or taken from coeff_in when non-NULL);
+ * residual in the activation dtype, r = rnd(x - rnd(c.q)); per-chunk top-k then the top-k of
+ * the union; ties to the lowest flat index; ascending flat order.  idx (k_saved) in index_bytes
+ * (2, 4 or 8); values (k_saved, dtype).  energy (fp32[3 + rank], device): [0] residual energy
+ * sqrt(max(|X|^2-|C|^2,0))/(sqrt(|X|^2)+1e-8) in the dtype's arithmetic (:1388-1393), [1] |X|^2,
+ * [2] |C|^2, [3 + j] mean over rows of c_j^2 in fp32 (:1953-1958); energy may be NULL.
+ */
+int stacr_adaptive_save(const void *x, const void *q, int dtype, int64_t rows, int64_t feats, int rank,
+                        double budget, int64_t chunk_rows, const void *coeff_in, void *coeff, void *idx,
+                        int index_bytes, void *values, float *energy, void *workspace, size_t workspace_bytes,
+                        void *stream);
+
+/*
+ * quantize_int8 / quantize_int4 (stacr/adaptive.py:44-120): scale = max|v| / qmax computed and
+ * rounded in the input dtype; q = round(v / scale) with the quotient rounded to the input dtype,
+ * clamped to [-qmax, qmax] (qmax 127 or 7); int4 stores q + 8 as nibbles, even entry low, odd
+ * length padded with 8 (all zero: every byte 0x88).  All-zero input: q = 0, scale 1.  A scale
+ * that underflows to 0 is recomputed in fp32 (16-bit inputs) or fp64 (fp32 inputs), as the
+ * reference's recursion does.  data: int8[n] or uint8[ceil(n/2)]; scale: 16-byte record (see
+ * STACR_SCALE_F64).  Needs 4 workspace bytes.
+ */
+int stacr_adaptive_quantize(const void *values, int dtype, int64_t n, int bits, void *data, void *scale,
+                            void *workspace, size_t workspace_bytes, void *stream);
+
+/* dequantize_int8 / dequantize_int4 (stacr/adaptive.py:79-90,123-131): q.to(scale dtype) * scale,
+ * then converted to out_dtype.  n is the element count (orig_len for int4). */
+int stacr_adaptive_dequantize(const void *data, int bits, const void *scale, int64_t n, void *out, int out_dtype,
+                              void *stream);
+
+/*
+ * CSR index compression of row-sorted flat indices (stacr/index_compression.py:193-229):
+ * row_ptrs[t] = entries in rows < t (t = 0..rows; int32 when nnz < 2^31 else int64 -> ptr_bytes),
+ * cols = idx mod n_cols (int16 when n_cols < 32768, int32 up to 2^31, else int64 -> col_bytes).
+ * The MI355X save already emits ascending indices, which are row-sorted.
+ */
+int stacr_csr_encode(const void *idx, int idx_bytes, int64_t nnz, int64_t rows, int64_t n_cols, void *row_ptrs,
+                     int ptr_bytes, void *cols, int col_bytes, void *stream);
+/* CSR back to flat indices row * n_cols + col (decompress_indices, :296-325). */
+int stacr_csr_decode(const void *row_ptrs, int ptr_bytes, const void *cols, int col_bytes, int64_t rows,
+                     int64_t n_cols, int64_t nnz, void *idx, int idx_bytes, void *stream);
+
+/* Largest gap between consecutive sorted indices (int64, device), used to choose the delta width. */
+int stacr_delta_max(const void *idx, int idx_bytes, int64_t nnz, void *max_delta, void *stream);
+/* Delta encoding of sorted indices (:231-269): base = idx[0]; deltas[e-1] = idx[e] - idx[e-1]. */
+int stacr_delta_encode(const void *idx, int idx_bytes, int64_t nnz, void *base, int base_bytes, void *deltas,
+                       int delta_bytes, void *stream);
+int stacr_delta_decode_workspace_bytes(int64_t nnz, size_t *bytes);
+/* base + prefix sums of the deltas (decompress_indices, :327-342). */
+int stacr_delta_decode(const void *base, int base_bytes, const void *deltas, int delta_bytes, int64_t nnz,
+                       void *idx, int idx_bytes, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
  * Kernel timing (benchmarking aid; no counterpart in the reference).  Between begin and end,

@@ -47,6 +47,9 @@ def lib():
         L.orc_quantize.argtypes = [P, i64, i32, P, P]
         L.orc_pack_int4.argtypes = [P, i64, P]
         L.orc_weight_grad.argtypes = [P, i64, i64, P, P, i64, i32, P, P, i64, P, P]
+        L.orc_round_dtype.argtypes, L.orc_round_dtype.restype = [ctypes.c_float, i32], ctypes.c_float
+        L.orc_residual_act.argtypes = [P, P, P, i64, i64, i32, i32, P]
+        L.orc_select_explicit.argtypes, L.orc_select_explicit.restype = [P, i64, i64, i64, i64, i64, P, P], i64
         _lib = L
     return _lib
 
@@ -200,3 +203,158 @@ def save(x: np.ndarray, q: np.ndarray, dtype: str, mode: str, budget: float, chu
         return coeff, idx, val, np.float32(1.0)
     qv, scale = quantize(val, bits)
     return coeff, idx, (pack_int4(qv) if bits == 4 else qv), scale
+
+
+# ================================================================ adaptive engine
+# (stacr/adaptive.py, stacr/index_compression.py).  Test infrastructure, like the rest of this file.
+DTYPE_CODE = {"f32": 0, "float32": 0, "bf16": 1, "bfloat16": 1, "f16": 2, "float16": 2}
+
+
+def round_dtype_scalar(v: float, dtype: str) -> float:
+    return float(lib().orc_round_dtype(float(v), DTYPE_CODE[dtype]))
+
+
+def residual_act(x: np.ndarray, c: np.ndarray, q: np.ndarray, dtype: str) -> np.ndarray:
+    """perp = rnd(x - rnd(C B^T)) in the activation dtype (stacr/adaptive.py:1518-1519)."""
+    x, c, q = _c(x, np.float32), _c(c, np.float32), _c(q, np.float32)
+    rows, d = x.shape
+    out = np.empty_like(x)
+    lib().orc_residual_act(_ptr(x), _ptr(c), _ptr(q), rows, d, q.shape[1], DTYPE_CODE[dtype], _ptr(out))
+    return out
+
+
+def adaptive_plan(rows: int, feats: int, budget: float, chunk_rows: int = 512):
+    """(k, per-chunk k, chunk rows, index dtype) of the adaptive "topk" mode (stacr/adaptive.py:1357-1365,1524)."""
+    total = rows * feats
+    k = int(total * budget)
+    idx_dtype = np.int16 if total < 32768 else (np.int32 if total <= 2**31 else np.int64)
+    if k <= 0:
+        return 0, 0, min(chunk_rows, rows), idx_dtype
+    k = min(k, total)
+    chunk = min(chunk_rows, rows)
+    per_chunk_k = max(1, (k * chunk + rows - 1) // rows)
+    return k, per_chunk_k, chunk, idx_dtype
+
+
+def select_explicit(resid: np.ndarray, chunk_rows: int, k_chunk: int, k_total: int):
+    resid = _c(resid, np.float32)
+    rows, d = resid.shape
+    n_chunks = (rows + chunk_rows - 1) // chunk_rows
+    cap = max(1, n_chunks * k_chunk)
+    idx = np.empty(cap, np.int64)
+    val = np.empty(cap, np.float32)
+    n = lib().orc_select_explicit(_ptr(resid), rows, d, int(chunk_rows), int(k_chunk), int(k_total), _ptr(idx),
+                                  _ptr(val))
+    return idx[:n].copy(), val[:n].copy()
+
+
+def adaptive_save(x: np.ndarray, q: np.ndarray, dtype: str, budget: float, chunk_rows: int = 512,
+                  coeff: np.ndarray | None = None):
+    """coeff, idx (ascending, the reference's index dtype), values (fp32 copies of dtype values)."""
+    xr, qr = round_to(x, dtype), round_to(q, dtype)
+    if coeff is None:
+        coeff = round_to(project_f64(xr, qr).astype(np.float32), dtype)
+    rows, d = xr.shape
+    k, pck, chunk, idx_dtype = adaptive_plan(rows, d, budget, chunk_rows)
+    if k == 0:
+        return coeff, None, None
+    resid = residual_act(xr, coeff, qr, dtype)
+    idx, val = select_explicit(resid, chunk, pck, k)
+    return coeff, idx.astype(idx_dtype), val
+
+
+def _np_dtype_round(a: np.ndarray, dtype: str) -> np.ndarray:
+    return round_to(np.asarray(a, np.float32), dtype)
+
+
+def adaptive_quantize(values: np.ndarray, dtype: str, bits: int):
+    """quantize_int8 / quantize_int4 (stacr/adaptive.py:44-120) on dtype values held as fp32.
+
+    Returns (q int8 in [-qmax, qmax], scale value (float), scale dtype name)."""
+    v = np.asarray(values, np.float32).reshape(-1)
+    qmax = 7.0 if bits == 4 else 127.0
+    if v.size == 0:
+        return np.zeros(0, np.int8), 1.0, dtype
+    amax = np.float32(np.max(np.abs(v)))
+    scale = _np_dtype_round(np.float32(amax) / np.float32(qmax), dtype).reshape(-1)[0]
+    if scale == 0:
+        if amax == 0:
+            return np.zeros(v.size, np.int8), 1.0, dtype
+        if dtype in ("bf16", "f16", "bfloat16", "float16"):
+            s32 = np.float32(amax) / np.float32(qmax)
+            q = np.clip(np.rint(v / s32), -qmax, qmax).astype(np.int8)
+            return q, float(s32), "f32"
+        s64 = np.float64(amax) / np.float64(qmax)
+        q = np.clip(np.rint(v.astype(np.float64) / s64), -qmax, qmax).astype(np.int8)
+        return q, float(s64), "f64"
+    with np.errstate(invalid="ignore", over="ignore"):
+        quot = _np_dtype_round(v / np.float32(scale), dtype)
+        q = np.clip(np.rint(quot), -qmax, qmax).astype(np.int8)
+    return q, float(scale), dtype
+
+
+def adaptive_pack_int4(q: np.ndarray) -> np.ndarray:
+    """(q + 8) nibbles, even entry low, odd length padded with 8 (stacr/adaptive.py:110-119)."""
+    u = (np.asarray(q, np.int16) + 8).astype(np.uint8)
+    if u.size % 2:
+        u = np.concatenate([u, np.array([8], np.uint8)])
+    return (u[0::2] | (u[1::2] << 4)).astype(np.uint8)
+
+
+def adaptive_dequantize(q: np.ndarray, scale: float, scale_dtype: str) -> np.ndarray:
+    """q.to(scale dtype) * scale, as fp32 (fp64 for an fp64 scale)."""
+    qf = np.asarray(q, np.float32)
+    if scale_dtype == "f64":
+        return qf.astype(np.float64) * np.float64(scale)
+    return _np_dtype_round(qf * np.float32(scale), scale_dtype)
+
+
+def csr_encode(sorted_idx: np.ndarray, b_flat: int, n: int):
+    """row_ptrs (int32) and column indices (int16 when n < 32768) of row-sorted flat indices."""
+    flat = np.asarray(sorted_idx, np.int64)
+    rows = flat // n
+    counts = np.bincount(rows, minlength=b_flat)[:b_flat]
+    ptr = np.zeros(b_flat + 1, np.int64)
+    ptr[1:] = np.cumsum(counts)
+    col_dtype = np.int16 if n < 32768 else (np.int32 if n <= 2**31 else np.int64)
+    return ptr.astype(np.int32 if flat.size < 2**31 else np.int64), (flat % n).astype(col_dtype)
+
+
+def csr_decode(ptr: np.ndarray, cols: np.ndarray, n: int) -> np.ndarray:
+    counts = np.diff(np.asarray(ptr, np.int64))
+    rows = np.repeat(np.arange(counts.size, dtype=np.int64), counts)
+    return rows * n + np.asarray(cols, np.int64)
+
+
+def delta_encode(sorted_idx: np.ndarray, b_flat: int, n: int):
+    flat = np.asarray(sorted_idx, np.int64)
+    base = flat[:1].astype(np.int32 if b_flat * n <= 2**31 else np.int64)
+    if flat.size > 1:
+        d = np.diff(flat)
+        m = int(d.max())
+        dd = np.int16 if m <= 32767 else (np.int32 if m < 2**31 else np.int64)
+        return base, d.astype(dd)
+    return base, np.zeros(0, np.int16)
+
+
+def delta_decode(base: np.ndarray, deltas: np.ndarray, nnz: int) -> np.ndarray:
+    out = np.zeros(nnz, np.int64)
+    out[0] = int(np.asarray(base).reshape(-1)[0])
+    out[1:] = np.asarray(deltas, np.int64)
+    return np.cumsum(out)
+
+
+def adaptive_energy(x: np.ndarray, c: np.ndarray, dtype: str):
+    """(residual energy, |X|^2, |C|^2, mean c_j^2) as stacr/adaptive.py:1388-1393,1953-1958 compute them,
+    with the sums in fp64 before the dtype rounding."""
+    xr, cr = np.asarray(x, np.float32), np.asarray(c, np.float32)
+    x2 = round_dtype_scalar(float(_np_dtype_round(xr * xr, dtype).astype(np.float64).sum()), dtype)
+    c2 = round_dtype_scalar(float(_np_dtype_round(cr * cr, dtype).astype(np.float64).sum()), dtype)
+    d0 = round_dtype_scalar(x2 - c2, dtype)
+    diff = d0 if np.isnan(d0) else max(d0, 0.0)  # torch.clamp keeps NaN
+    num = round_dtype_scalar(np.sqrt(np.float32(diff)), dtype)
+    den = round_dtype_scalar(round_dtype_scalar(np.sqrt(np.float32(x2)), dtype) + np.float32(1e-8), dtype)
+    e = round_dtype_scalar(np.float32(num) / np.float32(den), dtype)
+    per_rank = (cr.astype(np.float64) ** 2).mean(axis=0)
+    return e, x2, c2, per_rank
+

@@ -16,6 +16,9 @@
  *   orc_quantize          stacr/quant.py:49-65         symmetric per-tensor int8 / int4 / passthrough
  *   orc_pack_int4         stacr/quant.py:30-37         two's-complement nibbles, even index low
  *   orc_weight_grad       stacr/layers.py:172-193      dW = (G^T C) Q^T + G^T R_s  (fp64 accumulation)
+ *   orc_round_dtype       bf16 / fp16 round-to-nearest-even of an fp32 value (dtype-native ops)
+ *   orc_residual_act      stacr/adaptive.py:1518-1519  perp = x - (C B^T) in the activation dtype
+ *   orc_select_explicit   stacr/adaptive.py:1511-1548  per-chunk top-k_c, then top-k of the union
  *
  * Pinning (what checks each function; see tests/test_oracle.py):
  *   orc_select     reference known answers tests/test_integration.py:106-114 (global vs chunk),
@@ -30,6 +33,11 @@
  *                  the span of an orthonormal Q with exact coefficients.
  *   orc_weight_grad  closed forms: budget 1 selects every entry so dW = G^T X; rank-d identity
  *                  basis; and a single non-zero residual entry.
+ *   orc_round_dtype  numpy's float16 cast and torch's bfloat16 cast on every fp32 bit pattern class
+ *                  (normal, subnormal, ties, overflow, NaN).
+ *   orc_residual_act  fp64 projection rounded to the dtype (at most one ulp of the dtype apart), and
+ *                  exact zero for X in the span of an orthonormal basis with exact coefficients.
+ *   orc_select_explicit  brute force (numpy lexsort per chunk, then over the union) on random data.
  *
  * Tie rule.  torch.topk(sorted=False) leaves the choice among equal magnitudes unspecified.  The
  * oracle (and the HIP path) breaks ties by the lowest flat index, and returns indices in
@@ -273,3 +281,74 @@ void orc_weight_grad(const float *g, int64_t n, int64_t d_out, const float *c, c
     }
     free(m);
 }
+
+/* Round an fp32 value to bf16 (code 1) or fp16 (code 2), nearest-even, returned as fp32; code 0
+ * returns the value unchanged.  NaN stays NaN; fp16 overflow becomes +-inf. */
+float orc_round_dtype(float f, int code)
+{
+    if (code == 0 || isnan(f)) return f;
+    uint32_t u = f2u(f);
+    if (code == 1) {
+        u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+        return u2f(u);
+    }
+    const float a = fabsf(f);
+    if (isinf(a)) return f;
+    if (a < 6.103515625e-05f) {           /* below 2^-14: fp16 subnormal quantum 2^-24 */
+        const float q = nearbyintf(f * 16777216.0f) / 16777216.0f;
+        return q;
+    }
+    u = (u + 0xFFFu + ((u >> 13) & 1u)) & 0xFFFFE000u;  /* keep 10 mantissa bits */
+    const float r = u2f(u);
+    if (fabsf(r) > 65504.0f) return f < 0 ? -INFINITY : INFINITY;
+    return r;
+}
+
+/* perp = rnd(x - rnd(sum_j c_j q_j)), the projection an fp32 fma chain from 0, j ascending. */
+void orc_residual_act(const float *x, const float *c, const float *q, int64_t rows, int64_t d, int r, int code,
+                      float *out)
+{
+    for (int64_t i = 0; i < rows; ++i) {
+        const float *ci = c + i * r;
+        for (int64_t e = 0; e < d; ++e) {
+            const float *qe = q + e * r;
+            float p = 0.f;
+            for (int j = 0; j < r; ++j) p = fmaf(ci[j], qe[j], p);
+            p = orc_round_dtype(p, code);
+            out[i * d + e] = orc_round_dtype(x[i * d + e] - p, code);
+        }
+    }
+}
+
+/* Per chunk of chunk_rows rows keep the min(k_chunk, n_c) largest |r| (ties: lowest flat index),
+ * then the k_total largest of the union when it holds more.  Ascending idx order. */
+int64_t orc_select_explicit(const float *resid, int64_t rows, int64_t d, int64_t chunk_rows, int64_t k_chunk,
+                            int64_t k_total, int64_t *idx_out, float *val_out)
+{
+    if (k_total <= 0 || rows * d == 0 || k_chunk <= 0) return 0;
+    if (chunk_rows < 1) chunk_rows = 1;
+    const int64_t n_chunks = (rows + chunk_rows - 1) / chunk_rows;
+    uint64_t *sel = (uint64_t *)malloc(sizeof(uint64_t) * (size_t)(n_chunks * k_chunk));
+    uint64_t *buf = (uint64_t *)malloc(sizeof(uint64_t) * (size_t)((chunk_rows < rows ? chunk_rows : rows) * d));
+    int64_t nsel = 0;
+    for (int64_t start = 0; start < rows; start += chunk_rows) {
+        int64_t stop = start + chunk_rows < rows ? start + chunk_rows : rows;
+        int64_t n = (stop - start) * d, base = start * d;
+        int64_t k = k_chunk < n ? k_chunk : n;
+        for (int64_t e = 0; e < n; ++e) buf[e] = composite(resid[base + e], (uint64_t)(base + e));
+        select_largest(buf, n, k);
+        memcpy(sel + nsel, buf, sizeof(uint64_t) * (size_t)k);
+        nsel += k;
+    }
+    if (nsel > k_total) {
+        select_largest(sel, nsel, k_total);
+        nsel = k_total;
+    }
+    for (int64_t e = 0; e < nsel; ++e) idx_out[e] = (int64_t)(0xFFFFFFFFu - (uint32_t)(sel[e] & 0xFFFFFFFFu));
+    qsort(idx_out, (size_t)nsel, sizeof(int64_t), cmp_i64);
+    for (int64_t e = 0; e < nsel; ++e) val_out[e] = resid[idx_out[e]];
+    free(buf);
+    free(sel);
+    return nsel;
+}
+

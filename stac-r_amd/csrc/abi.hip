@@ -267,3 +267,217 @@ int stacr_weight_grad(const void *g, int dtype, int64_t rows, int64_t d_out, con
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------------ adaptive engine
+namespace {
+
+struct AdaptivePlan {
+    int64_t k = 0, k_full = 0, k_last = 0, k_sum = 0, k_saved = 0, chunk_rows = 1;
+    int index_bytes = 4;
+};
+
+// stacr/adaptive.py:1357-1365,1492,1524-1530 and _choose_index_dtype (:138-159)
+int plan_adaptive(int64_t rows, int64_t feats, double budget, int64_t chunk_rows, AdaptivePlan *p)
+{
+    if (rows < 0 || feats < 0) return stacr_fail(STACR_ERR_INVALID, "negative shape");
+    if (!(budget >= 0.0 && budget <= 1.0)) return stacr_fail(STACR_ERR_INVALID, "residual_budget must be in [0, 1]");
+    if (chunk_rows < 1) return stacr_fail(STACR_ERR_INVALID, "chunk_rows must be positive");
+    *p = AdaptivePlan{};
+    const int64_t total = rows * feats;
+    p->index_bytes = total < 32768 ? 2 : (total <= (1ll << 31) ? 4 : 8);
+    if (total == 0) return STACR_OK;
+    int64_t k = (int64_t)((double)total * budget);  // Python int() of a positive float truncates
+    if (k <= 0) return STACR_OK;
+    k = stacr::hmin(k, total);
+    const int64_t chunk = stacr::hmin(chunk_rows, rows);
+    const int64_t pck = stacr::hmax<int64_t>(1, (k * chunk + rows - 1) / rows);
+    const int64_t n_chunks = (rows + chunk - 1) / chunk;
+    const int64_t last_rows = rows - (n_chunks - 1) * chunk;
+    p->k = k;
+    p->chunk_rows = chunk;
+    p->k_full = stacr::hmin(pck, chunk * feats);
+    p->k_last = stacr::hmin(pck, last_rows * feats);
+    p->k_sum = p->k_full * (n_chunks - 1) + p->k_last;
+    p->k_saved = stacr::hmin(p->k_sum, k);
+    return STACR_OK;
+}
+
+int fill_adaptive_args(int64_t rows, int64_t feats, int rank, int dtype, double budget, int64_t chunk_rows,
+                       StacrSaveArgs *a, AdaptivePlan *p)
+{
+    if (!valid_dtype(dtype)) return stacr_fail(STACR_ERR_INVALID, "unsupported activation dtype code %d", dtype);
+    if (rank < 1 || rank > STACR_MAX_RANK)
+        return stacr_fail(STACR_ERR_UNSUPPORTED, "rank %d outside 1..%d", rank, STACR_MAX_RANK);
+    const int rc = plan_adaptive(rows, feats, budget, chunk_rows, p);
+    if (rc) return rc;
+    if ((uint64_t)rows * (uint64_t)feats >= (1ull << 32))
+        return stacr_fail(STACR_ERR_UNSUPPORTED, "rows*feats = %lld exceeds 2^32 elements", (long long)(rows * feats));
+    *a = StacrSaveArgs{};
+    a->dtype = dtype;
+    a->rows = rows;
+    a->feats = feats;
+    a->rank = rank;
+    a->mode = STACR_MODE_CHUNK_TOPK;
+    a->chunk_rows = p->chunk_rows;
+    a->k_total = p->k;
+    a->k_full = p->k_full;
+    a->k_last = p->k_last;
+    a->k_sum = p->k_sum;
+    a->act_resid = 1;
+    a->bits = 0;
+    return STACR_OK;
+}
+
+}  // namespace
+
+int stacr_adaptive_residual_plan(int64_t rows, int64_t feats, double budget, int64_t chunk_rows, int64_t *k,
+                                 int64_t *k_saved, int *index_bytes)
+{
+    AdaptivePlan p;
+    const int rc = plan_adaptive(rows, feats, budget, chunk_rows, &p);
+    if (rc) return rc;
+    if (k) *k = p.k;
+    if (k_saved) *k_saved = p.k_saved;
+    if (index_bytes) *index_bytes = p.index_bytes;
+    return STACR_OK;
+}
+
+int stacr_adaptive_save_workspace_bytes(int64_t rows, int64_t feats, int rank, int dtype, double budget,
+                                        int64_t chunk_rows, size_t *bytes)
+{
+    if (!bytes) return stacr_fail(STACR_ERR_INVALID, "bytes is NULL");
+    StacrSaveArgs a;
+    AdaptivePlan p;
+    const int rc = fill_adaptive_args(rows, feats, rank, dtype, budget, chunk_rows, &a, &p);
+    if (rc) return rc;
+    const size_t save = rows * feats ? stacr_save_ws_layout(a, nullptr) : 0;
+    *bytes = ((save + 255) & ~(size_t)255) + stacr_energy_ws();
+    return STACR_OK;
+}
+
+int stacr_adaptive_save(const void *x, const void *q, int dtype, int64_t rows, int64_t feats, int rank, double budget,
+                        int64_t chunk_rows, const void *coeff_in, void *coeff, void *idx, int index_bytes, void *values,
+                        float *energy, void *workspace, size_t workspace_bytes, void *stream)
+{
+    StacrSaveArgs a;
+    AdaptivePlan p;
+    int rc = fill_adaptive_args(rows, feats, rank, dtype, budget, chunk_rows, &a, &p);
+    if (rc) return rc;
+    if (rows * feats == 0) return STACR_OK;
+    if (!x || !q || (!coeff && !coeff_in) || !workspace)
+        return stacr_fail(STACR_ERR_INVALID, "stacr_adaptive_save: x, q, coeff (or coeff_in) and workspace must be non-NULL");
+    if (p.k > 0) {
+        if (!idx || !values) return stacr_fail(STACR_ERR_INVALID, "stacr_adaptive_save: idx and values must be non-NULL");
+        if (index_bytes != p.index_bytes)
+            return stacr_fail(STACR_ERR_INVALID, "stacr_adaptive_save: index_bytes must be %d", p.index_bytes);
+    }
+    const size_t save = stacr_save_ws_layout(a, nullptr);
+    const size_t off_energy = (save + 255) & ~(size_t)255;
+    if (workspace_bytes < off_energy + stacr_energy_ws())
+        return stacr_fail(STACR_ERR_WORKSPACE, "stacr_adaptive_save: workspace has %zu bytes, needs %zu",
+                          workspace_bytes, off_energy + stacr_energy_ws());
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    a.x = x;
+    a.q = q;
+    a.coeff_in = coeff_in;
+    a.coeff = coeff_in ? nullptr : coeff;
+    a.idx = idx;
+    a.index_bytes = index_bytes;
+    a.data = values;
+    a.scale = nullptr;
+    a.workspace = workspace;
+    a.workspace_bytes = save;
+    a.stream = s;
+    float scale_sink = 0.f;
+    (void)scale_sink;
+    rc = stacr_save_launch(a);
+    if (rc) return rc;
+    if (energy)
+        return stacr_energy_launch(x, coeff_in ? coeff_in : coeff, dtype, rows, feats, rank, energy,
+                                   static_cast<char *>(workspace) + off_energy, s);
+    return STACR_OK;
+}
+
+int stacr_adaptive_quantize(const void *values, int dtype, int64_t n, int bits, void *data, void *scale,
+                            void *workspace, size_t workspace_bytes, void *stream)
+{
+    if (!valid_dtype(dtype)) return stacr_fail(STACR_ERR_INVALID, "unsupported value dtype code %d", dtype);
+    if (bits != 4 && bits != 8) return stacr_fail(STACR_ERR_INVALID, "stacr_adaptive_quantize: bits must be 4 or 8");
+    if (n < 0) return stacr_fail(STACR_ERR_INVALID, "negative length");
+    if (!scale || !workspace || (n > 0 && (!values || !data)))
+        return stacr_fail(STACR_ERR_INVALID, "stacr_adaptive_quantize: NULL pointer argument");
+    if (workspace_bytes < 4) return stacr_fail(STACR_ERR_WORKSPACE, "stacr_adaptive_quantize needs 4 workspace bytes");
+    return stacr_aq_quantize_launch(values, dtype, n, bits, data, scale, workspace, static_cast<hipStream_t>(stream));
+}
+
+int stacr_adaptive_dequantize(const void *data, int bits, const void *scale, int64_t n, void *out, int out_dtype,
+                              void *stream)
+{
+    if (bits != 4 && bits != 8) return stacr_fail(STACR_ERR_INVALID, "stacr_adaptive_dequantize: bits must be 4 or 8");
+    if (!valid_dtype(out_dtype)) return stacr_fail(STACR_ERR_INVALID, "unsupported output dtype code %d", out_dtype);
+    if (n < 0) return stacr_fail(STACR_ERR_INVALID, "negative length");
+    if (n > 0 && (!data || !scale || !out)) return stacr_fail(STACR_ERR_INVALID, "stacr_adaptive_dequantize: NULL pointer");
+    return stacr_aq_dequantize_launch(data, bits, scale, n, out, out_dtype, static_cast<hipStream_t>(stream));
+}
+
+static bool valid_int_bytes(int b) { return b == 2 || b == 4 || b == 8; }
+
+int stacr_csr_encode(const void *idx, int idx_bytes, int64_t nnz, int64_t rows, int64_t n_cols, void *row_ptrs,
+                     int ptr_bytes, void *cols, int col_bytes, void *stream)
+{
+    if (!valid_int_bytes(idx_bytes) || !valid_int_bytes(col_bytes) || (ptr_bytes != 4 && ptr_bytes != 8))
+        return stacr_fail(STACR_ERR_INVALID, "stacr_csr_encode: bad integer width");
+    if (nnz < 0 || rows < 0 || n_cols < 1) return stacr_fail(STACR_ERR_INVALID, "stacr_csr_encode: bad size");
+    if (!row_ptrs || (nnz > 0 && (!idx || !cols))) return stacr_fail(STACR_ERR_INVALID, "stacr_csr_encode: NULL pointer");
+    return stacr_csr_encode_launch(idx, idx_bytes, nnz, rows, n_cols, row_ptrs, ptr_bytes, cols, col_bytes,
+                                   static_cast<hipStream_t>(stream));
+}
+
+int stacr_csr_decode(const void *row_ptrs, int ptr_bytes, const void *cols, int col_bytes, int64_t rows,
+                     int64_t n_cols, int64_t nnz, void *idx, int idx_bytes, void *stream)
+{
+    if (!valid_int_bytes(idx_bytes) || !valid_int_bytes(col_bytes) || (ptr_bytes != 4 && ptr_bytes != 8))
+        return stacr_fail(STACR_ERR_INVALID, "stacr_csr_decode: bad integer width");
+    if (nnz < 0 || rows < 1 || n_cols < 1) return stacr_fail(STACR_ERR_INVALID, "stacr_csr_decode: bad size");
+    if (nnz > 0 && (!row_ptrs || !cols || !idx)) return stacr_fail(STACR_ERR_INVALID, "stacr_csr_decode: NULL pointer");
+    return stacr_csr_decode_launch(row_ptrs, ptr_bytes, cols, col_bytes, rows, n_cols, nnz, idx, idx_bytes,
+                                   static_cast<hipStream_t>(stream));
+}
+
+int stacr_delta_max(const void *idx, int idx_bytes, int64_t nnz, void *max_delta, void *stream)
+{
+    if (!valid_int_bytes(idx_bytes)) return stacr_fail(STACR_ERR_INVALID, "stacr_delta_max: bad integer width");
+    if (nnz < 0 || !max_delta || (nnz > 0 && !idx)) return stacr_fail(STACR_ERR_INVALID, "stacr_delta_max: bad argument");
+    return stacr_delta_max_launch(idx, idx_bytes, nnz, max_delta, static_cast<hipStream_t>(stream));
+}
+
+int stacr_delta_encode(const void *idx, int idx_bytes, int64_t nnz, void *base, int base_bytes, void *deltas,
+                       int delta_bytes, void *stream)
+{
+    if (!valid_int_bytes(idx_bytes) || !valid_int_bytes(delta_bytes) || (base_bytes != 4 && base_bytes != 8))
+        return stacr_fail(STACR_ERR_INVALID, "stacr_delta_encode: bad integer width");
+    if (nnz < 0 || (nnz > 0 && (!idx || !base)) || (nnz > 1 && !deltas))
+        return stacr_fail(STACR_ERR_INVALID, "stacr_delta_encode: bad argument");
+    return stacr_delta_encode_launch(idx, idx_bytes, nnz, base, base_bytes, deltas, delta_bytes,
+                                     static_cast<hipStream_t>(stream));
+}
+
+int stacr_delta_decode_workspace_bytes(int64_t nnz, size_t *bytes)
+{
+    if (!bytes || nnz < 0) return stacr_fail(STACR_ERR_INVALID, "stacr_delta_decode_workspace_bytes: bad argument");
+    *bytes = stacr_delta_decode_ws(nnz);
+    return STACR_OK;
+}
+
+int stacr_delta_decode(const void *base, int base_bytes, const void *deltas, int delta_bytes, int64_t nnz, void *idx,
+                       int idx_bytes, void *workspace, size_t workspace_bytes, void *stream)
+{
+    if (!valid_int_bytes(idx_bytes) || !valid_int_bytes(delta_bytes) || (base_bytes != 4 && base_bytes != 8))
+        return stacr_fail(STACR_ERR_INVALID, "stacr_delta_decode: bad integer width");
+    if (nnz < 0 || (nnz > 0 && (!base || !idx || !workspace)) || (nnz > 1 && !deltas))
+        return stacr_fail(STACR_ERR_INVALID, "stacr_delta_decode: bad argument");
+    if (workspace_bytes < stacr_delta_decode_ws(nnz))
+        return stacr_fail(STACR_ERR_WORKSPACE, "stacr_delta_decode: workspace too small");
+    return stacr_delta_decode_launch(base, base_bytes, deltas, delta_bytes, nnz, idx, idx_bytes, workspace,
+                                     static_cast<hipStream_t>(stream));
+}

@@ -150,6 +150,7 @@ struct SaveGeom {
     int64_t wgs_per_chunk;  // uniform; trailing workgroups of the last chunk may be empty
     int L, log2L, rpi, mv;
     int rank;
+    int act_resid;          // residual in the activation dtype: r = rnd(x - rnd(c . q)) (adaptive engine)
 };
 
 // Per-chunk selection state after each radix level: prefix of the key found so far and the
@@ -200,6 +201,7 @@ struct StacrSaveArgs {
     int mode;
     int64_t chunk_rows;  // effective (global_topk: rows)
     int64_t k_total, k_full, k_last, k_sum;
+    int act_resid;         // residual arithmetic of the adaptive engine (see SaveGeom)
     int bits;
     const void *coeff_in;  // non-NULL: use these coefficients instead of projecting X
     void *coeff, *idx;
@@ -240,3 +242,22 @@ struct StacrGradArgs {
 };
 size_t stacr_grad_ws_layout(const StacrGradArgs &a, size_t *offsets);
 int stacr_grad_launch(const StacrGradArgs &a);
+
+// ------------------------------------------------------------------ launchers (adaptive.hip)
+int stacr_aq_quantize_launch(const void *v, int dtype, int64_t n, int bits, void *data, void *scale, void *ws,
+                             hipStream_t s);
+int stacr_aq_dequantize_launch(const void *data, int bits, const void *scale, int64_t n, void *out, int out_dt,
+                               hipStream_t s);
+int stacr_csr_encode_launch(const void *idx, int idx_bytes, int64_t nnz, int64_t rows, int64_t n_cols, void *ptr,
+                            int ptr_bytes, void *cols, int col_bytes, hipStream_t s);
+int stacr_csr_decode_launch(const void *ptr, int ptr_bytes, const void *cols, int col_bytes, int64_t rows,
+                            int64_t n_cols, int64_t nnz, void *idx, int idx_bytes, hipStream_t s);
+int stacr_delta_max_launch(const void *idx, int idx_bytes, int64_t nnz, void *out, hipStream_t s);
+int stacr_delta_encode_launch(const void *idx, int idx_bytes, int64_t nnz, void *base, int base_bytes, void *deltas,
+                              int delta_bytes, hipStream_t s);
+size_t stacr_delta_decode_ws(int64_t nnz);
+int stacr_delta_decode_launch(const void *base, int base_bytes, const void *deltas, int delta_bytes, int64_t nnz,
+                              void *idx, int idx_bytes, void *ws, hipStream_t s);
+size_t stacr_energy_ws();
+int stacr_energy_launch(const void *x, const void *c, int dtype, int64_t rows, int64_t feats, int rank, float *out,
+                        void *ws, hipStream_t s);

@@ -90,18 +90,29 @@ struct QCols {
     }
 };
 
-// r = x - sum_j c_j q_j as an fp32 fused multiply-add chain, j ascending (the oracle's order).
-template <int R, int V, bool QREG>
+// Residual of one vector.  Projection engine (act == 0, stacr/layers.py:32,73): r = x - sum_j c_j q_j
+// as an fp32 fused multiply-add chain from x, j ascending.  Adaptive engine (act == 1,
+// stacr/adaptive.py:1518-1519): p = sum_j c_j q_j (fma chain from 0, j ascending) rounded to the
+// activation dtype, then r = x - p rounded to the activation dtype, as its dtype-native GEMM and
+// subtraction do.  The oracle repeats both orders.
+template <int DT, int R, int V, bool QREG>
 __device__ __forceinline__ void residuals(const float (&xv)[V], const float (&c)[R],
                                           const QCols<R, V, QREG> &qc, const float *__restrict__ qp,
-                                          int64_t col, float (&r)[V])
+                                          int64_t col, float (&r)[V], int act)
 {
 #pragma unroll
     for (int e = 0; e < V; ++e) {
-        float acc = xv[e];
+        if (act) {
+            float p = 0.f;
 #pragma unroll
-        for (int j = 0; j < R; ++j) acc = fmaf(-c[j], qc.get(qp, col, e, j), acc);
-        r[e] = acc;
+            for (int j = 0; j < R; ++j) p = fmaf(c[j], qc.get(qp, col, e, j), p);
+            r[e] = Act<DT>::rnd(xv[e] - Act<DT>::rnd(p));
+        } else {
+            float acc = xv[e];
+#pragma unroll
+            for (int j = 0; j < R; ++j) acc = fmaf(-c[j], qc.get(qp, col, e, j), acc);
+            r[e] = acc;
+        }
     }
 }
 
@@ -116,7 +127,7 @@ __device__ __forceinline__ void load_coeff(const typename Act<DT>::T *__restrict
 
 struct OutSpec {
     void *idx;
-    int idx64;
+    int idx_bytes;   // 2, 4 or 8
     void *data;   // int8 (bits 8), int8 staging (bits 4), activation dtype (bits 0)
     int bits;
     uint32_t *list_rbits;  // trim path: chunk survivors as (fp32 bits, flat index)
@@ -143,8 +154,9 @@ __device__ __forceinline__ int8_t quantize_one(float v, float scale, int bits)
 template <int DT>
 __device__ __forceinline__ void write_entry(const OutSpec &o, uint32_t pos, uint32_t flat, float r, float scale)
 {
-    if (o.idx64) static_cast<int64_t *>(o.idx)[pos] = (int64_t)flat;
-    else static_cast<int32_t *>(o.idx)[pos] = (int32_t)flat;
+    if (o.idx_bytes == 8) static_cast<int64_t *>(o.idx)[pos] = (int64_t)flat;
+    else if (o.idx_bytes == 4) static_cast<int32_t *>(o.idx)[pos] = (int32_t)flat;
+    else static_cast<int16_t *>(o.idx)[pos] = (int16_t)flat;
     const float v = Act<DT>::rnd(r);
     if (o.bits == 0) static_cast<typename Act<DT>::T *>(o.data)[pos] = Act<DT>::st(v);
     else static_cast<int8_t *>(o.data)[pos] = quantize_one(v, scale, o.bits);
@@ -232,7 +244,7 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist(SaveGeom g, const typename
                 } else {
                     load_vec<DT, V>(xr + col, xv);
                 }
-                residuals<R, V, QREG>(xv, c, qc, qp, col, r);
+                residuals<DT, R, V, QREG>(xv, c, qc, qp, col, r, g.act_resid);
 #pragma unroll
                 for (int e = 0; e < V; ++e) {
                     const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -280,7 +292,7 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist(SaveGeom g, int lvl, con
             if (active && col < g.d) {
                 float xv[V], r[V];
                 load_vec<DT, V>(x + row * g.d + col, xv);
-                residuals<R, V, QREG>(xv, c, qc, qp, col, r);
+                residuals<DT, R, V, QREG>(xv, c, qc, qp, col, r, g.act_resid);
 #pragma unroll
                 for (int e = 0; e < V; ++e) {
                     const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -361,7 +373,7 @@ __global__ __launch_bounds__(kBlock) void k_count(SaveGeom g, const typename Act
             if (active && col < g.d) {
                 float xv[V], r[V];
                 load_vec<DT, V>(x + row * g.d + col, xv);
-                residuals<R, V, QREG>(xv, c, qc, qp, col, r);
+                residuals<DT, R, V, QREG>(xv, c, qc, qp, col, r, g.act_resid);
 #pragma unroll
                 for (int e = 0; e < V; ++e) {
                     const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -433,7 +445,7 @@ __global__ __launch_bounds__(kBlock) void k_emit(SaveGeom g, const typename Act<
             if (live) {
                 float xv[V];
                 load_vec<DT, V>(x + row * g.d + col, xv);
-                residuals<R, V, QREG>(xv, c, qc, qp, col, r);
+                residuals<DT, R, V, QREG>(xv, c, qc, qp, col, r, g.act_resid);
 #pragma unroll
                 for (int e = 0; e < V; ++e) {
                     const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -585,17 +597,24 @@ __device__ __forceinline__ void batch_coeff_load(const typename Act<DT>::T *__re
     }
 }
 
-// Residual keys of one vector: r = x - sum_j c_j q_j (fp32 fma chain, j ascending), |r| bits.
-template <int R, int V>
+// Residual of one vector in either engine's arithmetic (see residuals above).
+template <int DT, int R, int V>
 __device__ __forceinline__ void batch_residual(const float (&xv)[V], const float *c, const float (&q)[V][R],
-                                               float (&r)[V])
+                                               float (&r)[V], int act)
 {
 #pragma unroll
     for (int e = 0; e < V; ++e) {
-        float acc = xv[e];
+        if (act) {
+            float p = 0.f;
 #pragma unroll
-        for (int j = 0; j < R; ++j) acc = fmaf(-c[j], q[e][j], acc);
-        r[e] = acc;
+            for (int j = 0; j < R; ++j) p = fmaf(c[j], q[e][j], p);
+            r[e] = Act<DT>::rnd(xv[e] - Act<DT>::rnd(p));
+        } else {
+            float acc = xv[e];
+#pragma unroll
+            for (int j = 0; j < R; ++j) acc = fmaf(-c[j], q[e][j], acc);
+            r[e] = acc;
+        }
     }
 }
 
@@ -664,7 +683,7 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg,
             if (!(col_ok && rows[i] < row_end)) continue;
             float xv[V], r[V];
             unpack_raw<DT, V>(raw[i], xv);
-            batch_residual<R, V>(xv, c + i * R, qc.q, r);
+            batch_residual<DT, R, V>(xv, c + i * R, qc.q, r, g.act_resid);
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -718,7 +737,7 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
             if (!(col_ok && rows[i] < row_end)) continue;
             float xv[V], r[V];
             unpack_raw<DT, V>(raw[i], xv);
-            batch_residual<R, V>(xv, c + i * R, qc.q, r);
+            batch_residual<DT, R, V>(xv, c + i * R, qc.q, r, g.act_resid);
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -763,7 +782,7 @@ __global__ __launch_bounds__(kBlock) void k_count_b(SaveGeom g, FastGeom fg, con
             if (!(col_ok && rows[i] < row_end)) continue;
             float xv[V], r[V];
             unpack_raw<DT, V>(raw[i], xv);
-            batch_residual<R, V>(xv, c + i * R, qc.q, r);
+            batch_residual<DT, R, V>(xv, c + i * R, qc.q, r, g.act_resid);
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -820,7 +839,7 @@ __global__ __launch_bounds__(kBlock) void k_emit_b(SaveGeom g, FastGeom fg, cons
             const bool live = col_ok && rows[i] < row_end;
             float xv[V];
             unpack_raw<DT, V>(raw[i], xv);
-            batch_residual<R, V>(xv, c + i * R, qc.q, r[i]);
+            batch_residual<DT, R, V>(xv, c + i * R, qc.q, r[i], g.act_resid);
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const uint32_t key = __float_as_uint(r[i][e]) & 0x7fffffffu;
@@ -1046,6 +1065,7 @@ Plan make_plan(const StacrSaveArgs &a)
     g.rows = a.rows;
     g.d = a.feats;
     g.rank = a.rank;
+    g.act_resid = a.act_resid;
     const int64_t vecs = (a.feats + p.V - 1) / p.V;
     g.L = (int)hmin<int64_t>(kBlock, hmax<int64_t>(16, next_pow2(vecs)));
     g.log2L = ilog2(g.L);
@@ -1151,7 +1171,7 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
 
     OutSpec o{};
     o.idx = a.idx;
-    o.idx64 = a.index_bytes == 8;
+    o.idx_bytes = a.index_bytes;
     o.bits = a.bits;
     o.data = a.bits == 4 ? (void *)carve<int8_t>(ws, off[WS_Q4]) : a.data;
     uint32_t *lrb = carve<uint32_t>(ws, off[WS_LRBITS]);

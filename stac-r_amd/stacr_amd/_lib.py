@@ -22,6 +22,7 @@ STACR_ERR_HIP = 4
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 MODE_CHUNK_TOPK, MODE_GLOBAL_TOPK = 0, 1
 MAX_RANK = 32
+SCALE_F64 = 3  # scale record dtype code: fp64 (an fp32 scale that underflowed)
 
 # Every symbol declared in include/stacr_amd.h, with its ctypes signature.
 _i64, _i32, _f64, _p, _sz = ctypes.c_int64, ctypes.c_int, ctypes.c_double, ctypes.c_void_p, ctypes.c_size_t
@@ -41,6 +42,18 @@ SIGNATURES = {
     "stacr_weight_grad_workspace_bytes": ([_i64, _i64, _i64, _i32, _i64, _PSZ], _i32),
     "stacr_weight_grad": ([_p, _i32, _i64, _i64, _p, _p, _i64, _i32, _p, _i32, _p, _p, _i32, _i32, _i64, _i32, _p,
                            _i32, _p, _i32, _p, _sz, _p], _i32),
+    "stacr_adaptive_residual_plan": ([_i64, _i64, _f64, _i64, _P64, _P64, _PI32], _i32),
+    "stacr_adaptive_save_workspace_bytes": ([_i64, _i64, _i32, _i32, _f64, _i64, _PSZ], _i32),
+    "stacr_adaptive_save": ([_p, _p, _i32, _i64, _i64, _i32, _f64, _i64, _p, _p, _p, _i32, _p, _p, _p, _sz, _p],
+                            _i32),
+    "stacr_adaptive_quantize": ([_p, _i32, _i64, _i32, _p, _p, _p, _sz, _p], _i32),
+    "stacr_adaptive_dequantize": ([_p, _i32, _p, _i64, _p, _i32, _p], _i32),
+    "stacr_csr_encode": ([_p, _i32, _i64, _i64, _i64, _p, _i32, _p, _i32, _p], _i32),
+    "stacr_csr_decode": ([_p, _i32, _p, _i32, _i64, _i64, _i64, _p, _i32, _p], _i32),
+    "stacr_delta_max": ([_p, _i32, _i64, _p, _p], _i32),
+    "stacr_delta_encode": ([_p, _i32, _i64, _p, _i32, _p, _i32, _p], _i32),
+    "stacr_delta_decode_workspace_bytes": ([_i64, _PSZ], _i32),
+    "stacr_delta_decode": ([_p, _i32, _p, _i32, _i64, _p, _i32, _p, _sz, _p], _i32),
 }
 
 _lib = None
