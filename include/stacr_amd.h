@@ -205,6 +205,21 @@ int stacr_delta_decode_workspace_bytes(int64_t nnz, size_t *bytes);
 int stacr_delta_decode(const void *base, int base_bytes, const void *deltas, int delta_bytes, int64_t nnz,
                        void *idx, int idx_bytes, void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---------------------------------------------------------------- basis refresh (Oja step) */
+
+/* Workspace of stacr_oja_step for this shape (about rows*rank*4 + 4 MiB at rank 16). */
+int stacr_oja_workspace_bytes(int64_t rows, int64_t feats, int rank, size_t *bytes);
+/*
+ * One Oja subspace step on activations X (rows x feats, dtype) and basis Q (feats x rank, fp32,
+ * row-major), replacing the fp32 torch arithmetic of STACRLinear._refresh_basis
+ * (stacr/layers.py:346-348) and OjaBasis.update (stacr/oja.py:73-79):
+ *   Y = X Q;  update = X^T Y / max(1, rows) - Q (Y^T Y / max(1, rows));  out = Q + lr * update.
+ * update and out are feats x rank fp32.  The caller re-orthonormalizes `out` (reduced QR,
+ * stacr/oja.py:8-11, a library call).  Deterministic: every sum has a fixed order.
+ */
+int stacr_oja_step(const void *x, int dtype, int64_t rows, int64_t feats, const float *q, int rank, float lr,
+                   float *update, float *out, void *workspace, size_t workspace_bytes, void *stream);
+
 /*
  * Kernel timing (benchmarking aid; no counterpart in the reference).  Between begin and end,
  * every kernel this library launches is bracketed by HIP events on its stream, preceded by a

@@ -6,7 +6,8 @@ module.  It is the checker and the timed CPU baseline, never part of the product
 The integer/byte work (k rules, exact selection, quantization, nibble packing) and the fp64
 weight gradient live in ``stacr_oracle.c`` (each function there cites the reference line it
 restates).  This module adds the numpy pieces: dtype rounding, the fp64 projection
-(stacr/layers.py:135-137), dequantization (stacr/quant.py:17-21,40-46) and a composed save.
+(stacr/layers.py:135-137), dequantization (stacr/quant.py:17-21,40-46), a composed save, the
+adaptive engine's quantizers, index codecs and energies, and the fp64 Oja step.
 """
 from __future__ import annotations
 
@@ -354,7 +355,24 @@ def adaptive_energy(x: np.ndarray, c: np.ndarray, dtype: str):
     diff = d0 if np.isnan(d0) else max(d0, 0.0)  # torch.clamp keeps NaN
     num = round_dtype_scalar(np.sqrt(np.float32(diff)), dtype)
     den = round_dtype_scalar(round_dtype_scalar(np.sqrt(np.float32(x2)), dtype) + np.float32(1e-8), dtype)
-    e = round_dtype_scalar(np.float32(num) / np.float32(den), dtype)
+    with np.errstate(invalid="ignore", divide="ignore"):  # an overflowed 16-bit sum gives inf / inf
+        e = round_dtype_scalar(np.float32(num) / np.float32(den), dtype)
     per_rank = (cr.astype(np.float64) ** 2).mean(axis=0)
     return e, x2, c2, per_rank
 
+
+
+def oja_step(x: np.ndarray, q: np.ndarray, lr: float):
+    """(update, stepped) of one Oja step in fp64 (stacr/layers.py:346-348, stacr/oja.py:73-79):
+    Y = XQ, update = X^T Y / max(1, N) - Q (Y^T Y / max(1, N)), stepped = Q + lr * update."""
+    xd, qd = np.asarray(x, np.float64), np.asarray(q, np.float64)
+    n = max(1, xd.shape[0])
+    y = xd @ qd
+    update = xd.T @ y / n - qd @ (y.T @ y / n)
+    return update, qd + float(lr) * update
+
+
+def orthonormalize(m: np.ndarray) -> np.ndarray:
+    """Reduced QR's Q (stacr/oja.py:8-11); column signs follow numpy's LAPACK call."""
+    q, _ = np.linalg.qr(np.asarray(m, np.float64), mode="reduced")
+    return q

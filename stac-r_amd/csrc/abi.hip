@@ -388,8 +388,6 @@ int stacr_adaptive_save(const void *x, const void *q, int dtype, int64_t rows, i
     a.workspace = workspace;
     a.workspace_bytes = save;
     a.stream = s;
-    float scale_sink = 0.f;
-    (void)scale_sink;
     rc = stacr_save_launch(a);
     if (rc) return rc;
     if (energy)
@@ -480,4 +478,29 @@ int stacr_delta_decode(const void *base, int base_bytes, const void *deltas, int
         return stacr_fail(STACR_ERR_WORKSPACE, "stacr_delta_decode: workspace too small");
     return stacr_delta_decode_launch(base, base_bytes, deltas, delta_bytes, nnz, idx, idx_bytes, workspace,
                                      static_cast<hipStream_t>(stream));
+}
+
+int stacr_oja_workspace_bytes(int64_t rows, int64_t feats, int rank, size_t *bytes)
+{
+    if (!bytes || rows < 0 || feats < 0) return stacr_fail(STACR_ERR_INVALID, "stacr_oja_workspace_bytes: bad argument");
+    if (rank < 1 || rank > STACR_MAX_RANK)
+        return stacr_fail(STACR_ERR_UNSUPPORTED, "rank %d outside 1..%d", rank, STACR_MAX_RANK);
+    *bytes = stacr_oja_ws_bytes(rows, feats, rank);
+    return STACR_OK;
+}
+
+int stacr_oja_step(const void *x, int dtype, int64_t rows, int64_t feats, const float *q, int rank, float lr,
+                   float *update, float *out, void *workspace, size_t workspace_bytes, void *stream)
+{
+    if (!valid_dtype(dtype)) return stacr_fail(STACR_ERR_INVALID, "unsupported activation dtype code %d", dtype);
+    if (rows < 0 || feats < 1) return stacr_fail(STACR_ERR_INVALID, "stacr_oja_step: bad shape");
+    if (rank < 1 || rank > STACR_MAX_RANK)
+        return stacr_fail(STACR_ERR_UNSUPPORTED, "rank %d outside 1..%d", rank, STACR_MAX_RANK);
+    if (!q || !update || !out || !workspace || (rows > 0 && !x))
+        return stacr_fail(STACR_ERR_INVALID, "stacr_oja_step: NULL pointer argument");
+    if (!isfinite(lr)) return stacr_fail(STACR_ERR_INVALID, "stacr_oja_step: lr must be finite");
+    const size_t need = stacr_oja_ws_bytes(rows, feats, rank);
+    if (workspace_bytes < need)
+        return stacr_fail(STACR_ERR_WORKSPACE, "stacr_oja_step: workspace has %zu bytes, needs %zu", workspace_bytes, need);
+    return stacr_oja_launch(x, dtype, rows, feats, q, rank, lr, update, out, workspace, static_cast<hipStream_t>(stream));
 }

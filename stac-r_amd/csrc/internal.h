@@ -258,6 +258,9 @@ int stacr_delta_encode_launch(const void *idx, int idx_bytes, int64_t nnz, void 
 size_t stacr_delta_decode_ws(int64_t nnz);
 int stacr_delta_decode_launch(const void *base, int base_bytes, const void *deltas, int delta_bytes, int64_t nnz,
                               void *idx, int idx_bytes, void *ws, hipStream_t s);
+size_t stacr_oja_ws_bytes(int64_t rows, int64_t d, int rank);
+int stacr_oja_launch(const void *x, int dtype, int64_t rows, int64_t d, const float *q, int rank, float lr,
+                     float *update, float *out, void *ws, hipStream_t s);
 size_t stacr_energy_ws();
 int stacr_energy_launch(const void *x, const void *c, int dtype, int64_t rows, int64_t feats, int rank, float *out,
                         void *ws, hipStream_t s);

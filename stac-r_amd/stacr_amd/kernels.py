@@ -119,6 +119,32 @@ def quantize(values: torch.Tensor, bits: int):
     return data, scale
 
 
+def oja_step(x2d: torch.Tensor, q: torch.Tensor, lr: float):
+    """One Oja step in fp32 (stacr/layers.py:346-348, stacr/oja.py:73-79).
+
+    x2d: rows x feats activation in its own dtype; q: feats x rank basis (cast to fp32 here).
+    Returns (update, out) with update = X^T Y / N - Q (Y^T Y / N), Y = X Q, out = Q + lr * update,
+    both feats x rank fp32.  The caller re-orthonormalizes ``out``.
+    """
+    require_gpu(x2d, "activation")
+    x2d = x2d.contiguous()
+    q32 = q.to(device=x2d.device, dtype=torch.float32).contiguous()
+    rows, feats = x2d.shape
+    rank = q32.shape[1]
+    if q32.shape[0] != feats:
+        raise ValueError(f"basis has {q32.shape[0]} rows, activation has {feats} features")
+    L = _lib.load()
+    ws_bytes = ctypes.c_size_t()
+    _lib.check(L.stacr_oja_workspace_bytes(rows, feats, rank, ctypes.byref(ws_bytes)), "stacr_oja_workspace_bytes")
+    ws = torch.empty(max(1, ws_bytes.value), dtype=torch.uint8, device=x2d.device)
+    update = torch.empty(feats, rank, dtype=torch.float32, device=x2d.device)
+    out = torch.empty_like(update)
+    _lib.check(L.stacr_oja_step(_ptr(x2d), dtype_code(x2d.dtype), rows, feats, _ptr(q32), rank, float(lr),
+                                _ptr(update), _ptr(out), _ptr(ws), ws_bytes.value, _stream(x2d.device)),
+               "stacr_oja_step")
+    return update, out
+
+
 def weight_grad(g2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, residual, bits: int, transposed: bool,
                 out_dtype: torch.dtype, bias_dtype: torch.dtype | None = None):
     """dW (and dbias when bias_dtype is given) from the saved factors (stacr/layers.py:172-198).

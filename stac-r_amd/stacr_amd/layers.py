@@ -216,7 +216,8 @@ class STACRLinear(nn.Module):
     @torch.no_grad()
     def _refresh_basis(self, x2d: torch.Tensor) -> None:
         """SVD init on the first batch, then one Oja step per update interval
-        (stacr/layers.py:323-354).  The basis tensor is rebound, never mutated in place."""
+        (stacr/layers.py:323-354).  The basis tensor is rebound, never mutated in place.
+        The Oja step's reductions run in stacr_oja_step; SVD and QR stay library calls."""
         if not x2d.numel():
             return
         step = self.step
@@ -241,11 +242,9 @@ class STACRLinear(nn.Module):
                 return
             if self._turbo() or step % self.update_interval:
                 return
-            x, qb = x2d.detach().float(), self.basis.float()
-            n = x.shape[0]
-            y = x.mm(qb)
-            update = x.t().mm(y) / n - qb.mm(y.t().mm(y) / n)
-            self.basis = orthonormalize(qb + self.oja_lr * update).to(target)
+            # Y = XQ, X^T Y and Y^T Y in the HIP reduction (X read once more in its own dtype)
+            _, stepped = kernels.oja_step(x2d.detach(), self.basis, self.oja_lr)
+            self.basis = orthonormalize(stepped).to(target)
             self._last_update_step.fill_(step)
 
     def _native(self, x: torch.Tensor) -> torch.Tensor:
