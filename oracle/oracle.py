@@ -42,7 +42,6 @@ def lib():
         L.orc_py_round.argtypes, L.orc_py_round.restype = [f64], i64
         L.orc_chunk_k.argtypes, L.orc_chunk_k.restype = [i64, f64], i64
         L.orc_residual_plan.argtypes = [i64, i64, i32, f64, i64, P, P]
-        L.orc_residual_f32.argtypes = [P, P, P, i64, i64, i32, P]
         L.orc_select.argtypes, L.orc_select.restype = [P, i64, i64, i32, f64, i64, P, P], i64
         L.orc_sorted_keys.argtypes = [P, i64, P]
         L.orc_quantize.argtypes = [P, i64, i32, P, P]
@@ -104,15 +103,6 @@ def project_f64(x: np.ndarray, q: np.ndarray) -> np.ndarray:
 
 
 # ---------------------------------------------------------------- residual + selection
-def residual_f32(x: np.ndarray, c: np.ndarray, q: np.ndarray) -> np.ndarray:
-    x, c, q = _c(x, np.float32), _c(c, np.float32), _c(q, np.float32)
-    rows, d = x.shape
-    r = q.shape[1]
-    out = np.empty_like(x)
-    lib().orc_residual_f32(_ptr(x), _ptr(c), _ptr(q), rows, d, r, _ptr(out))
-    return out
-
-
 def select(resid: np.ndarray, mode: str, budget: float, chunk_rows: int):
     """Exact selection with the lowest-index tie rule; (idx int64 ascending, values fp32)."""
     resid = _c(resid, np.float32)
@@ -197,9 +187,8 @@ def save(x: np.ndarray, q: np.ndarray, dtype: str, mode: str, budget: float, chu
     qr = round_to(q, dtype)
     if coeff is None:
         coeff = round_to(project_f64(xr, qr).astype(np.float32), dtype)
-    resid = residual_f32(xr, coeff, qr)
+    resid = residual_act(xr, coeff, qr, dtype)
     idx, val = select(resid, mode, budget, chunk_rows)
-    val = round_to(val, dtype)
     if bits == 0:
         return coeff, idx, val, np.float32(1.0)
     qv, scale = quantize(val, bits)
@@ -216,7 +205,8 @@ def round_dtype_scalar(v: float, dtype: str) -> float:
 
 
 def residual_act(x: np.ndarray, c: np.ndarray, q: np.ndarray, dtype: str) -> np.ndarray:
-    """perp = rnd(x - rnd(C B^T)) in the activation dtype (stacr/adaptive.py:1518-1519)."""
+    """R = rnd(x - rnd(C Q^T)) in the activation dtype, both engines' arithmetic
+    (stacr/layers.py:32,73, stacr/adaptive.py:1518-1519)."""
     x, c, q = _c(x, np.float32), _c(c, np.float32), _c(q, np.float32)
     rows, d = x.shape
     out = np.empty_like(x)

@@ -11,13 +11,13 @@
  *   orc_py_round          Python round() on a float (half-to-even), used by every k rule
  *   orc_chunk_k           stacr/layers.py:25,33        k per chunk = max(1, min(n, round(b*n)))
  *   orc_residual_plan     stacr/layers.py:16-41,44-54  k_total and the chunk sum for a layer
- *   orc_residual_f32      stacr/layers.py:32,73        R = X - C Q^T (fixed fma order, see below)
  *   orc_select            stacr/layers.py:16-41,69-80,100-101   chunk_topk / global_topk
  *   orc_quantize          stacr/quant.py:49-65         symmetric per-tensor int8 / int4 / passthrough
  *   orc_pack_int4         stacr/quant.py:30-37         two's-complement nibbles, even index low
  *   orc_weight_grad       stacr/layers.py:172-193      dW = (G^T C) Q^T + G^T R_s  (fp64 accumulation)
  *   orc_round_dtype       bf16 / fp16 round-to-nearest-even of an fp32 value (dtype-native ops)
- *   orc_residual_act      stacr/adaptive.py:1518-1519  perp = x - (C B^T) in the activation dtype
+ *   orc_residual_act      stacr/layers.py:32,73 and stacr/adaptive.py:1518-1519
+ *                         R = X - C Q^T in the activation dtype (fixed fma order, see below)
  *   orc_select_explicit   stacr/adaptive.py:1511-1548  per-chunk top-k_c, then top-k of the union
  *
  * Pinning (what checks each function; see tests/test_oracle.py):
@@ -29,13 +29,12 @@
  *   orc_quantize   closed form: tiny-value case tests/test_integration.py:147-152, exact multiples
  *                  of the scale, clamping, and round-half-even ties.
  *   orc_pack_int4  nibble layout known answers; round trip through an independent unpack.
- *   orc_residual_f32  brute force in fp64 (differs by at most a few ulp) and exact zero for X in
- *                  the span of an orthonormal Q with exact coefficients.
  *   orc_weight_grad  closed forms: budget 1 selects every entry so dW = G^T X; rank-d identity
  *                  basis; and a single non-zero residual entry.
  *   orc_round_dtype  numpy's float16 cast and torch's bfloat16 cast on every fp32 bit pattern class
  *                  (normal, subnormal, ties, overflow, NaN).
- *   orc_residual_act  fp64 projection rounded to the dtype (at most one ulp of the dtype apart), and
+ *   orc_residual_act  fp64 projection rounded to the dtype (at most one ulp of the dtype apart),
+ *                  torch's own dtype-native mm and subtraction on the CPU (the reference's ops), and
  *                  exact zero for X in the span of an orthonormal basis with exact coefficients.
  *   orc_select_explicit  brute force (numpy lexsort per chunk, then over the union) on random data.
  *
@@ -44,9 +43,10 @@
  * ascending order.  Magnitude order is the integer order of the fp32 bit pattern with the sign
  * cleared, which places NaN above +inf exactly as torch.topk does.
  *
- * Residual arithmetic.  The HIP kernels form r = x - sum_j c_j q_j in fp32 as a fused
- * multiply-add chain over j = 0..r-1 starting from x.  orc_residual_f32 restates exactly that
- * order so selection can be compared bit for bit on the same residual.
+ * Residual arithmetic.  The reference forms R = X - C Q^T with torch ops in the activation dtype:
+ * the product rounded to the dtype, then the difference rounded to the dtype.  The HIP kernels
+ * and orc_residual_act both sum the product as an fp32 fused multiply-add chain over
+ * j = 0..r-1 from 0, so selection can be compared bit for bit on the same residual.
  */
 #include <math.h>
 #include <stdint.h>
@@ -92,21 +92,6 @@ void orc_residual_plan(int64_t rows, int64_t feats, int mode, double budget, int
         s += orc_chunk_k((stop - start) * feats, budget);
     }
     *k_chunk_sum = s;
-}
-
-/* r[i][e] = x[i][e] - sum_j c[i][j] * q[e][j]; fp32 fused multiply-add chain, j ascending. */
-void orc_residual_f32(const float *x, const float *c, const float *q, int64_t rows, int64_t d,
-                      int r, float *out)
-{
-    for (int64_t i = 0; i < rows; ++i) {
-        const float *ci = c + i * r;
-        for (int64_t e = 0; e < d; ++e) {
-            float acc = x[i * d + e];
-            const float *qe = q + e * r;
-            for (int j = 0; j < r; ++j) acc = fmaf(-ci[j], qe[j], acc);
-            out[i * d + e] = acc;
-        }
-    }
 }
 
 /* Composite sort key: larger magnitude first, then lower flat index first. */

@@ -323,7 +323,6 @@ int fill_adaptive_args(int64_t rows, int64_t feats, int rank, int dtype, double 
     a->k_full = p->k_full;
     a->k_last = p->k_last;
     a->k_sum = p->k_sum;
-    a->act_resid = 1;
     a->bits = 0;
     return STACR_OK;
 }

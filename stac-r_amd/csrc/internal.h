@@ -150,7 +150,6 @@ struct SaveGeom {
     int64_t wgs_per_chunk;  // uniform; trailing workgroups of the last chunk may be empty
     int L, log2L, rpi, mv;
     int rank;
-    int act_resid;          // residual in the activation dtype: r = rnd(x - rnd(c . q)) (adaptive engine)
 };
 
 // Per-chunk selection state after each radix level: prefix of the key found so far and the
@@ -201,7 +200,6 @@ struct StacrSaveArgs {
     int mode;
     int64_t chunk_rows;  // effective (global_topk: rows)
     int64_t k_total, k_full, k_last, k_sum;
-    int act_resid;         // residual arithmetic of the adaptive engine (see SaveGeom)
     int bits;
     const void *coeff_in;  // non-NULL: use these coefficients instead of projecting X
     void *coeff, *idx;

@@ -90,29 +90,21 @@ struct QCols {
     }
 };
 
-// Residual of one vector.  Projection engine (act == 0, stacr/layers.py:32,73): r = x - sum_j c_j q_j
-// as an fp32 fused multiply-add chain from x, j ascending.  Adaptive engine (act == 1,
-// stacr/adaptive.py:1518-1519): p = sum_j c_j q_j (fma chain from 0, j ascending) rounded to the
-// activation dtype, then r = x - p rounded to the activation dtype, as its dtype-native GEMM and
-// subtraction do.  The oracle repeats both orders.
+// Residual of one vector in the activation dtype, as both engines form it with dtype-native torch
+// ops (stacr/layers.py:32,73 and stacr/adaptive.py:1518-1519): p = sum_j c_j q_j as an fp32
+// fused multiply-add chain from 0 (j ascending) rounded to the dtype, then r = x - p rounded to the
+// dtype.  For fp32 the roundings are the identity.  The oracle repeats this order.
 template <int DT, int R, int V, bool QREG>
 __device__ __forceinline__ void residuals(const float (&xv)[V], const float (&c)[R],
                                           const QCols<R, V, QREG> &qc, const float *__restrict__ qp,
-                                          int64_t col, float (&r)[V], int act)
+                                          int64_t col, float (&r)[V])
 {
 #pragma unroll
     for (int e = 0; e < V; ++e) {
-        if (act) {
-            float p = 0.f;
+        float p = 0.f;
 #pragma unroll
-            for (int j = 0; j < R; ++j) p = fmaf(c[j], qc.get(qp, col, e, j), p);
-            r[e] = Act<DT>::rnd(xv[e] - Act<DT>::rnd(p));
-        } else {
-            float acc = xv[e];
-#pragma unroll
-            for (int j = 0; j < R; ++j) acc = fmaf(-c[j], qc.get(qp, col, e, j), acc);
-            r[e] = acc;
-        }
+        for (int j = 0; j < R; ++j) p = fmaf(c[j], qc.get(qp, col, e, j), p);
+        r[e] = Act<DT>::rnd(xv[e] - Act<DT>::rnd(p));
     }
 }
 
@@ -244,7 +236,7 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist(SaveGeom g, const typename
                 } else {
                     load_vec<DT, V>(xr + col, xv);
                 }
-                residuals<DT, R, V, QREG>(xv, c, qc, qp, col, r, g.act_resid);
+                residuals<DT, R, V, QREG>(xv, c, qc, qp, col, r);
 #pragma unroll
                 for (int e = 0; e < V; ++e) {
                     const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -292,7 +284,7 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist(SaveGeom g, int lvl, con
             if (active && col < g.d) {
                 float xv[V], r[V];
                 load_vec<DT, V>(x + row * g.d + col, xv);
-                residuals<DT, R, V, QREG>(xv, c, qc, qp, col, r, g.act_resid);
+                residuals<DT, R, V, QREG>(xv, c, qc, qp, col, r);
 #pragma unroll
                 for (int e = 0; e < V; ++e) {
                     const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -373,7 +365,7 @@ __global__ __launch_bounds__(kBlock) void k_count(SaveGeom g, const typename Act
             if (active && col < g.d) {
                 float xv[V], r[V];
                 load_vec<DT, V>(x + row * g.d + col, xv);
-                residuals<DT, R, V, QREG>(xv, c, qc, qp, col, r, g.act_resid);
+                residuals<DT, R, V, QREG>(xv, c, qc, qp, col, r);
 #pragma unroll
                 for (int e = 0; e < V; ++e) {
                     const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -445,7 +437,7 @@ __global__ __launch_bounds__(kBlock) void k_emit(SaveGeom g, const typename Act<
             if (live) {
                 float xv[V];
                 load_vec<DT, V>(x + row * g.d + col, xv);
-                residuals<DT, R, V, QREG>(xv, c, qc, qp, col, r, g.act_resid);
+                residuals<DT, R, V, QREG>(xv, c, qc, qp, col, r);
 #pragma unroll
                 for (int e = 0; e < V; ++e) {
                     const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -597,24 +589,17 @@ __device__ __forceinline__ void batch_coeff_load(const typename Act<DT>::T *__re
     }
 }
 
-// Residual of one vector in either engine's arithmetic (see residuals above).
+// Residual of one vector with the basis in registers (arithmetic as in residuals above).
 template <int DT, int R, int V>
 __device__ __forceinline__ void batch_residual(const float (&xv)[V], const float *c, const float (&q)[V][R],
-                                               float (&r)[V], int act)
+                                               float (&r)[V])
 {
 #pragma unroll
     for (int e = 0; e < V; ++e) {
-        if (act) {
-            float p = 0.f;
+        float p = 0.f;
 #pragma unroll
-            for (int j = 0; j < R; ++j) p = fmaf(c[j], q[e][j], p);
-            r[e] = Act<DT>::rnd(xv[e] - Act<DT>::rnd(p));
-        } else {
-            float acc = xv[e];
-#pragma unroll
-            for (int j = 0; j < R; ++j) acc = fmaf(-c[j], q[e][j], acc);
-            r[e] = acc;
-        }
+        for (int j = 0; j < R; ++j) p = fmaf(c[j], q[e][j], p);
+        r[e] = Act<DT>::rnd(xv[e] - Act<DT>::rnd(p));
     }
 }
 
@@ -683,7 +668,7 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg,
             if (!(col_ok && rows[i] < row_end)) continue;
             float xv[V], r[V];
             unpack_raw<DT, V>(raw[i], xv);
-            batch_residual<DT, R, V>(xv, c + i * R, qc.q, r, g.act_resid);
+            batch_residual<DT, R, V>(xv, c + i * R, qc.q, r);
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -737,7 +722,7 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
             if (!(col_ok && rows[i] < row_end)) continue;
             float xv[V], r[V];
             unpack_raw<DT, V>(raw[i], xv);
-            batch_residual<DT, R, V>(xv, c + i * R, qc.q, r, g.act_resid);
+            batch_residual<DT, R, V>(xv, c + i * R, qc.q, r);
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -782,7 +767,7 @@ __global__ __launch_bounds__(kBlock) void k_count_b(SaveGeom g, FastGeom fg, con
             if (!(col_ok && rows[i] < row_end)) continue;
             float xv[V], r[V];
             unpack_raw<DT, V>(raw[i], xv);
-            batch_residual<DT, R, V>(xv, c + i * R, qc.q, r, g.act_resid);
+            batch_residual<DT, R, V>(xv, c + i * R, qc.q, r);
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -839,7 +824,7 @@ __global__ __launch_bounds__(kBlock) void k_emit_b(SaveGeom g, FastGeom fg, cons
             const bool live = col_ok && rows[i] < row_end;
             float xv[V];
             unpack_raw<DT, V>(raw[i], xv);
-            batch_residual<DT, R, V>(xv, c + i * R, qc.q, r[i], g.act_resid);
+            batch_residual<DT, R, V>(xv, c + i * R, qc.q, r[i]);
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const uint32_t key = __float_as_uint(r[i][e]) & 0x7fffffffu;
@@ -1065,7 +1050,6 @@ Plan make_plan(const StacrSaveArgs &a)
     g.rows = a.rows;
     g.d = a.feats;
     g.rank = a.rank;
-    g.act_resid = a.act_resid;
     const int64_t vecs = (a.feats + p.V - 1) / p.V;
     g.L = (int)hmin<int64_t>(kBlock, hmax<int64_t>(16, next_pow2(vecs)));
     g.log2L = ilog2(g.L);

@@ -165,7 +165,7 @@ def test_residual_close_to_fp64_and_exact_in_span():
     x = rng.standard_normal((16, 40)).astype(np.float32)
     q = np.linalg.qr(rng.standard_normal((40, 8)))[0].astype(np.float32)
     c = (x.astype(np.float64) @ q).astype(np.float32)
-    r = orc.residual_f32(x, c, q)
+    r = orc.residual_act(x, c, q, "f32")
     r64 = x.astype(np.float64) - c.astype(np.float64) @ q.astype(np.float64).T
     assert np.abs(r - r64).max() <= 1e-5
     # X exactly in the span of a unit-vector basis with exact coefficients -> zero residual
@@ -173,7 +173,27 @@ def test_residual_close_to_fp64_and_exact_in_span():
     q[[3, 9, 17, 31], [0, 1, 2, 3]] = 1.0
     c = rng.integers(-5, 5, (16, 4)).astype(np.float32)
     x = c @ q.T
-    assert not orc.residual_f32(x, c, q).any()
+    assert not orc.residual_act(x, c, q, "f32").any()
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("rank", [1, 5, 8, 16])
+def test_residual_matches_torch_dtype_native_ops(dtype, rank):
+    """The reference forms the residual with torch ops in the activation dtype
+    (stacr/layers.py:32,73); torch's CPU kernels give the same bits as the restatement."""
+    import torch
+
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dtype]
+    rng = np.random.default_rng(rank)
+    q = torch.from_numpy(np.linalg.qr(rng.standard_normal((384, rank)))[0].astype(np.float32)).to(tdt)
+    x = torch.from_numpy((rng.standard_normal((256, 384)) * 2).astype(np.float32)).to(tdt)
+    c = x.mm(q)
+    ref = (x - c.mm(q.t())).float().numpy()
+    got = orc.residual_act(x.float().numpy(), c.float().numpy(), q.float().numpy(), dtype)
+    assert np.array_equal(got, ref)
+    # one rounding of the exact difference disagrees on many entries: the pin sees both roundings
+    one = orc.round_to((x.double() - c.double().mm(q.double().t())).float().numpy(), dtype)
+    assert np.mean(one != ref) > 0.02
 
 
 # ------------------------------------------------------------------ weight gradient closed forms
@@ -184,7 +204,7 @@ def test_weight_grad_full_budget_equals_dense():
     g = rng.standard_normal((n, d_out)).astype(np.float32)
     q = np.linalg.qr(rng.standard_normal((d_in, r)))[0].astype(np.float32)
     c = (x.astype(np.float64) @ q).astype(np.float32)
-    resid = orc.residual_f32(x, c, q)
+    resid = orc.residual_act(x, c, q, "f32")
     idx, val = orc.select(resid, "global_topk", 1.0, 512)
     assert idx.size == n * d_in
     dw, db = orc.weight_grad(g, c, q, idx, val, d_in)
