@@ -18,6 +18,11 @@
  *   stacr_adaptive_*         adaptive engine save and quantizers, stacr/adaptive.py:44-159,
  *                            1333-1572,1943-2108
  *   stacr_csr_* / stacr_delta_*   index codecs, stacr/index_compression.py:193-345
+ *   stacr_select_uniform / stacr_select_block_sparse / stacr_sample_magnitudes /
+ *   stacr_select_threshold   the "uniform", "block_sparse", "sampled" selectors,
+ *                            stacr/layers.py:55-99
+ *   stacr_oja_step           the Oja step of STACRLinear._refresh_basis, stacr/layers.py:346-348,
+ *                            and OjaBasis.update, stacr/oja.py:73-79
  */
 #ifndef STACR_AMD_H
 #define STACR_AMD_H
@@ -73,7 +78,9 @@ int stacr_save_workspace_bytes(int64_t rows, int64_t feats, int rank, int dtype,
 /*
  * One streaming save of the activation X (rows x feats, row-major, `dtype`):
  *   coeff (rows x rank, dtype)   = X . Q, fp32 accumulation, rounded once to dtype
- *   residual r = X - coeff . Q^T (fp32), selected by |r| per chunk_topk / global_topk with the
+ *   residual r = rnd(X - rnd(coeff . Q^T)) in dtype (the reference's torch ops: product rounded,
+ *   then difference rounded; fp32 fused multiply-adds over the rank), selected by |r| per
+ *   chunk_topk / global_topk with the
  *   reference's k rules; ties at the cut go to the lowest flat index; output is in ascending
  *   flat-index order:
  *   idx   (k_saved, int32 or int64 per index_bytes) = row * feats + col
@@ -204,6 +211,43 @@ int stacr_delta_decode_workspace_bytes(int64_t nnz, size_t *bytes);
 /* base + prefix sums of the deltas (decompress_indices, :327-342). */
 int stacr_delta_decode(const void *base, int base_bytes, const void *deltas, int delta_bytes, int64_t nnz,
                        void *idx, int idx_bytes, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------- other residual selectors
+ * The projection engine's "uniform", "block_sparse" and "sampled" residual modes
+ * (_select_residual, stacr/layers.py:44-101).  Inputs are the save's factors: x (rows x feats),
+ * coeff (rows x rank, from stacr_save with budget 0) and q (feats x rank), all in `dtype`.  The
+ * residual is r = rnd(x - rnd(coeff q^T)) in that dtype, as the reference's torch ops form it.
+ * Indices are flat row*feats + col, ascending; index_bytes is 4 when rows*feats < 2^31 - 1, else 8
+ * (stacr/layers.py:52).  Values are residual entries in `dtype`; the caller quantizes them with
+ * stacr_quantize_values as the reference does (stacr/layers.py:146). */
+
+/* uniform (:89-98): the k positions floor(i * rows * feats / k), i = 0..k-1, with
+ * k = round(budget * rows * feats) chosen by the caller. */
+int stacr_select_uniform(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t feats,
+                         int rank, int64_t k, void *idx, int index_bytes, void *values, void *stream);
+/* block_sparse counts (:81-88): per chunk of chunk_rows rows, count = max(1, round(budget * blocks));
+ * entries = sum of count * block_size.  Requires feats % block_size == 0 (otherwise the reference
+ * falls back to chunk_topk, :67-68) and 0 < budget <= 1. */
+int stacr_block_sparse_plan(int64_t rows, int64_t feats, double budget, int64_t chunk_rows, int64_t block_size,
+                            int64_t *count_full, int64_t *count_last, int64_t *entries, size_t *workspace_bytes);
+/* block_sparse selection: per chunk the `count` blocks of block_size consecutive elements with the
+ * largest energy rnd(sum rnd(r^2)) (ties: lowest block), every element of each chosen block. */
+int stacr_select_block_sparse(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t feats,
+                              int rank, double budget, int64_t chunk_rows, int64_t block_size, void *idx,
+                              int index_bytes, void *values, void *workspace, size_t workspace_bytes, void *stream);
+/* sampled (:55-66), step 1: out[i] = |r| at flat position positions[i] (int64, device), in dtype.
+ * The caller draws the positions (torch.randint with the reference's seeded generator) and takes
+ * the quantile of the magnitudes (torch.quantile), as the reference does.  A position outside
+ * [0, rows*feats) yields NaN. */
+int stacr_sample_magnitudes(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t feats,
+                            int rank, const int64_t *positions, int64_t n, void *out, void *stream);
+int stacr_threshold_workspace_bytes(int64_t rows, int64_t feats, size_t *bytes);
+/* sampled, step 2: the first `cap` flat positions (ascending) with |r| >= threshold, the fp32
+ * device scalar *threshold compared after rounding to dtype (torch's promotion for
+ * `magnitude >= threshold`).  *count (int64, device) receives min(cap, passing entries). */
+int stacr_select_threshold(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t feats,
+                           int rank, const float *threshold, int64_t cap, void *idx, int index_bytes, void *values,
+                           int64_t *count, void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---------------------------------------------------------------- basis refresh (Oja step) */
 

@@ -366,3 +366,66 @@ def orthonormalize(m: np.ndarray) -> np.ndarray:
     """Reduced QR's Q (stacr/oja.py:8-11); column signs follow numpy's LAPACK call."""
     q, _ = np.linalg.qr(np.asarray(m, np.float64), mode="reduced")
     return q
+
+
+# ================================================================ other projection-engine selectors
+# (stacr/layers.py:55-99), on the dtype-native residual of residual_act.
+def uniform_positions(total: int, k: int) -> np.ndarray:
+    """floor(i * total / k), i = 0..k-1: the union of the reference's per-chunk ranges (:89-98)."""
+    i = np.arange(k, dtype=np.uint64)
+    return (i * np.uint64(total) // np.uint64(k)).astype(np.int64)
+
+
+def select_uniform(resid: np.ndarray, k: int):
+    flat = np.asarray(resid, np.float32).reshape(-1)
+    idx = uniform_positions(flat.size, k)
+    return idx, flat[idx]
+
+
+def block_energies(resid: np.ndarray, block_size: int, dtype: str) -> np.ndarray:
+    """rnd(sum_o rnd(r_o^2)) per block of block_size consecutive elements, the sum an fp32
+    sequence of additions in element order (:84)."""
+    sq = round_to(np.asarray(resid, np.float32) ** 2, dtype).reshape(-1, block_size)
+    acc = np.zeros(sq.shape[0], np.float32)
+    for o in range(block_size):
+        acc = (acc + sq[:, o]).astype(np.float32)
+    return round_to(acc, dtype)
+
+
+def block_sparse_counts(rows: int, feats: int, budget: float, chunk_rows: int, block_size: int):
+    """count per chunk = max(1, round(budget * blocks in the chunk)) (:83)."""
+    out = []
+    for start in range(0, rows, chunk_rows):
+        blocks = min(chunk_rows, rows - start) * feats // block_size
+        out.append(max(1, int(round(budget * blocks))))
+    return out
+
+
+def select_block_sparse(resid: np.ndarray, budget: float, chunk_rows: int, block_size: int, dtype: str):
+    """Per chunk the top-count blocks by energy (ties: lowest block), all their elements, ascending."""
+    resid = np.asarray(resid, np.float32)
+    rows, feats = resid.shape
+    flat = resid.reshape(-1)
+    energy = block_energies(resid, block_size, dtype)
+    keys = energy.view(np.uint32) & np.uint32(0x7FFFFFFF)  # NaN above +inf, as torch.topk orders it
+    per_chunk_blocks = chunk_rows * feats // block_size
+    chosen = []
+    for c, count in enumerate(block_sparse_counts(rows, feats, budget, chunk_rows, block_size)):
+        lo = c * per_chunk_blocks
+        hi = min(lo + per_chunk_blocks, energy.size)
+        b = np.arange(lo, hi)
+        order = np.lexsort((b, -keys[lo:hi].astype(np.int64)))
+        chosen.append(np.sort(b[order[:count]]))
+    blocks = np.concatenate(chosen).astype(np.int64)
+    idx = (blocks[:, None] * block_size + np.arange(block_size)).reshape(-1)
+    return idx, flat[idx]
+
+
+def select_threshold(resid: np.ndarray, threshold: float, dtype: str, cap: int):
+    """First `cap` positions with |r| >= threshold rounded to dtype (torch promotes the fp32 0-dim
+    quantile to the magnitude's dtype for the comparison, :65)."""
+    flat = np.asarray(resid, np.float32).reshape(-1)
+    t = np.float32(round_dtype_scalar(float(threshold), dtype))
+    with np.errstate(invalid="ignore"):
+        idx = np.nonzero(np.abs(flat) >= t)[0][:cap].astype(np.int64)
+    return idx, flat[idx]

@@ -503,3 +503,114 @@ int stacr_oja_step(const void *x, int dtype, int64_t rows, int64_t feats, const 
         return stacr_fail(STACR_ERR_WORKSPACE, "stacr_oja_step: workspace has %zu bytes, needs %zu", workspace_bytes, need);
     return stacr_oja_launch(x, dtype, rows, feats, q, rank, lr, update, out, workspace, static_cast<hipStream_t>(stream));
 }
+
+// ------------------------------------------------------------------ uniform / block_sparse / sampled
+namespace {
+
+int check_factors(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t feats, int rank,
+                  const char *who)
+{
+    if (!valid_dtype(dtype)) return stacr_fail(STACR_ERR_INVALID, "%s: unsupported dtype code %d", who, dtype);
+    if (rows < 0 || feats < 1) return stacr_fail(STACR_ERR_INVALID, "%s: bad shape", who);
+    if (rank < 1 || rank > STACR_MAX_RANK)
+        return stacr_fail(STACR_ERR_UNSUPPORTED, "rank %d outside 1..%d", rank, STACR_MAX_RANK);
+    if (rows * feats >= (1ll << 32))
+        return stacr_fail(STACR_ERR_UNSUPPORTED, "rows*feats = %lld exceeds 2^32 elements", (long long)(rows * feats));
+    if (rows > 0 && (!x || !coeff || !q)) return stacr_fail(STACR_ERR_INVALID, "%s: NULL pointer argument", who);
+    return STACR_OK;
+}
+
+int index_bytes_for(int64_t total) { return total < (1ll << 31) - 1 ? 4 : 8; }
+
+}  // namespace
+
+int stacr_select_uniform(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t feats,
+                         int rank, int64_t k, void *idx, int index_bytes, void *values, void *stream)
+{
+    int rc = check_factors(x, coeff, q, dtype, rows, feats, rank, "stacr_select_uniform");
+    if (rc) return rc;
+    if (k < 0 || k > rows * feats) return stacr_fail(STACR_ERR_INVALID, "stacr_select_uniform: k outside [0, rows*feats]");
+    if (index_bytes != index_bytes_for(rows * feats))
+        return stacr_fail(STACR_ERR_INVALID, "stacr_select_uniform: index_bytes must be %d", index_bytes_for(rows * feats));
+    if (k > 0 && (!idx || !values)) return stacr_fail(STACR_ERR_INVALID, "stacr_select_uniform: NULL output");
+    return stacr_uniform_launch(x, coeff, q, dtype, rows, feats, rank, k, idx, index_bytes, values,
+                                static_cast<hipStream_t>(stream));
+}
+
+int stacr_block_sparse_plan(int64_t rows, int64_t feats, double budget, int64_t chunk_rows, int64_t block_size,
+                            int64_t *count_full, int64_t *count_last, int64_t *entries, size_t *workspace_bytes)
+{
+    if (rows < 1 || feats < 1 || chunk_rows < 1 || block_size < 1 || feats % block_size)
+        return stacr_fail(STACR_ERR_INVALID, "stacr_block_sparse_plan: needs rows, chunk_rows >= 1 and feats %% block_size == 0");
+    if (!(budget > 0.0 && budget <= 1.0)) return stacr_fail(STACR_ERR_INVALID, "budget %g outside (0, 1]", budget);
+    if (!count_full || !count_last || !entries || !workspace_bytes)
+        return stacr_fail(STACR_ERR_INVALID, "stacr_block_sparse_plan: NULL output");
+    const int64_t cr = chunk_rows < rows ? chunk_rows : rows;
+    const int64_t n_seg = (rows + cr - 1) / cr;
+    const int64_t last_rows = rows - (n_seg - 1) * cr;
+    auto count_of = [&](int64_t seg_rows) {  // max(1, round(budget * blocks)) (stacr/layers.py:83)
+        const int64_t blocks = seg_rows * feats / block_size;
+        const int64_t c = py_round(budget * (double)blocks);
+        return c < 1 ? (int64_t)1 : c;
+    };
+    *count_full = count_of(cr);
+    *count_last = count_of(last_rows);
+    *entries = ((n_seg - 1) * *count_full + *count_last) * block_size;
+    *workspace_bytes = stacr_block_ws(rows, feats, block_size, n_seg, *count_full > *count_last ? *count_full : *count_last);
+    return STACR_OK;
+}
+
+int stacr_select_block_sparse(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t feats,
+                              int rank, double budget, int64_t chunk_rows, int64_t block_size, void *idx,
+                              int index_bytes, void *values, void *workspace, size_t workspace_bytes, void *stream)
+{
+    int rc = check_factors(x, coeff, q, dtype, rows, feats, rank, "stacr_select_block_sparse");
+    if (rc) return rc;
+    int64_t cf, cl, n_out;
+    size_t need;
+    rc = stacr_block_sparse_plan(rows, feats, budget, chunk_rows, block_size, &cf, &cl, &n_out, &need);
+    if (rc) return rc;
+    if (index_bytes != index_bytes_for(rows * feats))
+        return stacr_fail(STACR_ERR_INVALID, "stacr_select_block_sparse: index_bytes must be %d",
+                          index_bytes_for(rows * feats));
+    if (!idx || !values || !workspace) return stacr_fail(STACR_ERR_INVALID, "stacr_select_block_sparse: NULL pointer");
+    if (workspace_bytes < need)
+        return stacr_fail(STACR_ERR_WORKSPACE, "stacr_select_block_sparse: workspace has %zu bytes, needs %zu",
+                          workspace_bytes, need);
+    const int64_t cr = chunk_rows < rows ? chunk_rows : rows;
+    return stacr_block_launch(x, coeff, q, dtype, rows, feats, rank, block_size, cr, cf, cl, idx, index_bytes, values,
+                              workspace, static_cast<hipStream_t>(stream));
+}
+
+int stacr_sample_magnitudes(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t feats,
+                            int rank, const int64_t *positions, int64_t n, void *out, void *stream)
+{
+    int rc = check_factors(x, coeff, q, dtype, rows, feats, rank, "stacr_sample_magnitudes");
+    if (rc) return rc;
+    if (n < 0 || (n > 0 && (!positions || !out))) return stacr_fail(STACR_ERR_INVALID, "stacr_sample_magnitudes: bad sample");
+    return stacr_sample_launch(x, coeff, q, dtype, rows, feats, rank, positions, n, out, static_cast<hipStream_t>(stream));
+}
+
+int stacr_threshold_workspace_bytes(int64_t rows, int64_t feats, size_t *bytes)
+{
+    if (!bytes || rows < 0 || feats < 1) return stacr_fail(STACR_ERR_INVALID, "stacr_threshold_workspace_bytes: bad argument");
+    *bytes = stacr_threshold_ws(rows, feats);
+    return STACR_OK;
+}
+
+int stacr_select_threshold(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t feats,
+                           int rank, const float *threshold, int64_t cap, void *idx, int index_bytes, void *values,
+                           int64_t *count, void *workspace, size_t workspace_bytes, void *stream)
+{
+    int rc = check_factors(x, coeff, q, dtype, rows, feats, rank, "stacr_select_threshold");
+    if (rc) return rc;
+    if (cap < 0 || cap > rows * feats) return stacr_fail(STACR_ERR_INVALID, "stacr_select_threshold: cap outside [0, rows*feats]");
+    if (index_bytes != index_bytes_for(rows * feats))
+        return stacr_fail(STACR_ERR_INVALID, "stacr_select_threshold: index_bytes must be %d", index_bytes_for(rows * feats));
+    if (!threshold || !count || !workspace || (cap > 0 && (!idx || !values)))
+        return stacr_fail(STACR_ERR_INVALID, "stacr_select_threshold: NULL pointer argument");
+    if (workspace_bytes < stacr_threshold_ws(rows, feats))
+        return stacr_fail(STACR_ERR_WORKSPACE, "stacr_select_threshold: workspace too small");
+    return stacr_threshold_launch(x, coeff, q, dtype, rows, feats, rank, threshold, cap, idx, index_bytes, values,
+                                  count, workspace, static_cast<hipStream_t>(stream));
+}

@@ -256,6 +256,20 @@ int stacr_delta_encode_launch(const void *idx, int idx_bytes, int64_t nnz, void 
 size_t stacr_delta_decode_ws(int64_t nnz);
 int stacr_delta_decode_launch(const void *base, int base_bytes, const void *deltas, int delta_bytes, int64_t nnz,
                               void *idx, int idx_bytes, void *ws, hipStream_t s);
+// ------------------------------------------------------------------ launchers (selectors.hip)
+int stacr_uniform_launch(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t d,
+                         int rank, int64_t k, void *idx, int idx_bytes, void *values, hipStream_t s);
+size_t stacr_block_ws(int64_t rows, int64_t d, int64_t bs, int64_t n_seg, int64_t count_full);
+int stacr_block_launch(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t d, int rank,
+                       int64_t bs, int64_t seg_rows, int64_t count_full, int64_t count_last, void *idx,
+                       int idx_bytes, void *values, void *ws, hipStream_t s);
+int stacr_sample_launch(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t d,
+                        int rank, const int64_t *pos, int64_t n, void *out, hipStream_t s);
+size_t stacr_threshold_ws(int64_t rows, int64_t d);
+int stacr_threshold_launch(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t d,
+                           int rank, const float *thr, int64_t cap, void *idx, int idx_bytes, void *values,
+                           int64_t *count, void *ws, hipStream_t s);
+
 size_t stacr_oja_ws_bytes(int64_t rows, int64_t d, int rank);
 int stacr_oja_launch(const void *x, int dtype, int64_t rows, int64_t d, const float *q, int rank, float lr,
                      float *update, float *out, void *ws, hipStream_t s);

@@ -104,6 +104,104 @@ def save(x2d: torch.Tensor, q: torch.Tensor, *, mode: str, budget: float, chunk_
     return coeff, idx, data, scale
 
 
+def _factor_args(x2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor):
+    require_gpu(x2d, "activation")
+    x2d, coeff, q = x2d.contiguous(), coeff.contiguous(), q.contiguous()
+    if coeff.dtype != x2d.dtype or q.dtype != x2d.dtype:
+        raise TypeError("coefficients and basis must be cast to the activation dtype")
+    rows, feats = x2d.shape
+    total = rows * feats
+    ib = 4 if total < 2**31 - 1 else 8
+    return x2d, coeff, q, rows, feats, q.shape[1], dtype_code(x2d.dtype), ib
+
+
+def _index_tensor(n: int, ib: int, device):
+    return torch.empty(n, dtype=torch.int32 if ib == 4 else torch.int64, device=device)
+
+
+def select_uniform(x2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, k: int):
+    """(idx, values) of the "uniform" selector: positions floor(i * total / k) (stacr/layers.py:89-98)."""
+    x2d, coeff, q, rows, feats, rank, dt, ib = _factor_args(x2d, coeff, q)
+    idx = _index_tensor(k, ib, x2d.device)
+    values = torch.empty(k, dtype=x2d.dtype, device=x2d.device)
+    _lib.check(_lib.load().stacr_select_uniform(_ptr(x2d), _ptr(coeff), _ptr(q), dt, rows, feats, rank, int(k),
+                                                _ptr(idx), ib, _ptr(values), _stream(x2d.device)),
+               "stacr_select_uniform")
+    return idx, values
+
+
+def select_block_sparse(x2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, budget: float, chunk_rows: int,
+                        block_size: int):
+    """(idx, values) of the "block_sparse" selector (stacr/layers.py:81-88); feats % block_size == 0."""
+    x2d, coeff, q, rows, feats, rank, dt, ib = _factor_args(x2d, coeff, q)
+    L = _lib.load()
+    cf, cl, n, ws_bytes = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64(), ctypes.c_size_t()
+    _lib.check(L.stacr_block_sparse_plan(rows, feats, float(budget), int(chunk_rows), int(block_size), ctypes.byref(cf),
+                                         ctypes.byref(cl), ctypes.byref(n), ctypes.byref(ws_bytes)),
+               "stacr_block_sparse_plan")
+    idx = _index_tensor(n.value, ib, x2d.device)
+    values = torch.empty(n.value, dtype=x2d.dtype, device=x2d.device)
+    ws = torch.empty(max(1, ws_bytes.value), dtype=torch.uint8, device=x2d.device)
+    _lib.check(L.stacr_select_block_sparse(_ptr(x2d), _ptr(coeff), _ptr(q), dt, rows, feats, rank, float(budget),
+                                           int(chunk_rows), int(block_size), _ptr(idx), ib, _ptr(values), _ptr(ws),
+                                           ws_bytes.value, _stream(x2d.device)), "stacr_select_block_sparse")
+    return idx, values
+
+
+def sample_magnitudes(x2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, positions: torch.Tensor):
+    """|r| at the given flat positions (int64), in the activation dtype."""
+    x2d, coeff, q, rows, feats, rank, dt, _ = _factor_args(x2d, coeff, q)
+    positions = positions.to(device=x2d.device, dtype=torch.int64).contiguous()
+    out = torch.empty(positions.numel(), dtype=x2d.dtype, device=x2d.device)
+    _lib.check(_lib.load().stacr_sample_magnitudes(_ptr(x2d), _ptr(coeff), _ptr(q), dt, rows, feats, rank,
+                                                   _ptr(positions), positions.numel(), _ptr(out),
+                                                   _stream(x2d.device)), "stacr_sample_magnitudes")
+    return out
+
+
+def select_sampled(x2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, budget: float, sample_ratio: float,
+                   k_total: int):
+    """(idx, values) of the "sampled" selector (stacr/layers.py:55-66).
+
+    The sample positions come from torch.randint with the reference's seeded generator on the
+    activation's device and the threshold from torch.quantile (library calls, as in the
+    reference); the magnitude gather and the ordered, capped compaction are HIP kernels.  One
+    device-to-host read of the selected count sizes the outputs (the reference's nonzero syncs
+    the same way).
+    """
+    x2d, coeff, q, rows, feats, _, _, _ = _factor_args(x2d, coeff, q)
+    device = x2d.device
+    total = rows * feats
+    generator = torch.Generator(device=device).manual_seed(0)
+    sample_n = max(1024, int(total * sample_ratio))
+    positions = torch.randint(total, (sample_n,), device=device, generator=generator)
+    sample = sample_magnitudes(x2d, coeff, q, positions)
+    threshold = torch.quantile(sample.float(), 1.0 - budget)
+    return select_threshold(x2d, coeff, q, threshold, k_total)
+
+
+def select_threshold(x2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, threshold: torch.Tensor, cap: int):
+    """The first ``cap`` flat positions with |r| >= threshold (an fp32 device scalar, compared in
+    the activation dtype), ascending, with their residual values."""
+    x2d, coeff, q, rows, feats, rank, dt, ib = _factor_args(x2d, coeff, q)
+    device = x2d.device
+    L = _lib.load()
+    threshold = threshold.to(device=device, dtype=torch.float32).reshape(()).contiguous()
+    ws_bytes = ctypes.c_size_t()
+    _lib.check(L.stacr_threshold_workspace_bytes(rows, feats, ctypes.byref(ws_bytes)), "stacr_threshold_workspace_bytes")
+    ws = torch.empty(max(1, ws_bytes.value), dtype=torch.uint8, device=device)
+    idx = _index_tensor(cap, ib, device)
+    values = torch.empty(cap, dtype=x2d.dtype, device=device)
+    count = torch.zeros((), dtype=torch.int64, device=device)
+    _lib.check(L.stacr_select_threshold(_ptr(x2d), _ptr(coeff), _ptr(q), dt, rows, feats, rank, _ptr(threshold),
+                                        int(cap), _ptr(idx), ib, _ptr(values), _ptr(count), _ptr(ws),
+                                        ws_bytes.value, _stream(device)), "stacr_select_threshold")
+    n = int(count.item())
+    if n < cap:
+        idx, values = idx[:n].clone(), values[:n].clone()
+    return idx, values
+
+
 def quantize(values: torch.Tensor, bits: int):
     """(data, scale) of quantize_values for bits 4/8 (stacr/quant.py:49-65)."""
     require_gpu(values, "values")

@@ -12,9 +12,9 @@ Same public surface and observable contract as stacr/layers.py:
     order of torch.topk(sorted=False) unspecified; readers only use them as a set).
   * STACRLinear(weight, bias, **options), from_linear, set_step, step, stored_bytes with the
     reference's validation and schedule (stacr/layers.py:202-473).
-Selectors "uniform", "block_sparse" and "sampled" are accepted by validation (as in the
-reference) but have no HIP kernel yet: using one in a training forward raises
-NotImplementedError.
+  * Selectors "uniform", "block_sparse" and "sampled" run as their own HIP kernels on the
+    save's coefficients (stacr_select_uniform / stacr_select_block_sparse / stacr_select_threshold),
+    and their values are quantized with quantize_values as in the reference (:146).
 """
 from __future__ import annotations
 
@@ -28,30 +28,39 @@ from torch.nn import functional as F
 from . import kernels
 from .adaptive_checkpointing import get_global_recomputation_guard
 from .oja import orthonormalize
-from .quant import QuantizedValues
+from .quant import QuantizedValues, quantize_values
 
 RESIDUAL_MODES = {"chunk_topk", "topk", "global_topk", "uniform", "none", "block_sparse", "sampled"}
-HIP_SELECTORS = {"chunk_topk", "topk", "global_topk"}
+TOPK_SELECTORS = {"chunk_topk", "topk", "global_topk"}
 
 
 def _check_selector(mode: str) -> None:
     if mode not in RESIDUAL_MODES:
         raise ValueError(f"Unknown residual_mode: {mode!r}")
-    if mode not in HIP_SELECTORS and mode != "none":
-        raise NotImplementedError(f"residual_mode {mode!r} has no HIP selection kernel in stacr_amd")
 
 
 def _select_residual(x, coeff, basis, budget, chunk_rows, mode, block_size=16, sample_ratio=0.1):
-    """(flat indices, values in x's dtype) of the selected residual, or (None, None).
-
-    Mirrors stacr/layers.py:44-102 for the top-k selectors on a given projection ``coeff``.
-    """
+    """(flat indices, values in x's dtype) of the selected residual, or (None, None)
+    (stacr/layers.py:44-101), on a given projection ``coeff``.  Indices ascend."""
     _check_selector(mode)
     if mode == "none" or budget <= 0 or x.numel() == 0:
         return None, None
-    _, idx, data, _ = kernels.save(x, basis.to(x.dtype), mode=mode, budget=float(budget),
-                                   chunk_rows=int(chunk_rows), bits=0, coeff=coeff.to(x.dtype))
-    return idx, data
+    q = basis.to(x.dtype)
+    coeff = coeff.to(x.dtype)
+    rows, features = x.shape
+    if mode in TOPK_SELECTORS or (mode == "block_sparse" and features % block_size):
+        sel = "global_topk" if mode == "global_topk" else "chunk_topk"
+        _, idx, data, _ = kernels.save(x, q, mode=sel, budget=float(budget), chunk_rows=int(chunk_rows), bits=0,
+                                       coeff=coeff)
+        return idx, data
+    k_total = int(round(budget * x.numel()))
+    if k_total == 0:
+        return None, None
+    if mode == "uniform":
+        return kernels.select_uniform(x, coeff, q, k_total)
+    if mode == "block_sparse":
+        return kernels.select_block_sparse(x, coeff, q, float(budget), int(chunk_rows), int(block_size))
+    return kernels.select_sampled(x, coeff, q, float(budget), float(sample_ratio), k_total)
 
 
 class STACRFunction(torch.autograd.Function):
@@ -73,19 +82,33 @@ class STACRFunction(torch.autograd.Function):
         budget = float(budget)
         mode = residual_mode
         _check_selector(mode)
+        bits = int(residual_bits)
         if mode == "none":
             mode, budget = "chunk_topk", 0.0
         with torch.autocast(device_type=x.device.type, enabled=False):
             activation, q = x2d.to(out2d.dtype), basis.to(out2d.dtype)
-            coeff, idx, data, scale = kernels.save(activation, q, mode=mode, budget=budget,
-                                                   chunk_rows=int(chunk_rows), bits=int(residual_bits))
+            fused = mode in TOPK_SELECTORS or (mode == "block_sparse" and d_in % int(residual_block_size))
+            if fused:  # projection, selection and quantization in one stacr_save call
+                sel = "global_topk" if mode == "global_topk" else "chunk_topk"
+                coeff, idx, data, scale = kernels.save(activation, q, mode=sel, budget=budget,
+                                                       chunk_rows=int(chunk_rows), bits=bits)
+                length = int(idx.numel()) if idx is not None else 0
+            else:  # projection, then the selector's kernels, then quantize_values
+                coeff, _, _, _ = kernels.save(activation, q, mode="chunk_topk", budget=0.0,
+                                              chunk_rows=int(chunk_rows), bits=0)
+                idx, val = _select_residual(activation, coeff, q, budget, int(chunk_rows), mode,
+                                            int(residual_block_size), float(residual_sample_ratio))
+                data = scale = None
+                if idx is not None:
+                    packed = quantize_values(val, bits)
+                    data, scale, bits, length = packed.data, packed.scale, packed.bits, packed.length
         saved = [coeff, weight, q]
         if idx is not None:
             saved += [idx, data, scale]
         ctx.save_for_backward(*saved)
         ctx.has_residual = idx is not None
-        ctx.residual_bits = int(residual_bits) if idx is not None else 0
-        ctx.residual_len = int(idx.numel()) if idx is not None else 0
+        ctx.residual_bits = bits if idx is not None else 0
+        ctx.residual_len = length if idx is not None else 0
         ctx.leading, ctx.in_features = x.shape[:-1], d_in
         ctx.out_features, ctx.transposed = out2d.shape[1], bool(transposed)
         ctx.input_dtype = x.dtype

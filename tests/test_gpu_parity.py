@@ -290,7 +290,7 @@ def test_layer_weight_gradient_matches_factor_identity(dev):
     assert torch.allclose(w.grad.cpu(), expected, atol=1e-3)
 
 
-@pytest.mark.parametrize("mode", ["chunk_topk", "global_topk", "none"])
+@pytest.mark.parametrize("mode", ["chunk_topk", "global_topk", "uniform", "block_sparse", "sampled", "none"])
 @pytest.mark.parametrize("bits", [0, 4, 8])
 def test_all_selectors_contract_from_the_saved_factors(dev, mode, bits):
     """Reference tests/test_integration.py:120-143: dW equals G^T (C Q^T + R_s) rebuilt from the
@@ -428,10 +428,10 @@ def test_autocast_forward_input_and_bias_gradient_match_native(dev, transposed):
 
 
 def test_stored_bytes_equals_saved_inventory_under_autocast(dev):
-    """Reference tests/test_memory.py:366-388 for the top-k selectors."""
+    """Reference tests/test_memory.py:43-65 (all four fixed-count selectors)."""
     from stacr_amd import STACRLinear
 
-    for mode in ("chunk_topk", "global_topk"):
+    for mode in ("chunk_topk", "block_sparse", "global_topk", "uniform"):
         announce("inventory", mode)
         layer = STACRLinear.from_linear(torch.nn.Linear(16, 7).to(dev), rank=4, residual_mode=mode, chunk_rows=1,
                                         residual_block_size=4, residual_budget=0.17)
