@@ -32,7 +32,8 @@ namespace {
 
 constexpr int kOSlab = 16;          // output features per workgroup
 constexpr int kMaxISlab = 1024;     // input features per part: S = 1024 x 16 fp32 = 64 KiB of LDS
-constexpr int kBwdThreads = 512;    // 8 waves
+constexpr int kBwdThreads = 1024;   // 16 waves: four per SIMD, so memory and LDS latency overlap
+constexpr int kPlanThreads = 512;   // the planner: two input features per thread
 constexpr int kRoundMax = 4096;     // residual entries bucketed per round (16-bit G; 2048 for fp32)
 constexpr int kMinPiece = 8;        // shortest piece (entries)
 constexpr int kMaxGroups = 256;     // piece groups of the widest configuration
@@ -60,7 +61,7 @@ struct GradCfg {
     using T = typename Act<DT>::T;
     static constexpr bool k16 = sizeof(T) == 2;
     // output features per thread: keeps the M accumulator at <= 72 fp32 registers
-    static constexpr int OT = k16 ? (R <= 8 ? 8 : (R == 16 ? 4 : 2)) : (R <= 16 ? 4 : 2);
+    static constexpr int OT = k16 ? (R <= 8 ? 4 : 2) : (R <= 8 ? 2 : 1);
     static constexpr int OG = kOSlab / OT;             // threads sharing one token row
     static constexpr int TP = kBwdThreads / OG;        // token-row pairs per block
     static constexpr int TB = 2 * TP;                  // token rows per block
@@ -71,7 +72,7 @@ struct GradCfg {
     static constexpr int ROUND = k16 ? kRoundMax : kRoundMax / 2;  // entries per round
     static constexpr int EPT = ROUND / kBwdThreads;    // staged entries per thread
     static constexpr int PD = 1;                       // blocks of C rows / plan data loaded ahead
-    static constexpr int GD = R <= 8 ? 2 : 1;          // blocks of G rows loaded ahead
+    static constexpr int GD = 1;                       // blocks of G rows loaded ahead
 };
 
 template <int B> struct Vec;
@@ -225,11 +226,11 @@ __device__ __forceinline__ uint32_t entry_value(const PlanArgs &a, int64_t e)
 }
 
 template <int IDX64>
-__global__ __launch_bounds__(kBwdThreads) void k_dw_plan(PlanArgs a)
+__global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
 {
     __shared__ uint32_t cnt[kMaxISlab], ccur[kMaxISlab];
     __shared__ uint32_t cstart[kMaxISlab], lstart[kMaxISlab], hstart[kMaxISlab], hidx[kMaxISlab];
-    __shared__ uint32_t s_tot[kBwdThreads / 64];
+    __shared__ uint32_t s_tot[kPlanThreads / 64];
     __shared__ uint32_t s_first;
     const int64_t b = blockIdx.x, p = blockIdx.y;
     const int64_t t0 = b * a.tb, t1 = min(t0 + a.tb, a.rows);
@@ -267,19 +268,19 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_plan(PlanArgs a)
     const bool f32 = a.g_dt == STACR_DTYPE_F32;
     for (uint32_t j = 0; j < n_rounds; ++j) {
         const uint32_t c0 = e0 + j * cap, c1 = min(c0 + cap, e1);
-        for (int c = threadIdx.x; c < ni; c += kBwdThreads) {
+        for (int c = threadIdx.x; c < ni; c += kPlanThreads) {
             cnt[c] = 0u;
             ccur[c] = 0u;
         }
         __syncthreads();
-        constexpr int EPT = kRoundMax / kBwdThreads;
+        constexpr int EPT = kRoundMax / kPlanThreads;
         uint32_t col[EPT], tl[EPT];
         uint32_t before = 0;
 #pragma unroll
         for (int k = 0; k < EPT; ++k) {
             col[k] = 0xffffffffu;
             tl[k] = 0u;
-            const uint32_t e = c0 + threadIdx.x + k * kBwdThreads;
+            const uint32_t e = c0 + threadIdx.x + k * kPlanThreads;
             const int64_t off64 = e < c1 ? flat_at<IDX64>(a.idx, e) - t0 * a.d_in : -1;
             if (off64 >= 0 && off64 < span) {
                 const uint32_t off = (uint32_t)off64;  // < 2^25: tb <= 512 rows of < 65536 features
@@ -295,7 +296,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_plan(PlanArgs a)
             }
         }
         uint32_t n_before;
-        block_exclusive_scan<kBwdThreads>(before, s_tot, &n_before);  // also orders the counts
+        block_exclusive_scan<kPlanThreads>(before, s_tot, &n_before);  // also orders the counts
         const uint32_t base = c0 + n_before;
         // prefix sums over the features (two per thread): bucket starts; then, with the piece
         // length fixed by the part's entry count, heavy-piece starts (= partial-sum slots), light
@@ -306,14 +307,14 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_plan(PlanArgs a)
             const int f0 = 2 * threadIdx.x;
             const uint32_t n0 = f0 < ni ? cnt[f0] : 0u, n1 = f0 + 1 < ni ? cnt[f0 + 1] : 0u;
             uint32_t tot_e, tot_h, tot_l, tot_x;
-            const uint32_t se = block_exclusive_scan<kBwdThreads>(n0 + n1, s_tot, &tot_e);
+            const uint32_t se = block_exclusive_scan<kPlanThreads>(n0 + n1, s_tot, &tot_e);
             piece = min(max((tot_e + a.groups - 1) / a.groups, (uint32_t)kMinPiece), 255u);
             const uint32_t p0 = (n0 + piece - 1) / piece, p1 = (n1 + piece - 1) / piece;
             const uint32_t h0 = p0 > 1 ? p0 : 0u, h1 = p1 > 1 ? p1 : 0u;
             const uint32_t l0 = p0 == 1, l1 = p1 == 1;
-            const uint32_t sh = block_exclusive_scan<kBwdThreads>(h0 + h1, s_tot, &tot_h);
-            const uint32_t sl = block_exclusive_scan<kBwdThreads>(l0 + l1, s_tot, &tot_l);
-            const uint32_t sx = block_exclusive_scan<kBwdThreads>((p0 > 1) + (p1 > 1), s_tot, &tot_x);
+            const uint32_t sh = block_exclusive_scan<kPlanThreads>(h0 + h1, s_tot, &tot_h);
+            const uint32_t sl = block_exclusive_scan<kPlanThreads>(l0 + l1, s_tot, &tot_l);
+            const uint32_t sx = block_exclusive_scan<kPlanThreads>((p0 > 1) + (p1 > 1), s_tot, &tot_x);
             if (f0 < ni) {
                 cstart[f0] = se; hstart[f0] = sh; lstart[f0] = tot_h + sl; hidx[f0] = sx;
             }
@@ -331,7 +332,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_plan(PlanArgs a)
 #pragma unroll
         for (int k = 0; k < EPT; ++k) {
             if (col[k] != 0xffffffffu) {
-                const uint32_t e = c0 + threadIdx.x + k * kBwdThreads;
+                const uint32_t e = c0 + threadIdx.x + k * kPlanThreads;
                 const uint32_t pos = base + cstart[col[k]] + atomicAdd(&ccur[col[k]], 1u);
                 const uint32_t v = entry_value(a, e);
                 if (f32)
@@ -340,7 +341,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_plan(PlanArgs a)
                     static_cast<uint32_t *>(a.ent)[pos] = (tl[k] << 16) | (v & 0xffffu);
             }
         }
-        for (int c = threadIdx.x; c < ni; c += kBwdThreads) {
+        for (int c = threadIdx.x; c < ni; c += kPlanThreads) {
             const uint32_t n = cnt[c];
             const uint32_t npc = (n + piece - 1) / piece;
             if (npc == 1) a.task[base + lstart[c]] = make_uint2((uint32_t)c | (kDirect << 16), (cstart[c] << 8) | n);
@@ -393,7 +394,8 @@ struct FusedLds {
     static constexpr size_t s_heavy = s_task + (size_t)kTaskCap * 8;                 // [kHeavyCap]
     static constexpr size_t s_slot = s_heavy + (size_t)kHeavyCap * 8;                // [kSlotCap][16]
     static constexpr size_t end = s_slot + (size_t)kSlotCap * kOSlab * 4;
-    static constexpr int HALF = (C::NV + 1) / 2;
+    static constexpr int NPASS = C::NV > 36 ? 4 : 2;  // M reduction passes (LDS holds NV / NPASS per thread)
+    static constexpr int HALF = (C::NV + NPASS - 1) / NPASS;
     static constexpr size_t red_end = s_gtile + ((size_t)kBwdThreads * HALF + (size_t)8 * C::OG * HALF +
                                                  (size_t)kOSlab * (R + 1)) * 4;
     static constexpr size_t bytes = end > red_end ? end : red_end;
@@ -664,25 +666,6 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
             }
             if (bh.n_rounds) store_stage(sq[0]);
         }
-        // advance the rings; block blk + PD's loads overlap the arithmetic of this block
-#pragma unroll
-        for (int d = 0; d + 1 < GD; ++d)
-#pragma unroll
-            for (int k = 0; k < NW; ++k) { wq[d][0][k] = wq[d + 1][0][k]; wq[d][1][k] = wq[d + 1][1][k]; }
-#pragma unroll
-        for (int d = 0; d + 1 < PD; ++d) {
-#pragma unroll
-            for (int k = 0; k < CW; ++k) { xq[d][0][k] = xq[d + 1][0][k]; xq[d][1][k] = xq[d + 1][1][k]; }
-            sq[d] = sq[d + 1];
-        }
-#pragma unroll
-        for (int d = 0; d + 1 < PD + 2; ++d) hq[d] = hq[d + 1];
-        if (blk + GD < n_blocks) load_grows(blk + GD, wq[GD - 1]);
-        if (blk + PD < n_blocks) {
-            load_crows(blk + PD, xq[PD - 1]);
-            if (hq[PD - 1].n_rounds) load_stage(sq[PD - 1], hq[PD - 1].r0);
-        }
-        hq[PD + 1] = load_hdr(blk + PD + 2);
         // ---- low rank: m[o][j] += G[t][o] C[t][j] + G[t+1][o] C[t+1][j];  m[o][R] += G[t][o] + G[t+1][o]
         if constexpr (K16) {
             uint32_t pr[OT];  // (G[t][o], G[t+1][o]) pairs
@@ -715,6 +698,29 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
 #pragma unroll
             for (int o = 0; o < OT; ++o) m[o][R] += __uint_as_float(ca[o]) + __uint_as_float(cb[o]);
         }
+        // advance the rings after this block's low-rank arithmetic, so the registers it consumed are
+        // free for the next block's loads, which overlap this block's sparse work
+#pragma unroll
+        for (int d = 0; d + 1 < GD; ++d)
+#pragma unroll
+            for (int k = 0; k < NW; ++k) { wq[d][0][k] = wq[d + 1][0][k]; wq[d][1][k] = wq[d + 1][1][k]; }
+#pragma unroll
+        for (int d = 0; d + 1 < PD; ++d) {
+#pragma unroll
+            for (int k = 0; k < CW; ++k) { xq[d][0][k] = xq[d + 1][0][k]; xq[d][1][k] = xq[d + 1][1][k]; }
+            sq[d] = sq[d + 1];
+        }
+#pragma unroll
+        for (int d = 0; d + 1 < PD + 2; ++d) hq[d] = hq[d + 1];
+        // Loads issue in the order they are consumed: the memory counter retires in issue order,
+        // so waiting for the next block's C rows and plan data must not also wait for G rows
+        // that are only needed GD blocks from now.
+        if (blk + PD < n_blocks) {
+            load_crows(blk + PD, xq[PD - 1]);
+            if (hq[PD - 1].n_rounds) load_stage(sq[PD - 1], hq[PD - 1].r0);
+        }
+        hq[PD + 1] = load_hdr(blk + PD + 2);
+        if (blk + GD < n_blocks) load_grows(blk + GD, wq[GD - 1]);
         if (!sparse || bh.n_rounds == 0) continue;
         __syncthreads();  // G tile and first round staged
         run_round(bh.r0);
@@ -731,13 +737,13 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
     __syncthreads();
 
     // ---- reduce m over the TP threads that share an output group, in a fixed order.
-    // Two halves of the per-thread values in turn: every thread parks its half in LDS, 8 threads
+    // NPASS slices of the per-thread values in turn: every thread parks its half in LDS, 8 threads
     // per output sum TP/8 rows each, one thread per output adds the 8 partial sums.
     constexpr int HALF = L::HALF;
     constexpr int TP = C::TP;
     float *psum = mred + kBwdThreads * HALF;  // [8][OG * HALF]
     float *mfin = psum + 8 * OG * HALF;       // final M: [kOSlab][R + 1]
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < L::NPASS; ++h) {
         const int v0 = h * HALF, v1 = min(C::NV, v0 + HALF);
 #pragma unroll
         for (int v = 0; v < C::NV; ++v)
@@ -762,10 +768,11 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
     }
 
     // ---- epilogue: dW tile = M Q^T + S, one rounding to the weight dtype; dbias from M[:, R].
-    // A thread takes whole input features i (its Q row in registers) and all 16 outputs.
+    // A thread takes one input feature i (its Q row in registers) and all 16 outputs.
     const T *q = static_cast<const T *>(a.q);
     const bool vec_out = a.transposed && a.out_vec_ok && o0 + kOSlab <= a.d_out;
-    for (int ii = threadIdx.x; ii < ni; ii += kBwdThreads) {
+    static_assert(kMaxISlab <= kBwdThreads, "one input feature per thread");
+    if (const int ii = threadIdx.x; ii < ni) {
         const int64_t i = i0 + ii;
         float qr[R];
 #pragma unroll
@@ -929,9 +936,9 @@ int launch_grad(const StacrGradArgs &a, const GPlan &p, char *ws, const size_t *
         pa.bhdr = reinterpret_cast<BlockHdr *>(ws + off[GW_BHDR]);
         const dim3 pg((unsigned)p.n_blocks, (unsigned)p.n_parts);
         if (a.index_bytes == 8)
-            stacr_launch("k_dw_plan", s, [&] { k_dw_plan<1><<<pg, kBwdThreads, 0, s>>>(pa); });
+            stacr_launch("k_dw_plan", s, [&] { k_dw_plan<1><<<pg, kPlanThreads, 0, s>>>(pa); });
         else
-            stacr_launch("k_dw_plan", s, [&] { k_dw_plan<0><<<pg, kBwdThreads, 0, s>>>(pa); });
+            stacr_launch("k_dw_plan", s, [&] { k_dw_plan<0><<<pg, kPlanThreads, 0, s>>>(pa); });
         f.ent = pa.ent;
         f.task = pa.task;
         f.heavy = pa.heavy;
