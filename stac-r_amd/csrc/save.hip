@@ -161,15 +161,98 @@ __global__ void k_zero_u32(uint32_t *p, int64_t n)
         p[i] = 0u;
 }
 
+// Set-up of a save: the padded fp32 basis, and the histograms and max key cleared (one launch).
 template <int DT>
-__global__ void k_pad_basis(const typename Act<DT>::T *__restrict__ q, int64_t d, int rank, int R, float *__restrict__ qp)
+__global__ void k_prep(const typename Act<DT>::T *__restrict__ q, int64_t d, int rank, int R, float *__restrict__ qp,
+                       uint32_t *__restrict__ zero, int64_t n_zero)
 {
     const int64_t n = d * R;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
         const int64_t row = i / R;
         const int j = (int)(i - row * R);
         qp[i] = j < rank ? Act<DT>::ld(q[row * rank + j]) : 0.f;
     }
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_zero; i += step) zero[i] = 0u;
+}
+
+// One radix level of one chunk, computed by a whole workgroup: the bin holding the need-th largest
+// key among those matching `prefix`.  Every thread calls it and receives the new state.
+__device__ SelState block_select(int lvl, const uint32_t *__restrict__ h, uint32_t prefix, uint32_t need,
+                                 uint32_t *s_tot, SelState *s_res)
+{
+    const int per = kDigitBins[lvl] / kBlock;
+    const int bits = lvl == 2 ? 9 : 11;
+    // thread t looks at the bins of owner 255 - t so that the exclusive scan counts the bins above
+    const int owner = kBlock - 1 - threadIdx.x;
+    uint32_t local = 0u;
+    for (int i = 0; i < per; ++i) local += h[owner * per + i];
+    if (threadIdx.x == 0) *s_res = SelState{prefix << bits, need};
+    uint32_t total;
+    const uint32_t above = block_exclusive_scan(local, s_tot, &total);
+    if (above < need && above + local >= need) {
+        uint32_t run = above;
+        for (int i = per - 1; i >= 0; --i) {
+            const int b = owner * per + i;
+            if (run + h[b] >= need) {
+                *s_res = SelState{(prefix << bits) | (uint32_t)b, need - run};
+                break;
+            }
+            run += h[b];
+        }
+    }
+    __syncthreads();
+    const SelState r = *s_res;
+    __syncthreads();  // s_res is free again
+    return r;
+}
+
+// Level lvl's state of a chunk, from its histogram and the previous level's state (level 0: the
+// chunk's k).  The first workgroup of the chunk records it for the kernels that follow.
+__device__ SelState chunk_select(int lvl, const uint32_t *__restrict__ hist, SelState *__restrict__ state,
+                                 int64_t chunk, int64_t n_chunks, uint32_t k_full, uint32_t k_last, bool record,
+                                 uint32_t *s_tot, SelState *s_res)
+{
+    uint32_t need, prefix;
+    if (lvl == 0) {
+        need = chunk == n_chunks - 1 ? k_last : k_full;
+        prefix = 0u;
+    } else {
+        const SelState sp = state[chunk * 3 + lvl - 1];
+        need = sp.need;
+        prefix = sp.prefix;
+    }
+    const SelState r = block_select(lvl, hist + (chunk * 3 + lvl) * kBins, prefix, need, s_tot, s_res);
+    if (record && threadIdx.x == 0) state[chunk * 3 + lvl] = r;
+    return r;
+}
+
+// The same as a kernel, one workgroup per chunk (the trim pass over the candidate list).
+__global__ __launch_bounds__(kBlock) void k_select_step(int lvl, const uint32_t *__restrict__ hist,
+                                                        SelState *__restrict__ state, int64_t n_chunks,
+                                                        uint32_t k_full, uint32_t k_last)
+{
+    __shared__ uint32_t s_tot[kWaves];
+    __shared__ SelState s_res;
+    chunk_select(lvl, hist, state, blockIdx.x, n_chunks, k_full, k_last, true, s_tot, &s_res);
+}
+
+// A workgroup's output offset and tie budget: its chunk's earlier workgroups in order, ties handed
+// out first come (the per-workgroup form of k_offsets).
+__device__ WgOffset wg_offset(const WgCount *__restrict__ counts, int64_t chunk, int64_t w, int64_t wgs_per_chunk,
+                              uint32_t need_eq, uint32_t chunk_k, uint32_t *s_tot)
+{
+    uint32_t gt = 0u, eq = 0u;
+    for (int64_t v = threadIdx.x; v < w; v += kBlock) {
+        const WgCount c = counts[chunk * wgs_per_chunk + v];
+        gt += c.gt;
+        eq += c.eq;
+    }
+    const uint32_t gt_before = block_sum(gt, s_tot);
+    const uint32_t eq_before = block_sum(eq, s_tot);
+    const WgCount mine = counts[chunk * wgs_per_chunk + w];
+    const uint32_t take = eq_before >= need_eq ? 0u : min(mine.eq, need_eq - eq_before);
+    return WgOffset{(uint32_t)chunk * chunk_k + gt_before + min(need_eq, eq_before), take};
 }
 
 // Pass 1: coefficients, first-digit histogram, max key.
@@ -261,13 +344,17 @@ template <int DT, int R, int V, bool QREG>
 __global__ __launch_bounds__(kBlock) void k_refine_hist(SaveGeom g, int lvl, const typename Act<DT>::T *__restrict__ x,
                                                         const float *__restrict__ qp,
                                                         const typename Act<DT>::T *__restrict__ coeff,
-                                                        uint32_t *__restrict__ hist, const SelState *__restrict__ state)
+                                                        uint32_t *__restrict__ hist, SelState *__restrict__ state,
+                                                        uint32_t k_full, uint32_t k_last)
 {
     __shared__ uint32_t s_hist[kBins];
     for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
-    const uint32_t prefix = state[chunk * 3 + lvl - 1].prefix;
+    __shared__ uint32_t s_tot[kWaves];
+    __shared__ SelState s_res;
+    const uint32_t prefix = chunk_select(lvl - 1, hist, state, chunk, g.n_chunks, k_full, k_last,
+                                         blockIdx.x % g.wgs_per_chunk == 0, s_tot, &s_res).prefix;
     const int match_shift = kDigitShift[lvl - 1], dshift = kDigitShift[lvl];
     const uint32_t dmask = (uint32_t)kDigitBins[lvl] - 1u;
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
@@ -299,58 +386,19 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist(SaveGeom g, int lvl, con
         if (s_hist[b]) atomicAdd(&gh[b], s_hist[b]);
 }
 
-// One radix level per chunk: find the bin holding the need-th largest key.
-// hist_stride/state_base let the same kernel serve the per-chunk pass and the trim pass.
-__global__ __launch_bounds__(kBlock) void k_select_step(int lvl, const uint32_t *__restrict__ hist,
-                                                        SelState *__restrict__ state, int64_t n_chunks,
-                                                        uint32_t k_full, uint32_t k_last)
-{
-    __shared__ uint32_t s_tot[kWaves];
-    const int64_t chunk = blockIdx.x;
-    uint32_t need, prefix;
-    if (lvl == 0) {
-        need = chunk == n_chunks - 1 ? k_last : k_full;
-        prefix = 0u;
-    } else {
-        const SelState s = state[chunk * 3 + lvl - 1];
-        need = s.need;
-        prefix = s.prefix;
-    }
-    const int nb = kDigitBins[lvl];
-    const int per = nb / kBlock;
-    const int bits = lvl == 2 ? 9 : 11;
-    const uint32_t *h = hist + (chunk * 3 + lvl) * kBins;
-    // thread t looks at the bins of owner 255 - t so that the exclusive scan counts the bins above
-    const int owner = kBlock - 1 - threadIdx.x;
-    uint32_t local = 0u;
-    for (int i = 0; i < per; ++i) local += h[owner * per + i];
-    uint32_t total;
-    const uint32_t above = block_exclusive_scan(local, s_tot, &total);
-    if (threadIdx.x == 0) state[chunk * 3 + lvl] = SelState{prefix << bits, need};
-    __syncthreads();
-    if (above < need && above + local >= need) {
-        uint32_t run = above;
-        for (int i = per - 1; i >= 0; --i) {
-            const int b = owner * per + i;
-            if (run + h[b] >= need) {
-                state[chunk * 3 + lvl] = SelState{(prefix << bits) | (uint32_t)b, need - run};
-                break;
-            }
-            run += h[b];
-        }
-    }
-}
-
 template <int DT, int R, int V, bool QREG>
 __global__ __launch_bounds__(kBlock) void k_count(SaveGeom g, const typename Act<DT>::T *__restrict__ x,
                                                   const float *__restrict__ qp,
                                                   const typename Act<DT>::T *__restrict__ coeff,
-                                                  const SelState *__restrict__ state, WgCount *__restrict__ counts)
+                                                  const uint32_t *__restrict__ hist, SelState *__restrict__ state,
+                                                  WgCount *__restrict__ counts, uint32_t k_full, uint32_t k_last)
 {
     __shared__ uint32_t s_tot[kWaves];
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
-    const uint32_t T = state[chunk * 3 + 2].prefix;
+    __shared__ SelState s_res;
+    const uint32_t T = chunk_select(2, hist, state, chunk, g.n_chunks, k_full, k_last,
+                                    blockIdx.x % g.wgs_per_chunk == 0, s_tot, &s_res).prefix;
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
     QCols<R, V, QREG> qc;
     qc.init(qp, (int64_t)u * V, g.d);
@@ -408,7 +456,7 @@ template <int DT, int R, int V, bool QREG>
 __global__ __launch_bounds__(kBlock) void k_emit(SaveGeom g, const typename Act<DT>::T *__restrict__ x,
                                                  const float *__restrict__ qp,
                                                  const typename Act<DT>::T *__restrict__ coeff,
-                                                 const SelState *__restrict__ state, const WgOffset *__restrict__ offs,
+                                                 const SelState *__restrict__ state, const WgCount *__restrict__ counts, uint32_t chunk_k,
                                                  const uint32_t *__restrict__ maxkey, OutSpec o, float *scale_out,
                                                  int to_list)
 {
@@ -416,7 +464,9 @@ __global__ __launch_bounds__(kBlock) void k_emit(SaveGeom g, const typename Act<
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
     const uint32_t T = state[chunk * 3 + 2].prefix;
-    const WgOffset wo = offs[blockIdx.x];
+    __shared__ uint32_t s_off[kWaves];
+    const WgOffset wo = wg_offset(counts, chunk, blockIdx.x - chunk * g.wgs_per_chunk, g.wgs_per_chunk,
+                                  state[chunk * 3 + 2].need, chunk_k, s_off);
     const float amax = Act<DT>::rnd(__uint_as_float(*maxkey));
     const float scale = o.bits ? quant_scale(*maxkey, o.bits, amax) : 1.f;
     if (!to_list && blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
@@ -693,14 +743,18 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
                                                           const typename Act<DT>::T *__restrict__ x,
                                                           const float *__restrict__ qp,
                                                           const typename Act<DT>::T *__restrict__ coeff,
-                                                          uint32_t *__restrict__ hist, const SelState *__restrict__ state)
+                                                          uint32_t *__restrict__ hist, SelState *__restrict__ state,
+                                                        uint32_t k_full, uint32_t k_last)
 {
     constexpr int NB = Batch<R>::NB;
     __shared__ uint32_t s_hist[kBins];
     for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
-    const uint32_t prefix = state[chunk * 3 + lvl - 1].prefix;
+    __shared__ uint32_t s_tot[kWaves];
+    __shared__ SelState s_res;
+    const uint32_t prefix = chunk_select(lvl - 1, hist, state, chunk, g.n_chunks, k_full, k_last,
+                                         blockIdx.x % g.wgs_per_chunk == 0, s_tot, &s_res).prefix;
     const int match_shift = kDigitShift[lvl - 1], dshift = kDigitShift[lvl];
     const uint32_t dmask = (uint32_t)kDigitBins[lvl] - 1u;
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
@@ -741,13 +795,16 @@ template <int DT, int R, int V>
 __global__ __launch_bounds__(kBlock) void k_count_b(SaveGeom g, FastGeom fg, const typename Act<DT>::T *__restrict__ x,
                                                     const float *__restrict__ qp,
                                                     const typename Act<DT>::T *__restrict__ coeff,
-                                                    const SelState *__restrict__ state, WgCount *__restrict__ counts)
+                                                    const uint32_t *__restrict__ hist, SelState *__restrict__ state,
+                                                  WgCount *__restrict__ counts, uint32_t k_full, uint32_t k_last)
 {
     constexpr int NB = Batch<R>::NB;
     __shared__ uint32_t s_tot[kWaves];
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
-    const uint32_t T = state[chunk * 3 + 2].prefix;
+    __shared__ SelState s_res;
+    const uint32_t T = chunk_select(2, hist, state, chunk, g.n_chunks, k_full, k_last,
+                                    blockIdx.x % g.wgs_per_chunk == 0, s_tot, &s_res).prefix;
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
     const int64_t col = (int64_t)u * V;
     const bool col_ok = col < g.d;
@@ -788,7 +845,7 @@ template <int DT, int R, int V>
 __global__ __launch_bounds__(kBlock) void k_emit_b(SaveGeom g, FastGeom fg, const typename Act<DT>::T *__restrict__ x,
                                                    const float *__restrict__ qp,
                                                    const typename Act<DT>::T *__restrict__ coeff,
-                                                   const SelState *__restrict__ state, const WgOffset *__restrict__ offs,
+                                                   const SelState *__restrict__ state, const WgCount *__restrict__ counts, uint32_t chunk_k,
                                                    const uint32_t *__restrict__ maxkey, OutSpec o, float *scale_out,
                                                    int to_list)
 {
@@ -797,7 +854,9 @@ __global__ __launch_bounds__(kBlock) void k_emit_b(SaveGeom g, FastGeom fg, cons
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
     const uint32_t T = state[chunk * 3 + 2].prefix;
-    const WgOffset wo = offs[blockIdx.x];
+    __shared__ uint32_t s_off[kWaves];
+    const WgOffset wo = wg_offset(counts, chunk, blockIdx.x - chunk * g.wgs_per_chunk, g.wgs_per_chunk,
+                                  state[chunk * 3 + 2].need, chunk_k, s_off);
     const float amax = Act<DT>::rnd(__uint_as_float(*maxkey));
     const float scale = o.bits ? quant_scale(*maxkey, o.bits, amax) : 1.f;
     if (!to_list && blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
@@ -1112,16 +1171,15 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     uint32_t *maxkey = carve<uint32_t>(ws, off[WS_MAXKEY]);
     SelState *state = carve<SelState>(ws, off[WS_STATE]);
     WgCount *counts = carve<WgCount>(ws, off[WS_COUNTS]);
-    WgOffset *offs = carve<WgOffset>(ws, off[WS_OFFS]);
     const bool resid = a.k_total > 0;
     const int nwg = (int)p.n_wgs;
 
-    stacr_launch("k_pad_basis", s, [&] { k_pad_basis<DT><<<grid_for(a.feats * R), kBlock, 0, s>>>(static_cast<const T *>(a.q), a.feats, a.rank, R, qp); });
-    if (resid) {
-        // histogram and max key are contiguous in the layout: one clear
-        stacr_launch("k_zero_u32", s, [&] { k_zero_u32<<<grid_for((int64_t)p.g.n_chunks * 3 * kBins + 64), kBlock, 0, s>>>(
-            hist, (int64_t)((off[WS_MAXKEY] + sizeof(uint32_t) - off[WS_HIST]) / sizeof(uint32_t))); });
-    }
+    // padded basis; histograms and max key (contiguous in the layout) cleared in the same launch
+    const int64_t n_zero = resid ? (int64_t)((off[WS_MAXKEY] + sizeof(uint32_t) - off[WS_HIST]) / sizeof(uint32_t)) : 0;
+    stacr_launch("k_prep", s, [&] {
+        k_prep<DT><<<grid_for(hmax<int64_t>(a.feats * R, n_zero)), kBlock, 0, s>>>(static_cast<const T *>(a.q), a.feats,
+                                                                                 a.rank, R, qp, hist, n_zero);
+    });
     // batched fast path: one aligned vector per thread per row, basis columns in registers
     constexpr bool kFastOk = QREG && V == Act<DT>::kVec && V * R <= 64;
     const bool fast = kFastOk && p.g.mv == 1 && p.g.L >= 64;
@@ -1137,21 +1195,19 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     }
     if (!resid) return stacr_hip_check(hipGetLastError(), "save kernels");
 
-    const int nch = (int)p.g.n_chunks;
     const uint32_t kf = (uint32_t)a.k_full, kl = (uint32_t)a.k_last;
-    stacr_launch("k_select_step", s, [&] { k_select_step<<<nch, kBlock, 0, s>>>(0, hist, state, p.g.n_chunks, kf, kl); });
+    // Each pass first finds the previous radix level's bin for its chunk (every workgroup from the
+    // completed histogram; the chunk's first workgroup records it), so no selection launches.
     for (int lvl = 1; lvl < 3; ++lvl) {
         if constexpr (kFastOk) {
-            if (fast) stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, x, qp, coeff, hist, state); });
+            if (fast) stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, x, qp, coeff, hist, state, kf, kl); });
         }
-        if (!fast) stacr_launch("k_refine_hist", s, [&] { k_refine_hist<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, lvl, x, qp, coeff, hist, state); });
-        stacr_launch("k_select_step", s, [&] { k_select_step<<<nch, kBlock, 0, s>>>(lvl, hist, state, p.g.n_chunks, kf, kl); });
+        if (!fast) stacr_launch("k_refine_hist", s, [&] { k_refine_hist<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, lvl, x, qp, coeff, hist, state, kf, kl); });
     }
     if constexpr (kFastOk) {
-        if (fast) stacr_launch("k_count", s, [&] { k_count_b<DT, R, V><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, counts); });
+        if (fast) stacr_launch("k_count", s, [&] { k_count_b<DT, R, V><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, hist, state, counts, kf, kl); });
     }
-    if (!fast) stacr_launch("k_count", s, [&] { k_count<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, counts); });
-    stacr_launch("k_offsets", s, [&] { k_offsets<<<nch, kBlock, 0, s>>>(counts, offs, state, p.g.wgs_per_chunk, kf); });
+    if (!fast) stacr_launch("k_count", s, [&] { k_count<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, hist, state, counts, kf, kl); });
 
     OutSpec o{};
     o.idx = a.idx;
@@ -1164,9 +1220,9 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     o.list_idx = lix;
     o.cap = (uint32_t)(p.trim ? a.k_sum : a.k_total);
     if constexpr (kFastOk) {
-        if (fast) stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, offs, maxkey, o, a.scale, p.trim ? 1 : 0); });
+        if (fast) stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0); });
     }
-    if (!fast) stacr_launch("k_emit", s, [&] { k_emit<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, offs, maxkey, o, a.scale, p.trim ? 1 : 0); });
+    if (!fast) stacr_launch("k_emit", s, [&] { k_emit<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0); });
 
     if (p.trim) {
         uint32_t *thist = carve<uint32_t>(ws, off[WS_THIST]);

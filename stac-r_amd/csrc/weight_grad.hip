@@ -7,8 +7,7 @@
 // 40-46): products use the exact integer code and the per-tensor fp32 scale multiplies each
 // segment's sum when it is added to the accumulator.
 //
-// Three launches:
-//   k_rowptr   ascending flat indices -> first residual entry of every token row (CSR offsets)
+// Two launches:
 //   k_dw_plan  for every block of TB token rows and every input-feature part: the block's residual
 //              entries bucketed by input feature (in rounds of <= 4096 entries) and cut into equal
 //              runs of P entries, one run per thread of the streaming kernel, plus the list of
@@ -147,28 +146,6 @@ __device__ __forceinline__ uint32_t div_small(uint32_t off, uint32_t d, float in
     return q;
 }
 
-// rowptr[t] = first entry whose flat index is >= t * d_in (t = 0..rows).  Indices are ascending
-// (stacr_save writes them so); entries with an index outside rows x d_in count as row `rows` and
-// so fall outside every block.
-template <int IDX64>
-__global__ void k_rowptr(const void *__restrict__ idx, int64_t nnz, int64_t d_in, int64_t rows,
-                         uint32_t *__restrict__ rowptr)
-{
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= nnz) return;
-    const int64_t lim = rows * d_in;
-    const int64_t f = flat_at<IDX64>(idx, e);
-    const int64_t t = (f < 0 || f >= lim) ? rows : f / d_in;
-    int64_t tprev = -1;
-    if (e) {
-        const int64_t fp = flat_at<IDX64>(idx, e - 1);
-        tprev = (fp < 0 || fp >= lim) ? rows : fp / d_in;
-    }
-    for (int64_t tt = tprev + 1; tt <= t; ++tt) rowptr[tt] = (uint32_t)e;
-    if (e == nnz - 1)
-        for (int64_t tt = t + 1; tt <= rows; ++tt) rowptr[tt] = (uint32_t)nnz;
-}
-
 // ------------------------------------------------------------------ the plan
 // One round of one (block, part): its bucketed entries, pieces and heavy records all start at
 // plan slot `base` (a part's entries of a round occupy a private slot range, and it never has
@@ -197,7 +174,6 @@ struct PlanArgs {
     uint32_t round_cap;      // entries per round (<= kRoundMax)
     uint32_t groups;         // piece groups of the streaming kernel
     uint32_t max_rounds;     // rounds the header array holds
-    const uint32_t *rowptr;
     void *ent;               // [nnz] 16-bit G: t_local << 16 | value code (uint32);
                              //       fp32 G: {t_local, value bits} (uint2)
     uint2 *task;             // [nnz] {feature | slot << 16, entry offset << 8 | entries}
@@ -231,7 +207,6 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
     __shared__ uint32_t cnt[kMaxISlab], ccur[kMaxISlab];
     __shared__ uint32_t cstart[kMaxISlab], lstart[kMaxISlab], hstart[kMaxISlab], hidx[kMaxISlab];
     __shared__ uint32_t s_tot[kPlanThreads / 64];
-    __shared__ uint32_t s_first;
     const int64_t b = blockIdx.x, p = blockIdx.y;
     const int64_t t0 = b * a.tb, t1 = min(t0 + a.tb, a.rows);
     const int64_t i0 = p * a.i_span;
@@ -241,27 +216,35 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
     const float inv_d = 1.f / (float)a.d_in;
     // entry range of a block; the clamps keep indices that are not ascending inside the arrays
     const uint32_t nnz = (uint32_t)a.nnz;
-    auto range = [&](int64_t bb, uint32_t &x0, uint32_t &x1) {
-        x0 = min(a.rowptr[bb * a.tb], nnz);
-        x1 = max(x0, min(a.rowptr[min((bb + 1) * a.tb, a.rows)], nnz));
-    };
+    // The block's entries [e0, e1): the first entries whose flat index is >= t0 * d_in and
+    // >= t1 * d_in, found together by a 512-way parallel search of the ascending indices (the
+    // result stays in [0, nnz] for indices that are not ascending, and e1 >= e0 is enforced).
     uint32_t e0, e1;
-    range(b, e0, e1);
+    {
+        const int64_t key0 = t0 * a.d_in, key1 = t1 * a.d_in;
+        uint32_t lo0 = 0u, hi0 = nnz, lo1 = 0u, hi1 = nnz;
+        while (lo0 < hi0 || lo1 < hi1) {
+            const uint32_t st0 = max(1u, (hi0 - lo0 + kPlanThreads - 1) / kPlanThreads);
+            const uint32_t st1 = max(1u, (hi1 - lo1 + kPlanThreads - 1) / kPlanThreads);
+            const uint32_t p0 = lo0 + threadIdx.x * st0, p1 = lo1 + threadIdx.x * st1;
+            const bool b0 = p0 < hi0 && flat_at<IDX64>(a.idx, p0) < key0;
+            const bool b1 = p1 < hi1 && flat_at<IDX64>(a.idx, p1) < key1;
+            const uint32_t c0 = (uint32_t)__syncthreads_count(b0), c1 = (uint32_t)__syncthreads_count(b1);
+            if (c0 == 0u) hi0 = lo0;  // the first sample is not below the key
+            else { lo0 += (c0 - 1u) * st0 + 1u; hi0 = min(hi0, lo0 - 1u + st0); }
+            if (c1 == 0u) hi1 = lo1;
+            else { lo1 += (c1 - 1u) * st1 + 1u; hi1 = min(hi1, lo1 - 1u + st1); }
+            if (st0 == 1u) hi0 = lo0;  // unit steps: every position was sampled
+            if (st1 == 1u) hi1 = lo1;
+        }
+        e0 = lo0;
+        e1 = max(e0, lo1);
+    }
     const uint32_t cap = a.round_cap;
     uint32_t n_rounds = (e1 - e0 + cap - 1) / cap;
-    if (threadIdx.x < 64) {  // rounds of the blocks before this one
-        uint32_t r = 0;
-        for (int64_t bb = threadIdx.x; bb < b; bb += 64) {
-            uint32_t x0, x1;
-            range(bb, x0, x1);
-            r += (x1 - x0 + cap - 1) / cap;
-        }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) r += __shfl_xor(r, off, 64);
-        if (threadIdx.x == 0) s_first = r;
-    }
-    __syncthreads();
-    const uint32_t first = s_first;
+    // Round numbering: floor(e0 / cap) + b.  A block with n entries has <= floor(n / cap) + 1
+    // rounds, so the ranges of consecutive blocks never overlap and stay below nnz / cap + blocks.
+    const uint32_t first = e0 / cap + (uint32_t)b;
     if (first + n_rounds > a.max_rounds) n_rounds = 0;  // only for indices that are not ascending
     if (threadIdx.x == 0 && n_rounds == 0)
         a.bhdr[b * a.n_parts + p] = BlockHdr{RoundHdr{0u, 0u, 0u, 0u}, first, 0u, {0u, 0u}};
@@ -828,7 +811,7 @@ CfgInfo block_geometry(int dt, int R)
     return R <= 4 ? cfg_info<1, 4>() : R <= 8 ? cfg_info<1, 8>() : R <= 16 ? cfg_info<1, 16>() : cfg_info<1, 32>();
 }
 
-enum { GW_ROWPTR, GW_ENT, GW_TASK, GW_HEAVY, GW_RHDR, GW_BHDR, GW_N };
+enum { GW_ENT, GW_TASK, GW_HEAVY, GW_RHDR, GW_BHDR, GW_N };
 
 struct GPlan {
     int R, tb, round_cap;
@@ -856,7 +839,6 @@ size_t glayout(const StacrGradArgs &a, const GPlan &p, size_t *off)
     auto take = [&](int slot, size_t bytes) { off[slot] = cur; cur += (bytes + 255) & ~(size_t)255; };
     const bool sp = a.nnz > 0;
     const size_t n = sp ? (size_t)a.nnz : 0;
-    take(GW_ROWPTR, sp ? (size_t)(a.rows + 1) * 4 : 0);
     take(GW_ENT, n * 8);
     take(GW_TASK, n * 8);
     take(GW_HEAVY, n * 8);
@@ -907,12 +889,6 @@ int launch_grad(const StacrGradArgs &a, const GPlan &p, char *ws, const size_t *
     f.dbias = a.dbias;
     f.db_dt = a.dbias_dtype;
     if (f.nnz > 0) {
-        uint32_t *rowptr = reinterpret_cast<uint32_t *>(ws + off[GW_ROWPTR]);
-        const int cg = (int)((a.nnz + kBlock - 1) / kBlock);
-        if (a.index_bytes == 8)
-            stacr_launch("k_rowptr", s, [&] { k_rowptr<1><<<cg, kBlock, 0, s>>>(a.idx, a.nnz, a.d_in, a.rows, rowptr); });
-        else
-            stacr_launch("k_rowptr", s, [&] { k_rowptr<0><<<cg, kBlock, 0, s>>>(a.idx, a.nnz, a.d_in, a.rows, rowptr); });
         PlanArgs pa{};
         pa.idx = a.idx;
         pa.data = a.data;
@@ -927,7 +903,6 @@ int launch_grad(const StacrGradArgs &a, const GPlan &p, char *ws, const size_t *
         pa.tb = p.tb;
         pa.round_cap = (uint32_t)p.round_cap;
         pa.max_rounds = (uint32_t)p.max_rounds;
-        pa.rowptr = rowptr;
         pa.groups = (uint32_t)Cfg::NGRP;
         pa.ent = ws + off[GW_ENT];
         pa.task = reinterpret_cast<uint2 *>(ws + off[GW_TASK]);
