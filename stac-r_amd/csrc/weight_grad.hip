@@ -45,6 +45,7 @@ constexpr int kHeavyCap = kMaxGroups;                     // heavy features per 
 constexpr int kTaskCap = kMaxISlab + kSlotCap;            // pieces per round
 constexpr uint32_t kDirect = 0xffffu;                     // piece slot: add straight into S
 constexpr int kTaskPT = (kTaskCap + kBwdThreads - 1) / kBwdThreads;  // staged pieces per thread
+constexpr int kHdrRing = 256;                             // block headers held in LDS
 static_assert(kHeavyCap <= kBwdThreads, "one heavy record per thread");
 
 // S row i holds the 16 outputs as four 16-byte chunks; chunk q sits at position q ^ (i & 3), which
@@ -376,7 +377,8 @@ struct FusedLds {
     static constexpr size_t s_task = s_ent + (size_t)C::ROUND * ent_bytes;           // [kTaskCap]
     static constexpr size_t s_heavy = s_task + (size_t)kTaskCap * 8;                 // [kHeavyCap]
     static constexpr size_t s_slot = s_heavy + (size_t)kHeavyCap * 8;                // [kSlotCap][16]
-    static constexpr size_t end = s_slot + (size_t)kSlotCap * kOSlab * 4;
+    static constexpr size_t s_hdr = s_slot + (size_t)kSlotCap * kOSlab * 4;        // [kHdrRing] BlockHdr
+    static constexpr size_t end = s_hdr + (size_t)kHdrRing * sizeof(BlockHdr);
     static constexpr int NPASS = C::NV > 36 ? 4 : 2;  // M reduction passes (LDS holds NV / NPASS per thread)
     static constexpr int HALF = (C::NV + NPASS - 1) / NPASS;
     static constexpr size_t red_end = s_gtile + ((size_t)kBwdThreads * HALF + (size_t)8 * C::OG * HALF +
@@ -392,7 +394,11 @@ struct Staged {
     uint2 heavy;
 };
 
-template <int DT, int R>
+// FAST: every G and C row access is a whole aligned vector and the slab lies inside d_out, so
+// each load is one unconditional instruction from a clamped row (rows past the matrix are
+// zeroed where the values are used).  A load whose result is merged from divergent paths would
+// be waited for at once; these are waited for only where they are consumed, a block later.
+template <int DT, int R, bool FAST>
 __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
 {
     using C = GradCfg<DT, R>;
@@ -414,6 +420,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
     uint2 *l_heavy = reinterpret_cast<uint2 *>(base + L::s_heavy);
     float *l_slot = reinterpret_cast<float *>(base + L::s_slot);
     float *mred = reinterpret_cast<float *>(base + L::s_gtile);  // reused after the stream
+    BlockHdr *l_hdr = reinterpret_cast<BlockHdr *>(base + L::s_hdr);
 
     // workgroup -> (o-slab, part); consecutive logical ids land on the same XCD (ids are dealt
     // round-robin over 8 XCDs), so the parts of a slab and neighbouring slabs share an L2
@@ -427,7 +434,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
 
     const int og = threadIdx.x % OG, tp = threadIdx.x / OG;
     const int64_t ob = o0 + og * OT;
-    const bool o_ok = ob < a.d_out;
+    const bool o_ok = FAST || ob < a.d_out;
     const bool vec_ok = a.vec_ok != 0;
     const T *g = static_cast<const T *>(a.g);
     const T *coeff = static_cast<const T *>(a.coeff);
@@ -476,13 +483,31 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
     uint32_t wq[GD][2][NW], xq[PD][2][CW];
     auto load_grows = [&](int64_t blk, uint32_t (&w)[2][NW]) {
         const int64_t t = blk * TB + 2 * tp;
-        load_g<DT, VB>(g + t * a.d_out, ob, a.d_out, o_ok && t < a.rows, vec_ok, w[0]);
-        load_g<DT, VB>(g + (t + 1) * a.d_out, ob, a.d_out, o_ok && t + 1 < a.rows, vec_ok, w[1]);
+        if constexpr (FAST) {
+            load_words<VB>(g + min(t, a.rows - 1) * a.d_out + ob, w[0]);
+            load_words<VB>(g + min(t + 1, a.rows - 1) * a.d_out + ob, w[1]);
+        } else {
+            load_g<DT, VB>(g + t * a.d_out, ob, a.d_out, o_ok && t < a.rows, vec_ok, w[0]);
+            load_g<DT, VB>(g + (t + 1) * a.d_out, ob, a.d_out, o_ok && t + 1 < a.rows, vec_ok, w[1]);
+        }
     };
     auto load_crows = [&](int64_t blk, uint32_t (&x)[2][CW]) {
         const int64_t t = blk * TB + 2 * tp;
-        load_c(t, x[0]);
-        load_c(t + 1, x[1]);
+        if constexpr (FAST) {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const char *p = reinterpret_cast<const char *>(coeff + min(t + r, a.rows - 1) * R);
+                if constexpr (CW % 4 == 0) {
+#pragma unroll
+                    for (int k = 0; k < CW / 4; ++k) load_words<16>(p + 16 * k, x[r] + 4 * k);
+                } else {
+                    load_words<8>(p, x[r]);
+                }
+            }
+        } else {
+            load_c(t, x[0]);
+            load_c(t + 1, x[1]);
+        }
     };
 
     // plan data of a round: global -> registers -> LDS (round sizes are bounded by the planner;
@@ -616,29 +641,37 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
     };
 
     const int64_t n_blocks = (a.rows + TB - 1) / TB;
-    auto load_hdr = [&](int64_t blk) {
-        BlockHdr h{};
-        if (sparse && blk < n_blocks) h = a.bhdr[blk * a.n_parts + part];
-        return h;
+    // Block headers live in an LDS ring of kHdrRing blocks (a uniform value loaded from global
+    // memory in the loop would be read into scalar registers, and so waited for, at once).  The
+    // ring starts with blocks [0, kHdrRing); every kHdrRing / 2 blocks the half just finished is
+    // refilled with the blocks kHdrRing / 2 further on.
+    auto hdr_fill = [&](int64_t b0, int64_t count) {
+        for (int64_t i = threadIdx.x; i < count; i += kBwdThreads) {
+            const int64_t b = b0 + i;
+            l_hdr[b % kHdrRing] = (sparse && b < n_blocks) ? a.bhdr[b * a.n_parts + part] : BlockHdr{};
+        }
     };
-    BlockHdr hq[PD + 2];
+    auto read_hdr = [&](int64_t b) { return b < n_blocks ? l_hdr[b % kHdrRing] : BlockHdr{}; };
+    hdr_fill(0, kHdrRing);
+    __syncthreads();
     Stage sq[PD];
 #pragma unroll
     for (int d = 0; d < GD; ++d) load_grows(d, wq[d]);  // rows past the matrix load as zero
 #pragma unroll
     for (int d = 0; d < PD; ++d) load_crows(d, xq[d]);
 #pragma unroll
-    for (int d = 0; d < PD + 2; ++d) hq[d] = load_hdr(d);
-#pragma unroll
-    for (int d = 0; d < PD; ++d)
-        if (hq[d].n_rounds) load_stage(sq[d], hq[d].r0);
+    for (int d = 0; d < PD; ++d) {
+        const BlockHdr h = read_hdr(d);
+        if (h.n_rounds) load_stage(sq[d], h.r0);
+    }
     for (int64_t blk = 0; blk < n_blocks; ++blk) {
         uint32_t ca[NW], cb[NW], ya[CW], yb[CW];
+        const bool ra = !FAST || blk * TB + 2 * tp < a.rows, rb = !FAST || blk * TB + 2 * tp + 1 < a.rows;
 #pragma unroll
-        for (int k = 0; k < NW; ++k) { ca[k] = wq[0][0][k]; cb[k] = wq[0][1][k]; }
+        for (int k = 0; k < NW; ++k) { ca[k] = ra ? wq[0][0][k] : 0u; cb[k] = rb ? wq[0][1][k] : 0u; }
 #pragma unroll
-        for (int k = 0; k < CW; ++k) { ya[k] = xq[0][0][k]; yb[k] = xq[0][1][k]; }
-        const BlockHdr bh = hq[0];
+        for (int k = 0; k < CW; ++k) { ya[k] = ra ? xq[0][0][k] : 0u; yb[k] = rb ? xq[0][1][k] : 0u; }
+        const BlockHdr bh = read_hdr(blk);
         if (sparse) {  // this block's G rows and first round of plan data into LDS
             uint32_t *da = reinterpret_cast<uint32_t *>(gtile + (2 * tp) * kOSlab + og * OT);
             uint32_t *db = reinterpret_cast<uint32_t *>(gtile + (2 * tp + 1) * kOSlab + og * OT);
@@ -693,17 +726,21 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
             for (int k = 0; k < CW; ++k) { xq[d][0][k] = xq[d + 1][0][k]; xq[d][1][k] = xq[d + 1][1][k]; }
             sq[d] = sq[d + 1];
         }
-#pragma unroll
-        for (int d = 0; d + 1 < PD + 2; ++d) hq[d] = hq[d + 1];
         // Loads issue in the order they are consumed: the memory counter retires in issue order,
         // so waiting for the next block's C rows and plan data must not also wait for G rows
-        // that are only needed GD blocks from now.
-        if (blk + PD < n_blocks) {
-            load_crows(blk + PD, xq[PD - 1]);
-            if (hq[PD - 1].n_rounds) load_stage(sq[PD - 1], hq[PD - 1].r0);
+        // that are only needed GD blocks from now.  (FAST loads past the last block re-read the
+        // last rows and are never used.)
+        if (FAST || blk + PD < n_blocks) load_crows(blk + PD, xq[PD - 1]);
+        {
+            const BlockHdr hn = read_hdr(blk + PD);
+            if (hn.n_rounds) load_stage(sq[PD - 1], hn.r0);
         }
-        hq[PD + 1] = load_hdr(blk + PD + 2);
-        if (blk + GD < n_blocks) load_grows(blk + GD, wq[GD - 1]);
+        if (FAST || blk + GD < n_blocks) load_grows(blk + GD, wq[GD - 1]);
+        if (blk % (kHdrRing / 2) == 0 && blk > 0) {  // refill the half of the ring just finished
+            __syncthreads();
+            hdr_fill(blk + kHdrRing / 2, kHdrRing / 2);
+            __syncthreads();
+        }
         if (!sparse || bh.n_rounds == 0) continue;
         __syncthreads();  // G tile and first round staged
         run_round(bh.r0);
@@ -923,8 +960,14 @@ int launch_grad(const StacrGradArgs &a, const GPlan &p, char *ws, const size_t *
     constexpr size_t lds = L::bytes;
     static_assert(lds <= 160 * 1024, "LDS budget");
     const unsigned nwg = (unsigned)(p.n_slabs * p.n_parts);
-    raise_lds_limit(k_dw_fused<DT, R>, lds);
-    stacr_launch("k_dw_fused", s, [&] { k_dw_fused<DT, R><<<nwg, kBwdThreads, lds, s>>>(f); });
+    const bool fast = a.rows > 0 && f.vec_ok && f.c_vec && a.d_out % kOSlab == 0;
+    if (fast) {
+        raise_lds_limit(k_dw_fused<DT, R, true>, lds);
+        stacr_launch("k_dw_fused", s, [&] { k_dw_fused<DT, R, true><<<nwg, kBwdThreads, lds, s>>>(f); });
+    } else {
+        raise_lds_limit(k_dw_fused<DT, R, false>, lds);
+        stacr_launch("k_dw_fused", s, [&] { k_dw_fused<DT, R, false><<<nwg, kBwdThreads, lds, s>>>(f); });
+    }
     return stacr_hip_check(hipGetLastError(), "weight_grad kernels");
 }
 
