@@ -154,8 +154,8 @@ __device__ __forceinline__ uint32_t div_small(uint32_t off, uint32_t d, float in
 struct RoundHdr {
     uint32_t base;
     uint32_t n_ent;
-    uint32_t n_task;
-    uint32_t n_heavy;
+    uint32_t n_task;   // column records + pieces
+    uint32_t n_heavy;  // features cut into several pieces | matrix-core columns << 16
 };
 
 struct BlockHdr {
@@ -174,10 +174,13 @@ struct PlanArgs {
     int tb;                  // token rows per block
     uint32_t round_cap;      // entries per round (<= kRoundMax)
     uint32_t groups;         // piece groups of the streaming kernel
+    uint32_t slot_cap;       // partial-sum slots of the streaming kernel
+    uint32_t cols;           // matrix-core columns per round (0: every feature goes to pieces)
     uint32_t max_rounds;     // rounds the header array holds
     void *ent;               // [nnz] 16-bit G: t_local << 16 | value code (uint32);
                              //       fp32 G: {t_local, value bits} (uint2)
-    uint2 *task;             // [nnz] {feature | slot << 16, entry offset << 8 | entries}
+    uint2 *task;             // [nnz] column features {feature, 0} first, then pieces
+                             //       {feature | slot << 16, entry offset << 8 | entries}
     uint2 *heavy;            // [nnz] {feature | first slot << 16, pieces}
     RoundHdr *rhdr;          // [global round][part]
     BlockHdr *bhdr;          // [block][part]
@@ -207,6 +210,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
 {
     __shared__ uint32_t cnt[kMaxISlab], ccur[kMaxISlab];
     __shared__ uint32_t cstart[kMaxISlab], lstart[kMaxISlab], hstart[kMaxISlab], hidx[kMaxISlab];
+    __shared__ uint32_t colh[kMaxISlab];  // 1 + matrix-core column of a feature, 0 for pieces
     __shared__ uint32_t s_tot[kPlanThreads / 64];
     const int64_t b = blockIdx.x, p = blockIdx.y;
     const int64_t t0 = b * a.tb, t1 = min(t0 + a.tb, a.rows);
@@ -282,18 +286,48 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
         uint32_t n_before;
         block_exclusive_scan<kPlanThreads>(before, s_tot, &n_before);  // also orders the counts
         const uint32_t base = c0 + n_before;
+        const int f0 = 2 * threadIdx.x;
+        const uint32_t n0 = f0 < ni ? cnt[f0] : 0u, n1 = f0 + 1 < ni ? cnt[f0 + 1] : 0u;
+        // Matrix-core columns (cols > 0): the features with the most entries, at most cols of them
+        // and at least 2 entries each; ties at the cut go to the lower feature index.  tau is the
+        // smallest count with #{count >= tau} <= cols; features with tau - 1 entries fill the rest.
+        bool k0 = false, k1 = false;
+        uint32_t n_cols = 0;
+        if (a.cols > 0) {
+            uint32_t lo = 2, hi = (uint32_t)kRoundMax + 1;
+            while (lo < hi) {
+                const uint32_t mid = (lo + hi) / 2;
+                const uint32_t m = (uint32_t)__syncthreads_count(n0 >= mid) + (uint32_t)__syncthreads_count(n1 >= mid);
+                if (m <= a.cols) hi = mid;
+                else lo = mid + 1;
+            }
+            const uint32_t tau = lo;
+            uint32_t n_above, n_tie;
+            (void)block_exclusive_scan<kPlanThreads>((n0 >= tau) + (n1 >= tau), s_tot, &n_above);
+            const bool t0 = tau > 2 && n0 == tau - 1, t1 = tau > 2 && n1 == tau - 1;
+            const uint32_t rt = block_exclusive_scan<kPlanThreads>(t0 + t1, s_tot, &n_tie);
+            const uint32_t room = a.cols - n_above;
+            k0 = n0 >= tau || (t0 && rt < room);
+            k1 = n1 >= tau || (t1 && rt + t0 < room);
+            const uint32_t sc = block_exclusive_scan<kPlanThreads>(k0 + k1, s_tot, &n_cols);
+            if (f0 < ni) colh[f0] = k0 ? sc + 1 : 0u;
+            if (f0 + 1 < ni) colh[f0 + 1] = k1 ? sc + k0 + 1 : 0u;
+        }
         // prefix sums over the features (two per thread): bucket starts; then, with the piece
-        // length fixed by the part's entry count, heavy-piece starts (= partial-sum slots), light
-        // piece positions and heavy-record positions.  Heavy pieces come first in the piece list,
-        // so the longest work starts first.
+        // length fixed by the part's piece-bound entry count, heavy-piece starts (= partial-sum
+        // slots), light piece positions and heavy-record positions.  Heavy pieces come first in the
+        // piece list (after the column records), so the longest work starts first.
         uint32_t piece;
         {
-            const int f0 = 2 * threadIdx.x;
-            const uint32_t n0 = f0 < ni ? cnt[f0] : 0u, n1 = f0 + 1 < ni ? cnt[f0 + 1] : 0u;
-            uint32_t tot_e, tot_h, tot_l, tot_x;
+            const uint32_t m0 = k0 ? 0u : n0, m1 = k1 ? 0u : n1;  // entries that go to pieces
+            uint32_t tot_e, tot_p, tot_h, tot_l, tot_x;
             const uint32_t se = block_exclusive_scan<kPlanThreads>(n0 + n1, s_tot, &tot_e);
-            piece = min(max((tot_e + a.groups - 1) / a.groups, (uint32_t)kMinPiece), 255u);
-            const uint32_t p0 = (n0 + piece - 1) / piece, p1 = (n1 + piece - 1) / piece;
+            (void)block_exclusive_scan<kPlanThreads>(m0 + m1, s_tot, &tot_p);
+            // pieces of heavy features number < 2 tot_p / piece <= slot_cap, and heavy features
+            // < tot_p / piece <= groups
+            piece = max((tot_p + a.groups - 1) / a.groups, (2 * tot_p + a.slot_cap - 1) / a.slot_cap);
+            piece = min(max(piece, (uint32_t)kMinPiece), 255u);
+            const uint32_t p0 = (m0 + piece - 1) / piece, p1 = (m1 + piece - 1) / piece;
             const uint32_t h0 = p0 > 1 ? p0 : 0u, h1 = p1 > 1 ? p1 : 0u;
             const uint32_t l0 = p0 == 1, l1 = p1 == 1;
             const uint32_t sh = block_exclusive_scan<kPlanThreads>(h0 + h1, s_tot, &tot_h);
@@ -301,13 +335,15 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
             const uint32_t sx = block_exclusive_scan<kPlanThreads>((p0 > 1) + (p1 > 1), s_tot, &tot_x);
             if (f0 < ni) {
                 cstart[f0] = se; hstart[f0] = sh; lstart[f0] = tot_h + sl; hidx[f0] = sx;
+                if (a.cols == 0) colh[f0] = 0u;
             }
             if (f0 + 1 < ni) {
                 cstart[f0 + 1] = se + n0; hstart[f0 + 1] = sh + h0; lstart[f0 + 1] = tot_h + sl + l0;
                 hidx[f0 + 1] = sx + (p0 > 1);
+                if (a.cols == 0) colh[f0 + 1] = 0u;
             }
             if (threadIdx.x == 0) {
-                const RoundHdr h{base, tot_e, tot_h + tot_l, tot_x};
+                const RoundHdr h{base, tot_e, n_cols + tot_h + tot_l, tot_x | (n_cols << 16)};
                 a.rhdr[(int64_t)(first + j) * a.n_parts + p] = h;
                 if (j == 0) a.bhdr[b * a.n_parts + p] = BlockHdr{h, first, n_rounds, {0u, 0u}};
             }
@@ -321,18 +357,23 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
                 const uint32_t v = entry_value(a, e);
                 if (f32)
                     static_cast<uint2 *>(a.ent)[pos] = make_uint2(tl[k], v);
-                else
-                    static_cast<uint32_t *>(a.ent)[pos] = (tl[k] << 16) | (v & 0xffffu);
+                else  // a column feature's entries carry 1 + its column in bits 26..30
+                    static_cast<uint32_t *>(a.ent)[pos] = (colh[col[k]] << 26) | (tl[k] << 16) | (v & 0xffffu);
             }
         }
         for (int c = threadIdx.x; c < ni; c += kPlanThreads) {
-            const uint32_t n = cnt[c];
+            const uint32_t n = cnt[c], hc = colh[c];
+            if (hc) {
+                a.task[base + hc - 1] = make_uint2((uint32_t)c, 0u);
+                continue;
+            }
             const uint32_t npc = (n + piece - 1) / piece;
-            if (npc == 1) a.task[base + lstart[c]] = make_uint2((uint32_t)c | (kDirect << 16), (cstart[c] << 8) | n);
+            const uint32_t tb = base + n_cols;  // pieces follow the column records
+            if (npc == 1) a.task[tb + lstart[c]] = make_uint2((uint32_t)c | (kDirect << 16), (cstart[c] << 8) | n);
             if (npc < 2) continue;
             for (uint32_t pc = 0; pc < npc; ++pc) {
                 const uint32_t len = min(piece, n - pc * piece);
-                a.task[base + hstart[c] + pc] =
+                a.task[tb + hstart[c] + pc] =
                     make_uint2((uint32_t)c | ((hstart[c] + pc) << 16), ((cstart[c] + pc * piece) << 8) | len);
             }
             a.heavy[base + hidx[c]] = make_uint2((uint32_t)c | (hstart[c] << 16), npc);
@@ -525,7 +566,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
             const uint32_t e = threadIdx.x + k * kBwdThreads;
             st.task[k] = e < nt ? a.task[h.base + e] : make_uint2(0u, 0u);
         }
-        st.heavy = threadIdx.x < min(h.n_heavy, (uint32_t)kHeavyCap) ? a.heavy[h.base + threadIdx.x]
+        st.heavy = threadIdx.x < min(h.n_heavy & 0xffffu, (uint32_t)kHeavyCap) ? a.heavy[h.base + threadIdx.x]
                                                                      : make_uint2(0u, 0u);
     };
     auto store_stage = [&](const Stage &st) {
@@ -607,7 +648,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
     // Sum the round's pieces (staged in LDS, the G tile complete) into S.  Group g (OG threads)
     // takes pieces g, g + NGRP, g + 2 NGRP, ...
     auto run_round = [&](const RoundHdr &h) {
-        const uint32_t nt = min(h.n_task, (uint32_t)kTaskCap), nh = min(h.n_heavy, (uint32_t)kHeavyCap);
+        const uint32_t nt = min(h.n_task, (uint32_t)kTaskCap), nh = min(h.n_heavy & 0xffffu, (uint32_t)kHeavyCap);
         if (o_ok) {
             for (uint32_t tk = threadIdx.x / OG; tk < nt; tk += NGRP) {
                 const uint2 td = l_task[tk];
@@ -832,6 +873,392 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
             if (o0 + oo < a.d_out) store_any(a.dbias, a.db_dt, o0 + oo, mfin[oo * (R + 1) + R]);
 }
 
+// ------------------------------------------------------------------ the matrix-core streaming pass
+// For 16-bit G, rank 4 or 8 and aligned rows (the FAST conditions): the same plan and the same
+// piece path as k_dw_fused for the light features, while the low-rank product, dbias and each
+// round's column features (the features with the most entries in the block) go through
+// v_mfma_f32_16x16x32 (bf16 / f16 operands, fp32 accumulation):
+//     D[o][j] += sum_t G[t][o] B[t][j],  32 token rows per instruction,
+// with the operands read row-contiguously from LDS copies of the tiles, G transposed (Gt[o][t]) and
+// the B columns (Bt[j][t]):
+//   * fixed tile, columns C[:, 0..R) and a column of ones (its D column is dbias): one instruction
+//     per wave per block (wave w takes rows 32w..32w+31), partial sums kept in registers across
+//     blocks and added over the 16 waves once, in wave order, at the end;
+//   * column tile, up to 16 column features whose integer codes are scattered into a zeroed
+//     Bt tile: wave 0 runs the 16 instructions of a round, adds each column's sums (scaled) into
+//     S, and the tile is zeroed again after the round.
+constexpr int kMCols = 16;            // column features per round
+constexpr int kMTB = 512;             // token rows per block
+constexpr int kMPitch = kMTB + 8;     // elements per Gt / Bt row; Gt element kMTB stays zero
+constexpr int kMSlotCap = 256;        // partial sums of heavy pieces
+constexpr int kMTaskCap = kMaxISlab + kMSlotCap + kMCols;
+constexpr int kMTaskPT = (kMTaskCap + kBwdThreads - 1) / kBwdThreads;
+
+template <int R>
+struct MfmaLds {
+    static constexpr size_t s_acc = 0;                                            // [1024][16] f32
+    static constexpr size_t s_gt = s_acc + (size_t)kMaxISlab * kAccPitch * 4;      // [16][kMPitch]
+    static constexpr size_t s_bc = s_gt + (size_t)kOSlab * kMPitch * 2;            // [R][kMPitch]
+    static constexpr size_t s_bh = s_bc + (size_t)R * kMPitch * 2;                 // [kMCols][kMPitch]
+    static constexpr size_t s_ent = s_bh + (size_t)kMCols * kMPitch * 2;           // [kRoundMax] u32
+    static constexpr size_t s_task = s_ent + (size_t)kRoundMax * 4;                // [kMTaskCap]
+    static constexpr size_t s_heavy = s_task + (size_t)kMTaskCap * 8;              // [kHeavyCap]
+    static constexpr size_t s_slot = s_heavy + (size_t)kHeavyCap * 8;              // [kMSlotCap][16] f32
+    static constexpr size_t s_hdr = s_slot + (size_t)kMSlotCap * kOSlab * 4;       // [kHdrRing]
+    static constexpr size_t bytes = s_hdr + (size_t)kHdrRing * sizeof(BlockHdr);
+    // after the stream, over the tiles: per-wave partial fixed tiles [16][16][16] f32, then M
+    static constexpr size_t s_red = s_gt;
+    static constexpr size_t s_mfin = s_red + (size_t)16 * 256 * 4;
+    static_assert(s_mfin + (size_t)kOSlab * (R + 1) * 4 <= s_ent, "reduction fits the tile region");
+    static_assert(s_gt % 16 == 0 && s_bc % 16 == 0 && s_bh % 16 == 0 && (kMPitch * 2) % 16 == 0,
+                  "16-byte operand rows");
+};
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma_16x16x32(uint4 a, uint4 b, f32x4 c)
+{
+    if constexpr (DT == STACR_DTYPE_BF16) {
+        typedef __attribute__((ext_vector_type(8))) __bf16 v8;
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0, 0);
+    } else {
+        typedef __attribute__((ext_vector_type(8))) _Float16 v8;
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0, 0);
+    }
+}
+
+template <int DT, int R>
+__global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
+{
+    static_assert(DT != STACR_DTYPE_F32 && (R == 4 || R == 8), "16-bit G, rank 4 or 8");
+    using L = MfmaLds<R>;
+    constexpr int OT = 4, OG = kOSlab / OT, TP = kBwdThreads / OG, TB = kMTB;
+    static_assert(2 * TP == TB, "two token rows per thread");
+    constexpr int CQ = R / 4;  // 32-bit words of C a thread loads: columns CQ * 2 * (og >> 1) ..
+    constexpr int ROUND = kRoundMax, EPT = ROUND / kBwdThreads;
+    constexpr int NGRP = kBwdThreads / OG;
+    constexpr uint32_t kOne = DT == STACR_DTYPE_BF16 ? 0x3f80u : 0x3c00u;
+
+    extern __shared__ float lds[];
+    char *base = reinterpret_cast<char *>(lds);
+    float *acc = reinterpret_cast<float *>(base + L::s_acc);
+    uint16_t *gt = reinterpret_cast<uint16_t *>(base + L::s_gt);
+    uint16_t *bc = reinterpret_cast<uint16_t *>(base + L::s_bc);
+    uint16_t *bh = reinterpret_cast<uint16_t *>(base + L::s_bh);
+    uint32_t *l_ent = reinterpret_cast<uint32_t *>(base + L::s_ent);
+    uint2 *l_task = reinterpret_cast<uint2 *>(base + L::s_task);
+    uint2 *l_heavy = reinterpret_cast<uint2 *>(base + L::s_heavy);
+    float *l_slot = reinterpret_cast<float *>(base + L::s_slot);
+    BlockHdr *l_hdr = reinterpret_cast<BlockHdr *>(base + L::s_hdr);
+
+    // workgroup -> (o-slab, part), consecutive logical ids on one XCD (as in k_dw_fused)
+    const int64_t nwg = a.n_slabs * a.n_parts;
+    int64_t lid = blockIdx.x;
+    if (nwg % 8 == 0) lid = (int64_t)(blockIdx.x % 8) * (nwg / 8) + blockIdx.x / 8;
+    const int64_t slab = lid / a.n_parts, part = lid - slab * a.n_parts;
+    const int64_t o0 = slab * kOSlab;
+    const int64_t i0 = part * a.i_span;
+    const int ni = (int)(min(i0 + a.i_span, a.d_in) - i0);
+    const int og = threadIdx.x % OG, tp = threadIdx.x / OG;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t ob = o0 + og * OT;
+    const uint16_t *g = static_cast<const uint16_t *>(a.g);
+    const uint16_t *coeff = static_cast<const uint16_t *>(a.coeff);
+    const bool sparse = a.nnz > 0;
+    const float qscale = (sparse && a.bits) ? a.scale[0] : 1.f;
+
+    for (int i = threadIdx.x; i < ni * kAccPitch; i += kBwdThreads) acc[i] = 0.f;
+    for (int i = threadIdx.x; i < kOSlab * (kMPitch - TB); i += kBwdThreads)
+        gt[(i / (kMPitch - TB)) * kMPitch + TB + i % (kMPitch - TB)] = 0;
+    for (int i = threadIdx.x; i < kMCols * kMPitch / 8; i += kBwdThreads)
+        reinterpret_cast<uint4 *>(bh)[i] = make_uint4(0u, 0u, 0u, 0u);
+
+    const int64_t n_blocks = (a.rows + TB - 1) / TB;
+    auto hdr_fill = [&](int64_t b0, int64_t count) {
+        for (int64_t i = threadIdx.x; i < count; i += kBwdThreads) {
+            const int64_t b = b0 + i;
+            l_hdr[b % kHdrRing] = (sparse && b < n_blocks) ? a.bhdr[b * a.n_parts + part] : BlockHdr{};
+        }
+    };
+    auto read_hdr = [&](int64_t b) { return b < n_blocks ? l_hdr[b % kHdrRing] : BlockHdr{}; };
+
+    // unconditional loads from clamped rows (the rows past the matrix are zeroed where used)
+    auto load_grows = [&](int64_t blk, uint32_t (&w)[2][2]) {
+        const int64_t t = blk * TB + 2 * tp;
+        load_words<8>(g + min(t, a.rows - 1) * a.d_out + ob, w[0]);
+        load_words<8>(g + min(t + 1, a.rows - 1) * a.d_out + ob, w[1]);
+    };
+    // thread (tp, og) loads C row 2 tp + (og & 1), columns [R / 2 (og >> 1), R / 2 (og >> 1) + R / 2)
+    auto load_crow = [&](int64_t blk, uint32_t (&x)[CQ]) {
+        const int64_t t = blk * TB + 2 * tp + (og & 1);
+        load_words<4 * CQ>(coeff + min(t, a.rows - 1) * R + (R / 2) * (og >> 1), x);
+    };
+    struct StageM {
+        uint32_t ent[EPT];
+        uint2 task[kMTaskPT];
+        uint2 heavy;
+    };
+    auto load_stage = [&](StageM &st, const RoundHdr &h) {
+        const uint32_t ne = min(h.n_ent, (uint32_t)ROUND), nt = min(h.n_task, (uint32_t)kMTaskCap);
+        const uint32_t *ge = static_cast<const uint32_t *>(a.ent) + h.base;
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+            const uint32_t e = threadIdx.x + k * kBwdThreads;
+            st.ent[k] = e < ne ? ge[e] : 0u;
+        }
+#pragma unroll
+        for (int k = 0; k < kMTaskPT; ++k) {
+            const uint32_t e = threadIdx.x + k * kBwdThreads;
+            st.task[k] = e < nt ? a.task[h.base + e] : make_uint2(0u, 0u);
+        }
+        st.heavy = threadIdx.x < min(h.n_heavy & 0xffffu, (uint32_t)kHeavyCap) ? a.heavy[h.base + threadIdx.x]
+                                                                               : make_uint2(0u, 0u);
+    };
+    // plan data into LDS, and each column feature's codes into its (zeroed) Bt row
+    auto store_stage = [&](const StageM &st) {
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+            const uint32_t w = st.ent[k];
+            l_ent[threadIdx.x + k * kBwdThreads] = w;
+            const uint32_t hc = w >> 26, t = (w >> 16) & 0x3ffu;
+            if (hc && hc <= (uint32_t)kMCols && t < (uint32_t)TB) bh[(hc - 1) * kMPitch + t] = (uint16_t)w;
+        }
+#pragma unroll
+        for (int k = 0; k < kMTaskPT; ++k)
+            if (threadIdx.x + k * kBwdThreads < kMTaskCap) l_task[threadIdx.x + k * kBwdThreads] = st.task[k];
+        if (threadIdx.x < kHeavyCap) l_heavy[threadIdx.x] = st.heavy;
+    };
+
+    // One piece's entries [e_lo, e_lo + n) into pa (this thread's 4 outputs), G from Gt: four
+    // entries per batch; entries past the piece read the zero column TB with value 0.
+    auto piece_batch = [&](uint32_t e, uint32_t e_lo, uint32_t n, float (&pa)[OT]) {
+        const uint32_t last = e_lo + (n ? n - 1 : 0u);
+        uint32_t w[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t x = l_ent[min(e + u, last) % ROUND];
+            w[u] = e + u < e_lo + n ? x : (uint32_t)TB << 16;
+        }
+        uint32_t gw[4][2];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint16_t *col = gt + (og * OT) * kMPitch + min((w[u] >> 16) & 0x3ffu, (uint32_t)TB);
+            gw[u][0] = (uint32_t)col[0] | ((uint32_t)col[kMPitch] << 16);
+            gw[u][1] = (uint32_t)col[2 * kMPitch] | ((uint32_t)col[3 * kMPitch] << 16);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t vlo = w[u] & 0xffffu, vhi = w[u] << 16;  // (v, 0) and (0, v)
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                pa[2 * k] = dot2<DT>(gw[u][k], vlo, pa[2 * k]);
+                pa[2 * k + 1] = dot2<DT>(gw[u][k], vhi, pa[2 * k + 1]);
+            }
+        }
+    };
+    auto flush = [&](uint2 td, const float (&pa)[OT]) {
+        const uint32_t c = td.x & 0xffffu, slot = td.x >> 16;
+        if (c >= (uint32_t)ni) return;
+        if (slot == kDirect) {
+            float4 *dst = reinterpret_cast<float4 *>(acc + s_index((int)c, og * OT));
+            float4 v = *dst;
+            v.x = fmaf(pa[0], qscale, v.x);
+            v.y = fmaf(pa[1], qscale, v.y);
+            v.z = fmaf(pa[2], qscale, v.z);
+            v.w = fmaf(pa[3], qscale, v.w);
+            *dst = v;
+        } else if (slot < (uint32_t)kMSlotCap) {
+            float *dst = l_slot + slot * kOSlab + og * OT;
+#pragma unroll
+            for (int o = 0; o < OT; ++o) dst[o] = pa[o];
+        }
+    };
+
+    // One round: the column tile (wave 0) and the pieces, then the split features' partial sums.
+    auto run_round = [&](const RoundHdr &h) {
+        const uint32_t ncol = min(h.n_heavy >> 16, (uint32_t)kMCols);
+        const uint32_t nt = min(h.n_task, (uint32_t)kMTaskCap), nh = min(h.n_heavy & 0xffffu, (uint32_t)kHeavyCap);
+        if (wave == 0 && ncol > 0) {
+            const int jj = lane & 15, k8 = 8 * (lane >> 4);
+            f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+            for (int s = 0; s < TB / 32; ++s) {
+                const uint4 av = *reinterpret_cast<const uint4 *>(gt + jj * kMPitch + 32 * s + k8);
+                const uint4 bv = *reinterpret_cast<const uint4 *>(bh + jj * kMPitch + 32 * s + k8);
+                d = mfma_16x16x32<DT>(av, bv, d);
+            }
+            // lane: column jj, outputs 4 (lane / 16) .. + 3
+            if ((uint32_t)jj < ncol) {
+                const uint32_t c = l_task[jj].x & 0xffffu;
+                if (c < (uint32_t)ni) {
+                    float4 *dst = reinterpret_cast<float4 *>(acc + s_index((int)c, 4 * (lane >> 4)));
+                    float4 v = *dst;
+                    v.x = fmaf(d[0], qscale, v.x);
+                    v.y = fmaf(d[1], qscale, v.y);
+                    v.z = fmaf(d[2], qscale, v.z);
+                    v.w = fmaf(d[3], qscale, v.w);
+                    *dst = v;
+                }
+            }
+        }
+        // pieces, group g taking pieces g, g + NGRP, ...; wave 0 (busy with the column tile) has
+        // the groups that come last
+        const uint32_t grp = (uint32_t)(threadIdx.x / OG + NGRP - 64 / OG) % NGRP;
+        for (uint32_t tk = ncol + grp; tk < nt; tk += NGRP) {
+            const uint2 td = l_task[tk];
+            const uint32_t lo = td.y >> 8, n = td.y & 255u;
+            float pa[OT] = {0.f, 0.f, 0.f, 0.f};
+            for (uint32_t k = 0; k < n; k += 4) piece_batch(lo + k, lo, n, pa);
+            flush(td, pa);
+        }
+        __syncthreads();
+        for (uint32_t w = threadIdx.x; w < nh * kOSlab; w += kBwdThreads) {
+            const uint2 hd = l_heavy[w / kOSlab];
+            const uint32_t o = w % kOSlab, c = hd.x & 0xffffu, s0 = hd.x >> 16;
+            if (c < (uint32_t)ni && s0 + hd.y <= (uint32_t)kMSlotCap) {
+                float s8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                uint32_t k = 0;
+                for (; k + 8 <= hd.y; k += 8) {
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) s8[u] += l_slot[(s0 + k + u) * kOSlab + o];
+                }
+                for (; k < hd.y; ++k) s8[0] += l_slot[(s0 + k) * kOSlab + o];
+                const float sum = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
+                acc[s_index((int)c, (int)o)] += sum * qscale;
+            }
+        }
+        for (uint32_t i = threadIdx.x; i < ncol * (kMPitch / 8); i += kBwdThreads)
+            reinterpret_cast<uint4 *>(bh)[i] = make_uint4(0u, 0u, 0u, 0u);
+        __syncthreads();
+    };
+
+    hdr_fill(0, kHdrRing);
+    __syncthreads();
+    uint32_t wq[2][2], xq[CQ];
+    StageM sq;
+    load_grows(0, wq);
+    load_crow(0, xq);
+    {
+        const BlockHdr h = read_hdr(0);
+        if (h.n_rounds) load_stage(sq, h.r0);
+    }
+    f32x4 accf = {0.f, 0.f, 0.f, 0.f};
+    uint32_t *gt32 = reinterpret_cast<uint32_t *>(gt);
+    for (int64_t blk = 0; blk < n_blocks; ++blk) {
+        const bool ra = blk * TB + 2 * tp < a.rows, rb = blk * TB + 2 * tp + 1 < a.rows;
+        const bool rc = (og & 1) ? rb : ra;
+        uint32_t ca[2], cb[2], yc[CQ];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) { ca[k] = ra ? wq[0][k] : 0u; cb[k] = rb ? wq[1][k] : 0u; }
+#pragma unroll
+        for (int k = 0; k < CQ; ++k) yc[k] = rc ? xq[k] : 0u;
+        const BlockHdr bh_ = read_hdr(blk), hn = read_hdr(blk + 1);
+        // Gt[o][t..t+1] = (G[t][o], G[t+1][o]); Bt[j][t..t+1] = (C[t][j], C[t+1][j]) for j = og, og + 4
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            gt32[((og * OT + 2 * k) * kMPitch + 2 * tp) / 2] = __builtin_amdgcn_perm(cb[k], ca[k], 0x05040100u);
+            gt32[((og * OT + 2 * k + 1) * kMPitch + 2 * tp) / 2] = __builtin_amdgcn_perm(cb[k], ca[k], 0x07060302u);
+        }
+        {   // Bt[j][t] = C[t][j] for this thread's row and R / 2 columns
+            const int t = 2 * tp + (og & 1), j0 = (R / 2) * (og >> 1);
+#pragma unroll
+            for (int k = 0; k < CQ; ++k) {
+                bc[(j0 + 2 * k) * kMPitch + t] = (uint16_t)yc[k];
+                bc[(j0 + 2 * k + 1) * kMPitch + t] = (uint16_t)(yc[k] >> 16);
+            }
+        }
+        if (sparse && bh_.n_rounds) store_stage(sq);
+        // next block's loads, in the order they are consumed (past the last block they re-read
+        // the last rows and are never used)
+        load_crow(blk + 1, xq);
+        if (hn.n_rounds) load_stage(sq, hn.r0);
+        load_grows(blk + 1, wq);
+        if (blk % (kHdrRing / 2) == 0 && blk > 0) {
+            __syncthreads();
+            hdr_fill(blk + kHdrRing / 2, kHdrRing / 2);
+        }
+        __syncthreads();  // tiles and the first round staged
+        {   // fixed tile: rows 32 wave .. 32 wave + 31 of the block
+            const int jj = lane & 15, kk = 32 * wave + 8 * (lane >> 4);
+            const uint4 av = *reinterpret_cast<const uint4 *>(gt + jj * kMPitch + kk);
+            uint4 bv = make_uint4(0u, 0u, 0u, 0u);
+            if (jj < R) bv = *reinterpret_cast<const uint4 *>(bc + jj * kMPitch + kk);
+            else if (jj == R) bv = make_uint4(kOne | kOne << 16, kOne | kOne << 16, kOne | kOne << 16, kOne | kOne << 16);
+            accf = mfma_16x16x32<DT>(av, bv, accf);
+        }
+        if (!sparse || bh_.n_rounds == 0) {
+            __syncthreads();  // the next block rewrites the tiles
+            continue;
+        }
+        run_round(bh_.r0);
+        for (uint32_t j = 1; j < bh_.n_rounds; ++j) {  // blocks with more than ROUND entries
+            const RoundHdr h = a.rhdr[(int64_t)(bh_.first_round + j) * a.n_parts + part];
+            StageM tmp;
+            load_stage(tmp, h);
+            store_stage(tmp);
+            __syncthreads();
+            run_round(h);
+        }
+    }
+    __syncthreads();
+
+    // ---- the fixed tile over the 16 waves, in wave order: M[o][j] (j < R), dbias (j = R)
+    float *red = reinterpret_cast<float *>(base + L::s_red);
+    float *mfin = reinterpret_cast<float *>(base + L::s_mfin);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[(wave * 16 + 4 * (lane >> 4) + r) * 16 + (lane & 15)] = accf[r];
+    __syncthreads();
+    for (int t = threadIdx.x; t < kOSlab * (R + 1); t += kBwdThreads) {
+        const int o = t / (R + 1), j = t % (R + 1);
+        float sum = 0.f;
+        for (int w = 0; w < 16; ++w) sum += red[(w * 16 + o) * 16 + j];
+        mfin[o * (R + 1) + j] = sum;
+    }
+    __syncthreads();
+
+    // ---- epilogue: dW tile = M Q^T + S, one rounding to the weight dtype; dbias from M[:, R]
+    const uint16_t *q = static_cast<const uint16_t *>(a.q);
+    const bool vec_out = a.transposed && a.out_vec_ok && o0 + kOSlab <= a.d_out;
+    if (const int ii = threadIdx.x; ii < ni) {
+        const int64_t i = i0 + ii;
+        float qr[R];
+#pragma unroll
+        for (int j = 0; j < R; ++j) qr[j] = Act<DT>::ld(q[i * R + j]);
+        float out[kOSlab];
+#pragma unroll
+        for (int oo = 0; oo < kOSlab; ++oo) {
+            float s = acc[s_index(ii, oo)];
+#pragma unroll
+            for (int j = 0; j < R; ++j) s = fmaf(mfin[oo * (R + 1) + j], qr[j], s);
+            out[oo] = s;
+        }
+        if (vec_out && a.dw_dt != STACR_DTYPE_F32) {
+            const bool bf = a.dw_dt == STACR_DTYPE_BF16;
+            uint32_t wv[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                wv[k] = bf ? (f_to_bf16_bits(out[2 * k]) | (f_to_bf16_bits(out[2 * k + 1]) << 16))
+                           : (f_to_f16_bits(out[2 * k]) | (f_to_f16_bits(out[2 * k + 1]) << 16));
+            uint4 *dst = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.dw) + i * a.d_out + o0);
+            dst[0] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+            dst[1] = make_uint4(wv[4], wv[5], wv[6], wv[7]);
+        } else if (vec_out) {
+            float4 *dst = reinterpret_cast<float4 *>(static_cast<float *>(a.dw) + i * a.d_out + o0);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) dst[k] = make_float4(out[4 * k], out[4 * k + 1], out[4 * k + 2], out[4 * k + 3]);
+        } else {
+#pragma unroll
+            for (int oo = 0; oo < kOSlab; ++oo)
+                if (o0 + oo < a.d_out)
+                    store_any(a.dw, a.dw_dt, a.transposed ? i * a.d_out + o0 + oo : (o0 + oo) * a.d_in + i, out[oo]);
+        }
+    }
+    if (a.dbias && part == 0)
+        for (int oo = threadIdx.x; oo < kOSlab; oo += kBwdThreads)
+            if (o0 + oo < a.d_out) store_any(a.dbias, a.db_dt, o0 + oo, mfin[oo * (R + 1) + R]);
+}
+
 int pad_rank(int rank) { return rank <= 4 ? 4 : rank <= 8 ? 8 : rank <= 16 ? 16 : 32; }
 
 struct CfgInfo {
@@ -925,6 +1352,9 @@ int launch_grad(const StacrGradArgs &a, const GPlan &p, char *ws, const size_t *
     f.dw_dt = a.dw_dtype;
     f.dbias = a.dbias;
     f.db_dt = a.dbias_dtype;
+    const bool fast = a.rows > 0 && f.vec_ok && f.c_vec && a.d_out % kOSlab == 0;
+    constexpr bool kMfmaCfg = DT != STACR_DTYPE_F32 && R <= 8;
+    const bool mfma = kMfmaCfg && fast;  // the matrix-core kernel (its plan has column features)
     if (f.nnz > 0) {
         PlanArgs pa{};
         pa.idx = a.idx;
@@ -941,6 +1371,8 @@ int launch_grad(const StacrGradArgs &a, const GPlan &p, char *ws, const size_t *
         pa.round_cap = (uint32_t)p.round_cap;
         pa.max_rounds = (uint32_t)p.max_rounds;
         pa.groups = (uint32_t)Cfg::NGRP;
+        pa.slot_cap = (uint32_t)(mfma ? kMSlotCap : kSlotCap);
+        pa.cols = mfma ? (uint32_t)kMCols : 0u;
         pa.ent = ws + off[GW_ENT];
         pa.task = reinterpret_cast<uint2 *>(ws + off[GW_TASK]);
         pa.heavy = reinterpret_cast<uint2 *>(ws + off[GW_HEAVY]);
@@ -960,7 +1392,16 @@ int launch_grad(const StacrGradArgs &a, const GPlan &p, char *ws, const size_t *
     constexpr size_t lds = L::bytes;
     static_assert(lds <= 160 * 1024, "LDS budget");
     const unsigned nwg = (unsigned)(p.n_slabs * p.n_parts);
-    const bool fast = a.rows > 0 && f.vec_ok && f.c_vec && a.d_out % kOSlab == 0;
+    if constexpr (kMfmaCfg) {
+        if (mfma) {
+            constexpr size_t ml = MfmaLds<R>::bytes;
+            static_assert(ml <= 160 * 1024, "LDS budget");
+            static_assert(GradCfg<DT, R>::TB == kMTB && GradCfg<DT, R>::ROUND == kRoundMax, "plan geometry");
+            raise_lds_limit(k_dw_fused_mfma<DT, R>, ml);
+            stacr_launch("k_dw_fused", s, [&] { k_dw_fused_mfma<DT, R><<<nwg, kBwdThreads, ml, s>>>(f); });
+            return stacr_hip_check(hipGetLastError(), "weight_grad kernels");
+        }
+    }
     if (fast) {
         raise_lds_limit(k_dw_fused<DT, R, true>, lds);
         stacr_launch("k_dw_fused", s, [&] { k_dw_fused<DT, R, true><<<nwg, kBwdThreads, lds, s>>>(f); });
