@@ -212,6 +212,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
     __shared__ uint32_t cstart[kMaxISlab], lstart[kMaxISlab], hstart[kMaxISlab], hidx[kMaxISlab];
     __shared__ uint32_t colh[kMaxISlab];  // 1 + matrix-core column of a feature, 0 for pieces
     __shared__ uint32_t s_tot[kPlanThreads / 64];
+    __shared__ uint32_t s_probe[2][7][kPlanThreads / 64];  // column search: per-wave counts
     const int64_t b = blockIdx.x, p = blockIdx.y;
     const int64_t t0 = b * a.tb, t1 = min(t0 + a.tb, a.rows);
     const int64_t i0 = p * a.i_span;
@@ -262,13 +263,14 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
         }
         __syncthreads();
         constexpr int EPT = kRoundMax / kPlanThreads;
-        uint32_t col[EPT], tl[EPT];
+        uint32_t col[EPT], tl[EPT], val[EPT];
         uint32_t before = 0;
 #pragma unroll
         for (int k = 0; k < EPT; ++k) {
             col[k] = 0xffffffffu;
             tl[k] = 0u;
             const uint32_t e = c0 + threadIdx.x + k * kPlanThreads;
+            val[k] = entry_value(a, min(e, c1 - 1u));  // loaded with the index, used at the end
             const int64_t off64 = e < c1 ? flat_at<IDX64>(a.idx, e) - t0 * a.d_in : -1;
             if (off64 >= 0 && off64 < span) {
                 const uint32_t off = (uint32_t)off64;  // < 2^25: tb <= 512 rows of < 65536 features
@@ -294,12 +296,34 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
         bool k0 = false, k1 = false;
         uint32_t n_cols = 0;
         if (a.cols > 0) {
+            // 8-way search: seven probes per step, counted by wave ballots, one barrier a step
             uint32_t lo = 2, hi = (uint32_t)kRoundMax + 1;
-            while (lo < hi) {
-                const uint32_t mid = (lo + hi) / 2;
-                const uint32_t m = (uint32_t)__syncthreads_count(n0 >= mid) + (uint32_t)__syncthreads_count(n1 >= mid);
-                if (m <= a.cols) hi = mid;
-                else lo = mid + 1;
+            for (int it = 0; lo < hi; ++it) {
+                const uint32_t span_ = hi - lo;
+                uint32_t pt[7];
+#pragma unroll
+                for (int i = 0; i < 7; ++i) {
+                    pt[i] = lo + (span_ * (uint32_t)(i + 1)) / 8;
+                    const uint32_t m = (uint32_t)__popcll(__ballot(n0 >= pt[i])) + (uint32_t)__popcll(__ballot(n1 >= pt[i]));
+                    if ((threadIdx.x & 63) == 0) s_probe[it & 1][i][threadIdx.x >> 6] = m;
+                }
+                __syncthreads();
+                uint32_t nlo = lo, nhi = hi;
+                bool found = false;
+#pragma unroll
+                for (int i = 0; i < 7; ++i) {
+                    uint32_t m = 0;
+#pragma unroll
+                    for (int w = 0; w < kPlanThreads / 64; ++w) m += s_probe[it & 1][i][w];
+                    if (!found && m <= a.cols) {
+                        nhi = pt[i];
+                        found = true;
+                    } else if (!found) {
+                        nlo = pt[i] + 1;
+                    }
+                }
+                lo = nlo;
+                hi = max(nhi, nlo);
             }
             const uint32_t tau = lo;
             uint32_t n_above, n_tie;
@@ -352,9 +376,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
 #pragma unroll
         for (int k = 0; k < EPT; ++k) {
             if (col[k] != 0xffffffffu) {
-                const uint32_t e = c0 + threadIdx.x + k * kPlanThreads;
                 const uint32_t pos = base + cstart[col[k]] + atomicAdd(&ccur[col[k]], 1u);
-                const uint32_t v = entry_value(a, e);
+                const uint32_t v = val[k];
                 if (f32)
                     static_cast<uint2 *>(a.ent)[pos] = make_uint2(tl[k], v);
                 else  // a column feature's entries carry 1 + its column in bits 26..30
