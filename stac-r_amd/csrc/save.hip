@@ -582,7 +582,7 @@ __device__ __forceinline__ float wave_reduce_scatter64(float (&a)[64])
 // writes them to `coeff`; the later passes load them.  s_c holds [slot][64] floats.
 template <int DT, int R>
 __device__ __forceinline__ void batch_coeff_from_acc(float (&acc)[64], int W, int slot, float *s_part, float *s_c,
-                                                     const int64_t (&rows)[Batch<R>::NB], int64_t row_end, int rank,
+                                                     int64_t base, int rpi, int64_t row_end, int rank,
                                                      typename Act<DT>::T *__restrict__ coeff, float (&c)[64])
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -596,7 +596,8 @@ __device__ __forceinline__ void batch_coeff_from_acc(float (&acc)[64], int W, in
         const float cv = Act<DT>::rnd(tot);
         s_c[slot * 64 + lane] = cv;
         const int i = lane / R, j = lane % R;
-        if (j < rank && rows[i] < row_end) coeff[rows[i] * rank + j] = Act<DT>::st(cv);
+        const int64_t row = base + (int64_t)i * rpi + slot;  // row i of the batch (computed, not indexed)
+        if (j < rank && row < row_end) coeff[row * rank + j] = Act<DT>::st(cv);
     }
     __syncthreads();
     const float4 *src = reinterpret_cast<const float4 *>(s_c + slot * 64);
@@ -666,6 +667,134 @@ __device__ __forceinline__ void batch_rows(const SaveGeom &g, int64_t base, int 
     for (int i = 0; i < Batch<R>::NB; ++i) rows[i] = base + (int64_t)i * g.rpi + slot;
 }
 
+// Fast-path loads are unconditional, from rows and columns clamped into range, and the values
+// outside the workgroup's rows or the matrix's columns are zeroed where they are used: a load
+// whose value is merged from divergent paths is waited for as soon as it is issued, whereas these
+// stay in flight together (histogram words for the selection first, then X, C and the basis) and
+// overlap the selection arithmetic.
+template <int DT, int R, int V, bool LOADC>
+struct FastLoads {
+    using T = typename Act<DT>::T;
+    static constexpr int NB = Batch<R>::NB;
+    static constexpr bool kCVec = LOADC && sizeof(T) * R % 16 == 0;        // whole 16-byte C rows
+    static constexpr int NWC = kCVec ? (int)(sizeof(T) * R / 16) : 1;
+    int64_t rows[NB];
+    uint4 raw[NB];
+    uint4 craw[kCVec ? NB : 1][NWC];
+
+    __device__ __forceinline__ void issue(const SaveGeom &g, int slot, int64_t base, int64_t row_end, int64_t colc,
+                                          const T *__restrict__ x, const T *__restrict__ coeff, bool cvec)
+    {
+        batch_rows<R>(g, base, slot, rows);  // callers issue only when the workgroup has rows (row_end > base)
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+            raw[i] = *reinterpret_cast<const uint4 *>(x + min(rows[i], row_end - 1) * g.d + colc);
+        if (kCVec && coeff && cvec) {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const uint4 *src = reinterpret_cast<const uint4 *>(coeff + min(rows[i], row_end - 1) * R);
+#pragma unroll
+                for (int k = 0; k < NWC; ++k) craw[i][k] = src[k];
+            }
+        }
+    }
+    // vector i as floats (zero outside the rows / columns)
+    __device__ __forceinline__ void x_at(int i, bool live, float (&xv)[V]) const
+    {
+        unpack_raw<DT, V>(live ? raw[i] : make_uint4(0u, 0u, 0u, 0u), xv);
+    }
+    // coefficient row of vector i (the loaded one when cvec, else read now), zero outside the rows
+    __device__ __forceinline__ void coeff_row(int i, const T *__restrict__ coeff, int rank, int64_t row_end,
+                                              bool cvec, float (&c)[R]) const
+    {
+        const bool ok = rows[i] < row_end;
+        if (kCVec && cvec) {
+#pragma unroll
+            for (int k = 0; k < NWC; ++k) {
+                const uint4 w = ok ? craw[kCVec ? i : 0][k] : make_uint4(0u, 0u, 0u, 0u);
+                const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+                if constexpr (sizeof(T) == 4) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) c[4 * k + e] = __uint_as_float(u[e]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) c[8 * k + e] = Act<DT>::ld((T)((u[e / 2] >> (16 * (e & 1))) & 0xffffu));
+                }
+            }
+        } else {
+            load_coeff<DT, R>(coeff, rows[i], rank, ok, c);
+        }
+    }
+};
+
+// Basis rows of this thread's columns from a clamped column (zeroed where the column is outside
+// the matrix, at the first use).
+template <int R, int V>
+__device__ __forceinline__ void basis_issue(const float *__restrict__ qp, int64_t colc, float (&q)[V][R])
+{
+    const float4 *src = reinterpret_cast<const float4 *>(qp + colc * R);
+#pragma unroll
+    for (int k = 0; k < V * R / 4; ++k) {
+        const float4 v = src[k];
+        q[(4 * k) / R][(4 * k) % R] = v.x;
+        q[(4 * k + 1) / R][(4 * k + 1) % R] = v.y;
+        q[(4 * k + 2) / R][(4 * k + 2) % R] = v.z;
+        q[(4 * k + 3) / R][(4 * k + 3) % R] = v.w;
+    }
+}
+template <int R, int V>
+__device__ __forceinline__ void basis_mask(bool col_ok, float (&q)[V][R])
+{
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+#pragma unroll
+        for (int j = 0; j < R; ++j) q[e][j] = col_ok ? q[e][j] : 0.f;
+}
+
+// The bins a thread reads for a block_select, loaded ahead.
+struct HistPre {
+    uint32_t v[kBins / kBlock];
+};
+__device__ __forceinline__ void hist_issue(int lvl, const uint32_t *__restrict__ h, HistPre &p)
+{
+    const int per = kDigitBins[lvl] / kBlock, owner = kBlock - 1 - threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < kBins / kBlock; ++i) p.v[i] = h[owner * per + min(i, per - 1)];
+}
+// block_select on the prefetched bins (same result as block_select on the histogram)
+__device__ SelState block_select_pre(int lvl, const HistPre &p, uint32_t prefix, uint32_t need, uint32_t *s_tot,
+                                     SelState *s_res)
+{
+    const int per = kDigitBins[lvl] / kBlock;
+    const int bits = lvl == 2 ? 9 : 11;
+    const int owner = kBlock - 1 - threadIdx.x;
+    uint32_t local = 0u;
+#pragma unroll
+    for (int i = 0; i < kBins / kBlock; ++i) local += i < per ? p.v[i] : 0u;
+    if (threadIdx.x == 0) *s_res = SelState{prefix << bits, need};
+    uint32_t total;
+    const uint32_t above = block_exclusive_scan(local, s_tot, &total);
+    if (above < need && above + local >= need) {
+        uint32_t run = above;
+        bool found = false;
+#pragma unroll
+        for (int i = kBins / kBlock - 1; i >= 0; --i) {
+            if (i < per && !found) {
+                if (run + p.v[i] >= need) {
+                    *s_res = SelState{(prefix << bits) | (uint32_t)(owner * per + i), need - run};
+                    found = true;
+                } else {
+                    run += p.v[i];
+                }
+            }
+        }
+    }
+    __syncthreads();
+    const SelState r = *s_res;
+    __syncthreads();  // s_res is free again
+    return r;
+}
+
 // Pass 1 (batched): coefficients, first-digit histogram, max key.
 template <int DT, int R, int V>
 __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg, const typename Act<DT>::T *__restrict__ x,
@@ -677,48 +806,47 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg,
     __shared__ uint32_t s_hist[kBins];
     __shared__ __align__(16) float s_part[kWaves * 64];
     __shared__ __align__(16) float s_c[kWaves * 64];
-    for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
+    if (row0 >= row_end) return;  // a trailing workgroup with no rows (uniform)
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
-    const int64_t col = (int64_t)u * V;
+    const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
     const bool col_ok = col < g.d;
-    QCols<R, V, true> qc;
-    qc.init(qp, col, g.d);
+    FastLoads<DT, R, V, false> ld;
+    ld.issue(g, slot, row0, row_end, colc, x, nullptr, false);
+    float q[V][R];
+    basis_issue<R, V>(qp, colc, q);
+    for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
     uint32_t kmax = 0u;
     __syncthreads();
-    for (int64_t base = row0; base < row_end; base += (int64_t)NB * g.rpi) {
-        int64_t rows[NB];
-        batch_rows<R>(g, base, slot, rows);
-        uint4 raw[NB];
-#pragma unroll
-        for (int i = 0; i < NB; ++i) raw[i] = load_raw<DT, V>(x + rows[i] * g.d + col, col_ok && rows[i] < row_end);
+    basis_mask<R, V>(col_ok, q);
+    {   // the workgroup's rows are one batch (the plan sizes them so)
         float c[64];
         if (coeff_in) {
-            batch_coeff_load<DT, R>(coeff_in, g.rank, rows, row_end, fg.c_vec != 0, c);
+            batch_coeff_load<DT, R>(coeff_in, g.rank, ld.rows, row_end, fg.c_vec != 0, c);
         } else {
             float acc[64];
 #pragma unroll
             for (int i = 0; i < NB; ++i) {
                 float xv[V];
-                unpack_raw<DT, V>(raw[i], xv);
+                ld.x_at(i, col_ok && ld.rows[i] < row_end, xv);
 #pragma unroll
                 for (int j = 0; j < R; ++j) {
                     float s = 0.f;
 #pragma unroll
-                    for (int e = 0; e < V; ++e) s = fmaf(xv[e], qc.q[e][j], s);
+                    for (int e = 0; e < V; ++e) s = fmaf(xv[e], q[e][j], s);
                     acc[i * R + j] = s;
                 }
             }
-            batch_coeff_from_acc<DT, R>(acc, fg.W, slot, s_part, s_c, rows, row_end, g.rank, coeff, c);
+            batch_coeff_from_acc<DT, R>(acc, fg.W, slot, s_part, s_c, row0, g.rpi, row_end, g.rank, coeff, c);
         }
-        if (!do_hist) continue;
+        if (!do_hist) return;
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
-            if (!(col_ok && rows[i] < row_end)) continue;
+            if (!(col_ok && ld.rows[i] < row_end)) continue;
             float xv[V], r[V];
-            unpack_raw<DT, V>(raw[i], xv);
-            batch_residual<DT, R, V>(xv, c + i * R, qc.q, r);
+            ld.x_at(i, true, xv);
+            batch_residual<DT, R, V>(xv, c + i * R, q, r);
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -727,7 +855,6 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg,
             }
         }
     }
-    if (!do_hist) return;
     __syncthreads();
     uint32_t *gh = hist + (chunk * 3 + 0) * kBins;
     for (int b = threadIdx.x; b < kBins; b += kBlock)
@@ -735,6 +862,14 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg,
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, off, 64));
     if ((threadIdx.x & 63) == 0 && kmax) atomicMax(maxkey, kmax);
+}
+
+// The previous level's state of the workgroup's chunk (level 0: its k).
+__device__ __forceinline__ SelState prev_state(int lvl, const SelState *__restrict__ state, int64_t chunk,
+                                               int64_t n_chunks, uint32_t k_full, uint32_t k_last)
+{
+    if (lvl == 0) return SelState{0u, chunk == n_chunks - 1 ? k_last : k_full};
+    return state[chunk * 3 + lvl - 1];
 }
 
 // Passes 2 and 3 (batched): histogram of digit `lvl` among keys matching the prefix so far.
@@ -748,35 +883,38 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
 {
     constexpr int NB = Batch<R>::NB;
     __shared__ uint32_t s_hist[kBins];
-    for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
-    int64_t chunk, row0, row_end;
-    wg_rows(g, blockIdx.x, chunk, row0, row_end);
     __shared__ uint32_t s_tot[kWaves];
     __shared__ SelState s_res;
-    const uint32_t prefix = chunk_select(lvl - 1, hist, state, chunk, g.n_chunks, k_full, k_last,
-                                         blockIdx.x % g.wgs_per_chunk == 0, s_tot, &s_res).prefix;
+    int64_t chunk, row0, row_end;
+    wg_rows(g, blockIdx.x, chunk, row0, row_end);
+    const bool has_rows = row0 < row_end;
+    const SelState sp = prev_state(lvl - 1, state, chunk, g.n_chunks, k_full, k_last);
+    HistPre hp;
+    hist_issue(lvl - 1, hist + (chunk * 3 + lvl - 1) * kBins, hp);
+    const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
+    const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
+    const bool col_ok = col < g.d;
+    FastLoads<DT, R, V, true> ld;
+    if (has_rows) ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
+    float q[V][R];
+    basis_issue<R, V>(qp, colc, q);
+    for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
+    // the chunk's first workgroup records the selection for the passes that follow
+    const SelState sel = block_select_pre(lvl - 1, hp, sp.prefix, sp.need, s_tot, &s_res);
+    if (blockIdx.x % g.wgs_per_chunk == 0 && threadIdx.x == 0) state[chunk * 3 + lvl - 1] = sel;
+    if (!has_rows) return;
+    const uint32_t prefix = sel.prefix;
     const int match_shift = kDigitShift[lvl - 1], dshift = kDigitShift[lvl];
     const uint32_t dmask = (uint32_t)kDigitBins[lvl] - 1u;
-    const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
-    const int64_t col = (int64_t)u * V;
-    const bool col_ok = col < g.d;
-    QCols<R, V, true> qc;
-    qc.init(qp, col, g.d);
-    __syncthreads();
-    for (int64_t base = row0; base < row_end; base += (int64_t)NB * g.rpi) {
-        int64_t rows[NB];
-        batch_rows<R>(g, base, slot, rows);
-        uint4 raw[NB];
-#pragma unroll
-        for (int i = 0; i < NB; ++i) raw[i] = load_raw<DT, V>(x + rows[i] * g.d + col, col_ok && rows[i] < row_end);
-        float c[64];
-        batch_coeff_load<DT, R>(coeff, g.rank, rows, row_end, fg.c_vec != 0, c);
+    basis_mask<R, V>(col_ok, q);
+    {   // the workgroup's rows are one batch
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
-            if (!(col_ok && rows[i] < row_end)) continue;
-            float xv[V], r[V];
-            unpack_raw<DT, V>(raw[i], xv);
-            batch_residual<DT, R, V>(xv, c + i * R, qc.q, r);
+            if (!(col_ok && ld.rows[i] < row_end)) continue;
+            float xv[V], r[V], ci[R];
+            ld.x_at(i, true, xv);
+            ld.coeff_row(i, coeff, g.rank, row_end, fg.c_vec != 0, ci);
+            batch_residual<DT, R, V>(xv, ci, q, r);
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -800,31 +938,33 @@ __global__ __launch_bounds__(kBlock) void k_count_b(SaveGeom g, FastGeom fg, con
 {
     constexpr int NB = Batch<R>::NB;
     __shared__ uint32_t s_tot[kWaves];
+    __shared__ SelState s_res;
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
-    __shared__ SelState s_res;
-    const uint32_t T = chunk_select(2, hist, state, chunk, g.n_chunks, k_full, k_last,
-                                    blockIdx.x % g.wgs_per_chunk == 0, s_tot, &s_res).prefix;
+    const bool has_rows = row0 < row_end;
+    const SelState sp = prev_state(2, state, chunk, g.n_chunks, k_full, k_last);
+    HistPre hp;
+    hist_issue(2, hist + (chunk * 3 + 2) * kBins, hp);
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
-    const int64_t col = (int64_t)u * V;
+    const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
     const bool col_ok = col < g.d;
-    QCols<R, V, true> qc;
-    qc.init(qp, col, g.d);
+    FastLoads<DT, R, V, true> ld;
+    if (has_rows) ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
+    float q[V][R];
+    basis_issue<R, V>(qp, colc, q);
+    const SelState sel = block_select_pre(2, hp, sp.prefix, sp.need, s_tot, &s_res);
+    if (blockIdx.x % g.wgs_per_chunk == 0 && threadIdx.x == 0) state[chunk * 3 + 2] = sel;
+    const uint32_t T = sel.prefix;
+    basis_mask<R, V>(col_ok, q);
     uint32_t gt = 0u, eq = 0u;
-    for (int64_t base = row0; base < row_end; base += (int64_t)NB * g.rpi) {
-        int64_t rows[NB];
-        batch_rows<R>(g, base, slot, rows);
-        uint4 raw[NB];
-#pragma unroll
-        for (int i = 0; i < NB; ++i) raw[i] = load_raw<DT, V>(x + rows[i] * g.d + col, col_ok && rows[i] < row_end);
-        float c[64];
-        batch_coeff_load<DT, R>(coeff, g.rank, rows, row_end, fg.c_vec != 0, c);
+    if (has_rows) {  // the workgroup's rows are one batch; a workgroup with none only reports zeros
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
-            if (!(col_ok && rows[i] < row_end)) continue;
-            float xv[V], r[V];
-            unpack_raw<DT, V>(raw[i], xv);
-            batch_residual<DT, R, V>(xv, c + i * R, qc.q, r);
+            if (!(col_ok && ld.rows[i] < row_end)) continue;
+            float xv[V], r[V], ci[R];
+            ld.x_at(i, true, xv);
+            ld.coeff_row(i, coeff, g.rank, row_end, fg.c_vec != 0, ci);
+            batch_residual<DT, R, V>(xv, ci, q, r);
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -851,39 +991,67 @@ __global__ __launch_bounds__(kBlock) void k_emit_b(SaveGeom g, FastGeom fg, cons
 {
     constexpr int NB = Batch<R>::NB;
     __shared__ uint32_t s_wt[kWaves * NB];
+    __shared__ uint32_t s_off[kWaves];
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
-    const uint32_t T = state[chunk * 3 + 2].prefix;
-    __shared__ uint32_t s_off[kWaves];
-    const WgOffset wo = wg_offset(counts, chunk, blockIdx.x - chunk * g.wgs_per_chunk, g.wgs_per_chunk,
-                                  state[chunk * 3 + 2].need, chunk_k, s_off);
-    const float amax = Act<DT>::rnd(__uint_as_float(*maxkey));
-    const float scale = o.bits ? quant_scale(*maxkey, o.bits, amax) : 1.f;
-    if (!to_list && blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
+    const SelState st = state[chunk * 3 + 2];
+    const uint32_t mk = *maxkey;
+    const int64_t w = blockIdx.x - chunk * g.wgs_per_chunk;
+    // counts of the chunk's earlier workgroups (at most two per thread in the usual geometry;
+    // wg_offset reads any further ones itself)
+    WgCount pre[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int64_t v = threadIdx.x + k * kBlock;
+        pre[k] = counts[chunk * g.wgs_per_chunk + min(v, w)];
+    }
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t col = (int64_t)u * V;
+    const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
     const bool col_ok = col < g.d;
-    QCols<R, V, true> qc;
-    qc.init(qp, col, g.d);
-    uint32_t carry = 0u;  // survivors (gt | eq << 16) of the workgroup's earlier batches
-    for (int64_t base = row0; base < row_end; base += (int64_t)NB * g.rpi) {
-        int64_t rows[NB];
-        batch_rows<R>(g, base, slot, rows);
-        uint4 raw[NB];
+    const bool has_rows = row0 < row_end;
+    FastLoads<DT, R, V, true> ld;
+    if (has_rows) ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
+    float q[V][R];
+    basis_issue<R, V>(qp, colc, q);
+    // the workgroup's output offset and tie budget (as wg_offset)
+    WgOffset wo;
+    {
+        uint32_t gt = 0u, eq = 0u;
 #pragma unroll
-        for (int i = 0; i < NB; ++i) raw[i] = load_raw<DT, V>(x + rows[i] * g.d + col, col_ok && rows[i] < row_end);
-        float c[64];
-        batch_coeff_load<DT, R>(coeff, g.rank, rows, row_end, fg.c_vec != 0, c);
+        for (int k = 0; k < 2; ++k) {
+            const int64_t v = threadIdx.x + k * kBlock;
+            gt += v < w ? pre[k].gt : 0u;
+            eq += v < w ? pre[k].eq : 0u;
+        }
+        for (int64_t v = threadIdx.x + 2 * kBlock; v < w; v += kBlock) {
+            const WgCount c = counts[chunk * g.wgs_per_chunk + v];
+            gt += c.gt;
+            eq += c.eq;
+        }
+        const uint32_t gt_before = block_sum(gt, s_off);
+        const uint32_t eq_before = block_sum(eq, s_off);
+        const WgCount mine = counts[chunk * g.wgs_per_chunk + w];
+        const uint32_t take = eq_before >= st.need ? 0u : min(mine.eq, st.need - eq_before);
+        wo = WgOffset{(uint32_t)chunk * chunk_k + gt_before + min(st.need, eq_before), take};
+    }
+    const uint32_t T = st.prefix;
+    const float amax = Act<DT>::rnd(__uint_as_float(mk));
+    const float scale = o.bits ? quant_scale(mk, o.bits, amax) : 1.f;
+    if (!to_list && blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
+    if (!has_rows) return;
+    basis_mask<R, V>(col_ok, q);
+    {   // the workgroup's rows are one batch
         float r[NB][V];
         uint32_t cnt[NB], incl[NB];
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             cnt[i] = 0u;
-            const bool live = col_ok && rows[i] < row_end;
-            float xv[V];
-            unpack_raw<DT, V>(raw[i], xv);
-            batch_residual<DT, R, V>(xv, c + i * R, qc.q, r[i]);
+            const bool live = col_ok && ld.rows[i] < row_end;
+            float xv[V], ci[R];
+            ld.x_at(i, live, xv);
+            ld.coeff_row(i, coeff, g.rank, row_end, fg.c_vec != 0, ci);
+            batch_residual<DT, R, V>(xv, ci, q, r[i]);
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const uint32_t key = __float_as_uint(r[i][e]) & 0x7fffffffu;
@@ -904,14 +1072,14 @@ __global__ __launch_bounds__(kBlock) void k_emit_b(SaveGeom g, FastGeom fg, cons
 #pragma unroll
             for (int i = 0; i < NB; ++i) s_wt[wave * NB + i] = incl[i];
         __syncthreads();
-        uint32_t before_iter = carry;  // survivors of the batch's earlier iterations (all waves)
+        uint32_t before_iter = 0u;  // survivors of the batch's earlier iterations (all waves)
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             uint32_t waves_before = 0u, iter_total = 0u;
 #pragma unroll
-            for (int w = 0; w < kWaves; ++w) {
-                const uint32_t t = s_wt[w * NB + i];
-                waves_before += w < wave ? t : 0u;
+            for (int wv = 0; wv < kWaves; ++wv) {
+                const uint32_t t = s_wt[wv * NB + i];
+                waves_before += wv < wave ? t : 0u;
                 iter_total += t;
             }
             const uint32_t ex = before_iter + waves_before + incl[i] - cnt[i];
@@ -923,7 +1091,7 @@ __global__ __launch_bounds__(kBlock) void k_emit_b(SaveGeom g, FastGeom fg, cons
                     const bool is_gt = key > T, is_eq = key == T;
                     if (is_gt || (is_eq && eb < wo.take)) {
                         const uint32_t pos = wo.off + gb + min(eb, wo.take);
-                        const uint32_t flat = (uint32_t)(rows[i] * g.d + col + e);
+                        const uint32_t flat = (uint32_t)(ld.rows[i] * g.d + col + e);
                         if (pos >= o.cap) {
                             // unreachable when the counts are consistent; never write out of bounds
                         } else if (to_list) {
@@ -939,8 +1107,6 @@ __global__ __launch_bounds__(kBlock) void k_emit_b(SaveGeom g, FastGeom fg, cons
             }
             before_iter += iter_total;
         }
-        carry = before_iter;
-        __syncthreads();  // s_wt is rewritten by the next batch
     }
 }
 
@@ -1093,6 +1259,7 @@ struct Plan {
     SaveGeom g;
     int V, R;
     bool qreg;
+    bool fast;  // the batched kernels (one batch per workgroup)
     int64_t n_wgs;
     bool trim;
     int64_t n_list_blocks;
@@ -1122,10 +1289,14 @@ Plan make_plan(const StacrSaveArgs &a)
     while (rpw * 2 <= target) rpw *= 2;
     if (a.mode != STACR_MODE_GLOBAL_TOPK)
         while (rpw > 1 && g.chunk_rows % rpw) rpw >>= 1;
+    p.qreg = g.mv == 1 && p.V * p.R <= 128;
+    // the batched kernels take exactly one batch (64 / R iterations of the row slots) per workgroup
+    const int vec_full = a.dtype == STACR_DTYPE_F32 ? 4 : 8;
+    p.fast = p.qreg && p.V == vec_full && p.V * p.R <= 64 && g.mv == 1 && g.L >= 64;
+    if (p.fast) rpw = hmin<int64_t>(rpw, (int64_t)(64 / p.R) * g.rpi);
     g.rows_per_wg = rpw;
     g.wgs_per_chunk = (g.chunk_rows + rpw - 1) / rpw;
     p.n_wgs = g.n_chunks * g.wgs_per_chunk;
-    p.qreg = g.mv == 1 && p.V * p.R <= 128;
     p.trim = a.k_sum > a.k_total;
     p.n_list_blocks = (a.k_sum + kListBlock - 1) / kListBlock;
     return p;
@@ -1182,7 +1353,7 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     });
     // batched fast path: one aligned vector per thread per row, basis columns in registers
     constexpr bool kFastOk = QREG && V == Act<DT>::kVec && V * R <= 64;
-    const bool fast = kFastOk && p.g.mv == 1 && p.g.L >= 64;
+    const bool fast = kFastOk && p.fast;
     FastGeom fg{p.g.L / 64, a.rank == R && ((uintptr_t)coeff % 16) == 0};
     if (!coeff_in || resid) {
         if constexpr (kFastOk) {
