@@ -380,7 +380,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
                 const uint32_t v = val[k];
                 if (f32)
                     static_cast<uint2 *>(a.ent)[pos] = make_uint2(tl[k], v);
-                else  // a column feature's entries carry 1 + its column in bits 26..30
+                else  // a column feature's entries carry 1 + its column in bits 26..31
                     static_cast<uint32_t *>(a.ent)[pos] = (colh[col[k]] << 26) | (tl[k] << 16) | (v & 0xffffu);
             }
         }
@@ -907,13 +907,14 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
 //   * fixed tile, columns C[:, 0..R) and a column of ones (its D column is dbias): one instruction
 //     per wave per block (wave w takes rows 32w..32w+31), partial sums kept in registers across
 //     blocks and added over the 16 waves once, in wave order, at the end;
-//   * column tile, up to 16 column features whose integer codes are scattered into a zeroed
-//     Bt tile: wave 0 runs the 16 instructions of a round, adds each column's sums (scaled) into
-//     S, and the tile is zeroed again after the round.
-constexpr int kMCols = 16;            // column features per round
+//   * column tiles, up to 32 column features whose integer codes are scattered into a zeroed
+//     Bt tile: waves 0 and 1 each run the 16 instructions of one 16-column tile per round, add
+//     each column's sums (scaled) into S, and the tile is zeroed again after the round.
+constexpr int kMCols = 32;            // column features per round (two 16-column tiles)
 constexpr int kMTB = 512;             // token rows per block
 constexpr int kMPitch = kMTB + 8;     // elements per Gt / Bt row; Gt element kMTB stays zero
-constexpr int kMSlotCap = 256;        // partial sums of heavy pieces
+constexpr int kMSlotCap = 64;         // partial sums of heavy pieces
+constexpr int kMHdrRing = 64;         // block headers held in LDS
 constexpr int kMTaskCap = kMaxISlab + kMSlotCap + kMCols;
 constexpr int kMTaskPT = (kMTaskCap + kBwdThreads - 1) / kBwdThreads;
 
@@ -927,8 +928,8 @@ struct MfmaLds {
     static constexpr size_t s_task = s_ent + (size_t)kRoundMax * 4;                // [kMTaskCap]
     static constexpr size_t s_heavy = s_task + (size_t)kMTaskCap * 8;              // [kHeavyCap]
     static constexpr size_t s_slot = s_heavy + (size_t)kHeavyCap * 8;              // [kMSlotCap][16] f32
-    static constexpr size_t s_hdr = s_slot + (size_t)kMSlotCap * kOSlab * 4;       // [kHdrRing]
-    static constexpr size_t bytes = s_hdr + (size_t)kHdrRing * sizeof(BlockHdr);
+    static constexpr size_t s_hdr = s_slot + (size_t)kMSlotCap * kOSlab * 4;       // [kMHdrRing]
+    static constexpr size_t bytes = s_hdr + (size_t)kMHdrRing * sizeof(BlockHdr);
     // after the stream, over the tiles: per-wave partial fixed tiles [16][16][16] f32, then M
     static constexpr size_t s_red = s_gt;
     static constexpr size_t s_mfin = s_red + (size_t)16 * 256 * 4;
@@ -1001,10 +1002,10 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
     auto hdr_fill = [&](int64_t b0, int64_t count) {
         for (int64_t i = threadIdx.x; i < count; i += kBwdThreads) {
             const int64_t b = b0 + i;
-            l_hdr[b % kHdrRing] = (sparse && b < n_blocks) ? a.bhdr[b * a.n_parts + part] : BlockHdr{};
+            l_hdr[b % kMHdrRing] = (sparse && b < n_blocks) ? a.bhdr[b * a.n_parts + part] : BlockHdr{};
         }
     };
-    auto read_hdr = [&](int64_t b) { return b < n_blocks ? l_hdr[b % kHdrRing] : BlockHdr{}; };
+    auto read_hdr = [&](int64_t b) { return b < n_blocks ? l_hdr[b % kMHdrRing] : BlockHdr{}; };
 
     // unconditional loads from clamped rows (the rows past the matrix are zeroed where used)
     auto load_grows = [&](int64_t blk, uint32_t (&w)[2][2]) {
@@ -1102,18 +1103,18 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
     auto run_round = [&](const RoundHdr &h) {
         const uint32_t ncol = min(h.n_heavy >> 16, (uint32_t)kMCols);
         const uint32_t nt = min(h.n_task, (uint32_t)kMTaskCap), nh = min(h.n_heavy & 0xffffu, (uint32_t)kHeavyCap);
-        if (wave == 0 && ncol > 0) {
-            const int jj = lane & 15, k8 = 8 * (lane >> 4);
+        if (wave < kMCols / 16 && ncol > (uint32_t)(16 * wave)) {  // wave w: columns 16 w .. 16 w + 15
+            const int jj = lane & 15, k8 = 8 * (lane >> 4), cj = 16 * wave + jj;
             f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
             for (int s = 0; s < TB / 32; ++s) {
                 const uint4 av = *reinterpret_cast<const uint4 *>(gt + jj * kMPitch + 32 * s + k8);
-                const uint4 bv = *reinterpret_cast<const uint4 *>(bh + jj * kMPitch + 32 * s + k8);
+                const uint4 bv = *reinterpret_cast<const uint4 *>(bh + cj * kMPitch + 32 * s + k8);
                 d = mfma_16x16x32<DT>(av, bv, d);
             }
-            // lane: column jj, outputs 4 (lane / 16) .. + 3
-            if ((uint32_t)jj < ncol) {
-                const uint32_t c = l_task[jj].x & 0xffffu;
+            // lane: column cj, outputs 4 (lane / 16) .. + 3
+            if ((uint32_t)cj < ncol) {
+                const uint32_t c = l_task[cj].x & 0xffffu;
                 if (c < (uint32_t)ni) {
                     float4 *dst = reinterpret_cast<float4 *>(acc + s_index((int)c, 4 * (lane >> 4)));
                     float4 v = *dst;
@@ -1125,9 +1126,9 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
                 }
             }
         }
-        // pieces, group g taking pieces g, g + NGRP, ...; wave 0 (busy with the column tile) has
-        // the groups that come last
-        const uint32_t grp = (uint32_t)(threadIdx.x / OG + NGRP - 64 / OG) % NGRP;
+        // pieces, group g taking pieces g, g + NGRP, ...; waves 0 and 1 (busy with the column
+        // tiles) have the groups that come last
+        const uint32_t grp = (uint32_t)(threadIdx.x / OG + NGRP - (kMCols / 16) * 64 / OG) % NGRP;
         for (uint32_t tk = ncol + grp; tk < nt; tk += NGRP) {
             const uint2 td = l_task[tk];
             const uint32_t lo = td.y >> 8, n = td.y & 255u;
@@ -1156,7 +1157,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
         __syncthreads();
     };
 
-    hdr_fill(0, kHdrRing);
+    hdr_fill(0, kMHdrRing);
     __syncthreads();
     uint32_t wq[2][2], xq[CQ];
     StageM sq;
@@ -1197,9 +1198,9 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
         load_crow(blk + 1, xq);
         if (hn.n_rounds) load_stage(sq, hn.r0);
         load_grows(blk + 1, wq);
-        if (blk % (kHdrRing / 2) == 0 && blk > 0) {
+        if (blk % (kMHdrRing / 2) == 0 && blk > 0) {
             __syncthreads();
-            hdr_fill(blk + kHdrRing / 2, kHdrRing / 2);
+            hdr_fill(blk + kMHdrRing / 2, kMHdrRing / 2);
         }
         __syncthreads();  // tiles and the first round staged
         {   // fixed tile: rows 32 wave .. 32 wave + 31 of the block
