@@ -27,6 +27,9 @@ FLAGS = [
     "-ffp-contract=off",
     # packed fp32 instructions stay off on this hardware pool
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # with them off, the SLP vectorizer's two-wide fp32 operations have nothing to lower to (the
+    # gfx950 backend fails to select a v2f32 negate in one of the save kernels)
+    "-fno-slp-vectorize",
     "-Wall",
     "-Wno-unused-function",
     "-I", os.path.join(ROOT, "include"),

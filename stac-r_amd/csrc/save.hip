@@ -168,10 +168,13 @@ __global__ void k_prep(const typename Act<DT>::T *__restrict__ q, int64_t d, int
 {
     const int64_t n = d * R;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    float *qpt = qp + n;  // the same values transposed, [R][d]: the batched passes read it per rank
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
         const int64_t row = i / R;
         const int j = (int)(i - row * R);
-        qp[i] = j < rank ? Act<DT>::ld(q[row * rank + j]) : 0.f;
+        const float v = j < rank ? Act<DT>::ld(q[row * rank + j]) : 0.f;
+        qp[i] = v;
+        qpt[j * d + row] = v;
     }
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_zero; i += step) zero[i] = 0u;
 }
@@ -727,19 +730,22 @@ struct FastLoads {
     }
 };
 
-// Basis rows of this thread's columns from a clamped column (zeroed where the column is outside
-// the matrix, at the first use).
+// Basis values of this thread's columns from a clamped column (zeroed where the column is outside
+// the matrix, at the first use), read from the transposed copy qpt[j][col]: per rank, the lanes of
+// a wave read consecutive 16- or 32-byte pieces of one row, not 256-byte-strided blocks.
 template <int R, int V>
-__device__ __forceinline__ void basis_issue(const float *__restrict__ qp, int64_t colc, float (&q)[V][R])
+__device__ __forceinline__ void basis_issue(const float *__restrict__ qpt, int64_t d, int64_t colc, float (&q)[V][R])
 {
-    const float4 *src = reinterpret_cast<const float4 *>(qp + colc * R);
 #pragma unroll
-    for (int k = 0; k < V * R / 4; ++k) {
-        const float4 v = src[k];
-        q[(4 * k) / R][(4 * k) % R] = v.x;
-        q[(4 * k + 1) / R][(4 * k + 1) % R] = v.y;
-        q[(4 * k + 2) / R][(4 * k + 2) % R] = v.z;
-        q[(4 * k + 3) / R][(4 * k + 3) % R] = v.w;
+    for (int j = 0; j < R; ++j) {
+#pragma unroll
+        for (int h = 0; h < V / 4; ++h) {
+            const float4 v = *reinterpret_cast<const float4 *>(qpt + j * d + colc + 4 * h);
+            q[4 * h][j] = v.x;
+            q[4 * h + 1][j] = v.y;
+            q[4 * h + 2][j] = v.z;
+            q[4 * h + 3][j] = v.w;
+        }
     }
 }
 template <int R, int V>
@@ -755,11 +761,22 @@ __device__ __forceinline__ void basis_mask(bool col_ok, float (&q)[V][R])
 struct HistPre {
     uint32_t v[kBins / kBlock];
 };
-__device__ __forceinline__ void hist_issue(int lvl, const uint32_t *__restrict__ h, HistPre &p)
+template <int PER>  // bins per thread: 8 for the 11-bit levels, 2 for the last
+__device__ __forceinline__ void hist_issue(const uint32_t *__restrict__ h, HistPre &p)
 {
-    const int per = kDigitBins[lvl] / kBlock, owner = kBlock - 1 - threadIdx.x;
+    const int owner = kBlock - 1 - threadIdx.x;
+    if constexpr (PER == 8) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(h + owner * 8);
+        const uint4 a = src[0], b = src[1];
+        p.v[0] = a.x; p.v[1] = a.y; p.v[2] = a.z; p.v[3] = a.w;
+        p.v[4] = b.x; p.v[5] = b.y; p.v[6] = b.z; p.v[7] = b.w;
+    } else {
+        static_assert(PER == 2, "level bins per thread");
+        const uint2 a = *reinterpret_cast<const uint2 *>(h + owner * 2);
+        p.v[0] = a.x; p.v[1] = a.y;
 #pragma unroll
-    for (int i = 0; i < kBins / kBlock; ++i) p.v[i] = h[owner * per + min(i, per - 1)];
+        for (int i = 2; i < kBins / kBlock; ++i) p.v[i] = 0u;
+    }
 }
 // block_select on the prefetched bins (same result as block_select on the histogram)
 __device__ SelState block_select_pre(int lvl, const HistPre &p, uint32_t prefix, uint32_t need, uint32_t *s_tot,
@@ -815,7 +832,7 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg,
     FastLoads<DT, R, V, false> ld;
     ld.issue(g, slot, row0, row_end, colc, x, nullptr, false);
     float q[V][R];
-    basis_issue<R, V>(qp, colc, q);
+    basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
     for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
     uint32_t kmax = 0u;
     __syncthreads();
@@ -890,14 +907,15 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
     const bool has_rows = row0 < row_end;
     const SelState sp = prev_state(lvl - 1, state, chunk, g.n_chunks, k_full, k_last);
     HistPre hp;
-    hist_issue(lvl - 1, hist + (chunk * 3 + lvl - 1) * kBins, hp);
+    static_assert(kDigitBins[0] / kBlock == 8 && kDigitBins[1] / kBlock == 8 && kDigitBins[2] / kBlock == 2, "bins per thread");
+    hist_issue<8>(hist + (chunk * 3 + lvl - 1) * kBins, hp);
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
     const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
     const bool col_ok = col < g.d;
     FastLoads<DT, R, V, true> ld;
     if (has_rows) ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
     float q[V][R];
-    basis_issue<R, V>(qp, colc, q);
+    basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
     for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
     // the chunk's first workgroup records the selection for the passes that follow
     const SelState sel = block_select_pre(lvl - 1, hp, sp.prefix, sp.need, s_tot, &s_res);
@@ -944,14 +962,14 @@ __global__ __launch_bounds__(kBlock) void k_count_b(SaveGeom g, FastGeom fg, con
     const bool has_rows = row0 < row_end;
     const SelState sp = prev_state(2, state, chunk, g.n_chunks, k_full, k_last);
     HistPre hp;
-    hist_issue(2, hist + (chunk * 3 + 2) * kBins, hp);
+    hist_issue<2>(hist + (chunk * 3 + 2) * kBins, hp);
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
     const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
     const bool col_ok = col < g.d;
     FastLoads<DT, R, V, true> ld;
     if (has_rows) ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
     float q[V][R];
-    basis_issue<R, V>(qp, colc, q);
+    basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
     const SelState sel = block_select_pre(2, hp, sp.prefix, sp.need, s_tot, &s_res);
     if (blockIdx.x % g.wgs_per_chunk == 0 && threadIdx.x == 0) state[chunk * 3 + 2] = sel;
     const uint32_t T = sel.prefix;
@@ -1013,7 +1031,7 @@ __global__ __launch_bounds__(kBlock) void k_emit_b(SaveGeom g, FastGeom fg, cons
     FastLoads<DT, R, V, true> ld;
     if (has_rows) ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
     float q[V][R];
-    basis_issue<R, V>(qp, colc, q);
+    basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
     // the workgroup's output offset and tie budget (as wg_offset)
     WgOffset wo;
     {
@@ -1311,7 +1329,7 @@ size_t layout(const StacrSaveArgs &a, const Plan &p, size_t *off)
 {
     size_t cur = 0;
     auto take = [&](int slot, size_t bytes) { off[slot] = cur; cur += (bytes + 255) & ~(size_t)255; };
-    take(WS_QP, (size_t)a.feats * p.R * sizeof(float));
+    take(WS_QP, 2 * (size_t)a.feats * p.R * sizeof(float));  // padded basis, then transposed
     take(WS_HIST, (size_t)p.g.n_chunks * 3 * kBins * sizeof(uint32_t));
     take(WS_MAXKEY, sizeof(uint32_t));
     take(WS_STATE, (size_t)p.g.n_chunks * 3 * sizeof(SelState));
