@@ -1000,7 +1000,7 @@ __global__ __launch_bounds__(kBlock) void k_count_b(SaveGeom g, FastGeom fg, con
 // which is ascending flat index: one multi-value block scan per batch gives every thread the
 // number of survivors (gt in the low half, ties in the high half) before each of its vectors.
 template <int DT, int R, int V>
-__global__ __launch_bounds__(kBlock) void k_emit_b(SaveGeom g, FastGeom fg, const typename Act<DT>::T *__restrict__ x,
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) void k_emit_b(SaveGeom g, FastGeom fg, const typename Act<DT>::T *__restrict__ x,
                                                    const float *__restrict__ qp,
                                                    const typename Act<DT>::T *__restrict__ coeff,
                                                    const SelState *__restrict__ state, const WgCount *__restrict__ counts, uint32_t chunk_k,
