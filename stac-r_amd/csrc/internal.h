@@ -152,6 +152,10 @@ struct SaveGeom {
     int64_t wgs_per_chunk;  // uniform; trailing workgroups of the last chunk may be empty
     int L, log2L, rpi, mv;
     int rank;
+    // copies of each chunk histogram level and of the max key (batched passes): workgroup w adds
+    // into copy w % hcopies, and readers sum the copies.  Device-scope atomics from hundreds of
+    // workgroups on one address serialize; eight copies cut that to a few tens per address.
+    int hcopies;
 };
 
 // Per-chunk selection state after each radix level: prefix of the key found so far and the

@@ -18,6 +18,9 @@ using namespace stacr;
 
 namespace {
 
+constexpr int kHistCopies = 8;     // histogram / max-key copies of a chunk with many workgroups
+constexpr int kMaxKeyStride = 32;  // max-key copies 128 bytes apart
+
 __device__ __forceinline__ void wg_rows(const SaveGeom &g, int64_t wg, int64_t &chunk, int64_t &row0,
                                         int64_t &row_end)
 {
@@ -761,19 +764,35 @@ __device__ __forceinline__ void basis_mask(bool col_ok, float (&q)[V][R])
 struct HistPre {
     uint32_t v[kBins / kBlock];
 };
-template <int PER>  // bins per thread: 8 for the 11-bit levels, 2 for the last
+// PER: bins per thread, 8 for the 11-bit levels, 2 for the last.  HC: histogram copies (kBins
+// apart) summed on the way in.
+template <int PER, int HC>
 __device__ __forceinline__ void hist_issue(const uint32_t *__restrict__ h, HistPre &p)
 {
     const int owner = kBlock - 1 - threadIdx.x;
     if constexpr (PER == 8) {
-        const uint4 *src = reinterpret_cast<const uint4 *>(h + owner * 8);
-        const uint4 a = src[0], b = src[1];
-        p.v[0] = a.x; p.v[1] = a.y; p.v[2] = a.z; p.v[3] = a.w;
-        p.v[4] = b.x; p.v[5] = b.y; p.v[6] = b.z; p.v[7] = b.w;
+        uint4 a[HC], b[HC];
+#pragma unroll
+        for (int c = 0; c < HC; ++c) {
+            const uint4 *src = reinterpret_cast<const uint4 *>(h + c * kBins + owner * 8);
+            a[c] = src[0];
+            b[c] = src[1];
+        }
+        p.v[0] = a[0].x; p.v[1] = a[0].y; p.v[2] = a[0].z; p.v[3] = a[0].w;
+        p.v[4] = b[0].x; p.v[5] = b[0].y; p.v[6] = b[0].z; p.v[7] = b[0].w;
+#pragma unroll
+        for (int c = 1; c < HC; ++c) {
+            p.v[0] += a[c].x; p.v[1] += a[c].y; p.v[2] += a[c].z; p.v[3] += a[c].w;
+            p.v[4] += b[c].x; p.v[5] += b[c].y; p.v[6] += b[c].z; p.v[7] += b[c].w;
+        }
     } else {
         static_assert(PER == 2, "level bins per thread");
-        const uint2 a = *reinterpret_cast<const uint2 *>(h + owner * 2);
-        p.v[0] = a.x; p.v[1] = a.y;
+        uint2 a[HC];
+#pragma unroll
+        for (int c = 0; c < HC; ++c) a[c] = *reinterpret_cast<const uint2 *>(h + c * kBins + owner * 2);
+        p.v[0] = a[0].x; p.v[1] = a[0].y;
+#pragma unroll
+        for (int c = 1; c < HC; ++c) { p.v[0] += a[c].x; p.v[1] += a[c].y; }
 #pragma unroll
         for (int i = 2; i < kBins / kBlock; ++i) p.v[i] = 0u;
     }
@@ -823,6 +842,7 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg,
     __shared__ uint32_t s_hist[kBins];
     __shared__ __align__(16) float s_part[kWaves * 64];
     __shared__ __align__(16) float s_c[kWaves * 64];
+    __shared__ uint32_t s_wmax[kWaves];
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
     if (row0 >= row_end) return;  // a trailing workgroup with no rows (uniform)
@@ -872,13 +892,21 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg,
             }
         }
     }
-    __syncthreads();
-    uint32_t *gh = hist + (chunk * 3 + 0) * kBins;
-    for (int b = threadIdx.x; b < kBins; b += kBlock)
-        if (s_hist[b]) atomicAdd(&gh[b], s_hist[b]);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, off, 64));
-    if ((threadIdx.x & 63) == 0 && kmax) atomicMax(maxkey, kmax);
+    if ((threadIdx.x & 63) == 0) s_wmax[threadIdx.x >> 6] = kmax;
+    __syncthreads();
+    // this workgroup's copy of the chunk histogram and of the max key (one atomic per workgroup)
+    const int copy = (int)(blockIdx.x % g.hcopies);
+    uint32_t *gh = hist + ((chunk * 3 + 0) * g.hcopies + copy) * kBins;
+    for (int b = threadIdx.x; b < kBins; b += kBlock)
+        if (s_hist[b]) atomicAdd(&gh[b], s_hist[b]);
+    if (threadIdx.x == 0) {
+        uint32_t m = 0u;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) m = max(m, s_wmax[w]);
+        if (m) atomicMax(maxkey + copy * kMaxKeyStride, m);
+    }
 }
 
 // The previous level's state of the workgroup's chunk (level 0: its k).
@@ -890,13 +918,13 @@ __device__ __forceinline__ SelState prev_state(int lvl, const SelState *__restri
 }
 
 // Passes 2 and 3 (batched): histogram of digit `lvl` among keys matching the prefix so far.
-template <int DT, int R, int V>
+template <int DT, int R, int V, int HC>
 __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom fg, int lvl,
                                                           const typename Act<DT>::T *__restrict__ x,
                                                           const float *__restrict__ qp,
                                                           const typename Act<DT>::T *__restrict__ coeff,
                                                           uint32_t *__restrict__ hist, SelState *__restrict__ state,
-                                                        uint32_t k_full, uint32_t k_last)
+                                                          uint32_t k_full, uint32_t k_last, uint32_t *__restrict__ maxkey)
 {
     constexpr int NB = Batch<R>::NB;
     __shared__ uint32_t s_hist[kBins];
@@ -908,7 +936,7 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
     const SelState sp = prev_state(lvl - 1, state, chunk, g.n_chunks, k_full, k_last);
     HistPre hp;
     static_assert(kDigitBins[0] / kBlock == 8 && kDigitBins[1] / kBlock == 8 && kDigitBins[2] / kBlock == 2, "bins per thread");
-    hist_issue<8>(hist + (chunk * 3 + lvl - 1) * kBins, hp);
+    hist_issue<8, HC>(hist + (chunk * 3 + lvl - 1) * HC * kBins, hp);
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
     const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
     const bool col_ok = col < g.d;
@@ -920,6 +948,12 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
     // the chunk's first workgroup records the selection for the passes that follow
     const SelState sel = block_select_pre(lvl - 1, hp, sp.prefix, sp.need, s_tot, &s_res);
     if (blockIdx.x % g.wgs_per_chunk == 0 && threadIdx.x == 0) state[chunk * 3 + lvl - 1] = sel;
+    if (HC > 1 && lvl == 1 && blockIdx.x == 0 && threadIdx.x == 0) {  // fold the max key's copies into the first
+        uint32_t m = maxkey[0];
+#pragma unroll
+        for (int c = 1; c < HC; ++c) m = max(m, maxkey[c * kMaxKeyStride]);
+        maxkey[0] = m;
+    }
     if (!has_rows) return;
     const uint32_t prefix = sel.prefix;
     const int match_shift = kDigitShift[lvl - 1], dshift = kDigitShift[lvl];
@@ -941,13 +975,13 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
         }
     }
     __syncthreads();
-    uint32_t *gh = hist + (chunk * 3 + lvl) * kBins;
+    uint32_t *gh = hist + ((chunk * 3 + lvl) * HC + blockIdx.x % HC) * kBins;
     for (int b = threadIdx.x; b < kDigitBins[lvl]; b += kBlock)
         if (s_hist[b]) atomicAdd(&gh[b], s_hist[b]);
 }
 
 // Survivor counts (batched).
-template <int DT, int R, int V>
+template <int DT, int R, int V, int HC>
 __global__ __launch_bounds__(kBlock) void k_count_b(SaveGeom g, FastGeom fg, const typename Act<DT>::T *__restrict__ x,
                                                     const float *__restrict__ qp,
                                                     const typename Act<DT>::T *__restrict__ coeff,
@@ -962,7 +996,7 @@ __global__ __launch_bounds__(kBlock) void k_count_b(SaveGeom g, FastGeom fg, con
     const bool has_rows = row0 < row_end;
     const SelState sp = prev_state(2, state, chunk, g.n_chunks, k_full, k_last);
     HistPre hp;
-    hist_issue<2>(hist + (chunk * 3 + 2) * kBins, hp);
+    hist_issue<2, HC>(hist + (chunk * 3 + 2) * HC * kBins, hp);
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
     const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
     const bool col_ok = col < g.d;
@@ -1314,6 +1348,7 @@ Plan make_plan(const StacrSaveArgs &a)
     if (p.fast) rpw = hmin<int64_t>(rpw, (int64_t)(64 / p.R) * g.rpi);
     g.rows_per_wg = rpw;
     g.wgs_per_chunk = (g.chunk_rows + rpw - 1) / rpw;
+    g.hcopies = p.fast && g.wgs_per_chunk >= 128 ? kHistCopies : 1;
     p.n_wgs = g.n_chunks * g.wgs_per_chunk;
     p.trim = a.k_sum > a.k_total;
     p.n_list_blocks = (a.k_sum + kListBlock - 1) / kListBlock;
@@ -1330,8 +1365,8 @@ size_t layout(const StacrSaveArgs &a, const Plan &p, size_t *off)
     size_t cur = 0;
     auto take = [&](int slot, size_t bytes) { off[slot] = cur; cur += (bytes + 255) & ~(size_t)255; };
     take(WS_QP, 2 * (size_t)a.feats * p.R * sizeof(float));  // padded basis, then transposed
-    take(WS_HIST, (size_t)p.g.n_chunks * 3 * kBins * sizeof(uint32_t));
-    take(WS_MAXKEY, sizeof(uint32_t));
+    take(WS_HIST, (size_t)p.g.n_chunks * 3 * p.g.hcopies * kBins * sizeof(uint32_t));
+    take(WS_MAXKEY, (size_t)p.g.hcopies * kMaxKeyStride * sizeof(uint32_t));
     take(WS_STATE, (size_t)p.g.n_chunks * 3 * sizeof(SelState));
     take(WS_COUNTS, (size_t)p.n_wgs * sizeof(WgCount));
     take(WS_OFFS, (size_t)p.n_wgs * sizeof(WgOffset));
@@ -1364,7 +1399,8 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     const int nwg = (int)p.n_wgs;
 
     // padded basis; histograms and max key (contiguous in the layout) cleared in the same launch
-    const int64_t n_zero = resid ? (int64_t)((off[WS_MAXKEY] + sizeof(uint32_t) - off[WS_HIST]) / sizeof(uint32_t)) : 0;
+    const int64_t n_zero = resid ? (int64_t)((off[WS_MAXKEY] + (size_t)p.g.hcopies * kMaxKeyStride * sizeof(uint32_t) -
+                                              off[WS_HIST]) / sizeof(uint32_t)) : 0;
     stacr_launch("k_prep", s, [&] {
         k_prep<DT><<<grid_for(hmax<int64_t>(a.feats * R, n_zero)), kBlock, 0, s>>>(static_cast<const T *>(a.q), a.feats,
                                                                                  a.rank, R, qp, hist, n_zero);
@@ -1372,6 +1408,8 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     // batched fast path: one aligned vector per thread per row, basis columns in registers
     constexpr bool kFastOk = QREG && V == Act<DT>::kVec && V * R <= 64;
     const bool fast = kFastOk && p.fast;
+    const bool hc8 = p.g.hcopies == kHistCopies;
+    if (!fast && p.g.hcopies != 1) return stacr_fail(STACR_ERR_INVALID, "stacr_save: histogram copies outside the batched path");
     FastGeom fg{p.g.L / 64, a.rank == R && ((uintptr_t)coeff % 16) == 0};
     if (!coeff_in || resid) {
         if constexpr (kFastOk) {
@@ -1389,12 +1427,18 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     // completed histogram; the chunk's first workgroup records it), so no selection launches.
     for (int lvl = 1; lvl < 3; ++lvl) {
         if constexpr (kFastOk) {
-            if (fast) stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, x, qp, coeff, hist, state, kf, kl); });
+            if (fast && hc8)
+                stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, x, qp, coeff, hist, state, kf, kl, maxkey); });
+            if (fast && !hc8)
+                stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, x, qp, coeff, hist, state, kf, kl, maxkey); });
         }
         if (!fast) stacr_launch("k_refine_hist", s, [&] { k_refine_hist<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, lvl, x, qp, coeff, hist, state, kf, kl); });
     }
     if constexpr (kFastOk) {
-        if (fast) stacr_launch("k_count", s, [&] { k_count_b<DT, R, V><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, hist, state, counts, kf, kl); });
+        if (fast && hc8)
+            stacr_launch("k_count", s, [&] { k_count_b<DT, R, V, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, hist, state, counts, kf, kl); });
+        if (fast && !hc8)
+            stacr_launch("k_count", s, [&] { k_count_b<DT, R, V, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, hist, state, counts, kf, kl); });
     }
     if (!fast) stacr_launch("k_count", s, [&] { k_count<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, hist, state, counts, kf, kl); });
 
