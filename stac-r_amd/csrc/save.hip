@@ -989,14 +989,19 @@ __global__ __launch_bounds__(kBlock) void k_count_b(SaveGeom g, FastGeom fg, con
                                                   WgCount *__restrict__ counts, uint32_t k_full, uint32_t k_last)
 {
     constexpr int NB = Batch<R>::NB;
+    // A 16-bit residual widened to fp32 has key bits 8..0 clear, so the last radix level always
+    // picks bin 0 with the need unchanged: for those types this pass makes the level-1 selection
+    // and derives the final state from it (the second refine pass is not launched).
+    constexpr int kLvl = sizeof(typename Act<DT>::T) == 2 ? 1 : 2;
     __shared__ uint32_t s_tot[kWaves];
     __shared__ SelState s_res;
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
     const bool has_rows = row0 < row_end;
-    const SelState sp = prev_state(2, state, chunk, g.n_chunks, k_full, k_last);
+    const SelState sp = prev_state(kLvl, state, chunk, g.n_chunks, k_full, k_last);
     HistPre hp;
-    hist_issue<2, HC>(hist + (chunk * 3 + 2) * HC * kBins, hp);
+    if constexpr (kLvl == 1) hist_issue<8, HC>(hist + (chunk * 3 + 1) * HC * kBins, hp);
+    else hist_issue<2, HC>(hist + (chunk * 3 + 2) * HC * kBins, hp);
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
     const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
     const bool col_ok = col < g.d;
@@ -1004,7 +1009,11 @@ __global__ __launch_bounds__(kBlock) void k_count_b(SaveGeom g, FastGeom fg, con
     if (has_rows) ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
     float q[V][R];
     basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
-    const SelState sel = block_select_pre(2, hp, sp.prefix, sp.need, s_tot, &s_res);
+    SelState sel = block_select_pre(kLvl, hp, sp.prefix, sp.need, s_tot, &s_res);
+    if (kLvl == 1) {
+        if (blockIdx.x % g.wgs_per_chunk == 0 && threadIdx.x == 0) state[chunk * 3 + 1] = sel;
+        sel = SelState{sel.prefix << kDigitShift[1], sel.need};
+    }
     if (blockIdx.x % g.wgs_per_chunk == 0 && threadIdx.x == 0) state[chunk * 3 + 2] = sel;
     const uint32_t T = sel.prefix;
     basis_mask<R, V>(col_ok, q);
@@ -1425,7 +1434,9 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     const uint32_t kf = (uint32_t)a.k_full, kl = (uint32_t)a.k_last;
     // Each pass first finds the previous radix level's bin for its chunk (every workgroup from the
     // completed histogram; the chunk's first workgroup records it), so no selection launches.
-    for (int lvl = 1; lvl < 3; ++lvl) {
+    // (the batched count pass makes the last selection of 16-bit types itself)
+    const int n_refine = fast && sizeof(T) == 2 ? 1 : 2;
+    for (int lvl = 1; lvl <= n_refine; ++lvl) {
         if constexpr (kFastOk) {
             if (fast && hc8)
                 stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, x, qp, coeff, hist, state, kf, kl, maxkey); });

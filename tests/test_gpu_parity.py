@@ -90,6 +90,12 @@ SAVE_CASES = [
     ("fp32_rank1", 256, 64, 1, "f32", "global_topk", 0.05, 512, 8, False),
     ("partial_last_chunk", 1000, 128, 8, "bf16", "chunk_topk", 0.01, 300, 8, False),
     ("no_residual_budget", 64, 64, 4, "f32", "chunk_topk", 0.0, 16, 8, False),
+    # batched path: 16-bit types skip the last radix pass; 128+ workgroups per chunk use
+    # histogram copies, fewer do not
+    ("f16_batched_global_copies", 2048, 1024, 8, "f16", "global_topk", 0.005, 512, 8, True),
+    ("f16_batched_chunk", 1024, 512, 4, "f16", "chunk_topk", 0.01, 256, 8, False),
+    ("bf16_batched_global_one_copy", 512, 1024, 8, "bf16", "global_topk", 0.01, 512, 8, False),
+    ("f32_batched_global_copies", 4096, 512, 8, "f32", "global_topk", 0.01, 512, 8, True),
 ]
 
 
