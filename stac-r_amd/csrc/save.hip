@@ -924,11 +924,14 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
                                                           const float *__restrict__ qp,
                                                           const typename Act<DT>::T *__restrict__ coeff,
                                                           uint32_t *__restrict__ hist, SelState *__restrict__ state,
-                                                          uint32_t k_full, uint32_t k_last, uint32_t *__restrict__ maxkey)
+                                                          uint32_t k_full, uint32_t k_last, uint32_t *__restrict__ maxkey,
+                                                          uint32_t *__restrict__ fold, int64_t fold_stride)
 {
     constexpr int NB = Batch<R>::NB;
+    constexpr bool kFold = DT == STACR_DTYPE_BF16;  // per-workgroup records for the emission pass
     __shared__ uint32_t s_hist[kBins];
     __shared__ uint32_t s_tot[kWaves];
+    __shared__ uint32_t s_above[kWaves];
     __shared__ SelState s_res;
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
@@ -954,11 +957,16 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
         for (int c = 1; c < HC; ++c) m = max(m, maxkey[c * kMaxKeyStride]);
         maxkey[0] = m;
     }
-    if (!has_rows) return;
+    const bool fold_rec = kFold && lvl == 1;
+    if (!has_rows) {
+        if (fold_rec && threadIdx.x <= 16) fold[threadIdx.x * fold_stride + blockIdx.x] = 0u;
+        return;
+    }
     const uint32_t prefix = sel.prefix;
     const int match_shift = kDigitShift[lvl - 1], dshift = kDigitShift[lvl];
     const uint32_t dmask = (uint32_t)kDigitBins[lvl] - 1u;
     basis_mask<R, V>(col_ok, q);
+    uint32_t above = 0u;
     {   // the workgroup's rows are one batch
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
@@ -971,10 +979,23 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
             for (int e = 0; e < V; ++e) {
                 const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
                 if ((key >> match_shift) == prefix) atomicAdd(&s_hist[(key >> dshift) & dmask], 1u);
+                if (kFold) above += (key >> match_shift) > prefix;
             }
         }
     }
+    if (kFold) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) above += (uint32_t)__shfl_xor((int)above, off, 64);
+        if ((threadIdx.x & 63) == 0) s_above[threadIdx.x >> 6] = above;
+    }
     __syncthreads();
+    if (fold_rec && threadIdx.x <= 16) {  // cum[b] for b = threadIdx.x (16: above B0 only)
+        uint32_t c = 0u;
+#pragma unroll
+        for (int wv = 0; wv < kWaves; ++wv) c += s_above[wv];
+        for (int b = threadIdx.x; b < 16; ++b) c += s_hist[b << 7];
+        fold[threadIdx.x * fold_stride + blockIdx.x] = c;
+    }
     uint32_t *gh = hist + ((chunk * 3 + lvl) * HC + blockIdx.x % HC) * kBins;
     for (int b = threadIdx.x; b < kDigitBins[lvl]; b += kBlock)
         if (s_hist[b]) atomicAdd(&gh[b], s_hist[b]);
@@ -1039,33 +1060,89 @@ __global__ __launch_bounds__(kBlock) void k_count_b(SaveGeom g, FastGeom fg, con
     if (threadIdx.x == 0) counts[blockIdx.x] = WgCount{tg, te};
 }
 
+// bf16 fold.  A bf16 residual widened to fp32 has key bits 15..0 clear, so inside the level-0 bin
+// B0 only bits 19..16 vary: the level-1 histogram has 16 live bins (b << 7).  The refine pass
+// records, per workgroup w, cum[b][w] = (its keys above B0) + (its keys in B0 with bits 19..16
+// >= b) for b = 0..16 (cum[16]: above B0 only).  Once the level-1 bin b1 is chosen, the threshold
+// is T = B0 << 20 | b1 << 16, and a workgroup has cum[b1 + 1] keys above T and cum[b1] -
+// cum[b1 + 1] equal to it, so the emission pass needs no separate count pass.
+//
+// The level-1 selection from the 16 live bins (hw: this lane's bin (lane & 15) in each histogram
+// copy), made by every wave on its own: suffix sums across 16 lanes, then the highest bin whose
+// suffix reaches the need.  Returns the final (31-bit) state; the same result as the generic
+// level-1 and level-2 selections.
+template <int HC>
+__device__ __forceinline__ SelState fold_select(const uint32_t (&hw)[HC], SelState s0, SelState *sel1)
+{
+    const int b = threadIdx.x & 15;
+    uint32_t suf = 0u;
+#pragma unroll
+    for (int c = 0; c < HC; ++c) suf += hw[c];
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+        const uint32_t y = __shfl_down(suf, off, 16);
+        if (b + off < 16) suf += y;
+    }
+    const uint64_t m = __ballot(suf >= s0.need) & 0xffffull;  // lanes 0..15 hold bins 0..15
+    const int b1 = m ? 63 - __clzll(m) : 0;                   // m != 0: B0 holds at least need keys
+    const uint32_t above = b1 < 15 ? (uint32_t)__shfl((int)suf, b1 + 1, 64) : 0u;
+    *sel1 = SelState{(s0.prefix << 11) | ((uint32_t)b1 << 7), s0.need - above};
+    return SelState{sel1->prefix << kDigitShift[1], sel1->need};
+}
+
 // Ordered compaction (batched).  Elements are enumerated as (iteration, slot, thread, element),
 // which is ascending flat index: one multi-value block scan per batch gives every thread the
 // number of survivors (gt in the low half, ties in the high half) before each of its vectors.
-template <int DT, int R, int V>
+template <int DT, int R, int V, int HC>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) void k_emit_b(SaveGeom g, FastGeom fg, const typename Act<DT>::T *__restrict__ x,
                                                    const float *__restrict__ qp,
                                                    const typename Act<DT>::T *__restrict__ coeff,
-                                                   const SelState *__restrict__ state, const WgCount *__restrict__ counts, uint32_t chunk_k,
+                                                   SelState *__restrict__ state, const WgCount *__restrict__ counts, uint32_t chunk_k,
                                                    const uint32_t *__restrict__ maxkey, OutSpec o, float *scale_out,
-                                                   int to_list)
+                                                   int to_list, const uint32_t *__restrict__ hist,
+                                                   const uint32_t *__restrict__ fold, int64_t fold_stride)
 {
     constexpr int NB = Batch<R>::NB;
+    constexpr bool kFold = DT == STACR_DTYPE_BF16;  // bf16: the selection ends here (no count pass)
     __shared__ uint32_t s_wt[kWaves * NB];
     __shared__ uint32_t s_off[kWaves];
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
-    const SelState st = state[chunk * 3 + 2];
-    const uint32_t mk = *maxkey;
     const int64_t w = blockIdx.x - chunk * g.wgs_per_chunk;
-    // counts of the chunk's earlier workgroups (at most two per thread in the usual geometry;
-    // wg_offset reads any further ones itself)
+    const int64_t wg0 = chunk * g.wgs_per_chunk;  // the chunk's first workgroup
+    SelState st;
     WgCount pre[2];
+    if constexpr (kFold) {
+        uint32_t hw[HC];
+        const uint32_t *h1 = hist + (chunk * 3 + 1) * HC * kBins + ((threadIdx.x & 15) << 7);
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int64_t v = threadIdx.x + k * kBlock;
-        pre[k] = counts[chunk * g.wgs_per_chunk + min(v, w)];
+        for (int c = 0; c < HC; ++c) hw[c] = h1[c * kBins];
+        SelState sel1;
+        st = fold_select<HC>(hw, state[chunk * 3 + 0], &sel1);
+        if (w == 0 && threadIdx.x == 0) {
+            state[chunk * 3 + 1] = sel1;
+            state[chunk * 3 + 2] = st;
+        }
+        // the earlier workgroups' counts above / equal to the threshold (clamped reads, masked at use)
+        const uint32_t b1 = (st.prefix >> 16) & 15u;
+        const uint32_t *hi = fold + (int64_t)(b1 + 1) * fold_stride + wg0, *lo = fold + (int64_t)b1 * fold_stride + wg0;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int64_t v = min((int64_t)threadIdx.x + k * kBlock, w);
+            const uint32_t a = hi[v], b = lo[v];
+            pre[k] = WgCount{a, b - a};
+        }
+    } else {
+        st = state[chunk * 3 + 2];
+        // counts of the chunk's earlier workgroups (at most two per thread in the usual geometry;
+        // the offset block reads any further ones itself)
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int64_t v = threadIdx.x + k * kBlock;
+            pre[k] = counts[wg0 + min(v, w)];
+        }
     }
+    const uint32_t mk = *maxkey;
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
@@ -1085,14 +1162,16 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
             gt += v < w ? pre[k].gt : 0u;
             eq += v < w ? pre[k].eq : 0u;
         }
+        const uint32_t b1 = (st.prefix >> 16) & 15u;
+        const uint32_t *hi = fold + (int64_t)(b1 + 1) * fold_stride + wg0, *lo = fold + (int64_t)b1 * fold_stride + wg0;
         for (int64_t v = threadIdx.x + 2 * kBlock; v < w; v += kBlock) {
-            const WgCount c = counts[chunk * g.wgs_per_chunk + v];
+            const WgCount c = kFold ? WgCount{hi[v], lo[v] - hi[v]} : counts[wg0 + v];
             gt += c.gt;
             eq += c.eq;
         }
         const uint32_t gt_before = block_sum(gt, s_off);
         const uint32_t eq_before = block_sum(eq, s_off);
-        const WgCount mine = counts[chunk * g.wgs_per_chunk + w];
+        const WgCount mine = kFold ? WgCount{hi[w], lo[w] - hi[w]} : counts[wg0 + w];
         const uint32_t take = eq_before >= st.need ? 0u : min(mine.eq, st.need - eq_before);
         wo = WgOffset{(uint32_t)chunk * chunk_k + gt_before + min(st.need, eq_before), take};
     }
@@ -1321,6 +1400,7 @@ struct Plan {
     int V, R;
     bool qreg;
     bool fast;  // the batched kernels (one batch per workgroup)
+    bool fold;  // bf16 on the batched path: the emission pass ends the selection (no count pass)
     int64_t n_wgs;
     bool trim;
     int64_t n_list_blocks;
@@ -1358,6 +1438,7 @@ Plan make_plan(const StacrSaveArgs &a)
     g.rows_per_wg = rpw;
     g.wgs_per_chunk = (g.chunk_rows + rpw - 1) / rpw;
     g.hcopies = p.fast && g.wgs_per_chunk >= 128 ? kHistCopies : 1;
+    p.fold = p.fast && a.dtype == STACR_DTYPE_BF16;
     p.n_wgs = g.n_chunks * g.wgs_per_chunk;
     p.trim = a.k_sum > a.k_total;
     p.n_list_blocks = (a.k_sum + kListBlock - 1) / kListBlock;
@@ -1367,7 +1448,7 @@ Plan make_plan(const StacrSaveArgs &a)
 template <typename T> T *carve(char *base, size_t off) { return reinterpret_cast<T *>(base + off); }
 
 enum { WS_QP, WS_HIST, WS_STATE, WS_MAXKEY, WS_COUNTS, WS_OFFS, WS_LRBITS, WS_LIDX, WS_THIST, WS_TSTATE,
-       WS_LCOUNTS, WS_LOFFS, WS_Q4, WS_N };
+       WS_LCOUNTS, WS_LOFFS, WS_Q4, WS_FOLD, WS_N };
 
 size_t layout(const StacrSaveArgs &a, const Plan &p, size_t *off)
 {
@@ -1387,6 +1468,7 @@ size_t layout(const StacrSaveArgs &a, const Plan &p, size_t *off)
     take(WS_LCOUNTS, nb * sizeof(WgCount));
     take(WS_LOFFS, nb * sizeof(WgOffset));
     take(WS_Q4, a.bits == 4 ? (size_t)a.k_total : 0);
+    take(WS_FOLD, p.fold ? (size_t)17 * p.n_wgs * sizeof(uint32_t) : 0);  // cum[0..16][workgroup]
     return cur;
 }
 
@@ -1418,6 +1500,8 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     constexpr bool kFastOk = QREG && V == Act<DT>::kVec && V * R <= 64;
     const bool fast = kFastOk && p.fast;
     const bool hc8 = p.g.hcopies == kHistCopies;
+    uint32_t *fold = carve<uint32_t>(ws, off[WS_FOLD]);
+    if (fast != p.fold && DT == STACR_DTYPE_BF16) return stacr_fail(STACR_ERR_INVALID, "stacr_save: bf16 fold outside the batched path");
     if (!fast && p.g.hcopies != 1) return stacr_fail(STACR_ERR_INVALID, "stacr_save: histogram copies outside the batched path");
     FastGeom fg{p.g.L / 64, a.rank == R && ((uintptr_t)coeff % 16) == 0};
     if (!coeff_in || resid) {
@@ -1439,16 +1523,16 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     for (int lvl = 1; lvl <= n_refine; ++lvl) {
         if constexpr (kFastOk) {
             if (fast && hc8)
-                stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, x, qp, coeff, hist, state, kf, kl, maxkey); });
+                stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, x, qp, coeff, hist, state, kf, kl, maxkey, fold, p.n_wgs); });
             if (fast && !hc8)
-                stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, x, qp, coeff, hist, state, kf, kl, maxkey); });
+                stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, x, qp, coeff, hist, state, kf, kl, maxkey, fold, p.n_wgs); });
         }
         if (!fast) stacr_launch("k_refine_hist", s, [&] { k_refine_hist<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, lvl, x, qp, coeff, hist, state, kf, kl); });
     }
     if constexpr (kFastOk) {
-        if (fast && hc8)
+        if (fast && hc8 && !p.fold)
             stacr_launch("k_count", s, [&] { k_count_b<DT, R, V, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, hist, state, counts, kf, kl); });
-        if (fast && !hc8)
+        if (fast && !hc8 && !p.fold)
             stacr_launch("k_count", s, [&] { k_count_b<DT, R, V, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, hist, state, counts, kf, kl); });
     }
     if (!fast) stacr_launch("k_count", s, [&] { k_count<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, hist, state, counts, kf, kl); });
@@ -1464,7 +1548,11 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     o.list_idx = lix;
     o.cap = (uint32_t)(p.trim ? a.k_sum : a.k_total);
     if constexpr (kFastOk) {
-        if (fast) stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0); });
+        // the fold variant (bf16) reads the level-1 histogram copies; other types take the counts
+        if (fast && hc8 && DT == STACR_DTYPE_BF16)
+            stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs); });
+        else if (fast)
+            stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs); });
     }
     if (!fast) stacr_launch("k_emit", s, [&] { k_emit<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0); });
 

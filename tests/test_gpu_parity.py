@@ -96,6 +96,10 @@ SAVE_CASES = [
     ("f16_batched_chunk", 1024, 512, 4, "f16", "chunk_topk", 0.01, 256, 8, False),
     ("bf16_batched_global_one_copy", 512, 1024, 8, "bf16", "global_topk", 0.01, 512, 8, False),
     ("f32_batched_global_copies", 4096, 512, 8, "f32", "global_topk", 0.01, 512, 8, True),
+    # bf16 batched path ends the selection in the emission pass: chunks with a partial last
+    # workgroup and a trim to k_total, and a chunked run without quantization
+    ("bf16_batched_chunk_trim", 1000, 1024, 8, "bf16", "chunk_topk", 0.005, 100, 8, True),
+    ("bf16_batched_chunk_bits0", 2048, 1024, 4, "bf16", "chunk_topk", 0.01, 512, 0, False),
 ]
 
 
