@@ -23,6 +23,8 @@
 //              then reduces M over its threads and writes dW = M Q^T + S for its tile.
 // Within a feature, entries follow the bucket order, which LDS integer atomics fill in arrival
 // order: the last bits of the sparse term may differ from run to run.
+#include <type_traits>
+
 #include "internal.h"
 
 using namespace stacr;
@@ -188,31 +190,71 @@ struct PlanArgs {
 
 // The product operand of entry e: the integer code (exact in bf16/fp16) for bits 4/8, the stored
 // value for bits 0; as G's 16-bit code, or fp32 bits for fp32 G.
-__device__ __forceinline__ uint32_t entry_value(const PlanArgs &a, int64_t e)
+// Entry values come in one of four layouts (VK): int8 codes (bits 8), packed int4 codes (bits
+// 4), 16-bit or fp32 stored values (bits 0).  The raw load is one branch-free instruction per
+// layout, so a thread's loads all stay in flight together; the decode follows.
+enum { kValI8 = 0, kValI4 = 1, kVal16 = 2, kVal32 = 3 };
+template <int VK>
+__device__ __forceinline__ uint32_t entry_raw(const void *data, uint32_t e)
+{
+    if constexpr (VK == kValI8) return static_cast<const uint8_t *>(data)[e];
+    else if constexpr (VK == kValI4) return static_cast<const uint8_t *>(data)[e >> 1];
+    else if constexpr (VK == kVal16) return static_cast<const uint16_t *>(data)[e];
+    else return static_cast<const uint32_t *>(data)[e];
+}
+template <int VK>
+__device__ __forceinline__ uint32_t entry_value(const PlanArgs &a, uint32_t raw, uint32_t e)
 {
     float v;
-    if (a.bits == 8) {
-        v = (float)static_cast<const int8_t *>(a.data)[e];
-    } else if (a.bits == 4) {
-        const uint32_t byte = static_cast<const uint8_t *>(a.data)[e >> 1];
-        const int n = (int)((e & 1) ? (byte >> 4) : (byte & 0xfu));
+    if constexpr (VK == kValI8) {
+        v = (float)(int8_t)raw;
+    } else if constexpr (VK == kValI4) {
+        const int n = (int)((e & 1) ? (raw >> 4) : (raw & 0xfu));
         v = (float)(n > 7 ? n - 16 : n);
+    } else if constexpr (VK == kVal16) {
+        v = a.val_dt == STACR_DTYPE_BF16 ? bf16_bits_to_f(raw) : f16_bits_to_f(raw);
     } else {
-        v = load_any(a.data, a.val_dt, e);
+        v = __uint_as_float(raw);
     }
     if (a.g_dt == STACR_DTYPE_BF16) return f_to_bf16_bits(v);
     if (a.g_dt == STACR_DTYPE_F16) return f_to_f16_bits(v);
     return __float_as_uint(v);
 }
 
-template <int IDX64>
+// Exclusive prefix sum over the planner's workgroup with one barrier: the per-wave totals go to
+// `buf`, which callers alternate between two arrays, so a wave still reading one scan's totals
+// never sees the next scan's (a buffer is reused only after another scan's barrier).
+__device__ __forceinline__ uint32_t scan1(uint32_t v, uint32_t *buf, uint32_t *total)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    if (lane == 63) buf[wave] = x;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kPlanThreads / 64; ++w) {
+        const uint32_t t = buf[w];
+        before += w < wave ? t : 0u;
+        all += t;
+    }
+    *total = all;
+    return before + x - v;
+}
+
+template <int IDX64, int VK>
 __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
 {
     __shared__ uint32_t cnt[kMaxISlab], ccur[kMaxISlab];
     __shared__ uint32_t cstart[kMaxISlab], lstart[kMaxISlab], hstart[kMaxISlab], hidx[kMaxISlab];
     __shared__ uint32_t colh[kMaxISlab];  // 1 + matrix-core column of a feature, 0 for pieces
-    __shared__ uint32_t s_tot[kPlanThreads / 64];
-    __shared__ uint32_t s_probe[2][7][kPlanThreads / 64];  // column search: per-wave counts
+    __shared__ uint32_t s_tot[2][kPlanThreads / 64];        // scan1 buffers, used alternately
+    __shared__ uint32_t s_cnt[2][kPlanThreads / 64];        // range search: per-wave counts
+    __shared__ uint32_t s_probe[2][15][kPlanThreads / 64];  // column search: per-wave counts
     const int64_t b = blockIdx.x, p = blockIdx.y;
     const int64_t t0 = b * a.tb, t1 = min(t0 + a.tb, a.rows);
     const int64_t i0 = p * a.i_span;
@@ -220,6 +262,9 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
     const int64_t span = (t1 - t0) * a.d_in;  // flat offsets of the block's rows
     const uint32_t d_in = (uint32_t)a.d_in;
     const float inv_d = 1.f / (float)a.d_in;
+    const bool one_part = a.n_parts == 1;
+    const uint32_t i_span = (uint32_t)a.i_span;  // features per part (< 65536)
+    const float inv_span = 1.f / (float)a.i_span;
     // entry range of a block; the clamps keep indices that are not ascending inside the arrays
     const uint32_t nnz = (uint32_t)a.nnz;
     // The block's entries [e0, e1): the first entries whose flat index is >= t0 * d_in and
@@ -229,13 +274,21 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
     {
         const int64_t key0 = t0 * a.d_in, key1 = t1 * a.d_in;
         uint32_t lo0 = 0u, hi0 = nnz, lo1 = 0u, hi1 = nnz;
-        while (lo0 < hi0 || lo1 < hi1) {
+        for (int it = 0; lo0 < hi0 || lo1 < hi1; ++it) {
             const uint32_t st0 = max(1u, (hi0 - lo0 + kPlanThreads - 1) / kPlanThreads);
             const uint32_t st1 = max(1u, (hi1 - lo1 + kPlanThreads - 1) / kPlanThreads);
             const uint32_t p0 = lo0 + threadIdx.x * st0, p1 = lo1 + threadIdx.x * st1;
-            const bool b0 = p0 < hi0 && flat_at<IDX64>(a.idx, p0) < key0;
-            const bool b1 = p1 < hi1 && flat_at<IDX64>(a.idx, p1) < key1;
-            const uint32_t c0 = (uint32_t)__syncthreads_count(b0), c1 = (uint32_t)__syncthreads_count(b1);
+            // both samples loaded unconditionally (clamped positions; nnz > 0 here), one barrier
+            const int64_t v0 = flat_at<IDX64>(a.idx, min(p0, nnz - 1u)), v1 = flat_at<IDX64>(a.idx, min(p1, nnz - 1u));
+            const bool b0 = p0 < hi0 && v0 < key0;
+            const bool b1 = p1 < hi1 && v1 < key1;
+            const uint32_t m = (uint32_t)__popcll(__ballot(b0)) | ((uint32_t)__popcll(__ballot(b1)) << 16);
+            if ((threadIdx.x & 63) == 0) s_cnt[it & 1][threadIdx.x >> 6] = m;  // <= 512 each: 16-bit halves
+            __syncthreads();
+            uint32_t c01 = 0u;
+#pragma unroll
+            for (int w = 0; w < kPlanThreads / 64; ++w) c01 += s_cnt[it & 1][w];
+            const uint32_t c0 = c01 & 0xffffu, c1 = c01 >> 16;
             if (c0 == 0u) hi0 = lo0;  // the first sample is not below the key
             else { lo0 += (c0 - 1u) * st0 + 1u; hi0 = min(hi0, lo0 - 1u + st0); }
             if (c1 == 0u) hi1 = lo1;
@@ -264,99 +317,122 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
         __syncthreads();
         constexpr int EPT = kRoundMax / kPlanThreads;
         uint32_t col[EPT], tl[EPT], val[EPT];
+        int64_t fl[EPT];
+        // every index and value load is issued before any is used: unconditional, from an entry
+        // clamped into the round (c1 > c0), masked below (a load merged from divergent paths
+        // would be waited for at once)
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+            const uint32_t e = min(c0 + threadIdx.x + k * kPlanThreads, c1 - 1u);
+            fl[k] = flat_at<IDX64>(a.idx, e);
+            val[k] = entry_raw<VK>(a.data, e);  // decoded where used, at the end
+        }
         uint32_t before = 0;
 #pragma unroll
         for (int k = 0; k < EPT; ++k) {
             col[k] = 0xffffffffu;
             tl[k] = 0u;
             const uint32_t e = c0 + threadIdx.x + k * kPlanThreads;
-            val[k] = entry_value(a, min(e, c1 - 1u));  // loaded with the index, used at the end
-            const int64_t off64 = e < c1 ? flat_at<IDX64>(a.idx, e) - t0 * a.d_in : -1;
+            const int64_t off64 = e < c1 ? fl[k] - t0 * a.d_in : -1;
             if (off64 >= 0 && off64 < span) {
                 const uint32_t off = (uint32_t)off64;  // < 2^25: tb <= 512 rows of < 65536 features
                 const uint32_t t = div_small(off, d_in, inv_d);
-                const int64_t c = (int64_t)(off - t * d_in);
-                const int64_t part = c / a.i_span;
-                before += part < p;
-                if (part == p) {
-                    col[k] = (uint32_t)(c - i0);
+                const uint32_t c = off - t * d_in;
+                const uint32_t part = one_part ? 0u : div_small(c, i_span, inv_span);
+                before += part < (uint32_t)p;
+                if (part == (uint32_t)p) {
+                    col[k] = c - (uint32_t)i0;
                     tl[k] = t;
                     atomicAdd(&cnt[col[k]], 1u);
                 }
             }
         }
-        uint32_t n_before;
-        block_exclusive_scan<kPlanThreads>(before, s_tot, &n_before);  // also orders the counts
+        // The planner's prefix sums take one barrier each (scan1, buffers alternating) and carry
+        // several small counts packed into one word; each field's bound is stated where it is packed.
+        uint32_t n_before = 0u;
+        if (a.n_parts > 1) (void)scan1(before, s_tot[0], &n_before);  // also orders the counts
+        else __syncthreads();  // the feature counts are complete
         const uint32_t base = c0 + n_before;
         const int f0 = 2 * threadIdx.x;
         const uint32_t n0 = f0 < ni ? cnt[f0] : 0u, n1 = f0 + 1 < ni ? cnt[f0 + 1] : 0u;
         // Matrix-core columns (cols > 0): the features with the most entries, at most cols of them
         // and at least 2 entries each; ties at the cut go to the lower feature index.  tau is the
         // smallest count with #{count >= tau} <= cols; features with tau - 1 entries fill the rest.
-        bool k0 = false, k1 = false;
-        uint32_t n_cols = 0;
+        // Any t > n / (cols + 1) qualifies (cols + 1 features of t entries would exceed the round's
+        // n entries), so tau lies in [2, n / (cols + 1) + 1]: at most 125 for rounds of 4096.
+        uint32_t tau = 0xffffffffu;
         if (a.cols > 0) {
-            // 8-way search: seven probes per step, counted by wave ballots, one barrier a step
-            uint32_t lo = 2, hi = (uint32_t)kRoundMax + 1;
+            // 16-way search: fifteen probes per step, counted by wave ballots, one barrier a step
+            uint32_t lo = 2, hi = max(2u, (c1 - c0) / (a.cols + 1) + 1);
             for (int it = 0; lo < hi; ++it) {
                 const uint32_t span_ = hi - lo;
-                uint32_t pt[7];
 #pragma unroll
-                for (int i = 0; i < 7; ++i) {
-                    pt[i] = lo + (span_ * (uint32_t)(i + 1)) / 8;
-                    const uint32_t m = (uint32_t)__popcll(__ballot(n0 >= pt[i])) + (uint32_t)__popcll(__ballot(n1 >= pt[i]));
+                for (int i = 0; i < 15; ++i) {
+                    const uint32_t pt = lo + (span_ * (uint32_t)(i + 1)) / 16;
+                    const uint32_t m = (uint32_t)__popcll(__ballot(n0 >= pt)) + (uint32_t)__popcll(__ballot(n1 >= pt));
                     if ((threadIdx.x & 63) == 0) s_probe[it & 1][i][threadIdx.x >> 6] = m;
                 }
                 __syncthreads();
-                uint32_t nlo = lo, nhi = hi;
-                bool found = false;
+                // lane i < 15 totals probe i; the counts fall as the probes rise, so the probes within
+                // the cap form a suffix and the first of them is the new upper end
+                const int ln = threadIdx.x & 63;
+                uint32_t m = 0;
 #pragma unroll
-                for (int i = 0; i < 7; ++i) {
-                    uint32_t m = 0;
-#pragma unroll
-                    for (int w = 0; w < kPlanThreads / 64; ++w) m += s_probe[it & 1][i][w];
-                    if (!found && m <= a.cols) {
-                        nhi = pt[i];
-                        found = true;
-                    } else if (!found) {
-                        nlo = pt[i] + 1;
-                    }
-                }
+                for (int w = 0; w < kPlanThreads / 64; ++w) m += s_probe[it & 1][min(ln, 14)][w];
+                const uint64_t ok = __ballot(ln < 15 && m <= a.cols);
+                const int i0 = ok ? __ffsll((unsigned long long)ok) - 1 : 15;
+                const uint32_t nlo = i0 > 0 ? lo + (span_ * (uint32_t)i0) / 16 + 1 : lo;
+                const uint32_t nhi = i0 < 15 ? lo + (span_ * (uint32_t)(i0 + 1)) / 16 : hi;
                 lo = nlo;
                 hi = max(nhi, nlo);
             }
-            const uint32_t tau = lo;
-            uint32_t n_above, n_tie;
-            (void)block_exclusive_scan<kPlanThreads>((n0 >= tau) + (n1 >= tau), s_tot, &n_above);
-            const bool t0 = tau > 2 && n0 == tau - 1, t1 = tau > 2 && n1 == tau - 1;
-            const uint32_t rt = block_exclusive_scan<kPlanThreads>(t0 + t1, s_tot, &n_tie);
-            const uint32_t room = a.cols - n_above;
-            k0 = n0 >= tau || (t0 && rt < room);
-            k1 = n1 >= tau || (t1 && rt + t0 < room);
-            const uint32_t sc = block_exclusive_scan<kPlanThreads>(k0 + k1, s_tot, &n_cols);
+            tau = lo;
+        }
+        bool k0 = false, k1 = false;
+        uint32_t n_cols, se, tot_e, tot_p;
+        {
+            // features at or above the cut (total <= cols <= 32: bits 0..5), features one below it
+            // (<= 1024 features: bits 6..16), entries (<= 4096: bits 17..31)
+            const uint32_t a0 = n0 >= tau, a1 = n1 >= tau;
+            const uint32_t t0 = tau > 2 && tau != 0xffffffffu && n0 == tau - 1, t1 = tau > 2 && tau != 0xffffffffu && n1 == tau - 1;
+            uint32_t tot;
+            const uint32_t x = scan1(a0 + a1 + ((t0 + t1) << 6) + ((n0 + n1) << 17), s_tot[1], &tot);
+            const uint32_t room = a.cols - (tot & 63u), rt = (x >> 6) & 2047u;
+            se = x >> 17;
+            tot_e = tot >> 17;
+            k0 = a0 || (t0 && rt < room);
+            k1 = a1 || (t1 && rt + t0 < room);
+            // column features (<= cols: bits 0..5) and the entries that go to pieces (<= 4096: 6..31)
+            const uint32_t m0 = k0 ? 0u : n0, m1 = k1 ? 0u : n1;
+            const uint32_t y = scan1(k0 + k1 + ((m0 + m1) << 6), s_tot[0], &tot);
+            n_cols = tot & 63u;
+            tot_p = tot >> 6;
+            const uint32_t sc = y & 63u;
             if (f0 < ni) colh[f0] = k0 ? sc + 1 : 0u;
             if (f0 + 1 < ni) colh[f0 + 1] = k1 ? sc + k0 + 1 : 0u;
         }
-        // prefix sums over the features (two per thread): bucket starts; then, with the piece
-        // length fixed by the part's piece-bound entry count, heavy-piece starts (= partial-sum
-        // slots), light piece positions and heavy-record positions.  Heavy pieces come first in the
-        // piece list (after the column records), so the longest work starts first.
+        // bucket starts; then, with the piece length fixed by the part's piece-bound entry count,
+        // heavy-piece starts (= partial-sum slots), light piece positions and heavy-record
+        // positions.  Heavy pieces come first in the piece list (after the column records), so the
+        // longest work starts first.
         uint32_t piece;
+        float inv_piece;
         {
             const uint32_t m0 = k0 ? 0u : n0, m1 = k1 ? 0u : n1;  // entries that go to pieces
-            uint32_t tot_e, tot_p, tot_h, tot_l, tot_x;
-            const uint32_t se = block_exclusive_scan<kPlanThreads>(n0 + n1, s_tot, &tot_e);
-            (void)block_exclusive_scan<kPlanThreads>(m0 + m1, s_tot, &tot_p);
             // pieces of heavy features number < 2 tot_p / piece <= slot_cap, and heavy features
             // < tot_p / piece <= groups
             piece = max((tot_p + a.groups - 1) / a.groups, (2 * tot_p + a.slot_cap - 1) / a.slot_cap);
             piece = min(max(piece, (uint32_t)kMinPiece), 255u);
-            const uint32_t p0 = (m0 + piece - 1) / piece, p1 = (m1 + piece - 1) / piece;
+            inv_piece = 1.f / (float)piece;  // divisions of counts < 2^25: exact with div_small
+            const uint32_t p0 = div_small(m0 + piece - 1, piece, inv_piece), p1 = div_small(m1 + piece - 1, piece, inv_piece);
             const uint32_t h0 = p0 > 1 ? p0 : 0u, h1 = p1 > 1 ? p1 : 0u;
             const uint32_t l0 = p0 == 1, l1 = p1 == 1;
-            const uint32_t sh = block_exclusive_scan<kPlanThreads>(h0 + h1, s_tot, &tot_h);
-            const uint32_t sl = block_exclusive_scan<kPlanThreads>(l0 + l1, s_tot, &tot_l);
-            const uint32_t sx = block_exclusive_scan<kPlanThreads>((p0 > 1) + (p1 > 1), s_tot, &tot_x);
+            // heavy pieces (<= slot_cap <= 512: bits 0..9), light pieces (<= 1024 features:
+            // bits 10..20), heavy features (<= 512: bits 21..31)
+            uint32_t tot;
+            const uint32_t z = scan1(h0 + h1 + ((l0 + l1) << 10) + (((p0 > 1) + (p1 > 1)) << 21), s_tot[1], &tot);
+            const uint32_t sh = z & 1023u, sl = (z >> 10) & 2047u, sx = z >> 21;
+            const uint32_t tot_h = tot & 1023u, tot_l = (tot >> 10) & 2047u, tot_x = tot >> 21;
             if (f0 < ni) {
                 cstart[f0] = se; hstart[f0] = sh; lstart[f0] = tot_h + sl; hidx[f0] = sx;
                 if (a.cols == 0) colh[f0] = 0u;
@@ -377,7 +453,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
         for (int k = 0; k < EPT; ++k) {
             if (col[k] != 0xffffffffu) {
                 const uint32_t pos = base + cstart[col[k]] + atomicAdd(&ccur[col[k]], 1u);
-                const uint32_t v = val[k];
+                const uint32_t v = entry_value<VK>(a, val[k], c0 + threadIdx.x + k * kPlanThreads);
                 if (f32)
                     static_cast<uint2 *>(a.ent)[pos] = make_uint2(tl[k], v);
                 else  // a column feature's entries carry 1 + its column in bits 26..31
@@ -390,7 +466,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
                 a.task[base + hc - 1] = make_uint2((uint32_t)c, 0u);
                 continue;
             }
-            const uint32_t npc = (n + piece - 1) / piece;
+            const uint32_t npc = div_small(n + piece - 1, piece, inv_piece);
             const uint32_t tb = base + n_cols;  // pieces follow the column records
             if (npc == 1) a.task[tb + lstart[c]] = make_uint2((uint32_t)c | (kDirect << 16), (cstart[c] << 8) | n);
             if (npc < 2) continue;
@@ -1403,10 +1479,17 @@ int launch_grad(const StacrGradArgs &a, const GPlan &p, char *ws, const size_t *
         pa.rhdr = reinterpret_cast<RoundHdr *>(ws + off[GW_RHDR]);
         pa.bhdr = reinterpret_cast<BlockHdr *>(ws + off[GW_BHDR]);
         const dim3 pg((unsigned)p.n_blocks, (unsigned)p.n_parts);
-        if (a.index_bytes == 8)
-            stacr_launch("k_dw_plan", s, [&] { k_dw_plan<1><<<pg, kPlanThreads, 0, s>>>(pa); });
-        else
-            stacr_launch("k_dw_plan", s, [&] { k_dw_plan<0><<<pg, kPlanThreads, 0, s>>>(pa); });
+        auto plan = [&](auto idx64, auto vk) {
+            stacr_launch("k_dw_plan", s, [&] { k_dw_plan<decltype(idx64)::value, decltype(vk)::value><<<pg, kPlanThreads, 0, s>>>(pa); });
+        };
+        auto plan_vk = [&](auto idx64) {
+            if (a.bits == 8) plan(idx64, std::integral_constant<int, kValI8>{});
+            else if (a.bits == 4) plan(idx64, std::integral_constant<int, kValI4>{});
+            else if (a.val_dtype == STACR_DTYPE_F32) plan(idx64, std::integral_constant<int, kVal32>{});
+            else plan(idx64, std::integral_constant<int, kVal16>{});
+        };
+        if (a.index_bytes == 8) plan_vk(std::integral_constant<int, 1>{});
+        else plan_vk(std::integral_constant<int, 0>{});
         f.ent = pa.ent;
         f.task = pa.task;
         f.heavy = pa.heavy;
