@@ -1093,6 +1093,10 @@ __device__ __forceinline__ SelState fold_select(const uint32_t (&hw)[HC], SelSta
 // Ordered compaction (batched).  Elements are enumerated as (iteration, slot, thread, element),
 // which is ascending flat index: one multi-value block scan per batch gives every thread the
 // number of survivors (gt in the low half, ties in the high half) before each of its vectors.
+// Loads go out in the order they are waited for (the selection's histogram words or the earlier
+// workgroups' counts, then X, C and the basis); the offset sums come after the residuals, so the
+// loads they need are hidden behind that arithmetic; survivors are kept as per-iteration bit masks
+// and only the set bits are visited when writing.
 template <int DT, int R, int V, int HC>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) void k_emit_b(SaveGeom g, FastGeom fg, const typename Act<DT>::T *__restrict__ x,
                                                    const float *__restrict__ qp,
@@ -1104,19 +1108,38 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
 {
     constexpr int NB = Batch<R>::NB;
     constexpr bool kFold = DT == STACR_DTYPE_BF16;  // bf16: the selection ends here (no count pass)
+    static_assert(V <= 8, "survivor masks hold 8 elements per vector");
     __shared__ uint32_t s_wt[kWaves * NB];
     __shared__ uint32_t s_off[kWaves];
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
     const int64_t w = blockIdx.x - chunk * g.wgs_per_chunk;
     const int64_t wg0 = chunk * g.wgs_per_chunk;  // the chunk's first workgroup
-    SelState st;
+    const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
+    const bool col_ok = col < g.d;
+    const bool has_rows = row0 < row_end;
+    uint32_t hw[kFold ? HC : 1];
     WgCount pre[2];
     if constexpr (kFold) {
-        uint32_t hw[HC];
         const uint32_t *h1 = hist + (chunk * 3 + 1) * HC * kBins + ((threadIdx.x & 15) << 7);
 #pragma unroll
         for (int c = 0; c < HC; ++c) hw[c] = h1[c * kBins];
+    } else {
+        // counts of the chunk's earlier workgroups (at most two per thread in the usual geometry;
+        // the offset block reads any further ones itself)
+#pragma unroll
+        for (int k = 0; k < 2; ++k) pre[k] = counts[wg0 + min((int64_t)threadIdx.x + k * kBlock, w)];
+    }
+    FastLoads<DT, R, V, true> ld;
+    if (has_rows) ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
+    float q[V][R];
+    basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
+    SelState st;
+    uint32_t rhi[2] = {0u, 0u}, rlo[2] = {0u, 0u};
+    const uint32_t *fhi = fold, *flo = fold;
+    if constexpr (kFold) {
         SelState sel1;
         st = fold_select<HC>(hw, state[chunk * 3 + 0], &sel1);
         if (w == 0 && threadIdx.x == 0) {
@@ -1125,128 +1148,119 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
         }
         // the earlier workgroups' counts above / equal to the threshold (clamped reads, masked at use)
         const uint32_t b1 = (st.prefix >> 16) & 15u;
-        const uint32_t *hi = fold + (int64_t)(b1 + 1) * fold_stride + wg0, *lo = fold + (int64_t)b1 * fold_stride + wg0;
+        fhi = fold + (int64_t)(b1 + 1) * fold_stride + wg0;
+        flo = fold + (int64_t)b1 * fold_stride + wg0;
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             const int64_t v = min((int64_t)threadIdx.x + k * kBlock, w);
-            const uint32_t a = hi[v], b = lo[v];
-            pre[k] = WgCount{a, b - a};
+            rhi[k] = fhi[v];
+            rlo[k] = flo[v];
         }
     } else {
         st = state[chunk * 3 + 2];
-        // counts of the chunk's earlier workgroups (at most two per thread in the usual geometry;
-        // the offset block reads any further ones itself)
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int64_t v = threadIdx.x + k * kBlock;
-            pre[k] = counts[wg0 + min(v, w)];
-        }
     }
     const uint32_t mk = *maxkey;
-    const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
-    const bool col_ok = col < g.d;
-    const bool has_rows = row0 < row_end;
-    FastLoads<DT, R, V, true> ld;
-    if (has_rows) ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
-    float q[V][R];
-    basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
-    // the workgroup's output offset and tie budget (as wg_offset)
+    const uint32_t T = st.prefix;
+    const float amax = Act<DT>::rnd(__uint_as_float(mk));
+    const float scale = o.bits ? quant_scale(mk, o.bits, amax) : 1.f;
+    if (!to_list && blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
+    if (!has_rows) return;  // uniform: a trailing workgroup with no rows writes nothing
+    basis_mask<R, V>(col_ok, q);
+    float r[NB][V];
+    uint32_t msk[NB];  // survivors of iteration i: bits 0..7 above T, bits 8..15 equal to T
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const bool live = col_ok && ld.rows[i] < row_end;
+        float xv[V], ci[R];
+        ld.x_at(i, live, xv);
+        ld.coeff_row(i, coeff, g.rank, row_end, fg.c_vec != 0, ci);
+        batch_residual<DT, R, V>(xv, ci, q, r[i]);
+        uint32_t m = 0u;
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            const uint32_t key = __float_as_uint(r[i][e]) & 0x7fffffffu;
+            m |= (live && key > T) ? 1u << e : 0u;
+            m |= (live && key == T) ? 0x100u << e : 0u;
+        }
+        msk[i] = m;
+    }
+    // the workgroup's output offset and tie budget
     WgOffset wo;
     {
         uint32_t gt = 0u, eq = 0u;
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             const int64_t v = threadIdx.x + k * kBlock;
-            gt += v < w ? pre[k].gt : 0u;
-            eq += v < w ? pre[k].eq : 0u;
+            const WgCount c = kFold ? WgCount{rhi[k], rlo[k] - rhi[k]} : pre[k];
+            gt += v < w ? c.gt : 0u;
+            eq += v < w ? c.eq : 0u;
         }
-        const uint32_t b1 = (st.prefix >> 16) & 15u;
-        const uint32_t *hi = fold + (int64_t)(b1 + 1) * fold_stride + wg0, *lo = fold + (int64_t)b1 * fold_stride + wg0;
         for (int64_t v = threadIdx.x + 2 * kBlock; v < w; v += kBlock) {
-            const WgCount c = kFold ? WgCount{hi[v], lo[v] - hi[v]} : counts[wg0 + v];
+            const WgCount c = kFold ? WgCount{fhi[v], flo[v] - fhi[v]} : counts[wg0 + v];
             gt += c.gt;
             eq += c.eq;
         }
         const uint32_t gt_before = block_sum(gt, s_off);
         const uint32_t eq_before = block_sum(eq, s_off);
-        const WgCount mine = kFold ? WgCount{hi[w], lo[w] - hi[w]} : counts[wg0 + w];
+        const WgCount mine = kFold ? WgCount{fhi[w], flo[w] - fhi[w]} : counts[wg0 + w];
         const uint32_t take = eq_before >= st.need ? 0u : min(mine.eq, st.need - eq_before);
         wo = WgOffset{(uint32_t)chunk * chunk_k + gt_before + min(st.need, eq_before), take};
     }
-    const uint32_t T = st.prefix;
-    const float amax = Act<DT>::rnd(__uint_as_float(mk));
-    const float scale = o.bits ? quant_scale(mk, o.bits, amax) : 1.f;
-    if (!to_list && blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
-    if (!has_rows) return;
-    basis_mask<R, V>(col_ok, q);
-    {   // the workgroup's rows are one batch
-        float r[NB][V];
-        uint32_t cnt[NB], incl[NB];
+    uint32_t cnt[NB], incl[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        cnt[i] = (uint32_t)__popc(msk[i] & 0xffu) | ((uint32_t)__popc(msk[i] >> 8) << 16);
+        incl[i] = cnt[i];
+    }
+    // inclusive scans over the wave's lanes, one per iteration
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
-            cnt[i] = 0u;
-            const bool live = col_ok && ld.rows[i] < row_end;
-            float xv[V], ci[R];
-            ld.x_at(i, live, xv);
-            ld.coeff_row(i, coeff, g.rank, row_end, fg.c_vec != 0, ci);
-            batch_residual<DT, R, V>(xv, ci, q, r[i]);
-#pragma unroll
-            for (int e = 0; e < V; ++e) {
-                const uint32_t key = __float_as_uint(r[i][e]) & 0x7fffffffu;
-                cnt[i] += live ? ((key > T) ? 1u : (key == T ? 0x10000u : 0u)) : 0u;
-            }
-            incl[i] = cnt[i];
+            const uint32_t y = __shfl_up(incl[i], off, 64);
+            if (lane >= off) incl[i] += y;
         }
-        // inclusive scans over the wave's lanes, one per iteration
+    }
+    if (lane == 63)
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
+        for (int i = 0; i < NB; ++i) s_wt[wave * NB + i] = incl[i];
+    __syncthreads();
+    uint32_t before_iter = 0u;  // survivors of the batch's earlier iterations (all waves)
 #pragma unroll
-            for (int i = 0; i < NB; ++i) {
-                const uint32_t y = __shfl_up(incl[i], off, 64);
-                if (lane >= off) incl[i] += y;
-            }
+    for (int i = 0; i < NB; ++i) {
+        uint32_t waves_before = 0u, iter_total = 0u;
+#pragma unroll
+        for (int wv = 0; wv < kWaves; ++wv) {
+            const uint32_t t = s_wt[wv * NB + i];
+            waves_before += wv < wave ? t : 0u;
+            iter_total += t;
         }
-        if (lane == 63)
+        const uint32_t ex = before_iter + waves_before + incl[i] - cnt[i];
+        uint32_t gb = ex & 0xffffu, eb = ex >> 16;
+        // this vector's survivors in element order (the lowest remaining element first)
+        for (uint32_t m = msk[i]; m != 0u;) {
+            const int e = __builtin_ctz((m | (m >> 8)) & 0xffu);
+            const uint32_t is_gt = (m >> e) & 1u, is_eq = (m >> (8 + e)) & 1u;
+            m &= ~((1u << e) | (0x100u << e));
+            if (is_gt || eb < wo.take) {
+                const uint32_t pos = wo.off + gb + min(eb, wo.take);
+                float rv = r[i][0];
 #pragma unroll
-            for (int i = 0; i < NB; ++i) s_wt[wave * NB + i] = incl[i];
-        __syncthreads();
-        uint32_t before_iter = 0u;  // survivors of the batch's earlier iterations (all waves)
-#pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            uint32_t waves_before = 0u, iter_total = 0u;
-#pragma unroll
-            for (int wv = 0; wv < kWaves; ++wv) {
-                const uint32_t t = s_wt[wv * NB + i];
-                waves_before += wv < wave ? t : 0u;
-                iter_total += t;
-            }
-            const uint32_t ex = before_iter + waves_before + incl[i] - cnt[i];
-            if (cnt[i]) {
-                uint32_t gb = ex & 0xffffu, eb = ex >> 16;
-#pragma unroll
-                for (int e = 0; e < V; ++e) {
-                    const uint32_t key = __float_as_uint(r[i][e]) & 0x7fffffffu;
-                    const bool is_gt = key > T, is_eq = key == T;
-                    if (is_gt || (is_eq && eb < wo.take)) {
-                        const uint32_t pos = wo.off + gb + min(eb, wo.take);
-                        const uint32_t flat = (uint32_t)(ld.rows[i] * g.d + col + e);
-                        if (pos >= o.cap) {
-                            // unreachable when the counts are consistent; never write out of bounds
-                        } else if (to_list) {
-                            o.list_rbits[pos] = __float_as_uint(r[i][e]);
-                            o.list_idx[pos] = flat;
-                        } else {
-                            write_entry<DT>(o, pos, flat, r[i][e], scale);
-                        }
-                    }
-                    gb += is_gt;
-                    eb += is_eq;
+                for (int k = 1; k < V; ++k) rv = e == k ? r[i][k] : rv;
+                const uint32_t flat = (uint32_t)(ld.rows[i] * g.d + col + e);
+                if (pos >= o.cap) {
+                    // unreachable when the counts are consistent; never write out of bounds
+                } else if (to_list) {
+                    o.list_rbits[pos] = __float_as_uint(rv);
+                    o.list_idx[pos] = flat;
+                } else {
+                    write_entry<DT>(o, pos, flat, rv, scale);
                 }
             }
-            before_iter += iter_total;
+            gb += is_gt;
+            eb += is_eq;
         }
+        before_iter += iter_total;
     }
 }
 
