@@ -691,14 +691,19 @@ struct FastLoads {
     __device__ __forceinline__ void issue(const SaveGeom &g, int slot, int64_t base, int64_t row_end, int64_t colc,
                                           const T *__restrict__ x, const T *__restrict__ coeff, bool cvec)
     {
-        batch_rows<R>(g, base, slot, rows);  // callers issue only when the workgroup has rows (row_end > base)
+        // rows clamped to row_end - 1, a row of the matrix even for a trailing workgroup with no rows
+        // (row_end is at least 1)
+        batch_rows<R>(g, base, slot, rows);
 #pragma unroll
         for (int i = 0; i < NB; ++i)
             raw[i] = *reinterpret_cast<const uint4 *>(x + min(rows[i], row_end - 1) * g.d + colc);
-        if (kCVec && coeff && cvec) {
+        if constexpr (kCVec) {
+            // without whole C rows (cvec false) the same loads read the row's start in X instead
+            // (valid memory: a batched-path X row is wider than NWC vectors) and are not used
 #pragma unroll
             for (int i = 0; i < NB; ++i) {
-                const uint4 *src = reinterpret_cast<const uint4 *>(coeff + min(rows[i], row_end - 1) * R);
+                const int64_t row = min(rows[i], row_end - 1);
+                const uint4 *src = reinterpret_cast<const uint4 *>(cvec ? coeff + row * R : x + row * g.d);
 #pragma unroll
                 for (int k = 0; k < NWC; ++k) craw[i][k] = src[k];
             }
@@ -944,7 +949,9 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
     const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
     const bool col_ok = col < g.d;
     FastLoads<DT, R, V, true> ld;
-    if (has_rows) ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
+    // issued whether or not the workgroup has rows: a load under a branch makes every later wait
+    // count as if it had not been issued, so waiting for the histogram words would wait for X too
+    ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
     float q[V][R];
     basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
     for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
@@ -1027,7 +1034,9 @@ __global__ __launch_bounds__(kBlock) void k_count_b(SaveGeom g, FastGeom fg, con
     const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
     const bool col_ok = col < g.d;
     FastLoads<DT, R, V, true> ld;
-    if (has_rows) ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
+    // issued whether or not the workgroup has rows: a load under a branch makes every later wait
+    // count as if it had not been issued, so waiting for the histogram words would wait for X too
+    ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
     float q[V][R];
     basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
     SelState sel = block_select_pre(kLvl, hp, sp.prefix, sp.need, s_tot, &s_res);
@@ -1133,7 +1142,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
         for (int k = 0; k < 2; ++k) pre[k] = counts[wg0 + min((int64_t)threadIdx.x + k * kBlock, w)];
     }
     FastLoads<DT, R, V, true> ld;
-    if (has_rows) ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
+    // issued whether or not the workgroup has rows: a load under a branch makes every later wait
+    // count as if it had not been issued, so waiting for the histogram words would wait for X too
+    ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
     float q[V][R];
     basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
     SelState st;
