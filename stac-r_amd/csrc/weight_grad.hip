@@ -423,6 +423,24 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
             // < tot_p / piece <= groups
             piece = max((tot_p + a.groups - 1) / a.groups, (2 * tot_p + a.slot_cap - 1) / a.slot_cap);
             piece = min(max(piece, (uint32_t)kMinPiece), 255u);
+            if (a.cols > 0) {
+                // Shorter pieces when the exact counts allow: a piece of 4 entries is one batch of
+                // the streaming kernel, so the waves' piece work evens out.  For P = 4, 8, 16 the
+                // partial-sum slots sum(ceil(m / P) over features with m > P) (<= 1843, 967, 496:
+                // 11, 10 and 9 bits) and the split features #(m > P) (<= 819, 455, 240: 10, 9 and 8
+                // bits) of the round, packed two words.
+                auto slots = [](uint32_t m, int sh) { return m > (1u << sh) ? (m + (1u << sh) - 1) >> sh : 0u; };
+                const uint32_t w1 = (slots(m0, 2) + slots(m1, 2)) | ((slots(m0, 3) + slots(m1, 3)) << 11) |
+                                    ((slots(m0, 4) + slots(m1, 4)) << 21);
+                const uint32_t w2 = ((m0 > 4) + (m1 > 4)) | (((m0 > 8) + (m1 > 8)) << 10) | (((m0 > 16) + (m1 > 16)) << 19);
+                uint32_t t1, t2;
+                (void)scan1(w1, s_tot[1], &t1);
+                (void)scan1(w2, s_tot[0], &t2);
+                const uint32_t hcap = min(a.groups, (uint32_t)kHeavyCap);
+                if ((t1 & 2047u) <= a.slot_cap && (t2 & 1023u) <= hcap) piece = 4;
+                else if (((t1 >> 11) & 1023u) <= a.slot_cap && ((t2 >> 10) & 511u) <= hcap) piece = min(piece, 8u);
+                else if ((t1 >> 21) <= a.slot_cap && (t2 >> 19) <= hcap) piece = min(piece, 16u);
+            }
             inv_piece = 1.f / (float)piece;  // divisions of counts < 2^25: exact with div_small
             const uint32_t p0 = div_small(m0 + piece - 1, piece, inv_piece), p1 = div_small(m1 + piece - 1, piece, inv_piece);
             const uint32_t h0 = p0 > 1 ? p0 : 0u, h1 = p1 > 1 ? p1 : 0u;
@@ -988,7 +1006,8 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
 //     each column's sums (scaled) into S, and the tile is zeroed again after the round.
 constexpr int kMCols = 32;            // column features per round (two 16-column tiles)
 constexpr int kMTB = 512;             // token rows per block
-constexpr int kMPitch = kMTB + 8;     // elements per Gt / Bt row; Gt element kMTB stays zero
+constexpr int kMPitch = kMTB + 8;     // elements per Bt row
+constexpr int kMGRows = kMTB + 1;     // G tile rows: the block's kMTB rows, then a row of zeros
 constexpr int kMSlotCap = 64;         // partial sums of heavy pieces
 constexpr int kMHdrRing = 64;         // block headers held in LDS
 constexpr int kMTaskCap = kMaxISlab + kMSlotCap + kMCols;
@@ -997,8 +1016,8 @@ constexpr int kMTaskPT = (kMTaskCap + kBwdThreads - 1) / kBwdThreads;
 template <int R>
 struct MfmaLds {
     static constexpr size_t s_acc = 0;                                            // [1024][16] f32
-    static constexpr size_t s_gt = s_acc + (size_t)kMaxISlab * kAccPitch * 4;      // [16][kMPitch]
-    static constexpr size_t s_bc = s_gt + (size_t)kOSlab * kMPitch * 2;            // [R][kMPitch]
+    static constexpr size_t s_gr = s_acc + (size_t)kMaxISlab * kAccPitch * 4;      // [kMGRows][16] row-major
+    static constexpr size_t s_bc = s_gr + (size_t)kMGRows * kOSlab * 2;            // [R][kMPitch]
     static constexpr size_t s_bh = s_bc + (size_t)R * kMPitch * 2;                 // [kMCols][kMPitch]
     static constexpr size_t s_ent = s_bh + (size_t)kMCols * kMPitch * 2;           // [kRoundMax] u32
     static constexpr size_t s_task = s_ent + (size_t)kRoundMax * 4;                // [kMTaskCap]
@@ -1007,14 +1026,23 @@ struct MfmaLds {
     static constexpr size_t s_hdr = s_slot + (size_t)kMSlotCap * kOSlab * 4;       // [kMHdrRing]
     static constexpr size_t bytes = s_hdr + (size_t)kMHdrRing * sizeof(BlockHdr);
     // after the stream, over the tiles: per-wave partial fixed tiles [16][16][16] f32, then M
-    static constexpr size_t s_red = s_gt;
+    static constexpr size_t s_red = s_gr;
     static constexpr size_t s_mfin = s_red + (size_t)16 * 256 * 4;
     static_assert(s_mfin + (size_t)kOSlab * (R + 1) * 4 <= s_ent, "reduction fits the tile region");
-    static_assert(s_gt % 16 == 0 && s_bc % 16 == 0 && s_bh % 16 == 0 && (kMPitch * 2) % 16 == 0,
+    static_assert(s_gr % 16 == 0 && s_bc % 16 == 0 && s_bh % 16 == 0 && (kMPitch * 2) % 16 == 0,
                   "16-byte operand rows");
 };
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16 (gfx950): four 16-bit values, transposed across each 16-lane group (see the
+// matrix-core kernel's operand reads); the bits are moved unchanged, so it serves fp16 as well
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t *p)
+{
+    typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+    bf16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4 *)(p));
+    return __builtin_bit_cast(uint2, v);
+}
 
 template <int DT>
 __device__ __forceinline__ f32x4 mfma_16x16x32(uint4 a, uint4 b, f32x4 c)
@@ -1043,7 +1071,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
     extern __shared__ float lds[];
     char *base = reinterpret_cast<char *>(lds);
     float *acc = reinterpret_cast<float *>(base + L::s_acc);
-    uint16_t *gt = reinterpret_cast<uint16_t *>(base + L::s_gt);
+    uint16_t *gr = reinterpret_cast<uint16_t *>(base + L::s_gr);
     uint16_t *bc = reinterpret_cast<uint16_t *>(base + L::s_bc);
     uint16_t *bh = reinterpret_cast<uint16_t *>(base + L::s_bh);
     uint32_t *l_ent = reinterpret_cast<uint32_t *>(base + L::s_ent);
@@ -1069,8 +1097,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
     const float qscale = (sparse && a.bits) ? a.scale[0] : 1.f;
 
     for (int i = threadIdx.x; i < ni * kAccPitch; i += kBwdThreads) acc[i] = 0.f;
-    for (int i = threadIdx.x; i < kOSlab * (kMPitch - TB); i += kBwdThreads)
-        gt[(i / (kMPitch - TB)) * kMPitch + TB + i % (kMPitch - TB)] = 0;
+    if (threadIdx.x < kOSlab) gr[TB * kOSlab + threadIdx.x] = 0;  // the zero row
     for (int i = threadIdx.x; i < kMCols * kMPitch / 8; i += kBwdThreads)
         reinterpret_cast<uint4 *>(bh)[i] = make_uint4(0u, 0u, 0u, 0u);
 
@@ -1130,7 +1157,17 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
         if (threadIdx.x < kHeavyCap) l_heavy[threadIdx.x] = st.heavy;
     };
 
-    // One piece's entries [e_lo, e_lo + n) into pa (this thread's 4 outputs), G from Gt: four
+    // Matrix-core operand Gᵀ[o][t0 + 8 (lane / 16) .. + 7], o = lane % 16, from the row-major tile by
+    // two transposing reads (ds_read_b64_tr_b16): in a 16-lane group, lane n receives value j from
+    // position n % 4 of the 8 bytes lane 4 j + n / 4 addresses (checked on the GPU), so lane m
+    // addresses row r0 + m / 4, outputs 4 (m % 4) .. + 3, and lane n gets G[r0 + j][n], j = 0..3.
+    auto g_operand = [&](int t0) -> uint4 {
+        const uint16_t *p = gr + (t0 + 8 * (lane >> 4) + ((lane & 15) >> 2)) * kOSlab + (lane & 3) * 4;
+        const uint2 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 4 * kOSlab);
+        return make_uint4(lo.x, lo.y, hi.x, hi.y);
+    };
+
+    // One piece's entries [e_lo, e_lo + n) into pa (this thread's 4 outputs), G from the tile: four
     // entries per batch; entries past the piece read the zero column TB with value 0.
     auto piece_batch = [&](uint32_t e, uint32_t e_lo, uint32_t n, float (&pa)[OT]) {
         const uint32_t last = e_lo + (n ? n - 1 : 0u);
@@ -1143,9 +1180,10 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
         uint32_t gw[4][2];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const uint16_t *col = gt + (og * OT) * kMPitch + min((w[u] >> 16) & 0x3ffu, (uint32_t)TB);
-            gw[u][0] = (uint32_t)col[0] | ((uint32_t)col[kMPitch] << 16);
-            gw[u][1] = (uint32_t)col[2 * kMPitch] | ((uint32_t)col[3 * kMPitch] << 16);
+            // G[t][og * 4 .. + 3]: (o0, o0 + 1) and (o0 + 2, o0 + 3) as the dot products' pairs
+            const uint2 g2 = *reinterpret_cast<const uint2 *>(gr + min((w[u] >> 16) & 0x3ffu, (uint32_t)TB) * kOSlab + og * OT);
+            gw[u][0] = g2.x;
+            gw[u][1] = g2.y;
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -1184,7 +1222,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
             f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
             for (int s = 0; s < TB / 32; ++s) {
-                const uint4 av = *reinterpret_cast<const uint4 *>(gt + jj * kMPitch + 32 * s + k8);
+                const uint4 av = g_operand(32 * s);
                 const uint4 bv = *reinterpret_cast<const uint4 *>(bh + cj * kMPitch + 32 * s + k8);
                 d = mfma_16x16x32<DT>(av, bv, d);
             }
@@ -1244,7 +1282,6 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
         if (h.n_rounds) load_stage(sq, h.r0);
     }
     f32x4 accf = {0.f, 0.f, 0.f, 0.f};
-    uint32_t *gt32 = reinterpret_cast<uint32_t *>(gt);
     for (int64_t blk = 0; blk < n_blocks; ++blk) {
         const bool ra = blk * TB + 2 * tp < a.rows, rb = blk * TB + 2 * tp + 1 < a.rows;
         const bool rc = (og & 1) ? rb : ra;
@@ -1254,12 +1291,9 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
 #pragma unroll
         for (int k = 0; k < CQ; ++k) yc[k] = rc ? xq[k] : 0u;
         const BlockHdr bh_ = read_hdr(blk), hn = read_hdr(blk + 1);
-        // Gt[o][t..t+1] = (G[t][o], G[t+1][o]); Bt[j][t..t+1] = (C[t][j], C[t+1][j]) for j = og, og + 4
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            gt32[((og * OT + 2 * k) * kMPitch + 2 * tp) / 2] = __builtin_amdgcn_perm(cb[k], ca[k], 0x05040100u);
-            gt32[((og * OT + 2 * k + 1) * kMPitch + 2 * tp) / 2] = __builtin_amdgcn_perm(cb[k], ca[k], 0x07060302u);
-        }
+        // G rows 2 tp and 2 tp + 1, outputs og * 4 .. + 3, into the row-major tile
+        *reinterpret_cast<uint2 *>(gr + (2 * tp) * kOSlab + og * OT) = make_uint2(ca[0], ca[1]);
+        *reinterpret_cast<uint2 *>(gr + (2 * tp + 1) * kOSlab + og * OT) = make_uint2(cb[0], cb[1]);
         {   // Bt[j][t] = C[t][j] for this thread's row and R / 2 columns
             const int t = 2 * tp + (og & 1), j0 = (R / 2) * (og >> 1);
 #pragma unroll
@@ -1281,7 +1315,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
         __syncthreads();  // tiles and the first round staged
         {   // fixed tile: rows 32 wave .. 32 wave + 31 of the block
             const int jj = lane & 15, kk = 32 * wave + 8 * (lane >> 4);
-            const uint4 av = *reinterpret_cast<const uint4 *>(gt + jj * kMPitch + kk);
+            const uint4 av = g_operand(32 * wave);
             uint4 bv = make_uint4(0u, 0u, 0u, 0u);
             if (jj < R) bv = *reinterpret_cast<const uint4 *>(bc + jj * kMPitch + kk);
             else if (jj == R) bv = make_uint4(kOne | kOne << 16, kOne | kOne << 16, kOne | kOne << 16, kOne | kOne << 16);
