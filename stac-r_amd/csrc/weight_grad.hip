@@ -49,6 +49,16 @@ constexpr uint32_t kDirect = 0xffffu;                     // piece slot: add str
 constexpr int kTaskPT = (kTaskCap + kBwdThreads - 1) / kBwdThreads;  // staged pieces per thread
 constexpr int kHdrRing = 256;                             // block headers held in LDS
 static_assert(kHeavyCap <= kBwdThreads, "one heavy record per thread");
+// the matrix-core streaming kernel (k_dw_fused_mfma)
+constexpr int kMCols = 32;            // column features per round (two 16-column tiles)
+constexpr int kMTB = 512;             // token rows per block
+constexpr int kMPitch = kMTB + 8;     // elements per Bt row
+constexpr int kMGRows = kMTB + 1;     // G tile rows: the block's kMTB rows, then a row of zeros
+constexpr int kMSlotCap = 64;         // partial sums of heavy pieces
+constexpr int kMHdrRing = 64;         // block headers held in LDS
+constexpr int kMTaskCap = kMaxISlab + kMSlotCap + kMCols;
+constexpr int kMTaskPT = (kMTaskCap + kBwdThreads - 1) / kBwdThreads;
+static_assert(kMCols * kMPitch <= 0x8000, "a column entry's tile element fits 15 bits");
 
 // S row i holds the 16 outputs as four 16-byte chunks; chunk q sits at position q ^ (i & 3), which
 // spreads rows over the LDS banks while keeping every chunk 16-byte aligned.
@@ -179,7 +189,8 @@ struct PlanArgs {
     uint32_t slot_cap;       // partial-sum slots of the streaming kernel
     uint32_t cols;           // matrix-core columns per round (0: every feature goes to pieces)
     uint32_t max_rounds;     // rounds the header array holds
-    void *ent;               // [nnz] 16-bit G: t_local << 16 | value code (uint32);
+    void *ent;               // [nnz] 16-bit G: t_local << 16 | value code (uint32); a matrix-core
+                             //       column feature's entry: bit 31 | its Bt tile element << 16 | code;
                              //       fp32 G: {t_local, value bits} (uint2)
     uint2 *task;             // [nnz] column features {feature, 0} first, then pieces
                              //       {feature | slot << 16, entry offset << 8 | entries}
@@ -474,8 +485,11 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
                 const uint32_t v = entry_value<VK>(a, val[k], c0 + threadIdx.x + k * kPlanThreads);
                 if (f32)
                     static_cast<uint2 *>(a.ent)[pos] = make_uint2(tl[k], v);
-                else  // a column feature's entries carry 1 + its column in bits 26..31
-                    static_cast<uint32_t *>(a.ent)[pos] = (colh[col[k]] << 26) | (tl[k] << 16) | (v & 0xffffu);
+                else if (colh[col[k]])  // a column feature's entry: bit 31, then its element of the Bt tile
+                    static_cast<uint32_t *>(a.ent)[pos] =
+                        0x80000000u | (((colh[col[k]] - 1) * (uint32_t)kMPitch + tl[k]) << 16) | (v & 0xffffu);
+                else
+                    static_cast<uint32_t *>(a.ent)[pos] = (tl[k] << 16) | (v & 0xffffu);
             }
         }
         for (int c = threadIdx.x; c < ni; c += kPlanThreads) {
@@ -1004,14 +1018,6 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused(FusedArgs a)
 //   * column tiles, up to 32 column features whose integer codes are scattered into a zeroed
 //     Bt tile: waves 0 and 1 each run the 16 instructions of one 16-column tile per round, add
 //     each column's sums (scaled) into S, and the tile is zeroed again after the round.
-constexpr int kMCols = 32;            // column features per round (two 16-column tiles)
-constexpr int kMTB = 512;             // token rows per block
-constexpr int kMPitch = kMTB + 8;     // elements per Bt row
-constexpr int kMGRows = kMTB + 1;     // G tile rows: the block's kMTB rows, then a row of zeros
-constexpr int kMSlotCap = 64;         // partial sums of heavy pieces
-constexpr int kMHdrRing = 64;         // block headers held in LDS
-constexpr int kMTaskCap = kMaxISlab + kMSlotCap + kMCols;
-constexpr int kMTaskPT = (kMTaskCap + kBwdThreads - 1) / kBwdThreads;
 
 template <int R>
 struct MfmaLds {
@@ -1090,7 +1096,6 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
     const int ni = (int)(min(i0 + a.i_span, a.d_in) - i0);
     const int og = threadIdx.x % OG, tp = threadIdx.x / OG;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t ob = o0 + og * OT;
     const uint16_t *g = static_cast<const uint16_t *>(a.g);
     const uint16_t *coeff = static_cast<const uint16_t *>(a.coeff);
     const bool sparse = a.nnz > 0;
@@ -1110,16 +1115,28 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
     };
     auto read_hdr = [&](int64_t b) { return b < n_blocks ? l_hdr[b % kMHdrRing] : BlockHdr{}; };
 
-    // unconditional loads from clamped rows (the rows past the matrix are zeroed where used)
+    // unconditional loads from clamped rows (the rows past the matrix are zeroed where used): a
+    // uniform base row rb = min(block start, rows - 1) and a 32-bit row offset clamped to the
+    // last row, so the address arithmetic per thread is 32-bit
+    const uint32_t dout32 = (uint32_t)a.d_out;
+    auto block_base = [&](int64_t blk, int64_t &rb, uint32_t &lim) {
+        rb = min(blk * TB, a.rows - 1);
+        lim = (uint32_t)min(a.rows - 1 - rb, (int64_t)TB);
+    };
     auto load_grows = [&](int64_t blk, uint32_t (&w)[2][2]) {
-        const int64_t t = blk * TB + 2 * tp;
-        load_words<8>(g + min(t, a.rows - 1) * a.d_out + ob, w[0]);
-        load_words<8>(g + min(t + 1, a.rows - 1) * a.d_out + ob, w[1]);
+        int64_t rb;
+        uint32_t lim;
+        block_base(blk, rb, lim);
+        const uint16_t *gb = g + rb * a.d_out + o0;
+        load_words<8>(gb + min((uint32_t)(2 * tp), lim) * dout32 + og * OT, w[0]);
+        load_words<8>(gb + min((uint32_t)(2 * tp + 1), lim) * dout32 + og * OT, w[1]);
     };
     // thread (tp, og) loads C row 2 tp + (og & 1), columns [R / 2 (og >> 1), R / 2 (og >> 1) + R / 2)
     auto load_crow = [&](int64_t blk, uint32_t (&x)[CQ]) {
-        const int64_t t = blk * TB + 2 * tp + (og & 1);
-        load_words<4 * CQ>(coeff + min(t, a.rows - 1) * R + (R / 2) * (og >> 1), x);
+        int64_t rb;
+        uint32_t lim;
+        block_base(blk, rb, lim);
+        load_words<4 * CQ>(coeff + rb * R + min((uint32_t)(2 * tp + (og & 1)), lim) * R + (R / 2) * (og >> 1), x);
     };
     struct StageM {
         uint32_t ent[EPT];
@@ -1148,8 +1165,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
         for (int k = 0; k < EPT; ++k) {
             const uint32_t w = st.ent[k];
             l_ent[threadIdx.x + k * kBwdThreads] = w;
-            const uint32_t hc = w >> 26, t = (w >> 16) & 0x3ffu;
-            if (hc && hc <= (uint32_t)kMCols && t < (uint32_t)TB) bh[(hc - 1) * kMPitch + t] = (uint16_t)w;
+            if (w >> 31) bh[min((w >> 16) & 0x7fffu, (uint32_t)(kMCols * kMPitch - 1))] = (uint16_t)w;
         }
 #pragma unroll
         for (int k = 0; k < kMTaskPT; ++k)
@@ -1283,7 +1299,8 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
     }
     f32x4 accf = {0.f, 0.f, 0.f, 0.f};
     for (int64_t blk = 0; blk < n_blocks; ++blk) {
-        const bool ra = blk * TB + 2 * tp < a.rows, rb = blk * TB + 2 * tp + 1 < a.rows;
+        const int rem = (int)min(a.rows - blk * TB, (int64_t)TB);  // rows of this block (uniform, >= 1)
+        const bool ra = 2 * tp < rem, rb = 2 * tp + 1 < rem;
         const bool rc = (og & 1) ? rb : ra;
         uint32_t ca[2], cb[2], yc[CQ];
 #pragma unroll
