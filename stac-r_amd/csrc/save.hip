@@ -562,6 +562,18 @@ __device__ __forceinline__ void unpack_raw(const uint4 &w, float (&x)[V])
     }
 }
 
+// V residuals of a 16-bit type (each exactly representable) packed as one 16-byte vector
+template <int DT, int V>
+__device__ __forceinline__ uint4 pack_raw(const float (&v)[V])
+{
+    static_assert(V == 8 && sizeof(typename Act<DT>::T) == 2, "16-bit vectors of 8");
+    uint32_t u[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        u[k] = (uint32_t)Act<DT>::st(v[2 * k]) | ((uint32_t)Act<DT>::st(v[2 * k + 1]) << 16);
+    return make_uint4(u[0], u[1], u[2], u[3]);
+}
+
 // Sum 64 values (v = i * R + j) over the 64 lanes of a wave: six halving exchanges leave lane l
 // with the wave's total of value l.
 __device__ __forceinline__ float wave_reduce_scatter64(float (&a)[64])
@@ -836,12 +848,14 @@ __device__ SelState block_select_pre(int lvl, const HistPre &p, uint32_t prefix,
     return r;
 }
 
-// Pass 1 (batched): coefficients, first-digit histogram, max key.
-template <int DT, int R, int V>
+// Pass 1 (batched): coefficients, first-digit histogram, max key; SR: the residual is also
+// stored (16-bit types, where it is exact in the activation dtype) for the later passes to read.
+template <int DT, int R, int V, bool SR>
 __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg, const typename Act<DT>::T *__restrict__ x,
                                                         const float *__restrict__ qp, typename Act<DT>::T *__restrict__ coeff,
                                                         uint32_t *__restrict__ hist, uint32_t *__restrict__ maxkey,
-                                                        int do_hist, const typename Act<DT>::T *__restrict__ coeff_in)
+                                                        int do_hist, const typename Act<DT>::T *__restrict__ coeff_in,
+                                                        typename Act<DT>::T *__restrict__ rout)
 {
     constexpr int NB = Batch<R>::NB;
     __shared__ uint32_t s_hist[kBins];
@@ -889,6 +903,7 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg,
             float xv[V], r[V];
             ld.x_at(i, true, xv);
             batch_residual<DT, R, V>(xv, c + i * R, q, r);
+            if constexpr (SR) *reinterpret_cast<uint4 *>(rout + ld.rows[i] * g.d + col) = pack_raw<DT, V>(r);
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -923,7 +938,7 @@ __device__ __forceinline__ SelState prev_state(int lvl, const SelState *__restri
 }
 
 // Passes 2 and 3 (batched): histogram of digit `lvl` among keys matching the prefix so far.
-template <int DT, int R, int V, int HC>
+template <int DT, int R, int V, int HC, bool RIN>
 __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom fg, int lvl,
                                                           const typename Act<DT>::T *__restrict__ x,
                                                           const float *__restrict__ qp,
@@ -948,12 +963,12 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
     const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
     const bool col_ok = col < g.d;
-    FastLoads<DT, R, V, true> ld;
+    FastLoads<DT, R, V, !RIN> ld;  // RIN: x is the stored residual
     // issued whether or not the workgroup has rows: a load under a branch makes every later wait
     // count as if it had not been issued, so waiting for the histogram words would wait for X too
     ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
     float q[V][R];
-    basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
+    if constexpr (!RIN) basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
     for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
     // the chunk's first workgroup records the selection for the passes that follow
     const SelState sel = block_select_pre(lvl - 1, hp, sp.prefix, sp.need, s_tot, &s_res);
@@ -972,16 +987,21 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
     const uint32_t prefix = sel.prefix;
     const int match_shift = kDigitShift[lvl - 1], dshift = kDigitShift[lvl];
     const uint32_t dmask = (uint32_t)kDigitBins[lvl] - 1u;
-    basis_mask<R, V>(col_ok, q);
+    if constexpr (!RIN) basis_mask<R, V>(col_ok, q);
     uint32_t above = 0u;
     {   // the workgroup's rows are one batch
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             if (!(col_ok && ld.rows[i] < row_end)) continue;
-            float xv[V], r[V], ci[R];
-            ld.x_at(i, true, xv);
-            ld.coeff_row(i, coeff, g.rank, row_end, fg.c_vec != 0, ci);
-            batch_residual<DT, R, V>(xv, ci, q, r);
+            float r[V];
+            if constexpr (RIN) {
+                ld.x_at(i, true, r);  // the stored residual
+            } else {
+                float xv[V], ci[R];
+                ld.x_at(i, true, xv);
+                ld.coeff_row(i, coeff, g.rank, row_end, fg.c_vec != 0, ci);
+                batch_residual<DT, R, V>(xv, ci, q, r);
+            }
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -1009,7 +1029,7 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
 }
 
 // Survivor counts (batched).
-template <int DT, int R, int V, int HC>
+template <int DT, int R, int V, int HC, bool RIN>
 __global__ __launch_bounds__(kBlock) void k_count_b(SaveGeom g, FastGeom fg, const typename Act<DT>::T *__restrict__ x,
                                                     const float *__restrict__ qp,
                                                     const typename Act<DT>::T *__restrict__ coeff,
@@ -1033,12 +1053,12 @@ __global__ __launch_bounds__(kBlock) void k_count_b(SaveGeom g, FastGeom fg, con
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
     const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
     const bool col_ok = col < g.d;
-    FastLoads<DT, R, V, true> ld;
+    FastLoads<DT, R, V, !RIN> ld;  // RIN: x is the stored residual
     // issued whether or not the workgroup has rows: a load under a branch makes every later wait
     // count as if it had not been issued, so waiting for the histogram words would wait for X too
     ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
     float q[V][R];
-    basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
+    if constexpr (!RIN) basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
     SelState sel = block_select_pre(kLvl, hp, sp.prefix, sp.need, s_tot, &s_res);
     if (kLvl == 1) {
         if (blockIdx.x % g.wgs_per_chunk == 0 && threadIdx.x == 0) state[chunk * 3 + 1] = sel;
@@ -1046,16 +1066,21 @@ __global__ __launch_bounds__(kBlock) void k_count_b(SaveGeom g, FastGeom fg, con
     }
     if (blockIdx.x % g.wgs_per_chunk == 0 && threadIdx.x == 0) state[chunk * 3 + 2] = sel;
     const uint32_t T = sel.prefix;
-    basis_mask<R, V>(col_ok, q);
+    if constexpr (!RIN) basis_mask<R, V>(col_ok, q);
     uint32_t gt = 0u, eq = 0u;
     if (has_rows) {  // the workgroup's rows are one batch; a workgroup with none only reports zeros
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             if (!(col_ok && ld.rows[i] < row_end)) continue;
-            float xv[V], r[V], ci[R];
-            ld.x_at(i, true, xv);
-            ld.coeff_row(i, coeff, g.rank, row_end, fg.c_vec != 0, ci);
-            batch_residual<DT, R, V>(xv, ci, q, r);
+            float r[V];
+            if constexpr (RIN) {
+                ld.x_at(i, true, r);  // the stored residual
+            } else {
+                float xv[V], ci[R];
+                ld.x_at(i, true, xv);
+                ld.coeff_row(i, coeff, g.rank, row_end, fg.c_vec != 0, ci);
+                batch_residual<DT, R, V>(xv, ci, q, r);
+            }
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
@@ -1106,7 +1131,7 @@ __device__ __forceinline__ SelState fold_select(const uint32_t (&hw)[HC], SelSta
 // workgroups' counts, then X, C and the basis); the offset sums come after the residuals, so the
 // loads they need are hidden behind that arithmetic; survivors are kept as per-iteration bit masks
 // and only the set bits are visited when writing.
-template <int DT, int R, int V, int HC>
+template <int DT, int R, int V, int HC, bool RIN>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) void k_emit_b(SaveGeom g, FastGeom fg, const typename Act<DT>::T *__restrict__ x,
                                                    const float *__restrict__ qp,
                                                    const typename Act<DT>::T *__restrict__ coeff,
@@ -1141,12 +1166,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
 #pragma unroll
         for (int k = 0; k < 2; ++k) pre[k] = counts[wg0 + min((int64_t)threadIdx.x + k * kBlock, w)];
     }
-    FastLoads<DT, R, V, true> ld;
+    FastLoads<DT, R, V, !RIN> ld;  // RIN: x is the stored residual
     // issued whether or not the workgroup has rows: a load under a branch makes every later wait
     // count as if it had not been issued, so waiting for the histogram words would wait for X too
     ld.issue(g, slot, row0, row_end, colc, x, coeff, fg.c_vec != 0);
     float q[V][R];
-    basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
+    if constexpr (!RIN) basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
     SelState st;
     uint32_t rhi[2] = {0u, 0u}, rlo[2] = {0u, 0u};
     const uint32_t *fhi = fold, *flo = fold;
@@ -1176,16 +1201,20 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
     const float scale = o.bits ? quant_scale(mk, o.bits, amax) : 1.f;
     if (!to_list && blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
     if (!has_rows) return;  // uniform: a trailing workgroup with no rows writes nothing
-    basis_mask<R, V>(col_ok, q);
+    if constexpr (!RIN) basis_mask<R, V>(col_ok, q);
     float r[NB][V];
     uint32_t msk[NB];  // survivors of iteration i: bits 0..7 above T, bits 8..15 equal to T
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         const bool live = col_ok && ld.rows[i] < row_end;
-        float xv[V], ci[R];
-        ld.x_at(i, live, xv);
-        ld.coeff_row(i, coeff, g.rank, row_end, fg.c_vec != 0, ci);
-        batch_residual<DT, R, V>(xv, ci, q, r[i]);
+        if constexpr (RIN) {
+            ld.x_at(i, live, r[i]);  // the stored residual (zero outside the rows / columns)
+        } else {
+            float xv[V], ci[R];
+            ld.x_at(i, live, xv);
+            ld.coeff_row(i, coeff, g.rank, row_end, fg.c_vec != 0, ci);
+            batch_residual<DT, R, V>(xv, ci, q, r[i]);
+        }
         uint32_t m = 0u;
 #pragma unroll
         for (int e = 0; e < V; ++e) {
@@ -1473,7 +1502,7 @@ Plan make_plan(const StacrSaveArgs &a)
 template <typename T> T *carve(char *base, size_t off) { return reinterpret_cast<T *>(base + off); }
 
 enum { WS_QP, WS_HIST, WS_STATE, WS_MAXKEY, WS_COUNTS, WS_OFFS, WS_LRBITS, WS_LIDX, WS_THIST, WS_TSTATE,
-       WS_LCOUNTS, WS_LOFFS, WS_Q4, WS_FOLD, WS_N };
+       WS_LCOUNTS, WS_LOFFS, WS_Q4, WS_FOLD, WS_R, WS_N };
 
 size_t layout(const StacrSaveArgs &a, const Plan &p, size_t *off)
 {
@@ -1494,6 +1523,8 @@ size_t layout(const StacrSaveArgs &a, const Plan &p, size_t *off)
     take(WS_LOFFS, nb * sizeof(WgOffset));
     take(WS_Q4, a.bits == 4 ? (size_t)a.k_total : 0);
     take(WS_FOLD, p.fold ? (size_t)17 * p.n_wgs * sizeof(uint32_t) : 0);  // cum[0..16][workgroup]
+    const bool rstore = p.fast && a.dtype != STACR_DTYPE_F32 && a.k_total > 0;
+    take(WS_R, rstore ? (size_t)a.rows * a.feats * 2 : 0);  // the stored residual (16-bit types)
     return cur;
 }
 
@@ -1526,13 +1557,18 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     const bool fast = kFastOk && p.fast;
     const bool hc8 = p.g.hcopies == kHistCopies;
     uint32_t *fold = carve<uint32_t>(ws, off[WS_FOLD]);
+    // 16-bit activations on the batched path: the projection pass stores the residual (exact in
+    // the activation dtype) and the later passes read it instead of X, C and the basis
+    constexpr bool kRin = sizeof(T) == 2;
+    T *rbuf = carve<T>(ws, off[WS_R]);
+    const T *xin = kRin ? rbuf : x;
     if (fast != p.fold && DT == STACR_DTYPE_BF16) return stacr_fail(STACR_ERR_INVALID, "stacr_save: bf16 fold outside the batched path");
     if (!fast && p.g.hcopies != 1) return stacr_fail(STACR_ERR_INVALID, "stacr_save: histogram copies outside the batched path");
     FastGeom fg{p.g.L / 64, a.rank == R && ((uintptr_t)coeff % 16) == 0};
     if (!coeff_in || resid) {
         if constexpr (kFastOk) {
             if (fast) {
-                stacr_launch("k_proj_hist", s, [&] { k_proj_hist_b<DT, R, V><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in); });
+                stacr_launch("k_proj_hist", s, [&] { k_proj_hist_b<DT, R, V, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in, rbuf); });
             }
         }
         if (!fast)
@@ -1548,17 +1584,17 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     for (int lvl = 1; lvl <= n_refine; ++lvl) {
         if constexpr (kFastOk) {
             if (fast && hc8)
-                stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, x, qp, coeff, hist, state, kf, kl, maxkey, fold, p.n_wgs); });
+                stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V, kHistCopies, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, xin, qp, coeff, hist, state, kf, kl, maxkey, fold, p.n_wgs); });
             if (fast && !hc8)
-                stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, x, qp, coeff, hist, state, kf, kl, maxkey, fold, p.n_wgs); });
+                stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V, 1, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, xin, qp, coeff, hist, state, kf, kl, maxkey, fold, p.n_wgs); });
         }
         if (!fast) stacr_launch("k_refine_hist", s, [&] { k_refine_hist<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, lvl, x, qp, coeff, hist, state, kf, kl); });
     }
     if constexpr (kFastOk) {
         if (fast && hc8 && !p.fold)
-            stacr_launch("k_count", s, [&] { k_count_b<DT, R, V, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, hist, state, counts, kf, kl); });
+            stacr_launch("k_count", s, [&] { k_count_b<DT, R, V, kHistCopies, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, hist, state, counts, kf, kl); });
         if (fast && !hc8 && !p.fold)
-            stacr_launch("k_count", s, [&] { k_count_b<DT, R, V, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, hist, state, counts, kf, kl); });
+            stacr_launch("k_count", s, [&] { k_count_b<DT, R, V, 1, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, hist, state, counts, kf, kl); });
     }
     if (!fast) stacr_launch("k_count", s, [&] { k_count<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, hist, state, counts, kf, kl); });
 
@@ -1575,9 +1611,9 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     if constexpr (kFastOk) {
         // the fold variant (bf16) reads the level-1 histogram copies; other types take the counts
         if (fast && hc8 && DT == STACR_DTYPE_BF16)
-            stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs); });
+            stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V, kHistCopies, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs); });
         else if (fast)
-            stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs); });
+            stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V, 1, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs); });
     }
     if (!fast) stacr_launch("k_emit", s, [&] { k_emit<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0); });
 
