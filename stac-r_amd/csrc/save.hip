@@ -12,6 +12,8 @@
 // list.  Ties at the threshold go to the lowest flat index.
 #include <float.h>
 
+#include <type_traits>
+
 #include "internal.h"
 
 using namespace stacr;
@@ -20,6 +22,7 @@ namespace {
 
 constexpr int kHistCopies = 8;     // histogram / max-key copies of a chunk with many workgroups
 constexpr int kMaxKeyStride = 32;  // max-key copies 128 bytes apart
+constexpr int kCoarse = 64;        // level-0 coarse bins (32 histogram bins each)
 
 __device__ __forceinline__ void wg_rows(const SaveGeom &g, int64_t wg, int64_t &chunk, int64_t &row0,
                                         int64_t &row_end)
@@ -855,7 +858,7 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg,
                                                         const float *__restrict__ qp, typename Act<DT>::T *__restrict__ coeff,
                                                         uint32_t *__restrict__ hist, uint32_t *__restrict__ maxkey,
                                                         int do_hist, const typename Act<DT>::T *__restrict__ coeff_in,
-                                                        typename Act<DT>::T *__restrict__ rout)
+                                                        typename Act<DT>::T *__restrict__ rout, uint32_t *__restrict__ coarse)
 {
     constexpr int NB = Batch<R>::NB;
     __shared__ uint32_t s_hist[kBins];
@@ -921,12 +924,54 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg,
     uint32_t *gh = hist + ((chunk * 3 + 0) * g.hcopies + copy) * kBins;
     for (int b = threadIdx.x; b < kBins; b += kBlock)
         if (s_hist[b]) atomicAdd(&gh[b], s_hist[b]);
+    if (threadIdx.x < kCoarse) {  // the same counts in 64 bins of 32
+        uint32_t sum = 0u;
+#pragma unroll 8
+        for (int b = 0; b < kBins / kCoarse; ++b) sum += s_hist[threadIdx.x * (kBins / kCoarse) + b];
+        if (sum) atomicAdd(&coarse[(chunk * g.hcopies + copy) * kCoarse + threadIdx.x], sum);
+    }
     if (threadIdx.x == 0) {
         uint32_t m = 0u;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) m = max(m, s_wmax[w]);
         if (m) atomicMax(maxkey + copy * kMaxKeyStride, m);
     }
+}
+
+// The level-0 selection from the coarse histogram (64 bins of 32) and then the chosen coarse bin's
+// 32 histogram bins, each summed over the HC copies, made by every wave on its own with suffix
+// sums across lanes and a ballot (no barrier): the same bin and need as block_select at level 0.
+// cv: this lane's coarse bin (lane) in each copy, loaded ahead by the caller.
+template <int HC>
+__device__ __forceinline__ SelState select_level0(const uint32_t (&cv)[HC], const uint32_t *__restrict__ fine, SelState s0)
+{
+    constexpr int FB = kBins / kCoarse;
+    const int lane = threadIdx.x & 63;
+    uint32_t suf = 0u;
+#pragma unroll
+    for (int h = 0; h < HC; ++h) suf += cv[h];
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_down(suf, off, 64);
+        if (lane + off < 64) suf += y;
+    }
+    const uint64_t m = __ballot(suf >= s0.need);
+    if (m == 0ull) return SelState{0u, s0.need};  // fewer keys than the need (block_select's default)
+    const int cb = 63 - __clzll(m);
+    const uint32_t need1 = s0.need - (cb < 63 ? (uint32_t)__shfl((int)suf, cb + 1, 64) : 0u);
+    const int fl = lane & (FB - 1);
+    uint32_t sf = 0u;
+#pragma unroll
+    for (int h = 0; h < HC; ++h) sf += fine[h * kBins + cb * FB + fl];
+#pragma unroll
+    for (int off = 1; off < FB; off <<= 1) {
+        const uint32_t y = __shfl_down(sf, off, FB);
+        if (fl + off < FB) sf += y;
+    }
+    const uint64_t mf = __ballot(sf >= need1) & ((1ull << FB) - 1);
+    const int fb = mf ? 63 - __clzll(mf) : 0;
+    const uint32_t above = fb < FB - 1 ? (uint32_t)__shfl((int)sf, fb + 1, 64) : 0u;
+    return SelState{(uint32_t)(cb * FB + fb), need1 - above};
 }
 
 // The previous level's state of the workgroup's chunk (level 0: its k).
@@ -938,17 +983,19 @@ __device__ __forceinline__ SelState prev_state(int lvl, const SelState *__restri
 }
 
 // Passes 2 and 3 (batched): histogram of digit `lvl` among keys matching the prefix so far.
-template <int DT, int R, int V, int HC, bool RIN>
-__global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom fg, int lvl,
+template <int DT, int R, int V, int HC, bool RIN, int LVL>
+__global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom fg,
                                                           const typename Act<DT>::T *__restrict__ x,
                                                           const float *__restrict__ qp,
                                                           const typename Act<DT>::T *__restrict__ coeff,
                                                           uint32_t *__restrict__ hist, SelState *__restrict__ state,
                                                           uint32_t k_full, uint32_t k_last, uint32_t *__restrict__ maxkey,
-                                                          uint32_t *__restrict__ fold, int64_t fold_stride)
+                                                          uint32_t *__restrict__ fold, int64_t fold_stride,
+                                                          const uint32_t *__restrict__ coarse)
 {
     constexpr int NB = Batch<R>::NB;
     constexpr bool kFold = DT == STACR_DTYPE_BF16;  // per-workgroup records for the emission pass
+    constexpr int lvl = LVL;                         // the key digit histogrammed here (1 or 2)
     __shared__ uint32_t s_hist[kBins];
     __shared__ uint32_t s_tot[kWaves];
     __shared__ uint32_t s_above[kWaves];
@@ -959,7 +1006,15 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
     const SelState sp = prev_state(lvl - 1, state, chunk, g.n_chunks, k_full, k_last);
     HistPre hp;
     static_assert(kDigitBins[0] / kBlock == 8 && kDigitBins[1] / kBlock == 8 && kDigitBins[2] / kBlock == 2, "bins per thread");
-    hist_issue<8, HC>(hist + (chunk * 3 + lvl - 1) * HC * kBins, hp);
+    // level 1 selects level 0 from the coarse histogram (below); level 2 scans the histogram.  The
+    // words go out before X.
+    uint32_t cv[HC];
+    if constexpr (LVL == 1) {
+#pragma unroll
+        for (int h = 0; h < HC; ++h) cv[h] = coarse[(chunk * HC + h) * kCoarse + (threadIdx.x & 63)];
+    } else {
+        hist_issue<8, HC>(hist + (chunk * 3 + lvl - 1) * HC * kBins, hp);
+    }
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
     const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
     const bool col_ok = col < g.d;
@@ -971,7 +1026,9 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
     if constexpr (!RIN) basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
     for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
     // the chunk's first workgroup records the selection for the passes that follow
-    const SelState sel = block_select_pre(lvl - 1, hp, sp.prefix, sp.need, s_tot, &s_res);
+    SelState sel;
+    if constexpr (LVL == 1) sel = select_level0<HC>(cv, hist + chunk * 3 * HC * kBins, sp);
+    else sel = block_select_pre(lvl - 1, hp, sp.prefix, sp.need, s_tot, &s_res);
     if (blockIdx.x % g.wgs_per_chunk == 0 && threadIdx.x == 0) state[chunk * 3 + lvl - 1] = sel;
     if (HC > 1 && lvl == 1 && blockIdx.x == 0 && threadIdx.x == 0) {  // fold the max key's copies into the first
         uint32_t m = maxkey[0];
@@ -1501,7 +1558,7 @@ Plan make_plan(const StacrSaveArgs &a)
 
 template <typename T> T *carve(char *base, size_t off) { return reinterpret_cast<T *>(base + off); }
 
-enum { WS_QP, WS_HIST, WS_STATE, WS_MAXKEY, WS_COUNTS, WS_OFFS, WS_LRBITS, WS_LIDX, WS_THIST, WS_TSTATE,
+enum { WS_QP, WS_HIST, WS_COARSE, WS_STATE, WS_MAXKEY, WS_COUNTS, WS_OFFS, WS_LRBITS, WS_LIDX, WS_THIST, WS_TSTATE,
        WS_LCOUNTS, WS_LOFFS, WS_Q4, WS_FOLD, WS_R, WS_N };
 
 size_t layout(const StacrSaveArgs &a, const Plan &p, size_t *off)
@@ -1510,6 +1567,7 @@ size_t layout(const StacrSaveArgs &a, const Plan &p, size_t *off)
     auto take = [&](int slot, size_t bytes) { off[slot] = cur; cur += (bytes + 255) & ~(size_t)255; };
     take(WS_QP, 2 * (size_t)a.feats * p.R * sizeof(float));  // padded basis, then transposed
     take(WS_HIST, (size_t)p.g.n_chunks * 3 * p.g.hcopies * kBins * sizeof(uint32_t));
+    take(WS_COARSE, (size_t)p.g.n_chunks * p.g.hcopies * kCoarse * sizeof(uint32_t));
     take(WS_MAXKEY, (size_t)p.g.hcopies * kMaxKeyStride * sizeof(uint32_t));
     take(WS_STATE, (size_t)p.g.n_chunks * 3 * sizeof(SelState));
     take(WS_COUNTS, (size_t)p.n_wgs * sizeof(WgCount));
@@ -1557,6 +1615,7 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     const bool fast = kFastOk && p.fast;
     const bool hc8 = p.g.hcopies == kHistCopies;
     uint32_t *fold = carve<uint32_t>(ws, off[WS_FOLD]);
+    uint32_t *coarse = carve<uint32_t>(ws, off[WS_COARSE]);
     // 16-bit activations on the batched path: the projection pass stores the residual (exact in
     // the activation dtype) and the later passes read it instead of X, C and the basis
     constexpr bool kRin = sizeof(T) == 2;
@@ -1568,7 +1627,7 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     if (!coeff_in || resid) {
         if constexpr (kFastOk) {
             if (fast) {
-                stacr_launch("k_proj_hist", s, [&] { k_proj_hist_b<DT, R, V, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in, rbuf); });
+                stacr_launch("k_proj_hist", s, [&] { k_proj_hist_b<DT, R, V, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in, rbuf, coarse); });
             }
         }
         if (!fast)
@@ -1583,10 +1642,25 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     const int n_refine = fast && sizeof(T) == 2 ? 1 : 2;
     for (int lvl = 1; lvl <= n_refine; ++lvl) {
         if constexpr (kFastOk) {
-            if (fast && hc8)
-                stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V, kHistCopies, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, xin, qp, coeff, hist, state, kf, kl, maxkey, fold, p.n_wgs); });
-            if (fast && !hc8)
-                stacr_launch("k_refine_hist", s, [&] { k_refine_hist_b<DT, R, V, 1, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, lvl, xin, qp, coeff, hist, state, kf, kl, maxkey, fold, p.n_wgs); });
+            if (fast) {
+                auto refine = [&](auto hc, auto level) {
+                    stacr_launch("k_refine_hist", s, [&] {
+                        k_refine_hist_b<DT, R, V, decltype(hc)::value, kRin, decltype(level)::value><<<nwg, kBlock, 0, s>>>(
+                            p.g, fg, xin, qp, coeff, hist, state, kf, kl, maxkey, fold, p.n_wgs, coarse);
+                    });
+                };
+                using L1 = std::integral_constant<int, 1>;
+                using L2 = std::integral_constant<int, 2>;
+                using H8 = std::integral_constant<int, kHistCopies>;
+                using H1 = std::integral_constant<int, 1>;
+                if (lvl == 1) {
+                    if (hc8) refine(H8{}, L1{});
+                    else refine(H1{}, L1{});
+                } else if constexpr (sizeof(T) == 4) {  // only fp32 runs the second refine pass
+                    if (hc8) refine(H8{}, L2{});
+                    else refine(H1{}, L2{});
+                }
+            }
         }
         if (!fast) stacr_launch("k_refine_hist", s, [&] { k_refine_hist<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, lvl, x, qp, coeff, hist, state, kf, kl); });
     }
