@@ -139,6 +139,20 @@ __device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t *s_tot)
     return total;
 }
 
+// Two 16-bit products (packed pairs of the activation / gradient type) added to an fp32 sum
+// (v_dot2_f32_bf16 / v_dot2_f32_f16).
+template <int DT>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c)
+{
+    if constexpr (DT == STACR_DTYPE_BF16) {
+        typedef __attribute__((ext_vector_type(2))) __bf16 v2;
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+    } else {
+        typedef __attribute__((ext_vector_type(2))) _Float16 v2;
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+    }
+}
+
 // ------------------------------------------------------------------ save geometry
 // A workgroup owns `rows_per_wg` consecutive rows inside one selection chunk.  Inside it, the
 // 256 threads form rpi = 256 / L row slots of L threads; each thread walks `mv` vectors of V

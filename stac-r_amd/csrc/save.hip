@@ -175,12 +175,15 @@ __global__ void k_prep(const typename Act<DT>::T *__restrict__ q, int64_t d, int
     const int64_t n = d * R;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
     float *qpt = qp + n;  // the same values transposed, [R][d]: the batched passes read it per rank
+    // 16-bit types: also the transposed copy in the activation dtype (the projection's dot products)
+    typename Act<DT>::T *qph = reinterpret_cast<typename Act<DT>::T *>(qpt + n);
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
         const int64_t row = i / R;
         const int j = (int)(i - row * R);
         const float v = j < rank ? Act<DT>::ld(q[row * rank + j]) : 0.f;
         qp[i] = v;
         qpt[j * d + row] = v;
+        if constexpr (sizeof(typename Act<DT>::T) == 2) qph[j * d + row] = j < rank ? q[row * rank + j] : (typename Act<DT>::T)0;
     }
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_zero; i += step) zero[i] = 0u;
 }
@@ -873,11 +876,29 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg,
     const bool col_ok = col < g.d;
     FastLoads<DT, R, V, false> ld;
     ld.issue(g, slot, row0, row_end, colc, x, nullptr, false);
+    // 16-bit types read the basis as 16-bit words: the projection takes them as v_dot2 operands
+    // (two products a step, fp32 sums) and the residual widens the same values to fp32
+    constexpr bool kPair = sizeof(typename Act<DT>::T) == 2 && V == 8;
     float q[V][R];
-    basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
+    uint4 qw[kPair ? R : 1];
+    if constexpr (kPair) {
+        const typename Act<DT>::T *qph = reinterpret_cast<const typename Act<DT>::T *>(qp + 2 * g.d * R);
+#pragma unroll
+        for (int j = 0; j < R; ++j) qw[j] = *reinterpret_cast<const uint4 *>(qph + j * g.d + colc);
+    } else {
+        basis_issue<R, V>(qp + g.d * R, g.d, colc, q);
+    }
     for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
     uint32_t kmax = 0u;
     __syncthreads();
+    if constexpr (kPair) {
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const uint32_t w[4] = {qw[j].x, qw[j].y, qw[j].z, qw[j].w};
+#pragma unroll
+            for (int e = 0; e < V; ++e) q[e][j] = Act<DT>::ld((typename Act<DT>::T)((w[e / 2] >> (16 * (e & 1))) & 0xffffu));
+        }
+    }
     basis_mask<R, V>(col_ok, q);
     {   // the workgroup's rows are one batch (the plan sizes them so)
         float c[64];
@@ -887,14 +908,28 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg,
             float acc[64];
 #pragma unroll
             for (int i = 0; i < NB; ++i) {
-                float xv[V];
-                ld.x_at(i, col_ok && ld.rows[i] < row_end, xv);
+                const bool live = col_ok && ld.rows[i] < row_end;
+                if constexpr (kPair) {
+                    const uint4 xr = live ? ld.raw[i] : make_uint4(0u, 0u, 0u, 0u);
+                    const uint32_t xw[4] = {xr.x, xr.y, xr.z, xr.w};
 #pragma unroll
-                for (int j = 0; j < R; ++j) {
-                    float s = 0.f;
+                    for (int j = 0; j < R; ++j) {
+                        const uint32_t w[4] = {qw[j].x, qw[j].y, qw[j].z, qw[j].w};
+                        float s = 0.f;
 #pragma unroll
-                    for (int e = 0; e < V; ++e) s = fmaf(xv[e], q[e][j], s);
-                    acc[i * R + j] = s;
+                        for (int k = 0; k < 4; ++k) s = dot2<DT>(xw[k], w[k], s);
+                        acc[i * R + j] = s;
+                    }
+                } else {
+                    float xv[V];
+                    ld.x_at(i, live, xv);
+#pragma unroll
+                    for (int j = 0; j < R; ++j) {
+                        float s = 0.f;
+#pragma unroll
+                        for (int e = 0; e < V; ++e) s = fmaf(xv[e], q[e][j], s);
+                        acc[i * R + j] = s;
+                    }
                 }
             }
             batch_coeff_from_acc<DT, R>(acc, fg.W, slot, s_part, s_c, row0, g.rpi, row_end, g.rank, coeff, c);
@@ -1565,7 +1600,8 @@ size_t layout(const StacrSaveArgs &a, const Plan &p, size_t *off)
 {
     size_t cur = 0;
     auto take = [&](int slot, size_t bytes) { off[slot] = cur; cur += (bytes + 255) & ~(size_t)255; };
-    take(WS_QP, 2 * (size_t)a.feats * p.R * sizeof(float));  // padded basis, then transposed
+    // padded basis, then transposed; then transposed in the activation dtype (16-bit types)
+    take(WS_QP, 2 * (size_t)a.feats * p.R * sizeof(float) + (size_t)a.feats * p.R * 2);
     take(WS_HIST, (size_t)p.g.n_chunks * 3 * p.g.hcopies * kBins * sizeof(uint32_t));
     take(WS_COARSE, (size_t)p.g.n_chunks * p.g.hcopies * kCoarse * sizeof(uint32_t));
     take(WS_MAXKEY, (size_t)p.g.hcopies * kMaxKeyStride * sizeof(uint32_t));

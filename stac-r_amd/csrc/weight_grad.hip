@@ -132,18 +132,6 @@ __device__ __forceinline__ void load_g(const typename Act<DT>::T *row, int64_t o
     }
 }
 
-template <int DT>
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c)
-{
-    if constexpr (DT == STACR_DTYPE_BF16) {
-        typedef __attribute__((ext_vector_type(2))) __bf16 v2;
-        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
-    } else {
-        typedef __attribute__((ext_vector_type(2))) _Float16 v2;
-        return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
-    }
-}
-
 template <int IDX64>
 __device__ __forceinline__ int64_t flat_at(const void *idx, int64_t k)
 {
