@@ -23,6 +23,7 @@ namespace {
 constexpr int kHistCopies = 8;     // histogram / max-key copies of a chunk with many workgroups
 constexpr int kMaxKeyStride = 32;  // max-key copies 128 bytes apart
 constexpr int kCoarse = 64;        // level-0 coarse bins (32 histogram bins each)
+constexpr int kEmitStage = 1024;   // survivors a batched emission workgroup stages in LDS
 
 __device__ __forceinline__ void wg_rows(const SaveGeom &g, int64_t wg, int64_t &chunk, int64_t &row0,
                                         int64_t &row_end)
@@ -1237,6 +1238,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
     static_assert(V <= 8, "survivor masks hold 8 elements per vector");
     __shared__ uint32_t s_wt[kWaves * NB];
     __shared__ uint32_t s_off[kWaves];
+    // the workgroup's survivors at their local rank, written out by consecutive threads afterwards
+    // (when they fit; otherwise each is written where it is found)
+    __shared__ uint32_t s_flat[kEmitStage], s_rv[kEmitStage];
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
     const int64_t w = blockIdx.x - chunk * g.wgs_per_chunk;
@@ -1316,8 +1320,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
         }
         msk[i] = m;
     }
-    // the workgroup's output offset and tie budget
+    // the workgroup's output offset and tie budget, and its number of survivors
     WgOffset wo;
+    uint32_t n_out;
     {
         uint32_t gt = 0u, eq = 0u;
 #pragma unroll
@@ -1337,7 +1342,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
         const WgCount mine = kFold ? WgCount{fhi[w], flo[w] - fhi[w]} : counts[wg0 + w];
         const uint32_t take = eq_before >= st.need ? 0u : min(mine.eq, st.need - eq_before);
         wo = WgOffset{(uint32_t)chunk * chunk_k + gt_before + min(st.need, eq_before), take};
+        n_out = mine.gt + take;
     }
+    const bool staged = n_out <= (uint32_t)kEmitStage;  // uniform
     uint32_t cnt[NB], incl[NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
@@ -1375,12 +1382,17 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
             const uint32_t is_gt = (m >> e) & 1u, is_eq = (m >> (8 + e)) & 1u;
             m &= ~((1u << e) | (0x100u << e));
             if (is_gt || eb < wo.take) {
-                const uint32_t pos = wo.off + gb + min(eb, wo.take);
+                const uint32_t local = gb + min(eb, wo.take), pos = wo.off + local;
                 float rv = r[i][0];
 #pragma unroll
                 for (int k = 1; k < V; ++k) rv = e == k ? r[i][k] : rv;
                 const uint32_t flat = (uint32_t)(ld.rows[i] * g.d + col + e);
-                if (pos >= o.cap) {
+                if (staged) {
+                    if (local < (uint32_t)kEmitStage) {  // always, when the counts are consistent
+                        s_flat[local] = flat;
+                        s_rv[local] = __float_as_uint(rv);
+                    }
+                } else if (pos >= o.cap) {
                     // unreachable when the counts are consistent; never write out of bounds
                 } else if (to_list) {
                     o.list_rbits[pos] = __float_as_uint(rv);
@@ -1393,6 +1405,21 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
             eb += is_eq;
         }
         before_iter += iter_total;
+    }
+    if (staged) {
+        __syncthreads();
+        for (uint32_t t = threadIdx.x; t < n_out; t += kBlock) {
+            const uint32_t pos = wo.off + t, flat = s_flat[t];
+            const float rv = __uint_as_float(s_rv[t]);
+            if (pos >= o.cap) {
+                // unreachable when the counts are consistent; never write out of bounds
+            } else if (to_list) {
+                o.list_rbits[pos] = __float_as_uint(rv);
+                o.list_idx[pos] = flat;
+            } else {
+                write_entry<DT>(o, pos, flat, rv, scale);
+            }
+        }
     }
 }
 
