@@ -1217,6 +1217,27 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
         }
     };
 
+    // A round's features split into several pieces have their partial sums in the slots.  Thread
+    // t (t < 16 x the round's split features) adds feature t / 16's output t % 16 into S; it runs
+    // after the round's last barrier and before the next round's pieces write the slots again
+    // (the planner keeps split features <= kMSlotCap / 2, so one item a thread suffices).
+    uint2 pend_hd = make_uint2(0xffffu, 0u);  // feature 0xffff: nothing pending
+    auto combine_pending = [&]() {
+        const uint32_t o = threadIdx.x % kOSlab, c = pend_hd.x & 0xffffu, s0 = pend_hd.x >> 16;
+        if (c < (uint32_t)ni && s0 + pend_hd.y <= (uint32_t)kMSlotCap) {
+            float s8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            uint32_t k = 0;
+            for (; k + 8 <= pend_hd.y; k += 8) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) s8[u] += l_slot[(s0 + k + u) * kOSlab + o];
+            }
+            for (; k < pend_hd.y; ++k) s8[0] += l_slot[(s0 + k) * kOSlab + o];
+            const float sum = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
+            acc[s_index((int)c, (int)o)] += sum * qscale;
+        }
+        pend_hd = make_uint2(0xffffu, 0u);
+    };
+
     // One round: the column tile (wave 0) and the pieces, then the split features' partial sums.
     auto run_round = [&](const RoundHdr &h) {
         const uint32_t ncol = min(h.n_heavy >> 16, (uint32_t)kMCols);
@@ -1255,21 +1276,9 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
             flush(td, pa);
         }
         __syncthreads();
-        for (uint32_t w = threadIdx.x; w < nh * kOSlab; w += kBwdThreads) {
-            const uint2 hd = l_heavy[w / kOSlab];
-            const uint32_t o = w % kOSlab, c = hd.x & 0xffffu, s0 = hd.x >> 16;
-            if (c < (uint32_t)ni && s0 + hd.y <= (uint32_t)kMSlotCap) {
-                float s8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-                uint32_t k = 0;
-                for (; k + 8 <= hd.y; k += 8) {
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) s8[u] += l_slot[(s0 + k + u) * kOSlab + o];
-                }
-                for (; k < hd.y; ++k) s8[0] += l_slot[(s0 + k) * kOSlab + o];
-                const float sum = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
-                acc[s_index((int)c, (int)o)] += sum * qscale;
-            }
-        }
+        // the split features' partial sums are added after the next barrier (combine_pending),
+        // by waves that wait there anyway; this keeps only the heavy record
+        pend_hd = threadIdx.x < nh * kOSlab ? l_heavy[threadIdx.x / kOSlab] : make_uint2(0xffffu, 0u);
         for (uint32_t i = threadIdx.x; i < ncol * (kMPitch / 8); i += kBwdThreads)
             reinterpret_cast<uint4 *>(bh)[i] = make_uint4(0u, 0u, 0u, 0u);
         __syncthreads();
@@ -1317,6 +1326,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
             __syncthreads();
             hdr_fill(blk + kMHdrRing / 2, kMHdrRing / 2);
         }
+        combine_pending();  // the previous round's split features
         __syncthreads();  // tiles and the first round staged
         {   // fixed tile: rows 32 wave .. 32 wave + 31 of the block
             const int jj = lane & 15, kk = 32 * wave + 8 * (lane >> 4);
@@ -1336,10 +1346,12 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
             StageM tmp;
             load_stage(tmp, h);
             store_stage(tmp);
+            combine_pending();
             __syncthreads();
             run_round(h);
         }
     }
+    combine_pending();
     __syncthreads();
 
     // ---- the fixed tile over the 16 waves, in wave order: M[o][j] (j < R), dbias (j = R)
