@@ -1245,7 +1245,7 @@ __global__ __launch_bounds__(kBwdThreads) void k_dw_fused_mfma(FusedArgs a)
         if (wave < kMCols / 16 && ncol > (uint32_t)(16 * wave)) {  // wave w: columns 16 w .. 16 w + 15
             const int jj = lane & 15, k8 = 8 * (lane >> 4), cj = 16 * wave + jj;
             f32x4 d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
+#pragma unroll
             for (int s = 0; s < TB / 32; ++s) {
                 const uint4 av = g_operand(32 * s);
                 const uint4 bv = *reinterpret_cast<const uint4 *>(bh + cj * kMPitch + 32 * s + k8);
