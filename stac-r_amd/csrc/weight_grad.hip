@@ -273,6 +273,43 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
     {
         const int64_t key0 = t0 * a.d_in, key1 = t1 * a.d_in;
         uint32_t lo0 = 0u, hi0 = nnz, lo1 = 0u, hi1 = nnz;
+        {   // First step: 2048 consecutive positions centred on the proportional guess nnz * t / rows
+            // (where rows of similar density put the boundary).  A boundary inside the window is
+            // found exactly; otherwise the search below continues on the side it lies on.
+            constexpr int kW = 4 * kPlanThreads;
+            const uint32_t g0 = (uint32_t)((uint64_t)nnz * (uint64_t)t0 / (uint64_t)a.rows);
+            const uint32_t g1 = (uint32_t)((uint64_t)nnz * (uint64_t)t1 / (uint64_t)a.rows);
+            const uint32_t w0 = min(g0 > kW / 2 ? g0 - kW / 2 : 0u, nnz - 1u);
+            const uint32_t w1 = min(g1 > kW / 2 ? g1 - kW / 2 : 0u, nnz - 1u);
+            const uint32_t nv0 = min((uint32_t)kW, nnz - w0), nv1 = min((uint32_t)kW, nnz - w1);
+            int64_t v0[4], v1[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {  // unconditional, clamped positions (nnz > 0 here)
+                v0[k] = flat_at<IDX64>(a.idx, min(w0 + threadIdx.x + k * kPlanThreads, nnz - 1u));
+                v1[k] = flat_at<IDX64>(a.idx, min(w1 + threadIdx.x + k * kPlanThreads, nnz - 1u));
+            }
+            uint32_t m = 0u;  // samples below the key, per wave (<= 256 each: 16-bit halves)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t j = threadIdx.x + k * kPlanThreads;
+                m += (uint32_t)__popcll(__ballot(j < nv0 && v0[k] < key0));
+                m += (uint32_t)__popcll(__ballot(j < nv1 && v1[k] < key1)) << 16;
+            }
+            if ((threadIdx.x & 63) == 0) s_cnt[1][threadIdx.x >> 6] = m;
+            __syncthreads();
+            uint32_t c01 = 0u;
+#pragma unroll
+            for (int w = 0; w < kPlanThreads / 64; ++w) c01 += s_cnt[1][w];
+            const uint32_t c0 = c01 & 0xffffu, c1 = c01 >> 16;
+            // c == 0: the boundary is at or before the window's first position; c == nv: after its
+            // last; otherwise at w + c
+            if (c0 == 0u) hi0 = w0;
+            else if (c0 < nv0) lo0 = hi0 = w0 + c0;
+            else lo0 = w0 + nv0;
+            if (c1 == 0u) hi1 = w1;
+            else if (c1 < nv1) lo1 = hi1 = w1 + c1;
+            else lo1 = w1 + nv1;
+        }
         for (int it = 0; lo0 < hi0 || lo1 < hi1; ++it) {
             const uint32_t st0 = max(1u, (hi0 - lo0 + kPlanThreads - 1) / kPlanThreads);
             const uint32_t st1 = max(1u, (hi1 - lo1 + kPlanThreads - 1) / kPlanThreads);

@@ -259,6 +259,32 @@ def test_weight_grad_heavy_features_and_many_rounds(dev, dtype, budget, rank):
     assert rel_l2(_np(db), odb) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("where", ["head", "tail", "middle"])
+def test_weight_grad_rows_of_unequal_density(dev, where):
+    """Global selection over rows of very unequal magnitude: the 512-row blocks' entry ranges lie
+    far from where a proportional share of the entries would put them (before, after and around
+    it), and one block holds most of the entries (several bucketing rounds)."""
+    from stacr_amd import kernels
+
+    announce("grad unequal rows", where)
+    rows, d_in, d_out, rank = 4096, 1024, 272, 8
+    x = make_activation(rows, d_in)
+    hot = {"head": slice(0, 256), "tail": slice(3840, 4096), "middle": slice(1900, 2200)}[where]
+    x[hot] *= 30.0
+    x = x.to(dev, torch.bfloat16)
+    q = make_basis(d_in, rank).to(dev, torch.bfloat16)
+    g = make_grad(rows, d_out).to(dev, torch.bfloat16)
+    coeff, idx, data, scale = kernels.save(x, q, mode="global_topk", budget=0.01, chunk_rows=512, bits=8)
+    oidx = idx.cpu().numpy().astype(np.int64)
+    t = oidx // d_in
+    assert np.count_nonzero((t >= hot.start) & (t < hot.stop)) > 0.9 * oidx.size  # skewed as intended
+    dw, db = kernels.weight_grad(g, coeff, q, (idx, data, scale), 8, False, torch.bfloat16, torch.bfloat16)
+    ovals = orc.dequantize(data.cpu().numpy().view(np.int8), np.float32(scale.item()), 8, oidx.size)
+    odw, odb = orc.weight_grad(_np(g), _np(coeff), _np(q), oidx, ovals, d_in)
+    assert rel_l2(_np(dw), odw) <= TOL["bf16"]
+    assert rel_l2(_np(db), odb) <= TOL["bf16"]
+
+
 def test_weight_grad_int64_indices(dev):
     """The backward accepts int64 flat indices (used when rows*d >= 2^31-1)."""
     from stacr_amd import kernels
