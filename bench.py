@@ -3,15 +3,20 @@
 
 Workload (c_fc layer): GPT-2-medium MLP c_fc as a Transformers Conv1D,
 N = 8 x 1024 = 8192 tokens, d_in 1024 -> d_out 4096, bf16, rank 8, residual_budget 0.005,
-residual_mode global_topk, int8 residual values, fused bias gradient.  Synthetic inputs with the
-configs' generator (low-rank + noise + 0.1% x20 outliers, per-channel log-normal scale), resident
-in HBM before timing.
+residual_mode global_topk, int8 residual values.  Synthetic inputs with the configs' generator
+(low-rank + noise + 0.1% x20 outliers, per-channel log-normal scale), resident in HBM before
+timing.
 
-One step = stacr_save (coefficients, exact global top-k selection, quantization) + stacr_weight_grad
-(dW = (G^T C) Q^T + G^T R_s and dbias).  The dense Y = X W^T and grad_input = G W GEMMs are not part
-of the STAC-R path and are not timed.  K steps are timed both as eager launches and replayed from
-a HIP graph captured once (checked against the eager result); the value is the faster of the two
-and both times are reported.  Prints one JSON line.
+One step = the two library calls STACRFunction makes for the STAC-R part of a layer-step:
+stacr_save in forward (coefficients, exact global top-k selection, quantization) and
+stacr_weight_grad in backward (dW = (G^T C) Q^T + G^T R_s).  The layer's other work is the
+native nn.Linear / Conv1D arithmetic, unchanged by STAC-R and bit-equal to it (Y = X W^T + b,
+grad_input = G W, grad_bias = G.sum(0)); it is not timed, and the time of G.sum(0) is reported
+beside the line.  K steps are timed as eager launches and replayed from a HIP graph captured
+once (every replay checked against the eager result; a mismatch fails the run); the value is
+the faster of the two and both are reported.  Other configured layers (cfg3 c_proj, cfg2 Turbo)
+and the basis refresh's Oja step are timed the same way and reported under "other_workloads".
+Prints one JSON line.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20]
 """
@@ -20,6 +25,8 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import platform
+import statistics
 import sys
 import time
 
@@ -31,25 +38,18 @@ for p in (ROOT, os.path.join(ROOT, "stac-r_amd"), os.path.join(ROOT, "tests")):
 METRIC = "STACRLinear save+bwd tokens/s (d=1024→4096 bf16) and % of HBM BW roofline"
 HBM_PEAK_GBS = 8000.0
 
-# workload
+# workload (cfg3 c_fc)
 N, D_IN, D_OUT, RANK = 8192, 1024, 4096, 8
 BUDGET, MODE, CHUNK, BITS = 0.005, "global_topk", 512, 8
-S_ACT = 2  # bf16 bytes
 
 
-def algorithmic_bytes(k: int) -> dict:
-    """Byte model per layer-step: U fp32, idx int32, int8 value + 4 B scale."""
-    save = N * D_IN * S_ACT + 4 * D_IN * RANK + N * RANK * S_ACT + 5 * k + 4
-    bwd = N * D_OUT * S_ACT + N * RANK * S_ACT + 5 * k + 4 + 4 * D_IN * RANK + D_OUT * D_IN * S_ACT
-    # minimal bytes each kernel's own job needs (reads of its inputs, writes of its outputs)
-    per_kernel = {
-        "k_proj_hist": N * D_IN * S_ACT + N * RANK * S_ACT,
-        "k_refine_hist": N * D_IN * S_ACT + N * RANK * S_ACT,
-        "k_count": N * D_IN * S_ACT + N * RANK * S_ACT,
-        "k_emit": N * D_IN * S_ACT + N * RANK * S_ACT + 5 * k,
-        "k_dw_fused": bwd,
-    }
-    return {"save": save, "bwd": bwd, "total": save + bwd, "per_kernel": per_kernel}
+def algorithmic_bytes(n, d_in, d_out, rank, k, s_act=2, s_w=2) -> dict:
+    """Byte model per layer-step: X, G, C in the activation dtype, U fp32, idx int32, int8 value,
+    4 B scale, dW in the weight dtype (save and backward each read the residual entries once)."""
+    res = 5 * k + 4 if k else 0
+    save = n * d_in * s_act + 4 * d_in * rank + n * rank * s_act + res
+    bwd = n * d_out * s_act + n * rank * s_act + res + 4 * d_in * rank + d_out * d_in * s_w
+    return {"save": save, "bwd": bwd, "total": save + bwd}
 
 
 def recorded_traffic(kernel: str):
@@ -64,33 +64,192 @@ def recorded_traffic(kernel: str):
     return None
 
 
-def cpu_baseline(x, q, g, budget_s: float = 12.0, max_steps: int = 6) -> dict:
-    """The oracle (a CPU restatement of the reference path) on the same workload, one thread."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
 
-    from oracle import oracle as orc
 
-    xf = x.float().cpu().numpy()
-    qf = q.float().cpu().numpy()
-    gf = g.float().cpu().numpy()
-    times = []
-    with threadpool_limits(1):
-        while len(times) < max_steps and sum(times) < budget_s:
+def cpu_baseline(x, q, g, budget_s: float = 25.0) -> dict:
+    """The reference op sequence as torch CPU library calls (oracle/torch_path.py) on the same
+    inputs, on all of this host's cores: 3 warm-up steps, then the median of up to 10."""
+    import torch
+
+    from oracle import torch_path
+
+    cores = os.cpu_count() or 1
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    xc, qc, gc = x.cpu(), q.cpu(), g.cpu()
+
+    def one():
+        torch_path.layer_step(xc, qc, gc, mode=MODE, budget=BUDGET, chunk_rows=CHUNK, bits=BITS, transposed=True,
+                              weight_dtype=torch.bfloat16)
+
+    try:
+        for _ in range(3):
+            one()
+        times, t_start = [], time.perf_counter()
+        while len(times) < 10 and time.perf_counter() - t_start < budget_s:
             t0 = time.perf_counter()
-            coeff, idx, data, scale = orc.save(xf, qf, "bf16", MODE, BUDGET, CHUNK, BITS)
-            vals = orc.dequantize(data, scale, BITS, idx.size)
-            orc.weight_grad(gf, coeff, qf, idx, vals, D_IN)
+            one()
             times.append(time.perf_counter() - t0)
-    per_step = float(np.median(times))
+    finally:
+        torch.set_num_threads(prev)
+    per_step = statistics.median(times)
     return {
         "value": N / per_step,
         "unit": "tokens/s",
-        "cores": 1,
+        "cores": cores,
         "kind": "port",
-        "sample": f"full c_fc layer-step (save + dW + dbias, {N} tokens), {len(times)} steps, median "
-                  f"{per_step * 1e3:.0f} ms/step; oracle/stacr_oracle.c + numpy fp64 projection, 1 thread",
+        "sample": f"full c_fc layer-step ({N} tokens, save + dW), median of {len(times)} after 3 warm-up, "
+                  f"{per_step * 1e3:.1f} ms/step; torch CPU ops in the reference's order (oracle/torch_path.py)",
+        "cpu_model": cpu_model(),
+        "torch": torch.__version__,
     }
+
+
+def time_steps(step, steps: int, warmup: int, check=None):
+    """(eager ms, graph ms or None, note) for `steps` calls of `step`; graph replays are checked
+    against an eager reference with `check(replay_outputs, eager_outputs)`, which raises."""
+    import torch
+
+    ref = step()
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / steps
+    try:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            outs = step()
+    except Exception as exc:  # capture itself unavailable: report eager timing only
+        torch.cuda.synchronize()
+        return eager_ms, None, f"graph capture unavailable ({exc}); value is eager"
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        step()  # eager work between replays
+        torch.cuda.synchronize()
+        if check is not None:
+            check(outs, ref)
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    return eager_ms, (time.perf_counter() - t0) * 1e3 / steps, None
+
+
+def _rel(a, b) -> float:
+    a, b = a.float(), b.float()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def check_layer(outs, ref):
+    """Save outputs are deterministic (bit-equal); dW sums the sparse term in arrival order."""
+    import torch
+
+    for a, b in zip(outs[:4], ref[:4]):
+        if (a is None) != (b is None) or (a is not None and not torch.equal(a, b)):
+            raise RuntimeError("graph replay of the save differs from the eager result")
+    if _rel(outs[4], ref[4]) > 1e-3:
+        raise RuntimeError("graph replay of the weight gradient differs from the eager result")
+
+
+def layer_workload(name, n, d_in, d_out, rank, budget, mode, steps, warmup, lognormal=True):
+    """Timing of one configured layer's save + dW (Conv1D layout, bf16)."""
+    import torch
+
+    from gpu_cases import make_activation, make_basis, make_grad
+    from stacr_amd import kernels
+
+    dev = torch.device("cuda:0")
+    x = make_activation(n, d_in, lognormal=lognormal).to(dev, torch.bfloat16)
+    q = make_basis(d_in, rank).to(dev, torch.bfloat16)
+    g = make_grad(n, d_out).to(dev, torch.bfloat16)
+    k = kernels.residual_plan(n, d_in, mode, budget, CHUNK)[1] if budget > 0 else 0
+
+    def step():
+        coeff, idx, data, scale = kernels.save(x, q, mode=mode, budget=budget, chunk_rows=CHUNK, bits=BITS)
+        res = (idx, data, scale) if idx is not None else None
+        dw, _ = kernels.weight_grad(g, coeff, q, res, BITS, True, torch.bfloat16)
+        return coeff, idx, data, scale, dw
+
+    eager, graph, note = time_steps(step, steps, warmup, check_layer)
+    ms = min(eager, graph) if graph is not None else eager
+    ab = algorithmic_bytes(n, d_in, d_out, rank, k)
+    out = {"config": name, "tokens": n, "d_in": d_in, "d_out": d_out, "rank": rank, "k": k,
+           "ms_per_step": ms, "tokens_per_s": n / (ms * 1e-3), "eager_ms": eager, "graph_ms": graph,
+           "algorithmic_bytes": ab["total"],
+           "pct_hbm_roofline": 100.0 * ab["total"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    if note:
+        out["note"] = note
+    return out
+
+
+def oja_workload(x, q, steps, warmup):
+    """The projection engine's basis refresh (one Oja step per training step by default,
+    stacr/layers.py:346-353) on the north-star activation: stacr_oja_step, then the reduced QR."""
+    import torch
+
+    from stacr_amd import kernels
+
+    q32 = q.float()
+
+    def step():
+        return kernels.oja_step(x, q32, 0.01)
+
+    def check(outs, ref):
+        for a, b in zip(outs, ref):
+            if not torch.equal(a, b):  # the Oja reductions have a fixed order
+                raise RuntimeError("graph replay of the Oja step differs from the eager result")
+
+    eager, graph, note = time_steps(step, steps, warmup, check)
+    ms = min(eager, graph) if graph is not None else eager
+    byts = N * D_IN * 2 + 2 * 4 * D_IN * RANK  # X once, basis in, update out (one fused pass)
+    out = {"config": "oja step on cfg3 c_fc X (8192 x 1024 bf16, rank 8), QR excluded",
+           "ms_per_step": ms, "eager_ms": eager, "graph_ms": graph, "algorithmic_bytes": byts,
+           "pct_hbm_roofline": 100.0 * byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    if note:
+        out["note"] = note
+    return out
+
+
+def copy_peak_gbs() -> float:
+    """Read + write GB/s of a 1 GiB device-to-device copy on this GPU (a measured stream peak)."""
+    import torch
+
+    a = torch.empty(1 << 30, dtype=torch.uint8, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    reps = 20
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    gbs = 2 * a.numel() * reps / (time.perf_counter() - t0) / 1e9
+    del a, b
+    torch.cuda.empty_cache()
+    return gbs
 
 
 def main() -> int:
@@ -98,8 +257,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of graph replay")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the other configured workloads")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -120,65 +279,16 @@ def main() -> int:
 
     def step():
         coeff, idx, data, scale = kernels.save(x, q, mode=MODE, budget=BUDGET, chunk_rows=CHUNK, bits=BITS)
-        dw, db = kernels.weight_grad(g, coeff, q, (idx, data, scale), BITS, True, torch.bfloat16, torch.bfloat16)
-        return coeff, idx, data, scale, dw, db
+        dw, _ = kernels.weight_grad(g, coeff, q, (idx, data, scale), BITS, True, torch.bfloat16)
+        return coeff, idx, data, scale, dw
 
     print(f"[bench] workload ready: k={k_saved}", file=sys.stderr, flush=True)
-    ref = step()
-    torch.cuda.synchronize()
-
-    # eager timing
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    print(f"[bench] eager {eager_ms:.4f} ms/step", file=sys.stderr, flush=True)
-
-    # graph replay: capture once, check replays against the eager result, then time
-    graph_ms, graph_note = None, None
-    if not args.no_graph:
-        try:
-            s = torch.cuda.Stream()
-            s.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(s):
-                step()
-            torch.cuda.current_stream().wait_stream(s)
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
-                outs = step()
-            for _ in range(3):
-                graph.replay()
-                torch.cuda.synchronize()
-                step()  # interleaved eager work between replays
-                torch.cuda.synchronize()
-                # save outputs are deterministic; dW/dbias sum the sparse term with LDS atomics
-                for a, b in zip(outs[:4], ref[:4]):
-                    if not torch.equal(a, b):
-                        raise RuntimeError("graph replay differs from the eager result")
-                for a, b in zip(outs[4:], ref[4:]):
-                    if ((a.float() - b.float()).norm() / b.float().norm()).item() > 1e-3:
-                        raise RuntimeError("graph replay differs from the eager result")
-            for _ in range(args.warmup):
-                graph.replay()
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            for _ in range(args.steps):
-                graph.replay()
-            torch.cuda.synchronize()
-            graph_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-            print(f"[bench] graph {graph_ms:.4f} ms/step", file=sys.stderr, flush=True)
-        except Exception as exc:  # graph capture unavailable: report eager
-            graph_note = f"graph replay unavailable ({exc}); value is eager"
-            print(f"[bench] {graph_note}", file=sys.stderr, flush=True)
-    # value: the faster of the two launch methods for the same K steps (both are reported)
+    eager_ms, graph_ms, graph_note = time_steps(step, args.steps, args.warmup, check_layer)
+    print(f"[bench] eager {eager_ms:.4f} ms/step, graph {graph_ms} ms/step", file=sys.stderr, flush=True)
     use_graph = graph_ms is not None and graph_ms <= eager_ms
     ms = graph_ms if use_graph else eager_ms
 
-    # per-kernel durations (HIP events around each launch, device kept busy ahead of each)
+    # per-kernel durations (HIP events around each launch on its stream, device kept busy ahead)
     prof_steps = 20
     with _lib.KernelTimer(max_launches=prof_steps * 64) as timer:
         for _ in range(prof_steps):
@@ -187,14 +297,26 @@ def main() -> int:
                    "launches_per_step": cnt / prof_steps}
             for name, (tot, cnt) in timer.results.items()}
     dominant = max(kern, key=lambda n: kern[n]["per_step_us"])
-    ab = algorithmic_bytes(k_saved)
-    dom_bytes = ab["per_kernel"].get(dominant)
+    ab = algorithmic_bytes(N, D_IN, D_OUT, RANK, k_saved)
+    per_kernel_bytes = {"k_dw_fused": ab["bwd"]}
+    dom_bytes = per_kernel_bytes.get(dominant)
     avg_s = kern[dominant]["avg_us"] * 1e-6
     achieved = dom_bytes / avg_s / 1e9 if dom_bytes else None
-    print(f"[bench] kernels: " + ", ".join(f"{n}={v['per_step_us']:.1f}us" for n, v in kern.items()),
+    print("[bench] kernels: " + ", ".join(f"{n}={v['per_step_us']:.1f}us" for n, v in kern.items()),
           file=sys.stderr, flush=True)
 
+    # the layer's native bias gradient (G.sum(0), unchanged from nn.Linear) for reference
+    for _ in range(5):
+        g.sum(0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(50):
+        g.sum(0)
+    torch.cuda.synchronize()
+    bias_us = (time.perf_counter() - t0) * 1e6 / 50
+
     path_gbs = ab["total"] / (ms * 1e-3) / 1e9
+    copy_gbs = copy_peak_gbs()
     out = {
         "metric": METRIC,
         "value": N / (ms * 1e-3),
@@ -210,14 +332,17 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": "cfg3 c_fc: STACRLinear save+bwd, Conv1D 1024->4096, N=8192 tokens, bf16, r=8, "
-                        "budget 0.005 global_topk, int8 residual, fused dbias",
+                        "budget 0.005 global_topk, int8 residual",
             "tokens": N, "d_in": D_IN, "d_out": D_OUT, "rank": RANK, "k": k_saved,
             "timing": "hip graph replay" if use_graph else "eager launches",
         },
         "pct_hbm_roofline": 100.0 * path_gbs / HBM_PEAK_GBS,
+        "pct_measured_copy_peak": 100.0 * path_gbs / copy_gbs,
+        "measured_copy_gbs": copy_gbs,
         "path_algorithmic_bytes": ab["total"],
         "eager_ms_per_step": eager_ms,
         "graph_ms_per_step": graph_ms,
+        "native_bias_grad_us": bias_us,
         "roofline": {
             "kernel": dominant,
             "bound": "hbm",
@@ -233,6 +358,17 @@ def main() -> int:
     }
     if graph_note:
         out["note"] = graph_note
+    if not args.no_extra:
+        extra_steps, extra_warm = max(10, args.steps // 4), max(3, args.warmup // 4)
+        out["other_workloads"] = [
+            layer_workload("cfg3 c_proj: Conv1D 4096->1024, N=8192, bf16, r=8, global_topk 0.005, int8",
+                           N, 4096, 1024, 8, BUDGET, MODE, extra_steps, extra_warm),
+            layer_workload("cfg2 Turbo: 1280->5120, N=8192, bf16, r=8, no residual",
+                           N, 1280, 5120, 8, 0.0, "chunk_topk", extra_steps, extra_warm, lognormal=False),
+            oja_workload(x, q, extra_steps, extra_warm),
+        ]
+        for w in out["other_workloads"]:
+            print(f"[bench] {w['config']}: {w['ms_per_step'] * 1e3:.1f} us", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(x, q, g)

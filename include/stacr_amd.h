@@ -270,7 +270,8 @@ int stacr_oja_step(const void *x, int dtype, int64_t rows, int64_t feats, const 
  * `sleep_us` device-side sleep so host enqueue gaps are not measured (up to max_launches
  * launches are recorded).  end synchronises the recorded events and returns, per kernel name in
  * first-launch order, the summed milliseconds and launch count (names: 64-byte slots).
- * Single-threaded use only; do not enable during stream capture.
+ * A session belongs to the thread that began it (thread-local state): it records that thread's
+ * launches only.  Do not enable during stream capture.
  */
 int stacr_profile_begin(int max_launches, double sleep_us);
 int stacr_profile_end(int max_kernels, char *names, double *total_ms, int *launches, int *n_kernels);

@@ -46,7 +46,7 @@ def lib():
         L.orc_sorted_keys.argtypes = [P, i64, P]
         L.orc_quantize.argtypes = [P, i64, i32, P, P]
         L.orc_pack_int4.argtypes = [P, i64, P]
-        L.orc_weight_grad.argtypes = [P, i64, i64, P, P, i64, i32, P, P, i64, P, P]
+        L.orc_weight_grad.argtypes, L.orc_weight_grad.restype = [P, i64, i64, P, P, i64, i32, P, P, i64, P, P], i32
         L.orc_round_dtype.argtypes, L.orc_round_dtype.restype = [ctypes.c_float, i32], ctypes.c_float
         L.orc_residual_act.argtypes = [P, P, P, i64, i64, i32, i32, P]
         L.orc_select_explicit.argtypes, L.orc_select_explicit.restype = [P, i64, i64, i64, i64, i64, P, P], i64
@@ -161,16 +161,35 @@ def dequantize(data: np.ndarray, scale: float, bits: int, length: int) -> np.nda
 
 
 # ---------------------------------------------------------------- weight gradient
+def check_indices(idx: np.ndarray, total: int, ascending: bool = False) -> None:
+    """Fail (AssertionError) when flat indices a kernel produced fall outside [0, total) or, with
+    ``ascending``, are not strictly increasing, before anything indexes memory with them."""
+    idx = np.asarray(idx, np.int64).reshape(-1)
+    if idx.size == 0:
+        return
+    lo, hi = int(idx.min()), int(idx.max())
+    if lo < 0 or hi >= total:
+        raise AssertionError(f"flat index out of range: min {lo}, max {hi}, allowed [0, {total})")
+    if ascending and idx.size > 1 and not bool(np.all(idx[1:] > idx[:-1])):
+        bad = int(np.argmax(idx[1:] <= idx[:-1]))
+        raise AssertionError(f"flat indices not strictly ascending at position {bad + 1}")
+
+
 def weight_grad(g, c, q, idx, vals, d_in: int):
     """fp64 dW (d_out x d_in) and dbias following stacr/layers.py:172-198."""
     g, c, q = _c(g, np.float32), _c(c, np.float32), _c(q, np.float32)
     idx, vals = _c(idx, np.int64).reshape(-1), _c(vals, np.float32).reshape(-1)
     n, d_out = g.shape
     r = c.shape[1]
+    check_indices(idx, n * d_in)
+    if vals.size != idx.size:
+        raise AssertionError(f"{idx.size} indices but {vals.size} values")
     dw = np.empty((d_out, d_in), np.float64)
     db = np.empty(d_out, np.float64)
-    lib().orc_weight_grad(_ptr(g), n, d_out, _ptr(c), _ptr(q), d_in, r, _ptr(idx), _ptr(vals),
-                          idx.size, _ptr(dw), _ptr(db))
+    rc = lib().orc_weight_grad(_ptr(g), n, d_out, _ptr(c), _ptr(q), d_in, r, _ptr(idx), _ptr(vals),
+                               idx.size, _ptr(dw), _ptr(db))
+    if rc != 0:
+        raise AssertionError("orc_weight_grad rejected an index outside [0, rows * d_in)")
     return dw, db
 
 

@@ -234,10 +234,13 @@ void orc_pack_int4(const int8_t *q, int64_t n, uint8_t *out)
  * Computed as M = G^T C (d_out x r) then M Q^T, then the sparse scatter, all in double.
  * dbias[o] = sum_t G[t][o] when dbias is not NULL (stacr/layers.py:197-198).
  */
-void orc_weight_grad(const float *g, int64_t n, int64_t d_out, const float *c, const float *q,
-                     int64_t d_in, int r, const int64_t *idx, const float *vals, int64_t nnz,
-                     double *dw, double *dbias)
+int orc_weight_grad(const float *g, int64_t n, int64_t d_out, const float *c, const float *q,
+                    int64_t d_in, int r, const int64_t *idx, const float *vals, int64_t nnz,
+                    double *dw, double *dbias)
 {
+    /* indices come from the kernel under test: reject any outside [0, n*d_in) before using them */
+    for (int64_t e = 0; e < nnz; ++e)
+        if (idx[e] < 0 || idx[e] >= n * d_in) return -1;
     double *m = (double *)calloc((size_t)(d_out * r), sizeof(double));
     for (int64_t t = 0; t < n; ++t) {
         const float *gt = g + t * d_out;
@@ -265,6 +268,7 @@ void orc_weight_grad(const float *g, int64_t n, int64_t d_out, const float *c, c
             for (int64_t o = 0; o < d_out; ++o) dbias[o] += (double)g[t * d_out + o];
     }
     free(m);
+    return 0;
 }
 
 /* Round an fp32 value to bf16 (code 1) or fp16 (code 2), nearest-even, returned as fp32; code 0

@@ -380,7 +380,9 @@ class STACRFunction(torch.autograd.Function):
         ctx.quantize_coefficients = coeff_scale is not None
         ctx.has_bias = bias is not None
         ctx.leading_shape = leading
-        ctx.basis = basis_c
+        # the backward must see the basis C was projected on: keep a private copy unless the
+        # dtype cast above already made one (a caller may update its basis in place meanwhile)
+        ctx.basis = basis_c.detach().clone() if basis_c is basis else basis_c.detach()
         ctx.b_flat, ctx.in_features = b_flat, in_features
         return out.reshape(*leading, weight.shape[0])
 

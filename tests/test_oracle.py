@@ -228,3 +228,25 @@ def test_weight_grad_single_entry_and_identity_basis():
     dw, _ = orc.weight_grad(g, x, np.eye(d_in, dtype=np.float32), np.zeros(0, np.int64),
                             np.zeros(0, np.float32), d_in)
     assert np.allclose(dw, g.astype(np.float64).T @ x.astype(np.float64), rtol=1e-12, atol=1e-12)
+
+
+def test_weight_grad_rejects_out_of_range_indices():
+    """Indices a kernel emitted are checked before the oracle indexes G with them: a bad one fails
+    the calling test (AssertionError) instead of crashing the test process."""
+    rng = np.random.default_rng(5)
+    g = rng.standard_normal((8, 3)).astype(np.float32)
+    c = rng.standard_normal((8, 2)).astype(np.float32)
+    q = rng.standard_normal((4, 2)).astype(np.float32)
+    vals = np.ones(2, np.float32)
+    for bad in ([0, 32], [-1, 3], [5, 1 << 40]):
+        with pytest.raises(AssertionError, match="out of range"):
+            orc.weight_grad(g, c, q, np.array(bad, np.int64), vals, 4)
+    with pytest.raises(AssertionError, match="ascending"):
+        orc.check_indices(np.array([3, 3, 7]), 32, ascending=True)
+    orc.check_indices(np.array([0, 3, 31]), 32, ascending=True)
+    # the C entry point itself refuses (returns non-zero) without the Python pre-check
+    idx = np.array([0, 32], np.int64)
+    dw = np.empty((3, 4)); db = np.empty(3)
+    rc = orc.lib().orc_weight_grad(orc._ptr(g), 8, 3, orc._ptr(c), orc._ptr(q), 4, 2, orc._ptr(idx),
+                                   orc._ptr(vals), 2, orc._ptr(dw), orc._ptr(db))
+    assert rc != 0
