@@ -21,6 +21,8 @@
  *   stacr_select_uniform / stacr_select_block_sparse / stacr_sample_magnitudes /
  *   stacr_select_threshold   the "uniform", "block_sparse", "sampled" selectors,
  *                            stacr/layers.py:55-99
+ *   stacr_adaptive_block_sparse_plan / stacr_adaptive_select_block_sparse
+ *                            the adaptive engine's block_sparse selector, stacr/adaptive.py:1788-1938
  *   stacr_oja_step           the Oja step of STACRLinear._refresh_basis, stacr/layers.py:346-348,
  *                            and OjaBasis.update, stacr/oja.py:73-79
  */
@@ -235,6 +237,22 @@ int stacr_block_sparse_plan(int64_t rows, int64_t feats, double budget, int64_t 
 int stacr_select_block_sparse(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t feats,
                               int rank, double budget, int64_t chunk_rows, int64_t block_size, void *idx,
                               int index_bytes, void *values, void *workspace, size_t workspace_bytes, void *stream);
+/* The adaptive engine's block_sparse (stacr/adaptive.py:1788-1938), its default residual mode.
+ * Blocks are `block_size` columns of one row (the row's last block padded with zeros when
+ * feats % block_size != 0).  k = floor(rows*feats*budget); k_blocks = max(1, ceil(k/block_size));
+ * per chunk of chunk_rows rows the max(1, ceil(k_blocks*chunk/rows)) blocks of largest energy
+ * rnd(sum rnd(r^2)) (ties: lowest block), then the k_blocks largest of all those candidates.  Every
+ * stored column of the kept blocks is written, ascending: *max_entries = kept blocks * block_size
+ * is exact when feats % block_size == 0 and an upper bound otherwise; the number written goes to
+ * the device int64 *count.  index_bytes follows _choose_index_dtype (2 below 32768 elements, 4 up
+ * to 2^31, else 8); *k_blocks = 0 means no residual (no kernel runs, *count = 0). */
+int stacr_adaptive_block_sparse_plan(int64_t rows, int64_t feats, double budget, int64_t chunk_rows,
+                                     int64_t block_size, int64_t *k_blocks, int64_t *max_entries, int *index_bytes,
+                                     size_t *workspace_bytes);
+int stacr_adaptive_select_block_sparse(const void *x, const void *coeff, const void *q, int dtype, int64_t rows,
+                                       int64_t feats, int rank, double budget, int64_t chunk_rows, int64_t block_size,
+                                       void *idx, int index_bytes, void *values, int64_t *count, void *workspace,
+                                       size_t workspace_bytes, void *stream);
 /* sampled (:55-66), step 1: out[i] = |r| at flat position positions[i] (int64, device), in dtype.
  * The caller draws the positions (torch.randint with the reference's seeded generator) and takes
  * the quantile of the magnitudes (torch.quantile), as the reference does.  A position outside

@@ -448,3 +448,59 @@ def select_threshold(resid: np.ndarray, threshold: float, dtype: str, cap: int):
     with np.errstate(invalid="ignore"):
         idx = np.nonzero(np.abs(flat) >= t)[0][:cap].astype(np.int64)
     return idx, flat[idx]
+
+
+# ================================================================ adaptive engine's block_sparse
+# (stacr/adaptive.py:1788-1938), on the dtype-native residual of residual_act.
+def adaptive_block_energies(resid: np.ndarray, block_size: int, dtype: str) -> np.ndarray:
+    """Energy of every block of `block_size` columns of one row, the row's last block padded with
+    zeros (:1847-1868): rnd(sum_o rnd(r_o^2)), an fp32 sum in column order; rows * ceil(d / bs) values."""
+    resid = np.asarray(resid, np.float32)
+    rows, d = resid.shape
+    bpr = -(-d // block_size)
+    padded = np.zeros((rows, bpr * block_size), np.float32)
+    padded[:, :d] = resid
+    sq = round_to(padded * padded, dtype).reshape(rows * bpr, block_size)
+    acc = np.zeros(rows * bpr, np.float32)
+    for o in range(block_size):
+        acc = (acc + sq[:, o]).astype(np.float32)
+    return round_to(acc, dtype)
+
+
+def adaptive_block_plan(rows: int, feats: int, budget: float, chunk_rows: int, block_size: int):
+    """(k_blocks, chunk rows, blocks kept per chunk) of the adaptive selector (:1791-1802, :1833)."""
+    total = rows * feats
+    k = min(int(total * budget), total)
+    if k <= 0:
+        return 0, 0, 0
+    k_blocks = max(1, -(-k // block_size))
+    chunk = min(chunk_rows, rows)
+    return k_blocks, chunk, max(1, (k_blocks * chunk + rows - 1) // rows)
+
+
+def adaptive_select_block_sparse(resid: np.ndarray, budget: float, chunk_rows: int, block_size: int, dtype: str):
+    """(idx ascending, values) of the adaptive block_sparse selector: per chunk the top blocks by
+    energy, then the top k_blocks of all candidates, ties to the lowest block (the reference's
+    torch.topk leaves them open); every stored column of the kept blocks (padding dropped)."""
+    resid = np.asarray(resid, np.float32)
+    rows, d = resid.shape
+    k_blocks, chunk, per = adaptive_block_plan(rows, d, budget, chunk_rows, block_size)
+    if k_blocks == 0:
+        return np.zeros(0, np.int64), np.zeros(0, np.float32)
+    bpr = -(-d // block_size)
+    keys = adaptive_block_energies(resid, block_size, dtype).view(np.uint32) & np.uint32(0x7FFFFFFF)
+    keys = keys.astype(np.int64)
+    cands = []
+    for start in range(0, rows, chunk):
+        lo, hi = start * bpr, min(start + chunk, rows) * bpr
+        b = np.arange(lo, hi)
+        order = np.lexsort((b, -keys[lo:hi]))
+        cands.append(b[order[:min(per, hi - lo)]])
+    cand = np.concatenate(cands)
+    if cand.size > k_blocks:
+        cand = cand[np.lexsort((cand, -keys[cand]))[:k_blocks]]
+    cand = np.sort(cand)
+    cols = (cand % bpr)[:, None] * block_size + np.arange(block_size)[None, :]
+    flat = (cand // bpr)[:, None] * d + cols
+    idx = flat[cols < d].astype(np.int64)
+    return idx, resid.reshape(-1)[idx]

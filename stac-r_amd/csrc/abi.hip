@@ -582,6 +582,83 @@ int stacr_select_block_sparse(const void *x, const void *coeff, const void *q, i
                               workspace, static_cast<hipStream_t>(stream));
 }
 
+namespace {
+
+// Counts of the adaptive block_sparse selector (stacr/adaptive.py:1788-1832): k = floor(total * b)
+// entries, k_blocks = max(1, ceil(k / bs)), per chunk max(1, ceil(k_blocks * chunk / rows)) blocks
+// (at most the chunk's own), the union cut to k_blocks.
+struct AdaptiveBlockPlan {
+    int64_t k_blocks = 0, chunk_rows = 0, count_full = 0, count_last = 0, n_cand = 0, n_final = 0;
+    int index_bytes = 4;
+};
+
+int plan_adaptive_blocks(int64_t rows, int64_t feats, double budget, int64_t chunk_rows, int64_t bs,
+                         AdaptiveBlockPlan *p)
+{
+    if (rows < 1 || feats < 1 || chunk_rows < 1 || bs < 1)
+        return stacr_fail(STACR_ERR_INVALID, "adaptive block_sparse: needs rows, feats, chunk_rows, block_size >= 1");
+    if (!(budget >= 0.0 && budget <= 1.0)) return stacr_fail(STACR_ERR_INVALID, "budget %g outside [0, 1]", budget);
+    const int64_t total = rows * feats;
+    p->index_bytes = total < 32768 ? 2 : (total <= (1ll << 31) ? 4 : 8);
+    int64_t k = (int64_t)((double)total * budget);
+    if (k > total) k = total;
+    if (k <= 0) return STACR_OK;
+    const int64_t bpr = (feats + bs - 1) / bs;
+    p->k_blocks = (k + bs - 1) / bs;
+    p->chunk_rows = chunk_rows < rows ? chunk_rows : rows;
+    const int64_t n_seg = (rows + p->chunk_rows - 1) / p->chunk_rows;
+    const int64_t last_rows = rows - (n_seg - 1) * p->chunk_rows;
+    int64_t per = (p->k_blocks * p->chunk_rows + rows - 1) / rows;
+    if (per < 1) per = 1;
+    p->count_full = per < p->chunk_rows * bpr ? per : p->chunk_rows * bpr;
+    p->count_last = per < last_rows * bpr ? per : last_rows * bpr;
+    p->n_cand = (n_seg - 1) * p->count_full + p->count_last;
+    p->n_final = p->n_cand < p->k_blocks ? p->n_cand : p->k_blocks;
+    return STACR_OK;
+}
+
+}  // namespace
+
+int stacr_adaptive_block_sparse_plan(int64_t rows, int64_t feats, double budget, int64_t chunk_rows,
+                                     int64_t block_size, int64_t *k_blocks, int64_t *max_entries, int *index_bytes,
+                                     size_t *workspace_bytes)
+{
+    AdaptiveBlockPlan p;
+    const int rc = plan_adaptive_blocks(rows, feats, budget, chunk_rows, block_size, &p);
+    if (rc) return rc;
+    if (k_blocks) *k_blocks = p.k_blocks;
+    if (max_entries) *max_entries = p.n_final * block_size;
+    if (index_bytes) *index_bytes = p.index_bytes;
+    if (workspace_bytes)
+        *workspace_bytes = p.k_blocks ? stacr_adaptive_block_ws(rows, feats, block_size, p.n_cand, p.k_blocks) : 0;
+    return STACR_OK;
+}
+
+int stacr_adaptive_select_block_sparse(const void *x, const void *coeff, const void *q, int dtype, int64_t rows,
+                                       int64_t feats, int rank, double budget, int64_t chunk_rows, int64_t block_size,
+                                       void *idx, int index_bytes, void *values, int64_t *count, void *workspace,
+                                       size_t workspace_bytes, void *stream)
+{
+    int rc = check_factors(x, coeff, q, dtype, rows, feats, rank, "stacr_adaptive_select_block_sparse");
+    if (rc) return rc;
+    AdaptiveBlockPlan p;
+    rc = plan_adaptive_blocks(rows, feats, budget, chunk_rows, block_size, &p);
+    if (rc) return rc;
+    if (index_bytes != p.index_bytes)
+        return stacr_fail(STACR_ERR_INVALID, "stacr_adaptive_select_block_sparse: index_bytes must be %d", p.index_bytes);
+    if (!count) return stacr_fail(STACR_ERR_INVALID, "stacr_adaptive_select_block_sparse: NULL count");
+    if (!p.k_blocks) return stacr_hip_check(hipMemsetAsync(count, 0, 8, static_cast<hipStream_t>(stream)), "count");
+    if (!idx || !values || !workspace)
+        return stacr_fail(STACR_ERR_INVALID, "stacr_adaptive_select_block_sparse: NULL pointer argument");
+    const size_t need = stacr_adaptive_block_ws(rows, feats, block_size, p.n_cand, p.k_blocks);
+    if (workspace_bytes < need)
+        return stacr_fail(STACR_ERR_WORKSPACE, "stacr_adaptive_select_block_sparse: workspace has %zu bytes, needs %zu",
+                          workspace_bytes, need);
+    return stacr_adaptive_block_launch(x, coeff, q, dtype, rows, feats, rank, block_size, p.chunk_rows, p.count_full,
+                                       p.count_last, p.k_blocks, idx, index_bytes, values, count, workspace,
+                                       static_cast<hipStream_t>(stream));
+}
+
 int stacr_sample_magnitudes(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t feats,
                             int rank, const int64_t *positions, int64_t n, void *out, void *stream)
 {

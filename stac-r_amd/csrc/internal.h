@@ -280,6 +280,11 @@ int stacr_delta_decode_launch(const void *base, int base_bytes, const void *delt
 int stacr_uniform_launch(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t d,
                          int rank, int64_t k, void *idx, int idx_bytes, void *values, hipStream_t s);
 size_t stacr_block_ws(int64_t rows, int64_t d, int64_t bs, int64_t n_seg, int64_t count_full);
+size_t stacr_adaptive_block_ws(int64_t rows, int64_t d, int64_t bs, int64_t n_cand, int64_t k_blocks);
+int stacr_adaptive_block_launch(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t d,
+                                int rank, int64_t bs, int64_t chunk_rows, int64_t count_full, int64_t count_last,
+                                int64_t k_blocks, void *idx, int idx_bytes, void *values, int64_t *count, void *ws,
+                                hipStream_t s);
 int stacr_block_launch(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t d, int rank,
                        int64_t bs, int64_t seg_rows, int64_t count_full, int64_t count_last, void *idx,
                        int idx_bytes, void *values, void *ws, hipStream_t s);

@@ -5,9 +5,12 @@
 //   sampled       |r| >= quantile of a seeded sample, first k_total in flat order (:55-66);
 //                 the sample positions and the quantile are torch library calls on the host side,
 //                 the gather of the sampled magnitudes and the ordered compaction run here.
+// and the adaptive engine's block_sparse (stacr/adaptive.py:1788-1938): blocks of `bs` columns of
+// one row (the last block of a row padded with zeros), per chunk of rows the top
+// ceil(k_blocks * chunk / rows) blocks by energy, then the top k_blocks of all those candidates.
 // Every residual is the dtype-native r = rnd(x - rnd(sum_j c_j q_j)) of the save kernels.
-// Output indices ascend.  Block ties take the lowest block index (the reference's
-// torch.topk(sorted=False) leaves that choice unspecified).
+// Output indices ascend.  Block ties take the lowest block index (the reference's torch.topk
+// leaves that choice unspecified).
 #include "internal.h"
 
 using namespace stacr;
@@ -33,7 +36,8 @@ __device__ __forceinline__ float resid_at(const typename Act<DT>::T *__restrict_
 __device__ __forceinline__ void put_index(void *idx, int bytes, int64_t i, int64_t v)
 {
     if (bytes == 8) static_cast<int64_t *>(idx)[i] = v;
-    else static_cast<int32_t *>(idx)[i] = (int32_t)v;
+    else if (bytes == 4) static_cast<int32_t *>(idx)[i] = (int32_t)v;
+    else static_cast<int16_t *>(idx)[i] = (int16_t)v;
 }
 
 // ------------------------------------------------------------------ uniform
@@ -53,20 +57,28 @@ __global__ __launch_bounds__(kBlock) void k_uniform(const typename Act<DT>::T *_
 }
 
 // ------------------------------------------------------------------ block_sparse
-// Key of block b: fp32 bits of rnd(sum_o rnd(r_o^2)) (energy >= 0; NaN sorts above +inf).
+// Key of block b: fp32 bits of rnd(sum_o rnd(r_o^2)) (energy >= 0; NaN sorts above +inf).  Block b
+// covers columns [(b % bpr) * bs, + bs) of row b / bpr, bpr = ceil(d / bs); columns past d are the
+// zero padding and add nothing.  (With d % bs == 0 the blocks are consecutive flat elements.)
+__device__ __forceinline__ int64_t block_width(int64_t b, int64_t bpr, int64_t bs, int64_t d)
+{
+    const int64_t col0 = (b % bpr) * bs;
+    return d - col0 < bs ? d - col0 : bs;
+}
+
 template <int DT>
 __global__ __launch_bounds__(kBlock) void k_block_keys(const typename Act<DT>::T *__restrict__ x,
                                                        const typename Act<DT>::T *__restrict__ coeff,
                                                        const typename Act<DT>::T *__restrict__ q, int64_t d,
-                                                       int rank, int64_t bs, int64_t n_blocks,
+                                                       int rank, int64_t bs, int64_t bpr, int64_t n_blocks,
                                                        uint32_t *__restrict__ keys)
 {
     const int64_t b = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     if (b >= n_blocks) return;
-    const int64_t pos0 = b * bs;
-    const int64_t row = pos0 / d, col0 = pos0 - row * d;  // d % bs == 0: a block never crosses a row
+    const int64_t row = b / bpr, col0 = (b - row * bpr) * bs;
+    const int64_t width = block_width(b, bpr, bs, d);
     float e = 0.f;
-    for (int64_t o = 0; o < bs; ++o) {
+    for (int64_t o = 0; o < width; ++o) {
         const float r = resid_at<DT>(x, coeff, q, d, rank, row, col0 + o);
         e += Act<DT>::rnd(r * r);
     }
@@ -157,6 +169,64 @@ __global__ __launch_bounds__(kBlock) void k_block_emit(const typename Act<DT>::T
     const int64_t pos = blk * bs + e % bs;
     const int64_t row = pos / d, col = pos - row * d;
     put_index(idx, idx_bytes, e, pos);
+    values[e] = Act<DT>::st(resid_at<DT>(x, coeff, q, d, rank, row, col));
+}
+
+// Keys of the candidate blocks, in candidate order (ascending block ids), for the global trim.
+__global__ __launch_bounds__(kBlock) void k_block_gather_keys(const uint32_t *__restrict__ keys,
+                                                              const uint32_t *__restrict__ cand, int64_t n_cand,
+                                                              uint32_t *__restrict__ ckeys)
+{
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i < n_cand) ckeys[i] = keys[cand[i]];
+}
+
+// One workgroup: the final block list (candidates, or the candidates at the trim's positions),
+// each block's first output slot (exclusive scan of the block widths) and the entry count.
+__global__ __launch_bounds__(kSegThreads) void k_block_offsets(const uint32_t *__restrict__ cand,
+                                                               const uint32_t *__restrict__ pick, int64_t n_final,
+                                                               int64_t bpr, int64_t bs, int64_t d,
+                                                               uint32_t *__restrict__ final_blocks,
+                                                               int64_t *__restrict__ offsets,
+                                                               int64_t *__restrict__ count)
+{
+    __shared__ uint32_t s_tot[kSegThreads / 64];
+    int64_t run = 0;
+    for (int64_t t0 = 0; t0 < n_final; t0 += kSegThreads) {
+        const int64_t i = t0 + threadIdx.x;
+        uint32_t width = 0;
+        if (i < n_final) {
+            const uint32_t b = pick ? cand[pick[i]] : cand[i];
+            final_blocks[i] = b;
+            width = (uint32_t)block_width(b, bpr, bs, d);
+        }
+        uint32_t all;
+        const uint32_t before = block_exclusive_scan<kSegThreads>(width, s_tot, &all);
+        if (i < n_final) offsets[i] = run + before;
+        run += all;
+    }
+    if (threadIdx.x == 0) *count = run;
+}
+
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_block_emit_rows(const typename Act<DT>::T *__restrict__ x,
+                                                            const typename Act<DT>::T *__restrict__ coeff,
+                                                            const typename Act<DT>::T *__restrict__ q, int64_t d,
+                                                            int rank, int64_t bs, int64_t bpr, int64_t n_blocks,
+                                                            const uint32_t *__restrict__ final_blocks,
+                                                            const int64_t *__restrict__ offsets, int64_t n_final,
+                                                            void *idx, int idx_bytes,
+                                                            typename Act<DT>::T *__restrict__ values)
+{
+    const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    const int64_t i = t / bs, o = t - (t / bs) * bs;
+    if (i >= n_final) return;
+    const int64_t b0 = final_blocks[i];
+    const int64_t b = b0 < n_blocks ? b0 : n_blocks - 1;  // reads stay inside X whatever the list holds
+    if (o >= block_width(b, bpr, bs, d)) return;  // zero padding past the row's end is not stored
+    const int64_t row = b / bpr, col = (b - row * bpr) * bs + o;
+    const int64_t e = offsets[i] + o;
+    put_index(idx, idx_bytes, e, row * d + col);
     values[e] = Act<DT>::st(resid_at<DT>(x, coeff, q, d, rank, row, col));
 }
 
@@ -285,7 +355,7 @@ int block_typed(const void *x, const void *coeff, const void *q, int64_t rows, i
     const int64_t n_out = ((n_seg - 1) * count_full + count_last) * bs;
     stacr_launch("k_block_keys", s, [&] {
         k_block_keys<DT><<<blocks_of(n_blocks), kBlock, 0, s>>>((TP<DT>)x, (TP<DT>)coeff, (TP<DT>)q, d, rank, bs,
-                                                               n_blocks, keys);
+                                                               d / bs, n_blocks, keys);
     });
     stacr_launch("k_block_select", s, [&] {
         k_block_select<<<(unsigned)n_seg, kSegThreads, 0, s>>>(keys, n_blocks, seg_blocks, count_full, count_last,
@@ -296,6 +366,76 @@ int block_typed(const void *x, const void *coeff, const void *q, int64_t rows, i
                                                             n_blocks, sel, n_out, idx, idx_bytes, (T *)values);
     });
     return stacr_hip_check(hipGetLastError(), "block_sparse selector");
+}
+
+// Workspace of the adaptive block_sparse selector, carved from one caller-supplied buffer.
+struct AdaptiveBlockWs {
+    uint32_t *keys;          // energy key per block (rows * bpr)
+    uint32_t *cand;          // per-chunk picks, chunk c at c * count_full (n_cand in total)
+    uint32_t *ckeys;         // keys of the candidates (global trim)
+    uint32_t *pick;          // positions in `cand` the global trim keeps (k_blocks)
+    uint32_t *final_blocks;  // the kept blocks, ascending
+    int64_t *offsets;        // first output slot of each kept block
+};
+
+AdaptiveBlockWs adaptive_block_layout(void *ws, int64_t n_blocks, int64_t n_cand, int64_t k_blocks, size_t *total)
+{
+    char *p = static_cast<char *>(ws);
+    size_t at = 0;
+    auto take = [&](size_t bytes) {
+        char *here = p ? p + at : nullptr;
+        at += (bytes + 255) & ~size_t(255);
+        return here;
+    };
+    AdaptiveBlockWs w;
+    w.keys = reinterpret_cast<uint32_t *>(take((size_t)n_blocks * 4));
+    w.cand = reinterpret_cast<uint32_t *>(take((size_t)n_cand * 4));
+    w.ckeys = reinterpret_cast<uint32_t *>(take((size_t)n_cand * 4));
+    w.pick = reinterpret_cast<uint32_t *>(take((size_t)k_blocks * 4));
+    w.final_blocks = reinterpret_cast<uint32_t *>(take((size_t)n_cand * 4));
+    w.offsets = reinterpret_cast<int64_t *>(take((size_t)n_cand * 8));
+    if (total) *total = at;
+    return w;
+}
+
+template <int DT>
+int adaptive_block_typed(const void *x, const void *coeff, const void *q, int64_t rows, int64_t d, int rank,
+                         int64_t bs, int64_t chunk_rows, int64_t n_seg, int64_t count_full, int64_t count_last,
+                         int64_t k_blocks, void *idx, int idx_bytes, void *values, int64_t *count,
+                         const AdaptiveBlockWs &w, hipStream_t s)
+{
+    using T = typename Act<DT>::T;
+    const int64_t bpr = (d + bs - 1) / bs;
+    const int64_t n_blocks = rows * bpr;
+    const int64_t n_cand = (n_seg - 1) * count_full + count_last;
+    const bool trim = n_cand > k_blocks;
+    const int64_t n_final = trim ? k_blocks : n_cand;
+    stacr_launch("k_block_keys", s, [&] {
+        k_block_keys<DT><<<blocks_of(n_blocks), kBlock, 0, s>>>((TP<DT>)x, (TP<DT>)coeff, (TP<DT>)q, d, rank, bs,
+                                                               bpr, n_blocks, w.keys);
+    });
+    stacr_launch("k_block_select", s, [&] {
+        k_block_select<<<(unsigned)n_seg, kSegThreads, 0, s>>>(w.keys, n_blocks, chunk_rows * bpr, count_full,
+                                                                count_last, w.cand);
+    });
+    if (trim) {
+        stacr_launch("k_block_gather_keys", s, [&] {
+            k_block_gather_keys<<<blocks_of(n_cand), kBlock, 0, s>>>(w.keys, w.cand, n_cand, w.ckeys);
+        });
+        stacr_launch("k_block_select", s, [&] {
+            k_block_select<<<1, kSegThreads, 0, s>>>(w.ckeys, n_cand, n_cand, k_blocks, k_blocks, w.pick);
+        });
+    }
+    stacr_launch("k_block_offsets", s, [&] {
+        k_block_offsets<<<1, kSegThreads, 0, s>>>(w.cand, trim ? w.pick : nullptr, n_final, bpr, bs, d, w.final_blocks,
+                                                  w.offsets, count);
+    });
+    stacr_launch("k_block_emit", s, [&] {
+        k_block_emit_rows<DT><<<blocks_of(n_final * bs), kBlock, 0, s>>>((TP<DT>)x, (TP<DT>)coeff, (TP<DT>)q, d, rank,
+                                                                        bs, bpr, n_blocks, w.final_blocks, w.offsets,
+                                                                        n_final, idx, idx_bytes, (T *)values);
+    });
+    return stacr_hip_check(hipGetLastError(), "adaptive block_sparse selector");
 }
 
 template <int DT>
@@ -367,6 +507,25 @@ int stacr_block_launch(const void *x, const void *coeff, const void *q, int dtyp
     const int64_t seg_blocks = seg_rows * d / bs;
     STACR_DT_SWITCH(dtype, block_typed<DT>(x, coeff, q, rows, d, rank, bs, seg_blocks, n_seg, count_full, count_last,
                                            idx, idx_bytes, values, keys, sel, s))
+}
+
+size_t stacr_adaptive_block_ws(int64_t rows, int64_t d, int64_t bs, int64_t n_cand, int64_t k_blocks)
+{
+    size_t total = 0;
+    adaptive_block_layout(nullptr, rows * ((d + bs - 1) / bs), n_cand, k_blocks, &total);
+    return total;
+}
+
+int stacr_adaptive_block_launch(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t d,
+                                int rank, int64_t bs, int64_t chunk_rows, int64_t count_full, int64_t count_last,
+                                int64_t k_blocks, void *idx, int idx_bytes, void *values, int64_t *count, void *ws,
+                                hipStream_t s)
+{
+    const int64_t n_seg = (rows + chunk_rows - 1) / chunk_rows;
+    const int64_t n_cand = (n_seg - 1) * count_full + count_last;
+    const AdaptiveBlockWs w = adaptive_block_layout(ws, rows * ((d + bs - 1) / bs), n_cand, k_blocks, nullptr);
+    STACR_DT_SWITCH(dtype, adaptive_block_typed<DT>(x, coeff, q, rows, d, rank, bs, chunk_rows, n_seg, count_full,
+                                                    count_last, k_blocks, idx, idx_bytes, values, count, w, s))
 }
 
 int stacr_sample_launch(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t d,

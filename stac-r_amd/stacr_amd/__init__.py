@@ -4,8 +4,9 @@ Drop-in for the reference package's public API (Manar-Hamed/STAC-R, stacr/__init
 ``import stacr_amd as stacr``.  The arithmetic runs in HIP kernels (libstacr_amd.so, C ABI in
 include/stacr_amd.h); this package is the host side.
 """
+from .adaptive import AdaptiveSTACRConfig, AdaptiveSTACRLinear, apply_adaptive_stacr, set_stacr_runtime_state
 from .layers import STACRFunction, STACRLinear
-from .memory import stacr_stored_bytes
+from .memory import saved_surface_predictor, stacr_stored_bytes
 from .quant import QuantizedValues, quantize_values
 from .surgery import apply_stacr, classify, select_target_names, set_step
 
@@ -19,4 +20,9 @@ __all__ = [
     "quantize_values",
     "QuantizedValues",
     "stacr_stored_bytes",
+    "saved_surface_predictor",
+    "AdaptiveSTACRConfig",
+    "AdaptiveSTACRLinear",
+    "apply_adaptive_stacr",
+    "set_stacr_runtime_state",
 ]

@@ -62,6 +62,9 @@ SIGNATURES = {
     "stacr_threshold_workspace_bytes": ([_i64, _i64, _PSZ], _i32),
     "stacr_select_threshold": ([_p, _p, _p, _i32, _i64, _i64, _i32, _p, _i64, _p, _i32, _p, _p, _p, _sz, _p],
                                _i32),
+    "stacr_adaptive_block_sparse_plan": ([_i64, _i64, _f64, _i64, _i64, _P64, _P64, _PI32, _PSZ], _i32),
+    "stacr_adaptive_select_block_sparse": ([_p, _p, _p, _i32, _i64, _i64, _i32, _f64, _i64, _i64, _p, _i32, _p, _p, _p,
+                                            _sz, _p], _i32),
     "stacr_oja_workspace_bytes": ([_i64, _i64, _i32, _PSZ], _i32),
     "stacr_oja_step": ([_p, _i32, _i64, _i64, _p, _i32, ctypes.c_float, _p, _p, _p, _sz, _p], _i32),
 }

@@ -140,24 +140,56 @@ _BASIS_DTYPES = {
     "float16": torch.float16, "fp16": torch.float16,
     "bfloat16": torch.bfloat16, "bf16": torch.bfloat16,
 }
+_FOLLOW_WEIGHT_DTYPE = ("auto", "activation")
 
 
-def _positive_int(name: str, value) -> None:
-    if isinstance(value, bool) or int(value) != value or value < 1:
-        raise ValueError(f"{name} must be a positive integer")
+def _is_int(value) -> bool:
+    return not isinstance(value, bool) and int(value) == value
 
 
-def _optional_nonneg_int(name: str, value) -> None:
-    if value is not None and (isinstance(value, bool) or int(value) != value or value < 0):
-        raise ValueError(f"{name} must be a nonnegative integer")
+def _finite(value) -> bool:
+    return math.isfinite(value)
+
+
+# Option checks in the order a caller meets them, with the reference's messages (callers catch the
+# ValueError; the first failing check names the option).  Each entry: (options, test, message).
+_OPTION_CHECKS = (
+    (("rank", "update_interval", "chunk_rows", "residual_block_size"),
+     lambda v: _is_int(v) and v >= 1, "{} must be a positive integer"),
+    (("residual_budget",), lambda v: _finite(v) and 0 <= v <= 1, "residual_budget must be between 0 and 1"),
+    (("residual_bits",), lambda v: v in (0, 4, 8), "residual_bits must be 0, 4, or 8"),
+    (("oja_lr",), lambda v: _finite(v) and v >= 0, "oja_lr must be finite and nonnegative"),
+    (("warmup_steps", "turbo_after_step"), lambda v: v is None or (_is_int(v) and v >= 0),
+     "{} must be a nonnegative integer"),
+    (("residual_mode",), lambda v: v in RESIDUAL_MODES, f"residual_mode must be one of {sorted(RESIDUAL_MODES)}"),
+    (("residual_sample_ratio",), lambda v: _finite(v) and 0 < v <= 1, "residual_sample_ratio must be in (0, 1]"),
+)
+
+
+def _check_options(options: dict) -> None:
+    for names, ok, message in _OPTION_CHECKS:
+        for name in names:
+            if not ok(options[name]):
+                raise ValueError(message.format(name))
+
+
+def _chunk_sizes(rows: int, chunk_rows: int):
+    return (min(chunk_rows, rows - start) for start in range(0, rows, chunk_rows))
 
 
 class STACRLinear(nn.Module):
-    """Linear projection whose saved input is compressed; parameters are unchanged.
+    """Linear projection whose saved input is compressed; the parameters are unchanged.
 
-    Call set_step (or stacr_amd.set_step) with the optimizer step before each training forward.
-    Eval, no-grad and frozen-weight calls use the exact native op.  Turbo (step >=
-    turbo_after_step) freezes the basis and drops the residual; the weights keep training.
+    Call set_step (or stacr_amd.set_step) with the optimizer step before each training forward;
+    every call within one step shares that step's basis, checkpoint replay included.  Eval,
+    no-grad and frozen-weight calls run the exact native op.  Turbo (step >= turbo_after_step)
+    freezes the basis and drops the residual; the weights keep training.
+
+    Basis schedule (stacr/layers.py:323-354): the first training forward fits the basis to its
+    batch (SVD of the fp32 rows; a seeded random basis when there are fewer rows than the rank);
+    afterwards one Oja step (stacr_oja_step, then QR) per `update_interval` steps, skipped under
+    Turbo and, with `freeze_after_warmup`, from `warmup_steps` on.  The basis buffer is rebound,
+    never written in place, so a forward still awaiting its backward keeps its version.
     """
 
     def __init__(self, weight: nn.Parameter, bias: nn.Parameter | None, *, rank: int = 8,
@@ -167,59 +199,53 @@ class STACRLinear(nn.Module):
                  transposed: bool = False, residual_mode: str = "chunk_topk", residual_block_size: int = 16,
                  residual_sample_ratio: float = 0.1):
         super().__init__()
-        # validation order and messages follow stacr/layers.py:232-270
-        if not isinstance(weight, nn.Parameter) or weight.ndim != 2 or not weight.is_floating_point():
+        if not (isinstance(weight, nn.Parameter) and weight.ndim == 2 and weight.is_floating_point()):
             raise ValueError("weight must be a floating-point 2-D Parameter")
-        for name, value in (("rank", rank), ("update_interval", update_interval), ("chunk_rows", chunk_rows),
-                            ("residual_block_size", residual_block_size)):
-            _positive_int(name, value)
-        if not math.isfinite(residual_budget) or not 0 <= residual_budget <= 1:
-            raise ValueError("residual_budget must be between 0 and 1")
-        if residual_bits not in (0, 4, 8):
-            raise ValueError("residual_bits must be 0, 4, or 8")
-        if not math.isfinite(oja_lr) or oja_lr < 0:
-            raise ValueError("oja_lr must be finite and nonnegative")
-        _optional_nonneg_int("warmup_steps", warmup_steps)
-        _optional_nonneg_int("turbo_after_step", turbo_after_step)
-        if residual_mode not in RESIDUAL_MODES:
-            raise ValueError(f"residual_mode must be one of {sorted(RESIDUAL_MODES)}")
-        if not math.isfinite(residual_sample_ratio) or not 0 < residual_sample_ratio <= 1:
-            raise ValueError("residual_sample_ratio must be in (0, 1]")
-        if basis_dtype in ("auto", "activation"):
-            basis_torch_dtype = weight.dtype
+        _check_options(dict(rank=rank, update_interval=update_interval, chunk_rows=chunk_rows,
+                            residual_block_size=residual_block_size, residual_budget=residual_budget,
+                            residual_bits=residual_bits, oja_lr=oja_lr, warmup_steps=warmup_steps,
+                            turbo_after_step=turbo_after_step, residual_mode=residual_mode,
+                            residual_sample_ratio=residual_sample_ratio))
+        if basis_dtype in _FOLLOW_WEIGHT_DTYPE:
+            store_dtype = weight.dtype
         elif basis_dtype in _BASIS_DTYPES:
-            basis_torch_dtype = _BASIS_DTYPES[basis_dtype]
+            store_dtype = _BASIS_DTYPES[basis_dtype]
         else:
             raise ValueError(f"Unknown basis_dtype: {basis_dtype!r}")
-        self.weight, self.bias = weight, bias
         self.transposed = bool(transposed)
-        self.in_features = int(weight.shape[0] if transposed else weight.shape[1])
-        self.out_features = int(weight.shape[1] if transposed else weight.shape[0])
+        # nn.Linear keeps (out, in); Conv1D keeps (in, out)
+        self.out_features, self.in_features = (int(d) for d in (weight.shape[::-1] if transposed else weight.shape))
         if bias is not None and (bias.ndim != 1 or bias.numel() != self.out_features):
             raise ValueError("bias shape must match the output feature count")
+        self.weight, self.bias = weight, bias
         self.rank = min(int(rank), self.in_features)
-        self.residual_budget, self.residual_bits = float(residual_budget), int(residual_bits)
-        self.oja_lr, self.update_interval = float(oja_lr), int(update_interval)
-        self.warmup_steps, self.freeze_after_warmup = int(warmup_steps), bool(freeze_after_warmup)
-        self.turbo_after_step, self.chunk_rows = turbo_after_step, int(chunk_rows)
-        self.residual_mode, self.residual_block_size = residual_mode, int(residual_block_size)
+        self.residual_budget = float(residual_budget)
+        self.residual_bits = int(residual_bits)
+        self.oja_lr = float(oja_lr)
+        self.update_interval = int(update_interval)
+        self.warmup_steps = int(warmup_steps)
+        self.freeze_after_warmup = bool(freeze_after_warmup)
+        self.turbo_after_step = turbo_after_step
+        self.chunk_rows = int(chunk_rows)
+        self.residual_mode = residual_mode
+        self.residual_block_size = int(residual_block_size)
         self.residual_sample_ratio = float(residual_sample_ratio)
-        dev = weight.device
-        self.register_buffer("basis", torch.zeros(self.in_features, self.rank, dtype=basis_torch_dtype, device=dev))
-        self.register_buffer("basis_ready", torch.zeros((), dtype=torch.bool, device=dev))
-        self.register_buffer("_step", torch.zeros((), dtype=torch.int64, device=dev))
-        self.register_buffer("_last_update_step", torch.full((), -1, dtype=torch.int64, device=dev))
+        on = {"device": weight.device}
+        self.register_buffer("basis", torch.zeros(self.in_features, self.rank, dtype=store_dtype, **on))
+        self.register_buffer("basis_ready", torch.zeros((), dtype=torch.bool, **on))
+        self.register_buffer("_step", torch.zeros((), dtype=torch.int64, **on))
+        self.register_buffer("_last_update_step", torch.full((), -1, dtype=torch.int64, **on))
 
     @classmethod
     def from_linear(cls, module: nn.Module, **options) -> "STACRLinear":
-        """Wrap an nn.Linear or a Transformers Conv1D (weight stored in x out)."""
-        transposed = type(module).__name__ == "Conv1D"
-        if not transposed and not isinstance(module, nn.Linear):
+        """Wrap an nn.Linear, or a Transformers Conv1D (weight kept as in x out)."""
+        conv1d = type(module).__name__ == "Conv1D"
+        if not (conv1d or isinstance(module, nn.Linear)):
             raise TypeError("from_linear requires nn.Linear or Transformers Conv1D")
-        layer = cls(module.weight, getattr(module, "bias", None), transposed=transposed, **options)
-        layer.train(module.training)
-        return layer
+        layer = cls(module.weight, getattr(module, "bias", None), transposed=conv1d, **options)
+        return layer.train(module.training)
 
+    # ---------------------------------------------------------------- step and schedule
     @property
     def step(self) -> int:
         return int(self._step.item())
@@ -229,114 +255,129 @@ class STACRLinear(nn.Module):
         self.set_step(value)
 
     def set_step(self, step: int) -> None:
-        if isinstance(step, bool) or int(step) != step or step < 0:
+        if not _is_int(step) or step < 0:
             raise ValueError("step must be a nonnegative integer")
         self._step.fill_(int(step))
 
     def _turbo(self) -> bool:
-        return self.turbo_after_step is not None and self.step >= int(self.turbo_after_step)
+        after = self.turbo_after_step
+        return after is not None and self.step >= int(after)
+
+    def _basis_action(self, step: int) -> str | None:
+        """What this step's first training forward does to the basis: "fit", "oja" or None."""
+        if not bool(self.basis_ready):
+            return "fit"
+        if int(self._last_update_step.item()) == step:
+            return None  # already refreshed for this step (micro-batches, recomputation)
+        frozen = self.freeze_after_warmup and step >= self.warmup_steps
+        if frozen or self._turbo() or step % self.update_interval:
+            return None
+        return "oja"
+
+    def _install_basis(self, basis: torch.Tensor, step: int) -> None:
+        self.basis = basis.to(self.basis.dtype)  # rebind: an outstanding forward keeps its version
+        self.basis_ready.fill_(True)
+        self._last_update_step.fill_(step)
 
     @torch.no_grad()
     def _refresh_basis(self, x2d: torch.Tensor) -> None:
-        """SVD init on the first batch, then one Oja step per update interval
-        (stacr/layers.py:323-354).  The basis tensor is rebound, never mutated in place.
-        The Oja step's reductions run in stacr_oja_step; SVD and QR stay library calls."""
         if not x2d.numel():
             return
         step = self.step
-        ready = bool(self.basis_ready)
-        if ready and int(self._last_update_step.item()) == step:
+        action = self._basis_action(step)
+        if action is None:
             return
-        target = self.basis.dtype
         with torch.autocast(device_type=x2d.device.type, enabled=False):
-            if not ready:
-                sample = x2d.detach().float()
-                if sample.shape[0] >= self.rank:
-                    _, _, vh = torch.linalg.svd(sample, full_matrices=False)
-                    init = vh[: self.rank].t().contiguous()
+            if action == "fit":
+                rows = x2d.detach().float()
+                if rows.shape[0] >= self.rank:
+                    start = torch.linalg.svd(rows, full_matrices=False)[2][: self.rank].t().contiguous()
                 else:
-                    gen = torch.Generator(device="cpu").manual_seed(0)
-                    init = torch.randn(self.in_features, self.rank, generator=gen).to(sample.device)
-                self.basis = orthonormalize(init).to(target)
-                self.basis_ready.fill_(True)
-                self._last_update_step.fill_(step)
-                return
-            if self.freeze_after_warmup and step >= self.warmup_steps:
-                return
-            if self._turbo() or step % self.update_interval:
-                return
-            # Y = XQ, X^T Y and Y^T Y in the HIP reduction (X read once more in its own dtype)
-            _, stepped = kernels.oja_step(x2d.detach(), self.basis, self.oja_lr)
-            self.basis = orthonormalize(stepped).to(target)
-            self._last_update_step.fill_(step)
+                    seeded = torch.Generator(device="cpu").manual_seed(0)
+                    start = torch.randn(self.in_features, self.rank, generator=seeded).to(rows.device)
+                self._install_basis(orthonormalize(start), step)
+            else:  # Y = XQ, X^T Y, Y^T Y and the stepped basis in the HIP reduction; QR in torch
+                _, stepped = kernels.oja_step(x2d.detach(), self.basis, self.oja_lr)
+                self._install_basis(orthonormalize(stepped), step)
 
+    # ---------------------------------------------------------------- forward
     def _native(self, x: torch.Tensor) -> torch.Tensor:
-        if self.transposed:
-            flat = x.reshape(-1, self.in_features)
-            out = flat.mm(self.weight) if self.bias is None else torch.addmm(self.bias, flat, self.weight)
-            return out.reshape(*x.shape[:-1], self.out_features)
-        return F.linear(x, self.weight, self.bias)
+        if not self.transposed:
+            return F.linear(x, self.weight, self.bias)
+        flat = x.reshape(-1, self.in_features)
+        out = torch.addmm(self.bias, flat, self.weight) if self.bias is not None else flat.mm(self.weight)
+        return out.reshape(*x.shape[:-1], self.out_features)
+
+    def _compresses(self, x: torch.Tensor) -> bool:
+        return self.training and torch.is_grad_enabled() and self.weight.requires_grad and x.numel() > 0
+
+    def _factor_state(self, x: torch.Tensor):
+        """(basis, budget) this forward saves with: recorded state when a checkpointed region is
+        recomputed, otherwise this step's (possibly refreshed) basis and the Turbo-aware budget."""
+        guard = get_global_recomputation_guard()
+        if guard.is_recomputing:
+            replayed = guard.replay_layer(self)
+            if replayed is not None:
+                return replayed
+            if not bool(self.basis_ready):
+                self._refresh_basis(x.reshape(-1, self.in_features))
+        else:
+            self._refresh_basis(x.reshape(-1, self.in_features))
+        state = (self.basis, 0.0 if self._turbo() else self.residual_budget)
+        guard.record_layer(self, state)
+        return state
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.ndim < 1 or x.shape[-1] != self.in_features:
             raise ValueError(f"Expected last input dimension {self.in_features}, got {tuple(x.shape)}")
-        if not self.training or not torch.is_grad_enabled() or not self.weight.requires_grad or x.numel() == 0:
+        if not self._compresses(x):
             return self._native(x)
-        guard = get_global_recomputation_guard()
-        replay = guard.replay_layer(self) if guard.is_recomputing else None
-        if replay is not None:
-            basis, budget = replay
-        else:
-            if not guard.is_recomputing or not bool(self.basis_ready):
-                self._refresh_basis(x.reshape(-1, self.in_features))
-            basis = self.basis
-            budget = 0.0 if self._turbo() else self.residual_budget
-            guard.record_layer(self, (basis, budget))
+        basis, budget = self._factor_state(x)
         return STACRFunction.apply(x, self.weight, self.bias, basis, budget, self.residual_bits, self.chunk_rows,
                                    self.transposed, self.residual_mode, self.residual_block_size,
                                    self.residual_sample_ratio)
 
-    def stored_bytes(self, rows: int, value_bytes: int = 2) -> dict[str, Any]:
-        """Saved-factor bytes for one forward of ``rows`` rows (stacr/layers.py:402-473).
+    # ---------------------------------------------------------------- accounting
+    def _saved_entries(self, rows: int, budget: float) -> int:
+        """Residual entries one forward of `rows` rows saves, with each selector's rounding
+        (stacr/layers.py:25-40, 51-54, 81-88); "sampled" is capped at round(budget * n)."""
+        d = self.in_features
+        whole = int(round(budget * rows * d))
+        if not whole:
+            return 0
+        block = self.residual_block_size
+        if self.residual_mode == "block_sparse" and d % block == 0:
+            return sum(max(1, int(round(budget * n * d / block))) * block for n in _chunk_sizes(rows, self.chunk_rows))
+        if self.residual_mode in ("chunk_topk", "topk", "block_sparse"):
+            per_chunk = sum(max(1, int(round(budget * n * d))) for n in _chunk_sizes(rows, self.chunk_rows))
+            return min(whole, per_chunk)
+        return whole
 
-        Counts follow the selectors' rounding; "sampled" reports an upper bound.  ``basis``
-        includes the persistent basis and the saved cast when value and basis widths differ.
+    def stored_bytes(self, rows: int, value_bytes: int = 2) -> dict[str, Any]:
+        """Saved-factor bytes for one forward of `rows` rows (weights and workspaces excluded).
+
+        `basis` counts the persistent basis plus the cast a forward saves when the value width
+        differs from the basis width; "sampled" reports an upper bound on its entries.
         """
-        if isinstance(rows, bool) or int(rows) != rows or rows < 0 or value_bytes not in (2, 4, 8):
+        if not _is_int(rows) or rows < 0 or value_bytes not in (2, 4, 8):
             raise ValueError("rows must be a nonnegative integer and value_bytes must be 2, 4, or 8")
         rows = int(rows)
-        d = self.in_features
         budget = 0.0 if self._turbo() or self.residual_mode == "none" else self.residual_budget
-        count = int(round(budget * rows * d))
-        starts = range(0, rows, self.chunk_rows)
-        if self.residual_mode == "block_sparse" and d % self.residual_block_size == 0 and count:
-            count = sum(
-                max(1, int(round(budget * min(self.chunk_rows, rows - s) * d / self.residual_block_size)))
-                * self.residual_block_size
-                for s in starts
-            )
-        elif self.residual_mode in ("chunk_topk", "topk", "block_sparse") and count:
-            count = min(count, sum(max(1, int(round(budget * min(self.chunk_rows, rows - s) * d))) for s in starts))
-        index_bytes = 4 if rows * d < 2**31 - 1 else 8
-        if self.residual_bits == 4:
-            value_store = (count + 1) // 2
-        elif self.residual_bits == 8:
-            value_store = count
-        else:
-            value_store = count * value_bytes
-        residual = count * index_bytes + value_store + (4 if count else 0)
+        entries = self._saved_entries(rows, budget)
+        index_bytes = 4 if rows * self.in_features < 2**31 - 1 else 8
+        value_store = {4: (entries + 1) // 2, 8: entries}.get(self.residual_bits, entries * value_bytes)
+        residual = entries * index_bytes + value_store + (4 if entries else 0)
         coeff = rows * self.rank * value_bytes
         persistent = self.basis.numel() * self.basis.element_size()
-        cast = self.basis.numel() * value_bytes if self.basis.element_size() != value_bytes and rows else 0
-        basis = persistent + cast
+        cast = self.basis.numel() * value_bytes if rows and self.basis.element_size() != value_bytes else 0
         return {
             "coeff": coeff,
             "residual": residual,
-            "basis": basis,
-            "total": coeff + residual + basis,
+            "basis": persistent + cast,
+            "total": coeff + residual + persistent + cast,
             "persistent_basis": persistent,
             "saved_basis_cast": cast,
-            "residual_count": count,
+            "residual_count": entries,
             "residual_count_is_upper_bound": self.residual_mode == "sampled",
         }
 

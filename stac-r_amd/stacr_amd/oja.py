@@ -1,11 +1,14 @@
-"""Basis orthonormalization and the persistent Oja basis (stacr/oja.py:8-106).
+"""Orthonormalization and the persistent Oja basis (interface of stacr/oja.py:8-106).
 
-QR and SVD stay torch library calls; the Oja step's reductions (Y = XQ, X^T Y, Y^T Y) run in the
-HIP kernel behind stacr_oja_step, so OjaBasis.update needs its basis on a ROCm GPU.
+QR and SVD stay torch library calls.  The Oja step's reductions (Y = XQ, X^T Y, Y^T Y and the
+stepped basis) run in the HIP kernels behind stacr_oja_step, so `OjaBasis.update` needs its
+basis on a ROCm GPU.
+
+The basis is versioned: every change installs a new tensor (never an in-place write) and bumps
+the version, so a tensor handed out by `shared` stays valid for the activations that used it,
+and the per-dtype casts `shared` hands out are cached for one version only.
 """
 from __future__ import annotations
-
-from dataclasses import dataclass
 
 import torch
 
@@ -13,83 +16,92 @@ from . import kernels
 
 
 def orthonormalize(matrix: torch.Tensor) -> torch.Tensor:
-    """Orthonormal columns spanning ``matrix`` (reduced QR in fp32, returned in its dtype)."""
+    """Orthonormal columns spanning ``matrix``: reduced QR in fp32, returned in its dtype."""
     q, _ = torch.linalg.qr(matrix.to(torch.float32), mode="reduced")
     return q.to(matrix.dtype)
 
 
-@dataclass
-class OjaBasis:
-    """Persistent per-feature basis updated from streamed activations (stacr/oja.py:15-106).
+def _seeded_orthonormal(features: int, rank: int, seed: int) -> torch.Tensor:
+    """QR of an fp32 normal draw from a CPU generator seeded with `seed` (reproducible anywhere)."""
+    draw = torch.randn(features, rank, generator=torch.Generator(device="cpu").manual_seed(int(seed)),
+                       dtype=torch.float32)
+    return orthonormalize(draw)
 
-    ``update`` rebinds ``basis`` to a new tensor, so a reference handed out by ``shared`` stays
-    valid for the activations that used it.
+
+def _top_right_singular_vectors(x: torch.Tensor, rank: int) -> torch.Tensor:
+    """features x rank: the leading right singular vectors of the fp32 rows of `x`."""
+    _, _, vh = torch.linalg.svd(x, full_matrices=False)
+    return vh[:rank].t().contiguous()
+
+
+class OjaBasis:
+    """A features x rank orthonormal basis tracked from streamed activations.
+
+    Starts as a seeded random orthonormal basis and uninitialized: the first `update` fits it to
+    that batch (SVD), later ones take one Oja step and re-orthonormalize.
     """
 
-    features: int
-    rank: int
-    dtype: torch.dtype = torch.float32
-    device: torch.device | str = "cpu"
-    initialized: bool = False
-
-    def __post_init__(self) -> None:
-        self.rank = max(1, min(int(self.rank), int(self.features)))
-        self.basis = torch.empty(self.features, self.rank, device=self.device, dtype=self.dtype)
-        self._views: dict[torch.dtype, torch.Tensor] = {}
+    def __init__(self, features: int, rank: int, dtype: torch.dtype = torch.float32,
+                 device: torch.device | str = "cpu", initialized: bool = False):
+        self.features = int(features)
+        self.rank = max(1, min(int(rank), self.features))
+        self.dtype = dtype
+        self.device = device
+        self.version = 0
+        self._casts: dict[torch.dtype, torch.Tensor] = {}
         self.reset_random(seed=0)
-        self.initialized = False
+        self.initialized = False  # a fresh basis is always fitted by its first update
 
-    def _invalidate(self) -> None:
-        self._views = {}
+    def _install(self, basis: torch.Tensor) -> None:
+        self.basis = basis.to(device=self.device, dtype=self.dtype)
+        self.version += 1
+        self._casts = {}
 
     def reset_random(self, seed: int = 0) -> None:
-        """QR of a seeded CPU normal draw (same draw as the reference for a given seed)."""
-        gen = torch.Generator(device="cpu")
-        gen.manual_seed(int(seed))
-        draw = torch.randn(self.features, self.rank, generator=gen, dtype=torch.float32)
-        self.basis = orthonormalize(draw.to(device=self.basis.device, dtype=self.dtype))
-        self._invalidate()
+        """Seeded random orthonormal basis (QR of a CPU fp32 normal draw); marks it initialized."""
+        self._install(_seeded_orthonormal(self.features, self.rank, seed))
         self.initialized = True
 
     def initialize_from_batch(self, activations: torch.Tensor, centre: bool = False) -> None:
-        """Top-``rank`` right singular vectors of the (uncentred by default) batch."""
+        """Fit the leading right singular vectors of the batch (uncentred unless `centre`): the
+        reconstruction C Q^T adds no mean back, so the mean direction belongs in the basis.  A
+        batch with fewer rows than the rank falls back to the seed-0 random basis."""
         x = activations.reshape(-1, activations.shape[-1]).detach().to(torch.float32)
         if centre:
             x = x - x.mean(dim=0, keepdim=True)
         if x.shape[0] < self.rank:
             self.reset_random(seed=0)
             return
-        _, _, vh = torch.linalg.svd(x, full_matrices=False)
-        self.basis = orthonormalize(vh[: self.rank].t().contiguous()).to(device=self.basis.device, dtype=self.dtype)
-        self._invalidate()
+        self._install(orthonormalize(_top_right_singular_vectors(x, self.rank)))
         self.initialized = True
 
     @torch.no_grad()
     def update(self, activations: torch.Tensor, lr: float = 0.01) -> None:
-        """One Oja subspace step, then re-orthonormalization (stacr/oja.py:64-81)."""
+        """Fit on the first call, then one Oja step Q + lr (X^T Y / n - Q Y^T Y / n), Y = X Q, in fp32
+        on the GPU, followed by re-orthonormalization."""
         if not self.initialized:
             self.initialize_from_batch(activations)
             return
-        x = activations.reshape(-1, activations.shape[-1]).detach().to(self.basis.device)
-        if x.numel() == 0:
+        rows = activations.reshape(-1, activations.shape[-1]).detach()
+        if rows.numel() == 0:
             return
-        if x.dtype not in kernels.DTYPE_CODES:
-            x = x.to(torch.float32)
-        _, stepped = kernels.oja_step(x, self.basis, float(lr))
-        self.basis = orthonormalize(stepped).to(dtype=self.dtype)
-        self._invalidate()
+        rows = rows.to(self.basis.device)
+        if rows.dtype not in kernels.DTYPE_CODES:
+            rows = rows.to(torch.float32)
+        _, stepped = kernels.oja_step(rows, self.basis, float(lr))
+        self._install(orthonormalize(stepped))
 
     def snapshot(self, dtype: torch.dtype | None = None) -> torch.Tensor:
-        out = self.basis.detach()
-        if dtype is not None:
-            out = out.to(dtype=dtype)
-        return out.clone()
+        """A private copy of the current basis (in `dtype` if given)."""
+        return self.basis.detach().to(dtype=dtype or self.basis.dtype).clone()
 
     def shared(self, dtype: torch.dtype | None = None) -> torch.Tensor:
-        """Basis of the current version, one tensor per dtype until the next update."""
-        target = self.basis.dtype if dtype is None else dtype
-        cached = self._views.get(target)
-        if cached is None:
-            cached = self.basis.detach() if target == self.basis.dtype else self.basis.detach().to(dtype=target)
-            self._views[target] = cached
-        return cached
+        """The current version's basis in `dtype`, one tensor per dtype until the next change, so
+        many saved activations can reference it without a copy each."""
+        want = dtype or self.basis.dtype
+        if want not in self._casts:
+            self._casts[want] = self.basis.detach() if want == self.basis.dtype else self.basis.detach().to(want)
+        return self._casts[want]
+
+
+__all__ = ["orthonormalize", "OjaBasis"]

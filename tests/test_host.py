@@ -201,3 +201,33 @@ def test_turbo_schedule_and_step_property():
     assert layer.stored_bytes(5)["residual_count"] == 0
     with pytest.raises(ValueError):
         layer.set_step(True)
+
+
+def test_stored_bytes_closed_forms_and_reference_known_answers():
+    from stacr_amd.memory import dense_bytes, saved_surface_predictor
+
+    # reference tests/test_memory.py:7-15
+    assert stacr_stored_bytes((8, 512), rank=8, dtype=torch.float16, residual_budget=0.005) < dense_bytes(
+        (8, 512), torch.float16)
+    assert saved_surface_predictor(10, 100) == 0.1
+    assert saved_surface_predictor(-3, 100) == 0.0
+    with pytest.raises(ValueError):
+        saved_surface_predictor(1, 0)
+    # (5, 16), rank 4, fp32, budget 0.25, int8 residual: 80 B coeff; 20 entries x (4 idx + 1) + 4 scale
+    assert stacr_stored_bytes((5, 16), 4, torch.float32, 0.25, residual_bits=8) == 80 + 20 * 5 + 4
+    # + an fp32 basis 16 x 4; int4 coefficients pack two per byte and add a scale
+    assert stacr_stored_bytes((5, 16), 4, torch.float32, 0.25, residual_bits=8, include_basis=True) == 184 + 256
+    assert stacr_stored_bytes((5, 16), 4, torch.float32, 0.0, coeff_bits=4) == 10 + 4
+    assert stacr_stored_bytes((5, 16), 4, torch.float32, 0.0, coeff_bits=4, include_scales=False) == 10
+    # residual_bits=0 keeps dtype values plus a unit scale; None keeps values without a scale
+    assert stacr_stored_bytes((5, 16), 4, torch.bfloat16, 0.25, residual_bits=0) == 40 + 20 * 6 + 4
+    assert stacr_stored_bytes((5, 16), 4, torch.bfloat16, 0.25) == 40 + 20 * 6
+    assert stacr_stored_bytes((2, 3, 64), 100, torch.float16, 0.0) == 6 * 64 * 2  # rank capped at features
+    assert stacr_stored_bytes((3, 0), 4) == 0 and stacr_stored_bytes((), 4) == 2
+    for bad in (dict(rank=0), dict(rank=True), dict(residual_budget=1.5), dict(index_bytes=3),
+                dict(coeff_bits=2), dict(residual_bits=16)):
+        args = dict(shape=(5, 16), rank=4) | bad
+        with pytest.raises(ValueError):
+            stacr_stored_bytes(**args)
+    with pytest.raises(ValueError, match="nonnegative"):
+        dense_bytes((2, -1), torch.float32)

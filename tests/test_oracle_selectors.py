@@ -80,3 +80,74 @@ def test_threshold_comparison_follows_torch_promotion(dtype):
         idx, val = orc.select_threshold(r.float().numpy(), thr, dtype, 300)
         assert np.array_equal(idx, ref)
         assert np.array_equal(val, r.float().numpy()[ref])
+
+
+def _brute_adaptive_blocks(resid, budget, chunk_rows, bs, dtype):
+    """Plain-Python restatement: energies block by block, candidates chunk by chunk, global cut."""
+    rows, d = resid.shape
+    bpr = -(-d // bs)
+    energies = []
+    for r in range(rows):
+        for b in range(bpr):
+            acc = np.float32(0)
+            for o in range(bs):
+                c = b * bs + o
+                v = np.float32(resid[r, c]) if c < d else np.float32(0)
+                acc = np.float32(acc + orc.round_to(np.array([v * v], np.float32), dtype)[0])
+            energies.append(float(orc.round_to(np.array([acc], np.float32), dtype)[0]))
+    k = min(int(rows * d * budget), rows * d)
+    k_blocks = max(1, -(-k // bs))
+    chunk = min(chunk_rows, rows)
+    per = max(1, (k_blocks * chunk + rows - 1) // rows)
+    cand = []
+    for start in range(0, rows, chunk):
+        blocks = list(range(start * bpr, min(start + chunk, rows) * bpr))
+        blocks.sort(key=lambda i: (-energies[i], i))
+        cand += blocks[:per]
+    cand.sort(key=lambda i: (-energies[i], i))
+    kept = sorted(cand[:k_blocks])
+    idx = [(b // bpr) * d + (b % bpr) * bs + o for b in kept for o in range(bs) if (b % bpr) * bs + o < d]
+    return np.array(idx, np.int64)
+
+
+@pytest.mark.parametrize("rows,d,chunk,bs,budget,dtype", [
+    (12, 40, 5, 16, 0.1, "f32"),    # padded row ends, three chunks, global cut
+    (9, 32, 4, 8, 0.3, "bf16"),     # no padding, partial last chunk
+    (7, 10, 7, 4, 0.5, "f16"),      # one chunk, padding, many blocks kept
+    (30, 17, 8, 16, 0.02, "f32"),   # blocks wider than the padding, per-chunk minimum of one
+])
+def test_adaptive_block_sparse_matches_brute_force(rows, d, chunk, bs, budget, dtype):
+    rng = np.random.default_rng(rows * d)
+    resid = orc.round_to(rng.standard_normal((rows, d)).astype(np.float32) * rng.uniform(0.1, 3, (1, d)), dtype)
+    idx, vals = orc.adaptive_select_block_sparse(resid, budget, chunk, bs, dtype)
+    assert np.array_equal(idx, _brute_adaptive_blocks(resid, budget, chunk, bs, dtype))
+    assert np.array_equal(vals, resid.reshape(-1)[idx])
+
+
+def test_adaptive_block_sparse_equals_projection_rule_when_counts_agree():
+    """With one chunk and feats % bs == 0 both engines keep the same number of whole blocks."""
+    rng = np.random.default_rng(3)
+    resid = orc.round_to(rng.standard_normal((16, 64)).astype(np.float32), "bf16")
+    a, _ = orc.adaptive_select_block_sparse(resid, 0.25, 16, 16, "bf16")   # k 256 -> 16 blocks
+    b, _ = orc.select_block_sparse(resid, 0.25, 16, 16, "bf16")            # round(0.25 * 64) = 16
+    assert np.array_equal(a, b)
+
+
+def test_adaptive_block_energy_matches_torch_padded_sum():
+    """The reference forms block scores with torch ops on the padded residual in its dtype
+    (stacr/adaptive.py:1857-1868): F.pad, view, square, sum(dim=2).  16-bit scores are bit-equal
+    (the final rounding hides the fp32 summation order); fp32 scores agree to a few ulps, the
+    order torch's own reduction adds in being internal to it."""
+    import torch
+    from torch.nn import functional as F
+
+    rng = np.random.default_rng(8)
+    for dtype, tdt in (("bf16", torch.bfloat16), ("f16", torch.float16), ("f32", torch.float32)):
+        resid = orc.round_to(rng.standard_normal((6, 37)).astype(np.float32), dtype)
+        t = F.pad(torch.from_numpy(resid).to(tdt), (0, 48 - 37)).view(6, 3, 16)
+        want = (t * t).sum(dim=2).float().reshape(-1).numpy()
+        got = orc.adaptive_block_energies(resid, 16, dtype)
+        if dtype == "f32":
+            assert np.allclose(got, want, rtol=16 * np.finfo(np.float32).eps, atol=0)
+        else:
+            assert np.array_equal(got, want)
