@@ -175,6 +175,7 @@ def _saved_factors(out, cfg, rows, d_in):
         IndexCompressionMode
 
     saved = list(out.grad_fn.saved_tensors)
+    saved = [t.to(saved[1].device) for t in saved]  # offloaded factors come back to the weight's device
     pos = 2
     if cfg.quantize_coefficients:
         coeff = dequantize_int8(saved[0], saved[2])
@@ -252,9 +253,9 @@ def test_low_rank_only_route_and_baseline_warmup(dev):
     out = layer(x)  # step 1: residuals off -> the low-rank-only route
     assert type(out.grad_fn).__name__.startswith(STACRLowRankOnlyFunction.__name__)
     assert layer.layer_state["b1_route_step_count"] == 1
-    out.backward(g)
     q = out.grad_fn.basis
     coeff = out.grad_fn.saved_tensors[0]
+    out.backward(g)
     odw, _ = _oracle_dw(g, _np(coeff), q, np.zeros(0, np.int64), np.zeros(0, np.float32), 256)
     assert rel_l2(_np(layer.linear.weight.grad), odw) <= 1e-5
 

@@ -50,7 +50,8 @@ def test_config5_gpt2_medium_full_step():
 
     def keep(name):
         def hook(module, inputs, output):
-            captured[name] = {"out": output}
+            # the saved factors, taken now: backward frees the graph's references to them
+            captured[name] = {"saved": output.grad_fn.saved_tensors, "has_residual": output.grad_fn.has_residual}
             output.register_hook(lambda g: captured[name].__setitem__("g", g.detach()))
         return hook
 
@@ -72,9 +73,9 @@ def test_config5_gpt2_medium_full_step():
     for name in SAMPLED:
         announce("cfg5 dW", name)
         layer = model.get_submodule(name)
-        out, g = captured[name]["out"], captured[name]["g"]
-        coeff, _, q, idx, data, scale = out.grad_fn.saved_tensors
-        assert coeff.dtype == torch.bfloat16 and out.grad_fn.has_residual
+        g = captured[name]["g"]
+        coeff, _, q, idx, data, scale = captured[name]["saved"]
+        assert coeff.dtype == torch.bfloat16 and captured[name]["has_residual"]
         rows, d_in = coeff.shape[0], layer.in_features
         oidx = idx.cpu().numpy().astype(np.int64)
         orc.check_indices(oidx, rows * d_in, ascending=True)
