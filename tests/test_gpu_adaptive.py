@@ -164,8 +164,9 @@ def test_adaptive_function_matches_factor_formula(dtype, cfg_i):
     x = make_activation(rows, d_in).to(DT[dtype]).to(dev).requires_grad_(True)
     basis = make_basis(d_in, r).to(dev)
     lin = torch.nn.Linear(d_in, d_out).to(dev).to(DT[dtype])
-    state = {}
-    y = ad.STACRFunction.apply(x, lin.weight, lin.bias, basis, cfg, state)
+    state = {"_schedule_step": 0}
+    full = ad.STACRConfig(rank=r, **cfg).to_dict()  # the reference's (…, config, step_counter, layer_state)
+    y = ad.STACRFunction.apply(x, lin.weight, lin.bias, basis, full, torch.zeros(1, dtype=torch.long), state)
     with torch.no_grad():  # the forward is the native dense op (mm, then the bias add)
         ref = torch.nn.functional.linear(x, lin.weight, lin.bias)
         assert torch.allclose(y.float(), ref.float(), rtol=1e-2 if dtype == "bf16" else 1e-5, atol=1e-2 if dtype == "bf16" else 1e-5)
