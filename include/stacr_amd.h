@@ -138,6 +138,21 @@ int stacr_weight_grad(const void *g, int dtype, int64_t rows, int64_t d_out, con
                       int transposed, void *dw, int dw_dtype, void *dbias, int dbias_dtype,
                       void *workspace, size_t workspace_bytes, void *stream);
 
+/*
+ * Allocation-free weight gradient.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, arithmetic and results as stacr_weight_grad, without the workspace:
+ * the plan lives in a static device array of STACR_NOALLOC_SCRATCH_BYTES per GPU, held until the
+ * process ends.  Problems whose stacr_weight_grad_workspace_bytes exceeds it are rejected with
+ * STACR_ERR_UNSUPPORTED.  The entry point allocates nothing (no hipMalloc / hipFree); calls that
+ * overlap on one GPU share its scratch and race, so serialize them (one stream, or events).
+ */
+#define STACR_NOALLOC_SCRATCH_BYTES (48u << 20)
+int stacr_weight_grad_noalloc(const void *g, int dtype, int64_t rows, int64_t d_out, const void *coeff,
+                              const void *q, int64_t d_in, int rank, const void *idx, int index_bytes,
+                              const void *data, const float *scale, int bits, int val_dtype, int64_t nnz,
+                              int transposed, void *dw, int dw_dtype, void *dbias, int dbias_dtype, void *stream);
+
 /* ------------------------------------------------------------------------------------------
  * Adaptive engine (stacr/adaptive.py, stacr/index_compression.py)
  * ---------------------------------------------------------------------------------------- */

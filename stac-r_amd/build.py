@@ -17,7 +17,8 @@ OUT = os.path.join(HERE, "stacr_amd", "libstacr_amd.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("STACR_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["abi.hip", "save.hip", "weight_grad.hip", "adaptive.hip", "oja.hip", "selectors.hip", "profile.hip"]
+SOURCES = ["abi.hip", "save.hip", "weight_grad.hip", "adaptive.hip", "oja.hip", "selectors.hip", "profile.hip",
+           "noalloc.hip"]
 
 FLAGS = [
     f"--offload-arch={ARCH}",
