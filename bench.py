@@ -173,6 +173,17 @@ def check_layer(outs, ref):
         raise RuntimeError("graph replay of the weight gradient differs from the eager result")
 
 
+def kernel_breakdown(step, reps: int = 10) -> dict:
+    """us per step of each library kernel over `reps` calls of `step` (HIP events on the launch
+    stream around every launch, the device kept busy ahead of each)."""
+    from stacr_amd import _lib
+
+    with _lib.KernelTimer(max_launches=reps * 64) as timer:
+        for _ in range(reps):
+            step()
+    return {name: round(tot / reps * 1e3, 3) for name, (tot, _cnt) in timer.results.items()}
+
+
 def layer_workload(name, n, d_in, d_out, rank, budget, mode, steps, warmup, lognormal=True):
     """Timing of one configured layer's save + dW (Conv1D layout, bf16)."""
     import torch
@@ -198,7 +209,8 @@ def layer_workload(name, n, d_in, d_out, rank, budget, mode, steps, warmup, logn
     out = {"config": name, "tokens": n, "d_in": d_in, "d_out": d_out, "rank": rank, "k": k,
            "ms_per_step": ms, "tokens_per_s": n / (ms * 1e-3), "eager_ms": eager, "graph_ms": graph,
            "algorithmic_bytes": ab["total"],
-           "pct_hbm_roofline": 100.0 * ab["total"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+           "pct_hbm_roofline": 100.0 * ab["total"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+           "kernels_us_per_step": kernel_breakdown(step)}
     if note:
         out["note"] = note
     return out
@@ -226,7 +238,8 @@ def oja_workload(x, q, steps, warmup):
     byts = N * D_IN * 2 + 2 * 4 * D_IN * RANK  # X once, basis in, update out (one fused pass)
     out = {"config": "oja step on cfg3 c_fc X (8192 x 1024 bf16, rank 8), QR excluded",
            "ms_per_step": ms, "eager_ms": eager, "graph_ms": graph, "algorithmic_bytes": byts,
-           "pct_hbm_roofline": 100.0 * byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+           "pct_hbm_roofline": 100.0 * byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+           "kernels_us_per_step": kernel_breakdown(step)}
     if note:
         out["note"] = note
     return out
@@ -368,7 +381,8 @@ def main() -> int:
             oja_workload(x, q, extra_steps, extra_warm),
         ]
         for w in out["other_workloads"]:
-            print(f"[bench] {w['config']}: {w['ms_per_step'] * 1e3:.1f} us", file=sys.stderr, flush=True)
+            print(f"[bench] {w['config']}: {w['ms_per_step'] * 1e3:.1f} us {w['kernels_us_per_step']}",
+                  file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(x, q, g)

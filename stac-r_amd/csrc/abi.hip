@@ -222,7 +222,9 @@ int stacr_weight_grad_workspace_bytes(int64_t rows, int64_t d_out, int64_t d_in,
     StacrGradArgs a;
     const int rc = fill_grad_args(rows, d_out, d_in, rank, nnz, &a);
     if (rc) return rc;
-    *bytes = stacr_grad_ws_layout(a, nullptr);
+    // the query does not know the dtypes, alignment or bias: enough for whichever path runs
+    const size_t legacy = stacr_grad_ws_layout(a, nullptr), tiles = stacr_tiles_ws_bound(rows, d_out, d_in, nnz);
+    *bytes = legacy > tiles ? legacy : tiles;
     return STACR_OK;
 }
 

@@ -260,6 +260,11 @@ struct StacrGradArgs {
 };
 size_t stacr_grad_ws_layout(const StacrGradArgs &a, size_t *offsets);
 int stacr_grad_launch(const StacrGradArgs &a);
+// the matrix-core path of weight_grad_tiles.hip (16-bit G, rank + bias column <= 16, d_out % 16 == 0)
+bool stacr_tiles_eligible(const StacrGradArgs &a);
+size_t stacr_tiles_ws(const StacrGradArgs &a);
+size_t stacr_tiles_ws_bound(int64_t rows, int64_t d_out, int64_t d_in, int64_t nnz);  // any dtype / bias
+int stacr_tiles_launch(const StacrGradArgs &a);
 
 // ------------------------------------------------------------------ launchers (adaptive.hip)
 int stacr_aq_quantize_launch(const void *v, int dtype, int64_t n, int bits, void *data, void *scale, void *ws,

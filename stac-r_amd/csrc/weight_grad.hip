@@ -1622,6 +1622,7 @@ int grad_dispatch(const StacrGradArgs &a, const GPlan &p, char *ws, const size_t
 
 size_t stacr_grad_ws_layout(const StacrGradArgs &a, size_t *offsets)
 {
+    if (stacr_tiles_eligible(a)) return stacr_tiles_ws(a);
     const GPlan p = make_gplan(a);
     size_t tmp[GW_N];
     return glayout(a, p, offsets ? offsets : tmp);
@@ -1629,6 +1630,7 @@ size_t stacr_grad_ws_layout(const StacrGradArgs &a, size_t *offsets)
 
 int stacr_grad_launch(const StacrGradArgs &a)
 {
+    if (stacr_tiles_eligible(a)) return stacr_tiles_launch(a);
     const GPlan p = make_gplan(a);
     size_t off[GW_N];
     const size_t need = glayout(a, p, off);
