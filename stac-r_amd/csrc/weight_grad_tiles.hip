@@ -1,31 +1,36 @@
-// Weight gradient from the saved factors on the matrix cores, with the G stream double-buffered
-// straight into LDS: dW = (G^T C) Q^T + G^T R_s, dbias = sum_t G (stacr/layers.py:172-198).
+// Weight gradient from the saved factors on the matrix cores: dW = (G^T C) Q^T + G^T R_s and
+// dbias = sum_t G (stacr/layers.py:172-198), with G streamed once from memory.
 //
-// For 16-bit G and C, rank (+ the bias column) <= 16, d_out a multiple of 16.  Other problems use
-// the kernels of weight_grad.hip.  Accumulation is fp32 and dW is rounded once to its dtype.
+// For 16-bit G and C, rank (+ the bias column) <= 16, d_out a multiple of 16, d_in <= 8192.  Other
+// problems use the kernels of weight_grad.hip.  Accumulation is fp32 and dW is rounded once.
 //
-// Two launches.
-//   k_tile_plan  one workgroup per (block of 512 token rows, input part of <= 1024 features):
-//     * the part's column features: those with at least kMinColCount entries in block 0 (the
-//       sample), the 32 with most entries, ties to the lowest feature, slots in feature order;
-//     * the block's column entries as a dense tile Bt[slot][t] (values in G's dtype, zero where
-//       no entry was selected);
+// Three launches.
+//   k_tile_count  (sparse only) 16 workgroups over contiguous chunks of the residual entries: the
+//     chunk's count of entries per input feature, and the first entry of every block of 512 token
+//     rows (entries are ascending, so block b starts where the block of the entries changes).
+//   k_tile_plan   one workgroup per (block of 512 rows, input part of <= 1024 features):
+//     * the part's column features: the 64 (32 for 16-bit values) with most entries over the whole
+//       problem, ties to the lowest feature; every workgroup selects the same set;
+//     * the block's column entries as dense matrix-core operands, in the order in which the lanes
+//       of the streaming kernel load them (int8 codes for 4 / 8-bit residuals, else the values in
+//       G's dtype), zero where no entry was selected;
 //     * the block's other ("light") entries of the part as records t | value << 16, grouped by
-//       feature and within a feature by ascending t: each entry's place is its feature's offset
-//       plus the number of that feature's entries in earlier rows of the block, counted from a
-//       per-feature row bitmap, so the order (and so every sum) is the same on every run;
-//     * block 0's workgroups also pack the block's coefficients transposed, Cp[col][t], with a
-//       column of ones (its matrix-core column is dbias) and zeros past the rank and the rows.
-//   k_tile_grad  one workgroup per (16 output features, input part); per block of 512 rows:
-//     * the next block's G tile [t][16], Cp tile, Bt tile, light records and their offsets are
-//       loaded straight into the other LDS buffer (global_load_lds_dwordx4) while this block runs;
-//     * wave w takes rows 32w..32w+31: one v_mfma_f32_16x16x32 for M = G^T [C | 1] and one per
-//       16-column tile of Bt, all on the same G^T operand, accumulated in registers across blocks;
-//     * thread f owns input feature f of the part and adds value * G[t][0..15] of each of its
-//       light entries to 16 fp32 registers;
+//       feature and within a feature by ascending t (each entry's place is its feature's offset
+//       plus the number of that feature's entries in earlier rows, counted from a per-feature row
+//       bitmap), so the order, and so every sum, is the same on every run;
+//     * part 0 also packs the block's coefficients [C | 1] as matrix-core operands.
+//   k_tile_grad   one workgroup per (16 output features, input part), over the blocks in order:
+//     * the G tile [512 rows][16 outputs], the light records and their offsets of block b + 2 are
+//       copied straight into one of three LDS buffers (global_load_lds) while block b runs, and the
+//       operands of block b + 1 are loaded into registers;
+//     * wave w takes rows 32w .. 32w + 31: one v_mfma_f32_16x16x32 for M = G^T [C | 1] and one per
+//       16-column tile of the column entries, all on the same G^T operand, accumulated in
+//       registers over the blocks;
+//     * thread f owns input feature f of the part and adds value * G[t][0..15] of each of its light
+//       entries to 16 fp32 registers;
 //     and at the end reduces the per-wave tiles over the waves (in wave order) and writes
 //     dW[o][f] = sum_j M[o][j] Q[f][j] + scale * (light sum + column sum).
-#include <mutex>
+#include <type_traits>
 
 #include "internal.h"
 
@@ -36,13 +41,23 @@ namespace {
 constexpr int kTB = 512;             // token rows per block
 constexpr int kOS = 16;              // output features per workgroup
 constexpr int kPartMax = 1024;       // input features per part (one owner thread each)
-constexpr int kNC = 32;              // column features per part (two 16-column tiles)
 constexpr int kThreads = 1024;       // 16 waves
-constexpr int kLightCap = 2048;      // light records staged per block (8 KiB); more are read from memory
-constexpr int kMinColCount = 16;     // entries in the sample block a column feature needs
-constexpr int kOffWords = kPartMax + 1 + 255;  // offsets staged as whole 1 KiB wave loads (5 of them)
+constexpr int kWaves = kThreads / 64;
+constexpr int kLightCap = 4096;      // light records staged per block (16 KiB); more are read from memory
+constexpr int kOffWords = kPartMax + 1 + 255;  // offsets staged as whole 1 KiB wave copies (5 of them)
+constexpr int kChunks = 16;          // entry chunks of the feature count
+constexpr int kMaxFeat = 8192;       // input features the count kernel's LDS histogram holds
+constexpr int kMaxBlocks = 256;      // blocks per problem (rows <= 131072): headers held in LDS
+constexpr int kNCMax = 64;           // column features per part, at most
 
-static_assert(kThreads == 2 * kTB, "two G tile rows per lane pair: one 16-byte load per lane");
+static_assert(kThreads == 2 * kTB, "two G tile rows per lane pair: one 16-byte copy per lane");
+static_assert(kLightCap == kWaves * 256, "one 1 KiB copy of light records per wave");
+
+// column tiles per part: 4 (64 columns) for one-byte integer codes, 2 for 16-bit values
+template <bool BT8> struct Cols {
+    static constexpr int nt = BT8 ? 4 : 2;
+    static constexpr int nc = 16 * nt;
+};
 
 struct TileHdr {  // per (block, part)
     uint32_t light_base;   // first light record (index into the record array)
@@ -62,12 +77,14 @@ struct TileArgs {
     // geometry
     int n_blocks, n_parts, part_w, ncol, bias_col;
     // workspace
-    uint16_t *cp;       // [n_blocks][ncol][kTB]
-    uint16_t *bt;       // [n_blocks][n_parts][kNC][kTB]
-    uint32_t *light;    // [nnz + kLightCap]
+    uint32_t *hist;     // [kChunks][d_in] entries per feature in each chunk
+    uint32_t *bstart;   // [n_blocks + 1] first entry of each block
+    uint16_t *cp;       // [n_blocks][16 waves][4 row groups][ncol][8] coefficient operands
+    void *bt;           // [n_blocks][n_parts][nt][16 waves][64 lanes][8] column operands
+    uint32_t *light;    // [nnz + 3 regions + 3 + kLightCap] light records
     uint32_t *loff;     // [n_blocks][n_parts][kOffWords]
     TileHdr *hdr;       // [n_blocks][n_parts]
-    int32_t *colmap;    // [n_parts][kNC] feature in the part, or -1
+    int32_t *colmap;    // [n_parts][kNCMax] feature in the part, or -1
     int sparse;         // nnz > 0: the plan builds the entry structures
 };
 
@@ -76,188 +93,219 @@ __device__ __forceinline__ int64_t flat_at(const void *idx, int idx64, int64_t k
     return idx64 ? static_cast<const int64_t *>(idx)[k] : (int64_t) static_cast<const int32_t *>(idx)[k];
 }
 
-// First entry position p in [0, n) with idx[p] >= key (idx ascending), found by the whole
-// workgroup: each round probes 1024 evenly spaced positions of the remaining range.
-__device__ int64_t block_lower_bound(const void *idx, int idx64, int64_t n, int64_t key)
+// (token row, feature) of a flat index; rows * d_in < 2^32 (the host checks), so 32-bit division.
+// An index outside the problem (invalid input) still yields a feature < d_in.
+__device__ __forceinline__ void split_flat(int64_t flat, uint32_t d_in, uint32_t &t, uint32_t &f)
 {
-    int64_t lo = 0, hi = n;  // the answer lies in [lo, hi]
-    for (int round = 0; round < 8 && lo < hi; ++round) {
-        const int64_t step = (hi - lo + kThreads - 1) / kThreads;
-        const int64_t p = lo + (int64_t)threadIdx.x * step;
-        const bool less = p < hi && flat_at(idx, idx64, p) < key;
-        const int64_t c = __syncthreads_count(less);
-        if (step == 1) return lo + c;
-        if (c == 0) return lo;
-        const int64_t nlo = lo + (c - 1) * step + 1;
-        hi = hi < lo + c * step ? hi : lo + c * step;
-        lo = nlo;
-    }
-    return lo;
+    const uint32_t x = (uint32_t)flat;
+    t = x / d_in;
+    f = x - t * d_in;
 }
 
-// The 16-bit G-dtype encoding of entry e's product operand: the integer code for bits 4 / 8
-// (exact), or the stored value rounded to G's dtype for bits 0 (the reference casts the values to
-// G's dtype before its sparse product).
-__device__ __forceinline__ uint32_t entry_operand(const TileArgs &a, int64_t e)
+// The integer code of entry e (bits 4 / 8).
+__device__ __forceinline__ int entry_code(const TileArgs &a, int64_t e)
 {
-    float v;
-    if (a.bits == 8) {
-        v = (float)static_cast<const int8_t *>(a.data)[e];
-    } else if (a.bits == 4) {
-        const uint32_t b = static_cast<const uint8_t *>(a.data)[e >> 1];
-        const int n = (int)((e & 1) ? (b >> 4) : (b & 0xfu));
-        v = (float)(n > 7 ? n - 16 : n);
-    } else {
-        v = load_any(a.data, a.val_dt, e);
-    }
+    if (a.bits == 8) return static_cast<const int8_t *>(a.data)[e];
+    const uint32_t b = static_cast<const uint8_t *>(a.data)[e >> 1];
+    const int n = (int)((e & 1) ? (b >> 4) : (b & 0xfu));
+    return n > 7 ? n - 16 : n;
+}
+
+// The product operand of entry e in G's dtype: the integer code for bits 4 / 8 (exact), or the
+// stored value rounded to G's dtype for bits 0 (the reference casts the values to G's dtype before
+// its sparse product).
+__device__ __forceinline__ uint32_t entry_g16(const TileArgs &a, int64_t e)
+{
+    const float v = a.bits ? (float)entry_code(a, e) : load_any(a.data, a.val_dt, e);
     return a.g_dt == STACR_DTYPE_BF16 ? f_to_bf16_bits(v) : f_to_f16_bits(v);
 }
 
-__device__ __forceinline__ float g16_to_f(uint32_t v, int g_dt)
+template <int DT>
+__device__ __forceinline__ float g16_to_f(uint32_t v)
 {
-    return g_dt == STACR_DTYPE_BF16 ? bf16_bits_to_f(v) : f16_bits_to_f(v);
+    if constexpr (DT == STACR_DTYPE_BF16) return bf16_bits_to_f(v);
+    else return f16_bits_to_f(v);
+}
+
+// an integer-valued float (|x| <= 256) in G's dtype, exactly
+template <int DT>
+__device__ __forceinline__ uint32_t int_to_g16(float f)
+{
+    if constexpr (DT == STACR_DTYPE_BF16) return __float_as_uint(f) >> 16;
+    else return f_to_f16_bits(f);
+}
+
+// ------------------------------------------------------------------ the entry count
+__global__ __launch_bounds__(kThreads) void k_tile_count(TileArgs a)
+{
+    __shared__ uint32_t s_h[kMaxFeat];
+    const int c = blockIdx.x, tid = threadIdx.x;
+    const int64_t per = (a.nnz + kChunks - 1) / kChunks;
+    const int64_t e0 = (int64_t)c * per < a.nnz ? (int64_t)c * per : a.nnz;
+    const int64_t e1 = e0 + per < a.nnz ? e0 + per : a.nnz;
+    const uint32_t d_in = (uint32_t)a.d_in;
+    const int64_t last_blk = a.n_blocks - 1;
+    for (int f = tid; f < (int)d_in; f += kThreads) s_h[f] = 0u;
+    __syncthreads();
+    auto block_of = [&](uint32_t t) {
+        const int64_t b = (int64_t)(t / kTB);
+        return b < last_blk ? b : last_blk;
+    };
+    for (int64_t e = e0 + tid; e < e1; e += kThreads) {
+        uint32_t t, f;
+        split_flat(flat_at(a.idx, a.idx64, e), d_in, t, f);
+        atomicAdd(&s_h[f], 1u);
+        // every block b with block(e - 1) < b <= block(e) starts at e; past the last entry, nnz
+        const int64_t bcur = block_of(t);
+        int64_t bprev = -1;
+        if (e > 0) {
+            uint32_t tp, fp;
+            split_flat(flat_at(a.idx, a.idx64, e - 1), d_in, tp, fp);
+            bprev = block_of(tp);
+        }
+        for (int64_t b = bprev + 1; b <= bcur; ++b) a.bstart[b] = (uint32_t)e;
+        if (e == a.nnz - 1)
+            for (int64_t b = bcur + 1; b <= a.n_blocks; ++b) a.bstart[b] = (uint32_t)a.nnz;
+    }
+    __syncthreads();
+    for (int f = tid; f < (int)d_in; f += kThreads) a.hist[(int64_t)c * d_in + f] = s_h[f];
 }
 
 // ------------------------------------------------------------------ the plan
+template <bool BT8>
 __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
 {
-    __shared__ uint32_t s_cnt[kPartMax];        // sample counts, then light counts of the block
+    using CO = Cols<BT8>;
+    using BE = typename std::conditional<BT8, uint8_t, uint16_t>::type;
+    __shared__ uint32_t s_key[kPartMax];         // selection keys, then light offsets
     __shared__ int32_t s_slot[kPartMax];         // column slot of each feature of the part, or -1
     __shared__ uint32_t s_mask[kPartMax * 16];   // light rows of each feature (512-bit bitmaps)
-    __shared__ uint16_t s_bt[kNC * kTB];         // the block's column tile
-    __shared__ uint32_t s_tot[kThreads / 64];
-    __shared__ uint32_t s_hist[kTB + 2];          // counts of the sample counts (0..512)
-    __shared__ uint32_t s_pick[2];
-    __shared__ int32_t s_colfeat[kNC];
+    __shared__ __attribute__((aligned(16))) BE s_bt[CO::nc * kTB];  // the block's column entries [slot][t]
+    __shared__ uint32_t s_tot[kWaves];
 
     const int b = blockIdx.x, part = blockIdx.y, tid = threadIdx.x;
     const int64_t plo = (int64_t)part * a.part_w;
     const int pw = (int)(a.d_in - plo < a.part_w ? a.d_in - plo : a.part_w);
-    const int64_t block_elems = (int64_t)kTB * a.d_in;
 
-    if (!a.sparse) goto pack_coefficients;
-    {
-    // ---- entry ranges: the sample (block 0) and this block
-    const int64_t e_s1 = block_lower_bound(a.idx, a.idx64, a.nnz, block_elems);
-    const int64_t e_b0 = b == 0 ? 0 : block_lower_bound(a.idx, a.idx64, a.nnz, (int64_t)b * block_elems);
-    const int64_t e_b1 = b == 0 ? e_s1 : block_lower_bound(a.idx, a.idx64, a.nnz, (int64_t)(b + 1) * block_elems);
+    if (a.sparse) {
+        // ---- entry range of the block (clamped, whatever the starts hold)
+        int64_t e_b0 = a.bstart[b], e_b1 = a.bstart[b + 1];
+        e_b0 = e_b0 < a.nnz ? e_b0 : a.nnz;
+        e_b1 = e_b1 < a.nnz ? e_b1 : a.nnz;
+        e_b1 = e_b1 > e_b0 ? e_b1 : e_b0;
 
-    // ---- column features of the part, from the sample's counts
-    for (int f = tid; f < kPartMax; f += kThreads) s_cnt[f] = 0u;
-    for (int h = tid; h < kTB + 2; h += kThreads) s_hist[h] = 0u;
-    __syncthreads();
-    for (int64_t e = tid; e < e_s1; e += kThreads) {
-        const int64_t f = flat_at(a.idx, a.idx64, e) % a.d_in - plo;
-        if (f >= 0 && f < pw) atomicAdd(&s_cnt[f], 1u);
-    }
-    __syncthreads();
-    // the count c32 of the 32nd feature (counts at least kMinColCount), then the features above
-    // it and the first `need` (by feature) at it
-    if (tid < pw && s_cnt[tid] >= (uint32_t)kMinColCount) atomicAdd(&s_hist[s_cnt[tid] > kTB ? kTB : s_cnt[tid]], 1u);
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t above = 0, c32 = 0xffffffffu, need = 0;
-        for (int c = kTB; c >= kMinColCount; --c) {
-            const uint32_t h = s_hist[c];
-            if (above + h >= (uint32_t)kNC) {
-                c32 = (uint32_t)c;
-                need = kNC - above;
-                break;
-            }
-            above += h;
-        }
-        if (c32 == 0xffffffffu) {  // fewer than 32 candidates: take every one
-            c32 = kMinColCount;
-            need = 0xffffffffu;
-        }
-        s_pick[0] = c32;
-        s_pick[1] = need;
-    }
-    __syncthreads();
-    const uint32_t c32 = s_pick[0], need = s_pick[1];
-    const uint32_t mycnt = tid < pw ? s_cnt[tid] : 0u;
-    const bool at_cut = mycnt == c32 && mycnt >= (uint32_t)kMinColCount;
-    uint32_t n_at;
-    const uint32_t rank_at = block_exclusive_scan<kThreads>(at_cut ? 1u : 0u, s_tot, &n_at);
-    const bool is_col = tid < pw && ((mycnt > c32 && mycnt >= (uint32_t)kMinColCount) || (at_cut && rank_at < need));
-    uint32_t n_col;
-    const uint32_t slot = block_exclusive_scan<kThreads>(is_col ? 1u : 0u, s_tot, &n_col);
-    if (tid < kPartMax) s_slot[tid] = is_col ? (int32_t)slot : -1;
-    if (tid < kNC) s_colfeat[tid] = -1;
-    __syncthreads();
-    if (is_col) s_colfeat[slot] = tid;
-    __syncthreads();
-    if (b == 0 && tid < kNC) a.colmap[part * kNC + tid] = s_colfeat[tid];
-
-    // ---- this block's entries: the column tile and the light bitmaps
-    for (int i = tid; i < kNC * kTB; i += kThreads) s_bt[i] = 0;
-    for (int i = tid; i < kPartMax * 16; i += kThreads) s_mask[i] = 0u;
-    __syncthreads();
-    const int64_t t_base = (int64_t)b * kTB;
-    uint32_t before_part = 0;  // entries of this block in lower parts: where the part's records start
-    for (int64_t e = e_b0 + tid; e < e_b1; e += kThreads) {
-        const int64_t flat = flat_at(a.idx, a.idx64, e);
-        const int64_t t = flat / a.d_in, f = flat - t * a.d_in - plo;
-        const int64_t tl64 = t - t_base;
-        if (tl64 < 0 || tl64 >= kTB) continue;  // only indices inside the block (valid input has no other)
-        before_part += f < 0;
-        if (f < 0 || f >= pw) continue;
-        const int tl = (int)tl64;
-        const int s = s_slot[f];
-        if (s >= 0) s_bt[s * kTB + tl] = (uint16_t)entry_operand(a, e);
-        else atomicOr(&s_mask[f * 16 + (tl >> 5)], 1u << (tl & 31));
-    }
-    __syncthreads();
-    uint32_t all_before;
-    (void)block_exclusive_scan<kThreads>(before_part, s_tot, &all_before);
-    // light count of each feature, their offsets
-    uint32_t cnt = 0;
-    if (tid < pw) {
+        // ---- column features: keys count << 16 | (65535 - f), sorted descending (bitonic)
+        uint32_t key = 0;
+        if (tid < pw) {
+            uint32_t cnt = 0;
 #pragma unroll
-        for (int w = 0; w < 16; ++w) cnt += __popc(s_mask[tid * 16 + w]);
-    }
-    uint32_t n_light;
-    const uint32_t off = block_exclusive_scan<kThreads>(cnt, s_tot, &n_light);
-    uint32_t *loff = a.loff + ((int64_t)b * a.n_parts + part) * kOffWords;
-    if (tid < pw) loff[tid] = off;
-    if (tid == 0) loff[pw] = n_light;  // the part's end (pw may be 1024, past the last thread)
-    // regions are disjoint and ordered by (block, part); shifting region r by 3 r and rounding up
-    // to 4 keeps them disjoint and makes every start 16-byte aligned for the staging loads
-    const uint32_t region = (uint32_t)(b * a.n_parts + part);
-    const uint32_t base = ((uint32_t)e_b0 + all_before + 3u * region + 3u) & ~3u;
-    if (tid == 0) a.hdr[b * a.n_parts + part] = TileHdr{base, n_light, {0u, 0u}};
-    if (tid < kPartMax) s_cnt[tid] = tid < pw ? off : 0u;
-    __syncthreads();
-    // each light entry at its feature's offset + the feature's light entries in earlier rows
-    for (int64_t e = e_b0 + tid; e < e_b1; e += kThreads) {
-        const int64_t flat = flat_at(a.idx, a.idx64, e);
-        const int64_t t = flat / a.d_in, f = flat - t * a.d_in - plo;
-        const int64_t tl64 = t - t_base;
-        if (tl64 < 0 || tl64 >= kTB || f < 0 || f >= pw || s_slot[f] >= 0) continue;
-        const int tl = (int)tl64;
-        uint32_t r = __popc(s_mask[f * 16 + (tl >> 5)] & ((1u << (tl & 31)) - 1u));
-        for (int w = 0; w < (tl >> 5); ++w) r += __popc(s_mask[f * 16 + w]);
-        a.light[base + s_cnt[f] + r] = (uint32_t)tl | (entry_operand(a, e) << 16);
-    }
-    // the column tile, coalesced
-    uint4 *bt = reinterpret_cast<uint4 *>(a.bt + ((int64_t)b * a.n_parts + part) * kNC * kTB);
-    const uint4 *sb = reinterpret_cast<const uint4 *>(s_bt);
-    for (int i = tid; i < kNC * kTB / 8; i += kThreads) bt[i] = sb[i];
+            for (int c = 0; c < kChunks; ++c) cnt += a.hist[(int64_t)c * a.d_in + plo + tid];
+            key = cnt ? ((cnt < 0xffffu ? cnt : 0xffffu) << 16) | (0xffffu - (uint32_t)tid) : 0u;
+        }
+        s_key[tid] = key;
+        s_slot[tid] = -1;
+        __syncthreads();
+        for (int k = 2; k <= kPartMax; k <<= 1) {
+            for (int j = k >> 1; j > 0; j >>= 1) {
+                const int ixj = tid ^ j;
+                if (ixj > tid) {
+                    const uint32_t x = s_key[tid], y = s_key[ixj];
+                    const bool desc = (tid & k) == 0;
+                    if (desc ? x < y : x > y) {
+                        s_key[tid] = y;
+                        s_key[ixj] = x;
+                    }
+                }
+                __syncthreads();
+            }
+        }
+        if (tid < CO::nc) {
+            const uint32_t kk = s_key[tid];
+            const int f = kk ? (int)(0xffffu - (kk & 0xffffu)) : -1;
+            if (f >= 0) s_slot[f] = tid;
+            if (b == 0) a.colmap[part * kNCMax + tid] = f;
+        }
+        if (b == 0 && tid >= CO::nc && tid < kNCMax) a.colmap[part * kNCMax + tid] = -1;
 
+        // ---- this block's entries: the column tile and the light bitmaps
+        for (int i = tid; i < CO::nc * kTB; i += kThreads) s_bt[i] = 0;
+        for (int i = tid; i < kPartMax * 16; i += kThreads) s_mask[i] = 0u;
+        __syncthreads();
+        const int64_t t_base = (int64_t)b * kTB;
+        const uint32_t d_in = (uint32_t)a.d_in;
+        uint32_t before_part = 0;  // entries of this block in lower parts: where the part's records start
+        for (int64_t e = e_b0 + tid; e < e_b1; e += kThreads) {
+            uint32_t t, fg;
+            split_flat(flat_at(a.idx, a.idx64, e), d_in, t, fg);
+            const int64_t tl64 = (int64_t)t - t_base, f = (int64_t)fg - plo;
+            if (tl64 < 0 || tl64 >= kTB) continue;  // only indices inside the block (valid input has no other)
+            before_part += f < 0;
+            if (f < 0 || f >= pw) continue;
+            const int tl = (int)tl64;
+            const int s = s_slot[f];
+            if (s >= 0) {
+                if constexpr (BT8) s_bt[s * kTB + tl] = (BE)(uint8_t)(int8_t)entry_code(a, e);
+                else s_bt[s * kTB + tl] = (BE)entry_g16(a, e);
+            } else {
+                atomicOr(&s_mask[f * 16 + (tl >> 5)], 1u << (tl & 31));
+            }
+        }
+        __syncthreads();
+        uint32_t all_before;
+        (void)block_exclusive_scan<kThreads>(before_part, s_tot, &all_before);
+        // light count of each feature, their offsets
+        uint32_t cnt = 0;
+        if (tid < pw) {
+#pragma unroll
+            for (int w = 0; w < 16; ++w) cnt += __popc(s_mask[tid * 16 + w]);
+        }
+        uint32_t n_light;
+        const uint32_t off = block_exclusive_scan<kThreads>(cnt, s_tot, &n_light);
+        uint32_t *loff = a.loff + ((int64_t)b * a.n_parts + part) * kOffWords;
+        if (tid < pw) loff[tid] = off;
+        if (tid == 0) loff[pw] = n_light;  // the part's end (pw may be 1024, past the last thread)
+        // regions are disjoint and ordered by (block, part); shifting region r by 3 r and rounding up
+        // to 4 keeps them disjoint and makes every start 16-byte aligned for the staging copies
+        const uint32_t region = (uint32_t)(b * a.n_parts + part);
+        const uint32_t base = ((uint32_t)e_b0 + all_before + 3u * region + 3u) & ~3u;
+        if (tid == 0) a.hdr[b * a.n_parts + part] = TileHdr{base, n_light, {0u, 0u}};
+        s_key[tid] = tid < pw ? off : 0u;
+        __syncthreads();
+        // each light entry at its feature's offset + the feature's light entries in earlier rows
+        for (int64_t e = e_b0 + tid; e < e_b1; e += kThreads) {
+            uint32_t t, fg;
+            split_flat(flat_at(a.idx, a.idx64, e), d_in, t, fg);
+            const int64_t tl64 = (int64_t)t - t_base, f = (int64_t)fg - plo;
+            if (tl64 < 0 || tl64 >= kTB || f < 0 || f >= pw || s_slot[f] >= 0) continue;
+            const int tl = (int)tl64;
+            uint32_t r = __popc(s_mask[f * 16 + (tl >> 5)] & ((1u << (tl & 31)) - 1u));
+            for (int w = 0; w < (tl >> 5); ++w) r += __popc(s_mask[f * 16 + w]);
+            a.light[base + s_key[f] + r] = (uint32_t)tl | (entry_g16(a, e) << 16);
+        }
+        // the column operands in lane order: (tile i, wave w, lane l) holds rows 32 w + 8 (l / 16)
+        // .. + 7 of column 16 i + l % 16, 8 elements
+        BE *bt = static_cast<BE *>(a.bt) + ((int64_t)b * a.n_parts + part) * CO::nt * kWaves * 64 * 8;
+        for (int u = tid; u < CO::nt * kWaves * 64; u += kThreads) {
+            const int l = u & 63, w = (u >> 6) & 15, i = u >> 10;
+            const BE *src = s_bt + (16 * i + (l & 15)) * kTB + 32 * w + 8 * (l >> 4);
+            if constexpr (BT8) *reinterpret_cast<uint2 *>(bt + (int64_t)u * 8) = *reinterpret_cast<const uint2 *>(src);
+            else *reinterpret_cast<uint4 *>(bt + (int64_t)u * 8) = *reinterpret_cast<const uint4 *>(src);
+        }
     }
-pack_coefficients:
-    // ---- the block's coefficients, transposed, with the ones column (part 0 only)
+
+    // ---- the block's coefficient operands [C | 1] (part 0): (wave w, row group g, column n)
+    // holds rows 32 w + 8 g .. + 7 of column n
     if (part == 0) {
         const uint16_t *c = static_cast<const uint16_t *>(a.coeff);
         const uint32_t one = a.g_dt == STACR_DTYPE_BF16 ? 0x3f80u : 0x3c00u;
-        uint16_t *cp = a.cp + (int64_t)b * a.ncol * kTB;
-        for (int i = tid; i < a.ncol * kTB; i += kThreads) {
-            const int col = i / kTB, tl = i - col * kTB;
-            const int64_t t = (int64_t)b * kTB + tl;
+        uint16_t *cp = a.cp + (int64_t)b * kTB * a.ncol;
+        for (int i = tid; i < kTB * a.ncol; i += kThreads) {
+            const int k = i & 7, n = (i >> 3) % a.ncol, wg = (i >> 3) / a.ncol;  // wg = 4 w + g
+            const int64_t t = (int64_t)b * kTB + 8 * wg + k;
             uint16_t v = 0;
             if (t < a.rows) {
-                if (col < a.rank) v = c[t * a.rank + col];
-                else if (col == a.bias_col) v = (uint16_t)one;
+                if (n < a.rank) v = c[t * a.rank + n];
+                else if (n == a.bias_col) v = (uint16_t)one;
             }
             cp[i] = v;
         }
@@ -287,37 +335,89 @@ __device__ __forceinline__ uint2 lds_tr16(const uint16_t *p)
     return __builtin_bit_cast(uint2, v);
 }
 
-// 16 bytes per lane from `src` into LDS at `wave_dst` + 16 * lane (wave_dst wave-uniform)
-__device__ __forceinline__ void async_copy16(const void *src, void *wave_dst)
+// c + a.lo b.lo + a.hi b.hi for two pairs of 16-bit values in G's dtype (v_dot2c_f32_bf16 / f16)
+template <int DT>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c)
 {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)wave_dst, 16, 0, 0);
+    if constexpr (DT == STACR_DTYPE_BF16) {
+        typedef __attribute__((ext_vector_type(2))) __bf16 v2;
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+    } else {
+        typedef __attribute__((ext_vector_type(2))) _Float16 v2;
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+    }
 }
 
-// LDS layout of one buffer (byte offsets)
-template <int NCOL, bool SP>
+// A raw buffer resource over `bytes` bytes at p (clamped to 4 GiB - 1); dword 3 is the gfx9-family
+// raw-buffer format word.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint64_t bytes)
+{
+    const int n = bytes < 0xffffffffull ? (int)(uint32_t)bytes : (int)0xffffffffu;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, n, 0x00020000);
+}
+
+// 16 bytes per lane at byte voffset + soffset of the resource into LDS at `wave_dst` + 16 * lane
+// (wave_dst and soffset wave-uniform)
+__device__ __forceinline__ void copy16(__amdgpu_buffer_rsrc_t r, void *wave_dst, uint32_t voffset, uint32_t soffset)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)wave_dst, 16, (int)voffset,
+                                             (int)soffset, 0, 0);
+}
+
+__device__ __forceinline__ uint4 load16(__amdgpu_buffer_rsrc_t r, uint32_t voffset, uint32_t soffset)
+{
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voffset, (int)soffset, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint2 load8(__amdgpu_buffer_rsrc_t r, uint32_t voffset, uint32_t soffset)
+{
+    typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+    const v2u v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voffset, (int)soffset, 0);
+    return make_uint2(v.x, v.y);
+}
+
+// eight int8 codes -> eight 16-bit operands (exact: |code| <= 128)
+template <int DT>
+__device__ __forceinline__ uint4 codes_to_operand(uint2 w)
+{
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t word = k < 2 ? w.x : w.y;
+        const int sh = 16 * (k & 1);
+        const float lo = (float)(int)(int8_t)(word >> sh), hi = (float)(int)(int8_t)(word >> (sh + 8));
+        o[k] = int_to_g16<DT>(lo) | (int_to_g16<DT>(hi) << 16);
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// LDS layout of one stream buffer (byte offsets).  The kernel holds three buffers as three
+// distinct __shared__ arrays: the compiler then knows that reads of one never alias the
+// direct-to-LDS copies into the others, and waits for those copies only where the code says so.
+template <bool SP>
 struct TileLds {
-    static constexpr size_t g = 0;                                   // [kTB][16] u16
-    static constexpr size_t c = g + (size_t)kTB * kOS * 2;           // [NCOL][kTB] u16
-    static constexpr size_t bt = c + (size_t)NCOL * kTB * 2;         // [kNC][kTB] u16
-    static constexpr size_t light = bt + (SP ? (size_t)kNC * kTB * 2 : 0);  // [kLightCap] u32
-    static constexpr size_t off = light + (SP ? (size_t)kLightCap * 4 : 0); // [kOffWords] u32
+    static constexpr size_t g = 0;                                           // [kTB][16] u16
+    static constexpr size_t light = g + (size_t)kTB * kOS * 2;               // [kLightCap] u32
+    static constexpr size_t off = light + (SP ? (size_t)kLightCap * 4 : 0);  // [kOffWords] u32
     static constexpr size_t size = off + (SP ? (size_t)kOffWords * 4 : 0);
-    // after the stream: the per-wave tiles [16 waves][16][16] f32 for M and the two column tiles
-    static constexpr size_t red = 0;
-    static constexpr size_t mfin = red + (size_t)3 * 16 * 256 * 4;
-    static constexpr size_t cfin = mfin + (size_t)256 * 4;
-    static constexpr size_t slots = cfin + (size_t)2 * 256 * 4;
-    static constexpr size_t reduce_end = slots + (size_t)kPartMax * 4;
-    static constexpr size_t total = 2 * size > reduce_end ? 2 * size : reduce_end;
     static_assert(size % 1024 == 0, "buffers start on 1 KiB boundaries");
-    static_assert(total <= 160 * 1024, "fits the CU's LDS");
+    static_assert(3 * size + kMaxBlocks * sizeof(TileHdr) <= 160 * 1024, "fits the CU's LDS");
+    static_assert(size >= (size_t)kWaves * 256 * 4, "one tile of every wave fits a buffer (the reduction)");
 };
 
-template <int DT, int NCOL, bool SP>
+template <int DT, bool SP, bool BT8>
 __global__ __launch_bounds__(kThreads) void k_tile_grad(TileArgs a)
 {
-    using L = TileLds<NCOL, SP>;
-    extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
+    using L = TileLds<SP>;
+    using CO = Cols<BT8>;
+    constexpr int NT = SP ? CO::nt : 0;
+    using BW = typename std::conditional<BT8, uint2, uint4>::type;  // one lane's column operand
+    __shared__ __attribute__((aligned(1024))) unsigned char lds0[L::size];
+    __shared__ __attribute__((aligned(1024))) unsigned char lds1[L::size];
+    __shared__ __attribute__((aligned(1024))) unsigned char lds2[L::size];
+    __shared__ TileHdr s_hdr[SP ? kMaxBlocks : 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
     // workgroup -> (o-slab, part): consecutive logical ids share an XCD (ids are dealt to the 8 XCDs
@@ -330,120 +430,202 @@ __global__ __launch_bounds__(kThreads) void k_tile_grad(TileArgs a)
     const int64_t plo = (int64_t)part * a.part_w;
     const int pw = (int)(a.d_in - plo < a.part_w ? a.d_in - plo : a.part_w);
     const int nb = a.n_blocks;
-    const int g_dt = a.g_dt;
 
-    const uint16_t *g = static_cast<const uint16_t *>(a.g);
-    const int64_t last_row = a.rows - 1;
+    const int n = lane & 15, grp = lane >> 4;
 
-    // this lane's source row of the G tile: row 32 wave + lane / 2, 8 outputs at half lane & 1.
-    // `h` is the block's header, loaded one iteration earlier so its latency never delays the copies.
-    auto issue = [&](int blk, int buf, const TileHdr &h) {
-        unsigned char *B = lds + (size_t)buf * L::size;
-        int64_t t = (int64_t)blk * kTB + 32 * wave + (lane >> 1);
-        t = t < last_row ? t : last_row;  // rows past the end repeat the last (their C is zero)
-        async_copy16(g + t * a.d_out + o0 + 8 * (lane & 1), B + L::g + (size_t)wave * 1024);
-        if (wave < NCOL) async_copy16(a.cp + ((int64_t)blk * NCOL + wave) * kTB + 8 * lane, B + L::c + (size_t)wave * 1024);
+    if constexpr (SP) {
+        for (int b = tid; b < nb; b += kThreads) s_hdr[b] = a.hdr[b * a.n_parts + part];
+        __syncthreads();
+    }
+
+    // Every load goes through a buffer resource (base and size in scalar registers) with a 32-bit
+    // per-lane offset that is the same for every block and a uniform per-block offset.  Kept apart
+    // like this, no 64-bit per-lane address has to live across the stream.
+    const uint32_t row_bytes = (uint32_t)a.d_out * 2;
+    const uint32_t g_lane_row = 32u * wave + (lane >> 1);                     // G tile row of this lane
+    const uint32_t g_lane_col = (uint32_t)o0 * 2 + 16u * (lane & 1);          // bytes into the row
+    const uint32_t rec_lane = (256u * wave + 4u * lane) * 4;                  // light / offset copies
+    const uint32_t cp_lane = ((wave * 4u + grp) * a.ncol + n) * 16;           // coefficient operand
+    const uint32_t bt_lane = (wave * 64u + lane) * sizeof(BW);                // column operand
+    const bool has_c = n < a.ncol;
+    const uint32_t regions = (uint32_t)nb * (uint32_t)a.n_parts;
+    const __amdgpu_buffer_rsrc_t r_cp = make_rsrc(a.cp, (uint64_t)nb * kTB * a.ncol * 2);
+    // (without entries these three are empty resources that nothing reads)
+    const __amdgpu_buffer_rsrc_t r_light = make_rsrc(a.light, SP ? ((uint64_t)a.nnz + 3ull * regions + 3 + kLightCap) * 4 : 0);
+    const __amdgpu_buffer_rsrc_t r_loff = make_rsrc(a.loff, SP ? (uint64_t)regions * kOffWords * 4 : 0);
+    const __amdgpu_buffer_rsrc_t r_bt = make_rsrc(a.bt, SP ? (uint64_t)regions * NT * kWaves * 64 * sizeof(BW) : 0);
+
+    // ---- block `blk`'s copies into buffer B: light records (only the 1 KiB chunks the block has)
+    // and offsets, then (issue_g) the G tile (this lane: row 32 wave + lane / 2, outputs 8 (lane & 1) ..)
+    auto issue_records = [&](int blk, unsigned char *B) {
         if constexpr (SP) {
-            const uint16_t *bt = a.bt + ((int64_t)blk * a.n_parts + part) * kNC * kTB;
-            async_copy16(bt + (size_t)wave * 512 + 8 * lane, B + L::bt + (size_t)wave * 1024);
-            async_copy16(bt + (size_t)(wave + 16) * 512 + 8 * lane, B + L::bt + (size_t)(wave + 16) * 1024);
-            if (wave < 8) async_copy16(a.light + h.light_base + 256 * wave + 4 * lane, B + L::light + (size_t)wave * 1024);
-            else if (wave < 13)
-                async_copy16(a.loff + ((int64_t)blk * a.n_parts + part) * kOffWords + 256 * (wave - 8) + 4 * lane,
-                             B + L::off + (size_t)(wave - 8) * 1024);
+            const uint32_t lbase = __builtin_amdgcn_readfirstlane(s_hdr[blk].light_base);
+            const uint32_t lcount = __builtin_amdgcn_readfirstlane(s_hdr[blk].light_count);
+            if (256u * (uint32_t)wave < lcount) copy16(r_light, B + L::light + (size_t)wave * 1024, rec_lane, lbase * 4);
+            if (wave < 5 && 256 * wave <= pw)
+                copy16(r_loff, B + L::off + (size_t)wave * 1024, rec_lane,
+                       ((uint32_t)blk * a.n_parts + part) * (uint32_t)kOffWords * 4);
+        }
+    };
+    auto issue_g = [&](int blk, unsigned char *B) {
+        // rows past the end repeat the last (their operands are zero)
+        const uint32_t rows_here = (uint32_t)(a.rows - (int64_t)blk * kTB) < (uint32_t)kTB
+                                       ? (uint32_t)(a.rows - (int64_t)blk * kTB) : (uint32_t)kTB;
+        const uint32_t r = g_lane_row < rows_here - 1 ? g_lane_row : rows_here - 1;
+        const __amdgpu_buffer_rsrc_t r_g =
+            make_rsrc(static_cast<const char *>(a.g) + (size_t)blk * kTB * row_bytes, (uint64_t)rows_here * row_bytes);
+        copy16(r_g, B + L::g + (size_t)wave * 1024, r * row_bytes + g_lane_col, 0u);
+    };
+
+    // ---- block `blk`'s operands for this lane: rows 32 wave + 8 grp .. + 7 of column n
+    struct Ops {
+        uint4 c;
+        BW t[NT > 0 ? NT : 1];
+    };
+    auto load_ops = [&](int blk, Ops &r) {
+        r.c = make_uint4(0u, 0u, 0u, 0u);
+        if (has_c) r.c = load16(r_cp, cp_lane, (uint32_t)blk * kTB * a.ncol * 2);
+        if constexpr (SP) {
+            const uint32_t base = ((uint32_t)blk * a.n_parts + part) * (uint32_t)(NT * kWaves * 64 * sizeof(BW));
+#pragma unroll
+            for (int i = 0; i < NT; ++i) {
+                const uint32_t so = base + (uint32_t)(i * kWaves * 64 * sizeof(BW));
+                if constexpr (BT8) r.t[i] = load8(r_bt, bt_lane, so);
+                else r.t[i] = load16(r_bt, bt_lane, so);
+            }
         }
     };
 
-    f32x4 acc_m = {0.f, 0.f, 0.f, 0.f}, acc_c0 = acc_m, acc_c1 = acc_m;
+    f32x4 acc_m = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc_t[NT > 0 ? NT : 1];
+#pragma unroll
+    for (int i = 0; i < (NT > 0 ? NT : 1); ++i) acc_t[i] = acc_m;
     float s[kOS];
 #pragma unroll
     for (int o = 0; o < kOS; ++o) s[o] = 0.f;
 
-    const TileHdr zero_hdr{0u, 0u, {0u, 0u}};
-    auto header = [&](int blk) { return SP && blk < nb ? a.hdr[blk * a.n_parts + part] : zero_hdr; };
-    TileHdr h_cur = header(0);
-    issue(0, 0, h_cur);
-    TileHdr h_next = header(1);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int blk = 0; blk < nb; ++blk) {
-        const int buf = blk & 1;
-        if (blk + 1 < nb) issue(blk + 1, buf ^ 1, h_next);
-        const TileHdr h_blk = h_cur;
-        h_cur = h_next;
-        h_next = header(blk + 2);
-        const unsigned char *B = lds + (size_t)buf * L::size;
+    // ---- the block in buffer B with operands r: the matrix-core products
+    auto products = [&](const unsigned char *B, const Ops &r) {
         const uint16_t *gt = reinterpret_cast<const uint16_t *>(B + L::g);
         // G^T[o][t0 .. t0 + 7], o = lane % 16, t0 = 32 wave + 8 (lane / 16): two transposing reads
         // (in a 16-lane group lane m addresses row r0 + m / 4, outputs 4 (m % 4) .. + 3, and lane n
         // receives G[r0 + j][n], j = 0..3)
-        const int kk = 32 * wave + 8 * (lane >> 4);
+        const int kk = 32 * wave + 8 * grp;
         const uint16_t *pa = gt + (kk + ((lane & 15) >> 2)) * kOS + (lane & 3) * 4;
         const uint2 lo = lds_tr16(pa), hi = lds_tr16(pa + 4 * kOS);
         const uint4 av = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        const int n = lane & 15;
-        const uint16_t *ct = reinterpret_cast<const uint16_t *>(B + L::c);
-        const uint4 bc = n < NCOL ? *reinterpret_cast<const uint4 *>(ct + n * kTB + kk) : make_uint4(0u, 0u, 0u, 0u);
-        acc_m = mfma16<DT>(av, bc, acc_m);
+        acc_m = mfma16<DT>(av, r.c, acc_m);
         if constexpr (SP) {
-            const uint16_t *bt = reinterpret_cast<const uint16_t *>(B + L::bt);
-            const uint4 b0 = *reinterpret_cast<const uint4 *>(bt + n * kTB + kk);
-            const uint4 b1 = *reinterpret_cast<const uint4 *>(bt + (16 + n) * kTB + kk);
-            acc_c0 = mfma16<DT>(av, b0, acc_c0);
-            acc_c1 = mfma16<DT>(av, b1, acc_c1);
-            // this thread's feature: its light entries of the block
+#pragma unroll
+            for (int i = 0; i < NT; ++i) {
+                uint4 bv;
+                if constexpr (BT8) bv = codes_to_operand<DT>(r.t[i]);
+                else bv = r.t[i];
+                acc_t[i] = mfma16<DT>(av, bv, acc_t[i]);
+            }
+        }
+    };
+
+    // ---- this thread's feature: its light entries of the block in buffer B
+    auto light_entries = [&](int blk, const unsigned char *B) {
+        if constexpr (SP) {
+            const uint16_t *gt = reinterpret_cast<const uint16_t *>(B + L::g);
             if (tid < pw) {
+                const TileHdr h = s_hdr[blk];
                 const uint32_t *off = reinterpret_cast<const uint32_t *>(B + L::off);
                 const uint32_t *lrec = reinterpret_cast<const uint32_t *>(B + L::light);
                 // the owner's range, clamped to the block's records whatever the offsets hold
-                const uint32_t k1 = off[tid + 1] < h_blk.light_count ? off[tid + 1] : h_blk.light_count;
+                const uint32_t k1 = off[tid + 1] < h.light_count ? off[tid + 1] : h.light_count;
                 const uint32_t k0 = off[tid] < k1 ? off[tid] : k1;
-                const uint32_t gbase = h_blk.light_base;
-#pragma unroll 2
-                for (uint32_t k = k0; k < k1; ++k) {
-                    const uint32_t rec = k < (uint32_t)kLightCap ? lrec[k] : a.light[gbase + k];
-                    const float v = g16_to_f(rec >> 16, g_dt);
+                // s[2 k] += lo(w_k) v and s[2 k + 1] += hi(w_k) v for the row's eight 32-bit words
+                // w_k: dot products with the pairs (v, 0) and (0, v), no conversions
+                auto add_entry = [&](uint32_t rec) {
+                    const uint32_t v_lo = rec >> 16, v_hi = rec & 0xffff0000u;
                     const uint4 *row = reinterpret_cast<const uint4 *>(gt + (rec & 511u) * kOS);
                     const uint4 w0 = row[0], w1 = row[1];
                     const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
                     for (int o = 0; o < 8; ++o) {
-                        s[2 * o] = fmaf(v, g16_to_f(w[o] & 0xffffu, g_dt), s[2 * o]);
-                        s[2 * o + 1] = fmaf(v, g16_to_f(w[o] >> 16, g_dt), s[2 * o + 1]);
+                        s[2 * o] = dot2<DT>(w[o], v_lo, s[2 * o]);
+                        s[2 * o + 1] = dot2<DT>(w[o], v_hi, s[2 * o + 1]);
                     }
-                }
+                };
+                // records staged in LDS, then (blocks with more than kLightCap) the rest from memory
+                const uint32_t kl = k1 < (uint32_t)kLightCap ? k1 : (uint32_t)kLightCap;
+                for (uint32_t k = k0; k < kl; ++k) add_entry(lrec[k]);
+                for (uint32_t k = k0 > kl ? k0 : kl; k < k1; ++k) add_entry(a.light[h.light_base + k]);
             }
         }
-        __builtin_amdgcn_s_waitcnt(0);  // the next block's tiles have landed
-        __syncthreads();                // and every wave is done with this block's buffer
-    }
+    };
 
-    // ---- reduce the per-wave tiles over the waves, in wave order
-    float *red = reinterpret_cast<float *>(lds + L::red);
-    float *mfin = reinterpret_cast<float *>(lds + L::mfin);
-    float *cfin = reinterpret_cast<float *>(lds + L::cfin);
-    int32_t *slots = reinterpret_cast<int32_t *>(lds + L::slots);
+    // ---- the stream: block blk runs in buffer blk % 3 while block blk + 2 is copied into
+    // buffer (blk + 2) % 3.  A step: the products of block blk (its operands then die), the operand
+    // loads of block blk + 1, the copies of block blk + 2 (the G copy last), the light entries of
+    // block blk; then a wait that lets only the last memory instruction (that G copy) stay in
+    // flight across the barrier.
+    Ops ops;
+    load_ops(0, ops);
+    issue_records(0, lds0);
+    issue_g(0, lds0);
+    if (nb > 1) {
+        issue_records(1, lds1);
+        issue_g(1, lds1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    auto step = [&](int blk, const unsigned char *__restrict__ B, unsigned char *__restrict__ B2) {
+        products(B, ops);
+        if (blk + 1 < nb) load_ops(blk + 1, ops);
+        if (blk + 2 < nb) issue_records(blk + 2, B2);
+        // every step ends its memory instructions with one G copy, so that the wait below always
+        // covers the operand loads; in the last two steps it copies the last block again into the
+        // buffer of block blk - 1, which nothing reads any more
+        issue_g(blk + 2 < nb ? blk + 2 : nb - 1, B2);
+        light_entries(blk, B);
+        // vmcnt(1) lgkmcnt(0) (expcnt unconstrained), as a builtin so that the compiler knows the
+        // operand loads have landed; then the barrier, not __syncthreads(), whose fence would wait
+        // for every copy in flight
+        __builtin_amdgcn_s_waitcnt(0x0071);
+        asm volatile("s_barrier" ::: "memory");
+    };
+    for (int blk = 0, cb = 0; blk < nb; ++blk, cb = cb == 2 ? 0 : cb + 1) {
+        unsigned char *B = cb == 0 ? lds0 : cb == 1 ? lds1 : lds2;
+        unsigned char *B2 = cb == 0 ? lds2 : cb == 1 ? lds0 : lds1;
+        step(blk, B, B2);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    // ---- reduce the per-wave tiles over the waves, in wave order: staged tile by tile in lds0,
+    // the sums and the part's column slots in lds1
+    constexpr int NTILE = 1 + NT;
+    static_assert(!SP || NTILE * 256 * 4 + kPartMax * 4 <= L::size, "sums and slots fit a buffer");
+    float *stage = reinterpret_cast<float *>(lds0);
+    float *fin = reinterpret_cast<float *>(lds1);                         // [NTILE][o][j]
+    int32_t *slots = reinterpret_cast<int32_t *>(lds1 + NTILE * 256 * 4);  // [pw]
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int row = 4 * (lane >> 4) + r;  // D layout: rows 4 (lane / 16) .. + 3 of column lane % 16
-        red[(0 * 16 + wave) * 256 + row * 16 + (lane & 15)] = acc_m[r];
-        red[(1 * 16 + wave) * 256 + row * 16 + (lane & 15)] = acc_c0[r];
-        red[(2 * 16 + wave) * 256 + row * 16 + (lane & 15)] = acc_c1[r];
+    for (int tile = 0; tile < NTILE; ++tile) {
+        const f32x4 acc = tile == 0 ? acc_m : acc_t[tile > 0 ? tile - 1 : 0];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)  // D layout: rows 4 (lane / 16) .. + 3 of column lane % 16
+            stage[wave * 256 + (4 * grp + r) * 16 + n] = acc[r];
+        __syncthreads();
+        if (tid < 256) {
+            float sum = 0.f;
+            for (int w = 0; w < kWaves; ++w) sum += stage[w * 256 + tid];
+            fin[tile * 256 + tid] = sum;
+        }
+        __syncthreads();
     }
-    if (tid < kPartMax) slots[tid] = -1;
-    __syncthreads();
-    if (SP && tid < kNC) {
-        const int f = a.colmap[part * kNC + tid];
-        if (f >= 0 && f < kPartMax) slots[f] = tid;
+    if constexpr (SP) {
+        if (tid < pw) slots[tid] = -1;
+        __syncthreads();
+        if (tid < CO::nc) {
+            const int f = a.colmap[part * kNCMax + tid];
+            if (f >= 0 && f < pw) slots[f] = tid;
+        }
+        __syncthreads();
     }
-    for (int i = tid; i < 3 * 256; i += kThreads) {
-        const int tile = i / 256, e = i % 256;
-        float sum = 0.f;
-        for (int w = 0; w < 16; ++w) sum += red[(tile * 16 + w) * 256 + e];
-        if (tile == 0) mfin[e] = sum;
-        else cfin[(tile - 1) * 256 + e] = sum;  // [tile][o][n]: slot 16 (tile - 1) + n
-    }
-    __syncthreads();
 
     // ---- dW tile: M Q^T + scale (light + column sums), one rounding; dbias from M[:, bias_col]
     // the scale exists only with residual entries (the C ABI checks it then); without them the
@@ -456,14 +638,14 @@ __global__ __launch_bounds__(kThreads) void k_tile_grad(TileArgs a)
         float out[kOS];
 #pragma unroll
         for (int o = 0; o < kOS; ++o) {
-            const float col = slot >= 0 ? cfin[(slot >> 4) * 256 + o * 16 + (slot & 15)] : 0.f;
+            const float col = slot >= 0 ? fin[(1 + (slot >> 4)) * 256 + o * 16 + (slot & 15)] : 0.f;
             out[o] = scale * (s[o] + col);
         }
         // + sum_j M[o][j] Q[i][j], one rank column at a time (the M reads are LDS broadcasts)
         for (int j = 0; j < a.rank; ++j) {
-            const float qj = g16_to_f(q[i * a.rank + j], g_dt);
+            const float qj = g16_to_f<DT>(q[i * a.rank + j]);
 #pragma unroll
-            for (int o = 0; o < kOS; ++o) out[o] = fmaf(mfin[o * 16 + j], qj, out[o]);
+            for (int o = 0; o < kOS; ++o) out[o] = fmaf(fin[o * 16 + j], qj, out[o]);
         }
         if (a.transposed) {  // Conv1D: dW is d_in x d_out, 16 consecutive outputs per thread
             if (a.dw_dt == STACR_DTYPE_F32) {
@@ -486,7 +668,7 @@ __global__ __launch_bounds__(kThreads) void k_tile_grad(TileArgs a)
             for (int o = 0; o < kOS; ++o) store_any(a.dw, a.dw_dt, (o0 + o) * a.d_in + i, out[o]);
         }
     }
-    if (a.dbias && part == 0 && tid < kOS) store_any(a.dbias, a.db_dt, o0 + tid, mfin[tid * 16 + a.bias_col]);
+    if (a.dbias && part == 0 && tid < kOS) store_any(a.dbias, a.db_dt, o0 + tid, fin[tid * 16 + a.bias_col]);
 }
 
 }  // namespace
@@ -496,7 +678,7 @@ namespace {
 
 struct TileGeom {
     int n_blocks, n_parts, part_w, ncol, bias_col;
-    bool sparse;
+    bool sparse, bt8;
 };
 
 bool tile_geom(const StacrGradArgs &a, TileGeom *g)
@@ -506,49 +688,53 @@ bool tile_geom(const StacrGradArgs &a, TileGeom *g)
     const int cols = a.rank + (a.dbias ? 1 : 0);
     if (cols > 16) return false;
     if ((uintptr_t)a.g % 16) return false;
+    if (a.rows > (int64_t)kMaxBlocks * kTB || a.d_in > kMaxFeat) return false;
+    if ((uint64_t)a.rows * (uint64_t)a.d_in >= (1ull << 32)) return false;  // 32-bit flat indices
+    if ((uint64_t)kTB * (uint64_t)a.d_out * 2 >= (1ull << 31)) return false;  // 32-bit lane offsets
     if (a.nnz > 0 && a.index_bytes != 4 && a.index_bytes != 8) return false;
+    if (a.nnz >= (1ll << 31)) return false;
     g->n_blocks = (int)((a.rows + kTB - 1) / kTB);
     g->n_parts = (int)((a.d_in + kPartMax - 1) / kPartMax);
     g->part_w = (int)((a.d_in + g->n_parts - 1) / g->n_parts);
-    g->ncol = cols <= 8 ? 8 : 16;
+    g->ncol = cols;
     g->bias_col = a.dbias ? a.rank : -1;
     g->sparse = a.nnz > 0;
+    g->bt8 = a.bits != 0;
     return true;
 }
 
-enum { TW_CP, TW_BT, TW_LIGHT, TW_LOFF, TW_HDR, TW_COLMAP, TW_N };
+enum { TW_HIST, TW_BSTART, TW_CP, TW_BT, TW_LIGHT, TW_LOFF, TW_HDR, TW_COLMAP, TW_N };
 
-size_t tile_layout(const StacrGradArgs &a, const TileGeom &g, size_t *off)
+size_t tile_layout(int64_t nnz, int64_t d_in, const TileGeom &g, size_t *off)
 {
     size_t cur = 0;
     auto take = [&](int slot, size_t bytes) { off[slot] = cur; cur += (bytes + 255) & ~(size_t)255; };
     const size_t regions = (size_t)g.n_blocks * g.n_parts;
-    take(TW_CP, (size_t)g.n_blocks * g.ncol * kTB * 2);
-    take(TW_BT, g.sparse ? regions * kNC * kTB * 2 : 0);
-    take(TW_LIGHT, g.sparse ? ((size_t)a.nnz + 3 * regions + 3 + kLightCap) * 4 : 0);
+    // column operands: 4 tiles of int8 codes or 2 tiles of 16-bit values, 32 KiB per region either way
+    const size_t bt_bytes = regions * (size_t)kWaves * 64 * 8 * (g.bt8 ? 4 * 1 : 2 * 2);
+    take(TW_HIST, g.sparse ? (size_t)kChunks * d_in * 4 : 0);
+    take(TW_BSTART, g.sparse ? ((size_t)g.n_blocks + 1) * 4 : 0);
+    take(TW_CP, (size_t)g.n_blocks * kTB * g.ncol * 2);
+    take(TW_BT, g.sparse ? bt_bytes : 0);
+    take(TW_LIGHT, g.sparse ? ((size_t)nnz + 3 * regions + 3 + kLightCap) * 4 : 0);
     take(TW_LOFF, g.sparse ? regions * kOffWords * 4 : 0);
     take(TW_HDR, g.sparse ? regions * sizeof(TileHdr) : 0);
-    take(TW_COLMAP, g.sparse ? (size_t)g.n_parts * kNC * 4 : 0);
+    take(TW_COLMAP, g.sparse ? (size_t)g.n_parts * kNCMax * 4 : 0);
     return cur;
 }
 
-template <typename K>
-void allow_lds(K kernel, size_t bytes, std::once_flag &once)
-{
-    std::call_once(once, [&] {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)bytes);
-    });
-}
-
-template <int DT, int NCOL, bool SP>
+template <int DT, bool SP, bool BT8>
 int launch_tile_grad(const TileArgs &t, int nwg, hipStream_t s)
 {
-    static std::once_flag once;
-    constexpr size_t bytes = TileLds<NCOL, SP>::total;
-    allow_lds(k_tile_grad<DT, NCOL, SP>, bytes, once);
-    stacr_launch("k_dw_fused", s, [&] { k_tile_grad<DT, NCOL, SP><<<nwg, kThreads, bytes, s>>>(t); });
+    stacr_launch("k_dw_fused", s, [&] { k_tile_grad<DT, SP, BT8><<<nwg, kThreads, 0, s>>>(t); });
     return stacr_hip_check(hipGetLastError(), "weight_grad matrix-core kernel");
+}
+
+template <int DT>
+int launch_tile_grad_dt(const TileArgs &t, const TileGeom &g, int nwg, hipStream_t s)
+{
+    if (!g.sparse) return launch_tile_grad<DT, false, true>(t, nwg, s);
+    return g.bt8 ? launch_tile_grad<DT, true, true>(t, nwg, s) : launch_tile_grad<DT, true, false>(t, nwg, s);
 }
 
 }  // namespace
@@ -563,26 +749,22 @@ size_t stacr_tiles_ws(const StacrGradArgs &a)
 {
     TileGeom g;
     size_t off[TW_N];
-    return tile_geom(a, &g) ? tile_layout(a, g, off) : 0;
+    return tile_geom(a, &g) ? tile_layout(a.nnz, a.d_in, g, off) : 0;
 }
 
 size_t stacr_tiles_ws_bound(int64_t rows, int64_t d_out, int64_t d_in, int64_t nnz)
 {
     if (rows < 1 || d_in < 1 || d_out < kOS) return 0;
-    StacrGradArgs a{};
-    a.rows = rows;
-    a.d_out = d_out;
-    a.d_in = d_in;
-    a.nnz = nnz;
     TileGeom g;
     g.n_blocks = (int)((rows + kTB - 1) / kTB);
     g.n_parts = (int)((d_in + kPartMax - 1) / kPartMax);
     g.part_w = (int)((d_in + g.n_parts - 1) / g.n_parts);
-    g.ncol = 16;  // the widest coefficient tile (rank + bias column up to 16)
+    g.ncol = 16;  // the widest coefficient operand (rank + bias column up to 16)
     g.bias_col = -1;
     g.sparse = nnz > 0;
+    g.bt8 = true;  // the two column-operand forms take the same bytes
     size_t off[TW_N];
-    return tile_layout(a, g, off);
+    return tile_layout(nnz, d_in, g, off);
 }
 
 int stacr_tiles_launch(const StacrGradArgs &a)
@@ -590,7 +772,7 @@ int stacr_tiles_launch(const StacrGradArgs &a)
     TileGeom g;
     if (!tile_geom(a, &g)) return stacr_fail(STACR_ERR_UNSUPPORTED, "stacr_weight_grad: matrix-core path not applicable");
     size_t off[TW_N];
-    const size_t need = tile_layout(a, g, off);
+    const size_t need = tile_layout(a.nnz, a.d_in, g, off);
     if (a.workspace_bytes < need)
         return stacr_fail(STACR_ERR_WORKSPACE, "stacr_weight_grad: workspace has %zu bytes, needs %zu", a.workspace_bytes,
                           need);
@@ -622,25 +804,29 @@ int stacr_tiles_launch(const StacrGradArgs &a)
     t.ncol = g.ncol;
     t.bias_col = g.bias_col;
     t.cp = reinterpret_cast<uint16_t *>(ws + off[TW_CP]);
-    t.bt = g.sparse ? reinterpret_cast<uint16_t *>(ws + off[TW_BT]) : nullptr;
-    t.light = g.sparse ? reinterpret_cast<uint32_t *>(ws + off[TW_LIGHT]) : nullptr;
-    t.loff = g.sparse ? reinterpret_cast<uint32_t *>(ws + off[TW_LOFF]) : nullptr;
-    t.hdr = g.sparse ? reinterpret_cast<TileHdr *>(ws + off[TW_HDR]) : nullptr;
-    t.colmap = g.sparse ? reinterpret_cast<int32_t *>(ws + off[TW_COLMAP]) : nullptr;
+    if (g.sparse) {
+        t.hist = reinterpret_cast<uint32_t *>(ws + off[TW_HIST]);
+        t.bstart = reinterpret_cast<uint32_t *>(ws + off[TW_BSTART]);
+        t.bt = ws + off[TW_BT];
+        t.light = reinterpret_cast<uint32_t *>(ws + off[TW_LIGHT]);
+        t.loff = reinterpret_cast<uint32_t *>(ws + off[TW_LOFF]);
+        t.hdr = reinterpret_cast<TileHdr *>(ws + off[TW_HDR]);
+        t.colmap = reinterpret_cast<int32_t *>(ws + off[TW_COLMAP]);
+    }
     t.sparse = g.sparse ? 1 : 0;
     hipStream_t s = a.stream;
+    int rc;
+    if (g.sparse) {
+        stacr_launch("k_dw_count", s, [&] { k_tile_count<<<kChunks, kThreads, 0, s>>>(t); });
+        rc = stacr_hip_check(hipGetLastError(), "weight_grad entry count");
+        if (rc) return rc;
+    }
     const dim3 pgrid((unsigned)g.n_blocks, g.sparse ? (unsigned)g.n_parts : 1u);
-    stacr_launch("k_dw_plan", s, [&] { k_tile_plan<<<pgrid, kThreads, 0, s>>>(t); });
-    int rc = stacr_hip_check(hipGetLastError(), "weight_grad plan");
+    if (g.bt8) stacr_launch("k_dw_plan", s, [&] { k_tile_plan<true><<<pgrid, kThreads, 0, s>>>(t); });
+    else stacr_launch("k_dw_plan", s, [&] { k_tile_plan<false><<<pgrid, kThreads, 0, s>>>(t); });
+    rc = stacr_hip_check(hipGetLastError(), "weight_grad plan");
     if (rc) return rc;
     const int nwg = (int)(a.d_out / kOS) * g.n_parts;
-    const bool bf = a.dtype == STACR_DTYPE_BF16;
-    if (g.sparse) {
-        if (g.ncol == 8)
-            return bf ? launch_tile_grad<STACR_DTYPE_BF16, 8, true>(t, nwg, s) : launch_tile_grad<STACR_DTYPE_F16, 8, true>(t, nwg, s);
-        return bf ? launch_tile_grad<STACR_DTYPE_BF16, 16, true>(t, nwg, s) : launch_tile_grad<STACR_DTYPE_F16, 16, true>(t, nwg, s);
-    }
-    if (g.ncol == 8)
-        return bf ? launch_tile_grad<STACR_DTYPE_BF16, 8, false>(t, nwg, s) : launch_tile_grad<STACR_DTYPE_F16, 8, false>(t, nwg, s);
-    return bf ? launch_tile_grad<STACR_DTYPE_BF16, 16, false>(t, nwg, s) : launch_tile_grad<STACR_DTYPE_F16, 16, false>(t, nwg, s);
+    return a.dtype == STACR_DTYPE_BF16 ? launch_tile_grad_dt<STACR_DTYPE_BF16>(t, g, nwg, s)
+                                       : launch_tile_grad_dt<STACR_DTYPE_F16>(t, g, nwg, s);
 }
