@@ -9,11 +9,12 @@
 //     chunk's count of entries per input feature, and the first entry of every block of 512 token
 //     rows (entries are ascending, so block b starts where the block of the entries changes).
 //   k_tile_plan   one workgroup per (block of 512 rows, input part of <= 1024 features):
-//     * the part's column features: the 64 (32 for 16-bit values) with most entries over the whole
-//       problem, ties to the lowest feature; every workgroup selects the same set;
+//     * the part's column features: the 64 with most entries over the whole problem, ties to the
+//       lowest feature; every workgroup selects the same set;
 //     * the block's column entries as dense matrix-core operands, in the order in which the lanes
-//       of the streaming kernel load them (int8 codes for 4 / 8-bit residuals, else the values in
-//       G's dtype), zero where no entry was selected;
+//       of the streaming kernel load them, zero where no entry was selected: int8 codes for 4 / 8-bit
+//       residuals (converted to G's dtype, exactly, as the streaming kernel loads them), else the
+//       values in G's dtype (rounded as the reference rounds them);
 //     * the block's other ("light") entries of the part as records t | value << 16, grouped by
 //       feature and within a feature by ascending t (each entry's place is its feature's offset
 //       plus the number of that feature's entries in earlier rows, counted from a per-feature row
@@ -43,24 +44,21 @@ constexpr int kOS = 16;              // output features per workgroup
 constexpr int kPartMax = 1024;       // input features per part (one owner thread each)
 constexpr int kThreads = 1024;       // 16 waves
 constexpr int kWaves = kThreads / 64;
-constexpr int kLightCap = 4096;      // light records staged per block (16 KiB); more are read from memory
-constexpr int kOffWords = kPartMax + 1 + 255;  // offsets staged as whole 1 KiB wave copies (5 of them)
+constexpr int kOffWords = kPartMax + 1 + 255;  // a region's offsets, padded to whole 1 KiB (5 of them)
+constexpr int kLightCap = kThreads / 64 * 256;   // light records staged per block (1 KiB per wave); more are read from memory
 constexpr int kChunks = 16;          // entry chunks of the feature count
 constexpr int kMaxFeat = 8192;       // input features the count kernel's LDS histogram holds
 constexpr int kMaxBlocks = 256;      // blocks per problem (rows <= 131072): headers held in LDS
-constexpr int kNCMax = 64;           // column features per part, at most
+constexpr int kBatch = 8;            // entries per thread whose loads the count and the plan issue together
 
 static_assert(kThreads == 2 * kTB, "two G tile rows per lane pair: one 16-byte copy per lane");
-static_assert(kLightCap == kWaves * 256, "one 1 KiB copy of light records per wave");
+static_assert(kOffWords % 256 == 0, "offsets are staged in whole 1 KiB copies");
 
-// column tiles per part: 4 (64 columns) for one-byte integer codes, 2 for 16-bit values
-template <bool BT8> struct Cols {
-    static constexpr int nt = BT8 ? 4 : 2;
-    static constexpr int nc = 16 * nt;
-};
+constexpr int kNT = 4;               // 16-column matrix-core tiles of column entries per part
+constexpr int kNC = 16 * kNT;        // column features per part
 
 struct TileHdr {  // per (block, part)
-    uint32_t light_base;   // first light record (index into the record array)
+    uint32_t light_base;   // the region's first word in the record array (its offsets, then its records)
     uint32_t light_count;  // records
     uint32_t pad[2];
 };
@@ -81,12 +79,18 @@ struct TileArgs {
     uint32_t *bstart;   // [n_blocks + 1] first entry of each block
     uint16_t *cp;       // [n_blocks][16 waves][4 row groups][ncol][8] coefficient operands
     void *bt;           // [n_blocks][n_parts][nt][16 waves][64 lanes][8] column operands
-    uint32_t *light;    // [nnz + 3 regions + 3 + kLightCap] light records
-    uint32_t *loff;     // [n_blocks][n_parts][kOffWords]
+    uint32_t *light;    // regions of kOffWords offsets then light records (see the plan)
     TileHdr *hdr;       // [n_blocks][n_parts]
-    int32_t *colmap;    // [n_parts][kNCMax] feature in the part, or -1
+    int32_t *colmap;    // [n_parts][kNC] feature in the part, or -1
     int sparse;         // nnz > 0: the plan builds the entry structures
 };
+
+// Words of the record array: every region's offsets and records (at most nnz records in all), the
+// alignment slack, and the staging copy's overrun past the last region.
+__host__ __device__ inline uint64_t record_words(int64_t nnz, uint64_t regions)
+{
+    return (uint64_t)nnz + regions * (uint64_t)(kOffWords + 3) + 3 + kLightCap;
+}
 
 __device__ __forceinline__ int64_t flat_at(const void *idx, int idx64, int64_t k)
 {
@@ -111,13 +115,17 @@ __device__ __forceinline__ int entry_code(const TileArgs &a, int64_t e)
     return n > 7 ? n - 16 : n;
 }
 
-// The product operand of entry e in G's dtype: the integer code for bits 4 / 8 (exact), or the
-// stored value rounded to G's dtype for bits 0 (the reference casts the values to G's dtype before
-// its sparse product).
-__device__ __forceinline__ uint32_t entry_g16(const TileArgs &a, int64_t e)
+// The product operand of entry e: the integer code for bits 4 / 8, or the stored value for bits 0.
+__device__ __forceinline__ float entry_value(const TileArgs &a, int64_t e)
 {
-    const float v = a.bits ? (float)entry_code(a, e) : load_any(a.data, a.val_dt, e);
-    return a.g_dt == STACR_DTYPE_BF16 ? f_to_bf16_bits(v) : f_to_f16_bits(v);
+    return a.bits ? (float)entry_code(a, e) : load_any(a.data, a.val_dt, e);
+}
+
+// An operand in G's dtype: exact for the integer codes; a stored value is rounded to G's dtype, as
+// the reference casts the values to G's dtype before its sparse product.
+__device__ __forceinline__ uint32_t to_g16(float v, int g_dt)
+{
+    return g_dt == STACR_DTYPE_BF16 ? f_to_bf16_bits(v) : f_to_f16_bits(v);
 }
 
 template <int DT>
@@ -125,14 +133,6 @@ __device__ __forceinline__ float g16_to_f(uint32_t v)
 {
     if constexpr (DT == STACR_DTYPE_BF16) return bf16_bits_to_f(v);
     else return f16_bits_to_f(v);
-}
-
-// an integer-valued float (|x| <= 256) in G's dtype, exactly
-template <int DT>
-__device__ __forceinline__ uint32_t int_to_g16(float f)
-{
-    if constexpr (DT == STACR_DTYPE_BF16) return __float_as_uint(f) >> 16;
-    else return f_to_f16_bits(f);
 }
 
 // ------------------------------------------------------------------ the entry count
@@ -151,36 +151,76 @@ __global__ __launch_bounds__(kThreads) void k_tile_count(TileArgs a)
         const int64_t b = (int64_t)(t / kTB);
         return b < last_blk ? b : last_blk;
     };
-    for (int64_t e = e0 + tid; e < e1; e += kThreads) {
-        uint32_t t, f;
-        split_flat(flat_at(a.idx, a.idx64, e), d_in, t, f);
-        atomicAdd(&s_h[f], 1u);
-        // every block b with block(e - 1) < b <= block(e) starts at e; past the last entry, nnz
-        const int64_t bcur = block_of(t);
-        int64_t bprev = -1;
-        if (e > 0) {
-            uint32_t tp, fp;
-            split_flat(flat_at(a.idx, a.idx64, e - 1), d_in, tp, fp);
-            bprev = block_of(tp);
+    // kBatch entries per thread per round, their loads issued together
+    for (int64_t r0 = e0; r0 < e1; r0 += kBatch * kThreads) {
+        int64_t cur[kBatch], prev[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int64_t e = r0 + k * kThreads + tid;
+            cur[k] = e < e1 ? flat_at(a.idx, a.idx64, e) : 0;
+            prev[k] = e < e1 && e > 0 ? flat_at(a.idx, a.idx64, e - 1) : 0;
         }
-        for (int64_t b = bprev + 1; b <= bcur; ++b) a.bstart[b] = (uint32_t)e;
-        if (e == a.nnz - 1)
-            for (int64_t b = bcur + 1; b <= a.n_blocks; ++b) a.bstart[b] = (uint32_t)a.nnz;
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int64_t e = r0 + k * kThreads + tid;
+            if (e >= e1) continue;
+            uint32_t t, f;
+            split_flat(cur[k], d_in, t, f);
+            atomicAdd(&s_h[f], 1u);
+            // every block b with block(e - 1) < b <= block(e) starts at e; past the last entry, nnz
+            const int64_t bcur = block_of(t);
+            int64_t bprev = -1;
+            if (e > 0) {
+                uint32_t tp, fp;
+                split_flat(prev[k], d_in, tp, fp);
+                bprev = block_of(tp);
+            }
+            for (int64_t b = bprev + 1; b <= bcur; ++b) a.bstart[b] = (uint32_t)e;
+            if (e == a.nnz - 1)
+                for (int64_t b = bcur + 1; b <= a.n_blocks; ++b) a.bstart[b] = (uint32_t)a.nnz;
+        }
     }
     __syncthreads();
     for (int f = tid; f < (int)d_in; f += kThreads) a.hist[(int64_t)c * d_in + f] = s_h[f];
 }
 
 // ------------------------------------------------------------------ the plan
+// Bitonic sort / merge of one value per lane across a wave, descending in lane order (lane 0 the
+// largest): compare-exchange with the lane at distance j, keeping the larger value in the lane that
+// comes first in the direction of its run.
+__device__ __forceinline__ uint32_t cmpx(uint32_t v, int lane, int j, bool desc)
+{
+    const uint32_t o = (uint32_t)__shfl_xor((int)v, j, 64);
+    const bool first = (lane & j) == 0;
+    const uint32_t hi = v > o ? v : o, lo = v > o ? o : v;
+    return first == desc ? hi : lo;
+}
+
+__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t v, int lane)
+{
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) v = cmpx(v, lane, j, (lane & k) == 0 || k == 64);
+    return v;
+}
+
+// a bitonic sequence across the wave -> descending
+__device__ __forceinline__ uint32_t wave_merge_desc(uint32_t v, int lane)
+{
+#pragma unroll
+    for (int j = 32; j > 0; j >>= 1) v = cmpx(v, lane, j, true);
+    return v;
+}
+
 template <bool BT8>
 __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
 {
-    using CO = Cols<BT8>;
-    using BE = typename std::conditional<BT8, uint8_t, uint16_t>::type;
+    using BE = typename std::conditional<BT8, uint8_t, uint16_t>::type;  // one column-operand element
     __shared__ uint32_t s_key[kPartMax];         // selection keys, then light offsets
     __shared__ int32_t s_slot[kPartMax];         // column slot of each feature of the part, or -1
     __shared__ uint32_t s_mask[kPartMax * 16];   // light rows of each feature (512-bit bitmaps)
-    __shared__ __attribute__((aligned(16))) BE s_bt[CO::nc * kTB];  // the block's column entries [slot][t]
+    __shared__ __attribute__((aligned(16))) BE s_bt[kNC * kTB];  // the block's column entries [slot][t]
     __shared__ uint32_t s_tot[kWaves];
 
     const int b = blockIdx.x, part = blockIdx.y, tid = threadIdx.x;
@@ -194,7 +234,10 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         e_b1 = e_b1 < a.nnz ? e_b1 : a.nnz;
         e_b1 = e_b1 > e_b0 ? e_b1 : e_b0;
 
-        // ---- column features: keys count << 16 | (65535 - f), sorted descending (bitonic)
+        // ---- column features: the nc largest of the unique keys count << 16 | (65535 - f) (count
+        // > 0).  Each wave sorts its 64 keys (descending, in registers); then four rounds merge the
+        // sorted lists pairwise, each keeping the 64 largest of the pair, until one list remains:
+        // its nc-th key is the smallest key taken.  The slots then follow the feature order.
         uint32_t key = 0;
         if (tid < pw) {
             uint32_t cnt = 0;
@@ -202,52 +245,81 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
             for (int c = 0; c < kChunks; ++c) cnt += a.hist[(int64_t)c * a.d_in + plo + tid];
             key = cnt ? ((cnt < 0xffffu ? cnt : 0xffffu) << 16) | (0xffffu - (uint32_t)tid) : 0u;
         }
-        s_key[tid] = key;
         s_slot[tid] = -1;
-        __syncthreads();
-        for (int k = 2; k <= kPartMax; k <<= 1) {
-            for (int j = k >> 1; j > 0; j >>= 1) {
-                const int ixj = tid ^ j;
-                if (ixj > tid) {
-                    const uint32_t x = s_key[tid], y = s_key[ixj];
-                    const bool desc = (tid & k) == 0;
-                    if (desc ? x < y : x > y) {
-                        s_key[tid] = y;
-                        s_key[ixj] = x;
-                    }
-                }
-                __syncthreads();
+        const int lane = tid & 63, wave = tid >> 6;
+        uint32_t v = wave_sort_desc(key, lane);
+        for (int width = kWaves / 2; width >= 1; width /= 2) {
+            // wave w < width merges its list with wave w + width's
+            s_key[tid] = v;
+            __syncthreads();
+            if (wave < width) {
+                // a bitonic sequence holding the 64 largest of both lists: own[i] vs other[63 - i]
+                const uint32_t other = s_key[(wave + width) * 64 + 63 - lane];
+                v = wave_merge_desc(v > other ? v : other, lane);
             }
+            __syncthreads();
         }
-        if (tid < CO::nc) {
-            const uint32_t kk = s_key[tid];
-            const int f = kk ? (int)(0xffffu - (kk & 0xffffu)) : -1;
-            if (f >= 0) s_slot[f] = tid;
-            if (b == 0) a.colmap[part * kNCMax + tid] = f;
+        if (tid < 64) s_key[tid] = v;
+        __syncthreads();
+        // the smallest key taken (0 when fewer than nc features have entries: every nonzero key)
+        const uint32_t kth = s_key[kNC - 1];
+        __syncthreads();
+        uint32_t n_col;
+        const uint32_t slot = block_exclusive_scan<kThreads>(key && key >= kth ? 1u : 0u, s_tot, &n_col);
+        const bool is_col = key && key >= kth && slot < (uint32_t)kNC;  // (the first bound always holds)
+        if (is_col) s_slot[tid] = (int32_t)slot;
+        if (b == 0 && tid < kNC) s_key[tid] = 0xffffffffu;
+        __syncthreads();
+        if (b == 0) {
+            if (is_col) s_key[slot] = (uint32_t)tid;
+            __syncthreads();
+            if (tid < kNC) a.colmap[part * kNC + tid] = tid < kNC ? (int32_t)s_key[tid] : -1;
         }
-        if (b == 0 && tid >= CO::nc && tid < kNCMax) a.colmap[part * kNCMax + tid] = -1;
 
         // ---- this block's entries: the column tile and the light bitmaps
-        for (int i = tid; i < CO::nc * kTB; i += kThreads) s_bt[i] = 0;
+        for (int i = tid; i < kNC * kTB; i += kThreads) s_bt[i] = 0;
         for (int i = tid; i < kPartMax * 16; i += kThreads) s_mask[i] = 0u;
         __syncthreads();
         const int64_t t_base = (int64_t)b * kTB;
         const uint32_t d_in = (uint32_t)a.d_in;
-        uint32_t before_part = 0;  // entries of this block in lower parts: where the part's records start
-        for (int64_t e = e_b0 + tid; e < e_b1; e += kThreads) {
+        // kBatch entries per thread per round, loaded together: flat index and value
+        int64_t fl[kBatch];
+        float val[kBatch];
+        auto load_batch = [&](int64_t r0) {
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                const int64_t e = r0 + k * kThreads + tid;
+                fl[k] = e < e_b1 ? flat_at(a.idx, a.idx64, e) : -1;
+                val[k] = e < e_b1 ? entry_value(a, e) : 0.f;
+            }
+        };
+        // (row in the block, feature in the part) of a loaded entry; false when it lies outside
+        // the block (valid input has no such entry) or, with `in_part`, outside the part
+        auto place = [&](int64_t flat, int &tl, int64_t &f) {
             uint32_t t, fg;
-            split_flat(flat_at(a.idx, a.idx64, e), d_in, t, fg);
-            const int64_t tl64 = (int64_t)t - t_base, f = (int64_t)fg - plo;
-            if (tl64 < 0 || tl64 >= kTB) continue;  // only indices inside the block (valid input has no other)
-            before_part += f < 0;
-            if (f < 0 || f >= pw) continue;
-            const int tl = (int)tl64;
-            const int s = s_slot[f];
-            if (s >= 0) {
-                if constexpr (BT8) s_bt[s * kTB + tl] = (BE)(uint8_t)(int8_t)entry_code(a, e);
-                else s_bt[s * kTB + tl] = (BE)entry_g16(a, e);
-            } else {
-                atomicOr(&s_mask[f * 16 + (tl >> 5)], 1u << (tl & 31));
+            split_flat(flat, d_in, t, fg);
+            const int64_t tl64 = (int64_t)t - t_base;
+            f = (int64_t)fg - plo;
+            tl = (int)tl64;
+            return flat >= 0 && tl64 >= 0 && tl64 < kTB;
+        };
+        uint32_t before_part = 0;  // entries of this block in lower parts: where the part's records start
+        for (int64_t r0 = e_b0; r0 < e_b1; r0 += kBatch * kThreads) {
+            load_batch(r0);
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                int tl;
+                int64_t f;
+                if (!place(fl[k], tl, f)) continue;
+                before_part += f < 0;
+                if (f < 0 || f >= pw) continue;
+                const int s = s_slot[f];
+                if (s >= 0) {
+                    if constexpr (BT8) s_bt[s * kTB + tl] = (BE)(uint8_t)(int8_t)(int)val[k];
+                    else s_bt[s * kTB + tl] = (BE)to_g16(val[k], a.g_dt);
+                } else {
+                    atomicOr(&s_mask[f * 16 + (tl >> 5)], 1u << (tl & 31));
+                }
             }
         }
         __syncthreads();
@@ -261,35 +333,39 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         }
         uint32_t n_light;
         const uint32_t off = block_exclusive_scan<kThreads>(cnt, s_tot, &n_light);
-        uint32_t *loff = a.loff + ((int64_t)b * a.n_parts + part) * kOffWords;
-        if (tid < pw) loff[tid] = off;
-        if (tid == 0) loff[pw] = n_light;  // the part's end (pw may be 1024, past the last thread)
-        // regions are disjoint and ordered by (block, part); shifting region r by 3 r and rounding up
-        // to 4 keeps them disjoint and makes every start 16-byte aligned for the staging copies
+        // the region of (block, part): kOffWords words of offsets (feature f's records start at
+        // word kOffWords + offset[f]; offset[pw] ends them), then the records.  Regions are ordered
+        // by (block, part); region r starts at or after the entries of the earlier regions plus
+        // r (kOffWords + 3) words, rounded up to 4 words: disjoint (a region holds at most its
+        // entries' records) and 16-byte aligned for the staging copies.
         const uint32_t region = (uint32_t)(b * a.n_parts + part);
-        const uint32_t base = ((uint32_t)e_b0 + all_before + 3u * region + 3u) & ~3u;
+        const uint32_t base = ((uint32_t)e_b0 + all_before + region * (uint32_t)(kOffWords + 3) + 3u) & ~3u;
+        uint32_t *reg = a.light + base;
+        if (tid < pw) reg[tid] = off;
+        if (tid == 0) reg[pw] = n_light;  // the part's end (pw may be 1024, past the last thread)
         if (tid == 0) a.hdr[b * a.n_parts + part] = TileHdr{base, n_light, {0u, 0u}};
         s_key[tid] = tid < pw ? off : 0u;
         __syncthreads();
         // each light entry at its feature's offset + the feature's light entries in earlier rows
-        for (int64_t e = e_b0 + tid; e < e_b1; e += kThreads) {
-            uint32_t t, fg;
-            split_flat(flat_at(a.idx, a.idx64, e), d_in, t, fg);
-            const int64_t tl64 = (int64_t)t - t_base, f = (int64_t)fg - plo;
-            if (tl64 < 0 || tl64 >= kTB || f < 0 || f >= pw || s_slot[f] >= 0) continue;
-            const int tl = (int)tl64;
-            uint32_t r = __popc(s_mask[f * 16 + (tl >> 5)] & ((1u << (tl & 31)) - 1u));
-            for (int w = 0; w < (tl >> 5); ++w) r += __popc(s_mask[f * 16 + w]);
-            a.light[base + s_key[f] + r] = (uint32_t)tl | (entry_g16(a, e) << 16);
+        for (int64_t r0 = e_b0; r0 < e_b1; r0 += kBatch * kThreads) {
+            load_batch(r0);
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                int tl;
+                int64_t f;
+                if (!place(fl[k], tl, f) || f < 0 || f >= pw || s_slot[f] >= 0) continue;
+                uint32_t r = __popc(s_mask[f * 16 + (tl >> 5)] & ((1u << (tl & 31)) - 1u));
+                for (int w = 0; w < (tl >> 5); ++w) r += __popc(s_mask[f * 16 + w]);
+                reg[kOffWords + s_key[f] + r] = (uint32_t)tl | (to_g16(val[k], a.g_dt) << 16);
+            }
         }
         // the column operands in lane order: (tile i, wave w, lane l) holds rows 32 w + 8 (l / 16)
         // .. + 7 of column 16 i + l % 16, 8 elements
-        BE *bt = static_cast<BE *>(a.bt) + ((int64_t)b * a.n_parts + part) * CO::nt * kWaves * 64 * 8;
-        for (int u = tid; u < CO::nt * kWaves * 64; u += kThreads) {
+        using BV = typename std::conditional<BT8, uint2, uint4>::type;  // 8 elements
+        BV *bt = static_cast<BV *>(a.bt) + ((int64_t)b * a.n_parts + part) * kNT * kWaves * 64;
+        for (int u = tid; u < kNT * kWaves * 64; u += kThreads) {
             const int l = u & 63, w = (u >> 6) & 15, i = u >> 10;
-            const BE *src = s_bt + (16 * i + (l & 15)) * kTB + 32 * w + 8 * (l >> 4);
-            if constexpr (BT8) *reinterpret_cast<uint2 *>(bt + (int64_t)u * 8) = *reinterpret_cast<const uint2 *>(src);
-            else *reinterpret_cast<uint4 *>(bt + (int64_t)u * 8) = *reinterpret_cast<const uint4 *>(src);
+            bt[u] = *reinterpret_cast<const BV *>(s_bt + (16 * i + (l & 15)) * kTB + 32 * w + 8 * (l >> 4));
         }
     }
 
@@ -378,19 +454,29 @@ __device__ __forceinline__ uint2 load8(__amdgpu_buffer_rsrc_t r, uint32_t voffse
     return make_uint2(v.x, v.y);
 }
 
-// eight int8 codes -> eight 16-bit operands (exact: |code| <= 128)
+// two integer-valued floats (|x| <= 128, exact in either dtype) packed in G's dtype: one packed
+// conversion (v_cvt_pk_bf16_f32 / v_cvt_pkrtz_f16_f32)
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi)
+{
+    if constexpr (DT == STACR_DTYPE_BF16) {
+        typedef __attribute__((ext_vector_type(2))) float f2;
+        typedef __attribute__((ext_vector_type(2))) __bf16 b2;
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, b2));
+    } else {
+        return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+    }
+}
+
+// eight int8 codes -> eight 16-bit operands in G's dtype
 template <int DT>
 __device__ __forceinline__ uint4 codes_to_operand(uint2 w)
 {
-    uint32_t o[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const uint32_t word = k < 2 ? w.x : w.y;
-        const int sh = 16 * (k & 1);
-        const float lo = (float)(int)(int8_t)(word >> sh), hi = (float)(int)(int8_t)(word >> (sh + 8));
-        o[k] = int_to_g16<DT>(lo) | (int_to_g16<DT>(hi) << 16);
-    }
-    return make_uint4(o[0], o[1], o[2], o[3]);
+    auto f = [&](int k) {
+        const uint32_t word = k < 4 ? w.x : w.y;
+        return (float)(int)(int8_t)(word >> (8 * (k & 3)));
+    };
+    return make_uint4(pack2<DT>(f(0), f(1)), pack2<DT>(f(2), f(3)), pack2<DT>(f(4), f(5)), pack2<DT>(f(6), f(7)));
 }
 
 // LDS layout of one stream buffer (byte offsets).  The kernel holds three buffers as three
@@ -399,20 +485,21 @@ __device__ __forceinline__ uint4 codes_to_operand(uint2 w)
 template <bool SP>
 struct TileLds {
     static constexpr size_t g = 0;                                           // [kTB][16] u16
-    static constexpr size_t light = g + (size_t)kTB * kOS * 2;               // [kLightCap] u32
-    static constexpr size_t off = light + (SP ? (size_t)kLightCap * 4 : 0);  // [kOffWords] u32
-    static constexpr size_t size = off + (SP ? (size_t)kOffWords * 4 : 0);
+    static constexpr size_t off = g + (size_t)kTB * kOS * 2;                 // [kOffWords] u32
+    static constexpr size_t light = off + (size_t)kOffWords * 4;             // [kLightCap] u32
+    static constexpr size_t size = SP ? light + (size_t)kLightCap * 4 : off;  // 37 KiB with entries
     static_assert(size % 1024 == 0, "buffers start on 1 KiB boundaries");
     static_assert(3 * size + kMaxBlocks * sizeof(TileHdr) <= 160 * 1024, "fits the CU's LDS");
     static_assert(size >= (size_t)kWaves * 256 * 4, "one tile of every wave fits a buffer (the reduction)");
 };
 
+// Without entries the buffers are small and two workgroups share a CU: 8 waves per SIMD, so
+// <= 64 VGPRs.
 template <int DT, bool SP, bool BT8>
-__global__ __launch_bounds__(kThreads) void k_tile_grad(TileArgs a)
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4 : 8, SP ? 4 : 8))) void k_tile_grad(TileArgs a)
 {
     using L = TileLds<SP>;
-    using CO = Cols<BT8>;
-    constexpr int NT = SP ? CO::nt : 0;
+    constexpr int NT = SP ? kNT : 0;
     using BW = typename std::conditional<BT8, uint2, uint4>::type;  // one lane's column operand
     __shared__ __attribute__((aligned(1024))) unsigned char lds0[L::size];
     __shared__ __attribute__((aligned(1024))) unsigned char lds1[L::size];
@@ -451,20 +538,20 @@ __global__ __launch_bounds__(kThreads) void k_tile_grad(TileArgs a)
     const uint32_t regions = (uint32_t)nb * (uint32_t)a.n_parts;
     const __amdgpu_buffer_rsrc_t r_cp = make_rsrc(a.cp, (uint64_t)nb * kTB * a.ncol * 2);
     // (without entries these three are empty resources that nothing reads)
-    const __amdgpu_buffer_rsrc_t r_light = make_rsrc(a.light, SP ? ((uint64_t)a.nnz + 3ull * regions + 3 + kLightCap) * 4 : 0);
-    const __amdgpu_buffer_rsrc_t r_loff = make_rsrc(a.loff, SP ? (uint64_t)regions * kOffWords * 4 : 0);
+    const __amdgpu_buffer_rsrc_t r_light = make_rsrc(a.light, SP ? record_words(a.nnz, regions) * 4 : 0);
     const __amdgpu_buffer_rsrc_t r_bt = make_rsrc(a.bt, SP ? (uint64_t)regions * NT * kWaves * 64 * sizeof(BW) : 0);
 
     // ---- block `blk`'s copies into buffer B: light records (only the 1 KiB chunks the block has)
     // and offsets, then (issue_g) the G tile (this lane: row 32 wave + lane / 2, outputs 8 (lane & 1) ..)
     auto issue_records = [&](int blk, unsigned char *B) {
         if constexpr (SP) {
+            // the region's offsets (1 KiB copies by waves 0..4, as far as the part needs) and the
+            // 1 KiB chunks of records the block has
             const uint32_t lbase = __builtin_amdgcn_readfirstlane(s_hdr[blk].light_base);
             const uint32_t lcount = __builtin_amdgcn_readfirstlane(s_hdr[blk].light_count);
-            if (256u * (uint32_t)wave < lcount) copy16(r_light, B + L::light + (size_t)wave * 1024, rec_lane, lbase * 4);
-            if (wave < 5 && 256 * wave <= pw)
-                copy16(r_loff, B + L::off + (size_t)wave * 1024, rec_lane,
-                       ((uint32_t)blk * a.n_parts + part) * (uint32_t)kOffWords * 4);
+            if (wave < kOffWords / 256 && 256 * wave <= pw) copy16(r_light, B + L::off + (size_t)wave * 1024, rec_lane, lbase * 4);
+            if (256u * (uint32_t)wave < lcount)
+                copy16(r_light, B + L::light + (size_t)wave * 1024, rec_lane, (lbase + kOffWords) * 4);
         }
     };
     auto issue_g = [&](int blk, unsigned char *B) {
@@ -518,10 +605,8 @@ __global__ __launch_bounds__(kThreads) void k_tile_grad(TileArgs a)
         if constexpr (SP) {
 #pragma unroll
             for (int i = 0; i < NT; ++i) {
-                uint4 bv;
-                if constexpr (BT8) bv = codes_to_operand<DT>(r.t[i]);
-                else bv = r.t[i];
-                acc_t[i] = mfma16<DT>(av, bv, acc_t[i]);
+                if constexpr (BT8) acc_t[i] = mfma16<DT>(av, codes_to_operand<DT>(r.t[i]), acc_t[i]);
+                else acc_t[i] = mfma16<DT>(av, r.t[i], acc_t[i]);
             }
         }
     };
@@ -539,10 +624,8 @@ __global__ __launch_bounds__(kThreads) void k_tile_grad(TileArgs a)
                 const uint32_t k0 = off[tid] < k1 ? off[tid] : k1;
                 // s[2 k] += lo(w_k) v and s[2 k + 1] += hi(w_k) v for the row's eight 32-bit words
                 // w_k: dot products with the pairs (v, 0) and (0, v), no conversions
-                auto add_entry = [&](uint32_t rec) {
+                auto add_row = [&](uint32_t rec, uint4 w0, uint4 w1) {
                     const uint32_t v_lo = rec >> 16, v_hi = rec & 0xffff0000u;
-                    const uint4 *row = reinterpret_cast<const uint4 *>(gt + (rec & 511u) * kOS);
-                    const uint4 w0 = row[0], w1 = row[1];
                     const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
                     for (int o = 0; o < 8; ++o) {
@@ -550,19 +633,33 @@ __global__ __launch_bounds__(kThreads) void k_tile_grad(TileArgs a)
                         s[2 * o + 1] = dot2<DT>(w[o], v_hi, s[2 * o + 1]);
                     }
                 };
-                // records staged in LDS, then (blocks with more than kLightCap) the rest from memory
+                auto row_of = [&](uint32_t rec) { return reinterpret_cast<const uint4 *>(gt + (rec & 511u) * kOS); };
+                auto add_entry = [&](uint32_t rec) {
+                    const uint4 *row = row_of(rec);
+                    add_row(rec, row[0], row[1]);
+                };
+                // records staged in LDS, two at a time (both rows read before either is summed, in
+                // record order), then (blocks with more than kLightCap) the rest from memory
                 const uint32_t kl = k1 < (uint32_t)kLightCap ? k1 : (uint32_t)kLightCap;
-                for (uint32_t k = k0; k < kl; ++k) add_entry(lrec[k]);
-                for (uint32_t k = k0 > kl ? k0 : kl; k < k1; ++k) add_entry(a.light[h.light_base + k]);
+                uint32_t k = k0;
+                for (; k + 1 < kl; k += 2) {
+                    const uint32_t ra = lrec[k], rb = lrec[k + 1];
+                    const uint4 *pa = row_of(ra), *pb = row_of(rb);
+                    const uint4 a0 = pa[0], a1 = pa[1], b0 = pb[0], b1 = pb[1];
+                    add_row(ra, a0, a1);
+                    add_row(rb, b0, b1);
+                }
+                if (k < kl) add_entry(lrec[k]);
+                for (uint32_t k = k0 > kl ? k0 : kl; k < k1; ++k) add_entry(a.light[h.light_base + kOffWords + k]);
             }
         }
     };
 
     // ---- the stream: block blk runs in buffer blk % 3 while block blk + 2 is copied into
     // buffer (blk + 2) % 3.  A step: the products of block blk (its operands then die), the operand
-    // loads of block blk + 1, the copies of block blk + 2 (the G copy last), the light entries of
-    // block blk; then a wait that lets only the last memory instruction (that G copy) stay in
-    // flight across the barrier.
+    // loads of block blk + 1, the copies of block blk + 2, the light entries of block blk, then
+    // (issue_g) the G copy of block blk + 2; then a wait that lets only that last memory
+    // instruction stay in flight across the barrier.
     Ops ops;
     load_ops(0, ops);
     issue_records(0, lds0);
@@ -575,24 +672,38 @@ __global__ __launch_bounds__(kThreads) void k_tile_grad(TileArgs a)
     __syncthreads();
     auto step = [&](int blk, const unsigned char *__restrict__ B, unsigned char *__restrict__ B2) {
         products(B, ops);
-        if (blk + 1 < nb) load_ops(blk + 1, ops);
+        load_ops(blk + 1, ops);
         if (blk + 2 < nb) issue_records(blk + 2, B2);
-        // every step ends its memory instructions with one G copy, so that the wait below always
-        // covers the operand loads; in the last two steps it copies the last block again into the
-        // buffer of block blk - 1, which nothing reads any more
-        issue_g(blk + 2 < nb ? blk + 2 : nb - 1, B2);
         light_entries(blk, B);
+        // every step ends its memory instructions with one G copy, so that the wait below always
+        // covers the operand loads; in the step before last it copies the last block again into
+        // the buffer of block blk - 1, which nothing reads any more
+        issue_g(blk + 2 < nb ? blk + 2 : nb - 1, B2);
         // vmcnt(1) lgkmcnt(0) (expcnt unconstrained), as a builtin so that the compiler knows the
         // operand loads have landed; then the barrier, not __syncthreads(), whose fence would wait
         // for every copy in flight
         __builtin_amdgcn_s_waitcnt(0x0071);
         asm volatile("s_barrier" ::: "memory");
     };
-    for (int blk = 0, cb = 0; blk < nb; ++blk, cb = cb == 2 ? 0 : cb + 1) {
+    // every block but the last through `step` (the last loads nothing more)
+    int cb = 0;
+    for (int blk = 0; blk + 1 < nb; ++blk, cb = cb == 2 ? 0 : cb + 1) {
         unsigned char *B = cb == 0 ? lds0 : cb == 1 ? lds1 : lds2;
         unsigned char *B2 = cb == 0 ? lds2 : cb == 1 ? lds0 : lds1;
         step(blk, B, B2);
     }
+    {
+        const unsigned char *B = cb == 0 ? lds0 : cb == 1 ? lds1 : lds2;
+        products(B, ops);
+        light_entries(nb - 1, B);
+    }
+
+    // ---- what the epilogue reads from memory, loaded before the reduction hides the latency: the
+    // scale (it exists only with residual entries; without them the sparse sums are zero) and the
+    // part's column map
+    const uint16_t *q = static_cast<const uint16_t *>(a.q);
+    const float scale = SP && a.bits ? *a.scale : 1.f;
+    const int colf = SP && tid < kNC ? a.colmap[part * kNC + tid] : -1;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
@@ -600,6 +711,7 @@ __global__ __launch_bounds__(kThreads) void k_tile_grad(TileArgs a)
     // the sums and the part's column slots in lds1
     constexpr int NTILE = 1 + NT;
     static_assert(!SP || NTILE * 256 * 4 + kPartMax * 4 <= L::size, "sums and slots fit a buffer");
+    static_assert(!SP || (size_t)kPartMax * 15 * 2 <= L::size / 2 * 2, "a part's Q rows fit a buffer");
     float *stage = reinterpret_cast<float *>(lds0);
     float *fin = reinterpret_cast<float *>(lds1);                         // [NTILE][o][j]
     int32_t *slots = reinterpret_cast<int32_t *>(lds1 + NTILE * 256 * 4);  // [pw]
@@ -620,30 +732,32 @@ __global__ __launch_bounds__(kThreads) void k_tile_grad(TileArgs a)
     if constexpr (SP) {
         if (tid < pw) slots[tid] = -1;
         __syncthreads();
-        if (tid < CO::nc) {
-            const int f = a.colmap[part * kNCMax + tid];
-            if (f >= 0 && f < pw) slots[f] = tid;
-        }
+        if (colf >= 0 && colf < pw) slots[colf] = tid;
         __syncthreads();
     }
 
-    // ---- dW tile: M Q^T + scale (light + column sums), one rounding; dbias from M[:, bias_col]
-    // the scale exists only with residual entries (the C ABI checks it then); without them the
-    // sparse sums are zero and no scale is read
-    const float scale = SP && a.bits ? *a.scale : 1.f;
-    if (tid < pw) {
-        const int64_t i = plo + tid;
-        const uint16_t *q = static_cast<const uint16_t *>(a.q);
-        const int slot = SP ? slots[tid] : -1;
+    // ---- dW tile: M Q^T + scale (light + column sums), one rounding; dbias from M[:, bias_col].
+    // With entries a part has <= 1024 features, one per thread; without, the threads loop over the
+    // features.  The Q rows of a chunk of features are first copied to LDS (lds2, unused now).
+    const int qchunk = (int)((L::size / 2) / (size_t)a.rank) < kThreads ? (int)((L::size / 2) / (size_t)a.rank) : kThreads;
+    uint16_t *sq = reinterpret_cast<uint16_t *>(lds2);
+    for (int c0 = 0; c0 < pw; c0 += qchunk) {
+        const int nf = pw - c0 < qchunk ? pw - c0 : qchunk;
+        __syncthreads();  // the previous chunk's Q rows are no longer read
+        for (int e = tid; e < nf * a.rank; e += kThreads) sq[e] = q[(plo + c0) * a.rank + e];
+        __syncthreads();
+        for (int fl = c0 + tid; fl < c0 + nf; fl += kThreads) {
+        const int64_t i = plo + fl;
+        const int slot = SP ? slots[fl] : -1;
         float out[kOS];
 #pragma unroll
         for (int o = 0; o < kOS; ++o) {
             const float col = slot >= 0 ? fin[(1 + (slot >> 4)) * 256 + o * 16 + (slot & 15)] : 0.f;
-            out[o] = scale * (s[o] + col);
+            out[o] = SP ? scale * (s[o] + col) : 0.f;
         }
-        // + sum_j M[o][j] Q[i][j], one rank column at a time (the M reads are LDS broadcasts)
+        // + sum_j M[o][j] Q[i][j] (the M reads are LDS broadcasts)
         for (int j = 0; j < a.rank; ++j) {
-            const float qj = g16_to_f<DT>(q[i * a.rank + j]);
+            const float qj = g16_to_f<DT>(sq[(fl - c0) * a.rank + j]);
 #pragma unroll
             for (int o = 0; o < kOS; ++o) out[o] = fmaf(fin[o * 16 + j], qj, out[o]);
         }
@@ -666,6 +780,7 @@ __global__ __launch_bounds__(kThreads) void k_tile_grad(TileArgs a)
         } else {  // nn.Linear: dW is d_out x d_in; consecutive threads write consecutive features
 #pragma unroll
             for (int o = 0; o < kOS; ++o) store_any(a.dw, a.dw_dt, (o0 + o) * a.d_in + i, out[o]);
+        }
         }
     }
     if (a.dbias && part == 0 && tid < kOS) store_any(a.dbias, a.db_dt, o0 + tid, fin[tid * 16 + a.bias_col]);
@@ -694,7 +809,8 @@ bool tile_geom(const StacrGradArgs &a, TileGeom *g)
     if (a.nnz > 0 && a.index_bytes != 4 && a.index_bytes != 8) return false;
     if (a.nnz >= (1ll << 31)) return false;
     g->n_blocks = (int)((a.rows + kTB - 1) / kTB);
-    g->n_parts = (int)((a.d_in + kPartMax - 1) / kPartMax);
+    // with entries, parts of <= 1024 features (one owner thread each); without, one part
+    g->n_parts = a.nnz > 0 ? (int)((a.d_in + kPartMax - 1) / kPartMax) : 1;
     g->part_w = (int)((a.d_in + g->n_parts - 1) / g->n_parts);
     g->ncol = cols;
     g->bias_col = a.dbias ? a.rank : -1;
@@ -703,23 +819,22 @@ bool tile_geom(const StacrGradArgs &a, TileGeom *g)
     return true;
 }
 
-enum { TW_HIST, TW_BSTART, TW_CP, TW_BT, TW_LIGHT, TW_LOFF, TW_HDR, TW_COLMAP, TW_N };
+enum { TW_HIST, TW_BSTART, TW_CP, TW_BT, TW_LIGHT, TW_HDR, TW_COLMAP, TW_N };
 
 size_t tile_layout(int64_t nnz, int64_t d_in, const TileGeom &g, size_t *off)
 {
     size_t cur = 0;
     auto take = [&](int slot, size_t bytes) { off[slot] = cur; cur += (bytes + 255) & ~(size_t)255; };
     const size_t regions = (size_t)g.n_blocks * g.n_parts;
-    // column operands: 4 tiles of int8 codes or 2 tiles of 16-bit values, 32 KiB per region either way
-    const size_t bt_bytes = regions * (size_t)kWaves * 64 * 8 * (g.bt8 ? 4 * 1 : 2 * 2);
+    // column operands: kNT tiles of int8 codes (32 KiB per region) or 16-bit values (64 KiB)
+    const size_t bt_bytes = regions * (size_t)kNT * kWaves * 64 * (g.bt8 ? 8 : 16);
     take(TW_HIST, g.sparse ? (size_t)kChunks * d_in * 4 : 0);
     take(TW_BSTART, g.sparse ? ((size_t)g.n_blocks + 1) * 4 : 0);
     take(TW_CP, (size_t)g.n_blocks * kTB * g.ncol * 2);
     take(TW_BT, g.sparse ? bt_bytes : 0);
-    take(TW_LIGHT, g.sparse ? ((size_t)nnz + 3 * regions + 3 + kLightCap) * 4 : 0);
-    take(TW_LOFF, g.sparse ? regions * kOffWords * 4 : 0);
+    take(TW_LIGHT, g.sparse ? (size_t)record_words(nnz, regions) * 4 : 0);
     take(TW_HDR, g.sparse ? regions * sizeof(TileHdr) : 0);
-    take(TW_COLMAP, g.sparse ? (size_t)g.n_parts * kNCMax * 4 : 0);
+    take(TW_COLMAP, g.sparse ? (size_t)g.n_parts * kNC * 4 : 0);
     return cur;
 }
 
@@ -757,12 +872,12 @@ size_t stacr_tiles_ws_bound(int64_t rows, int64_t d_out, int64_t d_in, int64_t n
     if (rows < 1 || d_in < 1 || d_out < kOS) return 0;
     TileGeom g;
     g.n_blocks = (int)((rows + kTB - 1) / kTB);
-    g.n_parts = (int)((d_in + kPartMax - 1) / kPartMax);
+    g.n_parts = nnz > 0 ? (int)((d_in + kPartMax - 1) / kPartMax) : 1;
     g.part_w = (int)((d_in + g.n_parts - 1) / g.n_parts);
     g.ncol = 16;  // the widest coefficient operand (rank + bias column up to 16)
     g.bias_col = -1;
     g.sparse = nnz > 0;
-    g.bt8 = true;  // the two column-operand forms take the same bytes
+    g.bt8 = false;  // the wider column-operand form
     size_t off[TW_N];
     return tile_layout(nnz, d_in, g, off);
 }
@@ -809,7 +924,6 @@ int stacr_tiles_launch(const StacrGradArgs &a)
         t.bstart = reinterpret_cast<uint32_t *>(ws + off[TW_BSTART]);
         t.bt = ws + off[TW_BT];
         t.light = reinterpret_cast<uint32_t *>(ws + off[TW_LIGHT]);
-        t.loff = reinterpret_cast<uint32_t *>(ws + off[TW_LOFF]);
         t.hdr = reinterpret_cast<TileHdr *>(ws + off[TW_HDR]);
         t.colmap = reinterpret_cast<int32_t *>(ws + off[TW_COLMAP]);
     }
