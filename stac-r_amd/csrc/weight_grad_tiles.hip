@@ -326,13 +326,13 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         uint32_t all_before;
         (void)block_exclusive_scan<kThreads>(before_part, s_tot, &all_before);
         // light count of each feature, their offsets
-        uint32_t cnt = 0;
+        uint32_t lcnt = 0;
         if (tid < pw) {
 #pragma unroll
-            for (int w = 0; w < 16; ++w) cnt += __popc(s_mask[tid * 16 + w]);
+            for (int w = 0; w < 16; ++w) lcnt += __popc(s_mask[tid * 16 + w]);
         }
         uint32_t n_light;
-        const uint32_t off = block_exclusive_scan<kThreads>(cnt, s_tot, &n_light);
+        const uint32_t off = block_exclusive_scan<kThreads>(lcnt, s_tot, &n_light);
         // the region of (block, part): kOffWords words of offsets (feature f's records start at
         // word kOffWords + offset[f]; offset[pw] ends them), then the records.  Regions are ordered
         // by (block, part); region r starts at or after the entries of the earlier regions plus
@@ -347,8 +347,10 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         s_key[tid] = tid < pw ? off : 0u;
         __syncthreads();
         // each light entry at its feature's offset + the feature's light entries in earlier rows
+        // (a block whose entries fit one round keeps them in registers from the first pass)
+        const bool one_round = e_b1 - e_b0 <= (int64_t)kBatch * kThreads;
         for (int64_t r0 = e_b0; r0 < e_b1; r0 += kBatch * kThreads) {
-            load_batch(r0);
+            if (!one_round) load_batch(r0);
 #pragma unroll
             for (int k = 0; k < kBatch; ++k) {
                 int tl;
