@@ -581,41 +581,6 @@ __device__ __forceinline__ uint4 pack_raw(const float (&v)[V])
     return make_uint4(u[0], u[1], u[2], u[3]);
 }
 
-// Sum 64 values (v = i * R + j) over the 64 lanes of a wave: six halving exchanges leave lane l
-// with the wave's total of value l.
-__device__ __forceinline__ float wave_reduce_scatter64(float (&a)[64])
-{
-    const int lane = threadIdx.x & 63;
-    // Stages 32 and 16 in the VALU: v_permlane32_swap(x, y) gives lanes 0..31 (x[l], x[l + 32])
-    // and lanes 32..63 (y[l - 32], y[l]); v_permlane16_swap does the same between even and odd
-    // 16-lane rows (checked on the GPU).  With x the lower half and y the upper, the sum of the
-    // pair is, in every lane, the total of the half that lane keeps (lane bit clear: lower).
-#pragma unroll
-    for (int k = 0; k < 32; ++k) {
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[k]), __float_as_uint(a[k + 32]), false, false);
-        a[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[k]), __float_as_uint(a[k + 16]), false, false);
-        a[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-    // stages 8, 4, 2, 1: both halves cross (the select then picks between computed sums, never
-    // between array elements, which keeps a[] in registers)
-#pragma unroll
-    for (int st = 2; st < 6; ++st) {
-        const int o = 32 >> st;
-        const bool upper = (lane & o) != 0;
-#pragma unroll
-        for (int k = 0; k < o; ++k) {
-            const float lo = a[k] + __shfl_xor(a[k], o, 64);
-            const float hi = a[k + o] + __shfl_xor(a[k + o], o, 64);
-            a[k] = upper ? hi : lo;
-        }
-    }
-    return a[0];
-}
-
 // Coefficients of the NB rows of a batch for this thread's slot, as the activation dtype rounds
 // them.  Pass 1 computes them (acc holds the thread's partial sums, flattened i * R + j) and
 // writes them to `coeff`; the later passes load them.  s_c holds [slot][64] floats.

@@ -31,6 +31,12 @@ OJA_CASES = [
     ("rank32_few_rows", 3, 40, 32, "f32", "random"),
     ("rank1_many_rows", 70000, 64, 1, "bf16", "random"),
     ("empty_batch", 0, 64, 4, "bf16", "random"),
+    # one-pass path: 16-bit X, d in {512, 1024, 2048}, rank <= 8
+    ("onepass_cfg3_c_fc_rank8", 8192, 1024, 8, "bf16", "random"),
+    ("onepass_aligned_rank8", 8192, 1024, 8, "bf16", "aligned"),
+    ("onepass_d512_f16_ragged_rows", 1001, 512, 5, "f16", "random"),
+    ("onepass_d2048_rank1", 300, 2048, 1, "bf16", "random"),
+    ("onepass_fewer_rows_than_a_batch", 3, 1024, 8, "bf16", "random"),
 ]
 
 
