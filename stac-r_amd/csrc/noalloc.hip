@@ -1,11 +1,12 @@
 // stacr_weight_grad_noalloc: stacr_weight_grad for callers that cannot allocate device memory
 // (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
-// backward's plan workspace (bucketed entries, pieces, round and block headers) lives in a
+// backward's plan workspace (entry counts, matrix-core operands, light-entry records and block
+// headers; or, for the general kernels, bucketed entries, pieces and round headers) lives in a
 // file-scope device array instead of a caller buffer.  Each GPU the library runs on holds its own
 // copy of the array until the process ends; the address of a device's copy is looked up once, on
 // the entry point's first call with that device current, and every later call on the device
 // reuses it.  Calls that overlap on one GPU share that scratch and race; nothing in it needs to
-// start at zero (the plan kernel writes every word the weight-gradient kernel reads).
+// start at zero (the count and plan kernels write every word the weight-gradient kernel uses).
 #include <mutex>
 
 #include "internal.h"

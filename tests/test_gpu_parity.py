@@ -345,6 +345,26 @@ def test_weight_grad_int64_indices(dev):
     assert rel_l2(_np(a), _np(b)) <= 1e-6
 
 
+@pytest.mark.parametrize("dtype,transposed", [("bf16", True), ("f16", False)])
+def test_weight_grad_matrix_core_path_is_deterministic(dev, dtype, transposed):
+    """16-bit G at rank 8: every sum of the weight gradient has a fixed order (light entries by one
+    owner thread in ascending row order, per-wave tiles reduced in wave order), so repeated calls
+    agree bit for bit, with int32 and int64 indices alike."""
+    from stacr_amd import kernels
+
+    announce("grad determinism", dtype, transposed)
+    rows, d_in, d_out, rank = 4096, 1024, 1024, 8
+    x = make_activation(rows, d_in, lognormal=True).to(dev, DT[dtype])
+    q = make_basis(d_in, rank).to(dev, DT[dtype])
+    g = make_grad(rows, d_out).to(dev, DT[dtype])
+    coeff, idx, data, scale = kernels.save(x, q, mode="global_topk", budget=0.005, chunk_rows=512, bits=8)
+    first = kernels.weight_grad(g, coeff, q, (idx, data, scale), 8, transposed, DT[dtype], DT[dtype])
+    for ix in (idx, idx.long(), idx):
+        again = kernels.weight_grad(g, coeff, q, (ix, data, scale), 8, transposed, DT[dtype], DT[dtype])
+        assert torch.equal(again[0], first[0])
+        assert torch.equal(again[1], first[1])
+
+
 # ------------------------------------------------------------------ the drop-in layer on the GPU
 def _lowrank(rows, feats, rank, seed=0):
     g = torch.Generator().manual_seed(seed)
