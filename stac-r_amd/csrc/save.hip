@@ -953,6 +953,137 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg,
     }
 }
 
+// Pass 1 for 16-bit rows wider than one vector per thread (d up to MV * 2048): the workgroup's 256
+// threads share each row, thread u holding the MV vectors at columns (m * 256 + u) * 8, and the
+// basis stays as packed 16-bit words (the projection's v_dot2 operands; the residual widens them
+// per vector).  The workgroup's rows are one batch of 64 / R rows.  Outputs as k_proj_hist_b with
+// the residual stored: coefficients, the residual (exact in the activation dtype), the level-0
+// histogram with its coarse sums, and the max key.  The later passes read the stored residual as
+// a matrix of MV * rows rows of d / MV columns: the same memory, the same flat indices.
+template <int DT, int R, int MV>
+__global__ __launch_bounds__(kBlock) void k_proj_hist_w(SaveGeom g, int c_vec, const typename Act<DT>::T *__restrict__ x,
+                                                        const float *__restrict__ qp, typename Act<DT>::T *__restrict__ coeff,
+                                                        uint32_t *__restrict__ hist, uint32_t *__restrict__ maxkey,
+                                                        int do_hist, const typename Act<DT>::T *__restrict__ coeff_in,
+                                                        typename Act<DT>::T *__restrict__ rout, uint32_t *__restrict__ coarse)
+{
+    using T = typename Act<DT>::T;
+    static_assert(sizeof(T) == 2, "16-bit activations");
+    constexpr int V = 8, NB = Batch<R>::NB;
+    __shared__ uint32_t s_hist[kBins];
+    __shared__ __align__(16) float s_part[kWaves * 64];
+    __shared__ __align__(16) float s_c[kWaves * 64];
+    __shared__ uint32_t s_wmax[kWaves];
+    int64_t chunk, row0, row_end;
+    wg_rows(g, blockIdx.x, chunk, row0, row_end);
+    if (row0 >= row_end) return;  // a trailing workgroup with no rows (uniform)
+    const int u = threadIdx.x;
+    int64_t col[MV], colc[MV];
+    bool col_ok[MV];
+#pragma unroll
+    for (int m = 0; m < MV; ++m) {
+        col[m] = (int64_t)(m * kBlock + u) * V;
+        colc[m] = min(col[m], g.d - V);
+        col_ok[m] = col[m] < g.d;
+    }
+    // every load issued before any is used: X rows clamped into the workgroup's range, columns
+    // clamped into the row (values outside are zeroed where used)
+    int64_t rows[NB];
+    uint4 raw[NB][MV];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        rows[i] = row0 + i;
+        const T *src = x + min(rows[i], row_end - 1) * g.d;
+#pragma unroll
+        for (int m = 0; m < MV; ++m) raw[i][m] = *reinterpret_cast<const uint4 *>(src + colc[m]);
+    }
+    const T *qph = reinterpret_cast<const T *>(qp + 2 * g.d * R);  // [R][d] in the activation dtype
+    uint4 qw[MV][R];
+#pragma unroll
+    for (int m = 0; m < MV; ++m)
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const uint4 w = *reinterpret_cast<const uint4 *>(qph + j * g.d + colc[m]);
+            qw[m][j] = col_ok[m] ? w : make_uint4(0u, 0u, 0u, 0u);
+        }
+    for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
+    uint32_t kmax = 0u;
+    __syncthreads();
+    float c[64];
+    if (coeff_in) {
+        batch_coeff_load<DT, R>(coeff_in, g.rank, rows, row_end, c_vec != 0, c);
+    } else {
+        float acc[64];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const bool row_ok = rows[i] < row_end;
+#pragma unroll
+            for (int j = 0; j < R; ++j) acc[i * R + j] = 0.f;
+#pragma unroll
+            for (int m = 0; m < MV; ++m) {
+                const uint4 xr = row_ok && col_ok[m] ? raw[i][m] : make_uint4(0u, 0u, 0u, 0u);
+                const uint32_t xw[4] = {xr.x, xr.y, xr.z, xr.w};
+#pragma unroll
+                for (int j = 0; j < R; ++j) {
+                    const uint32_t w[4] = {qw[m][j].x, qw[m][j].y, qw[m][j].z, qw[m][j].w};
+                    float s = acc[i * R + j];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) s = dot2<DT>(xw[k], w[k], s);
+                    acc[i * R + j] = s;
+                }
+            }
+        }
+        // the workgroup's 4 waves are one row slot: rows row0 + i, i < NB
+        batch_coeff_from_acc<DT, R>(acc, kWaves, 0, s_part, s_c, row0, 1, row_end, g.rank, coeff, c);
+    }
+    if (!do_hist) return;
+#pragma unroll
+    for (int m = 0; m < MV; ++m) {
+        if (!col_ok[m]) continue;
+        float q[V][R];  // this vector's basis values, widened
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const uint32_t w[4] = {qw[m][j].x, qw[m][j].y, qw[m][j].z, qw[m][j].w};
+#pragma unroll
+            for (int e = 0; e < V; ++e) q[e][j] = Act<DT>::ld((T)((w[e / 2] >> (16 * (e & 1))) & 0xffffu));
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            if (rows[i] >= row_end) continue;
+            float xv[V], r[V];
+            unpack_raw<DT, V>(raw[i][m], xv);
+            batch_residual<DT, R, V>(xv, c + i * R, q, r);
+            *reinterpret_cast<uint4 *>(rout + rows[i] * g.d + col[m]) = pack_raw<DT, V>(r);
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
+                atomicAdd(&s_hist[key >> kDigitShift[0]], 1u);
+                kmax = max(kmax, key);
+            }
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, off, 64));
+    if ((threadIdx.x & 63) == 0) s_wmax[threadIdx.x >> 6] = kmax;
+    __syncthreads();
+    const int copy = (int)(blockIdx.x % g.hcopies);
+    uint32_t *gh = hist + ((chunk * 3 + 0) * g.hcopies + copy) * kBins;
+    for (int b = threadIdx.x; b < kBins; b += kBlock)
+        if (s_hist[b]) atomicAdd(&gh[b], s_hist[b]);
+    if (threadIdx.x < kCoarse) {
+        uint32_t sum = 0u;
+#pragma unroll 8
+        for (int b = 0; b < kBins / kCoarse; ++b) sum += s_hist[threadIdx.x * (kBins / kCoarse) + b];
+        if (sum) atomicAdd(&coarse[(chunk * g.hcopies + copy) * kCoarse + threadIdx.x], sum);
+    }
+    if (threadIdx.x == 0) {
+        uint32_t mx = 0u;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) mx = max(mx, s_wmax[w]);
+        if (mx) atomicMax(maxkey + copy * kMaxKeyStride, mx);
+    }
+}
+
 // The level-0 selection from the coarse histogram (64 bins of 32) and then the chosen coarse bin's
 // 32 histogram bins, each summed over the HC copies, made by every wave on its own with suffix
 // sums across lanes and a ballot (no barrier): the same bin and need as block_select at level 0.
@@ -1554,11 +1685,18 @@ struct Plan {
     bool fast;  // the batched kernels (one batch per workgroup)
     bool fold;  // bf16 on the batched path: the emission pass ends the selection (no count pass)
     int64_t n_wgs;
+    // wide rows (16-bit, d / kWideMv <= 2048): g, V, fast and n_wgs describe the stored residual as
+    // kWideMv * rows rows of d / kWideMv columns (the later passes); gw and n_wgs_w the projection pass
+    bool wide;
+    SaveGeom gw;
+    int64_t n_wgs_w;
     bool trim;
     int64_t n_list_blocks;
 };
 
-Plan make_plan(const StacrSaveArgs &a)
+constexpr int kWideMv = 2;  // vectors per thread per row in the wide projection pass
+
+Plan make_plan_rows(const StacrSaveArgs &a)
 {
     Plan p{};
     const int vec = a.dtype == STACR_DTYPE_F32 ? 4 : 8;
@@ -1597,6 +1735,45 @@ Plan make_plan(const StacrSaveArgs &a)
     return p;
 }
 
+// 16-bit rows of 2048 < d <= 4096 features (d % 16 == 0, aligned, rank <= 8) are too wide for one
+// vector per thread.  Their projection pass (k_proj_hist_w) gives each thread two vectors of a row
+// and stores the residual; the later passes run on the batched kernels over that residual viewed as
+// 2 * rows rows of d / 2 columns (row-major, so the flat indices are the same; chunks are 2 *
+// chunk_rows such rows, so the chunks are the same).
+Plan make_plan(const StacrSaveArgs &a)
+{
+    Plan p = make_plan_rows(a);
+    if (p.fast || a.dtype == STACR_DTYPE_F32 || p.V != 8 || p.R > 8 || a.feats <= 2048 ||
+        a.feats > 2048 * kWideMv || a.feats % (8 * kWideMv) != 0)
+        return p;
+    StacrSaveArgs av = a;
+    av.feats = a.feats / kWideMv;
+    av.rows = a.rows * kWideMv;
+    av.chunk_rows = a.chunk_rows * kWideMv;
+    Plan pv = make_plan_rows(av);
+    if (!pv.fast) return p;
+    SaveGeom &gw = pv.gw;
+    gw.rows = a.rows;
+    gw.d = a.feats;
+    gw.rank = a.rank;
+    gw.L = kBlock;
+    gw.log2L = ilog2(kBlock);
+    gw.rpi = 1;
+    gw.mv = kWideMv;
+    gw.chunk_rows = a.mode == STACR_MODE_GLOBAL_TOPK ? a.rows : min(a.chunk_rows, a.rows);
+    if (gw.chunk_rows < 1) gw.chunk_rows = 1;
+    gw.n_chunks = (a.rows + gw.chunk_rows - 1) / gw.chunk_rows;
+    int64_t rpw = 64 / pv.R;  // one batch of rows per workgroup
+    if (a.mode != STACR_MODE_GLOBAL_TOPK)
+        while (rpw > 1 && gw.chunk_rows % rpw) rpw >>= 1;
+    gw.rows_per_wg = rpw;
+    gw.wgs_per_chunk = (gw.chunk_rows + rpw - 1) / rpw;
+    gw.hcopies = pv.g.hcopies;  // the later passes sum the copies the projection pass fills
+    pv.n_wgs_w = gw.n_chunks * gw.wgs_per_chunk;
+    pv.wide = gw.n_chunks == pv.g.n_chunks;
+    return pv.wide ? pv : p;
+}
+
 template <typename T> T *carve(char *base, size_t off) { return reinterpret_cast<T *>(base + off); }
 
 enum { WS_QP, WS_HIST, WS_COARSE, WS_STATE, WS_MAXKEY, WS_COUNTS, WS_OFFS, WS_LRBITS, WS_LIDX, WS_THIST, WS_TSTATE,
@@ -1623,7 +1800,7 @@ size_t layout(const StacrSaveArgs &a, const Plan &p, size_t *off)
     take(WS_LOFFS, nb * sizeof(WgOffset));
     take(WS_Q4, a.bits == 4 ? (size_t)a.k_total : 0);
     take(WS_FOLD, p.fold ? (size_t)17 * p.n_wgs * sizeof(uint32_t) : 0);  // cum[0..16][workgroup]
-    const bool rstore = p.fast && a.dtype != STACR_DTYPE_F32 && a.k_total > 0;
+    const bool rstore = p.fast && a.dtype != STACR_DTYPE_F32 && a.k_total > 0;  // (wide rows: p.fast)
     take(WS_R, rstore ? (size_t)a.rows * a.feats * 2 : 0);  // the stored residual (16-bit types)
     return cur;
 }
@@ -1668,7 +1845,14 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     FastGeom fg{p.g.L / 64, a.rank == R && ((uintptr_t)coeff % 16) == 0};
     if (!coeff_in || resid) {
         if constexpr (kFastOk) {
-            if (fast) {
+            if (fast && p.wide) {
+                if constexpr (kRin && R <= 8) {
+                    const int c_vec = a.rank == R && ((uintptr_t)coeff % 16) == 0;
+                    stacr_launch("k_proj_hist", s, [&] { k_proj_hist_w<DT, R, kWideMv><<<(unsigned)p.n_wgs_w, kBlock, 0, s>>>(p.gw, c_vec, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in, rbuf, coarse); });
+                } else {
+                    return stacr_fail(STACR_ERR_INVALID, "stacr_save: wide rows outside 16-bit ranks <= 8");
+                }
+            } else if (fast) {
                 stacr_launch("k_proj_hist", s, [&] { k_proj_hist_b<DT, R, V, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in, rbuf, coarse); });
             }
         }
@@ -1795,7 +1979,7 @@ int stacr_save_launch(const StacrSaveArgs &a)
     const size_t need = layout(a, p, off);
     if (a.workspace_bytes < need)
         return stacr_fail(STACR_ERR_WORKSPACE, "stacr_save: workspace has %zu bytes, needs %zu", a.workspace_bytes, need);
-    if (p.n_wgs > INT32_MAX)
+    if (p.n_wgs > INT32_MAX || p.n_wgs_w > INT32_MAX)
         return stacr_fail(STACR_ERR_UNSUPPORTED, "stacr_save: too many workgroups");
     char *ws = static_cast<char *>(a.workspace);
     switch (a.dtype) {

@@ -136,12 +136,37 @@ SAVE_CASES = [
     # workgroup and a trim to k_total, and a chunked run without quantization
     ("bf16_batched_chunk_trim", 1000, 1024, 8, "bf16", "chunk_topk", 0.005, 100, 8, True),
     ("bf16_batched_chunk_bits0", 2048, 1024, 4, "bf16", "chunk_topk", 0.01, 512, 0, False),
+    # 16-bit rows of 2048 < d <= 4096: the projection pass takes two vectors a thread and stores
+    # the residual; the later passes read it as twice the rows of half the width (cfg3 c_proj,
+    # cfg5 c_proj and chunk_trim_bf16 above also run here)
+    ("f16_wide_global_copies", 2048, 4096, 8, "f16", "global_topk", 0.005, 512, 8, True),
+    ("bf16_wide_2560_partial_vectors", 1024, 2560, 8, "bf16", "global_topk", 0.01, 512, 8, True),
+    ("bf16_wide_chunk_partial_int4", 1000, 3072, 5, "bf16", "chunk_topk", 0.01, 300, 4, False),
+    ("f16_wide_rank4_bits0", 512, 4096, 4, "f16", "global_topk", 0.01, 512, 0, False),
+    ("bf16_wide_rank1_odd_chunk", 777, 2064, 1, "bf16", "chunk_topk", 0.02, 37, 8, False),
+    ("bf16_wide_no_residual", 256, 4096, 8, "bf16", "chunk_topk", 0.0, 128, 8, False),
 ]
 
 
 @pytest.mark.parametrize("case", SAVE_CASES, ids=[c[0] for c in SAVE_CASES])
 def test_save_matches_oracle(dev, case):
     run_and_check_save(dev, *case[1:])
+
+
+@pytest.mark.parametrize("d,dtype", [(4096, "bf16"), (2560, "f16"), (1024, "bf16")])
+def test_save_from_given_coefficients_matches_full_save(dev, d, dtype):
+    """With the coefficients given (stacr_select_residual), the selection and quantization are the
+    full save's, bit for bit, on the batched and wide-row paths."""
+    from stacr_amd import kernels
+
+    announce("save from coeff", d, dtype)
+    rows = 1024
+    xd = make_activation(rows, d, lognormal=True).to(dev, DT[dtype])
+    qd = make_basis(d, 8).to(dev, DT[dtype])
+    coeff, idx, data, scale = kernels.save(xd, qd, mode="global_topk", budget=0.005, chunk_rows=512, bits=8)
+    c2, i2, d2, s2 = kernels.save(xd, qd, mode="global_topk", budget=0.005, chunk_rows=512, bits=8, coeff=coeff)
+    torch.cuda.synchronize()
+    assert torch.equal(i2, idx) and torch.equal(d2, data) and torch.equal(s2, scale)
 
 
 def test_save_is_deterministic(dev):
