@@ -953,36 +953,38 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg,
     }
 }
 
-// Pass 1 for 16-bit rows wider than one vector per thread (d up to MV * 2048): the workgroup's 256
-// threads share each row, thread u holding the MV vectors at columns (m * 256 + u) * 8, and the
-// basis stays as packed 16-bit words (the projection's v_dot2 operands; the residual widens them
-// per vector).  The workgroup's rows are one batch of 64 / R rows.  Outputs as k_proj_hist_b with
-// the residual stored: coefficients, the residual (exact in the activation dtype), the level-0
-// histogram with its coarse sums, and the max key.  The later passes read the stored residual as
-// a matrix of MV * rows rows of d / MV columns: the same memory, the same flat indices.
-template <int DT, int R, int MV>
-__global__ __launch_bounds__(kBlock) void k_proj_hist_w(SaveGeom g, int c_vec, const typename Act<DT>::T *__restrict__ x,
-                                                        const float *__restrict__ qp, typename Act<DT>::T *__restrict__ coeff,
-                                                        uint32_t *__restrict__ hist, uint32_t *__restrict__ maxkey,
-                                                        int do_hist, const typename Act<DT>::T *__restrict__ coeff_in,
-                                                        typename Act<DT>::T *__restrict__ rout, uint32_t *__restrict__ coarse)
+// Pass 1 for 16-bit rows the batched kernels do not take (2048 < d <= 8192, or rank 16): the
+// workgroup's NT threads share each row, thread u holding the MV vectors at columns
+// (m * NT + u) * 8, and the basis stays as packed 16-bit words (the projection's v_dot2 operands;
+// the residual widens one vector's worth at a time).  The workgroup's rows are one batch of
+// 64 / R rows.  Outputs as k_proj_hist_b with the residual stored: coefficients, the residual
+// (exact in the activation dtype), the level-0 histogram with its coarse sums, and the max key.
+// The later passes read the stored residual as a matrix of f * rows rows of d / f columns (the
+// same memory, the same flat indices), so they never need the basis or C.
+template <int DT, int R, int MV, int NT>
+__global__ __launch_bounds__(NT) void k_proj_hist_w(SaveGeom g, int c_vec, const typename Act<DT>::T *__restrict__ x,
+                                                    const float *__restrict__ qp, typename Act<DT>::T *__restrict__ coeff,
+                                                    uint32_t *__restrict__ hist, uint32_t *__restrict__ maxkey,
+                                                    int do_hist, const typename Act<DT>::T *__restrict__ coeff_in,
+                                                    typename Act<DT>::T *__restrict__ rout, uint32_t *__restrict__ coarse)
 {
     using T = typename Act<DT>::T;
     static_assert(sizeof(T) == 2, "16-bit activations");
-    constexpr int V = 8, NB = Batch<R>::NB;
+    constexpr int V = 8, NB = Batch<R>::NB, W = NT / 64;
+    static_assert(NB * R == 64 && NT % 64 == 0 && kBins % NT == 0, "batch and block shape");
     __shared__ uint32_t s_hist[kBins];
-    __shared__ __align__(16) float s_part[kWaves * 64];
-    __shared__ __align__(16) float s_c[kWaves * 64];
-    __shared__ uint32_t s_wmax[kWaves];
+    __shared__ __align__(16) float s_part[W * 64];
+    __shared__ __align__(16) float s_c[64];
+    __shared__ uint32_t s_wmax[W];
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
     if (row0 >= row_end) return;  // a trailing workgroup with no rows (uniform)
-    const int u = threadIdx.x;
+    const int u = threadIdx.x, lane = u & 63, wave = u >> 6;
     int64_t col[MV], colc[MV];
     bool col_ok[MV];
 #pragma unroll
     for (int m = 0; m < MV; ++m) {
-        col[m] = (int64_t)(m * kBlock + u) * V;
+        col[m] = (int64_t)(m * NT + u) * V;
         colc[m] = min(col[m], g.d - V);
         col_ok[m] = col[m] < g.d;
     }
@@ -1006,57 +1008,106 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_w(SaveGeom g, int c_vec, c
             const uint4 w = *reinterpret_cast<const uint4 *>(qph + j * g.d + colc[m]);
             qw[m][j] = col_ok[m] ? w : make_uint4(0u, 0u, 0u, 0u);
         }
-    for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
+    for (int b = u; b < kBins; b += NT) s_hist[b] = 0u;
     uint32_t kmax = 0u;
-    __syncthreads();
     float c[64];
     if (coeff_in) {
         batch_coeff_load<DT, R>(coeff_in, g.rank, rows, row_end, c_vec != 0, c);
     } else {
         float acc[64];
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            const bool row_ok = rows[i] < row_end;
+        for (int k = 0; k < 64; ++k) acc[k] = 0.f;
 #pragma unroll
-            for (int j = 0; j < R; ++j) acc[i * R + j] = 0.f;
+        for (int m = 0; m < MV; ++m) {  // vector by vector: vector m's basis words die after it
 #pragma unroll
-            for (int m = 0; m < MV; ++m) {
-                const uint4 xr = row_ok && col_ok[m] ? raw[i][m] : make_uint4(0u, 0u, 0u, 0u);
+            for (int i = 0; i < NB; ++i) {
+                const uint4 xr = rows[i] < row_end && col_ok[m] ? raw[i][m] : make_uint4(0u, 0u, 0u, 0u);
                 const uint32_t xw[4] = {xr.x, xr.y, xr.z, xr.w};
 #pragma unroll
                 for (int j = 0; j < R; ++j) {
                     const uint32_t w[4] = {qw[m][j].x, qw[m][j].y, qw[m][j].z, qw[m][j].w};
-                    float s = acc[i * R + j];
+                    float sum = acc[i * R + j];
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) s = dot2<DT>(xw[k], w[k], s);
-                    acc[i * R + j] = s;
+                    for (int k = 0; k < 4; ++k) sum = dot2<DT>(xw[k], w[k], sum);
+                    acc[i * R + j] = sum;
                 }
             }
         }
-        // the workgroup's 4 waves are one row slot: rows row0 + i, i < NB
-        batch_coeff_from_acc<DT, R>(acc, kWaves, 0, s_part, s_c, row0, 1, row_end, g.rank, coeff, c);
+        // lane l of every wave: the wave's total of value l = (row l / R, basis column l % R); the
+        // first wave adds the other waves' totals in wave order and rounds once
+        const float part = wave_reduce_scatter64(acc);
+        s_part[wave * 64 + lane] = part;
+        __syncthreads();
+        if (wave == 0) {
+            float tot = part;
+            for (int w = 1; w < W; ++w) tot += s_part[w * 64 + lane];
+            const float cv = Act<DT>::rnd(tot);
+            s_c[lane] = cv;
+            const int i = lane / R, j = lane % R;
+            const int64_t row = row0 + i;
+            if (j < g.rank && row < row_end) coeff[row * g.rank + j] = Act<DT>::st(cv);
+        }
+        __syncthreads();
+        const float4 *src = reinterpret_cast<const float4 *>(s_c);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const float4 v = src[k];
+            c[4 * k] = v.x; c[4 * k + 1] = v.y; c[4 * k + 2] = v.z; c[4 * k + 3] = v.w;
+        }
     }
     if (!do_hist) return;
+    if (coeff_in) __syncthreads();  // the histogram is clear
+    // Residual r = rnd(x - rnd(sum_j c_j q_j)) (an fp32 fused-multiply-add chain over j, as in
+    // batch_residual), element by element across the batch's rows, packed in the activation
+    // dtype as it is formed.  The basis words of vectors m >= 1 are read again here (from L2: the
+    // basis is shared by every workgroup) rather than kept from the projection, which leaves room
+    // for the batch's coefficients in registers.
 #pragma unroll
     for (int m = 0; m < MV; ++m) {
-        if (!col_ok[m]) continue;
-        float q[V][R];  // this vector's basis values, widened
+        uint4 qm[R];
+        if (m == 0) {
 #pragma unroll
-        for (int j = 0; j < R; ++j) {
-            const uint32_t w[4] = {qw[m][j].x, qw[m][j].y, qw[m][j].z, qw[m][j].w};
+            for (int j = 0; j < R; ++j) qm[j] = qw[0][j];
+        } else {
+            int64_t o = colc[m];
+            asm volatile("" : "+v"(o));  // a fresh load, not the projection's registers
 #pragma unroll
-            for (int e = 0; e < V; ++e) q[e][j] = Act<DT>::ld((T)((w[e / 2] >> (16 * (e & 1))) & 0xffffu));
+            for (int j = 0; j < R; ++j) {
+                const uint4 w = *reinterpret_cast<const uint4 *>(qph + j * g.d + o);
+                qm[j] = col_ok[m] ? w : make_uint4(0u, 0u, 0u, 0u);
+            }
         }
+        uint32_t rp[NB][4];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) rp[i][0] = rp[i][1] = rp[i][2] = rp[i][3] = 0u;
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            float qe[R];
+#pragma unroll
+            for (int j = 0; j < R; ++j) {
+                const uint32_t w = e < 2 ? qm[j].x : e < 4 ? qm[j].y : e < 6 ? qm[j].z : qm[j].w;
+                qe[j] = Act<DT>::ld((T)((w >> (16 * (e & 1))) & 0xffffu));
+            }
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const uint4 xr = raw[i][m];
+                const uint32_t xw = e < 2 ? xr.x : e < 4 ? xr.y : e < 6 ? xr.z : xr.w;
+                const float xe = Act<DT>::ld((T)((xw >> (16 * (e & 1))) & 0xffffu));
+                float pj = 0.f;
+#pragma unroll
+                for (int j = 0; j < R; ++j) pj = fmaf(c[i * R + j], qe[j], pj);
+                rp[i][e >> 1] |= (uint32_t)Act<DT>::st(xe - Act<DT>::rnd(pj)) << (16 * (e & 1));
+            }
+        }
+        if (!col_ok[m]) continue;
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             if (rows[i] >= row_end) continue;
-            float xv[V], r[V];
-            unpack_raw<DT, V>(raw[i][m], xv);
-            batch_residual<DT, R, V>(xv, c + i * R, q, r);
-            *reinterpret_cast<uint4 *>(rout + rows[i] * g.d + col[m]) = pack_raw<DT, V>(r);
+            *reinterpret_cast<uint4 *>(rout + rows[i] * g.d + col[m]) = make_uint4(rp[i][0], rp[i][1], rp[i][2], rp[i][3]);
 #pragma unroll
             for (int e = 0; e < V; ++e) {
-                const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
+                const float rv = Act<DT>::ld((T)((rp[i][e >> 1] >> (16 * (e & 1))) & 0xffffu));
+                const uint32_t key = __float_as_uint(rv) & 0x7fffffffu;
                 atomicAdd(&s_hist[key >> kDigitShift[0]], 1u);
                 kmax = max(kmax, key);
             }
@@ -1064,22 +1115,22 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_w(SaveGeom g, int c_vec, c
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, off, 64));
-    if ((threadIdx.x & 63) == 0) s_wmax[threadIdx.x >> 6] = kmax;
+    if (lane == 0) s_wmax[wave] = kmax;
     __syncthreads();
     const int copy = (int)(blockIdx.x % g.hcopies);
     uint32_t *gh = hist + ((chunk * 3 + 0) * g.hcopies + copy) * kBins;
-    for (int b = threadIdx.x; b < kBins; b += kBlock)
+    for (int b = u; b < kBins; b += NT)
         if (s_hist[b]) atomicAdd(&gh[b], s_hist[b]);
-    if (threadIdx.x < kCoarse) {
+    if (u < kCoarse) {
         uint32_t sum = 0u;
 #pragma unroll 8
-        for (int b = 0; b < kBins / kCoarse; ++b) sum += s_hist[threadIdx.x * (kBins / kCoarse) + b];
-        if (sum) atomicAdd(&coarse[(chunk * g.hcopies + copy) * kCoarse + threadIdx.x], sum);
+        for (int b = 0; b < kBins / kCoarse; ++b) sum += s_hist[u * (kBins / kCoarse) + b];
+        if (sum) atomicAdd(&coarse[(chunk * g.hcopies + copy) * kCoarse + u], sum);
     }
-    if (threadIdx.x == 0) {
+    if (u == 0) {
         uint32_t mx = 0u;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) mx = max(mx, s_wmax[w]);
+        for (int w = 0; w < W; ++w) mx = max(mx, s_wmax[w]);
         if (mx) atomicMax(maxkey + copy * kMaxKeyStride, mx);
     }
 }
@@ -1685,16 +1736,17 @@ struct Plan {
     bool fast;  // the batched kernels (one batch per workgroup)
     bool fold;  // bf16 on the batched path: the emission pass ends the selection (no count pass)
     int64_t n_wgs;
-    // wide rows (16-bit, d / kWideMv <= 2048): g, V, fast and n_wgs describe the stored residual as
-    // kWideMv * rows rows of d / kWideMv columns (the later passes); gw and n_wgs_w the projection pass
+    int Rq;  // the basis copies' padded rank (R, except on the wide path)
+    // wide rows (16-bit, see make_plan): g, V, R, fast and n_wgs describe the stored residual as
+    // f * rows rows of d / f columns (the later passes); gw, Rq, mvw, ntw and n_wgs_w the
+    // projection pass
     bool wide;
     SaveGeom gw;
+    int mvw, ntw;
     int64_t n_wgs_w;
     bool trim;
     int64_t n_list_blocks;
 };
-
-constexpr int kWideMv = 2;  // vectors per thread per row in the wide projection pass
 
 Plan make_plan_rows(const StacrSaveArgs &a)
 {
@@ -1703,6 +1755,7 @@ Plan make_plan_rows(const StacrSaveArgs &a)
     const bool aligned = ((uintptr_t)a.x % 16) == 0;
     p.V = (a.feats % vec == 0 && aligned) ? vec : 1;
     p.R = pad_rank(a.rank);
+    p.Rq = p.R;
     SaveGeom &g = p.g;
     g.rows = a.rows;
     g.d = a.feats;
@@ -1712,13 +1765,14 @@ Plan make_plan_rows(const StacrSaveArgs &a)
     g.log2L = ilog2(g.L);
     g.rpi = kBlock / g.L;
     g.mv = (int)((vecs + g.L - 1) / g.L);
-    g.chunk_rows = a.mode == STACR_MODE_GLOBAL_TOPK ? a.rows : min(a.chunk_rows, a.rows);
+    // without a residual there is no selection, and so no chunk: the rows are one span
+    g.chunk_rows = a.mode == STACR_MODE_GLOBAL_TOPK || a.k_total == 0 ? a.rows : min(a.chunk_rows, a.rows);
     if (g.chunk_rows < 1) g.chunk_rows = 1;
     g.n_chunks = (a.rows + g.chunk_rows - 1) / g.chunk_rows;
     int64_t target = hmax<int64_t>(1, 16384 / hmax<int64_t>(1, a.feats));
     int64_t rpw = 1;
     while (rpw * 2 <= target) rpw *= 2;
-    if (a.mode != STACR_MODE_GLOBAL_TOPK)
+    if (a.mode != STACR_MODE_GLOBAL_TOPK && a.k_total > 0)
         while (rpw > 1 && g.chunk_rows % rpw) rpw >>= 1;
     p.qreg = g.mv == 1 && p.V * p.R <= 128;
     // the batched kernels take exactly one batch (64 / R iterations of the row slots) per workgroup
@@ -1735,36 +1789,54 @@ Plan make_plan_rows(const StacrSaveArgs &a)
     return p;
 }
 
-// 16-bit rows of 2048 < d <= 4096 features (d % 16 == 0, aligned, rank <= 8) are too wide for one
-// vector per thread.  Their projection pass (k_proj_hist_w) gives each thread two vectors of a row
-// and stores the residual; the later passes run on the batched kernels over that residual viewed as
-// 2 * rows rows of d / 2 columns (row-major, so the flat indices are the same; chunks are 2 *
-// chunk_rows such rows, so the chunks are the same).
+// 16-bit rows the batched kernels do not take: 2048 < d <= 8192 features (d % 8 == 0, aligned,
+// rank <= 16), or rank 16 at d <= 2048.  The projection pass (k_proj_hist_w) gives a row to
+// ntw threads with mvw vectors each and stores the residual; the later passes run on the batched
+// kernels over that residual viewed as f * rows rows of d / f <= 2048 columns (row-major, so the
+// flat indices are the same; chunks are f * chunk_rows such rows, so the chunks are the same) at
+// rank 8 (they read neither the basis nor C).
 Plan make_plan(const StacrSaveArgs &a)
 {
     Plan p = make_plan_rows(a);
-    if (p.fast || a.dtype == STACR_DTYPE_F32 || p.V != 8 || p.R > 8 || a.feats <= 2048 ||
-        a.feats > 2048 * kWideMv || a.feats % (8 * kWideMv) != 0)
-        return p;
+    if (p.fast || a.dtype == STACR_DTYPE_F32 || p.V != 8 || p.R > 16 || a.feats > 8192) return p;
+    int mv, nt;
+    if (p.R <= 8) {
+        if (a.feats <= 2048) return p;  // (the batched kernels take these when aligned)
+        mv = 2;
+        nt = a.feats <= 4096 ? 256 : 512;
+    } else {
+        // (fp16 at rank 16 above 4096 features stays on the per-row kernels: the wide kernel's
+        // fp16 conversions push that shape past 256 registers)
+        if (a.feats > 4096 && a.dtype == STACR_DTYPE_F16) return p;
+        mv = a.feats <= 4096 ? 1 : 2;
+        nt = a.feats <= 2048 ? 256 : 512;
+    }
+    int f = 1;  // virtual rows per row
+    while (a.feats / f > 2048 || a.feats % (8 * f) != 0)
+        if (++f > 8) return p;
     StacrSaveArgs av = a;
-    av.feats = a.feats / kWideMv;
-    av.rows = a.rows * kWideMv;
-    av.chunk_rows = a.chunk_rows * kWideMv;
+    av.feats = a.feats / f;
+    av.rows = a.rows * f;
+    av.chunk_rows = a.chunk_rows * f;
+    av.rank = a.rank < 8 ? a.rank : 8;
     Plan pv = make_plan_rows(av);
     if (!pv.fast) return p;
+    pv.Rq = p.R <= 8 ? 8 : 16;  // (ranks below 8 padded to 8: one kernel shape fewer)
+    pv.mvw = mv;
+    pv.ntw = nt;
     SaveGeom &gw = pv.gw;
     gw.rows = a.rows;
     gw.d = a.feats;
     gw.rank = a.rank;
-    gw.L = kBlock;
-    gw.log2L = ilog2(kBlock);
+    gw.L = nt;
+    gw.log2L = ilog2(nt);
     gw.rpi = 1;
-    gw.mv = kWideMv;
-    gw.chunk_rows = a.mode == STACR_MODE_GLOBAL_TOPK ? a.rows : min(a.chunk_rows, a.rows);
+    gw.mv = mv;
+    gw.chunk_rows = a.mode == STACR_MODE_GLOBAL_TOPK || a.k_total == 0 ? a.rows : min(a.chunk_rows, a.rows);
     if (gw.chunk_rows < 1) gw.chunk_rows = 1;
     gw.n_chunks = (a.rows + gw.chunk_rows - 1) / gw.chunk_rows;
-    int64_t rpw = 64 / pv.R;  // one batch of rows per workgroup
-    if (a.mode != STACR_MODE_GLOBAL_TOPK)
+    int64_t rpw = 64 / pv.Rq;  // one batch of rows per workgroup
+    if (a.mode != STACR_MODE_GLOBAL_TOPK && a.k_total > 0)
         while (rpw > 1 && gw.chunk_rows % rpw) rpw >>= 1;
     gw.rows_per_wg = rpw;
     gw.wgs_per_chunk = (gw.chunk_rows + rpw - 1) / rpw;
@@ -1784,7 +1856,7 @@ size_t layout(const StacrSaveArgs &a, const Plan &p, size_t *off)
     size_t cur = 0;
     auto take = [&](int slot, size_t bytes) { off[slot] = cur; cur += (bytes + 255) & ~(size_t)255; };
     // padded basis, then transposed; then transposed in the activation dtype (16-bit types)
-    take(WS_QP, 2 * (size_t)a.feats * p.R * sizeof(float) + (size_t)a.feats * p.R * 2);
+    take(WS_QP, 2 * (size_t)a.feats * p.Rq * sizeof(float) + (size_t)a.feats * p.Rq * 2);
     take(WS_HIST, (size_t)p.g.n_chunks * 3 * p.g.hcopies * kBins * sizeof(uint32_t));
     take(WS_COARSE, (size_t)p.g.n_chunks * p.g.hcopies * kCoarse * sizeof(uint32_t));
     take(WS_MAXKEY, (size_t)p.g.hcopies * kMaxKeyStride * sizeof(uint32_t));
@@ -1803,6 +1875,39 @@ size_t layout(const StacrSaveArgs &a, const Plan &p, size_t *off)
     const bool rstore = p.fast && a.dtype != STACR_DTYPE_F32 && a.k_total > 0;  // (wide rows: p.fast)
     take(WS_R, rstore ? (size_t)a.rows * a.feats * 2 : 0);  // the stored residual (16-bit types)
     return cur;
+}
+
+// The wide projection pass for the plan's (rank, vectors a thread, threads a row).
+template <int DT>
+int launch_wide_pass1(const StacrSaveArgs &a, const Plan &p, const typename Act<DT>::T *x, const float *qp,
+                      typename Act<DT>::T *coeff, uint32_t *hist, uint32_t *maxkey, int do_hist,
+                      const typename Act<DT>::T *coeff_in, typename Act<DT>::T *rout, uint32_t *coarse)
+{
+    hipStream_t s = a.stream;
+    const unsigned n = (unsigned)p.n_wgs_w;
+    const void *cp = coeff_in ? (const void *)coeff_in : (const void *)coeff;
+    const int c_vec = a.rank == p.Rq && ((uintptr_t)cp % 16) == 0;
+    bool done = false;
+    auto go = [&](auto r, auto mv, auto nt) {
+        constexpr int R = decltype(r)::value, MV = decltype(mv)::value, NT = decltype(nt)::value;
+        if (done || p.Rq != R || p.mvw != MV || p.ntw != NT) return;
+        done = true;
+        stacr_launch("k_proj_hist", s, [&] {
+            k_proj_hist_w<DT, R, MV, NT><<<n, NT, 0, s>>>(p.gw, c_vec, x, qp, coeff, hist, maxkey, do_hist, coeff_in, rout, coarse);
+        });
+    };
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using N256 = std::integral_constant<int, 256>;
+    using N512 = std::integral_constant<int, 512>;
+    go(std::integral_constant<int, 8>{}, I2{}, N256{});
+    go(std::integral_constant<int, 8>{}, I2{}, N512{});
+    go(std::integral_constant<int, 16>{}, I1{}, N256{});
+    go(std::integral_constant<int, 16>{}, I1{}, N512{});
+    if constexpr (DT == STACR_DTYPE_BF16) go(std::integral_constant<int, 16>{}, I2{}, N512{});
+    if (!done)
+        return stacr_fail(STACR_ERR_INVALID, "stacr_save: no wide projection kernel for rank %d, %d x %d", p.Rq, p.mvw, p.ntw);
+    return STACR_OK;
 }
 
 template <int DT, int R, int V, bool QREG>
@@ -1826,8 +1931,8 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     const int64_t n_zero = resid ? (int64_t)((off[WS_MAXKEY] + (size_t)p.g.hcopies * kMaxKeyStride * sizeof(uint32_t) -
                                               off[WS_HIST]) / sizeof(uint32_t)) : 0;
     stacr_launch("k_prep", s, [&] {
-        k_prep<DT><<<grid_for(hmax<int64_t>(a.feats * R, n_zero)), kBlock, 0, s>>>(static_cast<const T *>(a.q), a.feats,
-                                                                                 a.rank, R, qp, hist, n_zero);
+        k_prep<DT><<<grid_for(hmax<int64_t>(a.feats * p.Rq, n_zero)), kBlock, 0, s>>>(static_cast<const T *>(a.q), a.feats,
+                                                                                    a.rank, p.Rq, qp, hist, n_zero);
     });
     // batched fast path: one aligned vector per thread per row, basis columns in registers
     constexpr bool kFastOk = QREG && V == Act<DT>::kVec && V * R <= 64;
@@ -1846,11 +1951,11 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     if (!coeff_in || resid) {
         if constexpr (kFastOk) {
             if (fast && p.wide) {
-                if constexpr (kRin && R <= 8) {
-                    const int c_vec = a.rank == R && ((uintptr_t)coeff % 16) == 0;
-                    stacr_launch("k_proj_hist", s, [&] { k_proj_hist_w<DT, R, kWideMv><<<(unsigned)p.n_wgs_w, kBlock, 0, s>>>(p.gw, c_vec, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in, rbuf, coarse); });
+                if constexpr (kRin) {
+                    const int rc = launch_wide_pass1<DT>(a, p, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in, rbuf, coarse);
+                    if (rc) return rc;
                 } else {
-                    return stacr_fail(STACR_ERR_INVALID, "stacr_save: wide rows outside 16-bit ranks <= 8");
+                    return stacr_fail(STACR_ERR_INVALID, "stacr_save: wide rows outside 16-bit activations");
                 }
             } else if (fast) {
                 stacr_launch("k_proj_hist", s, [&] { k_proj_hist_b<DT, R, V, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in, rbuf, coarse); });

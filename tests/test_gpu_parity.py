@@ -145,6 +145,15 @@ SAVE_CASES = [
     ("f16_wide_rank4_bits0", 512, 4096, 4, "f16", "global_topk", 0.01, 512, 0, False),
     ("bf16_wide_rank1_odd_chunk", 777, 2064, 1, "bf16", "chunk_topk", 0.02, 37, 8, False),
     ("bf16_wide_no_residual", 256, 4096, 8, "bf16", "chunk_topk", 0.0, 128, 8, False),
+    # rank 16 (cfg4) and rows up to 8192 features: the projection pass with 256 / 512 threads a
+    # row, the later passes on the residual as rows of <= 2048 features (2, 3 or 4 per row)
+    ("bf16_rank16_d2048_chunk", 2048, 2048, 16, "bf16", "chunk_topk", 0.005, 512, 8, True),
+    ("f16_rank16_d3072_global", 1024, 3072, 16, "f16", "global_topk", 0.01, 512, 8, False),
+    ("bf16_rank12_d6144_chunk_int4", 600, 6144, 12, "bf16", "chunk_topk", 0.005, 200, 4, False),
+    ("bf16_rank3_d8192_global", 512, 8192, 3, "bf16", "global_topk", 0.005, 512, 8, True),
+    ("bf16_rank16_d1024_bits0", 1000, 1024, 16, "bf16", "global_topk", 0.01, 512, 0, False),
+    ("f16_rank16_d8192_per_row", 256, 8192, 16, "f16", "chunk_topk", 0.005, 128, 8, False),
+    ("bf16_rank16_d8192_no_residual", 256, 8192, 16, "bf16", "chunk_topk", 0.0, 128, 8, False),
 ]
 
 
@@ -153,16 +162,17 @@ def test_save_matches_oracle(dev, case):
     run_and_check_save(dev, *case[1:])
 
 
-@pytest.mark.parametrize("d,dtype", [(4096, "bf16"), (2560, "f16"), (1024, "bf16")])
-def test_save_from_given_coefficients_matches_full_save(dev, d, dtype):
+@pytest.mark.parametrize("d,dtype,rank", [(4096, "bf16", 8), (2560, "f16", 8), (1024, "bf16", 8), (8192, "bf16", 16),
+                                          (2048, "f16", 16)])
+def test_save_from_given_coefficients_matches_full_save(dev, d, dtype, rank):
     """With the coefficients given (stacr_select_residual), the selection and quantization are the
     full save's, bit for bit, on the batched and wide-row paths."""
     from stacr_amd import kernels
 
-    announce("save from coeff", d, dtype)
+    announce("save from coeff", d, dtype, rank)
     rows = 1024
     xd = make_activation(rows, d, lognormal=True).to(dev, DT[dtype])
-    qd = make_basis(d, 8).to(dev, DT[dtype])
+    qd = make_basis(d, rank).to(dev, DT[dtype])
     coeff, idx, data, scale = kernels.save(xd, qd, mode="global_topk", budget=0.005, chunk_rows=512, bits=8)
     c2, i2, d2, s2 = kernels.save(xd, qd, mode="global_topk", budget=0.005, chunk_rows=512, bits=8, coeff=coeff)
     torch.cuda.synchronize()
