@@ -166,9 +166,14 @@ def check_layer(outs, ref):
     """Save outputs are deterministic (bit-equal); dW sums the sparse term in arrival order."""
     import torch
 
-    for a, b in zip(outs[:4], ref[:4]):
+    for name, a, b in zip(("coeff", "idx", "data", "scale"), outs[:4], ref[:4]):
         if (a is None) != (b is None) or (a is not None and not torch.equal(a, b)):
-            raise RuntimeError("graph replay of the save differs from the eager result")
+            detail = ""
+            if a is not None and b is not None and a.shape == b.shape:
+                diff = (a != b).reshape(-1)
+                first = int(diff.nonzero()[0].item()) if diff.any() else -1
+                detail = f": {int(diff.sum().item())} of {diff.numel()} elements, first at {first}"
+            raise RuntimeError(f"graph replay of the save differs from the eager result in {name}{detail}")
     if _rel(outs[4], ref[4]) > 1e-3:
         raise RuntimeError("graph replay of the weight gradient differs from the eager result")
 

@@ -25,6 +25,8 @@
  *                            the adaptive engine's block_sparse selector, stacr/adaptive.py:1788-1938
  *   stacr_oja_step           the Oja step of STACRLinear._refresh_basis, stacr/layers.py:346-348,
  *                            and OjaBasis.update, stacr/oja.py:73-79
+ *   stacr_reconstruct        the saved-tensor hooks' dense unpack, stacr/compressor.py:127-133 with
+ *                            stacr/residual.py:13-20
  */
 #ifndef STACR_AMD_H
 #define STACR_AMD_H
@@ -296,6 +298,24 @@ int stacr_oja_workspace_bytes(int64_t rows, int64_t feats, int rank, size_t *byt
  */
 int stacr_oja_step(const void *x, int dtype, int64_t rows, int64_t feats, const float *q, int rank, float lr,
                    float *update, float *out, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------- dense reconstruction */
+
+/*
+ * The dense activation a saved-tensor compressor hands back to autograd, replacing
+ * STACRCompressor.unpack (stacr/compressor.py:127-133) and SparseResidual.dense
+ * (stacr/residual.py:13-20):
+ *   out = coeff Q^T                      (rows x feats, dtype; each element an fp32 chain over the
+ *                                         rank, rounded once)
+ *   out = out + dense(idx, values)       when has_residual (every element gets the addition, so
+ *                                         -0 becomes +0 away from the entries, as in the reference)
+ * coeff: rows x rank, q: feats x rank, values: nnz elements, all in dtype; idx: nnz flat indices
+ * into rows x feats (index_bytes 4 or 8), unique (entries outside the tensor are skipped).
+ * No workspace.
+ */
+int stacr_reconstruct(const void *coeff, const void *q, int dtype, int64_t rows, int64_t feats, int rank,
+                      const void *idx, int index_bytes, const void *values, int64_t nnz, int has_residual,
+                      void *out, void *stream);
 
 /*
  * Kernel timing (benchmarking aid; no counterpart in the reference).  Between begin and end,

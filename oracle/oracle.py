@@ -49,6 +49,7 @@ def lib():
         L.orc_weight_grad.argtypes, L.orc_weight_grad.restype = [P, i64, i64, P, P, i64, i32, P, P, i64, P, P], i32
         L.orc_round_dtype.argtypes, L.orc_round_dtype.restype = [ctypes.c_float, i32], ctypes.c_float
         L.orc_residual_act.argtypes = [P, P, P, i64, i64, i32, i32, P]
+        L.orc_lowrank.argtypes = [P, P, i64, i64, i32, i32, P]
         L.orc_select_explicit.argtypes, L.orc_select_explicit.restype = [P, i64, i64, i64, i64, i64, P, P], i64
         _lib = L
     return _lib
@@ -230,6 +231,31 @@ def residual_act(x: np.ndarray, c: np.ndarray, q: np.ndarray, dtype: str) -> np.
     rows, d = x.shape
     out = np.empty_like(x)
     lib().orc_residual_act(_ptr(x), _ptr(c), _ptr(q), rows, d, q.shape[1], DTYPE_CODE[dtype], _ptr(out))
+    return out
+
+
+def lowrank(c: np.ndarray, q: np.ndarray, dtype: str) -> np.ndarray:
+    """L = rnd(C Q^T) in the activation dtype, the chain of residual_act (stacr/compressor.py:128)."""
+    c, q = _c(c, np.float32), _c(q, np.float32)
+    out = np.empty((c.shape[0], q.shape[0]), np.float32)
+    lib().orc_lowrank(_ptr(c), _ptr(q), c.shape[0], q.shape[0], q.shape[1], DTYPE_CODE[dtype], _ptr(out))
+    return out
+
+
+def reconstruct(c: np.ndarray, q: np.ndarray, idx: np.ndarray | None, vals: np.ndarray | None,
+                dtype: str) -> np.ndarray:
+    """The saved-tensor hooks' dense unpack (stacr/compressor.py:127-133, stacr/residual.py:13-20):
+    L = rnd(C Q^T) in the activation dtype (the fp32 chain of residual_act), then, with a residual
+    (idx is not None), every element gets + dense: rnd(L + v) at the entries and L + 0 elsewhere
+    (turning -0 into +0)."""
+    low = lowrank(c, q, dtype)
+    if idx is None:
+        return low
+    out = low + np.float32(0.0)
+    flat = out.reshape(-1)
+    idx = np.asarray(idx, np.int64)
+    if idx.size:
+        flat[idx] = round_to(low.reshape(-1)[idx] + np.asarray(vals, np.float32), dtype)
     return out
 
 

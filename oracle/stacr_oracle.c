@@ -19,6 +19,7 @@
  *   orc_residual_act      stacr/layers.py:32,73 and stacr/adaptive.py:1518-1519
  *                         R = X - C Q^T in the activation dtype (fixed fma order, see below)
  *   orc_select_explicit   stacr/adaptive.py:1511-1548  per-chunk top-k_c, then top-k of the union
+ *   orc_lowrank           stacr/compressor.py:128      L = C Q^T in the activation dtype (same chain)
  *
  * Pinning (what checks each function; see tests/test_oracle.py):
  *   orc_select     reference known answers tests/test_integration.py:106-114 (global vs chunk),
@@ -37,6 +38,8 @@
  *                  torch's own dtype-native mm and subtraction on the CPU (the reference's ops), and
  *                  exact zero for X in the span of an orthonormal basis with exact coefficients.
  *   orc_select_explicit  brute force (numpy lexsort per chunk, then over the union) on random data.
+ *   orc_lowrank    torch's own dtype-native mm on the CPU (the reference's unpack op), and
+ *                  orc_residual_act with X = L giving exact zeros.
  *
  * Tie rule.  torch.topk(sorted=False) leaves the choice among equal magnitudes unspecified.  The
  * oracle (and the HIP path) breaks ties by the lowest flat index, and returns indices in
@@ -305,6 +308,21 @@ void orc_residual_act(const float *x, const float *c, const float *q, int64_t ro
             for (int j = 0; j < r; ++j) p = fmaf(ci[j], qe[j], p);
             p = orc_round_dtype(p, code);
             out[i * d + e] = orc_round_dtype(x[i * d + e] - p, code);
+        }
+    }
+}
+
+/* L = rnd(C Q^T) in the activation dtype: the same fp32 chain as orc_residual_act
+ * (stacr/compressor.py:128, the low-rank part of the dense unpack). */
+void orc_lowrank(const float *c, const float *q, int64_t rows, int64_t d, int r, int code, float *out)
+{
+    for (int64_t i = 0; i < rows; ++i) {
+        const float *ci = c + i * r;
+        for (int64_t e = 0; e < d; ++e) {
+            const float *qe = q + e * r;
+            float p = 0.f;
+            for (int j = 0; j < r; ++j) p = fmaf(ci[j], qe[j], p);
+            out[i * d + e] = orc_round_dtype(p, code);
         }
     }
 }

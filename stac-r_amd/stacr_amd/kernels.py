@@ -278,3 +278,39 @@ def weight_grad(g2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, residua
                                    dtype_code(out_dtype), _ptr(db), dtype_code(bias_dtype) if db is not None else 0,
                                    _ptr(ws), ws_bytes.value, _stream(device)), "stacr_weight_grad")
     return dw, db
+
+
+def reconstruct(coeff: torch.Tensor, q: torch.Tensor, residual=None) -> torch.Tensor:
+    """rnd(coeff Q^T) + the dense residual, in coeff's dtype (stacr/compressor.py:127-133,
+    stacr/residual.py:13-20).
+
+    ``residual`` is None or (flat indices, values); with a residual every element gets the
+    addition (zeros away from the entries), as the reference adds the dense tensor.
+    """
+    require_gpu(coeff, "coefficients")
+    coeff = coeff.contiguous()
+    rows, rank = coeff.shape
+    feats = q.shape[0]
+    if q.shape[1] != rank:
+        raise ValueError(f"basis has rank {q.shape[1]}, coefficients {rank}")
+    q = q.to(coeff.dtype).contiguous()
+    dt = dtype_code(coeff.dtype)
+    out = torch.empty(rows, feats, dtype=coeff.dtype, device=coeff.device)
+    idx = values = None
+    nnz, ib = 0, 4
+    if residual is not None:
+        idx, values = residual
+        nnz = idx.numel()
+        if nnz:
+            if idx.dtype not in (torch.int32, torch.int64):
+                idx = idx.to(torch.int64)
+            idx = idx.contiguous()
+            ib = idx.element_size()
+            values = values.to(coeff.dtype).contiguous()
+            if values.numel() != nnz:
+                raise ValueError("residual indices and values differ in length")
+    L = _lib.load()
+    _lib.check(L.stacr_reconstruct(_ptr(coeff), _ptr(q), dt, rows, feats, rank, _ptr(idx) if nnz else None, ib,
+                                   _ptr(values) if nnz else None, nnz, 1 if residual is not None else 0, _ptr(out),
+                                   _stream(coeff.device)), "stacr_reconstruct")
+    return out

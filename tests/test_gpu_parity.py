@@ -380,6 +380,36 @@ def test_weight_grad_int64_indices(dev):
     assert rel_l2(_np(a), _np(b)) <= 1e-6
 
 
+@pytest.mark.parametrize("rows,d_in,d_out,rank,bias,dtype,lognormal", [
+    (4096, 2048, 512, 16, False, "bf16", False),   # two parts, rank 16 without bias, many records a feature
+    (2000, 3000, 272, 15, True, "f16", False),     # three parts of 1000, rank 15 + bias, partial last block
+    (3072, 1024, 1024, 8, True, "bf16", True),     # one part, skewed columns
+])
+def test_weight_grad_matrix_core_shapes(dev, rows, d_in, d_out, rank, bias, dtype, lognormal):
+    """The matrix-core path (16-bit G, rank + bias <= 16) against the oracle at shapes where a
+    part's Q rows span two LDS stages, features have more light records a block than the two the
+    streaming kernel loads with the operands, and parts do not cover whole 1024-feature spans."""
+    from stacr_amd import kernels
+
+    announce("grad tiles shape", rows, d_in, d_out, rank, bias, dtype)
+    x = make_activation(rows, d_in, lognormal=lognormal).to(dev, DT[dtype])
+    q = make_basis(d_in, rank).to(dev, DT[dtype])
+    g = make_grad(rows, d_out).to(dev, DT[dtype])
+    coeff, idx, data, scale = kernels.save(x, q, mode="chunk_topk", budget=0.01, chunk_rows=512, bits=8)
+    dw, db = kernels.weight_grad(g, coeff, q, (idx, data, scale), 8, False, DT[dtype], DT[dtype] if bias else None)
+    torch.cuda.synchronize()
+    oidx = idx.cpu().numpy().astype(np.int64)
+    ovals = orc.dequantize(data.cpu().numpy().view(np.int8), np.float32(scale.item()), 8, oidx.size)
+    odw, odb = orc.weight_grad(_np(g), _np(coeff), _np(q), oidx, ovals, d_in)
+    assert rel_l2(_np(dw), odw) <= TOL[dtype]
+    if dtype == "bf16":
+        assert_rounded_once_bf16(_np(dw), odw, what="dW")
+    if bias:
+        assert rel_l2(_np(db), odb) <= TOL[dtype]
+    else:
+        assert db is None
+
+
 @pytest.mark.parametrize("dtype,transposed", [("bf16", True), ("f16", False)])
 def test_weight_grad_matrix_core_path_is_deterministic(dev, dtype, transposed):
     """16-bit G at rank 8: every sum of the weight gradient has a fixed order (light entries by one

@@ -127,13 +127,49 @@ def test_empty_selection_is_explicit_and_frozen_weights_are_skipped():
 @pytest.mark.parametrize(
     "config,overrides,expected",
     [(None, {}, 50), ({}, {}, 50), ({"turbo_after_step": None}, {}, None), ({"turbo_after_step": 17}, {}, 17),
-     ({"turbo_after_step": 17}, {"turbo_after_step": None}, None)],
+     ({"turbo_after_step": 17}, {"turbo_after_step": None}, None),
+     (stacr_amd.STACRConfig(), {}, None), (stacr_amd.STACRConfig(), {"turbo_after_step": 50}, 50)],
 )
 def test_apply_stacr_honors_explicit_turbo_configuration(config, overrides, expected):
+    """Reference tests/test_surgery.py:130-148, including the compressor's config dataclass."""
     model = nn.Sequential(nn.Linear(12, 7))
     layers = apply_stacr(model, config, surface="all", min_features=1, rank=3, **overrides)
     assert layers[0].turbo_after_step == expected
     assert STACRLinear.from_linear(nn.Linear(12, 7), rank=3).turbo_after_step is None
+    assert stacr_amd.STACRConfig().turbo_after_step is None
+
+
+def test_saved_tensor_hooks_never_compress_parameter_views():
+    """Reference tests/test_adaptive.py:222-226: a parameter, or a view of one (linear autograd
+    saves the transposed weight), is never compressed; activations of the right size are."""
+    from stacr_amd.compressor import STACRCompressor, STACRConfig
+
+    weight = nn.Parameter(torch.randn(7, 16))
+    compressor = STACRCompressor(STACRConfig(min_features=1, min_numel=1))
+    assert not compressor.should_compress(weight.t())
+    assert not compressor.should_compress(weight)
+    assert compressor.should_compress(torch.randn(3, 16))
+    assert not compressor.should_compress(torch.randn(16))  # one dimension
+    assert not compressor.should_compress(torch.arange(48).reshape(3, 16))  # integer
+    big = STACRCompressor(STACRConfig())  # defaults: >= 128 features and >= 4096 elements
+    assert not big.should_compress(torch.randn(64, 64)) and not big.should_compress(torch.randn(8, 128))
+    assert big.should_compress(torch.randn(32, 128))
+    # pack passes ineligible tensors (and everything during warmup) through untouched
+    assert compressor.pack(weight) is weight
+    warm = STACRCompressor(STACRConfig(min_features=1, min_numel=1, warmup_steps=3))
+    t = torch.randn(4, 16)
+    assert warm.pack(t) is t and warm.unpack(t) is t
+
+
+def test_sparse_residual_dense_scatters_flat_indices():
+    """stacr/residual.py:13-20: zeros away from the entries, the values at their flat indices."""
+    from stacr_amd.compressor import SparseResidual
+
+    r = SparseResidual((2, 3), torch.tensor([5, 0, 3]), torch.tensor([1.5, -2.0, 4.0]))
+    d = r.dense(device=torch.device("cpu"), dtype=torch.float32)
+    assert torch.equal(d, torch.tensor([[-2.0, 0.0, 0.0], [4.0, 0.0, 1.5]]))
+    empty = SparseResidual((2, 2), torch.empty(0, dtype=torch.long), torch.empty(0))
+    assert torch.equal(empty.dense(device=torch.device("cpu"), dtype=torch.bfloat16), torch.zeros(2, 2, dtype=torch.bfloat16))
 
 
 def test_conv1d_is_wrapped_transposed_and_basis_follows_weight_device():

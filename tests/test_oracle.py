@@ -196,6 +196,55 @@ def test_residual_matches_torch_dtype_native_ops(dtype, rank):
     assert np.mean(one != ref) > 0.02
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("rank", [1, 5, 8, 16])
+def test_reconstruct_matches_torch_dtype_native_ops(dtype, rank):
+    """The saved-tensor hooks' unpack (stacr/compressor.py:127-133, stacr/residual.py:13-20) with
+    torch's CPU ops: coeff.mm(basis.t()) in the dtype, plus the dense residual (zeros elsewhere)."""
+    import torch
+
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dtype]
+    rng = np.random.default_rng(10 + rank)
+    q = torch.from_numpy(np.linalg.qr(rng.standard_normal((384, rank)))[0].astype(np.float32)).to(tdt)
+    x = torch.from_numpy((rng.standard_normal((96, 384)) * 2).astype(np.float32)).to(tdt)
+    c = x.mm(q)
+    low = c.mm(q.t())
+    assert np.array_equal(orc.lowrank(c.float().numpy(), q.float().numpy(), dtype), low.float().numpy())
+    idx = np.sort(rng.choice(96 * 384, 500, replace=False))
+    vals = torch.from_numpy(rng.standard_normal(500).astype(np.float32)).to(tdt)
+    dense = torch.zeros(96 * 384, dtype=tdt)
+    dense[torch.from_numpy(idx)] = vals
+    ref = (low + dense.reshape(96, 384)).float().numpy()
+    got = orc.reconstruct(c.float().numpy(), q.float().numpy(), idx, vals.float().numpy(), dtype)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))  # bits, signed zeros included
+    assert np.array_equal(orc.reconstruct(c.float().numpy(), q.float().numpy(), None, None, dtype), low.float().numpy())
+
+
+def test_reconstruct_closed_forms_and_signed_zeros():
+    """Unit basis vectors and exact coefficients give X back exactly; an empty residual still turns
+    -0 into +0 (the reference adds a zero tensor), while no residual leaves -0; C = 0 gives the
+    dense residual."""
+    rng = np.random.default_rng(4)
+    q = np.zeros((40, 4), np.float32)
+    q[[3, 9, 17, 31], [0, 1, 2, 3]] = 1.0
+    c = rng.integers(-5, 5, (16, 4)).astype(np.float32)
+    assert np.array_equal(orc.reconstruct(c, q, None, None, "bf16"), c @ q.T)
+    # a tiny negative product rounds to -0 in fp16 (the chain itself never yields -0 from +0)
+    ct, qt = np.array([[-1e-8]], np.float32), np.array([[1.0]], np.float32)
+    low = orc.lowrank(ct, qt, "f16")
+    assert low[0, 0] == 0 and np.signbit(low[0, 0])
+    assert np.signbit(orc.reconstruct(ct, qt, None, None, "f16")[0, 0])
+    assert not np.signbit(orc.reconstruct(ct, qt, np.zeros(0, np.int64), np.zeros(0, np.float32), "f16")[0, 0])
+    # at an entry: rnd(L + v), with L = -0 and v = -0 staying -0
+    assert np.signbit(orc.reconstruct(ct, qt, np.array([0]), np.array([-0.0], np.float32), "f16")[0, 0])
+    idx = np.array([0, 7, 79], np.int64)
+    vals = np.array([1.5, -2.0, 3.25], np.float32)
+    out = orc.reconstruct(np.zeros((2, 4), np.float32), q, idx, vals, "f32")
+    want = np.zeros(80, np.float32)
+    want[idx] = vals
+    assert np.array_equal(out.reshape(-1), want)
+
+
 # ------------------------------------------------------------------ weight gradient closed forms
 def test_weight_grad_full_budget_equals_dense():
     rng = np.random.default_rng(5)
