@@ -39,10 +39,19 @@ _SCALE_CODES = {v: k for k, v in _SCALE_DTYPES.items()}
 
 
 # ---------------------------------------------------------------- scale records
+def _record_code(rec: torch.Tensor) -> torch.Tensor:
+    """The dtype code of a scale record, as a (1,) device tensor (not read back)."""
+    return rec.view(torch.int32)[2:3]
+
+
+def _scale_from_record(rec: torch.Tensor, code: int) -> torch.Tensor:
+    """The reference's scale tensor, shape (1,), in the dtype `code` names (a device-side cast)."""
+    return rec.view(torch.float64)[:1].to(_SCALE_DTYPES[int(code)])
+
+
 def _scale_record_to_tensor(rec: torch.Tensor) -> torch.Tensor:
     """The reference's scale tensor, shape (1,), in the dtype the record names (reads 4 bytes back)."""
-    code = int(rec.view(torch.int32)[2].item())
-    return rec.view(torch.float64)[:1].to(_SCALE_DTYPES[code])
+    return _scale_from_record(rec, int(_record_code(rec).item()))
 
 
 def _tensor_to_scale_record(scale: torch.Tensor) -> torch.Tensor:
@@ -688,34 +697,35 @@ class STACRFunction(torch.autograd.Function):
         rank = basis_c.shape[1]
         chunk = int(config.get("chunk_size", 512))
         coeff, idx, values, energy = save(x2d, basis_c, budget if mode == "topk" else 0.0, chunk)
-        # one device-to-host read per forward: the rank and refresh policy consume the energies
-        energy_host = energy.tolist()
-        skipped = gate is not None and mode in ("topk", "block_sparse") and energy_host[0] < gate
+        # The host reads of a forward: the energies (the rank controller, refresh triggers and skip
+        # gate consume them every step, as in the reference) and the dtype code of each quantized
+        # scale, fetched together in one transfer after every kernel is queued.  Only a skip gate
+        # needs the energy first, to decide whether the residual is kept.
+        energy_host = None
+        if gate is not None and mode in ("topk", "block_sparse"):
+            energy_host = energy.tolist()
+        skipped = energy_host is not None and energy_host[0] < gate
         if skipped:
             idx = values = None
         elif mode == "block_sparse":
             idx, values = select_block_sparse(x2d, coeff, basis_c, budget, chunk,
                                               int(config.get("residual_block_size", 16)))
-        if not recomputing:
-            _record_energy(layer_state, energy_host, rank, coeff.shape[0], schedule_step)
-            if skipped:
-                layer_state["skipped_residuals"] = layer_state.get("skipped_residuals", 0) + 1
-            if not config.get("use_fused_kernel", False):
-                layer_state["b4_fused_kernel_route"] = "disabled"
-                layer_state["b4_numerical_parity_error"] = None
 
-        coeff_scale = None
+        coeff_rec = None
         if config.get("quantize_coefficients", False):
             if int(config.get("quantize_bits", 8)) != 8:
                 raise ValueError(f"Only int8 coefficient quantization supported, got {config.get('quantize_bits')}")
-            coeff_saved, coeff_scale = quantize_int8(coeff)
+            if coeff.numel():
+                coeff_saved, rec = _quantize_record(coeff, 8)
+                coeff_saved, coeff_rec = coeff_saved.reshape(coeff.shape), (rec,)
+            else:
+                coeff_saved, coeff_rec = quantize_int8(coeff)  # (no record: the reference's ones scale)
         else:
             coeff_saved = coeff
-        tensors = [coeff_saved, weight] + ([coeff_scale] if coeff_scale is not None else [])
-        tensors += [bias] if bias is not None else []
         ctx.index_compression_mode = config.get("index_compression", "none")
         ctx.index_compression_nnz, ctx.index_compression_B_flat = 0, b_flat
         ctx.index_compression_N, ctx.index_compression_original_dtype = in_features, torch.int32
+        streams, stored, res_rec = [], None, None
         if idx is not None:
             # the save emits ascending flat indices, which is both the row order CSR needs and the
             # sorted order delta needs, so no permutation of the values is required
@@ -728,8 +738,35 @@ class STACRFunction(torch.autograd.Function):
                     streams = [deltas, base]
                 ctx.index_compression_nnz = idx.numel()
                 ctx.index_compression_original_dtype = idx.dtype
-            stored, scale = _quantize_residual(values, quant_res, res_bits, ctx)
-            tensors += [stored] + streams + ([scale] if scale is not None else [])
+            stored, res_rec = _quantize_residual_record(values, quant_res, res_bits, ctx)
+
+        # the one transfer: energies (unless already read) and the records' dtype codes
+        reads = [] if energy_host is not None or recomputing else [energy.to(torch.float64)]
+        recs = [r for r in (coeff_rec, res_rec) if isinstance(r, tuple)]
+        reads += [_record_code(r[0]).to(torch.float64) for r in recs]
+        host = torch.cat(reads).tolist() if reads else []
+        if energy_host is None and not recomputing:
+            energy_host, host = host[:energy.numel()], host[energy.numel():]
+        codes = {id(r): host[i] for i, r in enumerate(recs)}
+        coeff_scale = None
+        if coeff_rec is not None:
+            coeff_scale = _scale_from_record(coeff_rec[0], codes[id(coeff_rec)]) if isinstance(coeff_rec, tuple) else coeff_rec
+        res_scale = None
+        if res_rec is not None:
+            res_scale = _scale_from_record(res_rec[0], codes[id(res_rec)]) if isinstance(res_rec, tuple) else res_rec
+
+        if not recomputing:
+            _record_energy(layer_state, energy_host, rank, coeff.shape[0], schedule_step)
+            if skipped:
+                layer_state["skipped_residuals"] = layer_state.get("skipped_residuals", 0) + 1
+            if not config.get("use_fused_kernel", False):
+                layer_state["b4_fused_kernel_route"] = "disabled"
+                layer_state["b4_numerical_parity_error"] = None
+
+        tensors = [coeff_saved, weight] + ([coeff_scale] if coeff_scale is not None else [])
+        tensors += [bias] if bias is not None else []
+        if idx is not None:
+            tensors += [stored] + streams + ([res_scale] if res_scale is not None else [])
         first_residual = 2 + (coeff_scale is not None) + (bias is not None)
         if config.get("cpu_offload", False) and tensors[0].is_cuda:
             ctx.cpu_offload = True
@@ -800,6 +837,23 @@ class STACRFunction(torch.autograd.Function):
                 values = _dequantize_residual(values, _onload(saved[pos], device), ctx)
             residual = (idx, values)
         return _factor_grads(ctx, g2d, weight, bias, coefficients, ctx.basis, residual)
+
+
+def _quantize_residual_record(values, quantize: bool, bits: int, ctx):
+    """(stored values, (record,) or a scale tensor or None): as _quantize_residual, but a non-empty
+    tensor's scale stays a device record whose dtype code the caller reads with its others."""
+    if not quantize:
+        return values, None
+    if not values.numel():
+        return _quantize_residual(values, quantize, bits, ctx)
+    if bits not in (4, 8):
+        raise ValueError(f"Unsupported residual_quantize_bits: {bits}")
+    data, rec = _quantize_record(values, bits)
+    if bits == 4:
+        ctx.residual_orig_len = values.numel()
+    else:
+        data = data.reshape(values.shape)
+    return data, (rec,)
 
 
 def _quantize_residual(values, quantize: bool, bits: int, ctx):
@@ -1006,13 +1060,31 @@ class STACRLinear(nn.Module):
         return layer.train(module.training)
 
     # ---------------------------------------------------------------- persistent state
+    # Host mirrors of the one-element buffers step_counter and _basis_initialized, so the forward
+    # does not read them back from the GPU: a mirror holds the value, the tensor and its in-place
+    # version counter (host metadata), and is trusted only while both still match, so a write from
+    # outside (fill_, load_state_dict's copy_, a move to another device) forces one fresh read.
+    def _host_value(self, name: str):
+        t = getattr(self, name)
+        cached = self.__dict__.get("_host_" + name)
+        if cached is not None and cached[1] is t and cached[2] == t._version:
+            return cached[0]
+        v = t.item()
+        self.__dict__["_host_" + name] = (v, t, t._version)
+        return v
+
+    def _set_host_value(self, name: str, value) -> None:
+        t = getattr(self, name)
+        self.__dict__["_host_" + name] = (value, t, t._version)
+
     @property
     def basis_initialized(self) -> bool:
-        return bool(self._basis_initialized.item())
+        return bool(self._host_value("_basis_initialized"))
 
     @basis_initialized.setter
     def basis_initialized(self, value: bool) -> None:
         self._basis_initialized.fill_(bool(value))
+        self._set_host_value("_basis_initialized", bool(value))
 
     def _save_to_state_dict(self, destination, prefix, keep_vars):
         plain = {k: v for k, v in self.layer_state.items() if isinstance(v, (str, int, float, bool, list, dict,
@@ -1070,7 +1142,7 @@ class STACRLinear(nn.Module):
 
     def _get_schedule_step(self) -> int:
         runtime = self.layer_state.get("_optimizer_step_runtime") if self._use_optimizer_step_schedule() else None
-        return int(runtime) if runtime is not None else int(self.step_counter.item())
+        return int(runtime) if runtime is not None else int(self._host_value("step_counter"))
 
     _get_forward_schedule_step = _get_schedule_step
 
@@ -1223,7 +1295,7 @@ class STACRLinear(nn.Module):
             self._init_basis_from_batch(x.reshape(-1, self.in_features))
         step_tensor = self.step_counter
         if recomputing:  # the counter already advanced past the forward being recomputed
-            step_tensor = self.step_counter.new_tensor([max(int(self.step_counter.item()) - 1, 0)])
+            step_tensor = self.step_counter.new_tensor([max(int(self._host_value("step_counter")) - 1, 0)])
             st["skipped_recompute"] = st.get("skipped_recompute", 0) + 1
         schedule_step = self._get_forward_schedule_step()
         st["_schedule_step"] = schedule_step
@@ -1252,7 +1324,7 @@ class STACRLinear(nn.Module):
             st["_schedule_step"] = schedule_step
             step_tensor = self.step_counter.new_tensor([recorded])
         elif not recomputing:
-            guard.record_layer(self, (basis, schedule_step, int(step_tensor.item())))
+            guard.record_layer(self, (basis, schedule_step, int(self._host_value("step_counter"))))
 
         config_dict = cfg.to_dict()
         residual_off = basis is not None and not sparse_only and self._residual_off(schedule_step)
@@ -1264,7 +1336,9 @@ class STACRLinear(nn.Module):
                 st["b1_route_step_count"] = st.get("b1_route_step_count", 0) + 1
             elif residual_off:
                 st["b1_generic_fallback_count"] = st.get("b1_generic_fallback_count", 0) + 1
+            steps = int(self._host_value("step_counter"))
             self.step_counter += 1
+            self._set_host_value("step_counter", steps + 1)
             if not sparse_only and self.basis_initialized and self._should_update_basis():
                 self._update_basis_oja(x.reshape(-1, self.in_features))
         return output

@@ -205,6 +205,36 @@ def _saved_factors(out, cfg, rows, d_in):
     return coeff, idx, values
 
 
+def test_training_forward_reads_the_gpu_once(dev, monkeypatch):
+    """After the first forward (which fits the basis), a training forward with int8 coefficients and
+    int8 residual values reads the GPU once: the energies and both scales' dtype codes in one
+    transfer (the step counter and the initialization flag have host mirrors)."""
+    announce("adaptive host reads")
+    cfg = _cfg(rank=8, residual_mode="topk", residual_budget=0.01, quantize_coefficients=True,
+               quantize_residuals=True, residual_quantize_bits=8, freeze_basis_after_warmup=True)
+    layer = _layer(dev, 512, 384, cfg)
+    x = make_activation(1024, 512).to(dev)
+    layer(x).sum().backward()
+    reads = []
+    for name in ("item", "tolist", "__bool__", "__int__", "__float__", "__index__"):
+        orig = getattr(torch.Tensor, name)
+
+        def counted(t, *a, _orig=orig, _name=name, **k):
+            if t.is_cuda:
+                reads.append(_name)
+            return _orig(t, *a, **k)
+
+        monkeypatch.setattr(torch.Tensor, name, counted)
+    out = layer(x)
+    monkeypatch.undo()
+    assert reads == ["tolist"]
+    saved = out.grad_fn.saved_tensors
+    assert saved[2].dtype == torch.float32 and saved[-1].dtype == torch.float32  # both scales, x's dtype
+    assert int(layer.step_counter) == 2 and layer.basis_initialized
+    layer.step_counter.fill_(7)  # a write from outside: the mirror notices the version change
+    assert layer._get_schedule_step() == 7 or layer._use_optimizer_step_schedule()
+
+
 @pytest.mark.parametrize("compression,bits,offload", [("none", 8, False), ("csr", 4, False), ("delta", 8, True),
                                                       ("csr", 8, True)])
 def test_saved_layout_and_weight_gradient_against_oracle(dev, compression, bits, offload):
