@@ -1584,6 +1584,499 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
     }
 }
 
+// ------------------------------------------------------------------ candidate path (bf16, batched)
+// The projection pass keeps, per workgroup, its local candidates: the elements in the level-0 bins
+// at or above the cut where the workgroup's own count from the top reaches a quota (several times
+// its share of the chunk's k), in ascending flat order, with their residuals; the residual is not
+// stored.  The chunk's level-0 bin B0 is known after the pass.  A workgroup whose cut is at or
+// below B0, and whose candidates fit kCandCap, holds every element of bin B0 and above among its
+// candidates, so the level-1 pass and the emission work on those lists; any other workgroup
+// recomputes its residuals from X, C and the basis there (the same values, rarely needed).  The
+// selection is the same as the full passes'.
+constexpr int kCandCap = 2048;               // candidates a workgroup keeps
+constexpr int kCandPer = kCandCap / kBlock;  // candidates a thread reads (consecutive)
+static_assert(kCandPer == 8, "one 16-byte vector of bf16 candidate values per thread");
+
+struct CandMeta {
+    uint32_t cut;    // level-0 bin of the workgroup's cut
+    uint32_t count;  // candidates (more than kCandCap: the list overflowed and is not used)
+};
+
+__device__ __forceinline__ uint32_t bf16_key(uint32_t bits16)
+{
+    return __float_as_uint(bf16_bits_to_f(bits16 & 0xffffu)) & 0x7fffffffu;
+}
+
+// Pass 1: as k_proj_hist_b (coefficients computed or loaded, level-0 histogram with its coarse
+// sums, max key), then the workgroup's cut and its candidates.
+template <int R>
+__global__ __launch_bounds__(kBlock) void k_proj_cand(SaveGeom g, FastGeom fg, const uint16_t *__restrict__ x,
+                                                      const float *__restrict__ qp, uint16_t *__restrict__ coeff,
+                                                      uint32_t *__restrict__ hist, uint32_t *__restrict__ maxkey,
+                                                      const uint16_t *__restrict__ coeff_in,
+                                                      uint32_t *__restrict__ coarse, uint32_t quota,
+                                                      uint32_t *__restrict__ cand_idx, uint16_t *__restrict__ cand_val,
+                                                      CandMeta *__restrict__ meta)
+{
+    constexpr int DT = STACR_DTYPE_BF16, V = 8, NB = Batch<R>::NB;
+    using T = typename Act<DT>::T;
+    // the packed residuals wait for the cut in LDS where they fit in 32 KiB (rank 8; registers
+    // would cost this kernel its second wave per SIMD), else in registers
+    constexpr bool kLdsRes = NB * kBlock * 16 <= 32768;
+    __shared__ uint32_t s_hist[kBins];
+    __shared__ __align__(16) float s_part[kWaves * 64];
+    __shared__ __align__(16) float s_c[kWaves * 64];
+    __shared__ uint32_t s_wmax[kWaves];
+    __shared__ uint32_t s_wt[kWaves * NB];
+    __shared__ uint32_t s_cut;
+    __shared__ uint4 s_res[kLdsRes ? NB * kBlock : 1];
+    int64_t chunk, row0, row_end;
+    wg_rows(g, blockIdx.x, chunk, row0, row_end);
+    if (row0 >= row_end) return;  // a trailing workgroup with no rows (uniform; later passes skip it)
+    const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t col = (int64_t)u * V, colc = min(col, g.d - V);
+    const bool col_ok = col < g.d;
+    FastLoads<DT, R, V, false> ld;
+    ld.issue(g, slot, row0, row_end, colc, reinterpret_cast<const T *>(x), nullptr, false);
+    float q[V][R];
+    uint4 qw[R];
+    const uint16_t *qph = reinterpret_cast<const uint16_t *>(qp + 2 * g.d * R);
+#pragma unroll
+    for (int j = 0; j < R; ++j) qw[j] = *reinterpret_cast<const uint4 *>(qph + j * g.d + colc);
+    for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
+    uint32_t kmax = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const uint32_t w[4] = {qw[j].x, qw[j].y, qw[j].z, qw[j].w};
+#pragma unroll
+        for (int e = 0; e < V; ++e) q[e][j] = Act<DT>::ld((T)((w[e / 2] >> (16 * (e & 1))) & 0xffffu));
+    }
+    basis_mask<R, V>(col_ok, q);
+    float c[64];
+    if (coeff_in) {
+        batch_coeff_load<DT, R>(reinterpret_cast<const T *>(coeff_in), g.rank, ld.rows, row_end, fg.c_vec != 0, c);
+    } else {
+        float acc[64];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const bool live = col_ok && ld.rows[i] < row_end;
+            const uint4 xr = live ? ld.raw[i] : make_uint4(0u, 0u, 0u, 0u);
+            const uint32_t xw[4] = {xr.x, xr.y, xr.z, xr.w};
+#pragma unroll
+            for (int j = 0; j < R; ++j) {
+                const uint32_t w[4] = {qw[j].x, qw[j].y, qw[j].z, qw[j].w};
+                float sum = 0.f;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) sum = dot2<DT>(xw[k], w[k], sum);
+                acc[i * R + j] = sum;
+            }
+        }
+        batch_coeff_from_acc<DT, R>(acc, fg.W, slot, s_part, s_c, row0, g.rpi, row_end, g.rank,
+                                    reinterpret_cast<T *>(coeff), c);
+    }
+    // residuals packed as bf16 (exact), the histogram and the max key
+    uint4 rp[kLdsRes ? 1 : NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        if (!(col_ok && ld.rows[i] < row_end)) continue;
+        float xv[V], r[V];
+        ld.x_at(i, true, xv);
+        batch_residual<DT, R, V>(xv, c + i * R, q, r);
+        const uint4 pr = pack_raw<DT, V>(r);
+        if constexpr (kLdsRes) s_res[i * kBlock + threadIdx.x] = pr;
+        else rp[i] = pr;
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
+            atomicAdd(&s_hist[key >> kDigitShift[0]], 1u);
+            kmax = max(kmax, key);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, off, 64));
+    if (lane == 0) s_wmax[wave] = kmax;
+    __syncthreads();
+    // the cut: the highest bin where the count from the top reaches the quota (bin 0 when the
+    // workgroup has fewer keys), from 64 sums of 32 bins and then the chosen 32 bins
+    if (wave == 0) {
+        constexpr int FB = kBins / kCoarse;
+        uint32_t suf = 0u;
+#pragma unroll 8
+        for (int b = 0; b < FB; ++b) suf += s_hist[lane * FB + b];
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t y = __shfl_down(suf, off, 64);
+            if (lane + off < 64) suf += y;
+        }
+        const uint64_t m = __ballot(suf >= quota);
+        uint32_t cut = 0u;
+        if (m != 0ull) {
+            const int cb = 63 - __clzll(m);
+            const uint32_t need1 = quota - (cb < 63 ? (uint32_t)__shfl((int)suf, cb + 1, 64) : 0u);
+            const int fl = lane & (FB - 1);
+            uint32_t sf = s_hist[cb * FB + fl];
+#pragma unroll
+            for (int off = 1; off < FB; off <<= 1) {
+                const uint32_t y = __shfl_down(sf, off, FB);
+                if (fl + off < FB) sf += y;
+            }
+            const uint64_t mf = __ballot(sf >= need1) & ((1ull << FB) - 1);
+            cut = (uint32_t)(cb * FB + (mf ? 63 - __clzll(mf) : 0));
+        }
+        if (lane == 0) s_cut = cut;
+    }
+    __syncthreads();
+    const uint32_t cut = s_cut;
+    // the candidates in ascending flat order: (iteration, wave, lane, element)
+    uint32_t msk[NB], cnt[NB], incl[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        uint32_t m = 0u;
+        if (col_ok && ld.rows[i] < row_end) {
+            const uint4 pr = kLdsRes ? s_res[i * kBlock + threadIdx.x] : rp[kLdsRes ? 0 : i];
+            const uint32_t w[4] = {pr.x, pr.y, pr.z, pr.w};
+#pragma unroll
+            for (int e = 0; e < V; ++e)
+                m |= (bf16_key(w[e >> 1] >> (16 * (e & 1))) >> kDigitShift[0]) >= cut ? 1u << e : 0u;
+        }
+        msk[i] = m;
+        cnt[i] = incl[i] = (uint32_t)__popc(m);
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const uint32_t y = __shfl_up(incl[i], off, 64);
+            if (lane >= off) incl[i] += y;
+        }
+    }
+    if (lane == 63)
+#pragma unroll
+        for (int i = 0; i < NB; ++i) s_wt[wave * NB + i] = incl[i];
+    __syncthreads();
+    uint32_t before_iter = 0u;
+    uint32_t *ci = cand_idx + (int64_t)blockIdx.x * kCandCap;
+    uint16_t *cv = cand_val + (int64_t)blockIdx.x * kCandCap;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        uint32_t waves_before = 0u, iter_total = 0u;
+#pragma unroll
+        for (int wv = 0; wv < kWaves; ++wv) {
+            const uint32_t t = s_wt[wv * NB + i];
+            waves_before += wv < wave ? t : 0u;
+            iter_total += t;
+        }
+        uint32_t pos = before_iter + waves_before + incl[i] - cnt[i];
+        if (msk[i]) {
+            const uint4 pr = kLdsRes ? s_res[i * kBlock + threadIdx.x] : rp[kLdsRes ? 0 : i];
+            const uint32_t wd[4] = {pr.x, pr.y, pr.z, pr.w};
+            for (uint32_t m = msk[i]; m != 0u; m &= m - 1u, ++pos) {
+                const int e = __builtin_ctz(m);
+                uint32_t word = wd[0];
+#pragma unroll
+                for (int k = 1; k < 4; ++k) word = (e >> 1) == k ? wd[k] : word;
+                if (pos < (uint32_t)kCandCap) {
+                    ci[pos] = (uint32_t)(ld.rows[i] * g.d + col + e);
+                    cv[pos] = (uint16_t)((word >> (16 * (e & 1))) & 0xffffu);
+                }
+            }
+        }
+        before_iter += iter_total;
+    }
+    if (threadIdx.x == 0) meta[blockIdx.x] = CandMeta{cut, before_iter};
+    // this workgroup's copy of the chunk histogram and of the max key (as k_proj_hist_b)
+    const int copy = (int)(blockIdx.x % g.hcopies);
+    uint32_t *gh = hist + ((chunk * 3 + 0) * g.hcopies + copy) * kBins;
+    for (int b = threadIdx.x; b < kBins; b += kBlock)
+        if (s_hist[b]) atomicAdd(&gh[b], s_hist[b]);
+    if (threadIdx.x < kCoarse) {
+        uint32_t sum = 0u;
+#pragma unroll 8
+        for (int b = 0; b < kBins / kCoarse; ++b) sum += s_hist[threadIdx.x * (kBins / kCoarse) + b];
+        if (sum) atomicAdd(&coarse[(chunk * g.hcopies + copy) * kCoarse + threadIdx.x], sum);
+    }
+    if (threadIdx.x == 0) {
+        uint32_t mx = 0u;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) mx = max(mx, s_wmax[w]);
+        if (mx) atomicMax(maxkey + copy * kMaxKeyStride, mx);
+    }
+}
+
+// One vector's residual recomputed from X, C and the basis (the candidate passes' fallback, one
+// iteration at a time so that it does not set the kernels' register budget); false outside the
+// matrix or the workgroup's rows.
+template <int R>
+__device__ __forceinline__ bool cand_residual(const SaveGeom &g, const uint16_t *__restrict__ x,
+                                              const uint16_t *__restrict__ coeff, const float (&q)[8][R], int64_t row,
+                                              int64_t row_end, int64_t col, bool col_ok, float (&r)[8])
+{
+    constexpr int DT = STACR_DTYPE_BF16;
+    const bool live = col_ok && row < row_end;
+    float xv[8], c[R];
+    unpack_raw<DT, 8>(load_raw<DT, 8>(x + row * g.d + col, live), xv);
+    load_coeff<DT, R>(coeff, row, g.rank, live, c);
+    batch_residual<DT, R, 8>(xv, c, q, r);
+    return live;
+}
+
+// A thread's 8 consecutive candidate values (16 bytes), and their flat indices; entries at or past
+// `count` are read (inside the workgroup's region) but not used.
+struct CandVals {
+    uint32_t w[4];
+    __device__ __forceinline__ uint32_t bits(int j) const { return (w[j >> 1] >> (16 * (j & 1))) & 0xffffu; }
+};
+
+// Level 1 (bf16, batched, candidates): the level-0 selection, then the histogram of key bits
+// 19..16 inside B0 and the per-workgroup records of k_refine_hist_b, from the candidates.
+template <int R, int HC>
+__global__ __launch_bounds__(kBlock) void k_refine_cand(SaveGeom g, FastGeom fg, const uint16_t *__restrict__ x,
+                                                        const float *__restrict__ qp, const uint16_t *__restrict__ coeff,
+                                                        uint32_t *__restrict__ hist, SelState *__restrict__ state,
+                                                        uint32_t k_full, uint32_t k_last, uint32_t *__restrict__ maxkey,
+                                                        uint32_t *__restrict__ fold, int64_t fold_stride,
+                                                        const uint32_t *__restrict__ coarse,
+                                                        const uint16_t *__restrict__ cand_val,
+                                                        const CandMeta *__restrict__ meta)
+{
+    constexpr int NB = Batch<R>::NB;
+    __shared__ uint32_t s_hist[kBins];
+    __shared__ uint32_t s_above[kWaves];
+    int64_t chunk, row0, row_end;
+    wg_rows(g, blockIdx.x, chunk, row0, row_end);
+    const bool has_rows = row0 < row_end;
+    const SelState sp = prev_state(0, state, chunk, g.n_chunks, k_full, k_last);
+    uint32_t cv[HC];
+#pragma unroll
+    for (int h = 0; h < HC; ++h) cv[h] = coarse[(chunk * HC + h) * kCoarse + (threadIdx.x & 63)];
+    const CandMeta mine = meta[has_rows ? blockIdx.x : 0];
+    // the candidate values go out before the selection's histogram words
+    CandVals vals;
+    {
+        const uint4 v = *reinterpret_cast<const uint4 *>(cand_val + (int64_t)blockIdx.x * kCandCap + kCandPer * threadIdx.x);
+        vals.w[0] = v.x; vals.w[1] = v.y; vals.w[2] = v.z; vals.w[3] = v.w;
+    }
+    for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
+    const SelState sel = select_level0<HC>(cv, hist + chunk * 3 * HC * kBins, sp);
+    if (blockIdx.x % g.wgs_per_chunk == 0 && threadIdx.x == 0) state[chunk * 3 + 0] = sel;
+    if (HC > 1 && blockIdx.x == 0 && threadIdx.x == 0) {  // fold the max key's copies into the first
+        uint32_t m = maxkey[0];
+#pragma unroll
+        for (int c = 1; c < HC; ++c) m = max(m, maxkey[c * kMaxKeyStride]);
+        maxkey[0] = m;
+    }
+    if (!has_rows) {
+        if (threadIdx.x <= 16) fold[threadIdx.x * fold_stride + blockIdx.x] = 0u;
+        return;
+    }
+    const uint32_t prefix = sel.prefix;  // B0
+    const bool valid = mine.count <= (uint32_t)kCandCap && mine.cut <= prefix;  // uniform
+    __syncthreads();  // s_hist is clear
+    uint32_t above = 0u;
+    if (valid) {
+#pragma unroll
+        for (int j = 0; j < kCandPer; ++j) {
+            if (kCandPer * threadIdx.x + j >= mine.count) break;
+            const uint32_t key = bf16_key(vals.bits(j));
+            if ((key >> kDigitShift[0]) == prefix) atomicAdd(&s_hist[(key >> kDigitShift[1]) & (kDigitBins[1] - 1)], 1u);
+            above += (key >> kDigitShift[0]) > prefix;
+        }
+    } else {
+        const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
+        const int64_t col = (int64_t)u * 8, colc = min(col, g.d - 8);
+        const bool col_ok = col < g.d;
+        float q[8][R];
+        basis_issue<R, 8>(qp + g.d * R, g.d, colc, q);
+        basis_mask<R, 8>(col_ok, q);
+#pragma unroll 1
+        for (int i = 0; i < NB; ++i) {
+            float r[8];
+            if (!cand_residual<R>(g, x, coeff, q, row0 + (int64_t)i * g.rpi + slot, row_end, col, col_ok, r)) continue;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
+                if ((key >> kDigitShift[0]) == prefix) atomicAdd(&s_hist[(key >> kDigitShift[1]) & (kDigitBins[1] - 1)], 1u);
+                above += (key >> kDigitShift[0]) > prefix;
+            }
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) above += (uint32_t)__shfl_xor((int)above, off, 64);
+    if ((threadIdx.x & 63) == 0) s_above[threadIdx.x >> 6] = above;
+    __syncthreads();
+    if (threadIdx.x <= 16) {  // cum[b] for b = threadIdx.x (16: above B0 only), as k_refine_hist_b
+        uint32_t c = 0u;
+#pragma unroll
+        for (int wv = 0; wv < kWaves; ++wv) c += s_above[wv];
+        for (int b = threadIdx.x; b < 16; ++b) c += s_hist[b << 7];
+        fold[threadIdx.x * fold_stride + blockIdx.x] = c;
+    }
+    uint32_t *gh = hist + ((chunk * 3 + 1) * HC + blockIdx.x % HC) * kBins;
+    for (int b = threadIdx.x; b < kDigitBins[1]; b += kBlock)
+        if (s_hist[b]) atomicAdd(&gh[b], s_hist[b]);
+}
+
+// Emission (bf16, batched, candidates): the final selection and the workgroup's offset and tie
+// budget as in k_emit_b, then its survivors from the candidate list (or, for a workgroup without a
+// usable list, from recomputed residuals) quantized and written in ascending flat order.
+template <int R, int HC>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) void k_emit_cand(
+    SaveGeom g, FastGeom fg, const uint16_t *__restrict__ x, const float *__restrict__ qp,
+    const uint16_t *__restrict__ coeff, SelState *__restrict__ state, uint32_t chunk_k,
+    const uint32_t *__restrict__ maxkey, OutSpec o, float *scale_out, int to_list, const uint32_t *__restrict__ hist,
+    const uint32_t *__restrict__ fold, int64_t fold_stride, const uint32_t *__restrict__ cand_idx,
+    const uint16_t *__restrict__ cand_val, const CandMeta *__restrict__ meta)
+{
+    constexpr int DT = STACR_DTYPE_BF16, NB = Batch<R>::NB;
+    __shared__ uint32_t s_off[kWaves];
+    __shared__ uint32_t s_wt[kWaves];
+    int64_t chunk, row0, row_end;
+    wg_rows(g, blockIdx.x, chunk, row0, row_end);
+    const int64_t w = blockIdx.x - chunk * g.wgs_per_chunk;
+    const int64_t wg0 = chunk * g.wgs_per_chunk;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const bool has_rows = row0 < row_end;
+    uint32_t hw[HC];
+    {
+        const uint32_t *h1 = hist + (chunk * 3 + 1) * HC * kBins + ((threadIdx.x & 15) << 7);
+#pragma unroll
+        for (int c = 0; c < HC; ++c) hw[c] = h1[c * kBins];
+    }
+    const CandMeta mine = meta[has_rows ? blockIdx.x : 0];
+    // the candidates go out before the selection's and the offsets' words
+    CandVals vals;
+    uint32_t flat[kCandPer];
+    {
+        const int64_t base = (int64_t)blockIdx.x * kCandCap + kCandPer * threadIdx.x;
+        const uint4 v = *reinterpret_cast<const uint4 *>(cand_val + base);
+        const uint4 f0 = *reinterpret_cast<const uint4 *>(cand_idx + base);
+        const uint4 f1 = *reinterpret_cast<const uint4 *>(cand_idx + base + 4);
+        vals.w[0] = v.x; vals.w[1] = v.y; vals.w[2] = v.z; vals.w[3] = v.w;
+        flat[0] = f0.x; flat[1] = f0.y; flat[2] = f0.z; flat[3] = f0.w;
+        flat[4] = f1.x; flat[5] = f1.y; flat[6] = f1.z; flat[7] = f1.w;
+    }
+    SelState sel1;
+    const SelState st = fold_select<HC>(hw, state[chunk * 3 + 0], &sel1);
+    if (w == 0 && threadIdx.x == 0) {
+        state[chunk * 3 + 1] = sel1;
+        state[chunk * 3 + 2] = st;
+    }
+    const uint32_t b1 = (st.prefix >> 16) & 15u;
+    const uint32_t *fhi = fold + (int64_t)(b1 + 1) * fold_stride + wg0;
+    const uint32_t *flo = fold + (int64_t)b1 * fold_stride + wg0;
+    const uint32_t mk = *maxkey;
+    const uint32_t T = st.prefix;
+    const float amax = Act<DT>::rnd(__uint_as_float(mk));
+    const float scale = o.bits ? quant_scale(mk, o.bits, amax) : 1.f;
+    if (!to_list && blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
+    if (!has_rows) return;  // uniform: a trailing workgroup with no rows writes nothing
+    // the workgroup's output offset and tie budget (the earlier workgroups' records)
+    WgOffset wo;
+    {
+        uint32_t gt = 0u, eq = 0u;
+        for (int64_t v = threadIdx.x; v < w; v += kBlock) {
+            const uint32_t hi = fhi[v], lo = flo[v];
+            gt += hi;
+            eq += lo - hi;
+        }
+        const uint32_t gt_before = block_sum(gt, s_off);
+        const uint32_t eq_before = block_sum(eq, s_off);
+        const uint32_t my_eq = flo[w] - fhi[w];
+        const uint32_t take = eq_before >= st.need ? 0u : min(my_eq, st.need - eq_before);
+        wo = WgOffset{(uint32_t)chunk * chunk_k + gt_before + min(st.need, eq_before), take};
+    }
+    auto put = [&](uint32_t pos, uint32_t fl, float rv) {
+        if (pos >= o.cap) {
+            // unreachable when the counts are consistent; never write out of bounds
+        } else if (to_list) {
+            o.list_rbits[pos] = __float_as_uint(rv);
+            o.list_idx[pos] = fl;
+        } else {
+            write_entry<DT>(o, pos, fl, rv, scale);
+        }
+    };
+    const bool valid = mine.count <= (uint32_t)kCandCap && mine.cut <= (T >> kDigitShift[0]);  // uniform
+    if (valid) {
+        uint32_t ngt = 0u, neq = 0u, key[kCandPer];
+#pragma unroll
+        for (int j = 0; j < kCandPer; ++j) {
+            const bool in = kCandPer * threadIdx.x + j < mine.count;
+            key[j] = in ? bf16_key(vals.bits(j)) : 0u;
+            ngt += in && key[j] > T;
+            neq += in && key[j] == T;
+        }
+        uint32_t tot;
+        const uint32_t pre = block_exclusive_scan(ngt | (neq << 16), s_off, &tot);
+        uint32_t gb = pre & 0xffffu, eb = pre >> 16;
+#pragma unroll
+        for (int j = 0; j < kCandPer; ++j) {
+            if (kCandPer * threadIdx.x + j >= mine.count) break;
+            const bool is_gt = key[j] > T, is_eq = key[j] == T;
+            if (is_gt || (is_eq && eb < wo.take)) put(wo.off + gb + min(eb, wo.take), flat[j], bf16_bits_to_f(vals.bits(j)));
+            gb += is_gt;
+            eb += is_eq;
+        }
+        return;
+    }
+    // fallback: the workgroup's residuals recomputed one iteration at a time, survivors compacted
+    // in the order of k_emit_b
+    const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
+    const int64_t col = (int64_t)u * 8, colc = min(col, g.d - 8);
+    const bool col_ok = col < g.d;
+    float q[8][R];
+    basis_issue<R, 8>(qp + g.d * R, g.d, colc, q);
+    basis_mask<R, 8>(col_ok, q);
+    uint32_t before_iter = 0u;  // survivors of the earlier iterations (all waves)
+#pragma unroll 1
+    for (int i = 0; i < NB; ++i) {
+        const int64_t row = row0 + (int64_t)i * g.rpi + slot;
+        float r[8];
+        const bool live = cand_residual<R>(g, x, coeff, q, row, row_end, col, col_ok, r);
+        uint32_t m = 0u;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t k = __float_as_uint(r[e]) & 0x7fffffffu;
+            m |= (live && k > T) ? 1u << e : 0u;
+            m |= (live && k == T) ? 0x100u << e : 0u;
+        }
+        const uint32_t cnt = (uint32_t)__popc(m & 0xffu) | ((uint32_t)__popc(m >> 8) << 16);
+        uint32_t incl = cnt;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t y = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += y;
+        }
+        if (lane == 63) s_wt[wave] = incl;
+        __syncthreads();
+        uint32_t waves_before = 0u, iter_total = 0u;
+#pragma unroll
+        for (int wv = 0; wv < kWaves; ++wv) {
+            const uint32_t t = s_wt[wv];
+            waves_before += wv < wave ? t : 0u;
+            iter_total += t;
+        }
+        __syncthreads();  // s_wt is free for the next iteration
+        const uint32_t ex = before_iter + waves_before + incl - cnt;
+        uint32_t gb = ex & 0xffffu, eb = ex >> 16;
+        while (m != 0u) {
+            const int e = __builtin_ctz((m | (m >> 8)) & 0xffu);
+            const uint32_t is_gt = (m >> e) & 1u, is_eq = (m >> (8 + e)) & 1u;
+            m &= ~((1u << e) | (0x100u << e));
+            if (is_gt || eb < wo.take) {
+                float rv = r[0];
+#pragma unroll
+                for (int k = 1; k < 8; ++k) rv = e == k ? r[k] : rv;
+                put(wo.off + gb + min(eb, wo.take), (uint32_t)(row * g.d + col + e), rv);
+            }
+            gb += is_gt;
+            eb += is_eq;
+        }
+        before_iter += iter_total;
+    }
+}
+
 // ------------------------------------------------------------------ trim pass over the list
 __global__ __launch_bounds__(kBlock) void k_list_hist(int lvl, const uint32_t *__restrict__ rbits, int64_t n,
                                                       uint32_t *__restrict__ hist, const SelState *__restrict__ state)
@@ -1744,6 +2237,10 @@ struct Plan {
     SaveGeom gw;
     int mvw, ntw;
     int64_t n_wgs_w;
+    // bf16 on the batched path with a residual and not wide: the candidate passes (k_proj_cand,
+    // k_refine_cand, k_emit_cand) with the workgroups' quota
+    bool cand;
+    uint32_t quota;
     bool trim;
     int64_t n_list_blocks;
 };
@@ -1795,7 +2292,7 @@ Plan make_plan_rows(const StacrSaveArgs &a)
 // kernels over that residual viewed as f * rows rows of d / f <= 2048 columns (row-major, so the
 // flat indices are the same; chunks are f * chunk_rows such rows, so the chunks are the same) at
 // rank 8 (they read neither the basis nor C).
-Plan make_plan(const StacrSaveArgs &a)
+Plan make_plan_wide(const StacrSaveArgs &a)
 {
     Plan p = make_plan_rows(a);
     if (p.fast || a.dtype == STACR_DTYPE_F32 || p.V != 8 || p.R > 16 || a.feats > 8192) return p;
@@ -1846,10 +2343,30 @@ Plan make_plan(const StacrSaveArgs &a)
     return pv.wide ? pv : p;
 }
 
+// The candidate passes take bf16 saves on the batched path (not wide rows) when a workgroup's
+// quota, four times its mean share of its chunk's k plus 64, fits half the candidate list: a
+// workgroup then needs more than four times its share above the chunk's level-0 bin before it
+// falls back to recomputing.
+Plan make_plan(const StacrSaveArgs &a)
+{
+    Plan p = make_plan_wide(a);
+    if (!p.fold || p.wide || a.k_total <= 0) return p;
+    const SaveGeom &g = p.g;
+    const double wg_elems = (double)g.rows_per_wg * (double)g.d;
+    const int64_t last_rows = g.rows - (g.n_chunks - 1) * g.chunk_rows;
+    const double dens = hmax<double>((double)a.k_full / ((double)g.chunk_rows * (double)g.d),
+                                     (double)a.k_last / ((double)last_rows * (double)g.d));
+    const double quota = 4.0 * dens * wg_elems + 64.0;
+    if (quota > kCandCap / 2) return p;
+    p.cand = true;
+    p.quota = (uint32_t)quota;
+    return p;
+}
+
 template <typename T> T *carve(char *base, size_t off) { return reinterpret_cast<T *>(base + off); }
 
 enum { WS_QP, WS_HIST, WS_COARSE, WS_STATE, WS_MAXKEY, WS_COUNTS, WS_OFFS, WS_LRBITS, WS_LIDX, WS_THIST, WS_TSTATE,
-       WS_LCOUNTS, WS_LOFFS, WS_Q4, WS_FOLD, WS_R, WS_N };
+       WS_LCOUNTS, WS_LOFFS, WS_Q4, WS_FOLD, WS_R, WS_CIDX, WS_CVAL, WS_CMETA, WS_N };
 
 size_t layout(const StacrSaveArgs &a, const Plan &p, size_t *off)
 {
@@ -1872,8 +2389,12 @@ size_t layout(const StacrSaveArgs &a, const Plan &p, size_t *off)
     take(WS_LOFFS, nb * sizeof(WgOffset));
     take(WS_Q4, a.bits == 4 ? (size_t)a.k_total : 0);
     take(WS_FOLD, p.fold ? (size_t)17 * p.n_wgs * sizeof(uint32_t) : 0);  // cum[0..16][workgroup]
-    const bool rstore = p.fast && a.dtype != STACR_DTYPE_F32 && a.k_total > 0;  // (wide rows: p.fast)
+    const bool rstore = p.fast && a.dtype != STACR_DTYPE_F32 && a.k_total > 0 && !p.cand;  // (wide rows: p.fast)
     take(WS_R, rstore ? (size_t)a.rows * a.feats * 2 : 0);  // the stored residual (16-bit types)
+    const size_t nc = p.cand ? (size_t)p.n_wgs * kCandCap : 0;  // the candidate lists
+    take(WS_CIDX, nc * sizeof(uint32_t));
+    take(WS_CVAL, nc * sizeof(uint16_t));
+    take(WS_CMETA, p.cand ? (size_t)p.n_wgs * sizeof(CandMeta) : 0);
     return cur;
 }
 
@@ -1948,6 +2469,14 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     if (fast != p.fold && DT == STACR_DTYPE_BF16) return stacr_fail(STACR_ERR_INVALID, "stacr_save: bf16 fold outside the batched path");
     if (!fast && p.g.hcopies != 1) return stacr_fail(STACR_ERR_INVALID, "stacr_save: histogram copies outside the batched path");
     FastGeom fg{p.g.L / 64, a.rank == R && ((uintptr_t)coeff % 16) == 0};
+    // bf16 candidate passes (the plan takes them only with a residual, so the projection pass
+    // always runs them)
+    constexpr bool kCandOk = kFastOk && DT == STACR_DTYPE_BF16;
+    const bool cand = kCandOk && fast && p.cand && resid;
+    if (p.cand && !cand) return stacr_fail(STACR_ERR_INVALID, "stacr_save: candidate passes outside the bf16 batched path");
+    uint32_t *cidx = carve<uint32_t>(ws, off[WS_CIDX]);
+    uint16_t *cval = carve<uint16_t>(ws, off[WS_CVAL]);
+    CandMeta *cmeta = carve<CandMeta>(ws, off[WS_CMETA]);
     if (!coeff_in || resid) {
         if constexpr (kFastOk) {
             if (fast && p.wide) {
@@ -1957,6 +2486,9 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
                 } else {
                     return stacr_fail(STACR_ERR_INVALID, "stacr_save: wide rows outside 16-bit activations");
                 }
+            } else if (fast && cand) {
+                if constexpr (kCandOk)
+                    stacr_launch("k_proj_hist", s, [&] { k_proj_cand<R><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff_out, hist, maxkey, coeff_in, coarse, p.quota, cidx, cval, cmeta); });
             } else if (fast) {
                 stacr_launch("k_proj_hist", s, [&] { k_proj_hist_b<DT, R, V, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in, rbuf, coarse); });
             }
@@ -1984,7 +2516,17 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
                 using L2 = std::integral_constant<int, 2>;
                 using H8 = std::integral_constant<int, kHistCopies>;
                 using H1 = std::integral_constant<int, 1>;
-                if (lvl == 1) {
+                auto refine_cand = [&](auto hc) {
+                    if constexpr (kCandOk)
+                        stacr_launch("k_refine_hist", s, [&] {
+                            k_refine_cand<R, decltype(hc)::value><<<nwg, kBlock, 0, s>>>(
+                                p.g, fg, x, qp, coeff, hist, state, kf, kl, maxkey, fold, p.n_wgs, coarse, cval, cmeta);
+                        });
+                };
+                if (lvl == 1 && cand) {
+                    if (hc8) refine_cand(H8{});
+                    else refine_cand(H1{});
+                } else if (lvl == 1) {
                     if (hc8) refine(H8{}, L1{});
                     else refine(H1{}, L1{});
                 } else if constexpr (sizeof(T) == 4) {  // only fp32 runs the second refine pass
@@ -2015,9 +2557,15 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     o.cap = (uint32_t)(p.trim ? a.k_sum : a.k_total);
     if constexpr (kFastOk) {
         // the fold variant (bf16) reads the level-1 histogram copies; other types take the counts
-        if (fast && hc8 && DT == STACR_DTYPE_BF16)
+        if constexpr (kCandOk) {
+            if (cand && hc8)
+                stacr_launch("k_emit", s, [&] { k_emit_cand<R, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta); });
+            else if (cand)
+                stacr_launch("k_emit", s, [&] { k_emit_cand<R, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta); });
+        }
+        if (!cand && fast && hc8 && DT == STACR_DTYPE_BF16)
             stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V, kHistCopies, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs); });
-        else if (fast)
+        else if (!cand && fast)
             stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V, 1, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs); });
     }
     if (!fast) stacr_launch("k_emit", s, [&] { k_emit<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0); });

@@ -136,6 +136,8 @@ SAVE_CASES = [
     # workgroup and a trim to k_total, and a chunked run without quantization
     ("bf16_batched_chunk_trim", 1000, 1024, 8, "bf16", "chunk_topk", 0.005, 100, 8, True),
     ("bf16_batched_chunk_bits0", 2048, 1024, 4, "bf16", "chunk_topk", 0.01, 512, 0, False),
+    # a budget whose per-workgroup quota exceeds the candidate list: the stored-residual passes
+    ("bf16_batched_large_budget", 1024, 1024, 8, "bf16", "global_topk", 0.05, 512, 8, True),
     # 16-bit rows of 2048 < d <= 4096: the projection pass takes two vectors a thread and stores
     # the residual; the later passes read it as twice the rows of half the width (cfg3 c_proj,
     # cfg5 c_proj and chunk_trim_bf16 above also run here)
@@ -160,6 +162,57 @@ SAVE_CASES = [
 @pytest.mark.parametrize("case", SAVE_CASES, ids=[c[0] for c in SAVE_CASES])
 def test_save_matches_oracle(dev, case):
     run_and_check_save(dev, *case[1:])
+
+
+def _crafted_activation(kind, rows, d):
+    """Inputs on which some bf16 batched workgroups cannot use their candidate lists: 'outlier_rows'
+    scales rows 32..47 (one workgroup's rows at d = 1024) by 1000, so that workgroup alone holds
+    more than its quota above the chunk's level-0 bin; 'tie_block' sets rows 0..15 to +-1 under a
+    zero basis, so one bin holds 16384 equal keys (more than the list holds, and ties at the
+    threshold); 'outlier_scattered' scales every 40th row by 300."""
+    x = make_activation(rows, d, lognormal=True)
+    if kind == "outlier_rows":
+        x[32:48] *= 1000.0
+    elif kind == "outlier_scattered":
+        x[::40] *= 300.0
+    elif kind == "tie_block":
+        g = torch.Generator().manual_seed(7)
+        x = 0.01 * torch.randn(rows, d, generator=g)
+        x[:16] = torch.where(torch.rand(16, d, generator=g) < 0.5, -1.0, 1.0)
+    return x
+
+
+@pytest.mark.parametrize("kind,rows,mode,budget,chunk,bits", [
+    ("outlier_rows", 2048, "global_topk", 0.005, 512, 8),
+    ("outlier_rows", 2048, "chunk_topk", 0.005, 256, 8),
+    ("tie_block", 512, "global_topk", 0.005, 512, 0),
+    ("tie_block", 1024, "chunk_topk", 0.01, 128, 8),
+    ("outlier_scattered", 4096, "global_topk", 0.005, 512, 8),
+])
+def test_save_candidate_fallback_matches_oracle(dev, kind, rows, mode, budget, chunk, bits):
+    """bf16 saves on the batched path keep per-workgroup candidate lists; a workgroup whose list
+    cannot hold every element at or above its chunk's level-0 bin recomputes its residuals from X.
+    Selection and quantization stay bit-exact against the oracle either way."""
+    from stacr_amd import kernels
+
+    d, rank = 1024, 8
+    announce("save candidate fallback", kind, rows, mode, budget, chunk, bits)
+    x = _crafted_activation(kind, rows, d)
+    q = torch.zeros(d, rank) if kind == "tie_block" else make_basis(d, rank)
+    xd, qd = x.to(dev, torch.bfloat16), q.to(dev, torch.bfloat16)
+    coeff, idx, data, scale = kernels.save(xd, qd, mode=mode, budget=budget, chunk_rows=chunk, bits=bits)
+    torch.cuda.synchronize()
+    xf, qf, cf = _np(xd), _np(qd), _np(coeff)
+    _, oidx, odata, oscale = orc.save(xf, qf, "bf16", mode, budget, chunk, bits, coeff=cf)
+    assert np.array_equal(idx.cpu().numpy().astype(np.int64), oidx)
+    if bits == 0:
+        assert np.array_equal(_np(data), odata)
+    else:
+        assert np.array_equal(data.cpu().numpy().view(np.int8), odata)
+        assert np.float32(scale.item()) == oscale
+    if kind == "tie_block":  # the ties at the threshold (chunk 0) go to its lowest flat indices
+        first = oidx[oidx < min(chunk, rows) * d] if mode == "chunk_topk" else oidx
+        assert first.size > 0 and first.max() < 16 * d
 
 
 @pytest.mark.parametrize("d,dtype,rank", [(4096, "bf16", 8), (2560, "f16", 8), (1024, "bf16", 8), (8192, "bf16", 16),
