@@ -27,6 +27,10 @@
  *                            and OjaBasis.update, stacr/oja.py:73-79
  *   stacr_reconstruct        the saved-tensor hooks' dense unpack, stacr/compressor.py:127-133 with
  *                            stacr/residual.py:13-20
+ *   stacr_index_stream_*     a bit-packed form of the delta index codec, stacr/index_compression.py:
+ *                            231-269 (encode) and :327-342 (decode)
+ *   stacr_*_rows_int8        int8 coefficients with a scale per row (the C1 codec's quantizer,
+ *                            stacr/protocols/checkpointing.py:374-400, per row)
  */
 #ifndef STACR_AMD_H
 #define STACR_AMD_H
@@ -316,6 +320,35 @@ int stacr_oja_step(const void *x, int dtype, int64_t rows, int64_t feats, const 
 int stacr_reconstruct(const void *coeff, const void *q, int dtype, int64_t rows, int64_t feats, int rank,
                       const void *idx, int index_bytes, const void *values, int64_t nnz, int has_residual,
                       void *out, void *stream);
+
+/* ---------------------------------------------------------------- compact save outputs
+ * Bit-packed delta stream of sorted flat indices (a denser form of the delta codec,
+ * stacr/index_compression.py:231-269; decoding gives decompress_indices' base + cumulative deltas,
+ * :327-342).  Blocks of 256 entries: base[b] = idx[256 b] (int64); slot j holds
+ * d_j = idx[256 b + j] - idx[256 b + j - 1] (d_0 = 0) in w_b bits, w_b the bit length of the
+ * block's largest delta; the block's 256 slots fill 8 w_b uint32 words, slot j at bits
+ * [j w_b, (j + 1) w_b), least significant bit first, unused slots 0.  word_off[b] (uint32, nb + 1
+ * entries) is block b's first word; word_off[nb] is the stream's length in words.
+ * sizes: nb = ceil(nnz / 256) and the longest stream, 256 nb words (nnz < 2^31). */
+int stacr_index_stream_sizes(int64_t nnz, int64_t *blocks, int64_t *max_words);
+/* idx: nnz int32 / int64 (idx_bytes 4 / 8), non-decreasing and non-negative.  base: int64[nb];
+ * word_off: uint32[nb + 1]; words: uint32[max_words]; status: one uint32 on the device, set to the
+ * OR of 1 (a decreasing pair), 2 (a gap of 2^32 or more) and 4 (a negative index); a nonzero status
+ * means the stream does not hold the input (such deltas are stored as 0). */
+int stacr_index_stream_encode(const void *idx, int idx_bytes, int64_t nnz, void *base, void *word_off, void *words,
+                              void *status, void *stream);
+/* The sorted indices back, as int32 or int64 (idx_bytes 4 / 8). */
+int stacr_index_stream_decode(const void *base, const void *word_off, const void *words, int64_t nnz, void *idx,
+                              int idx_bytes, void *stream);
+
+/* int8 coefficients with one fp32 scale per row of C (rows x rank, dtype): m = max |c| over the
+ * row (NaN if the row holds one), s = (m finite and > 0 ? m : 1) / 127, q = clamp(round half to even
+ * (c / s), -127, 127), a NaN quotient coded 0.  codes: int8[rows * rank]; scales: float[rows]. */
+int stacr_quantize_rows_int8(const void *coeff, int dtype, int64_t rows, int rank, void *codes, void *scales,
+                             void *stream);
+/* out = q * s in fp32, rounded once to out_dtype. */
+int stacr_dequantize_rows_int8(const void *codes, const void *scales, int64_t rows, int rank, void *out,
+                               int out_dtype, void *stream);
 
 /*
  * Kernel timing (benchmarking aid; no counterpart in the reference).  Between begin and end,

@@ -530,3 +530,82 @@ def adaptive_select_block_sparse(resid: np.ndarray, budget: float, chunk_rows: i
     flat = (cand // bpr)[:, None] * d + cols
     idx = flat[cols < d].astype(np.int64)
     return idx, resid.reshape(-1)[idx]
+
+
+# ================================================================ compact save outputs
+# The bit-packed index stream and row-quantized coefficients of the library's codecs.  The stream
+# is a denser form of the delta codec (stacr/index_compression.py:231-269) and decodes by its rule
+# (base plus cumulative deltas, :327-342); the row quantizer is the C1 codec's safe-max rule
+# (stacr/protocols/checkpointing.py:374-393) with the maximum taken per row.
+STREAM_BLOCK = 256
+
+
+def index_stream_encode(idx: np.ndarray):
+    """(base int64[nb], word_off uint32[nb + 1], words uint32[word_off[nb]], status) of the stream:
+    block b's deltas d_0 = 0, d_j = idx[256 b + j] - idx[256 b + j - 1] in w_b = bit length of the
+    block's largest delta, slot j at bits [j w_b, (j + 1) w_b) of the block's 8 w_b words (least
+    significant bit first).  status: 1 a decreasing pair, 2 a gap >= 2^32, 4 a negative index (such
+    deltas are stored as 0)."""
+    v = np.asarray(idx, np.int64).reshape(-1)
+    nnz = v.size
+    nb = -(-nnz // STREAM_BLOCK)
+    base = np.zeros(nb, np.int64)
+    word_off = np.zeros(nb + 1, np.uint64)
+    blocks = []
+    status = 0
+    for b in range(nb):
+        blk = v[b * STREAM_BLOCK:(b + 1) * STREAM_BLOCK]
+        base[b] = blk[0]
+        d = np.zeros(STREAM_BLOCK, np.int64)
+        d[1:blk.size] = np.diff(blk)
+        if (blk < 0).any():
+            status |= 4
+        if (d < 0).any():
+            status |= 1
+        if (d > 0xFFFFFFFF).any():
+            status |= 2
+        d[(d < 0) | (d > 0xFFFFFFFF)] = 0
+        w = int(d.max()).bit_length()
+        bits = 0
+        for j in range(STREAM_BLOCK):
+            bits |= int(d[j]) << (j * w)
+        words = np.array([(bits >> (32 * k)) & 0xFFFFFFFF for k in range(8 * w)], np.uint64)
+        blocks.append(words.astype(np.uint32))
+        word_off[b + 1] = word_off[b] + 8 * w
+    words = np.concatenate(blocks) if blocks else np.zeros(0, np.uint32)
+    return base, word_off.astype(np.uint32), words, status
+
+
+def index_stream_decode(base: np.ndarray, word_off: np.ndarray, words: np.ndarray, nnz: int) -> np.ndarray:
+    """base[b] + inclusive prefix sums of block b's deltas (int64)."""
+    out = np.zeros(nnz, np.int64)
+    words = np.asarray(words, np.uint64)
+    for b in range(len(base)):
+        lo, hi = int(word_off[b]), int(word_off[b + 1])
+        w = (hi - lo) // 8
+        bits = 0
+        for k in range(hi - lo):
+            bits |= int(words[lo + k]) << (32 * k)
+        n = min(STREAM_BLOCK, nnz - b * STREAM_BLOCK)
+        d = [(bits >> (j * w)) & ((1 << w) - 1) for j in range(n)]
+        out[b * STREAM_BLOCK:b * STREAM_BLOCK + n] = int(base[b]) + np.cumsum(np.asarray(d, np.int64))
+    return out
+
+
+def quantize_rows_int8(c: np.ndarray):
+    """(codes int8 rows x rank, scales fp32[rows]): m = the row's max |c| in fp32 (NaN if it holds
+    one), s = (m finite and > 0 ? m : 1) / 127 in fp32, q = clamp(round half to even(c / s), -127,
+    127) with fp32 division, a NaN quotient coded 0."""
+    c = np.asarray(c, np.float32)
+    with np.errstate(invalid="ignore"):
+        m = np.abs(c).max(axis=1) if c.shape[1] else np.zeros(c.shape[0], np.float32)
+        safe = np.where(np.isfinite(m) & (m > 0), m, np.float32(1.0)).astype(np.float32)
+        s = (safe / np.float32(127.0)).astype(np.float32)
+        qv = np.rint((c / s[:, None]).astype(np.float32))
+        qv = np.where(np.isnan(qv), np.float32(0.0), np.clip(qv, -127, 127))
+    return qv.astype(np.int8), s
+
+
+def dequantize_rows_int8(codes: np.ndarray, scales: np.ndarray, dtype: str) -> np.ndarray:
+    """codes * scale in fp32, rounded once to dtype."""
+    return round_to(np.asarray(codes, np.float32) * np.asarray(scales, np.float32)[:, None], dtype)

@@ -18,7 +18,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("STACR_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["abi.hip", "save.hip", "weight_grad.hip", "adaptive.hip", "oja.hip", "selectors.hip", "profile.hip",
-           "noalloc.hip", "weight_grad_tiles.hip", "reconstruct.hip"]
+           "noalloc.hip", "weight_grad_tiles.hip", "reconstruct.hip", "codecs.hip"]
 
 FLAGS = [
     f"--offload-arch={ARCH}",

@@ -314,3 +314,79 @@ def reconstruct(coeff: torch.Tensor, q: torch.Tensor, residual=None) -> torch.Te
                                    _ptr(values) if nnz else None, nnz, 1 if residual is not None else 0, _ptr(out),
                                    _stream(coeff.device)), "stacr_reconstruct")
     return out
+
+
+def index_stream_encode(idx: torch.Tensor):
+    """Bit-packed delta stream of sorted flat indices (blocks of 256, one bit width per block).
+
+    Returns (base int64[nb], word_off int32[nb + 1], words int32[256 nb], status int32[1]); the
+    int32 tensors hold uint32 bit patterns, words[:word_off[nb]] is the stream, and a nonzero
+    status means the input was not non-decreasing and non-negative with gaps below 2^32.
+    """
+    require_gpu(idx, "indices")
+    if idx.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"indices must be int32 or int64, got {idx.dtype}")
+    idx = idx.contiguous().reshape(-1)
+    nnz = idx.numel()
+    L = _lib.load()
+    nb, mw = ctypes.c_int64(), ctypes.c_int64()
+    _lib.check(L.stacr_index_stream_sizes(nnz, ctypes.byref(nb), ctypes.byref(mw)), "stacr_index_stream_sizes")
+    dev = idx.device
+    base = torch.empty(nb.value, dtype=torch.int64, device=dev)
+    word_off = torch.empty(nb.value + 1, dtype=torch.int32, device=dev)
+    words = torch.empty(mw.value, dtype=torch.int32, device=dev)
+    status = torch.empty(1, dtype=torch.int32, device=dev)
+    _lib.check(L.stacr_index_stream_encode(_ptr(idx) if nnz else None, idx.element_size(), nnz,
+                                           _ptr(base) if nnz else None, _ptr(word_off), _ptr(words) if nnz else None,
+                                           _ptr(status), _stream(dev)), "stacr_index_stream_encode")
+    return base, word_off, words, status
+
+
+def index_stream_decode(base: torch.Tensor, word_off: torch.Tensor, words: torch.Tensor, nnz: int,
+                        dtype: torch.dtype = torch.int32) -> torch.Tensor:
+    """The sorted flat indices of a stream from index_stream_encode, as int32 or int64."""
+    if dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"indices decode to int32 or int64, not {dtype}")
+    dev = word_off.device
+    require_gpu(word_off, "stream offsets")
+    out = torch.empty(int(nnz), dtype=dtype, device=dev)
+    if nnz == 0:
+        return out
+    if words.numel() == 0:  # every block of width 0 (a stream of no words); the library wants a buffer
+        words = torch.zeros(1, dtype=torch.int32, device=dev)
+    L = _lib.load()
+    _lib.check(L.stacr_index_stream_decode(_ptr(base.contiguous()), _ptr(word_off.contiguous()),
+                                           _ptr(words.contiguous()), int(nnz), _ptr(out), out.element_size(),
+                                           _stream(dev)), "stacr_index_stream_decode")
+    return out
+
+
+def quantize_rows_int8(coeff: torch.Tensor):
+    """(int8 codes rows x rank, fp32 scales[rows]): one scale per row, s = safe max |c| / 127."""
+    require_gpu(coeff, "coefficients")
+    if coeff.dim() != 2:
+        raise ValueError(f"coefficients must be rows x rank, got shape {tuple(coeff.shape)}")
+    coeff = coeff.contiguous()
+    rows, rank = coeff.shape
+    codes = torch.empty(rows, rank, dtype=torch.int8, device=coeff.device)
+    scales = torch.empty(rows, dtype=torch.float32, device=coeff.device)
+    if rows and rank:
+        L = _lib.load()
+        _lib.check(L.stacr_quantize_rows_int8(_ptr(coeff), dtype_code(coeff.dtype), rows, rank, _ptr(codes),
+                                              _ptr(scales), _stream(coeff.device)), "stacr_quantize_rows_int8")
+    return codes, scales
+
+
+def dequantize_rows_int8(codes: torch.Tensor, scales: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """codes * scale[row] in fp32, rounded once to ``dtype``."""
+    require_gpu(codes, "codes")
+    if codes.dtype != torch.int8 or scales.dtype != torch.float32:
+        raise TypeError("codes must be int8 and scales float32")
+    codes = codes.contiguous()
+    rows, rank = codes.shape
+    out = torch.empty(rows, rank, dtype=dtype, device=codes.device)
+    if rows and rank:
+        L = _lib.load()
+        _lib.check(L.stacr_dequantize_rows_int8(_ptr(codes), _ptr(scales.contiguous()), rows, rank, _ptr(out),
+                                                dtype_code(dtype), _stream(codes.device)), "stacr_dequantize_rows_int8")
+    return out
