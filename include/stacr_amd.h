@@ -31,6 +31,9 @@
  *                            231-269 (encode) and :327-342 (decode)
  *   stacr_*_rows_int8        int8 coefficients with a scale per row (the C1 codec's quantizer,
  *                            stacr/protocols/checkpointing.py:374-400, per row)
+ *   stacr_c1_*               the C1 checkpoint-boundary codec's device work,
+ *                            CheckpointBoundaryCodec.pack_tensor / unpack_record,
+ *                            stacr/protocols/checkpointing.py:374-400,411-545
  */
 #ifndef STACR_AMD_H
 #define STACR_AMD_H
@@ -340,6 +343,54 @@ int stacr_index_stream_encode(const void *idx, int idx_bytes, int64_t nnz, void 
 /* The sorted indices back, as int32 or int64 (idx_bytes 4 / 8). */
 int stacr_index_stream_decode(const void *base, const void *word_off, const void *words, int64_t nnz, void *idx,
                               int idx_bytes, void *stream);
+
+/* ---------------------------------------------------------------- C1 checkpoint-boundary codec
+ * pack_tensor (stacr/protocols/checkpointing.py:411-529) forms C = X Q in fp32 (the caller's GEMM,
+ * as the reference's `flat_fp32 @ basis_fp32`); stacr_c1_observe then reads X once and reports
+ * everything the reference inspects before it decides between a compressed record and a dense
+ * fallback, and stacr_c1_store writes the record's coefficients; unpack_record (:531-545) is
+ * stacr_c1_restore. */
+#define STACR_DTYPE_I8 3 /* int8 coefficient codes (stacr_c1_store / stacr_c1_restore) */
+#define STACR_C1_MAX_RANK 128
+/* stats flags, per tensor (X, C, the reconstruction C Q^T, the residual X - C Q^T, the basis):
+ * "holds a NaN" and "holds a value that is not NaN".  With the tensor's max below: non-finite =
+ * NaN or max = inf; the reference's _safe_max_abs (:80-99) = NaN without a non-NaN value, FLT_MAX
+ * with a NaN and an inf (torch.nan_to_num clamps the inf), else the max. */
+#define STACR_C1_INPUT_NAN 1u
+#define STACR_C1_COEFF_NAN 2u
+#define STACR_C1_RECON_NAN 4u
+#define STACR_C1_BASIS_NAN 8u
+#define STACR_C1_INPUT_VALID 16u
+#define STACR_C1_COEFF_VALID 32u
+#define STACR_C1_RECON_VALID 64u
+#define STACR_C1_RESIDUAL_VALID 128u
+#define STACR_C1_BASIS_VALID 256u
+#define STACR_C1_RESIDUAL_NAN 512u
+typedef struct {
+    double error;  /* sum over X of rnd32((x - p)^2), p = sum_j c_j q_j (fp32 chain), in fp64 */
+    double denom;  /* sum of rnd32(x^2), in fp64 */
+    float energy;  /* (float)error / max((float)denom, 1e-12) */
+    float input_max_abs, coeff_max_abs, reconstruction_max_abs, residual_max_abs, basis_max_abs;
+    /* (the largest |v| that is not NaN, inf included; 0 when there is none) */
+    uint32_t flags;
+    uint32_t reserved;
+} StacrC1Stats;
+int stacr_c1_workspace_bytes(int64_t rows, int64_t hidden, int rank, size_t *bytes);
+/* x: rows x hidden (dtype); coeff: fp32 rows x rank; basis: hidden x rank (basis_dtype, widened to
+ * fp32 as the reference's `basis.to(float32)`).  stats: one StacrC1Stats on the device; scales:
+ * fp32[rank], s_j = (m_j finite and > 0 ? m_j : 1) / 127 with m_j = max |c_j| over the rows (NaN if
+ * one is NaN).  Deterministic: the partial sums are combined in a fixed order. */
+int stacr_c1_observe(const void *x, int dtype, int64_t rows, int64_t hidden, const float *coeff, const void *basis,
+                     int basis_dtype, int rank, void *stats, float *scales, void *workspace, size_t workspace_bytes,
+                     void *stream);
+/* The record's coefficients: quantize -> int8 clamp(round half to even(c / s_j), -127, 127) (out_dtype
+ * STACR_DTYPE_I8), else C rounded once to out_dtype (the basis dtype, :376-377). */
+int stacr_c1_store(const float *coeff, int64_t rows, int rank, const float *scales, int quantize, void *out,
+                   int out_dtype, void *stream);
+/* out = sum_j c'_j q_j in fp32, rounded once to out_dtype; c' = code * s_j for coeff_dtype
+ * STACR_DTYPE_I8, else the stored coefficient widened to fp32. */
+int stacr_c1_restore(const void *coeff, int coeff_dtype, const float *scales, const void *basis, int basis_dtype,
+                     int64_t rows, int64_t hidden, int rank, void *out, int out_dtype, void *stream);
 
 /* int8 coefficients with one fp32 scale per row of C (rows x rank, dtype): m = max |c| over the
  * row (NaN if the row holds one), s = (m finite and > 0 ? m : 1) / 127, q = clamp(round half to even

@@ -609,3 +609,62 @@ def quantize_rows_int8(c: np.ndarray):
 def dequantize_rows_int8(codes: np.ndarray, scales: np.ndarray, dtype: str) -> np.ndarray:
     """codes * scale in fp32, rounded once to dtype."""
     return round_to(np.asarray(codes, np.float32) * np.asarray(scales, np.float32)[:, None], dtype)
+
+
+# ================================================================ C1 checkpoint-boundary codec
+# CheckpointBoundaryCodec.pack_tensor / unpack_record (stacr/protocols/checkpointing.py:374-400,
+# 411-545) on given fp32 coefficients, in the library's arithmetic: the reconstruction is the
+# fp32 chain of lowrank, squares are rounded to fp32 and summed in fp64.
+def _safe_max(a: np.ndarray):
+    """(largest |v| that is not NaN (inf included) or 0, any value not NaN, any NaN)."""
+    a = np.abs(np.asarray(a, np.float32)).reshape(-1)
+    ok = ~np.isnan(a)
+    return (float(a[ok].max()) if ok.any() else 0.0), bool(ok.any()), bool((~ok).any())
+
+
+def c1_scales(coeff: np.ndarray) -> np.ndarray:
+    """s_j = (m_j finite and > 0 ? m_j : 1) / 127 in fp32, m_j = max over rows of |c_j| (NaN if one
+    is NaN) (_quantize_coefficients, :383-392)."""
+    c = np.abs(np.asarray(coeff, np.float32))
+    m = np.where(np.isnan(c).any(axis=0), np.float32(np.nan), np.where(np.isnan(c), 0, c).max(axis=0, initial=0.0))
+    safe = np.where(np.isfinite(m) & (m > 0), m, np.float32(1.0)).astype(np.float32)
+    return (safe / np.float32(127.0)).astype(np.float32)
+
+
+def c1_observe(x: np.ndarray, coeff: np.ndarray, basis: np.ndarray) -> dict:
+    x = np.asarray(x, np.float32)
+    c = np.asarray(coeff, np.float32)
+    q = np.asarray(basis, np.float32)
+    p = lowrank(c, q, "f32")
+    with np.errstate(invalid="ignore", over="ignore"):
+        e = (x - p).astype(np.float32)
+        err = float((e * e).astype(np.float32).astype(np.float64).sum())
+        den = float((x * x).astype(np.float32).astype(np.float64).sum())
+        energy = float(np.float32(err) / max(np.float32(den), np.float32(1e-12)))
+    out = {"error": err, "denom": den, "energy": energy, "flags": 0}
+    for name, arr, bits in (("input", x, (1, 16)), ("coeff", c, (2, 32)), ("reconstruction", p, (4, 64)),
+                            ("basis", q, (8, 256)), ("residual", e, (512, 128))):
+        m, valid, nan = _safe_max(arr)
+        out[f"{name}_max_abs"] = m
+        out["flags"] |= (bits[0] if nan else 0) | (bits[1] if valid else 0)
+    return out
+
+
+def c1_store(coeff: np.ndarray, scales: np.ndarray | None, dtype: str):
+    """int8 clamp(round half even(c / s_j), -127, 127) (fp32 division, NaN coded 0) when scales are
+    given, else C rounded to dtype."""
+    c = np.asarray(coeff, np.float32)
+    if scales is None:
+        return round_to(c, dtype)
+    with np.errstate(invalid="ignore"):
+        qv = np.rint((c / np.asarray(scales, np.float32)[None, :]).astype(np.float32))
+        qv = np.where(np.isnan(qv), np.float32(0.0), np.clip(qv, -127, 127))
+    return qv.astype(np.int8)
+
+
+def c1_restore(coeff: np.ndarray, scales: np.ndarray | None, basis: np.ndarray, dtype: str) -> np.ndarray:
+    """sum_j c'_j q_j (the fp32 chain) rounded to dtype; c' = code * s_j in fp32 for int8 codes."""
+    c = np.asarray(coeff, np.float32)
+    if scales is not None:
+        c = (c * np.asarray(scales, np.float32)[None, :]).astype(np.float32)
+    return lowrank(c, np.asarray(basis, np.float32), dtype)

@@ -75,6 +75,10 @@ SIGNATURES = {
     "stacr_index_stream_decode": ([_p, _p, _p, _i64, _p, _i32, _p], _i32),
     "stacr_quantize_rows_int8": ([_p, _i32, _i64, _i32, _p, _p, _p], _i32),
     "stacr_dequantize_rows_int8": ([_p, _p, _i64, _i32, _p, _i32, _p], _i32),
+    "stacr_c1_workspace_bytes": ([_i64, _i64, _i32, _p], _i32),
+    "stacr_c1_observe": ([_p, _i32, _i64, _i64, _p, _p, _i32, _i32, _p, _p, _p, _sz, _p], _i32),
+    "stacr_c1_store": ([_p, _i64, _i32, _p, _i32, _p, _i32, _p], _i32),
+    "stacr_c1_restore": ([_p, _i32, _p, _p, _i32, _i64, _i64, _i32, _p, _i32, _p], _i32),
 }
 
 _lib = None

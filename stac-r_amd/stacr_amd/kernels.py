@@ -390,3 +390,75 @@ def dequantize_rows_int8(codes: torch.Tensor, scales: torch.Tensor, dtype: torch
         _lib.check(L.stacr_dequantize_rows_int8(_ptr(codes), _ptr(scales.contiguous()), rows, rank, _ptr(out),
                                                 dtype_code(dtype), _stream(codes.device)), "stacr_dequantize_rows_int8")
     return out
+
+
+# ------------------------------------------------------------------ C1 checkpoint-boundary codec
+C1_STATS_BYTES = 48
+C1_FLAGS = {"input_nan": 1, "coeff_nan": 2, "recon_nan": 4, "basis_nan": 8, "input_valid": 16, "coeff_valid": 32,
+            "recon_valid": 64, "residual_valid": 128, "basis_valid": 256, "residual_nan": 512}
+DTYPE_I8 = 3
+
+
+def c1_observe(x2d: torch.Tensor, coeff: torch.Tensor, basis: torch.Tensor):
+    """One pass over the boundary X (rows x hidden) with its fp32 coefficients and the basis:
+    (stats uint8[48] on the device, fp32 scales[rank]); parse the stats with c1_parse_stats."""
+    require_gpu(x2d, "boundary activation")
+    if coeff.dtype != torch.float32:
+        raise TypeError("C1 coefficients are fp32")
+    x2d, coeff, basis = x2d.contiguous(), coeff.contiguous(), basis.contiguous()
+    rows, hidden = x2d.shape
+    rank = basis.shape[1]
+    if coeff.shape != (rows, rank) or basis.shape[0] != hidden:
+        raise ValueError("C1 shapes: x rows x hidden, coeff rows x rank, basis hidden x rank")
+    L = _lib.load()
+    nbytes = ctypes.c_size_t()
+    _lib.check(L.stacr_c1_workspace_bytes(rows, hidden, rank, ctypes.byref(nbytes)), "stacr_c1_workspace_bytes")
+    dev = x2d.device
+    ws = torch.empty(max(1, nbytes.value), dtype=torch.uint8, device=dev)
+    stats = torch.empty(C1_STATS_BYTES, dtype=torch.uint8, device=dev)
+    scales = torch.empty(rank, dtype=torch.float32, device=dev)
+    _lib.check(L.stacr_c1_observe(_ptr(x2d), dtype_code(x2d.dtype), rows, hidden, _ptr(coeff), _ptr(basis),
+                                  dtype_code(basis.dtype), rank, _ptr(stats), _ptr(scales), _ptr(ws), nbytes.value,
+                                  _stream(dev)), "stacr_c1_observe")
+    return stats, scales
+
+
+def c1_parse_stats(raw) -> dict:
+    """The StacrC1Stats record (48 bytes, host copy) as a dict."""
+    import struct
+
+    b = bytes(raw.cpu().numpy().tobytes()) if isinstance(raw, torch.Tensor) else bytes(raw)
+    err, denom, energy, xm, cm, rm, em, bm, flags, _ = struct.unpack("<ddffffffII", b[:C1_STATS_BYTES])
+    return {"error": err, "denom": denom, "energy": energy, "input_max_abs": xm, "coeff_max_abs": cm,
+            "reconstruction_max_abs": rm, "residual_max_abs": em, "basis_max_abs": bm, "flags": flags}
+
+
+def c1_store(coeff: torch.Tensor, scales: torch.Tensor | None, quantize: bool, dtype: torch.dtype) -> torch.Tensor:
+    """The record's coefficients: int8 codes with the per-component scales, or C in ``dtype``."""
+    require_gpu(coeff, "coefficients")
+    coeff = coeff.contiguous()
+    rows, rank = coeff.shape
+    out = torch.empty(rows, rank, dtype=torch.int8 if quantize else dtype, device=coeff.device)
+    L = _lib.load()
+    _lib.check(L.stacr_c1_store(_ptr(coeff), rows, rank, _ptr(scales) if quantize else None, 1 if quantize else 0,
+                                _ptr(out), DTYPE_I8 if quantize else dtype_code(dtype), _stream(coeff.device)),
+               "stacr_c1_store")
+    return out
+
+
+def c1_restore(coeff: torch.Tensor, scales: torch.Tensor | None, basis: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """sum_j c'_j q_j in fp32 rounded once to ``dtype`` (c' = code * scale for int8 coefficients)."""
+    require_gpu(coeff, "coefficients")
+    coeff, basis = coeff.contiguous(), basis.contiguous()
+    rows, rank = coeff.shape
+    hidden = basis.shape[0]
+    out = torch.empty(rows, hidden, dtype=dtype, device=coeff.device)
+    quant = coeff.dtype == torch.int8
+    if quant and scales is None:
+        raise ValueError("int8 coefficients need their scales")
+    L = _lib.load()
+    _lib.check(L.stacr_c1_restore(_ptr(coeff), DTYPE_I8 if quant else dtype_code(coeff.dtype),
+                                  _ptr(scales.to(torch.float32).contiguous().reshape(-1)) if quant else None,
+                                  _ptr(basis), dtype_code(basis.dtype), rows, hidden, rank, _ptr(out), dtype_code(dtype),
+                                  _stream(coeff.device)), "stacr_c1_restore")
+    return out

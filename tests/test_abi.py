@@ -103,3 +103,23 @@ def test_python_errors_map_from_status_codes():
         L.check(2, "probe")
     with pytest.raises(ValueError):
         L.check(1, "probe")
+
+
+def test_compact_output_and_c1_host_rules():
+    """Host-side sizes and argument checks of the index stream and the C1 codec (no launches)."""
+    L = _lib()
+    lib = L.load()
+    nb, mw = ctypes.c_int64(), ctypes.c_int64()
+    assert lib.stacr_index_stream_sizes(41943, ctypes.byref(nb), ctypes.byref(mw)) == 0
+    assert (nb.value, mw.value) == (164, 164 * 256)
+    assert lib.stacr_index_stream_sizes(-1, ctypes.byref(nb), ctypes.byref(mw)) == 1
+    assert lib.stacr_index_stream_sizes(1 << 31, ctypes.byref(nb), ctypes.byref(mw)) == 1
+    assert lib.stacr_index_stream_encode(None, 3, 0, None, None, None, None, None) == 1  # idx_bytes 3
+    ws = ctypes.c_size_t()
+    assert lib.stacr_c1_workspace_bytes(8192, 1024, 96, ctypes.byref(ws)) == 0 and ws.value > 0
+    for rank in (0, 129):
+        assert lib.stacr_c1_workspace_bytes(8, 8, rank, ctypes.byref(ws)) == 1
+    # int8 storage needs the int8 code and its scales; a float store cannot be int8
+    assert lib.stacr_c1_store(None, 4, 8, None, 1, None, 1, None) == 1
+    assert lib.stacr_c1_store(None, 4, 8, None, 0, None, 3, None) == 1
+    assert lib.stacr_quantize_rows_int8(None, 7, 4, 8, None, None, None) == 1
