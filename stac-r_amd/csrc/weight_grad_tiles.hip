@@ -56,6 +56,10 @@ static_assert(kOffWords % 256 == 0, "offsets are staged in whole 1 KiB copies");
 
 constexpr int kNT = 4;               // 16-column matrix-core tiles of column entries per part
 constexpr int kNC = 16 * kNT;        // column features per part
+// LDS stride of one column of a block's column entries in the plan (elements): 8 past the block's
+// rows, so that the 16 columns a 16-lane group reads when the tile is written out in lane order
+// start in different banks
+constexpr int kBtStride = kTB + 8;
 
 struct TileHdr {  // per (block, part)
     uint32_t light_base;   // the region's first word in the record array (its offsets, then its records)
@@ -220,14 +224,17 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
     __shared__ uint32_t s_key[kPartMax];         // selection keys, then light offsets
     __shared__ int32_t s_slot[kPartMax];         // column slot of each feature of the part, or -1
     __shared__ uint32_t s_mask[kPartMax * 16];   // light rows of each feature (512-bit bitmaps)
-    __shared__ __attribute__((aligned(16))) BE s_bt[kNC * kTB];  // the block's column entries [slot][t]
+    __shared__ __attribute__((aligned(16))) BE s_bt[kNC * kBtStride];  // the block's column entries [slot][t]
     __shared__ uint32_t s_tot[kWaves];
 
     const int b = blockIdx.x, part = blockIdx.y, tid = threadIdx.x;
+    // with entries, the workgroups past the last part pack the coefficient operands, in parallel
+    // with the parts' entry work; without, part 0 packs them
+    const bool pack_c = a.sparse ? part == a.n_parts : part == 0;
     const int64_t plo = (int64_t)part * a.part_w;
     const int pw = (int)(a.d_in - plo < a.part_w ? a.d_in - plo : a.part_w);
 
-    if (a.sparse) {
+    if (a.sparse && !pack_c) {
         // ---- entry range of the block (clamped, whatever the starts hold)
         int64_t e_b0 = a.bstart[b], e_b1 = a.bstart[b + 1];
         e_b0 = e_b0 < a.nnz ? e_b0 : a.nnz;
@@ -277,7 +284,7 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         }
 
         // ---- this block's entries: the column tile and the light bitmaps
-        for (int i = tid; i < kNC * kTB; i += kThreads) s_bt[i] = 0;
+        for (int i = tid; i < kNC * kBtStride; i += kThreads) s_bt[i] = 0;
         for (int i = tid; i < kPartMax * 16; i += kThreads) s_mask[i] = 0u;
         __syncthreads();
         const int64_t t_base = (int64_t)b * kTB;
@@ -315,8 +322,8 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
                 if (f < 0 || f >= pw) continue;
                 const int s = s_slot[f];
                 if (s >= 0) {
-                    if constexpr (BT8) s_bt[s * kTB + tl] = (BE)(uint8_t)(int8_t)(int)val[k];
-                    else s_bt[s * kTB + tl] = (BE)to_g16(val[k], a.g_dt);
+                    if constexpr (BT8) s_bt[s * kBtStride + tl] = (BE)(uint8_t)(int8_t)(int)val[k];
+                    else s_bt[s * kBtStride + tl] = (BE)to_g16(val[k], a.g_dt);
                 } else {
                     atomicOr(&s_mask[f * 16 + (tl >> 5)], 1u << (tl & 31));
                 }
@@ -367,13 +374,13 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         BV *bt = static_cast<BV *>(a.bt) + ((int64_t)b * a.n_parts + part) * kNT * kWaves * 64;
         for (int u = tid; u < kNT * kWaves * 64; u += kThreads) {
             const int l = u & 63, w = (u >> 6) & 15, i = u >> 10;
-            bt[u] = *reinterpret_cast<const BV *>(s_bt + (16 * i + (l & 15)) * kTB + 32 * w + 8 * (l >> 4));
+            bt[u] = *reinterpret_cast<const BV *>(s_bt + (16 * i + (l & 15)) * kBtStride + 32 * w + 8 * (l >> 4));
         }
     }
 
-    // ---- the block's coefficient operands [C | 1] (part 0): (wave w, row group g, column n)
-    // holds rows 32 w + 8 g .. + 7 of column n
-    if (part == 0) {
+    // ---- the block's coefficient operands [C | 1]: (wave w, row group g, column n) holds rows
+    // 32 w + 8 g .. + 7 of column n
+    if (pack_c) {
         const uint16_t *c = static_cast<const uint16_t *>(a.coeff);
         const uint32_t one = a.g_dt == STACR_DTYPE_BF16 ? 0x3f80u : 0x3c00u;
         uint16_t *cp = a.cp + (int64_t)b * kTB * a.ncol;
@@ -937,7 +944,7 @@ int stacr_tiles_launch(const StacrGradArgs &a)
         rc = stacr_hip_check(hipGetLastError(), "weight_grad entry count");
         if (rc) return rc;
     }
-    const dim3 pgrid((unsigned)g.n_blocks, g.sparse ? (unsigned)g.n_parts : 1u);
+    const dim3 pgrid((unsigned)g.n_blocks, g.sparse ? (unsigned)g.n_parts + 1u : 1u);
     if (g.bt8) stacr_launch("k_dw_plan", s, [&] { k_tile_plan<true><<<pgrid, kThreads, 0, s>>>(t); });
     else stacr_launch("k_dw_plan", s, [&] { k_tile_plan<false><<<pgrid, kThreads, 0, s>>>(t); });
     rc = stacr_hip_check(hipGetLastError(), "weight_grad plan");
