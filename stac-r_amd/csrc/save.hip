@@ -1607,6 +1607,20 @@ __device__ __forceinline__ uint32_t bf16_key(uint32_t bits16)
     return __float_as_uint(bf16_bits_to_f(bits16 & 0xffffu)) & 0x7fffffffu;
 }
 
+// Two fp32 values rounded to bf16 by one v_cvt_pk_bf16_f32 (the same rounding as two single
+// conversions): lo in bits 15..0, hi in bits 31..16.
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi)
+{
+    typedef __attribute__((ext_vector_type(2))) float f2;
+    typedef __attribute__((ext_vector_type(2))) __bf16 b2;
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, b2));
+}
+
+// Level-0 bins (key bits 30..20) of the two bf16 residuals of a packed word: a bf16 value's key is
+// its bits 14..0 shifted up by 16, so its bin is bits 14..4 of the value.
+__device__ __forceinline__ uint32_t bin_lo(uint32_t w) { return __builtin_amdgcn_ubfe(w, 4, 11); }
+__device__ __forceinline__ uint32_t bin_hi(uint32_t w) { return __builtin_amdgcn_ubfe(w, 20, 11); }
+
 // Pass 1: as k_proj_hist_b (coefficients computed or loaded, level-0 histogram with its coarse
 // sums, max key), then the workgroup's cut and its candidates.
 template <int R>
@@ -1676,24 +1690,37 @@ __global__ __launch_bounds__(kBlock) void k_proj_cand(SaveGeom g, FastGeom fg, c
         batch_coeff_from_acc<DT, R>(acc, fg.W, slot, s_part, s_c, row0, g.rpi, row_end, g.rank,
                                     reinterpret_cast<T *>(coeff), c);
     }
-    // residuals packed as bf16 (exact), the histogram and the max key
+    // residuals r = rnd(x - rnd(sum_j c_j q_j)) (the chain of batch_residual), rounded two at a time
+    // into the packed bf16 words they are kept as; the histogram bins and the max key come from
+    // those words (the max as a packed 16-bit max of |r|'s bits)
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    u16x2 kmax2 = {0, 0};
     uint4 rp[kLdsRes ? 1 : NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         if (!(col_ok && ld.rows[i] < row_end)) continue;
-        float xv[V], r[V];
+        float xv[V];
         ld.x_at(i, true, xv);
-        batch_residual<DT, R, V>(xv, c + i * R, q, r);
-        const uint4 pr = pack_raw<DT, V>(r);
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float p0 = 0.f, p1 = 0.f;
+#pragma unroll
+            for (int j = 0; j < R; ++j) {
+                p0 = fmaf(c[i * R + j], q[2 * k][j], p0);
+                p1 = fmaf(c[i * R + j], q[2 * k + 1][j], p1);
+            }
+            const uint32_t pb = bf16_pair(p0, p1);
+            w[k] = bf16_pair(xv[2 * k] - __uint_as_float(pb << 16), xv[2 * k + 1] - __uint_as_float(pb & 0xffff0000u));
+            atomicAdd(&s_hist[bin_lo(w[k])], 1u);
+            atomicAdd(&s_hist[bin_hi(w[k])], 1u);
+            kmax2 = __builtin_elementwise_max(kmax2, __builtin_bit_cast(u16x2, w[k] & 0x7fff7fffu));
+        }
+        const uint4 pr = make_uint4(w[0], w[1], w[2], w[3]);
         if constexpr (kLdsRes) s_res[i * kBlock + threadIdx.x] = pr;
         else rp[i] = pr;
-#pragma unroll
-        for (int e = 0; e < V; ++e) {
-            const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
-            atomicAdd(&s_hist[key >> kDigitShift[0]], 1u);
-            kmax = max(kmax, key);
-        }
     }
+    kmax = (uint32_t)max(kmax2.x, kmax2.y) << 16;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, off, 64));
     if (lane == 0) s_wmax[wave] = kmax;
@@ -1738,8 +1765,10 @@ __global__ __launch_bounds__(kBlock) void k_proj_cand(SaveGeom g, FastGeom fg, c
             const uint4 pr = kLdsRes ? s_res[i * kBlock + threadIdx.x] : rp[kLdsRes ? 0 : i];
             const uint32_t w[4] = {pr.x, pr.y, pr.z, pr.w};
 #pragma unroll
-            for (int e = 0; e < V; ++e)
-                m |= (bf16_key(w[e >> 1] >> (16 * (e & 1))) >> kDigitShift[0]) >= cut ? 1u << e : 0u;
+            for (int k = 0; k < 4; ++k) {
+                m |= bin_lo(w[k]) >= cut ? 1u << (2 * k) : 0u;
+                m |= bin_hi(w[k]) >= cut ? 2u << (2 * k) : 0u;
+            }
         }
         msk[i] = m;
         cnt[i] = incl[i] = (uint32_t)__popc(m);
