@@ -8,8 +8,9 @@ residual_mode global_topk, int8 residual values.  Synthetic inputs with the conf
 timing.
 
 One step = the two library calls STACRFunction makes for the STAC-R part of a layer-step:
-stacr_save in forward (coefficients, exact global top-k selection, quantization) and
-stacr_weight_grad in backward (dW = (G^T C) Q^T + G^T R_s).  The layer's other work is the
+stacr_save_census in forward (coefficients, exact global top-k selection, quantization, and the
+entry census it hands to the backward) and stacr_weight_grad_census in backward
+(dW = (G^T C) Q^T + G^T R_s).  The layer's other work is the
 native nn.Linear / Conv1D arithmetic, unchanged by STAC-R and bit-equal to it (Y = X W^T + b,
 grad_input = G W, grad_bias = G.sum(0)); it is not timed, and the time of G.sum(0) is reported
 beside the line.  K steps are timed as eager launches and replayed from a HIP graph captured
@@ -203,9 +204,10 @@ def layer_workload(name, n, d_in, d_out, rank, budget, mode, steps, warmup, logn
     k = kernels.residual_plan(n, d_in, mode, budget, CHUNK)[1] if budget > 0 else 0
 
     def step():
-        coeff, idx, data, scale = kernels.save(x, q, mode=mode, budget=budget, chunk_rows=CHUNK, bits=BITS)
+        coeff, idx, data, scale, census = kernels.save_with_census(x, q, mode=mode, budget=budget, chunk_rows=CHUNK,
+                                                                   bits=BITS)
         res = (idx, data, scale) if idx is not None else None
-        dw, _ = kernels.weight_grad(g, coeff, q, res, BITS, True, torch.bfloat16)
+        dw, _ = kernels.weight_grad(g, coeff, q, res, BITS, True, torch.bfloat16, census=census)
         return coeff, idx, data, scale, dw
 
     eager, graph, note = time_steps(step, steps, warmup, check_layer)
@@ -296,8 +298,9 @@ def main() -> int:
     k_total, k_saved, _ = kernels.residual_plan(N, D_IN, MODE, BUDGET, CHUNK)
 
     def step():
-        coeff, idx, data, scale = kernels.save(x, q, mode=MODE, budget=BUDGET, chunk_rows=CHUNK, bits=BITS)
-        dw, _ = kernels.weight_grad(g, coeff, q, (idx, data, scale), BITS, True, torch.bfloat16)
+        coeff, idx, data, scale, census = kernels.save_with_census(x, q, mode=MODE, budget=BUDGET, chunk_rows=CHUNK,
+                                                                   bits=BITS)
+        dw, _ = kernels.weight_grad(g, coeff, q, (idx, data, scale), BITS, True, torch.bfloat16, census=census)
         return coeff, idx, data, scale, dw
 
     print(f"[bench] workload ready: k={k_saved}", file=sys.stderr, flush=True)

@@ -108,6 +108,22 @@ int stacr_save(const void *x, const void *q, int dtype, int64_t rows, int64_t fe
                size_t workspace_bytes, void *stream);
 
 /*
+ * stacr_save that can also write an entry census for the weight gradient (no counterpart in the
+ * reference: an internal hand-off between the save and the backward of one layer, so that the
+ * backward skips its own count of the entries).  The census (census_bytes from
+ * stacr_save_census_bytes; uint32 words) holds, per input feature, the number of saved entries
+ * (in 8 copies, [copy][feats], to be summed) and the first entry of every block of 512 rows
+ * ([ceil(rows / 512) + 1], the last = nnz).  The save fills it when its bf16 candidate passes run
+ * without a trim; *census_written (host memory) is set to 1 then, else 0 (pass the census to
+ * stacr_weight_grad_census only when it is 1).  Outputs otherwise as stacr_save.
+ */
+int stacr_save_census_bytes(int64_t rows, int64_t feats, size_t *bytes);
+int stacr_save_census(const void *x, const void *q, int dtype, int64_t rows, int64_t feats, int rank, int mode,
+                      double budget, int64_t chunk_rows, int bits, void *coeff, void *idx, int index_bytes,
+                      void *data, float *scale, void *workspace, size_t workspace_bytes, void *census,
+                      size_t census_bytes, int *census_written, void *stream);
+
+/*
  * Selection and quantization only, on caller-supplied coefficients (rows x rank, dtype):
  * the reference's _select_residual(x, coeff, basis, ...) followed by quantize_values
  * (stacr/layers.py:44-102,148).  Same residual arithmetic, rules and outputs as stacr_save;
@@ -146,6 +162,14 @@ int stacr_weight_grad(const void *g, int dtype, int64_t rows, int64_t d_out, con
                       const void *data, const float *scale, int bits, int val_dtype, int64_t nnz,
                       int transposed, void *dw, int dw_dtype, void *dbias, int dbias_dtype,
                       void *workspace, size_t workspace_bytes, void *stream);
+/* stacr_weight_grad with the census a stacr_save_census call wrote for these entries (same rows,
+ * d_in and residual): the matrix-core path takes the counts and block starts from it instead of
+ * counting (one launch fewer); the other paths ignore it.  Same results as stacr_weight_grad. */
+int stacr_weight_grad_census(const void *g, int dtype, int64_t rows, int64_t d_out, const void *coeff, const void *q,
+                             int64_t d_in, int rank, const void *idx, int index_bytes, const void *data,
+                             const float *scale, int bits, int val_dtype, int64_t nnz, int transposed, void *dw,
+                             int dw_dtype, void *dbias, int dbias_dtype, const void *census, void *workspace,
+                             size_t workspace_bytes, void *stream);
 
 /*
  * Allocation-free weight gradient.  No counterpart in the reference: it is for callers that cannot

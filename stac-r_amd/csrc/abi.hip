@@ -130,10 +130,12 @@ int stacr_save_workspace_bytes(int64_t rows, int64_t feats, int rank, int dtype,
     return STACR_OK;
 }
 
-int stacr_save(const void *x, const void *q, int dtype, int64_t rows, int64_t feats, int rank, int mode,
-               double budget, int64_t chunk_rows, int bits, void *coeff, void *idx, int index_bytes, void *data,
-               float *scale, void *workspace, size_t workspace_bytes, void *stream)
+static int save_impl(const void *x, const void *q, int dtype, int64_t rows, int64_t feats, int rank, int mode,
+                     double budget, int64_t chunk_rows, int bits, void *coeff, void *idx, int index_bytes, void *data,
+                     float *scale, void *workspace, size_t workspace_bytes, void *stream, void *census,
+                     size_t census_bytes, int *census_written)
 {
+    if (census_written) *census_written = 0;
     StacrSaveArgs a;
     int rc = fill_save_args(rows, feats, rank, dtype, mode, budget, chunk_rows, bits, &a);
     if (rc) return rc;
@@ -157,7 +159,40 @@ int stacr_save(const void *x, const void *q, int dtype, int64_t rows, int64_t fe
     a.workspace = workspace;
     a.workspace_bytes = workspace_bytes;
     a.stream = static_cast<hipStream_t>(stream);
+    if (census) {
+        if (census_bytes < (size_t)census_words(rows, feats) * 4)
+            return stacr_fail(STACR_ERR_INVALID, "stacr_save_census: census has %zu bytes, needs %zu", census_bytes,
+                              (size_t)census_words(rows, feats) * 4);
+        a.census = static_cast<uint32_t *>(census);
+        a.census_written = census_written;
+    }
     return stacr_save_launch(a);
+}
+
+int stacr_save(const void *x, const void *q, int dtype, int64_t rows, int64_t feats, int rank, int mode,
+               double budget, int64_t chunk_rows, int bits, void *coeff, void *idx, int index_bytes, void *data,
+               float *scale, void *workspace, size_t workspace_bytes, void *stream)
+{
+    return save_impl(x, q, dtype, rows, feats, rank, mode, budget, chunk_rows, bits, coeff, idx, index_bytes, data,
+                     scale, workspace, workspace_bytes, stream, nullptr, 0, nullptr);
+}
+
+int stacr_save_census_bytes(int64_t rows, int64_t feats, size_t *bytes)
+{
+    if (rows < 0 || feats < 0 || !bytes) return stacr_fail(STACR_ERR_INVALID, "stacr_save_census_bytes: bad argument");
+    *bytes = (size_t)census_words(rows, feats) * 4;
+    return STACR_OK;
+}
+
+int stacr_save_census(const void *x, const void *q, int dtype, int64_t rows, int64_t feats, int rank, int mode,
+                      double budget, int64_t chunk_rows, int bits, void *coeff, void *idx, int index_bytes, void *data,
+                      float *scale, void *workspace, size_t workspace_bytes, void *census, size_t census_bytes,
+                      int *census_written, void *stream)
+{
+    if (!census || !census_written)
+        return stacr_fail(STACR_ERR_INVALID, "stacr_save_census: census and census_written must be non-NULL");
+    return save_impl(x, q, dtype, rows, feats, rank, mode, budget, chunk_rows, bits, coeff, idx, index_bytes, data,
+                     scale, workspace, workspace_bytes, stream, census, census_bytes, census_written);
 }
 
 int stacr_select_residual(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t feats,
@@ -228,10 +263,10 @@ int stacr_weight_grad_workspace_bytes(int64_t rows, int64_t d_out, int64_t d_in,
     return STACR_OK;
 }
 
-int stacr_weight_grad(const void *g, int dtype, int64_t rows, int64_t d_out, const void *coeff, const void *q,
-                      int64_t d_in, int rank, const void *idx, int index_bytes, const void *data, const float *scale,
-                      int bits, int val_dtype, int64_t nnz, int transposed, void *dw, int dw_dtype, void *dbias,
-                      int dbias_dtype, void *workspace, size_t workspace_bytes, void *stream)
+static int grad_impl(const void *g, int dtype, int64_t rows, int64_t d_out, const void *coeff, const void *q,
+                     int64_t d_in, int rank, const void *idx, int index_bytes, const void *data, const float *scale,
+                     int bits, int val_dtype, int64_t nnz, int transposed, void *dw, int dw_dtype, void *dbias,
+                     int dbias_dtype, void *workspace, size_t workspace_bytes, void *stream, const void *census)
 {
     StacrGradArgs a;
     int rc = fill_grad_args(rows, d_out, d_in, rank, nnz, &a);
@@ -265,7 +300,28 @@ int stacr_weight_grad(const void *g, int dtype, int64_t rows, int64_t d_out, con
     a.workspace = workspace;
     a.workspace_bytes = workspace_bytes;
     a.stream = static_cast<hipStream_t>(stream);
+    a.census = static_cast<const uint32_t *>(census);
     return stacr_grad_launch(a);
+}
+
+int stacr_weight_grad(const void *g, int dtype, int64_t rows, int64_t d_out, const void *coeff, const void *q,
+                      int64_t d_in, int rank, const void *idx, int index_bytes, const void *data, const float *scale,
+                      int bits, int val_dtype, int64_t nnz, int transposed, void *dw, int dw_dtype, void *dbias,
+                      int dbias_dtype, void *workspace, size_t workspace_bytes, void *stream)
+{
+    return grad_impl(g, dtype, rows, d_out, coeff, q, d_in, rank, idx, index_bytes, data, scale, bits, val_dtype, nnz,
+                     transposed, dw, dw_dtype, dbias, dbias_dtype, workspace, workspace_bytes, stream, nullptr);
+}
+
+int stacr_weight_grad_census(const void *g, int dtype, int64_t rows, int64_t d_out, const void *coeff, const void *q,
+                             int64_t d_in, int rank, const void *idx, int index_bytes, const void *data,
+                             const float *scale, int bits, int val_dtype, int64_t nnz, int transposed, void *dw,
+                             int dw_dtype, void *dbias, int dbias_dtype, const void *census, void *workspace,
+                             size_t workspace_bytes, void *stream)
+{
+    if (!census) return stacr_fail(STACR_ERR_INVALID, "stacr_weight_grad_census: census is NULL");
+    return grad_impl(g, dtype, rows, d_out, coeff, q, d_in, rank, idx, index_bytes, data, scale, bits, val_dtype, nnz,
+                     transposed, dw, dw_dtype, dbias, dbias_dtype, workspace, workspace_bytes, stream, census);
 }
 
 }  // extern "C"

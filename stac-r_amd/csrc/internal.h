@@ -264,8 +264,24 @@ struct StacrSaveArgs {
     void *workspace;
     size_t workspace_bytes;
     hipStream_t stream;
+    // optional entry census for the weight gradient (NULL: none); *census_written (host) tells
+    // whether this save filled it
+    uint32_t *census = nullptr;
+    int *census_written = nullptr;
 };
 size_t stacr_save_ws_layout(const StacrSaveArgs &a, size_t *offsets);
+
+// Entry census: what the weight gradient's matrix-core plan needs to know about a save's residual
+// entries, written by the save's emission pass when it can (bf16 candidate passes, no trim):
+// per-feature entry counts in kCensusCopies copies ([copy][feats], summed by the reader), then
+// the first entry of every block of kCensusRows token rows ([ceil(rows / kCensusRows) + 1], the
+// last = the entry count).
+constexpr int kCensusCopies = 8;
+constexpr int kCensusRows = 512;
+inline int64_t census_words(int64_t rows, int64_t feats)
+{
+    return (int64_t)kCensusCopies * feats + (rows + kCensusRows - 1) / kCensusRows + 1;
+}
 int stacr_save_launch(const StacrSaveArgs &a);
 int stacr_quantize_launch(const void *v, int dtype, int64_t n, int bits, void *data, float *scale, void *workspace,
                           hipStream_t s);
@@ -292,6 +308,7 @@ struct StacrGradArgs {
     void *workspace;
     size_t workspace_bytes;
     hipStream_t stream;
+    const uint32_t *census = nullptr;  // optional entry census from the save (see above)
 };
 size_t stacr_grad_ws_layout(const StacrGradArgs &a, size_t *offsets);
 int stacr_grad_launch(const StacrGradArgs &a);

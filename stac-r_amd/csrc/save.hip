@@ -171,7 +171,7 @@ __global__ void k_zero_u32(uint32_t *p, int64_t n)
 // Set-up of a save: the padded fp32 basis, and the histograms and max key cleared (one launch).
 template <int DT>
 __global__ void k_prep(const typename Act<DT>::T *__restrict__ q, int64_t d, int rank, int R, float *__restrict__ qp,
-                       uint32_t *__restrict__ zero, int64_t n_zero)
+                       uint32_t *__restrict__ zero, int64_t n_zero, uint32_t *__restrict__ zero2, int64_t n_zero2)
 {
     const int64_t n = d * R;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
@@ -187,6 +187,7 @@ __global__ void k_prep(const typename Act<DT>::T *__restrict__ q, int64_t d, int
         if constexpr (sizeof(typename Act<DT>::T) == 2) qph[j * d + row] = j < rank ? q[row * rank + j] : (typename Act<DT>::T)0;
     }
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_zero; i += step) zero[i] = 0u;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_zero2; i += step) zero2[i] = 0u;
 }
 
 // One radix level of one chunk, computed by a whole workgroup: the bin holding the need-th largest
@@ -1947,110 +1948,17 @@ __global__ __launch_bounds__(kBlock) void k_refine_cand(SaveGeom g, FastGeom fg,
         if (s_hist[b]) atomicAdd(&gh[b], s_hist[b]);
 }
 
-// Emission (bf16, batched, candidates): the final selection and the workgroup's offset and tie
-// budget as in k_emit_b, then its survivors from the candidate list (or, for a workgroup without a
-// usable list, from recomputed residuals) quantized and written in ascending flat order.
-template <int R, int HC>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) void k_emit_cand(
-    SaveGeom g, FastGeom fg, const uint16_t *__restrict__ x, const float *__restrict__ qp,
-    const uint16_t *__restrict__ coeff, SelState *__restrict__ state, uint32_t chunk_k,
-    const uint32_t *__restrict__ maxkey, OutSpec o, float *scale_out, int to_list, const uint32_t *__restrict__ hist,
-    const uint32_t *__restrict__ fold, int64_t fold_stride, const uint32_t *__restrict__ cand_idx,
-    const uint16_t *__restrict__ cand_val, const CandMeta *__restrict__ meta)
+// The emission's fallback for a workgroup without a usable candidate list: its residuals
+// recomputed one iteration at a time, survivors compacted in the order of k_emit_b and handed to
+// `put` (position, flat index, value).
+template <int R, typename Put>
+__device__ __forceinline__ void emit_cand_fallback(const SaveGeom &g, const FastGeom &fg, const uint16_t *__restrict__ x,
+                                                   const float *__restrict__ qp, const uint16_t *__restrict__ coeff,
+                                                   int64_t row0, int64_t row_end, uint32_t T, const WgOffset &wo,
+                                                   uint32_t *s_wt, Put &put)
 {
-    constexpr int DT = STACR_DTYPE_BF16, NB = Batch<R>::NB;
-    __shared__ uint32_t s_off[kWaves];
-    __shared__ uint32_t s_wt[kWaves];
-    int64_t chunk, row0, row_end;
-    wg_rows(g, blockIdx.x, chunk, row0, row_end);
-    const int64_t w = blockIdx.x - chunk * g.wgs_per_chunk;
-    const int64_t wg0 = chunk * g.wgs_per_chunk;
+    constexpr int NB = Batch<R>::NB;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const bool has_rows = row0 < row_end;
-    uint32_t hw[HC];
-    {
-        const uint32_t *h1 = hist + (chunk * 3 + 1) * HC * kBins + ((threadIdx.x & 15) << 7);
-#pragma unroll
-        for (int c = 0; c < HC; ++c) hw[c] = h1[c * kBins];
-    }
-    const CandMeta mine = meta[has_rows ? blockIdx.x : 0];
-    // the candidates go out before the selection's and the offsets' words
-    CandVals vals;
-    uint32_t flat[kCandPer];
-    {
-        const int64_t base = (int64_t)blockIdx.x * kCandCap + kCandPer * threadIdx.x;
-        const uint4 v = *reinterpret_cast<const uint4 *>(cand_val + base);
-        const uint4 f0 = *reinterpret_cast<const uint4 *>(cand_idx + base);
-        const uint4 f1 = *reinterpret_cast<const uint4 *>(cand_idx + base + 4);
-        vals.w[0] = v.x; vals.w[1] = v.y; vals.w[2] = v.z; vals.w[3] = v.w;
-        flat[0] = f0.x; flat[1] = f0.y; flat[2] = f0.z; flat[3] = f0.w;
-        flat[4] = f1.x; flat[5] = f1.y; flat[6] = f1.z; flat[7] = f1.w;
-    }
-    SelState sel1;
-    const SelState st = fold_select<HC>(hw, state[chunk * 3 + 0], &sel1);
-    if (w == 0 && threadIdx.x == 0) {
-        state[chunk * 3 + 1] = sel1;
-        state[chunk * 3 + 2] = st;
-    }
-    const uint32_t b1 = (st.prefix >> 16) & 15u;
-    const uint32_t *fhi = fold + (int64_t)(b1 + 1) * fold_stride + wg0;
-    const uint32_t *flo = fold + (int64_t)b1 * fold_stride + wg0;
-    const uint32_t mk = *maxkey;
-    const uint32_t T = st.prefix;
-    const float amax = Act<DT>::rnd(__uint_as_float(mk));
-    const float scale = o.bits ? quant_scale(mk, o.bits, amax) : 1.f;
-    if (!to_list && blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
-    if (!has_rows) return;  // uniform: a trailing workgroup with no rows writes nothing
-    // the workgroup's output offset and tie budget (the earlier workgroups' records)
-    WgOffset wo;
-    {
-        uint32_t gt = 0u, eq = 0u;
-        for (int64_t v = threadIdx.x; v < w; v += kBlock) {
-            const uint32_t hi = fhi[v], lo = flo[v];
-            gt += hi;
-            eq += lo - hi;
-        }
-        const uint32_t gt_before = block_sum(gt, s_off);
-        const uint32_t eq_before = block_sum(eq, s_off);
-        const uint32_t my_eq = flo[w] - fhi[w];
-        const uint32_t take = eq_before >= st.need ? 0u : min(my_eq, st.need - eq_before);
-        wo = WgOffset{(uint32_t)chunk * chunk_k + gt_before + min(st.need, eq_before), take};
-    }
-    auto put = [&](uint32_t pos, uint32_t fl, float rv) {
-        if (pos >= o.cap) {
-            // unreachable when the counts are consistent; never write out of bounds
-        } else if (to_list) {
-            o.list_rbits[pos] = __float_as_uint(rv);
-            o.list_idx[pos] = fl;
-        } else {
-            write_entry<DT>(o, pos, fl, rv, scale);
-        }
-    };
-    const bool valid = mine.count <= (uint32_t)kCandCap && mine.cut <= (T >> kDigitShift[0]);  // uniform
-    if (valid) {
-        uint32_t ngt = 0u, neq = 0u, key[kCandPer];
-#pragma unroll
-        for (int j = 0; j < kCandPer; ++j) {
-            const bool in = kCandPer * threadIdx.x + j < mine.count;
-            key[j] = in ? bf16_key(vals.bits(j)) : 0u;
-            ngt += in && key[j] > T;
-            neq += in && key[j] == T;
-        }
-        uint32_t tot;
-        const uint32_t pre = block_exclusive_scan(ngt | (neq << 16), s_off, &tot);
-        uint32_t gb = pre & 0xffffu, eb = pre >> 16;
-#pragma unroll
-        for (int j = 0; j < kCandPer; ++j) {
-            if (kCandPer * threadIdx.x + j >= mine.count) break;
-            const bool is_gt = key[j] > T, is_eq = key[j] == T;
-            if (is_gt || (is_eq && eb < wo.take)) put(wo.off + gb + min(eb, wo.take), flat[j], bf16_bits_to_f(vals.bits(j)));
-            gb += is_gt;
-            eb += is_eq;
-        }
-        return;
-    }
-    // fallback: the workgroup's residuals recomputed one iteration at a time, survivors compacted
-    // in the order of k_emit_b
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
     const int64_t col = (int64_t)u * 8, colc = min(col, g.d - 8);
     const bool col_ok = col < g.d;
@@ -2103,6 +2011,126 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
             eb += is_eq;
         }
         before_iter += iter_total;
+    }
+}
+
+// Emission (bf16, batched, candidates): the final selection and the workgroup's offset and tie
+// budget as in k_emit_b, then its survivors from the candidate list (or, for a workgroup without a
+// usable list, from recomputed residuals) quantized and written in ascending flat order.
+template <int R, int HC>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) void k_emit_cand(
+    SaveGeom g, FastGeom fg, const uint16_t *__restrict__ x, const float *__restrict__ qp,
+    const uint16_t *__restrict__ coeff, SelState *__restrict__ state, uint32_t chunk_k,
+    const uint32_t *__restrict__ maxkey, OutSpec o, float *scale_out, int to_list, const uint32_t *__restrict__ hist,
+    const uint32_t *__restrict__ fold, int64_t fold_stride, const uint32_t *__restrict__ cand_idx,
+    const uint16_t *__restrict__ cand_val, const CandMeta *__restrict__ meta, uint32_t *__restrict__ census,
+    uint32_t n_entries)
+{
+    constexpr int DT = STACR_DTYPE_BF16;
+    __shared__ uint32_t s_off[kWaves];
+    __shared__ uint32_t s_wt[kWaves];
+    __shared__ uint32_t s_feat[kBins];  // with a census: this workgroup's entries per feature (d <= 2048)
+    int64_t chunk, row0, row_end;
+    wg_rows(g, blockIdx.x, chunk, row0, row_end);
+    const int64_t w = blockIdx.x - chunk * g.wgs_per_chunk;
+    const int64_t wg0 = chunk * g.wgs_per_chunk;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const bool has_rows = row0 < row_end;
+    uint32_t hw[HC];
+    {
+        const uint32_t *h1 = hist + (chunk * 3 + 1) * HC * kBins + ((threadIdx.x & 15) << 7);
+#pragma unroll
+        for (int c = 0; c < HC; ++c) hw[c] = h1[c * kBins];
+    }
+    const CandMeta mine = meta[has_rows ? blockIdx.x : 0];
+    // the candidates go out before the selection's and the offsets' words
+    CandVals vals;
+    uint32_t flat[kCandPer];
+    {
+        const int64_t base = (int64_t)blockIdx.x * kCandCap + kCandPer * threadIdx.x;
+        const uint4 v = *reinterpret_cast<const uint4 *>(cand_val + base);
+        const uint4 f0 = *reinterpret_cast<const uint4 *>(cand_idx + base);
+        const uint4 f1 = *reinterpret_cast<const uint4 *>(cand_idx + base + 4);
+        vals.w[0] = v.x; vals.w[1] = v.y; vals.w[2] = v.z; vals.w[3] = v.w;
+        flat[0] = f0.x; flat[1] = f0.y; flat[2] = f0.z; flat[3] = f0.w;
+        flat[4] = f1.x; flat[5] = f1.y; flat[6] = f1.z; flat[7] = f1.w;
+    }
+    SelState sel1;
+    const SelState st = fold_select<HC>(hw, state[chunk * 3 + 0], &sel1);
+    if (w == 0 && threadIdx.x == 0) {
+        state[chunk * 3 + 1] = sel1;
+        state[chunk * 3 + 2] = st;
+    }
+    const uint32_t b1 = (st.prefix >> 16) & 15u;
+    const uint32_t *fhi = fold + (int64_t)(b1 + 1) * fold_stride + wg0;
+    const uint32_t *flo = fold + (int64_t)b1 * fold_stride + wg0;
+    const uint32_t mk = *maxkey;
+    const uint32_t T = st.prefix;
+    const float amax = Act<DT>::rnd(__uint_as_float(mk));
+    const float scale = o.bits ? quant_scale(mk, o.bits, amax) : 1.f;
+    if (!to_list && blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
+    if (!has_rows) return;  // uniform: a trailing workgroup with no rows writes nothing
+    if (census)  // (cleared before the offset sums' barriers)
+        for (int f = threadIdx.x; f < kBins; f += kBlock) s_feat[f] = 0u;
+    // the workgroup's output offset and tie budget (the earlier workgroups' records)
+    WgOffset wo;
+    {
+        uint32_t gt = 0u, eq = 0u;
+        for (int64_t v = threadIdx.x; v < w; v += kBlock) {
+            const uint32_t hi = fhi[v], lo = flo[v];
+            gt += hi;
+            eq += lo - hi;
+        }
+        const uint32_t gt_before = block_sum(gt, s_off);
+        const uint32_t eq_before = block_sum(eq, s_off);
+        const uint32_t my_eq = flo[w] - fhi[w];
+        const uint32_t take = eq_before >= st.need ? 0u : min(my_eq, st.need - eq_before);
+        wo = WgOffset{(uint32_t)chunk * chunk_k + gt_before + min(st.need, eq_before), take};
+    }
+    auto put = [&](uint32_t pos, uint32_t fl, float rv) {
+        if (pos >= o.cap) {
+            // unreachable when the counts are consistent; never write out of bounds
+        } else if (to_list) {
+            o.list_rbits[pos] = __float_as_uint(rv);
+            o.list_idx[pos] = fl;
+        } else {
+            write_entry<DT>(o, pos, fl, rv, scale);
+        }
+        if (census) atomicAdd(&s_feat[fl % (uint32_t)g.d], 1u);
+    };
+    const bool valid = mine.count <= (uint32_t)kCandCap && mine.cut <= (T >> kDigitShift[0]);  // uniform
+    if (valid) {
+        uint32_t ngt = 0u, neq = 0u, key[kCandPer];
+#pragma unroll
+        for (int j = 0; j < kCandPer; ++j) {
+            const bool in = kCandPer * threadIdx.x + j < mine.count;
+            key[j] = in ? bf16_key(vals.bits(j)) : 0u;
+            ngt += in && key[j] > T;
+            neq += in && key[j] == T;
+        }
+        uint32_t tot;
+        const uint32_t pre = block_exclusive_scan(ngt | (neq << 16), s_off, &tot);
+        uint32_t gb = pre & 0xffffu, eb = pre >> 16;
+#pragma unroll
+        for (int j = 0; j < kCandPer; ++j) {
+            if (kCandPer * threadIdx.x + j >= mine.count) break;
+            const bool is_gt = key[j] > T, is_eq = key[j] == T;
+            if (is_gt || (is_eq && eb < wo.take)) put(wo.off + gb + min(eb, wo.take), flat[j], bf16_bits_to_f(vals.bits(j)));
+            gb += is_gt;
+            eb += is_eq;
+        }
+    } else {
+        emit_cand_fallback<R>(g, fg, x, qp, coeff, row0, row_end, T, wo, s_wt, put);
+    }
+    if (census) {  // the entries per feature (copy w % 8) and, at a block's first row, its first entry
+        __syncthreads();
+        const uint32_t d = (uint32_t)g.d;
+        uint32_t *counts = census + (int64_t)(blockIdx.x % kCensusCopies) * d;
+        for (uint32_t f = threadIdx.x; f < d; f += kBlock)
+            if (s_feat[f]) atomicAdd(&counts[f], s_feat[f]);
+        uint32_t *bstart = census + (int64_t)kCensusCopies * d;
+        if (threadIdx.x == 0 && row0 % kCensusRows == 0) bstart[row0 / kCensusRows] = wo.off;
+        if (blockIdx.x == 0 && threadIdx.x == 0) bstart[(g.rows + kCensusRows - 1) / kCensusRows] = n_entries;
     }
 }
 
@@ -2480,9 +2508,13 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     // padded basis; histograms and max key (contiguous in the layout) cleared in the same launch
     const int64_t n_zero = resid ? (int64_t)((off[WS_MAXKEY] + (size_t)p.g.hcopies * kMaxKeyStride * sizeof(uint32_t) -
                                               off[WS_HIST]) / sizeof(uint32_t)) : 0;
+    // the entry census (bf16 candidate passes without a trim, blocks of whole workgroups): its
+    // counts are cleared here and filled by the emission pass
+    const bool census = a.census && p.cand && !p.trim && kCensusRows % p.g.rows_per_wg == 0 && p.g.d <= kBins;
+    const int64_t n_census = census ? (int64_t)kCensusCopies * a.feats : 0;
     stacr_launch("k_prep", s, [&] {
-        k_prep<DT><<<grid_for(hmax<int64_t>(a.feats * p.Rq, n_zero)), kBlock, 0, s>>>(static_cast<const T *>(a.q), a.feats,
-                                                                                    a.rank, p.Rq, qp, hist, n_zero);
+        k_prep<DT><<<grid_for(hmax<int64_t>(hmax<int64_t>(a.feats * p.Rq, n_zero), n_census)), kBlock, 0, s>>>(
+            static_cast<const T *>(a.q), a.feats, a.rank, p.Rq, qp, hist, n_zero, census ? a.census : nullptr, n_census);
     });
     // batched fast path: one aligned vector per thread per row, basis columns in registers
     constexpr bool kFastOk = QREG && V == Act<DT>::kVec && V * R <= 64;
@@ -2587,10 +2619,13 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     if constexpr (kFastOk) {
         // the fold variant (bf16) reads the level-1 histogram copies; other types take the counts
         if constexpr (kCandOk) {
+            uint32_t *cen = census ? a.census : nullptr;
+            const uint32_t kt = (uint32_t)a.k_sum;  // the entries emitted (no trim: the chunks' k summed)
             if (cand && hc8)
-                stacr_launch("k_emit", s, [&] { k_emit_cand<R, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta); });
+                stacr_launch("k_emit", s, [&] { k_emit_cand<R, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt); });
             else if (cand)
-                stacr_launch("k_emit", s, [&] { k_emit_cand<R, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta); });
+                stacr_launch("k_emit", s, [&] { k_emit_cand<R, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt); });
+            if (census && a.census_written) *a.census_written = 1;
         }
         if (!cand && fast && hc8 && DT == STACR_DTYPE_BF16)
             stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V, kHistCopies, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs); });

@@ -52,6 +52,7 @@ constexpr int kMaxBlocks = 256;      // blocks per problem (rows <= 131072): hea
 constexpr int kBatch = 8;            // entries per thread whose loads the count and the plan issue together
 
 static_assert(kThreads == 2 * kTB, "two G tile rows per lane pair: one 16-byte copy per lane");
+static_assert(kTB == kCensusRows, "a save's entry census gives the first entry of every block");
 static_assert(kOffWords % 256 == 0, "offsets are staged in whole 1 KiB copies");
 
 constexpr int kNT = 4;               // 16-column matrix-core tiles of column entries per part
@@ -79,7 +80,8 @@ struct TileArgs {
     // geometry
     int n_blocks, n_parts, part_w, ncol, bias_col;
     // workspace
-    uint32_t *hist;     // [kChunks][d_in] entries per feature in each chunk
+    uint32_t *hist;     // [n_hist][d_in] partial entry counts per feature (chunks, or census copies)
+    int n_hist;
     uint32_t *bstart;   // [n_blocks + 1] first entry of each block
     uint16_t *cp;       // [n_blocks][16 waves][4 row groups][ncol][8] coefficient operands
     void *bt;           // [n_blocks][n_parts][nt][16 waves][64 lanes][8] column operands
@@ -249,7 +251,7 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         if (tid < pw) {
             uint32_t cnt = 0;
 #pragma unroll
-            for (int c = 0; c < kChunks; ++c) cnt += a.hist[(int64_t)c * a.d_in + plo + tid];
+            for (int c = 0; c < a.n_hist; ++c) cnt += a.hist[(int64_t)c * a.d_in + plo + tid];
             key = cnt ? ((cnt < 0xffffu ? cnt : 0xffffu) << 16) | (0xffffu - (uint32_t)tid) : 0u;
         }
         s_slot[tid] = -1;
@@ -928,9 +930,13 @@ int stacr_tiles_launch(const StacrGradArgs &a)
     t.ncol = g.ncol;
     t.bias_col = g.bias_col;
     t.cp = reinterpret_cast<uint16_t *>(ws + off[TW_CP]);
+    // with a census from the save, its per-feature counts and block starts replace the count pass
+    const bool census = g.sparse && a.census;
     if (g.sparse) {
-        t.hist = reinterpret_cast<uint32_t *>(ws + off[TW_HIST]);
-        t.bstart = reinterpret_cast<uint32_t *>(ws + off[TW_BSTART]);
+        t.hist = census ? const_cast<uint32_t *>(a.census) : reinterpret_cast<uint32_t *>(ws + off[TW_HIST]);
+        t.n_hist = census ? kCensusCopies : kChunks;
+        t.bstart = census ? const_cast<uint32_t *>(a.census) + (size_t)kCensusCopies * a.d_in
+                          : reinterpret_cast<uint32_t *>(ws + off[TW_BSTART]);
         t.bt = ws + off[TW_BT];
         t.light = reinterpret_cast<uint32_t *>(ws + off[TW_LIGHT]);
         t.hdr = reinterpret_cast<TileHdr *>(ws + off[TW_HDR]);
@@ -939,7 +945,7 @@ int stacr_tiles_launch(const StacrGradArgs &a)
     t.sparse = g.sparse ? 1 : 0;
     hipStream_t s = a.stream;
     int rc;
-    if (g.sparse) {
+    if (g.sparse && !census) {
         stacr_launch("k_dw_count", s, [&] { k_tile_count<<<kChunks, kThreads, 0, s>>>(t); });
         rc = stacr_hip_check(hipGetLastError(), "weight_grad entry count");
         if (rc) return rc;

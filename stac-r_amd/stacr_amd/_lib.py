@@ -34,6 +34,9 @@ SIGNATURES = {
     "stacr_save_workspace_bytes": ([_i64, _i64, _i32, _i32, _i32, _f64, _i64, _i32, _PSZ], _i32),
     "stacr_save": ([_p, _p, _i32, _i64, _i64, _i32, _i32, _f64, _i64, _i32, _p, _p, _i32, _p, _p, _p, _sz, _p],
                    _i32),
+    "stacr_save_census_bytes": ([_i64, _i64, _PSZ], _i32),
+    "stacr_save_census": ([_p, _p, _i32, _i64, _i64, _i32, _i32, _f64, _i64, _i32, _p, _p, _i32, _p, _p, _p, _sz, _p,
+                           _sz, _p, _p], _i32),
     "stacr_select_residual": ([_p, _p, _p, _i32, _i64, _i64, _i32, _i32, _f64, _i64, _i32, _p, _i32, _p, _p, _p,
                                _sz, _p], _i32),
     "stacr_quantize_values": ([_p, _i32, _i64, _i32, _p, _p, _p, _sz, _p], _i32),
@@ -42,6 +45,8 @@ SIGNATURES = {
     "stacr_weight_grad_workspace_bytes": ([_i64, _i64, _i64, _i32, _i64, _PSZ], _i32),
     "stacr_weight_grad": ([_p, _i32, _i64, _i64, _p, _p, _i64, _i32, _p, _i32, _p, _p, _i32, _i32, _i64, _i32, _p,
                            _i32, _p, _i32, _p, _sz, _p], _i32),
+    "stacr_weight_grad_census": ([_p, _i32, _i64, _i64, _p, _p, _i64, _i32, _p, _i32, _p, _p, _i32, _i32, _i64, _i32,
+                                  _p, _i32, _p, _i32, _p, _p, _sz, _p], _i32),
     "stacr_weight_grad_noalloc": ([_p, _i32, _i64, _i64, _p, _p, _i64, _i32, _p, _i32, _p, _p, _i32, _i32, _i64, _i32,
                                    _p, _i32, _p, _i32, _p], _i32),
     "stacr_adaptive_residual_plan": ([_i64, _i64, _f64, _i64, _P64, _P64, _PI32], _i32),

@@ -69,6 +69,16 @@ def save(x2d: torch.Tensor, q: torch.Tensor, *, mode: str, budget: float, chunk_
     x2d: rows x feats activation (cast to the compute dtype), q: feats x rank basis in that dtype.
     With ``coeff`` given, only selection and quantization run (stacr_select_residual).
     """
+    return _save(x2d, q, mode, budget, chunk_rows, bits, coeff, False)[:4]
+
+
+def save_with_census(x2d: torch.Tensor, q: torch.Tensor, *, mode: str, budget: float, chunk_rows: int, bits: int):
+    """save() plus the entry census the weight gradient can take instead of counting the entries
+    (stacr_save_census): (coeff, idx, data, scale, census or None when this save writes none)."""
+    return _save(x2d, q, mode, budget, chunk_rows, bits, None, True)
+
+
+def _save(x2d, q, mode, budget, chunk_rows, bits, coeff, want_census):
     require_gpu(x2d, "activation")
     x2d = x2d.contiguous()
     q = q.contiguous()
@@ -89,7 +99,20 @@ def save(x2d: torch.Tensor, q: torch.Tensor, *, mode: str, budget: float, chunk_
         idx, data, scale = _outputs(k_saved, bits, x2d.dtype, ib, device)
     else:
         idx = data = scale = None
-    if coeff is None:
+    census = None
+    if coeff is None and want_census and k_total > 0:
+        coeff = torch.empty(rows, rank, dtype=x2d.dtype, device=device)
+        cb = ctypes.c_size_t()
+        _lib.check(L.stacr_save_census_bytes(rows, feats, ctypes.byref(cb)), "stacr_save_census_bytes")
+        census = torch.empty(cb.value // 4, dtype=torch.int32, device=device)
+        written = ctypes.c_int(0)
+        _lib.check(L.stacr_save_census(_ptr(x2d), _ptr(q), dt, rows, feats, rank, MODE_CODES[mode], float(budget),
+                                       int(chunk_rows), int(bits), _ptr(coeff), _ptr(idx), ib, _ptr(data),
+                                       _ptr(scale), _ptr(ws), ws_bytes.value, _ptr(census), cb.value,
+                                       ctypes.byref(written), stream), "stacr_save_census")
+        if not written.value:
+            census = None
+    elif coeff is None:
         coeff = torch.empty(rows, rank, dtype=x2d.dtype, device=device)
         _lib.check(L.stacr_save(_ptr(x2d), _ptr(q), dt, rows, feats, rank, MODE_CODES[mode], float(budget),
                                 int(chunk_rows), int(bits), _ptr(coeff), _ptr(idx), ib, _ptr(data), _ptr(scale),
@@ -101,7 +124,7 @@ def save(x2d: torch.Tensor, q: torch.Tensor, *, mode: str, budget: float, chunk_
                                                MODE_CODES[mode], float(budget), int(chunk_rows), int(bits),
                                                _ptr(idx), ib, _ptr(data), _ptr(scale), _ptr(ws), ws_bytes.value,
                                                stream), "stacr_select_residual")
-    return coeff, idx, data, scale
+    return coeff, idx, data, scale, census
 
 
 def _factor_args(x2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor):
@@ -244,11 +267,12 @@ def oja_step(x2d: torch.Tensor, q: torch.Tensor, lr: float):
 
 
 def weight_grad(g2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, residual, bits: int, transposed: bool,
-                out_dtype: torch.dtype, bias_dtype: torch.dtype | None = None):
+                out_dtype: torch.dtype, bias_dtype: torch.dtype | None = None, census: torch.Tensor | None = None):
     """dW (and dbias when bias_dtype is given) from the saved factors (stacr/layers.py:172-198).
 
     ``residual`` is None or (idx, data, scale); ``coeff`` and ``q`` are cast to G's dtype first, as
-    the reference does.  dW is d_out x d_in, or d_in x d_out when ``transposed``.
+    the reference does.  dW is d_out x d_in, or d_in x d_out when ``transposed``.  ``census``: the
+    entry census save_with_census returned with this residual (the same dW, one launch fewer).
     """
     require_gpu(g2d, "grad_output")
     g2d = g2d.contiguous()
@@ -273,6 +297,13 @@ def weight_grad(g2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, residua
     _lib.check(L.stacr_weight_grad_workspace_bytes(rows, d_out, d_in, rank, nnz, ctypes.byref(ws_bytes)),
                "stacr_weight_grad")
     ws = torch.empty(max(1, ws_bytes.value), dtype=torch.uint8, device=device)
+    if census is not None and nnz:
+        _lib.check(L.stacr_weight_grad_census(_ptr(g2d), dt, rows, d_out, _ptr(coeff), _ptr(q), d_in, rank, _ptr(idx),
+                                              ib, _ptr(data), _ptr(scale), int(bits), vdt, nnz,
+                                              1 if transposed else 0, _ptr(dw), dtype_code(out_dtype), _ptr(db),
+                                              dtype_code(bias_dtype) if db is not None else 0, _ptr(census), _ptr(ws),
+                                              ws_bytes.value, _stream(device)), "stacr_weight_grad_census")
+        return dw, db
     _lib.check(L.stacr_weight_grad(_ptr(g2d), dt, rows, d_out, _ptr(coeff), _ptr(q), d_in, rank, _ptr(idx), ib,
                                    _ptr(data), _ptr(scale), int(bits), vdt, nnz, 1 if transposed else 0, _ptr(dw),
                                    dtype_code(out_dtype), _ptr(db), dtype_code(bias_dtype) if db is not None else 0,

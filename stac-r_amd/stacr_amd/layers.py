@@ -88,10 +88,11 @@ class STACRFunction(torch.autograd.Function):
         with torch.autocast(device_type=x.device.type, enabled=False):
             activation, q = x2d.to(out2d.dtype), basis.to(out2d.dtype)
             fused = mode in TOPK_SELECTORS or (mode == "block_sparse" and d_in % int(residual_block_size))
+            census = None
             if fused:  # projection, selection and quantization in one stacr_save call
                 sel = "global_topk" if mode == "global_topk" else "chunk_topk"
-                coeff, idx, data, scale = kernels.save(activation, q, mode=sel, budget=budget,
-                                                       chunk_rows=int(chunk_rows), bits=bits)
+                coeff, idx, data, scale, census = kernels.save_with_census(activation, q, mode=sel, budget=budget,
+                                                                           chunk_rows=int(chunk_rows), bits=bits)
                 length = int(idx.numel()) if idx is not None else 0
             else:  # projection, then the selector's kernels, then quantize_values
                 coeff, _, _, _ = kernels.save(activation, q, mode="chunk_topk", budget=0.0,
@@ -105,8 +106,11 @@ class STACRFunction(torch.autograd.Function):
         saved = [coeff, weight, q]
         if idx is not None:
             saved += [idx, data, scale]
-        ctx.save_for_backward(*saved)
+        ctx.save_for_backward(*saved)  # the reference's six (or three) saved tensors
         ctx.has_residual = idx is not None
+        # the save's entry census (an intermediate kept on ctx, outside the saved tensors): the
+        # backward skips its own count of the entries
+        ctx.census = census if idx is not None else None
         ctx.residual_bits = bits if idx is not None else 0
         ctx.residual_len = length if idx is not None else 0
         ctx.leading, ctx.in_features = x.shape[:-1], d_in
@@ -129,7 +133,7 @@ class STACRFunction(torch.autograd.Function):
             if ctx.needs_input_grad[1]:
                 res = tuple(residual) if ctx.has_residual and residual[0].numel() else None
                 grad_weight, _ = kernels.weight_grad(g2d, coeff, q, res, ctx.residual_bits, ctx.transposed,
-                                                     weight.dtype)
+                                                     weight.dtype, census=ctx.census)
             if ctx.needs_input_grad[2]:
                 grad_bias = g2d.sum(0).to(ctx.bias_dtype)
         return (grad_input, grad_weight, grad_bias) + (None,) * (ctx.arg_count - 3)

@@ -726,3 +726,43 @@ def test_turbo_step_50_freezes_basis_and_drops_residual(dev, full):
     if not full:
         low = (x.detach() @ step49) @ step49.t()
         torch.testing.assert_close(weight.grad, upstream.t() @ low)
+
+
+@pytest.mark.parametrize("rows,d_in,d_out,mode,budget,chunk,dtype,expect", [
+    (8192, 1024, 4096, "global_topk", 0.005, 512, "bf16", True),    # the north-star layer
+    (2048, 1024, 512, "chunk_topk", 0.01, 256, "bf16", True),
+    (64, 1024, 256, "chunk_topk", 0.0001, 1, "bf16", False),         # one entry a row, trimmed to 7: no census
+    (1000, 1024, 256, "chunk_topk", 0.005, 100, "bf16", True),       # chunks of 100 rows, 4-row workgroups
+    (2048, 1024, 512, "global_topk", 0.005, 512, "f16", False),      # fp16 keeps the stored residual
+])
+def test_entry_census_matches_count_and_gives_the_same_weight_gradient(dev, rows, d_in, d_out, mode, budget, chunk,
+                                                                       dtype, expect):
+    """stacr_save_census: the per-feature entry counts (8 copies summed) and every 512-row block's
+    first entry equal a count of the saved indices; stacr_weight_grad_census gives the same dW bit
+    for bit as stacr_weight_grad; saves that cannot write a census say so."""
+    from stacr_amd import kernels
+
+    announce("entry census", rows, d_in, d_out, mode, budget, chunk, dtype)
+    x = make_activation(rows, d_in, lognormal=True).to(dev, DT[dtype])
+    q = make_basis(d_in, 8).to(dev, DT[dtype])
+    g = make_grad(rows, d_out).to(dev, DT[dtype])
+    coeff, idx, data, scale, census = kernels.save_with_census(x, q, mode=mode, budget=budget, chunk_rows=chunk,
+                                                               bits=8)
+    c2, i2, d2, s2 = kernels.save(x, q, mode=mode, budget=budget, chunk_rows=chunk, bits=8)
+    torch.cuda.synchronize()
+    assert torch.equal(idx, i2) and torch.equal(data, d2) and torch.equal(scale, s2) and torch.equal(coeff, c2)
+    assert (census is not None) == expect
+    if census is None:
+        return
+    flat = idx.cpu().numpy().astype(np.int64)
+    cen = census.cpu().numpy().view(np.uint32).astype(np.int64)
+    counts = cen[:8 * d_in].reshape(8, d_in).sum(axis=0)
+    assert np.array_equal(counts, np.bincount(flat % d_in, minlength=d_in))
+    nb = -(-rows // 512)
+    bstart = cen[8 * d_in:8 * d_in + nb + 1]
+    assert np.array_equal(bstart, np.searchsorted(flat // d_in, np.arange(nb + 1) * 512))
+    res = (idx, data, scale)
+    dw1, _ = kernels.weight_grad(g, coeff, q, res, 8, True, DT[dtype])
+    dw2, _ = kernels.weight_grad(g, coeff, q, res, 8, True, DT[dtype], census=census)
+    torch.cuda.synchronize()
+    assert torch.equal(dw1, dw2)
