@@ -1882,10 +1882,13 @@ __global__ __launch_bounds__(kBlock) void k_refine_cand(SaveGeom g, FastGeom fg,
 #pragma unroll
     for (int h = 0; h < HC; ++h) cv[h] = coarse[(chunk * HC + h) * kCoarse + (threadIdx.x & 63)];
     const CandMeta mine = meta[has_rows ? blockIdx.x : 0];
-    // the candidate values go out before the selection's histogram words
+    // the candidate values go out before the selection's histogram words (only the list's used
+    // part: the threads past it read nothing)
     CandVals vals;
     {
-        const uint4 v = *reinterpret_cast<const uint4 *>(cand_val + (int64_t)blockIdx.x * kCandCap + kCandPer * threadIdx.x);
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if ((uint32_t)(kCandPer * threadIdx.x) < min(mine.count, (uint32_t)kCandCap))
+            v = *reinterpret_cast<const uint4 *>(cand_val + (int64_t)blockIdx.x * kCandCap + kCandPer * threadIdx.x);
         vals.w[0] = v.x; vals.w[1] = v.y; vals.w[2] = v.z; vals.w[3] = v.w;
     }
     for (int b = threadIdx.x; b < kBins; b += kBlock) s_hist[b] = 0u;
@@ -2043,14 +2046,19 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
         for (int c = 0; c < HC; ++c) hw[c] = h1[c * kBins];
     }
     const CandMeta mine = meta[has_rows ? blockIdx.x : 0];
-    // the candidates go out before the selection's and the offsets' words
+    // the candidates go out before the selection's and the offsets' words (only the list's used
+    // part)
     CandVals vals;
     uint32_t flat[kCandPer];
     {
         const int64_t base = (int64_t)blockIdx.x * kCandCap + kCandPer * threadIdx.x;
-        const uint4 v = *reinterpret_cast<const uint4 *>(cand_val + base);
-        const uint4 f0 = *reinterpret_cast<const uint4 *>(cand_idx + base);
-        const uint4 f1 = *reinterpret_cast<const uint4 *>(cand_idx + base + 4);
+        const uint32_t n_list = min(mine.count, (uint32_t)kCandCap), t0 = kCandPer * threadIdx.x;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u), f0 = v, f1 = v;
+        if (t0 < n_list) {
+            v = *reinterpret_cast<const uint4 *>(cand_val + base);
+            f0 = *reinterpret_cast<const uint4 *>(cand_idx + base);
+        }
+        if (t0 + 4 < n_list) f1 = *reinterpret_cast<const uint4 *>(cand_idx + base + 4);
         vals.w[0] = v.x; vals.w[1] = v.y; vals.w[2] = v.z; vals.w[3] = v.w;
         flat[0] = f0.x; flat[1] = f0.y; flat[2] = f0.z; flat[3] = f0.w;
         flat[4] = f1.x; flat[5] = f1.y; flat[6] = f1.z; flat[7] = f1.w;
@@ -2070,8 +2078,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
     const float scale = o.bits ? quant_scale(mk, o.bits, amax) : 1.f;
     if (!to_list && blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
     if (!has_rows) return;  // uniform: a trailing workgroup with no rows writes nothing
+    const uint32_t dmask = (g.d & (g.d - 1)) == 0 ? (uint32_t)g.d - 1u : 0u;  // power-of-two widths: a mask
     if (census)  // (cleared before the offset sums' barriers)
-        for (int f = threadIdx.x; f < kBins; f += kBlock) s_feat[f] = 0u;
+        for (int f = threadIdx.x; f < g.d; f += kBlock) s_feat[f] = 0u;
     // the workgroup's output offset and tie budget (the earlier workgroups' records)
     WgOffset wo;
     {
@@ -2096,7 +2105,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
         } else {
             write_entry<DT>(o, pos, fl, rv, scale);
         }
-        if (census) atomicAdd(&s_feat[fl % (uint32_t)g.d], 1u);
+        if (census) atomicAdd(&s_feat[dmask ? fl & dmask : fl % (uint32_t)g.d], 1u);
     };
     const bool valid = mine.count <= (uint32_t)kCandCap && mine.cut <= (T >> kDigitShift[0]);  // uniform
     if (valid) {
