@@ -138,6 +138,21 @@ __device__ __forceinline__ float wave_reduce_scatter64(float (&a)[64])
     return a[0];
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave in data-parallel moves (no LDS round trips):
+// within each row of 16 lanes, adds of the value 1, 2, 4 and 8 lanes down (row_shr; a lane with no
+// such lane in its row adds 0), then lane 15's total into rows 1 and 3 and lane 31's into rows 2
+// and 3 (row_bcast:15 / row_bcast:31, the rows chosen by the row mask; the other rows add 0).
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t x)
+{
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false);  // row_shr:1
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false);  // row_shr:2
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false);  // row_shr:4
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false);  // row_shr:8
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return x;
+}
+
 // ------------------------------------------------------------------ block primitives
 // Exclusive prefix sum over the NT threads of a workgroup (NT a multiple of 64); *total receives
 // the sum.  s_tot needs NT / 64 entries.  Every thread must call it (it contains __syncthreads).

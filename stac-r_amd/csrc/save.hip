@@ -24,6 +24,14 @@ constexpr int kHistCopies = 8;     // histogram / max-key copies of a chunk with
 constexpr int kMaxKeyStride = 32;  // max-key copies 128 bytes apart
 constexpr int kCoarse = 64;        // level-0 coarse bins (32 histogram bins each)
 constexpr int kEmitStage = 1024;   // survivors a batched emission workgroup stages in LDS
+constexpr int kCandCap = 2048;               // candidates a workgroup keeps
+constexpr int kCandPer = kCandCap / kBlock;  // candidates a thread reads (consecutive)
+static_assert(kCandPer == 8, "one 16-byte vector of bf16 candidate values per thread");
+
+struct CandMeta {
+    uint32_t cut;    // level-0 bin of the workgroup's cut
+    uint32_t count;  // candidates (more than kCandCap: the list overflowed and is not used)
+};
 
 __device__ __forceinline__ void wg_rows(const SaveGeom &g, int64_t wg, int64_t &chunk, int64_t &row0,
                                         int64_t &row_end)
@@ -1181,7 +1189,9 @@ __device__ __forceinline__ SelState prev_state(int lvl, const SelState *__restri
 }
 
 // Passes 2 and 3 (batched): histogram of digit `lvl` among keys matching the prefix so far.
-template <int DT, int R, int V, int HC, bool RIN, int LVL>
+// CAND (bf16, stored residual, level 1): the pass also writes the workgroup's elements in bin B0
+// and above, in ascending flat order, as its candidate list for k_emit_cand (cut = B0).
+template <int DT, int R, int V, int HC, bool RIN, int LVL, bool CAND = false>
 __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom fg,
                                                           const typename Act<DT>::T *__restrict__ x,
                                                           const float *__restrict__ qp,
@@ -1189,8 +1199,12 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
                                                           uint32_t *__restrict__ hist, SelState *__restrict__ state,
                                                           uint32_t k_full, uint32_t k_last, uint32_t *__restrict__ maxkey,
                                                           uint32_t *__restrict__ fold, int64_t fold_stride,
-                                                          const uint32_t *__restrict__ coarse)
+                                                          const uint32_t *__restrict__ coarse,
+                                                          uint32_t *__restrict__ cand_idx = nullptr,
+                                                          uint16_t *__restrict__ cand_val = nullptr,
+                                                          CandMeta *__restrict__ meta = nullptr)
 {
+    static_assert(!CAND || (DT == STACR_DTYPE_BF16 && RIN && LVL == 1), "lists from the stored bf16 residual");
     constexpr int NB = Batch<R>::NB;
     constexpr bool kFold = DT == STACR_DTYPE_BF16;  // per-workgroup records for the emission pass
     constexpr int lvl = LVL;                         // the key digit histogrammed here (1 or 2)
@@ -1244,9 +1258,11 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
     const uint32_t dmask = (uint32_t)kDigitBins[lvl] - 1u;
     if constexpr (!RIN) basis_mask<R, V>(col_ok, q);
     uint32_t above = 0u;
+    uint32_t cmsk[CAND ? NB : 1];  // CAND: elements of vector i in bin B0 and above
     {   // the workgroup's rows are one batch
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
+            if constexpr (CAND) cmsk[i] = 0u;
             if (!(col_ok && ld.rows[i] < row_end)) continue;
             float r[V];
             if constexpr (RIN) {
@@ -1262,8 +1278,51 @@ __global__ __launch_bounds__(kBlock) void k_refine_hist_b(SaveGeom g, FastGeom f
                 const uint32_t key = __float_as_uint(r[e]) & 0x7fffffffu;
                 if ((key >> match_shift) == prefix) atomicAdd(&s_hist[(key >> dshift) & dmask], 1u);
                 if (kFold) above += (key >> match_shift) > prefix;
+                if constexpr (CAND) cmsk[i] |= (key >> match_shift) >= prefix ? 1u << e : 0u;
             }
         }
+    }
+    if constexpr (CAND) {
+        // the list: (iteration, wave, lane, element) order is ascending flat order
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        uint32_t incl[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) incl[i] = wave_inclusive_scan((uint32_t)__popc(cmsk[i]));
+        __shared__ uint32_t s_cwt[kWaves * NB];
+        if (lane == 63)
+#pragma unroll
+            for (int i = 0; i < NB; ++i) s_cwt[wave * NB + i] = incl[i];
+        __syncthreads();
+        uint32_t before_iter = 0u;
+        uint32_t *ci = cand_idx + (int64_t)blockIdx.x * kCandCap;
+        uint16_t *cv = cand_val + (int64_t)blockIdx.x * kCandCap;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            uint32_t waves_before = 0u, iter_total = 0u;
+#pragma unroll
+            for (int wv = 0; wv < kWaves; ++wv) {
+                const uint32_t t = s_cwt[wv * NB + i];
+                waves_before += wv < wave ? t : 0u;
+                iter_total += t;
+            }
+            uint32_t pos = before_iter + waves_before + incl[i] - (uint32_t)__popc(cmsk[i]);
+            if (cmsk[i]) {
+                const uint4 raw = ld.raw[i];
+                const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
+                for (uint32_t m = cmsk[i]; m != 0u; m &= m - 1u, ++pos) {
+                    const int e = __builtin_ctz(m);
+                    uint32_t word = wd[0];
+#pragma unroll
+                    for (int k = 1; k < 4; ++k) word = (e >> 1) == k ? wd[k] : word;
+                    if (pos < (uint32_t)kCandCap) {
+                        ci[pos] = (uint32_t)(ld.rows[i] * g.d + col + e);
+                        cv[pos] = (uint16_t)((word >> (16 * (e & 1))) & 0xffffu);
+                    }
+                }
+            }
+            before_iter += iter_total;
+        }
+        if (threadIdx.x == 0) meta[blockIdx.x] = CandMeta{prefix, before_iter};
     }
     if (kFold) {
 #pragma unroll
@@ -1594,14 +1653,6 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
 // candidates, so the level-1 pass and the emission work on those lists; any other workgroup
 // recomputes its residuals from X, C and the basis there (the same values, rarely needed).  The
 // selection is the same as the full passes'.
-constexpr int kCandCap = 2048;               // candidates a workgroup keeps
-constexpr int kCandPer = kCandCap / kBlock;  // candidates a thread reads (consecutive)
-static_assert(kCandPer == 8, "one 16-byte vector of bf16 candidate values per thread");
-
-struct CandMeta {
-    uint32_t cut;    // level-0 bin of the workgroup's cut
-    uint32_t count;  // candidates (more than kCandCap: the list overflowed and is not used)
-};
 
 __device__ __forceinline__ uint32_t bf16_key(uint32_t bits16)
 {
@@ -1772,15 +1823,8 @@ __global__ __launch_bounds__(kBlock) void k_proj_cand(SaveGeom g, FastGeom fg, c
             }
         }
         msk[i] = m;
-        cnt[i] = incl[i] = (uint32_t)__popc(m);
-    }
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-#pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            const uint32_t y = __shfl_up(incl[i], off, 64);
-            if (lane >= off) incl[i] += y;
-        }
+        cnt[i] = (uint32_t)__popc(m);
+        incl[i] = wave_inclusive_scan(cnt[i]);
     }
     if (lane == 63)
 #pragma unroll
@@ -1952,9 +1996,9 @@ __global__ __launch_bounds__(kBlock) void k_refine_cand(SaveGeom g, FastGeom fg,
 }
 
 // The emission's fallback for a workgroup without a usable candidate list: its residuals
-// recomputed one iteration at a time, survivors compacted in the order of k_emit_b and handed to
-// `put` (position, flat index, value).
-template <int R, typename Put>
+// recomputed (RIN: read from the stored residual) one iteration at a time, survivors compacted in
+// the order of k_emit_b and handed to `put` (position, flat index, value).
+template <int R, bool RIN, typename Put>
 __device__ __forceinline__ void emit_cand_fallback(const SaveGeom &g, const FastGeom &fg, const uint16_t *__restrict__ x,
                                                    const float *__restrict__ qp, const uint16_t *__restrict__ coeff,
                                                    int64_t row0, int64_t row_end, uint32_t T, const WgOffset &wo,
@@ -1965,15 +2009,23 @@ __device__ __forceinline__ void emit_cand_fallback(const SaveGeom &g, const Fast
     const int slot = threadIdx.x >> g.log2L, u = threadIdx.x & (g.L - 1);
     const int64_t col = (int64_t)u * 8, colc = min(col, g.d - 8);
     const bool col_ok = col < g.d;
-    float q[8][R];
-    basis_issue<R, 8>(qp + g.d * R, g.d, colc, q);
-    basis_mask<R, 8>(col_ok, q);
+    float q[8][RIN ? 1 : R];
+    if constexpr (!RIN) {
+        basis_issue<R, 8>(qp + g.d * R, g.d, colc, q);
+        basis_mask<R, 8>(col_ok, q);
+    }
     uint32_t before_iter = 0u;  // survivors of the earlier iterations (all waves)
 #pragma unroll 1
     for (int i = 0; i < NB; ++i) {
         const int64_t row = row0 + (int64_t)i * g.rpi + slot;
         float r[8];
-        const bool live = cand_residual<R>(g, x, coeff, q, row, row_end, col, col_ok, r);
+        bool live;
+        if constexpr (RIN) {
+            live = col_ok && row < row_end;
+            unpack_raw<STACR_DTYPE_BF16, 8>(load_raw<STACR_DTYPE_BF16, 8>(x + row * g.d + col, live), r);
+        } else {
+            live = cand_residual<R>(g, x, coeff, q, row, row_end, col, col_ok, r);
+        }
         uint32_t m = 0u;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -2020,7 +2072,7 @@ __device__ __forceinline__ void emit_cand_fallback(const SaveGeom &g, const Fast
 // Emission (bf16, batched, candidates): the final selection and the workgroup's offset and tie
 // budget as in k_emit_b, then its survivors from the candidate list (or, for a workgroup without a
 // usable list, from recomputed residuals) quantized and written in ascending flat order.
-template <int R, int HC>
+template <int R, int HC, bool RIN = false>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) void k_emit_cand(
     SaveGeom g, FastGeom fg, const uint16_t *__restrict__ x, const float *__restrict__ qp,
     const uint16_t *__restrict__ coeff, SelState *__restrict__ state, uint32_t chunk_k,
@@ -2037,7 +2089,6 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
     const int64_t w = blockIdx.x - chunk * g.wgs_per_chunk;
     const int64_t wg0 = chunk * g.wgs_per_chunk;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const bool has_rows = row0 < row_end;
     uint32_t hw[HC];
     {
@@ -2129,7 +2180,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
             eb += is_eq;
         }
     } else {
-        emit_cand_fallback<R>(g, fg, x, qp, coeff, row0, row_end, T, wo, s_wt, put);
+        emit_cand_fallback<R, RIN>(g, fg, x, qp, coeff, row0, row_end, T, wo, s_wt, put);
     }
     if (census) {  // the entries per feature (copy w % 8) and, at a block's first row, its first entry
         __syncthreads();
@@ -2307,6 +2358,9 @@ struct Plan {
     // k_refine_cand, k_emit_cand) with the workgroups' quota
     bool cand;
     uint32_t quota;
+    // bf16 on the batched passes over a stored residual (wide rows, or a quota past the list): the
+    // level-1 pass writes the candidate lists (bin B0 and above) and k_emit_cand reads them
+    bool cand_rin;
     bool trim;
     int64_t n_list_blocks;
 };
@@ -2416,7 +2470,9 @@ Plan make_plan_wide(const StacrSaveArgs &a)
 Plan make_plan(const StacrSaveArgs &a)
 {
     Plan p = make_plan_wide(a);
-    if (!p.fold || p.wide || a.k_total <= 0) return p;
+    if (!p.fold || a.k_total <= 0) return p;
+    p.cand_rin = true;  // (unless the projection pass keeps lists itself, below)
+    if (p.wide) return p;
     const SaveGeom &g = p.g;
     const double wg_elems = (double)g.rows_per_wg * (double)g.d;
     const int64_t last_rows = g.rows - (g.n_chunks - 1) * g.chunk_rows;
@@ -2425,6 +2481,7 @@ Plan make_plan(const StacrSaveArgs &a)
     const double quota = 4.0 * dens * wg_elems + 64.0;
     if (quota > kCandCap / 2) return p;
     p.cand = true;
+    p.cand_rin = false;
     p.quota = (uint32_t)quota;
     return p;
 }
@@ -2457,10 +2514,11 @@ size_t layout(const StacrSaveArgs &a, const Plan &p, size_t *off)
     take(WS_FOLD, p.fold ? (size_t)17 * p.n_wgs * sizeof(uint32_t) : 0);  // cum[0..16][workgroup]
     const bool rstore = p.fast && a.dtype != STACR_DTYPE_F32 && a.k_total > 0 && !p.cand;  // (wide rows: p.fast)
     take(WS_R, rstore ? (size_t)a.rows * a.feats * 2 : 0);  // the stored residual (16-bit types)
-    const size_t nc = p.cand ? (size_t)p.n_wgs * kCandCap : 0;  // the candidate lists
+    const bool lists = p.cand || p.cand_rin;
+    const size_t nc = lists ? (size_t)p.n_wgs * kCandCap : 0;  // the candidate lists
     take(WS_CIDX, nc * sizeof(uint32_t));
     take(WS_CVAL, nc * sizeof(uint16_t));
-    take(WS_CMETA, p.cand ? (size_t)p.n_wgs * sizeof(CandMeta) : 0);
+    take(WS_CMETA, lists ? (size_t)p.n_wgs * sizeof(CandMeta) : 0);
     return cur;
 }
 
@@ -2543,7 +2601,9 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     // always runs them)
     constexpr bool kCandOk = kFastOk && DT == STACR_DTYPE_BF16;
     const bool cand = kCandOk && fast && p.cand && resid;
-    if (p.cand && !cand) return stacr_fail(STACR_ERR_INVALID, "stacr_save: candidate passes outside the bf16 batched path");
+    const bool cand_rin = kCandOk && fast && p.cand_rin && resid;
+    if ((p.cand && !cand) || (p.cand_rin && !cand_rin))
+        return stacr_fail(STACR_ERR_INVALID, "stacr_save: candidate passes outside the bf16 batched path");
     uint32_t *cidx = carve<uint32_t>(ws, off[WS_CIDX]);
     uint16_t *cval = carve<uint16_t>(ws, off[WS_CVAL]);
     CandMeta *cmeta = carve<CandMeta>(ws, off[WS_CMETA]);
@@ -2593,9 +2653,20 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
                                 p.g, fg, x, qp, coeff, hist, state, kf, kl, maxkey, fold, p.n_wgs, coarse, cval, cmeta);
                         });
                 };
+                auto refine_lists = [&](auto hc) {
+                    if constexpr (kCandOk && kRin)
+                        stacr_launch("k_refine_hist", s, [&] {
+                            k_refine_hist_b<DT, R, V, decltype(hc)::value, true, 1, true><<<nwg, kBlock, 0, s>>>(
+                                p.g, fg, xin, qp, coeff, hist, state, kf, kl, maxkey, fold, p.n_wgs, coarse, cidx, cval,
+                                cmeta);
+                        });
+                };
                 if (lvl == 1 && cand) {
                     if (hc8) refine_cand(H8{});
                     else refine_cand(H1{});
+                } else if (lvl == 1 && cand_rin) {
+                    if (hc8) refine_lists(H8{});
+                    else refine_lists(H1{});
                 } else if (lvl == 1) {
                     if (hc8) refine(H8{}, L1{});
                     else refine(H1{}, L1{});
@@ -2634,11 +2705,17 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
                 stacr_launch("k_emit", s, [&] { k_emit_cand<R, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt); });
             else if (cand)
                 stacr_launch("k_emit", s, [&] { k_emit_cand<R, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt); });
+            if constexpr (kRin) {  // the lists of the level-1 pass; the fallback reads the stored residual
+                if (cand_rin && hc8)
+                    stacr_launch("k_emit", s, [&] { k_emit_cand<R, kHistCopies, true><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, nullptr, kt); });
+                else if (cand_rin)
+                    stacr_launch("k_emit", s, [&] { k_emit_cand<R, 1, true><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, nullptr, kt); });
+            }
             if (census && a.census_written) *a.census_written = 1;
         }
-        if (!cand && fast && hc8 && DT == STACR_DTYPE_BF16)
+        if (!cand && !cand_rin && fast && hc8 && DT == STACR_DTYPE_BF16)
             stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V, kHistCopies, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs); });
-        else if (!cand && fast)
+        else if (!cand && !cand_rin && fast)
             stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V, 1, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs); });
     }
     if (!fast) stacr_launch("k_emit", s, [&] { k_emit<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0); });

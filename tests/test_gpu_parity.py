@@ -182,21 +182,27 @@ def _crafted_activation(kind, rows, d):
     return x
 
 
-@pytest.mark.parametrize("kind,rows,mode,budget,chunk,bits", [
-    ("outlier_rows", 2048, "global_topk", 0.005, 512, 8),
-    ("outlier_rows", 2048, "chunk_topk", 0.005, 256, 8),
-    ("tie_block", 512, "global_topk", 0.005, 512, 0),
-    ("tie_block", 1024, "chunk_topk", 0.01, 128, 8),
-    ("outlier_scattered", 4096, "global_topk", 0.005, 512, 8),
+@pytest.mark.parametrize("kind,rows,d,mode,budget,chunk,bits", [
+    ("outlier_rows", 2048, 1024, "global_topk", 0.005, 512, 8),
+    ("outlier_rows", 2048, 1024, "chunk_topk", 0.005, 256, 8),
+    ("tie_block", 512, 1024, "global_topk", 0.005, 512, 0),
+    ("tie_block", 1024, 1024, "chunk_topk", 0.01, 128, 8),
+    ("outlier_scattered", 4096, 1024, "global_topk", 0.005, 512, 8),
+    # wide rows (the level-1 pass writes the lists from the stored residual; overflowing lists
+    # fall back to the stored residual)
+    ("tie_block", 512, 4096, "global_topk", 0.005, 512, 0),
+    ("outlier_rows", 1024, 4096, "chunk_topk", 0.005, 256, 8),
+    ("outlier_scattered", 2048, 4096, "global_topk", 0.005, 512, 8),
 ])
-def test_save_candidate_fallback_matches_oracle(dev, kind, rows, mode, budget, chunk, bits):
-    """bf16 saves on the batched path keep per-workgroup candidate lists; a workgroup whose list
-    cannot hold every element at or above its chunk's level-0 bin recomputes its residuals from X.
+def test_save_candidate_fallback_matches_oracle(dev, kind, rows, d, mode, budget, chunk, bits):
+    """bf16 saves keep per-workgroup candidate lists (kept by the projection pass, or by the level-1
+    pass from a stored residual); a workgroup whose list cannot hold every element at or above its
+    chunk's level-0 bin recomputes its residuals from X (reads them from the stored residual).
     Selection and quantization stay bit-exact against the oracle either way."""
     from stacr_amd import kernels
 
-    d, rank = 1024, 8
-    announce("save candidate fallback", kind, rows, mode, budget, chunk, bits)
+    rank = 8
+    announce("save candidate fallback", kind, rows, d, mode, budget, chunk, bits)
     x = _crafted_activation(kind, rows, d)
     q = torch.zeros(d, rank) if kind == "tie_block" else make_basis(d, rank)
     xd, qd = x.to(dev, torch.bfloat16), q.to(dev, torch.bfloat16)
