@@ -1570,16 +1570,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         cnt[i] = (uint32_t)__popc(msk[i] & 0xffu) | ((uint32_t)__popc(msk[i] >> 8) << 16);
-        incl[i] = cnt[i];
-    }
-    // inclusive scans over the wave's lanes, one per iteration
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-#pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            const uint32_t y = __shfl_up(incl[i], off, 64);
-            if (lane >= off) incl[i] += y;
-        }
+        incl[i] = wave_inclusive_scan(cnt[i]);  // over the wave's lanes, one per iteration
     }
     if (lane == 63)
 #pragma unroll
@@ -2034,12 +2025,7 @@ __device__ __forceinline__ void emit_cand_fallback(const SaveGeom &g, const Fast
             m |= (live && k == T) ? 0x100u << e : 0u;
         }
         const uint32_t cnt = (uint32_t)__popc(m & 0xffu) | ((uint32_t)__popc(m >> 8) << 16);
-        uint32_t incl = cnt;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const uint32_t y = __shfl_up(incl, off, 64);
-            if (lane >= off) incl += y;
-        }
+        const uint32_t incl = wave_inclusive_scan(cnt);
         if (lane == 63) s_wt[wave] = incl;
         __syncthreads();
         uint32_t waves_before = 0u, iter_total = 0u;
