@@ -187,12 +187,19 @@ __global__ void k_prep(const typename Act<DT>::T *__restrict__ q, int64_t d, int
     // 16-bit types: also the transposed copy in the activation dtype (the projection's dot products)
     typename Act<DT>::T *qph = reinterpret_cast<typename Act<DT>::T *>(qpt + n);
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
-        const int64_t row = i / R;
-        const int j = (int)(i - row * R);
-        const float v = j < rank ? Act<DT>::ld(q[row * rank + j]) : 0.f;
-        qp[i] = v;
-        qpt[j * d + row] = v;
-        if constexpr (sizeof(typename Act<DT>::T) == 2) qph[j * d + row] = j < rank ? q[row * rank + j] : (typename Act<DT>::T)0;
+        {   // padded copy: element i is (row i / R, column i % R)
+            const int64_t row = i / R;
+            const int j = (int)(i - row * R);
+            qp[i] = j < rank ? Act<DT>::ld(q[row * rank + j]) : 0.f;
+        }
+        {   // transposed copies: element i is (column i / d, row i % d), so consecutive threads write
+            // consecutive addresses
+            const int j = (int)(i / d);
+            const int64_t row = i - (int64_t)j * d;
+            const typename Act<DT>::T raw = j < rank ? q[row * rank + j] : (typename Act<DT>::T)0;
+            qpt[i] = j < rank ? Act<DT>::ld(raw) : 0.f;
+            if constexpr (sizeof(typename Act<DT>::T) == 2) qph[i] = raw;
+        }
     }
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_zero; i += step) zero[i] = 0u;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_zero2; i += step) zero2[i] = 0u;
