@@ -20,6 +20,10 @@ and the basis refresh's Oja step are timed the same way and reported under "othe
 Prints one JSON line.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20]
+    python bench.py --workload {c_proj,turbo,cfg1,cfg4_up,cfg4_down,oja} [--steps K] [--warmup W]
+
+The second form times one other configured shape alone (cfg1's fp32 nn.Linear, cfg4's 2048 <-> 8192
+layers at rank 16 through the projection engine, ...) and prints its own line, for profiling.
 """
 from __future__ import annotations
 
@@ -190,30 +194,34 @@ def kernel_breakdown(step, reps: int = 10) -> dict:
     return {name: round(tot / reps * 1e3, 3) for name, (tot, _cnt) in timer.results.items()}
 
 
-def layer_workload(name, n, d_in, d_out, rank, budget, mode, steps, warmup, lognormal=True):
-    """Timing of one configured layer's save + dW (Conv1D layout, bf16)."""
+def layer_workload(name, n, d_in, d_out, rank, budget, mode, steps, warmup, lognormal=True, dtype="bf16",
+                   conv1d=True):
+    """Timing of one configured layer's save + dW (Conv1D layout unless `conv1d` is False, when dW
+    is the nn.Linear d_out x d_in; activations, basis and G in `dtype`, dW in it too)."""
     import torch
 
     from gpu_cases import make_activation, make_basis, make_grad
     from stacr_amd import kernels
 
     dev = torch.device("cuda:0")
-    x = make_activation(n, d_in, lognormal=lognormal).to(dev, torch.bfloat16)
-    q = make_basis(d_in, rank).to(dev, torch.bfloat16)
-    g = make_grad(n, d_out).to(dev, torch.bfloat16)
+    tdt = {"bf16": torch.bfloat16, "fp32": torch.float32}[dtype]
+    x = make_activation(n, d_in, lognormal=lognormal).to(dev, tdt)
+    q = make_basis(d_in, rank).to(dev, tdt)
+    g = make_grad(n, d_out).to(dev, tdt)
     k = kernels.residual_plan(n, d_in, mode, budget, CHUNK)[1] if budget > 0 else 0
 
     def step():
         coeff, idx, data, scale, census = kernels.save_with_census(x, q, mode=mode, budget=budget, chunk_rows=CHUNK,
                                                                    bits=BITS)
         res = (idx, data, scale) if idx is not None else None
-        dw, _ = kernels.weight_grad(g, coeff, q, res, BITS, True, torch.bfloat16, census=census)
+        dw, _ = kernels.weight_grad(g, coeff, q, res, BITS, conv1d, tdt, census=census)
         return coeff, idx, data, scale, dw
 
     eager, graph, note = time_steps(step, steps, warmup, check_layer)
     ms = min(eager, graph) if graph is not None else eager
-    ab = algorithmic_bytes(n, d_in, d_out, rank, k)
-    out = {"config": name, "tokens": n, "d_in": d_in, "d_out": d_out, "rank": rank, "k": k,
+    s = x.element_size()
+    ab = algorithmic_bytes(n, d_in, d_out, rank, k, s_act=s, s_w=s)
+    out = {"config": name, "tokens": n, "d_in": d_in, "d_out": d_out, "rank": rank, "k": k, "dtype": dtype,
            "ms_per_step": ms, "tokens_per_s": n / (ms * 1e-3), "eager_ms": eager, "graph_ms": graph,
            "algorithmic_bytes": ab["total"],
            "pct_hbm_roofline": 100.0 * ab["total"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
@@ -252,6 +260,28 @@ def oja_workload(x, q, steps, warmup):
     return out
 
 
+# The configured layers besides the headline, by name: (description, N, d_in, d_out, rank, budget,
+# mode, options).  Each runs through the same save + dW calls; `--workload NAME` times and prints
+# one of them alone (a line for profiling, not the contract line).
+WORKLOADS = {
+    "c_proj": ("cfg3 c_proj: Conv1D 4096->1024, N=8192, bf16, r=8, global_topk 0.005, int8",
+               N, 4096, 1024, 8, BUDGET, MODE, {}),
+    "turbo": ("cfg2 Turbo: 1280->5120, N=8192, bf16, r=8, no residual",
+              N, 1280, 5120, 8, 0.0, "chunk_topk", {"lognormal": False}),
+    "cfg1": ("cfg1: nn.Linear 768->3072, N=4096, fp32, r=8, chunk_topk 0.005 (512-row chunks), int8",
+             4096, 768, 3072, 8, BUDGET, "chunk_topk", {"lognormal": False, "dtype": "fp32", "conv1d": False}),
+    "cfg4_up": ("cfg4 shape: 2048->8192, N=32768, bf16, r=16, chunk_topk 0.005, int8 (projection engine)",
+                32768, 2048, 8192, 16, BUDGET, "chunk_topk", {"lognormal": False, "conv1d": False}),
+    "cfg4_down": ("cfg4 shape: 8192->2048, N=32768, bf16, r=16, chunk_topk 0.005, int8 (projection engine)",
+                  32768, 8192, 2048, 16, BUDGET, "chunk_topk", {"lognormal": False, "conv1d": False}),
+}
+
+
+def run_workload(key, steps, warmup) -> dict:
+    name, n, d_in, d_out, rank, budget, mode, opts = WORKLOADS[key]
+    return layer_workload(name, n, d_in, d_out, rank, budget, mode, steps, warmup, **opts)
+
+
 def copy_peak_gbs() -> float:
     """Read + write GB/s of a 1 GiB device-to-device copy on this GPU (a measured stream peak)."""
     import torch
@@ -279,11 +309,26 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the other configured workloads")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["oja"],
+                    help="time only this other configured workload and print its line (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
               file=sys.stderr)
         return 2
+    if args.workload:
+        import torch
+
+        from gpu_cases import make_activation, make_basis
+
+        torch.cuda.set_device(0)
+        if args.workload == "oja":
+            x = make_activation(N, D_IN, lognormal=True).to("cuda:0", torch.bfloat16)
+            w = oja_workload(x, make_basis(D_IN, RANK).to("cuda:0", torch.bfloat16), args.steps, args.warmup)
+        else:
+            w = run_workload(args.workload, args.steps, args.warmup)
+        print(json.dumps({"workload": args.workload, **w}), flush=True)
+        return 0
 
     import torch
 
@@ -381,13 +426,8 @@ def main() -> int:
         out["note"] = graph_note
     if not args.no_extra:
         extra_steps, extra_warm = max(10, args.steps // 4), max(3, args.warmup // 4)
-        out["other_workloads"] = [
-            layer_workload("cfg3 c_proj: Conv1D 4096->1024, N=8192, bf16, r=8, global_topk 0.005, int8",
-                           N, 4096, 1024, 8, BUDGET, MODE, extra_steps, extra_warm),
-            layer_workload("cfg2 Turbo: 1280->5120, N=8192, bf16, r=8, no residual",
-                           N, 1280, 5120, 8, 0.0, "chunk_topk", extra_steps, extra_warm, lognormal=False),
-            oja_workload(x, q, extra_steps, extra_warm),
-        ]
+        out["other_workloads"] = [run_workload(key, extra_steps, extra_warm) for key in ("c_proj", "turbo")]
+        out["other_workloads"].append(oja_workload(x, q, extra_steps, extra_warm))
         for w in out["other_workloads"]:
             print(f"[bench] {w['config']}: {w['ms_per_step'] * 1e3:.1f} us {w['kernels_us_per_step']}",
                   file=sys.stderr, flush=True)

@@ -516,6 +516,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
     __shared__ __attribute__((aligned(1024))) unsigned char lds1[L::size];
     __shared__ __attribute__((aligned(1024))) unsigned char lds2[L::size];
     __shared__ TileHdr s_hdr[SP ? kMaxBlocks : 1];
+    // with entries, the part's Q rows (<= 1024 features x <= 16 values), loaded while the first two
+    // blocks are copied and read by the epilogue
+    __shared__ uint16_t s_q[SP ? kPartMax * 16 : 1];
+    static_assert(!SP || 3 * L::size + kMaxBlocks * sizeof(TileHdr) + kPartMax * 16 * 2 <= 160 * 1024,
+                  "the stream buffers, headers and Q rows fit the CU's LDS");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
     // workgroup -> (o-slab, part): consecutive logical ids share an XCD (ids are dealt to the 8 XCDs
@@ -679,6 +684,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
         issue_records(1, lds1);
         issue_g(1, lds1);
     }
+    const uint16_t *q = static_cast<const uint16_t *>(a.q);
+    if constexpr (SP) {
+        // the part's Q rows (pw * rank <= 16384 values, contiguous): all loads issued, then stored
+        const int n_q = pw * a.rank;
+        const uint16_t *qs = q + plo * a.rank;
+        uint32_t qv[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) qv[k] = tid + k * kThreads < n_q ? qs[tid + k * kThreads] : 0u;
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            if (tid + k * kThreads < n_q) s_q[tid + k * kThreads] = (uint16_t)qv[k];
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     auto step = [&](int blk, const unsigned char *__restrict__ B, unsigned char *__restrict__ B2) {
@@ -712,51 +729,63 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
     // ---- what the epilogue reads from memory, loaded before the reduction hides the latency: the
     // scale (it exists only with residual entries; without them the sparse sums are zero) and the
     // part's column map
-    const uint16_t *q = static_cast<const uint16_t *>(a.q);
     const float scale = SP && a.bits ? *a.scale : 1.f;
     const int colf = SP && tid < kNC ? a.colmap[part * kNC + tid] : -1;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
-    // ---- reduce the per-wave tiles over the waves, in wave order: staged tile by tile in lds0,
-    // the sums and the part's column slots in lds1
+    // ---- reduce the per-wave tiles over the waves, in wave order.  Every wave's tiles are staged
+    // at once (16 KiB a tile: tiles 0, 1 in lds0, 2, 3 in lds1, 4 in lds2); the sums and the part's
+    // column slots follow the last tile (in lds1 without entries, whose one tile is in lds0)
     constexpr int NTILE = 1 + NT;
-    static_assert(!SP || NTILE * 256 * 4 + kPartMax * 4 <= L::size, "sums and slots fit a buffer");
-    static_assert(!SP || (size_t)kPartMax * 15 * 2 <= L::size / 2 * 2, "a part's Q rows fit a buffer");
-    float *stage = reinterpret_cast<float *>(lds0);
-    float *fin = reinterpret_cast<float *>(lds1);                         // [NTILE][o][j]
-    int32_t *slots = reinterpret_cast<int32_t *>(lds1 + NTILE * 256 * 4);  // [pw]
+    constexpr size_t kTileBytes = (size_t)kWaves * 256 * 4;
+    static_assert(L::size >= (SP ? 2 : 1) * kTileBytes, "two tiles (one without entries) fit a buffer");
+    static_assert(!SP || NTILE == 5, "five tiles with entries");
+    static_assert(!SP || kTileBytes + NTILE * 256 * 4 + kPartMax * 4 <= L::size, "the last tile, sums and slots fit a buffer");
+    auto stage_of = [&](int tile) {
+        unsigned char *b = tile < 2 ? lds0 : tile < 4 ? lds1 : lds2;
+        return reinterpret_cast<float *>(b + (size_t)(tile & 1) * kTileBytes);
+    };
+    unsigned char *fin_base = SP ? lds2 + kTileBytes : lds1;
+    float *fin = reinterpret_cast<float *>(fin_base);                         // [NTILE][o][j]
+    int32_t *slots = reinterpret_cast<int32_t *>(fin_base + NTILE * 256 * 4);  // [pw]
 #pragma unroll
     for (int tile = 0; tile < NTILE; ++tile) {
         const f32x4 acc = tile == 0 ? acc_m : acc_t[tile > 0 ? tile - 1 : 0];
+        float *stage = stage_of(tile);
 #pragma unroll
         for (int r = 0; r < 4; ++r)  // D layout: rows 4 (lane / 16) .. + 3 of column lane % 16
             stage[wave * 256 + (4 * grp + r) * 16 + n] = acc[r];
-        __syncthreads();
-        if (tid < 256) {
-            float sum = 0.f;
-            for (int w = 0; w < kWaves; ++w) sum += stage[w * 256 + tid];
-            fin[tile * 256 + tid] = sum;
-        }
-        __syncthreads();
     }
     if constexpr (SP) {
         if (tid < pw) slots[tid] = -1;
-        __syncthreads();
-        if (colf >= 0 && colf < pw) slots[colf] = tid;
-        __syncthreads();
     }
+    __syncthreads();
+    for (int e = tid; e < NTILE * 256; e += kThreads) {
+        const float *stage = stage_of(e >> 8);
+        float sum = 0.f;
+        for (int w = 0; w < kWaves; ++w) sum += stage[w * 256 + (e & 255)];
+        fin[e] = sum;
+    }
+    if constexpr (SP) {
+        if (colf >= 0 && colf < pw) slots[colf] = tid;
+    }
+    __syncthreads();
 
     // ---- dW tile: M Q^T + scale (light + column sums), one rounding; dbias from M[:, bias_col].
-    // With entries a part has <= 1024 features, one per thread; without, the threads loop over the
-    // features.  The Q rows of a chunk of features are first copied to LDS (lds2, unused now).
-    const int qchunk = (int)((L::size / 2) / (size_t)a.rank) < kThreads ? (int)((L::size / 2) / (size_t)a.rank) : kThreads;
-    uint16_t *sq = reinterpret_cast<uint16_t *>(lds2);
+    // With entries a part has <= 1024 features, one per thread, and its Q rows are in s_q already;
+    // without, the threads loop over the features, and the Q rows of a chunk of features are first
+    // copied to LDS (lds2, unused now).
+    const int qchunk = SP ? kThreads
+                          : ((int)((L::size / 2) / (size_t)a.rank) < kThreads ? (int)((L::size / 2) / (size_t)a.rank) : kThreads);
+    uint16_t *sq = SP ? s_q : reinterpret_cast<uint16_t *>(lds2);
     for (int c0 = 0; c0 < pw; c0 += qchunk) {
         const int nf = pw - c0 < qchunk ? pw - c0 : qchunk;
-        __syncthreads();  // the previous chunk's Q rows are no longer read
-        for (int e = tid; e < nf * a.rank; e += kThreads) sq[e] = q[(plo + c0) * a.rank + e];
-        __syncthreads();
+        if constexpr (!SP) {
+            __syncthreads();  // the previous chunk's Q rows are no longer read
+            for (int e = tid; e < nf * a.rank; e += kThreads) sq[e] = q[(plo + c0) * a.rank + e];
+            __syncthreads();
+        }
         for (int fl = c0 + tid; fl < c0 + nf; fl += kThreads) {
         const int64_t i = plo + fl;
         const int slot = SP ? slots[fl] : -1;
