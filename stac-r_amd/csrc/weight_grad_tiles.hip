@@ -1,8 +1,9 @@
 // Weight gradient from the saved factors on the matrix cores: dW = (G^T C) Q^T + G^T R_s and
 // dbias = sum_t G (stacr/layers.py:172-198), with G streamed once from memory.
 //
-// For 16-bit G and C, rank (+ the bias column) <= 16, d_out a multiple of 16, d_in <= 8192.  Other
-// problems use the kernels of weight_grad.hip.  Accumulation is fp32 and dW is rounded once.
+// For 16-bit G and C, or fp32 G and C with 4 / 8-bit residual codes, rank (+ the bias column) <= 16,
+// d_out a multiple of 16, d_in <= 8192.  Other problems use the kernels of weight_grad.hip.
+// Accumulation is fp32 and dW is rounded once.
 //
 // Three launches.
 //   k_tile_count  (sparse only) 16 workgroups over contiguous chunks of the residual entries: the
@@ -83,7 +84,7 @@ struct TileArgs {
     uint32_t *hist;     // [n_hist][d_in] partial entry counts per feature (chunks, or census copies)
     int n_hist;
     uint32_t *bstart;   // [n_blocks + 1] first entry of each block
-    uint16_t *cp;       // [n_blocks][16 waves][4 row groups][ncol][8] coefficient operands
+    void *cp;           // [n_blocks][16 waves][4 row groups][ncol][8] coefficient operands (G's dtype)
     void *bt;           // [n_blocks][n_parts][nt][16 waves][64 lanes][8] column operands
     uint32_t *light;    // regions of kOffWords offsets then light records (see the plan)
     TileHdr *hdr;       // [n_blocks][n_parts]
@@ -127,11 +128,12 @@ __device__ __forceinline__ float entry_value(const TileArgs &a, int64_t e)
     return a.bits ? (float)entry_code(a, e) : load_any(a.data, a.val_dt, e);
 }
 
-// An operand in G's dtype: exact for the integer codes; a stored value is rounded to G's dtype, as
-// the reference casts the values to G's dtype before its sparse product.
+// A light record's 16-bit value: an operand in G's dtype, exact for the integer codes; a stored value
+// is rounded to G's dtype, as the reference casts the values to G's dtype before its sparse product.
+// fp32 G takes codes only, kept as bf16 (exact for |code| <= 127).
 __device__ __forceinline__ uint32_t to_g16(float v, int g_dt)
 {
-    return g_dt == STACR_DTYPE_BF16 ? f_to_bf16_bits(v) : f_to_f16_bits(v);
+    return g_dt == STACR_DTYPE_F16 ? f_to_f16_bits(v) : f_to_bf16_bits(v);
 }
 
 template <int DT>
@@ -383,19 +385,24 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
     // ---- the block's coefficient operands [C | 1]: (wave w, row group g, column n) holds rows
     // 32 w + 8 g .. + 7 of column n
     if (pack_c) {
-        const uint16_t *c = static_cast<const uint16_t *>(a.coeff);
-        const uint32_t one = a.g_dt == STACR_DTYPE_BF16 ? 0x3f80u : 0x3c00u;
-        uint16_t *cp = a.cp + (int64_t)b * kTB * a.ncol;
-        for (int i = tid; i < kTB * a.ncol; i += kThreads) {
-            const int k = i & 7, n = (i >> 3) % a.ncol, wg = (i >> 3) / a.ncol;  // wg = 4 w + g
-            const int64_t t = (int64_t)b * kTB + 8 * wg + k;
-            uint16_t v = 0;
-            if (t < a.rows) {
-                if (n < a.rank) v = c[t * a.rank + n];
-                else if (n == a.bias_col) v = (uint16_t)one;
+        auto pack = [&](auto *cp, const auto *c, auto one) {
+            cp += (int64_t)b * kTB * a.ncol;
+            for (int i = tid; i < kTB * a.ncol; i += kThreads) {
+                const int k = i & 7, n = (i >> 3) % a.ncol, wg = (i >> 3) / a.ncol;  // wg = 4 w + g
+                const int64_t t = (int64_t)b * kTB + 8 * wg + k;
+                decltype(one) v = 0;
+                if (t < a.rows) {
+                    if (n < a.rank) v = c[t * a.rank + n];
+                    else if (n == a.bias_col) v = one;
+                }
+                cp[i] = v;
             }
-            cp[i] = v;
-        }
+        };
+        if (a.g_dt == STACR_DTYPE_F32)
+            pack(static_cast<uint32_t *>(a.cp), static_cast<const uint32_t *>(a.coeff), 0x3f800000u);
+        else
+            pack(static_cast<uint16_t *>(a.cp), static_cast<const uint16_t *>(a.coeff),
+                 (uint16_t)(a.g_dt == STACR_DTYPE_BF16 ? 0x3f80u : 0x3c00u));
     }
 }
 
@@ -493,23 +500,30 @@ __device__ __forceinline__ uint4 codes_to_operand(uint2 w)
 // LDS layout of one stream buffer (byte offsets).  The kernel holds three buffers as three
 // distinct __shared__ arrays: the compiler then knows that reads of one never alias the
 // direct-to-LDS copies into the others, and waits for those copies only where the code says so.
-template <bool SP>
+template <bool SP, int GB>
 struct TileLds {
-    static constexpr size_t g = 0;                                           // [kTB][16] u16
-    static constexpr size_t off = g + (size_t)kTB * kOS * 2;                 // [kOffWords] u32
-    static constexpr size_t light = off + (size_t)kOffWords * 4;             // [kLightCap] u32
-    static constexpr size_t size = SP ? light + (size_t)kLightCap * 4 : off;  // 37 KiB with entries
+    // light records staged per block: fp32 G tiles are twice as large, so half as many records
+    static constexpr int light_cap = GB == 4 ? kLightCap / 2 : kLightCap;
+    static constexpr size_t g = 0;                                           // [kTB][16] G elements
+    static constexpr size_t off = g + (size_t)kTB * kOS * GB;                // [kOffWords] u32
+    static constexpr size_t light = off + (size_t)kOffWords * 4;             // [light_cap] u32
+    static constexpr size_t size = SP ? light + (size_t)light_cap * 4 : off;  // with entries 37 KiB (45 fp32)
     static_assert(size % 1024 == 0, "buffers start on 1 KiB boundaries");
     static_assert(3 * size + kMaxBlocks * sizeof(TileHdr) <= 160 * 1024, "fits the CU's LDS");
     static_assert(size >= (size_t)kWaves * 256 * 4, "one tile of every wave fits a buffer (the reduction)");
 };
 
 // Without entries the buffers are small and two workgroups share a CU: 8 waves per SIMD, so
-// <= 64 VGPRs.
+// <= 64 VGPRs.  fp32 G (entries with 4 / 8-bit codes only) runs v_mfma_f32_16x16x4_f32: eight
+// products a tile over the same 32 rows a wave takes, row 32 w + 8 (lane / 16) + s in step s, so the
+// operands keep the 16-bit layout's (row, column) assignment per lane.
 template <int DT, bool SP, bool BT8>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4 : 8, SP ? 4 : 8))) void k_tile_grad(TileArgs a)
 {
-    using L = TileLds<SP>;
+    constexpr int GB = DT == STACR_DTYPE_F32 ? 4 : 2;  // bytes of a G / C / Q element
+    static_assert(GB == 2 || (SP && BT8), "fp32 G with residual codes only");
+    using L = TileLds<SP, GB>;
+    using QT = typename std::conditional<GB == 4, uint32_t, uint16_t>::type;
     constexpr int NT = SP ? kNT : 0;
     using BW = typename std::conditional<BT8, uint2, uint4>::type;  // one lane's column operand
     __shared__ __attribute__((aligned(1024))) unsigned char lds0[L::size];
@@ -518,8 +532,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
     __shared__ TileHdr s_hdr[SP ? kMaxBlocks : 1];
     // with entries, the part's Q rows (<= 1024 features x <= 16 values), loaded while the first two
     // blocks are copied and read by the epilogue
-    __shared__ uint16_t s_q[SP ? kPartMax * 16 : 1];
-    static_assert(!SP || 3 * L::size + kMaxBlocks * sizeof(TileHdr) + kPartMax * 16 * 2 <= 160 * 1024,
+    constexpr bool kQLds = SP && GB == 2;  // (fp32 Q rows would not fit beside the fp32 buffers)
+    __shared__ uint16_t s_q[kQLds ? kPartMax * 16 : 1];
+    static_assert(!kQLds || 3 * L::size + kMaxBlocks * sizeof(TileHdr) + kPartMax * 16 * 2 <= 160 * 1024,
                   "the stream buffers, headers and Q rows fit the CU's LDS");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
@@ -544,15 +559,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
     // Every load goes through a buffer resource (base and size in scalar registers) with a 32-bit
     // per-lane offset that is the same for every block and a uniform per-block offset.  Kept apart
     // like this, no 64-bit per-lane address has to live across the stream.
-    const uint32_t row_bytes = (uint32_t)a.d_out * 2;
-    const uint32_t g_lane_row = 32u * wave + (lane >> 1);                     // G tile row of this lane
-    const uint32_t g_lane_col = (uint32_t)o0 * 2 + 16u * (lane & 1);          // bytes into the row
+    const uint32_t row_bytes = (uint32_t)a.d_out * GB;
+    // G tile row and bytes into the row of this lane's 16-byte copy (fp32: one of two, 256 rows apart)
+    const uint32_t g_lane_row = GB == 2 ? 32u * wave + (lane >> 1) : 16u * wave + (lane >> 2);
+    const uint32_t g_lane_col = (uint32_t)o0 * GB + (GB == 2 ? 16u * (lane & 1) : 16u * (lane & 3));
     const uint32_t rec_lane = (256u * wave + 4u * lane) * 4;                  // light / offset copies
-    const uint32_t cp_lane = ((wave * 4u + grp) * a.ncol + n) * 16;           // coefficient operand
+    const uint32_t cp_lane = ((wave * 4u + grp) * a.ncol + n) * 8 * GB;       // coefficient operand
     const uint32_t bt_lane = (wave * 64u + lane) * sizeof(BW);                // column operand
     const bool has_c = n < a.ncol;
     const uint32_t regions = (uint32_t)nb * (uint32_t)a.n_parts;
-    const __amdgpu_buffer_rsrc_t r_cp = make_rsrc(a.cp, (uint64_t)nb * kTB * a.ncol * 2);
+    const __amdgpu_buffer_rsrc_t r_cp = make_rsrc(a.cp, (uint64_t)nb * kTB * a.ncol * GB);
     // (without entries these three are empty resources that nothing reads)
     const __amdgpu_buffer_rsrc_t r_light = make_rsrc(a.light, SP ? record_words(a.nnz, regions) * 4 : 0);
     const __amdgpu_buffer_rsrc_t r_bt = make_rsrc(a.bt, SP ? (uint64_t)regions * NT * kWaves * 64 * sizeof(BW) : 0);
@@ -566,7 +582,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
             const uint32_t lbase = __builtin_amdgcn_readfirstlane(s_hdr[blk].light_base);
             const uint32_t lcount = __builtin_amdgcn_readfirstlane(s_hdr[blk].light_count);
             if (wave < kOffWords / 256 && 256 * wave <= pw) copy16(r_light, B + L::off + (size_t)wave * 1024, rec_lane, lbase * 4);
-            if (256u * (uint32_t)wave < lcount)
+            if (wave < L::light_cap / 256 && 256u * (uint32_t)wave < lcount)
                 copy16(r_light, B + L::light + (size_t)wave * 1024, rec_lane, (lbase + kOffWords) * 4);
         }
     };
@@ -574,20 +590,27 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
         // rows past the end repeat the last (their operands are zero)
         const uint32_t rows_here = (uint32_t)(a.rows - (int64_t)blk * kTB) < (uint32_t)kTB
                                        ? (uint32_t)(a.rows - (int64_t)blk * kTB) : (uint32_t)kTB;
-        const uint32_t r = g_lane_row < rows_here - 1 ? g_lane_row : rows_here - 1;
         const __amdgpu_buffer_rsrc_t r_g =
             make_rsrc(static_cast<const char *>(a.g) + (size_t)blk * kTB * row_bytes, (uint64_t)rows_here * row_bytes);
-        copy16(r_g, B + L::g + (size_t)wave * 1024, r * row_bytes + g_lane_col, 0u);
+#pragma unroll
+        for (int h = 0; h < GB / 2; ++h) {
+            const uint32_t row = g_lane_row + 256u * h;
+            const uint32_t r = row < rows_here - 1 ? row : rows_here - 1;
+            copy16(r_g, B + L::g + (size_t)h * 16384 + (size_t)wave * 1024, r * row_bytes + g_lane_col, 0u);
+        }
     };
 
     // ---- block `blk`'s operands for this lane: rows 32 wave + 8 grp .. + 7 of column n
     struct Ops {
-        uint4 c;
+        uint4 c[GB / 2];
         BW t[NT > 0 ? NT : 1];
     };
     auto load_ops = [&](int blk, Ops &r) {
-        r.c = make_uint4(0u, 0u, 0u, 0u);
-        if (has_c) r.c = load16(r_cp, cp_lane, (uint32_t)blk * kTB * a.ncol * 2);
+#pragma unroll
+        for (int h = 0; h < GB / 2; ++h) {
+            r.c[h] = make_uint4(0u, 0u, 0u, 0u);
+            if (has_c) r.c[h] = load16(r_cp, cp_lane + 16u * h, (uint32_t)blk * kTB * a.ncol * GB);
+        }
         if constexpr (SP) {
             const uint32_t base = ((uint32_t)blk * a.n_parts + part) * (uint32_t)(NT * kWaves * 64 * sizeof(BW));
 #pragma unroll
@@ -609,20 +632,44 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
 
     // ---- the block in buffer B with operands r: the matrix-core products
     auto products = [&](const unsigned char *B, const Ops &r) {
-        const uint16_t *gt = reinterpret_cast<const uint16_t *>(B + L::g);
-        // G^T[o][t0 .. t0 + 7], o = lane % 16, t0 = 32 wave + 8 (lane / 16): two transposing reads
-        // (in a 16-lane group lane m addresses row r0 + m / 4, outputs 4 (m % 4) .. + 3, and lane n
-        // receives G[r0 + j][n], j = 0..3)
-        const int kk = 32 * wave + 8 * grp;
-        const uint16_t *pa = gt + (kk + ((lane & 15) >> 2)) * kOS + (lane & 3) * 4;
-        const uint2 lo = lds_tr16(pa), hi = lds_tr16(pa + 4 * kOS);
-        const uint4 av = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        acc_m = mfma16<DT>(av, r.c, acc_m);
-        if constexpr (SP) {
+        if constexpr (GB == 4) {
+            // step s: lane (g, n) gives G[32 w + 8 g + s][n] and the operands of that row, column n
+            const float *gt = reinterpret_cast<const float *>(B + L::g);
+            const int r0 = 32 * wave + 8 * grp;
+            float av[8];
 #pragma unroll
-            for (int i = 0; i < NT; ++i) {
-                if constexpr (BT8) acc_t[i] = mfma16<DT>(av, codes_to_operand<DT>(r.t[i]), acc_t[i]);
-                else acc_t[i] = mfma16<DT>(av, r.t[i], acc_t[i]);
+            for (int k = 0; k < 8; ++k) av[k] = gt[(r0 + k) * kOS + n];
+            const uint32_t cw[8] = {r.c[0].x, r.c[0].y, r.c[0].z, r.c[0].w, r.c[GB / 2 - 1].x, r.c[GB / 2 - 1].y,
+                                    r.c[GB / 2 - 1].z, r.c[GB / 2 - 1].w};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc_m = __builtin_amdgcn_mfma_f32_16x16x4f32(av[k], __uint_as_float(cw[k]), acc_m, 0, 0, 0);
+            if constexpr (SP) {
+#pragma unroll
+                for (int i = 0; i < NT; ++i) {
+                    const uint32_t w2[2] = {r.t[i].x, r.t[i].y};  // eight int8 codes, row order
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const float code = (float)(int)(int8_t)(w2[k >> 2] >> (8 * (k & 3)));  // signed
+                        acc_t[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[k], code, acc_t[i], 0, 0, 0);
+                    }
+                }
+            }
+        } else {
+            const uint16_t *gt = reinterpret_cast<const uint16_t *>(B + L::g);
+            // G^T[o][t0 .. t0 + 7], o = lane % 16, t0 = 32 wave + 8 (lane / 16): two transposing reads
+            // (in a 16-lane group lane m addresses row r0 + m / 4, outputs 4 (m % 4) .. + 3, and lane n
+            // receives G[r0 + j][n], j = 0..3)
+            const int kk = 32 * wave + 8 * grp;
+            const uint16_t *pa = gt + (kk + ((lane & 15) >> 2)) * kOS + (lane & 3) * 4;
+            const uint2 lo = lds_tr16(pa), hi = lds_tr16(pa + 4 * kOS);
+            const uint4 av = make_uint4(lo.x, lo.y, hi.x, hi.y);
+            acc_m = mfma16<DT>(av, r.c[0], acc_m);
+            if constexpr (SP) {
+#pragma unroll
+                for (int i = 0; i < NT; ++i) {
+                    if constexpr (BT8) acc_t[i] = mfma16<DT>(av, codes_to_operand<DT>(r.t[i]), acc_t[i]);
+                    else acc_t[i] = mfma16<DT>(av, r.t[i], acc_t[i]);
+                }
             }
         }
     };
@@ -630,7 +677,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
     // ---- this thread's feature: its light entries of the block in buffer B
     auto light_entries = [&](int blk, const unsigned char *B) {
         if constexpr (SP) {
-            const uint16_t *gt = reinterpret_cast<const uint16_t *>(B + L::g);
             if (tid < pw) {
                 const TileHdr h = s_hdr[blk];
                 const uint32_t *off = reinterpret_cast<const uint32_t *>(B + L::off);
@@ -638,32 +684,51 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
                 // the owner's range, clamped to the block's records whatever the offsets hold
                 const uint32_t k1 = off[tid + 1] < h.light_count ? off[tid + 1] : h.light_count;
                 const uint32_t k0 = off[tid] < k1 ? off[tid] : k1;
-                // s[2 k] += lo(w_k) v and s[2 k + 1] += hi(w_k) v for the row's eight 32-bit words
-                // w_k: dot products with the pairs (v, 0) and (0, v), no conversions
-                auto add_row = [&](uint32_t rec, uint4 w0, uint4 w1) {
-                    const uint32_t v_lo = rec >> 16, v_hi = rec & 0xffff0000u;
-                    const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                // the record's G row (GB 16-byte words) from the tile
+                struct GRow {
+                    uint4 w[GB];
+                };
+                auto read_row = [&](uint32_t rec) {
+                    const uint4 *p = reinterpret_cast<const uint4 *>(B + L::g + (size_t)(rec & 511u) * kOS * GB);
+                    GRow r;
 #pragma unroll
-                    for (int o = 0; o < 8; ++o) {
-                        s[2 * o] = dot2<DT>(w[o], v_lo, s[2 * o]);
-                        s[2 * o + 1] = dot2<DT>(w[o], v_hi, s[2 * o + 1]);
+                    for (int i = 0; i < GB; ++i) r.w[i] = p[i];
+                    return r;
+                };
+                auto add_row = [&](uint32_t rec, const GRow &g) {
+                    if constexpr (GB == 4) {
+                        // s[o] += G[t][o] v, the code v kept as bf16 in the record's high half
+                        const float v = __uint_as_float(rec & 0xffff0000u);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            s[4 * i] = fmaf(__uint_as_float(g.w[i].x), v, s[4 * i]);
+                            s[4 * i + 1] = fmaf(__uint_as_float(g.w[i].y), v, s[4 * i + 1]);
+                            s[4 * i + 2] = fmaf(__uint_as_float(g.w[i].z), v, s[4 * i + 2]);
+                            s[4 * i + 3] = fmaf(__uint_as_float(g.w[i].w), v, s[4 * i + 3]);
+                        }
+                    } else {
+                        // s[2 k] += lo(w_k) v and s[2 k + 1] += hi(w_k) v for the row's eight 32-bit
+                        // words w_k: dot products with the pairs (v, 0) and (0, v), no conversions
+                        const uint32_t v_lo = rec >> 16, v_hi = rec & 0xffff0000u;
+                        const uint32_t w[8] = {g.w[0].x, g.w[0].y, g.w[0].z, g.w[0].w,
+                                               g.w[GB - 1].x, g.w[GB - 1].y, g.w[GB - 1].z, g.w[GB - 1].w};
+#pragma unroll
+                        for (int o = 0; o < 8; ++o) {
+                            s[2 * o] = dot2<DT>(w[o], v_lo, s[2 * o]);
+                            s[2 * o + 1] = dot2<DT>(w[o], v_hi, s[2 * o + 1]);
+                        }
                     }
                 };
-                auto row_of = [&](uint32_t rec) { return reinterpret_cast<const uint4 *>(gt + (rec & 511u) * kOS); };
-                auto add_entry = [&](uint32_t rec) {
-                    const uint4 *row = row_of(rec);
-                    add_row(rec, row[0], row[1]);
-                };
+                auto add_entry = [&](uint32_t rec) { add_row(rec, read_row(rec)); };
                 // records staged in LDS, two at a time (both rows read before either is summed, in
-                // record order), then (blocks with more than kLightCap) the rest from memory
-                const uint32_t kl = k1 < (uint32_t)kLightCap ? k1 : (uint32_t)kLightCap;
+                // record order), then (blocks with more than the staged records) the rest from memory
+                const uint32_t kl = k1 < (uint32_t)L::light_cap ? k1 : (uint32_t)L::light_cap;
                 uint32_t k = k0;
                 for (; k + 1 < kl; k += 2) {
                     const uint32_t ra = lrec[k], rb = lrec[k + 1];
-                    const uint4 *pa = row_of(ra), *pb = row_of(rb);
-                    const uint4 a0 = pa[0], a1 = pa[1], b0 = pb[0], b1 = pb[1];
-                    add_row(ra, a0, a1);
-                    add_row(rb, b0, b1);
+                    const GRow ga = read_row(ra), gb = read_row(rb);
+                    add_row(ra, ga);
+                    add_row(rb, gb);
                 }
                 if (k < kl) add_entry(lrec[k]);
                 for (uint32_t k = k0 > kl ? k0 : kl; k < k1; ++k) add_entry(a.light[h.light_base + kOffWords + k]);
@@ -684,8 +749,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
         issue_records(1, lds1);
         issue_g(1, lds1);
     }
-    const uint16_t *q = static_cast<const uint16_t *>(a.q);
-    if constexpr (SP) {
+    const QT *q = static_cast<const QT *>(a.q);
+    if constexpr (kQLds) {
         // the part's Q rows (pw * rank <= 16384 values, contiguous): all loads issued, then stored
         const int n_q = pw * a.rank;
         const uint16_t *qs = q + plo * a.rank;
@@ -703,14 +768,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
         load_ops(blk + 1, ops);
         if (blk + 2 < nb) issue_records(blk + 2, B2);
         light_entries(blk, B);
-        // every step ends its memory instructions with one G copy, so that the wait below always
-        // covers the operand loads; in the step before last it copies the last block again into
-        // the buffer of block blk - 1, which nothing reads any more
+        // every step ends its memory instructions with the G copy (fp32: two), so that the wait
+        // below always covers the operand loads; in the step before last it copies the last block
+        // again into the buffer of block blk - 1, which nothing reads any more
         issue_g(blk + 2 < nb ? blk + 2 : nb - 1, B2);
-        // vmcnt(1) lgkmcnt(0) (expcnt unconstrained), as a builtin so that the compiler knows the
-        // operand loads have landed; then the barrier, not __syncthreads(), whose fence would wait
-        // for every copy in flight
-        __builtin_amdgcn_s_waitcnt(0x0071);
+        // vmcnt(1) (fp32: 2) lgkmcnt(0) (expcnt unconstrained), as a builtin so that the compiler
+        // knows the operand loads have landed; then the barrier, not __syncthreads(), whose fence
+        // would wait for every copy in flight
+        if constexpr (GB == 4) __builtin_amdgcn_s_waitcnt(0x0072);
+        else __builtin_amdgcn_s_waitcnt(0x0071);
         asm volatile("s_barrier" ::: "memory");
     };
     // every block but the last through `step` (the last loads nothing more)
@@ -773,20 +839,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
     __syncthreads();
 
     // ---- dW tile: M Q^T + scale (light + column sums), one rounding; dbias from M[:, bias_col].
-    // With entries a part has <= 1024 features, one per thread, and its Q rows are in s_q already;
-    // without, the threads loop over the features, and the Q rows of a chunk of features are first
-    // copied to LDS (lds2, unused now).
-    const int qchunk = SP ? kThreads
-                          : ((int)((L::size / 2) / (size_t)a.rank) < kThreads ? (int)((L::size / 2) / (size_t)a.rank) : kThreads);
-    uint16_t *sq = SP ? s_q : reinterpret_cast<uint16_t *>(lds2);
+    // With entries a part has <= 1024 features, one per thread (thread f finishes feature f); 16-bit
+    // Q rows are in s_q already.  Otherwise the Q rows of a chunk of features are first copied to
+    // LDS (fp32 with entries: lds0, free after the reduction; without entries: lds2), and without
+    // entries the threads loop over the chunk's features.
+    const int qfit = (int)(L::size / ((size_t)a.rank * GB));
+    const int qchunk = kQLds || qfit > kThreads ? kThreads : qfit;
+    QT *sq = kQLds ? reinterpret_cast<QT *>(s_q) : reinterpret_cast<QT *>(SP ? lds0 : lds2);
+    auto qval = [&](QT v) {
+        if constexpr (GB == 4) return __uint_as_float(v);
+        else return g16_to_f<DT>(v);
+    };
     for (int c0 = 0; c0 < pw; c0 += qchunk) {
         const int nf = pw - c0 < qchunk ? pw - c0 : qchunk;
-        if constexpr (!SP) {
+        if constexpr (!kQLds) {
             __syncthreads();  // the previous chunk's Q rows are no longer read
             for (int e = tid; e < nf * a.rank; e += kThreads) sq[e] = q[(plo + c0) * a.rank + e];
             __syncthreads();
         }
-        for (int fl = c0 + tid; fl < c0 + nf; fl += kThreads) {
+        for (int fl = SP ? tid : c0 + tid; fl < c0 + nf; fl += kThreads) {
+        if (SP && fl < c0) continue;  // (with entries: this thread's feature is in a later chunk)
         const int64_t i = plo + fl;
         const int slot = SP ? slots[fl] : -1;
         float out[kOS];
@@ -797,7 +869,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
         }
         // + sum_j M[o][j] Q[i][j] (the M reads are LDS broadcasts)
         for (int j = 0; j < a.rank; ++j) {
-            const float qj = g16_to_f<DT>(sq[(fl - c0) * a.rank + j]);
+            const float qj = qval(sq[(fl - c0) * a.rank + j]);
 #pragma unroll
             for (int o = 0; o < kOS; ++o) out[o] = fmaf(fin[o * 16 + j], qj, out[o]);
         }
@@ -833,19 +905,22 @@ namespace {
 
 struct TileGeom {
     int n_blocks, n_parts, part_w, ncol, bias_col;
+    int gb;  // bytes of a G / C element
     bool sparse, bt8;
 };
 
 bool tile_geom(const StacrGradArgs &a, TileGeom *g)
 {
-    if (a.dtype != STACR_DTYPE_BF16 && a.dtype != STACR_DTYPE_F16) return false;
+    // 16-bit G; or fp32 G with residual codes (bits 4 / 8: integer operands, kept as bf16 exactly)
+    const bool f32 = a.dtype == STACR_DTYPE_F32;
+    if (a.dtype != STACR_DTYPE_BF16 && a.dtype != STACR_DTYPE_F16 && !(f32 && a.nnz > 0 && a.bits != 0)) return false;
     if (a.rows < 1 || a.d_in < 1 || a.d_out < kOS || a.d_out % kOS) return false;
     const int cols = a.rank + (a.dbias ? 1 : 0);
     if (cols > 16) return false;
     if ((uintptr_t)a.g % 16) return false;
     if (a.rows > (int64_t)kMaxBlocks * kTB || a.d_in > kMaxFeat) return false;
     if ((uint64_t)a.rows * (uint64_t)a.d_in >= (1ull << 32)) return false;  // 32-bit flat indices
-    if ((uint64_t)kTB * (uint64_t)a.d_out * 2 >= (1ull << 31)) return false;  // 32-bit lane offsets
+    if ((uint64_t)kTB * (uint64_t)a.d_out * (f32 ? 4 : 2) >= (1ull << 31)) return false;  // 32-bit lane offsets
     if (a.nnz > 0 && a.index_bytes != 4 && a.index_bytes != 8) return false;
     if (a.nnz >= (1ll << 31)) return false;
     g->n_blocks = (int)((a.rows + kTB - 1) / kTB);
@@ -854,6 +929,7 @@ bool tile_geom(const StacrGradArgs &a, TileGeom *g)
     g->part_w = (int)((a.d_in + g->n_parts - 1) / g->n_parts);
     g->ncol = cols;
     g->bias_col = a.dbias ? a.rank : -1;
+    g->gb = f32 ? 4 : 2;
     g->sparse = a.nnz > 0;
     g->bt8 = a.bits != 0;
     return true;
@@ -870,7 +946,7 @@ size_t tile_layout(int64_t nnz, int64_t d_in, const TileGeom &g, size_t *off)
     const size_t bt_bytes = regions * (size_t)kNT * kWaves * 64 * (g.bt8 ? 8 : 16);
     take(TW_HIST, g.sparse ? (size_t)kChunks * d_in * 4 : 0);
     take(TW_BSTART, g.sparse ? ((size_t)g.n_blocks + 1) * 4 : 0);
-    take(TW_CP, (size_t)g.n_blocks * kTB * g.ncol * 2);
+    take(TW_CP, (size_t)g.n_blocks * kTB * g.ncol * g.gb);
     take(TW_BT, g.sparse ? bt_bytes : 0);
     take(TW_LIGHT, g.sparse ? (size_t)record_words(nnz, regions) * 4 : 0);
     take(TW_HDR, g.sparse ? regions * sizeof(TileHdr) : 0);
@@ -916,6 +992,7 @@ size_t stacr_tiles_ws_bound(int64_t rows, int64_t d_out, int64_t d_in, int64_t n
     g.part_w = (int)((d_in + g.n_parts - 1) / g.n_parts);
     g.ncol = 16;  // the widest coefficient operand (rank + bias column up to 16)
     g.bias_col = -1;
+    g.gb = 4;       // fp32 coefficient operands
     g.sparse = nnz > 0;
     g.bt8 = false;  // the wider column-operand form
     size_t off[TW_N];
@@ -958,7 +1035,7 @@ int stacr_tiles_launch(const StacrGradArgs &a)
     t.part_w = g.part_w;
     t.ncol = g.ncol;
     t.bias_col = g.bias_col;
-    t.cp = reinterpret_cast<uint16_t *>(ws + off[TW_CP]);
+    t.cp = ws + off[TW_CP];
     // with a census from the save, its per-feature counts and block starts replace the count pass
     const bool census = g.sparse && a.census;
     if (g.sparse) {
@@ -985,6 +1062,7 @@ int stacr_tiles_launch(const StacrGradArgs &a)
     rc = stacr_hip_check(hipGetLastError(), "weight_grad plan");
     if (rc) return rc;
     const int nwg = (int)(a.d_out / kOS) * g.n_parts;
+    if (a.dtype == STACR_DTYPE_F32) return launch_tile_grad<STACR_DTYPE_F32, true, true>(t, nwg, s);
     return a.dtype == STACR_DTYPE_BF16 ? launch_tile_grad_dt<STACR_DTYPE_BF16>(t, g, nwg, s)
                                        : launch_tile_grad_dt<STACR_DTYPE_F16>(t, g, nwg, s);
 }

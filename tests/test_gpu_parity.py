@@ -443,11 +443,15 @@ def test_weight_grad_int64_indices(dev):
     (4096, 2048, 512, 16, False, "bf16", False),   # two parts, rank 16 without bias, many records a feature
     (2000, 3000, 272, 15, True, "f16", False),     # three parts of 1000, rank 15 + bias, partial last block
     (3072, 1024, 1024, 8, True, "bf16", True),     # one part, skewed columns
+    (2000, 3000, 272, 15, True, "f32", False),     # fp32: Q rows of a part in two LDS chunks, partial block
+    (3072, 1024, 1024, 8, True, "f32", True),      # fp32: one part, skewed columns
+    (4096, 2048, 512, 16, False, "f32", False),    # fp32: two parts, rank 16, records past the staged ones
 ])
 def test_weight_grad_matrix_core_shapes(dev, rows, d_in, d_out, rank, bias, dtype, lognormal):
-    """The matrix-core path (16-bit G, rank + bias <= 16) against the oracle at shapes where a
-    part's Q rows span two LDS stages, features have more light records a block than the two the
-    streaming kernel loads with the operands, and parts do not cover whole 1024-feature spans."""
+    """The matrix-core path (16-bit G, or fp32 G with residual codes; rank + bias <= 16) against the
+    oracle at shapes where a part's Q rows span two LDS stages, features have more light records a
+    block than the two the streaming kernel loads with the operands, and parts do not cover whole
+    1024-feature spans."""
     from stacr_amd import kernels
 
     announce("grad tiles shape", rows, d_in, d_out, rank, bias, dtype)
@@ -469,11 +473,12 @@ def test_weight_grad_matrix_core_shapes(dev, rows, d_in, d_out, rank, bias, dtyp
         assert db is None
 
 
-@pytest.mark.parametrize("dtype,transposed", [("bf16", True), ("f16", False)])
+@pytest.mark.parametrize("dtype,transposed", [("bf16", True), ("f16", False), ("f32", False)])
 def test_weight_grad_matrix_core_path_is_deterministic(dev, dtype, transposed):
-    """16-bit G at rank 8: every sum of the weight gradient has a fixed order (light entries by one
-    owner thread in ascending row order, per-wave tiles reduced in wave order), so repeated calls
-    agree bit for bit, with int32 and int64 indices alike."""
+    """The matrix-core path at rank 8 (16-bit G; fp32 G with int8 codes): every sum of the weight
+    gradient has a fixed order (light entries by one owner thread in ascending row order, per-wave
+    tiles reduced in wave order), so repeated calls agree bit for bit, with int32 and int64 indices
+    alike."""
     from stacr_amd import kernels
 
     announce("grad determinism", dtype, transposed)
