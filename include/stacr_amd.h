@@ -310,7 +310,10 @@ int stacr_sample_magnitudes(const void *x, const void *coeff, const void *q, int
 int stacr_threshold_workspace_bytes(int64_t rows, int64_t feats, size_t *bytes);
 /* sampled, step 2: the first `cap` flat positions (ascending) with |r| >= threshold, the fp32
  * device scalar *threshold compared after rounding to dtype (torch's promotion for
- * `magnitude >= threshold`).  *count (int64, device) receives min(cap, passing entries). */
+ * `magnitude >= threshold`).  *count (int64, device) receives min(cap, passing entries); with
+ * cap = 0 nothing is written and *count receives every passing entry (a count-only call, which
+ * sizes the outputs of the adaptive engine's threshold selections, stacr/adaptive.py:1416-1517,
+ * 1574-1622,1628-1786: count, then select with cap = count). */
 int stacr_select_threshold(const void *x, const void *coeff, const void *q, int dtype, int64_t rows, int64_t feats,
                            int rank, const float *threshold, int64_t cap, void *idx, int index_bytes, void *values,
                            int64_t *count, void *workspace, size_t workspace_bytes, void *stream);

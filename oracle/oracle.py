@@ -476,6 +476,18 @@ def select_threshold(resid: np.ndarray, threshold: float, dtype: str, cap: int):
     return idx, flat[idx]
 
 
+def adaptive_select_above(resid: np.ndarray, threshold: float, dtype: str):
+    """Every position with |r| > threshold, ascending, with its value: the adaptive engine's
+    `chunk_flat.abs() > threshold_val` + `nonzero` over its chunks (stacr/adaptive.py:1493-1517 streaming
+    top-k, :1590-1606 "threshold", :1762-1778 "adaptive_threshold").  torch compares a tensor with a
+    Python float or a 0-dim tensor in the tensor's dtype, so the threshold is rounded to dtype first."""
+    flat = np.asarray(resid, np.float32).reshape(-1)
+    t = np.float32(round_dtype_scalar(float(threshold), dtype))
+    with np.errstate(invalid="ignore"):
+        idx = np.nonzero(np.abs(flat) > t)[0].astype(np.int64)
+    return idx, flat[idx]
+
+
 # ================================================================ adaptive engine's block_sparse
 # (stacr/adaptive.py:1788-1938), on the dtype-native residual of residual_act.
 def adaptive_block_energies(resid: np.ndarray, block_size: int, dtype: str) -> np.ndarray:

@@ -276,7 +276,8 @@ __global__ __launch_bounds__(kBlock) void k_thr_count(const typename Act<DT>::T 
     if (threadIdx.x == 0) wg_count[blockIdx.x] = sum;
 }
 
-// Exclusive offsets of the per-workgroup counts; count_out = min(cap, passing entries).
+// Exclusive offsets of the per-workgroup counts; count_out = min(cap, passing entries), or every
+// passing entry when cap is 0 (a count-only call).
 __global__ __launch_bounds__(kSegThreads) void k_thr_offsets(const uint32_t *__restrict__ wg_count, int64_t n_wg,
                                                              int64_t cap, uint32_t *__restrict__ wg_off,
                                                              int64_t *__restrict__ count_out)
@@ -291,7 +292,7 @@ __global__ __launch_bounds__(kSegThreads) void k_thr_offsets(const uint32_t *__r
         if (i < n_wg) wg_off[i] = (uint32_t)(run + ex);  // total < 2^32
         run += tile;
     }
-    if (threadIdx.x == 0) *count_out = (int64_t)run < cap ? (int64_t)run : cap;
+    if (threadIdx.x == 0) *count_out = cap == 0 || (int64_t)run < cap ? (int64_t)run : cap;
 }
 
 template <int DT>

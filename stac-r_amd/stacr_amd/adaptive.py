@@ -407,10 +407,9 @@ class STACRConfig:
     """Adaptive-engine configuration: the reference's fields, defaults and validation
     (stacr/adaptive.py:599-977), so configs and checkpoints written for it load here.
 
-    This build runs residual_mode "topk", "none" and "sparse_only" (plus the warmup baseline) on
-    the HIP kernels, as do "block_sparse" (the default) and the warmup baseline; "threshold",
-    "adaptive_threshold", streaming top-k and basis sharing raise NotImplementedError when a layer
-    meets them.
+    Every residual_mode runs on the HIP kernels ("topk" and its streaming form, "threshold",
+    "adaptive_threshold", "block_sparse" (the default), "none", "sparse_only", and the warmup
+    baseline); basis sharing raises NotImplementedError when a layer meets it.
     """
 
     method: str = "stacr"
@@ -616,7 +615,51 @@ def _residual_plan(config: dict, layer_state: dict, step_counter) -> tuple[str, 
     return mode, budget, gate
 
 
-_UNBUILT_MODES = ("threshold", "adaptive_threshold")
+def _select_above(x2d: torch.Tensor, coeff: torch.Tensor, basis: torch.Tensor, threshold):
+    """(indices, values) of every residual with |r| > threshold, ascending, as the reference's
+    `chunk_flat.abs() > threshold_val` + `nonzero` over the chunks (stacr/adaptive.py:1493-1517,
+    1574-1622, 1762-1786): the threshold (a Python float, or a 0-dim tensor) is rounded to the
+    activation dtype as torch's comparison does, and the strict comparison becomes the HIP
+    selector's |r| >= t' with t' the next value of that dtype above it.  Indices in
+    _choose_index_dtype(rows * feats)."""
+    dt = x2d.dtype
+    t = torch.as_tensor(threshold, device="cpu").to(dt)  # the dtype rounding of the comparison
+    index_dtype = _choose_index_dtype(x2d.numel())
+    tv = float(t)
+    if tv != tv or tv == math.inf:  # nothing compares above NaN or +inf
+        return torch.empty(0, dtype=index_dtype, device=x2d.device), torch.empty(0, dtype=dt, device=x2d.device)
+    if tv < 0:
+        # every residual but NaN passes (|r| >= 0); the selector's >= 0 gives exactly that
+        nxt = torch.zeros((), dtype=torch.float32)
+    else:
+        # the next representable value above t in the activation dtype (t >= 0: one ulp up)
+        ibits = {torch.float32: torch.int32, torch.bfloat16: torch.int16, torch.float16: torch.int16}[dt]
+        nxt = (t.reshape(1).view(ibits) + 1).view(dt).float().reshape(())
+    from .kernels import select_threshold
+    idx, values = select_threshold(x2d, coeff, basis, nxt.to(x2d.device), None)
+    return idx.to(index_dtype), values
+
+
+def _sampled_threshold(x2d: torch.Tensor, coeff: torch.Tensor, basis: torch.Tensor, chunk_size: int,
+                       sample_size: int, quantile: float) -> torch.Tensor:
+    """The threshold the reference's sampling passes estimate (stacr/adaptive.py:1422-1470,
+    1694-1738): per chunk of `chunk_size` rows, min(samples_per_chunk, chunk elements) positions
+    from torch.randint on the activation's device (the global generator, drawn chunk by chunk in
+    the reference's order), |r| there (one HIP gather for all chunks), then torch.quantile of
+    those magnitudes (in fp32 for 16-bit types, rounded back to the activation dtype)."""
+    from .kernels import sample_magnitudes
+    rows, feats = x2d.shape
+    per_chunk = max(1, (sample_size * chunk_size) // rows)
+    positions = []
+    for start in range(0, rows, chunk_size):
+        n_el = (min(start + chunk_size, rows) - start) * feats
+        n = min(per_chunk, n_el)
+        if n > 0:
+            positions.append(torch.randint(0, n_el, (n,), device=x2d.device) + start * feats)
+    samples = sample_magnitudes(x2d, coeff, basis, torch.cat(positions))
+    if samples.dtype in (torch.float16, torch.bfloat16):
+        return torch.quantile(samples.float(), quantile).to(samples.dtype)
+    return torch.quantile(samples, quantile)
 
 
 def _record_energy(layer_state: dict, energy_host: list, rank: int, coeff_rows: int, schedule_step: int) -> None:
@@ -663,10 +706,9 @@ class STACRFunction(torch.autograd.Function):
         ctx.residual_shape, ctx.cpu_offload = (b_flat, in_features), False
         recomputing = _is_recomputing()
 
-        if mode in _UNBUILT_MODES or (mode == "topk" and config.get("streaming_topk", False)):
-            what = "streaming top-k" if mode == "topk" else f"residual_mode {mode!r}"
-            raise NotImplementedError(f"adaptive {what} has no HIP kernel here (topk, block_sparse, none and "
-                                      "sparse_only do)")
+        # streaming top-k: the reference's fused route takes precedence when it runs (budget > 0)
+        streaming = (mode == "topk" and config.get("streaming_topk", False)
+                     and not (config.get("use_fused_kernel", False) and budget > 0))
         if config.get("use_fused_kernel", False):
             layer_state["b4_fused_kernel_route"] = "hip_save"
 
@@ -696,13 +738,18 @@ class STACRFunction(torch.autograd.Function):
         basis_c = basis if basis.dtype == x2d.dtype else basis.to(x2d.dtype)
         rank = basis_c.shape[1]
         chunk = int(config.get("chunk_size", 512))
-        coeff, idx, values, energy = save(x2d, basis_c, budget if mode == "topk" else 0.0, chunk)
+        total = b_flat * in_features
+        k_budget = min(int(total * budget), total)  # the k of "topk" and "adaptive_threshold"
+        exact_topk = mode == "topk" and not streaming
+        coeff, idx, values, energy = save(x2d, basis_c, budget if exact_topk else 0.0, chunk)
+        # "adaptive_threshold" with k = 0 keeps no residual and computes no energy (it stays 0)
+        no_energy = mode == "adaptive_threshold" and k_budget <= 0
         # The host reads of a forward: the energies (the rank controller, refresh triggers and skip
         # gate consume them every step, as in the reference) and the dtype code of each quantized
         # scale, fetched together in one transfer after every kernel is queued.  Only a skip gate
         # needs the energy first, to decide whether the residual is kept.
         energy_host = None
-        if gate is not None and mode in ("topk", "block_sparse"):
+        if gate is not None and not no_energy and mode in ("topk", "block_sparse", "threshold", "adaptive_threshold"):
             energy_host = energy.tolist()
         skipped = energy_host is not None and energy_host[0] < gate
         if skipped:
@@ -710,6 +757,17 @@ class STACRFunction(torch.autograd.Function):
         elif mode == "block_sparse":
             idx, values = select_block_sparse(x2d, coeff, basis_c, budget, chunk,
                                               int(config.get("residual_block_size", 16)))
+        elif mode == "threshold":  # every |r| above the configured value (stacr/adaptive.py:1574-1622)
+            idx, values = _select_above(x2d, coeff, basis_c, float(config["residual_threshold"]))
+        elif mode == "adaptive_threshold" and k_budget > 0:  # (stacr/adaptive.py:1628-1786)
+            thr = _sampled_threshold(x2d, coeff, basis_c, min(chunk, b_flat),
+                                     min(100000, max(10000, total // 10)), 1.0 - budget)
+            idx, values = _select_above(x2d, coeff, basis_c, thr)
+        elif streaming and k_budget > 0:  # streaming top-k (stacr/adaptive.py:1416-1517)
+            ratio = float(config.get("streaming_topk_sample_ratio", 0.1))
+            thr = _sampled_threshold(x2d, coeff, basis_c, min(chunk, b_flat),
+                                     min(100000, max(10000, int(total * ratio))), 1.0 - k_budget / total)
+            idx, values = _select_above(x2d, coeff, basis_c, thr)
 
         coeff_rec = None
         if config.get("quantize_coefficients", False):
@@ -756,6 +814,8 @@ class STACRFunction(torch.autograd.Function):
             res_scale = _scale_from_record(res_rec[0], codes[id(res_rec)]) if isinstance(res_rec, tuple) else res_rec
 
         if not recomputing:
+            if no_energy:
+                energy_host = [0.0] + list(energy_host[1:])
             _record_energy(layer_state, energy_host, rank, coeff.shape[0], schedule_step)
             if skipped:
                 layer_state["skipped_residuals"] = layer_state.get("skipped_residuals", 0) + 1

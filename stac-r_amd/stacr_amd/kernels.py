@@ -203,9 +203,11 @@ def select_sampled(x2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, budg
     return select_threshold(x2d, coeff, q, threshold, k_total)
 
 
-def select_threshold(x2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, threshold: torch.Tensor, cap: int):
+def select_threshold(x2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, threshold: torch.Tensor,
+                     cap: int | None):
     """The first ``cap`` flat positions with |r| >= threshold (an fp32 device scalar, compared in
-    the activation dtype), ascending, with their residual values."""
+    the activation dtype), ascending, with their residual values.  ``cap`` None selects every
+    passing position (a count-only call sizes the outputs first)."""
     x2d, coeff, q, rows, feats, rank, dt, ib = _factor_args(x2d, coeff, q)
     device = x2d.device
     L = _lib.load()
@@ -213,13 +215,21 @@ def select_threshold(x2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, th
     ws_bytes = ctypes.c_size_t()
     _lib.check(L.stacr_threshold_workspace_bytes(rows, feats, ctypes.byref(ws_bytes)), "stacr_threshold_workspace_bytes")
     ws = torch.empty(max(1, ws_bytes.value), dtype=torch.uint8, device=device)
+    count = torch.zeros((), dtype=torch.int64, device=device)
+
+    def call(c, idx, values):
+        _lib.check(L.stacr_select_threshold(_ptr(x2d), _ptr(coeff), _ptr(q), dt, rows, feats, rank, _ptr(threshold),
+                                            int(c), _ptr(idx), ib, _ptr(values), _ptr(count), _ptr(ws),
+                                            ws_bytes.value, _stream(device)), "stacr_select_threshold")
+        return int(count.item())
+
+    if cap is None:
+        cap = call(0, None, None)  # cap 0: the count of every passing entry, nothing written
+    if cap == 0:
+        return _index_tensor(0, ib, device), torch.empty(0, dtype=x2d.dtype, device=device)
     idx = _index_tensor(cap, ib, device)
     values = torch.empty(cap, dtype=x2d.dtype, device=device)
-    count = torch.zeros((), dtype=torch.int64, device=device)
-    _lib.check(L.stacr_select_threshold(_ptr(x2d), _ptr(coeff), _ptr(q), dt, rows, feats, rank, _ptr(threshold),
-                                        int(cap), _ptr(idx), ib, _ptr(values), _ptr(count), _ptr(ws),
-                                        ws_bytes.value, _stream(device)), "stacr_select_threshold")
-    n = int(count.item())
+    n = min(call(cap, idx, values), cap)
     if n < cap:
         idx, values = idx[:n].clone(), values[:n].clone()
     return idx, values

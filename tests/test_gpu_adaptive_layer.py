@@ -42,7 +42,7 @@ def _layer(dev, d_in, d_out, cfg, seed=21, dtype=torch.float32):
     return layer
 
 
-@pytest.mark.parametrize("mode", ["none", "topk", "block_sparse", "sparse_only"])
+@pytest.mark.parametrize("mode", ["none", "topk", "block_sparse", "sparse_only", "threshold", "adaptive_threshold"])
 def test_modes_preserve_forward_and_input_gradient(dev, mode):
     """Reference tests/test_adaptive.py:21-36."""
     announce("adaptive modes", mode)
@@ -59,11 +59,94 @@ def test_modes_preserve_forward_and_input_gradient(dev, mode):
     assert torch.isfinite(layer.linear.weight.grad).all()
 
 
-@pytest.mark.parametrize("mode", ["threshold", "adaptive_threshold"])
-def test_unbuilt_selectors_fail_loudly(dev, mode):
-    layer = _layer(dev, 16, 7, _cfg(rank=4, residual_mode=mode, residual_budget=0.2))
-    with pytest.raises(NotImplementedError):
-        layer(torch.randn(8, 16, device=dev))
+THRESHOLD_CASES = [("threshold", "f32"), ("threshold", "bf16"), ("adaptive_threshold", "bf16"),
+                   ("adaptive_threshold", "f32"), ("streaming_topk", "bf16"), ("streaming_topk", "f16")]
+
+
+@pytest.mark.parametrize("mode,dtype", THRESHOLD_CASES)
+def test_threshold_selections_match_oracle(dev, mode, dtype):
+    """residual_mode "threshold" (every |r| above residual_threshold), "adaptive_threshold" and
+    streaming top-k (a quantile of sampled |r|, then every |r| above it), stacr/adaptive.py:1416-1517,
+    1574-1622, 1628-1786: the saved indices and values bit-exact against the oracle on the kernel's
+    coefficients, with the sample positions redrawn by the same torch.randint calls under the same
+    seed and the quantile taken by torch as the reference takes it; then dW from the saved factors
+    against the fp64 oracle."""
+    from stacr_amd import adaptive as ad
+
+    announce("adaptive threshold selection", mode, dtype)
+    rows, d_in, d_out, r, budget = 2000, 384, 256, 8, 0.01
+    tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[dtype]
+    x = make_activation(rows, d_in, lognormal=True).to(dev, tdt)
+    basis = make_basis(d_in, r).to(dev)
+    lin = nn.Linear(d_in, d_out).to(dev).to(tdt)
+    kw = dict(rank=r, residual_budget=budget, quantize_coefficients=False, quantize_residuals=False, warmup_steps=0,
+              use_fused_kernel=False)
+    if mode == "streaming_topk":
+        kw.update(residual_mode="topk", streaming_topk=True, streaming_topk_sample_ratio=0.05)
+    else:
+        kw.update(residual_mode=mode, residual_threshold=6.0)
+    cfg = ad.STACRConfig(**kw).to_dict()
+    torch.manual_seed(77)
+    y = ad.STACRFunction.apply(x, lin.weight, lin.bias, basis, cfg, torch.zeros(1, dtype=torch.long),
+                               {"_schedule_step": 0})
+    saved = y.grad_fn.saved_tensors
+    coeff, values, idx = saved[0], saved[3], saved[4]  # (coefficients, weight, bias, values, indices)
+    used_basis = y.grad_fn.basis
+    resid = orc.residual_act(_np(x), _np(coeff), _np(used_basis), dtype)
+    total = rows * d_in
+    if mode == "threshold":
+        thr = 6.0
+    else:
+        # the reference's sampling: per 512-row chunk, torch.randint positions, then torch.quantile
+        torch.manual_seed(77)
+        if mode == "adaptive_threshold":
+            sample, quant = min(100000, max(10000, total // 10)), 1.0 - budget
+        else:
+            sample, quant = min(100000, max(10000, int(total * 0.05))), 1.0 - int(total * budget) / total
+        chunk = min(512, rows)
+        per = max(1, (sample * chunk) // rows)
+        pos = []
+        for s in range(0, rows, chunk):
+            n_el = (min(s + chunk, rows) - s) * d_in
+            pos.append(torch.randint(0, n_el, (min(per, n_el),), device=dev).cpu().numpy() + s * d_in)
+        samp = torch.from_numpy(np.abs(resid.reshape(-1)[np.concatenate(pos)])).to(dev).to(tdt)
+        thr_t = torch.quantile(samp.float(), quant).to(tdt) if tdt != torch.float32 else torch.quantile(samp, quant)
+        thr = float(thr_t)
+    oidx, oval = orc.adaptive_select_above(resid, thr, dtype)
+    assert idx.dtype == torch.int32 and values.dtype == tdt
+    got = idx.cpu().numpy().astype(np.int64)
+    orc.check_indices(got, total, ascending=True)
+    assert 0 < oidx.size < total
+    assert np.array_equal(got, oidx)
+    assert np.array_equal(_np(values), oval)
+    g = make_grad(rows, d_out).to(dev, tdt)
+    y.backward(g)
+    odw, _ = _oracle_dw(g, _np(coeff), used_basis, oidx, oval, d_in)
+    assert rel_l2(_np(lin.weight.grad), odw) <= (1e-5 if dtype == "f32" else 4e-3)
+
+
+def test_threshold_mode_keeps_an_empty_residual_and_adaptive_threshold_k0_has_none(dev):
+    """A threshold above every residual keeps an empty residual (the reference's empty tensors,
+    int16 indices for a small layer, quantized as its empty-input rule says); adaptive_threshold
+    with k = int(n * budget) = 0 keeps none and reports zero residual energy."""
+    from stacr_amd import adaptive as ad
+
+    x = torch.randn(8, 16, device=dev)
+    lin = nn.Linear(16, 7).to(dev)
+    basis = make_basis(16, 4).to(dev)
+    cfg = ad.STACRConfig(rank=4, residual_mode="threshold", residual_threshold=1e6, warmup_steps=0,
+                         quantize_coefficients=False, quantize_residuals=True).to_dict()
+    y = ad.STACRFunction.apply(x, lin.weight, lin.bias, basis, cfg, torch.zeros(1, dtype=torch.long),
+                               {"_schedule_step": 0})
+    saved = y.grad_fn.saved_tensors
+    assert saved[4].numel() == 0 and saved[4].dtype == torch.int16 and saved[3].numel() == 0
+    y.sum().backward()
+    assert torch.isfinite(lin.weight.grad).all()
+    state = {"_schedule_step": 0}
+    cfg = ad.STACRConfig(rank=4, residual_mode="adaptive_threshold", residual_budget=0.001, warmup_steps=0,
+                         quantize_coefficients=False).to_dict()
+    y = ad.STACRFunction.apply(x, lin.weight, lin.bias, basis, cfg, torch.zeros(1, dtype=torch.long), state)
+    assert len(y.grad_fn.saved_tensors) == 3 and state["last_residual_energy"] == 0.0
 
 
 def test_state_restores_runtime_controller_and_basis(dev):

@@ -119,14 +119,17 @@ def test_sampled_matches_oracle(name, rows, d, r, dtype, budget, ratio):
     assert idx.numel() <= k_total
 
 
-@pytest.mark.parametrize("thr,cap", [(0.0, 700), (0.0, 0), (1e30, 500), (float("nan"), 500), (0.7, 10 ** 6)])
+@pytest.mark.parametrize("thr,cap", [(0.0, 700), (0.0, 0), (1e30, 500), (float("nan"), 500), (0.7, 10 ** 6),
+                                     (0.7, None), (1e30, None)])
 def test_threshold_compaction_cap_and_empty(thr, cap):
+    """Capped, empty and uncapped selections; cap None is the count-only call (cap 0 at the C ABI),
+    then the selection sized by that count."""
     from stacr_amd import kernels
 
     dev = _dev()
     x, q, coeff, resid = _factors(40, 32, 4, "bf16", dev)
-    cap = min(cap, 40 * 32)
+    cap = min(cap, 40 * 32) if cap is not None else None
     idx, val = kernels.select_threshold(x, coeff, q, torch.tensor(thr), cap)
-    idx_ref, val_ref = orc.select_threshold(resid, thr, "bf16", cap)
+    idx_ref, val_ref = orc.select_threshold(resid, thr, "bf16", 40 * 32 if cap is None else cap)
     assert np.array_equal(idx.cpu().numpy().astype(np.int64), idx_ref)
     assert np.array_equal(val.float().cpu().numpy(), val_ref)

@@ -178,3 +178,30 @@ def test_energy_closed_forms():
     # C carrying all of X's energy: residual energy 0
     e, _, _, _ = orc.adaptive_energy(x, x, "f32")
     assert e == 0.0
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+def test_select_above_matches_torch_comparison(dtype):
+    """The threshold modes' selection against torch's own `abs() > threshold` + `nonzero` (the
+    reference's ops) on dtype-native values: thresholds equal to present magnitudes (strict, so
+    excluded), ones that round up or down to a present magnitude in the dtype, 0-dim tensors as
+    the sampled quantiles are, zero, and NaN residuals."""
+    tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[dtype]
+    rng = np.random.default_rng(5)
+    r = torch.from_numpy(rng.standard_normal(4096).astype(np.float32)).to(tdt)
+    r[::97] = 0.0
+    r[5] = float("nan")
+    r[11] = 0.1  # 0.1 rounded to the dtype: a threshold of 0.1 excludes it (strict after rounding)
+    resid = r.float().numpy()
+    present = float(r[40].abs())
+    thresholds = [0.1, present, np.nextafter(np.float32(present), np.float32(0)), 0.0, 1.0, 2.5, 1e-30,
+                  torch.tensor(present, dtype=tdt), torch.tensor(0.75, dtype=torch.float32)]
+    for t in thresholds:
+        expected = (r.abs() > t).nonzero().reshape(-1).numpy()
+        tv = float(t) if torch.is_tensor(t) else t
+        if torch.is_tensor(t) and t.dtype != tdt:
+            continue  # (the engine rounds 0-dim quantiles to the activation dtype before comparing)
+        idx, vals = orc.adaptive_select_above(resid, tv, dtype)
+        assert np.array_equal(idx, expected), (dtype, t)
+        assert np.array_equal(vals, resid[expected])
+    assert 11 not in orc.adaptive_select_above(resid, 0.1, dtype)[0]
