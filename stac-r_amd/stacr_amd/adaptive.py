@@ -21,6 +21,7 @@ import copy
 import ctypes
 import json
 import math
+import threading
 import warnings
 from dataclasses import asdict, dataclass
 from enum import Enum
@@ -409,7 +410,7 @@ class STACRConfig:
 
     Every residual_mode runs on the HIP kernels ("topk" and its streaming form, "threshold",
     "adaptive_threshold", "block_sparse" (the default), "none", "sparse_only", and the warmup
-    baseline); basis sharing raises NotImplementedError when a layer meets it.
+    baseline), with or without basis sharing between layers.
     """
 
     method: str = "stacr"
@@ -530,6 +531,55 @@ class STACRConfig:
         if isinstance(out["basis_dtype"], torch.dtype):
             out["basis_dtype"] = str(out["basis_dtype"])
         return out
+
+
+class BasisPool:
+    """The bases that the layers of a sharing group use when basis_sharing is on (the interface of
+    stacr/adaptive.py:271-381): one tensor per (group, in_features, rank), all zeros until a member
+    of the group fits it.  An update installs a new tensor rather than writing into the old one, so
+    a forward that took the previous basis keeps it for its backward and its recomputation."""
+
+    def __init__(self):
+        self._lock = threading.Lock()
+        self._bases: dict = {}
+
+    def get_or_create_basis(self, group_id: int, in_features: int, rank: int, device, dtype: torch.dtype):
+        key = (group_id, in_features, rank)
+        with self._lock:
+            basis = self._bases.get(key)
+            if basis is None:
+                basis = torch.zeros(in_features, rank, dtype=dtype, device=device)
+            elif basis.device != torch.device(device) or basis.dtype != dtype:
+                basis = basis.to(device=device, dtype=dtype)
+            self._bases[key] = basis
+            return basis
+
+    def update_basis(self, group_id: int, in_features: int, rank: int, new_basis: torch.Tensor) -> None:
+        fresh = new_basis.detach().clone()
+        with self._lock:
+            self._bases[(group_id, in_features, rank)] = fresh
+
+    def is_initialized(self, group_id: int, in_features: int, rank: int) -> bool:
+        """Whether a member has fitted the group's basis (it is no longer all zeros)."""
+        with self._lock:
+            basis = self._bases.get((group_id, in_features, rank))
+        return basis is not None and bool(basis.abs().sum().item() > 0)
+
+    def clear(self) -> None:
+        with self._lock:
+            self._bases.clear()
+
+
+_BASIS_POOL = BasisPool()
+
+
+def get_basis_pool() -> BasisPool:
+    """The process-wide pool of shared bases."""
+    return _BASIS_POOL
+
+
+_SHARING_GROUP = {"all": lambda i: 0, "every_2": lambda i: i // 2, "every_3": lambda i: i // 3,
+                  "every_4": lambda i: i // 4}
 
 
 def _is_int(value) -> bool:
@@ -1083,8 +1133,6 @@ class STACRLinear(nn.Module):
         super().__init__()
         self.in_features, self.out_features = int(in_features), int(out_features)
         self.config = config or STACRConfig()
-        if self.config.basis_sharing != "none":
-            raise NotImplementedError("basis_sharing is not built in this engine; use basis_sharing='none'")
         self.linear = nn.Linear(self.in_features, self.out_features, bias=bias)
         base = self.config.rank
         self.effective_rank = (self.config.get_layer_rank(layer_index, base, num_layers)
@@ -1092,8 +1140,26 @@ class STACRLinear(nn.Module):
         rank = min(self.effective_rank, self.in_features)
         self.basis_dtype = _resolve_basis_dtype(self.config.basis_dtype)
         self.layer_index, self.num_layers = layer_index, num_layers
+        # basis sharing (stacr/adaptive.py:2735-2792): the group from the explicit group or the layer
+        # index; the layer then keeps no basis of its own and reads and writes the pool's
         self.use_basis_sharing, self.basis_group_id = False, None
-        self.register_buffer("basis", torch.zeros(self.in_features, rank, dtype=self.basis_dtype))
+        sharing = self.config.basis_sharing
+        if sharing != "none":
+            if self.config.rank_mode != "fixed":
+                warnings.warn("basis_sharing only supports rank_mode='fixed'; disabling basis sharing "
+                              f"for rank_mode={self.config.rank_mode!r}.")
+            elif self.config.basis_sharing_group is not None:
+                self.use_basis_sharing, self.basis_group_id = True, self.config.basis_sharing_group
+            elif layer_index is None:
+                warnings.warn("basis_sharing enabled but layer_index not provided, disabling sharing")
+            elif sharing in _SHARING_GROUP:
+                self.use_basis_sharing, self.basis_group_id = True, _SHARING_GROUP[sharing](layer_index)
+            else:
+                warnings.warn(f"Unknown basis_sharing mode: {sharing}, using 'none'")
+        if self.use_basis_sharing:
+            self.basis = None
+        else:
+            self.register_buffer("basis", torch.zeros(self.in_features, rank, dtype=self.basis_dtype))
         self.register_buffer("_basis_initialized", torch.zeros(1, dtype=torch.bool), persistent=True)
         self.register_buffer("step_counter", torch.zeros(1, dtype=torch.long))
         self.register_buffer("_runtime_state", torch.empty(0, dtype=torch.uint8))
@@ -1154,6 +1220,8 @@ class STACRLinear(nn.Module):
             cfg["basis_dtype"] = str(cfg["basis_dtype"])
         blob = json.dumps({"layer_state": plain, "config": cfg, "effective_rank": self.effective_rank}).encode()
         self._runtime_state = torch.tensor(list(blob), dtype=torch.uint8, device=self.step_counter.device)
+        if self.use_basis_sharing and self.basis_initialized:
+            self._shared_basis_state = self.effective_basis.detach()
         super()._save_to_state_dict(destination, prefix, keep_vars)
 
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
@@ -1169,11 +1237,15 @@ class STACRLinear(nn.Module):
         else:
             state_dict[runtime_key] = self._runtime_state
         if shared_key in state_dict:
-            self._shared_basis_state = torch.empty_like(state_dict[shared_key], device=self.step_counter.device)
+            shared = state_dict[shared_key]
+            self._shared_basis_state = torch.empty_like(shared, device=self.step_counter.device)
+            if shared.numel() and self.use_basis_sharing:
+                get_basis_pool().update_basis(self.basis_group_id, self.in_features, shared.shape[1],
+                                              shared.to(self.linear.weight.device))
         else:
             state_dict[shared_key] = self._shared_basis_state
         stored = state_dict.get(prefix + "basis")
-        if stored is not None and stored.shape != self.basis.shape:
+        if stored is not None and self.basis is not None and stored.shape != self.basis.shape:
             self.basis = torch.empty_like(stored, device=self.basis.device)
         super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
                                       error_msgs)
@@ -1244,13 +1316,28 @@ class STACRLinear(nn.Module):
 
     @property
     def effective_basis(self) -> Optional[torch.Tensor]:
+        """The layer's basis, or with sharing its group's basis from the pool."""
+        if self.use_basis_sharing:
+            return get_basis_pool().get_or_create_basis(self.basis_group_id, self.in_features, self._basis_rank(),
+                                                        self.linear.weight.device, self.basis_dtype)
         return self.basis
 
+    def _basis_rank(self) -> int:
+        return self.basis.shape[1] if self.basis is not None else min(self.effective_rank, self.in_features)
+
     # ---------------------------------------------------------------- basis maintenance
+    def _set_basis(self, basis: torch.Tensor) -> None:
+        """Install `basis` as the layer's own, or with sharing as its group's."""
+        if self.use_basis_sharing:
+            get_basis_pool().update_basis(self.basis_group_id, self.in_features, basis.shape[1],
+                                          basis.to(device=self.linear.weight.device, dtype=self.basis_dtype))
+        else:
+            self.basis = basis.to(device=self.basis.device, dtype=self.basis.dtype)
+
     def _install_basis(self, basis: torch.Tensor) -> None:
-        self.basis = basis.to(device=self.basis.device, dtype=self.basis.dtype)
+        self._set_basis(basis)
         self.basis_initialized = True
-        allocated = self.basis.shape[1]
+        allocated = basis.shape[1]
         self.layer_state["allocated_rank"] = allocated
         self.layer_state["active_rank"] = min(self.layer_state.get("active_rank", allocated), allocated)
 
@@ -1263,7 +1350,7 @@ class STACRLinear(nn.Module):
         cfg = self.config
         with torch.no_grad(), torch.autocast(device_type=input_2d.device.type, enabled=False):
             rows, feats = input_2d.shape
-            target = self.basis.shape[1]
+            target = self._basis_rank()
             if cfg.rank_mode == "variance" and cfg.use_random_qr_init:
                 warnings.warn("rank_mode='variance' is incompatible with use_random_qr_init; "
                               "using configured rank for random-QR init.")
@@ -1320,11 +1407,12 @@ class STACRLinear(nn.Module):
             rows = input_2d.detach()
             if rows.dtype not in kernels.DTYPE_CODES:
                 rows = rows.float()
-            _, stepped = kernels.oja_step(rows, self.basis, float(lr))
+            current = self.effective_basis
+            _, stepped = kernels.oja_step(rows, current, float(lr))
             q, r = torch.linalg.qr(stepped)
             if cfg.use_mgs:  # Gram-Schmidt's factor has a positive diagonal: the same Q up to column signs
                 q = q * torch.sign(torch.diagonal(r)).where(torch.diagonal(r) != 0, torch.ones_like(q[0]))
-            self.basis = q[:, :self.basis.shape[1]].to(self.basis_dtype)
+            self._set_basis(q[:, :current.shape[1]].to(self.basis_dtype))
         st["basis_updates"] += 1
         st["last_oja_lr"] = lr
         if cfg.cache_basis_per_optimizer_step and self._get_accum_steps() > 1:
@@ -1351,6 +1439,9 @@ class STACRLinear(nn.Module):
         sparse_only = cfg.residual_mode == "sparse_only"
         guard = get_global_recomputation_guard()
         recomputing = guard.is_recomputing
+        if (not sparse_only and not self.basis_initialized and self.use_basis_sharing
+                and get_basis_pool().is_initialized(self.basis_group_id, self.in_features, self._basis_rank())):
+            self.basis_initialized = True  # another member of the group fitted the shared basis
         if not sparse_only and not self.basis_initialized and not recomputing:
             self._init_basis_from_batch(x.reshape(-1, self.in_features))
         step_tensor = self.step_counter
@@ -1360,7 +1451,7 @@ class STACRLinear(nn.Module):
         schedule_step = self._get_forward_schedule_step()
         st["_schedule_step"] = schedule_step
 
-        basis = None if sparse_only or not self.basis_initialized else self.basis
+        basis = None if sparse_only or not self.basis_initialized else self.effective_basis
         if basis is not None:
             allocated = basis.shape[1]
             st["allocated_rank"] = allocated

@@ -104,9 +104,37 @@ def test_apply_adaptive_validates_before_mutation():
     with pytest.raises(ValueError, match="No trainable"):
         apply_adaptive_stacr(model, surface="mlp")
     assert apply_adaptive_stacr(model, surface="mlp", allow_empty=True) == []
-    with pytest.raises(NotImplementedError):
-        apply_adaptive_stacr(model, target_names=["0"], basis_sharing="all", rank_mode="fixed")
     assert isinstance(model[0], nn.Linear)
+
+
+def test_basis_sharing_groups_and_pool():
+    """Sharing groups from the layer index (stacr/adaptive.py:2735-2792) and the pool's contract:
+    zero until fitted, replaced (not written into) by an update, keyed by (group, in_features, rank)."""
+    from stacr_amd.adaptive import STACRConfig, STACRLinear, get_basis_pool
+
+    pool = get_basis_pool()
+    pool.clear()
+    groups = {}
+    for mode, expect in (("all", [0, 0, 0, 0, 0]), ("every_2", [0, 0, 1, 1, 2]), ("every_3", [0, 0, 0, 1, 1]),
+                         ("every_4", [0, 0, 0, 0, 1])):
+        cfg = STACRConfig(rank=4, basis_sharing=mode, rank_mode="fixed")
+        layers = [STACRLinear(16, 7, cfg, layer_index=i) for i in range(5)]
+        assert [lyr.basis_group_id for lyr in layers] == expect and all(lyr.basis is None for lyr in layers)
+        groups[mode] = layers
+    explicit = STACRLinear(16, 7, STACRConfig(rank=4, basis_sharing="all", basis_sharing_group=9), layer_index=3)
+    assert explicit.basis_group_id == 9
+    with pytest.warns(UserWarning, match="layer_index not provided"):
+        alone = STACRLinear(16, 7, STACRConfig(rank=4, basis_sharing="all"))
+    assert not alone.use_basis_sharing and alone.basis is not None
+    a, b = groups["every_2"][0], groups["every_2"][1]
+    first = a.effective_basis
+    assert first is b.effective_basis and not pool.is_initialized(0, 16, 4) and not first.any()
+    fitted = torch.linalg.qr(torch.randn(16, 4))[0]
+    a._install_basis(fitted)
+    assert pool.is_initialized(0, 16, 4) and torch.equal(b.effective_basis, fitted)
+    assert not first.any()  # the tensor an earlier forward took is left as it was
+    assert not pool.is_initialized(1, 16, 4)
+    pool.clear()
 
 
 def test_runtime_state_and_set_step_reach_adaptive_layers():

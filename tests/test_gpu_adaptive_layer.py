@@ -510,3 +510,49 @@ def test_adaptive_default_block_sparse_layer_weight_gradient(dev):
     orc.check_indices(oidx, rows * d_in, ascending=True)
     odw, _ = _oracle_dw(g, _np(coeff), out.grad_fn.basis, oidx, _np(values), d_in)
     assert rel_l2(_np(layer.linear.weight.grad), odw) <= 1e-5
+
+
+def test_basis_sharing_layers_use_and_refresh_one_basis(dev):
+    """basis_sharing="every_2" (stacr/adaptive.py:2735-2792, 3100-3115, 3555-3580, 3368-3378): the
+    group's first layer fits the basis from its batch and the second uses that basis without
+    fitting its own; an Oja step by either layer replaces the group's basis for both; the basis
+    travels in _shared_basis_state through state_dict into an empty pool; and dW on the shared
+    basis matches the fp64 oracle on the saved factors."""
+    from stacr_amd.adaptive import STACRLinear, get_basis_pool
+
+    announce("adaptive basis sharing")
+    pool = get_basis_pool()
+    pool.clear()
+    rows, d_in, d_out = 512, 256, 128
+    cfg = _cfg(rank=8, basis_sharing="every_2", rank_mode="fixed", residual_mode="topk", residual_budget=0.01,
+               quantize_coefficients=False)
+    torch.manual_seed(3)
+    first = STACRLinear(d_in, d_out, cfg, layer_index=0).to(dev)
+    second = STACRLinear(d_in, d_out, cfg, layer_index=1).to(dev)
+    assert first.basis is None and second.basis is None and not pool.is_initialized(0, d_in, 8)
+    first(make_activation(rows, d_in).to(dev)).sum().backward()
+    assert pool.is_initialized(0, d_in, 8) and first.basis_initialized
+    before = second.effective_basis.clone()
+    x = make_activation(rows, d_in, seed=99).to(dev)
+    out = second(x)
+    assert torch.equal(out.grad_fn.basis, before)  # the group's basis, not a fit of its own batch
+    assert first.effective_basis is second.effective_basis
+    shared = first.effective_basis.clone()
+    second._update_basis_oja(x)
+    assert not torch.equal(first.effective_basis, shared)
+    assert first.effective_basis is second.effective_basis
+    state = first.state_dict()
+    assert torch.equal(state["_shared_basis_state"], first.effective_basis)
+    pool.clear()
+    fresh = STACRLinear(d_in, d_out, cfg, layer_index=1).to(dev)
+    fresh.load_state_dict(state)
+    assert torch.equal(fresh.effective_basis, state["_shared_basis_state"])
+    g = make_grad(rows, d_out).to(dev)
+    coeff, idx, values = _saved_factors(out, cfg, rows, d_in)
+    used = out.grad_fn.basis
+    out.backward(g)
+    oidx = idx.cpu().numpy().astype(np.int64)
+    orc.check_indices(oidx, rows * d_in, ascending=True)
+    odw, _ = _oracle_dw(g, _np(coeff), used, oidx, _np(values), d_in)
+    assert rel_l2(_np(second.linear.weight.grad), odw) <= 1e-5
+    pool.clear()
