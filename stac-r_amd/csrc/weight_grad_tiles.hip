@@ -245,6 +245,22 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         e_b1 = e_b1 < a.nnz ? e_b1 : a.nnz;
         e_b1 = e_b1 > e_b0 ? e_b1 : e_b0;
 
+        // kBatch entries per thread per round, loaded together: flat index and value.  A block whose
+        // entries fit one round loads them here, so their latency overlaps the column selection,
+        // and keeps them in registers for both passes below.
+        int64_t fl[kBatch];
+        float val[kBatch];
+        auto load_batch = [&](int64_t r0) {
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                const int64_t e = r0 + k * kThreads + tid;
+                fl[k] = e < e_b1 ? flat_at(a.idx, a.idx64, e) : -1;
+                val[k] = e < e_b1 ? entry_value(a, e) : 0.f;
+            }
+        };
+        const bool one_round = e_b1 - e_b0 <= (int64_t)kBatch * kThreads;
+        if (one_round) load_batch(e_b0);
+
         // ---- column features: the nc largest of the unique keys count << 16 | (65535 - f) (count
         // > 0).  Each wave sorts its 64 keys (descending, in registers); then four rounds merge the
         // sorted lists pairwise, each keeping the 64 largest of the pair, until one list remains:
@@ -293,17 +309,6 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         __syncthreads();
         const int64_t t_base = (int64_t)b * kTB;
         const uint32_t d_in = (uint32_t)a.d_in;
-        // kBatch entries per thread per round, loaded together: flat index and value
-        int64_t fl[kBatch];
-        float val[kBatch];
-        auto load_batch = [&](int64_t r0) {
-#pragma unroll
-            for (int k = 0; k < kBatch; ++k) {
-                const int64_t e = r0 + k * kThreads + tid;
-                fl[k] = e < e_b1 ? flat_at(a.idx, a.idx64, e) : -1;
-                val[k] = e < e_b1 ? entry_value(a, e) : 0.f;
-            }
-        };
         // (row in the block, feature in the part) of a loaded entry; false when it lies outside
         // the block (valid input has no such entry) or, with `in_part`, outside the part
         auto place = [&](int64_t flat, int &tl, int64_t &f) {
@@ -316,7 +321,7 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         };
         uint32_t before_part = 0;  // entries of this block in lower parts: where the part's records start
         for (int64_t r0 = e_b0; r0 < e_b1; r0 += kBatch * kThreads) {
-            load_batch(r0);
+            if (!one_round) load_batch(r0);
 #pragma unroll
             for (int k = 0; k < kBatch; ++k) {
                 int tl;
@@ -358,8 +363,7 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         s_key[tid] = tid < pw ? off : 0u;
         __syncthreads();
         // each light entry at its feature's offset + the feature's light entries in earlier rows
-        // (a block whose entries fit one round keeps them in registers from the first pass)
-        const bool one_round = e_b1 - e_b0 <= (int64_t)kBatch * kThreads;
+        // (a block whose entries fit one round has them in registers already)
         for (int64_t r0 = e_b0; r0 < e_b1; r0 += kBatch * kThreads) {
             if (!one_round) load_batch(r0);
 #pragma unroll
