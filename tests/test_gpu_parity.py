@@ -330,6 +330,7 @@ GRAD_CASES = [
     ("cfg2_turbo_bf16_full", 8192, 1280, 5120, 8, "bf16", False, 8, "chunk_topk", 0.0, False),
     ("cfg3_cfc_bf16_conv1d", 2048, 1024, 4096, 8, "bf16", True, 8, "global_topk", 0.005, False),
     ("fp32_bits0", 512, 256, 384, 4, "f32", False, 0, "chunk_topk", 0.02, False),
+    ("fp32_bits4_conv1d_rank5", 1100, 300, 160, 5, "f32", True, 4, "chunk_topk", 0.02, True),
     ("f16_bits4_rank3", 300, 40, 70, 3, "f16", False, 4, "chunk_topk", 0.1, False),
     ("fp32_lowrank_only", 256, 128, 96, 8, "f32", True, 8, "chunk_topk", 0.0, False),
     ("bf16_rank16", 1024, 2048, 512, 16, "bf16", False, 8, "chunk_topk", 0.005, False),
