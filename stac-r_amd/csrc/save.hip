@@ -2568,9 +2568,10 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     // padded basis; histograms and max key (contiguous in the layout) cleared in the same launch
     const int64_t n_zero = resid ? (int64_t)((off[WS_MAXKEY] + (size_t)p.g.hcopies * kMaxKeyStride * sizeof(uint32_t) -
                                               off[WS_HIST]) / sizeof(uint32_t)) : 0;
-    // the entry census (bf16 candidate passes without a trim, blocks of whole workgroups): its
-    // counts are cleared here and filled by the emission pass
-    const bool census = a.census && p.cand && !p.trim && kCensusRows % p.g.rows_per_wg == 0 && p.g.d <= kBins;
+    // the entry census (bf16 candidate passes without a trim, blocks of whole workgroups, rows not
+    // split into segments, d <= 2048): its counts are cleared here and filled by the emission pass
+    const bool census = a.census && (p.cand || p.cand_rin) && !p.trim && kCensusRows % p.g.rows_per_wg == 0 &&
+                        p.g.d == a.feats && p.g.d <= kBins;
     const int64_t n_census = census ? (int64_t)kCensusCopies * a.feats : 0;
     stacr_launch("k_prep", s, [&] {
         k_prep<DT><<<grid_for(hmax<int64_t>(hmax<int64_t>(a.feats * p.Rq, n_zero), n_census)), kBlock, 0, s>>>(
@@ -2700,11 +2701,13 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
                 stacr_launch("k_emit", s, [&] { k_emit_cand<R, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt); });
             if constexpr (kRin) {  // the lists of the level-1 pass; the fallback reads the stored residual
                 if (cand_rin && hc8)
-                    stacr_launch("k_emit", s, [&] { k_emit_cand<R, kHistCopies, true><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, nullptr, kt); });
+                    stacr_launch("k_emit", s, [&] { k_emit_cand<R, kHistCopies, true><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt); });
                 else if (cand_rin)
-                    stacr_launch("k_emit", s, [&] { k_emit_cand<R, 1, true><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, nullptr, kt); });
+                    stacr_launch("k_emit", s, [&] { k_emit_cand<R, 1, true><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt); });
             }
-            if (census && a.census_written) *a.census_written = 1;
+            // (written only by an emission that ran: candidate lists from X, or from the stored
+            // residual where this type and rank build that pass)
+            if (census && a.census_written && (cand || (kRin && cand_rin))) *a.census_written = 1;
         }
         if (!cand && !cand_rin && fast && hc8 && DT == STACR_DTYPE_BF16)
             stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V, kHistCopies, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs); });
