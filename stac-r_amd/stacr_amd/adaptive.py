@@ -676,6 +676,8 @@ def _select_above(x2d: torch.Tensor, coeff: torch.Tensor, basis: torch.Tensor, t
     t = torch.as_tensor(threshold, device="cpu").to(dt)  # the dtype rounding of the comparison
     index_dtype = _choose_index_dtype(x2d.numel())
     tv = float(t)
+    if tv == 0:
+        t = torch.zeros((), dtype=dt)  # -0 compares as +0: one ulp above it is the smallest subnormal
     if tv != tv or tv == math.inf:  # nothing compares above NaN or +inf
         return torch.empty(0, dtype=index_dtype, device=x2d.device), torch.empty(0, dtype=dt, device=x2d.device)
     if tv < 0:

@@ -125,6 +125,31 @@ def test_threshold_selections_match_oracle(dev, mode, dtype):
     assert rel_l2(_np(lin.weight.grad), odw) <= (1e-5 if dtype == "f32" else 4e-3)
 
 
+@pytest.mark.parametrize("thr", [0.0, -0.0])
+def test_threshold_mode_at_zero(dev, thr):
+    """residual_threshold 0 and -0 (the config accepts no negative value) keep every nonzero
+    residual, as torch's abs() > 0 does; rows of X in the basis's span (here zero rows) give exact
+    zeros, which stay out."""
+    from stacr_amd import adaptive as ad
+
+    rows, d_in, d_out = 256, 64, 32
+    x = make_activation(rows, d_in).to(dev)
+    x[::3] = 0.0
+    basis = make_basis(d_in, 4).to(dev)
+    lin = nn.Linear(d_in, d_out).to(dev)
+    cfg = ad.STACRConfig(rank=4, residual_mode="threshold", residual_threshold=thr, warmup_steps=0,
+                         quantize_coefficients=False, quantize_residuals=False).to_dict()
+    y = ad.STACRFunction.apply(x, lin.weight, lin.bias, basis, cfg, torch.zeros(1, dtype=torch.long),
+                               {"_schedule_step": 0})
+    saved = y.grad_fn.saved_tensors
+    coeff, values, idx = saved[0], saved[3], saved[4]
+    resid = orc.residual_act(_np(x), _np(coeff), _np(y.grad_fn.basis), "f32")
+    oidx, oval = orc.adaptive_select_above(resid, thr, "f32")
+    assert np.array_equal(idx.cpu().numpy().astype(np.int64), oidx)
+    assert np.array_equal(_np(values), oval)
+    assert 0 < oidx.size < rows * d_in
+
+
 def test_threshold_mode_keeps_an_empty_residual_and_adaptive_threshold_k0_has_none(dev):
     """A threshold above every residual keeps an empty residual (the reference's empty tensors,
     int16 indices for a small layer, quantized as its empty-input rule says); adaptive_threshold

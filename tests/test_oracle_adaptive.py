@@ -194,7 +194,7 @@ def test_select_above_matches_torch_comparison(dtype):
     r[11] = 0.1  # 0.1 rounded to the dtype: a threshold of 0.1 excludes it (strict after rounding)
     resid = r.float().numpy()
     present = float(r[40].abs())
-    thresholds = [0.1, present, np.nextafter(np.float32(present), np.float32(0)), 0.0, 1.0, 2.5, 1e-30,
+    thresholds = [0.1, present, np.nextafter(np.float32(present), np.float32(0)), 0.0, -0.0, -1.0, 1.0, 2.5, 1e-30,
                   torch.tensor(present, dtype=tdt), torch.tensor(0.75, dtype=torch.float32)]
     for t in thresholds:
         expected = (r.abs() > t).nonzero().reshape(-1).numpy()
