@@ -2072,12 +2072,15 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
     const uint32_t *__restrict__ maxkey, OutSpec o, float *scale_out, int to_list, const uint32_t *__restrict__ hist,
     const uint32_t *__restrict__ fold, int64_t fold_stride, const uint32_t *__restrict__ cand_idx,
     const uint16_t *__restrict__ cand_val, const CandMeta *__restrict__ meta, uint32_t *__restrict__ census,
-    uint32_t n_entries)
+    uint32_t n_entries, uint32_t census_feats)
 {
     constexpr int DT = STACR_DTYPE_BF16;
     __shared__ uint32_t s_off[kWaves];
     __shared__ uint32_t s_wt[kWaves];
-    __shared__ uint32_t s_feat[kBins];  // with a census: this workgroup's entries per feature (d <= 2048)
+    // with a census: this workgroup's entries per feature of the layer, two 16-bit counts a word
+    // (features f and f + 2048; a workgroup emits at most kCandCap entries, so no half overflows):
+    // census_feats <= 4096
+    __shared__ uint32_t s_feat[kBins];
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
     const int64_t w = blockIdx.x - chunk * g.wgs_per_chunk;
@@ -2122,9 +2125,13 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
     const float scale = o.bits ? quant_scale(mk, o.bits, amax) : 1.f;
     if (!to_list && blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
     if (!has_rows) return;  // uniform: a trailing workgroup with no rows writes nothing
-    const uint32_t dmask = (g.d & (g.d - 1)) == 0 ? (uint32_t)g.d - 1u : 0u;  // power-of-two widths: a mask
+    // the census counts features of the layer's rows (census_feats = segs x g.d when rows are split
+    // into segments of g.d features; segment rows run in flat order); power-of-two widths: a mask
+    const uint32_t cfeat = census_feats, segs = cfeat / (uint32_t)g.d;
+    const uint32_t dmask = (cfeat & (cfeat - 1)) == 0 ? cfeat - 1u : 0u;
+    const uint32_t cwords = cfeat < (uint32_t)kBins ? cfeat : (uint32_t)kBins;
     if (census)  // (cleared before the offset sums' barriers)
-        for (int f = threadIdx.x; f < g.d; f += kBlock) s_feat[f] = 0u;
+        for (uint32_t f = threadIdx.x; f < cwords; f += kBlock) s_feat[f] = 0u;
     // the workgroup's output offset and tie budget (the earlier workgroups' records)
     WgOffset wo;
     {
@@ -2149,7 +2156,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
         } else {
             write_entry<DT>(o, pos, fl, rv, scale);
         }
-        if (census) atomicAdd(&s_feat[dmask ? fl & dmask : fl % (uint32_t)g.d], 1u);
+        if (census) {
+            const uint32_t f = dmask ? fl & dmask : fl % cfeat;
+            atomicAdd(&s_feat[f & (kBins - 1)], f >= (uint32_t)kBins ? 0x10000u : 1u);
+        }
     };
     const bool valid = mine.count <= (uint32_t)kCandCap && mine.cut <= (T >> kDigitShift[0]);  // uniform
     if (valid) {
@@ -2177,13 +2187,16 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
     }
     if (census) {  // the entries per feature (copy w % 8) and, at a block's first row, its first entry
         __syncthreads();
-        const uint32_t d = (uint32_t)g.d;
-        uint32_t *counts = census + (int64_t)(blockIdx.x % kCensusCopies) * d;
-        for (uint32_t f = threadIdx.x; f < d; f += kBlock)
-            if (s_feat[f]) atomicAdd(&counts[f], s_feat[f]);
-        uint32_t *bstart = census + (int64_t)kCensusCopies * d;
-        if (threadIdx.x == 0 && row0 % kCensusRows == 0) bstart[row0 / kCensusRows] = wo.off;
-        if (blockIdx.x == 0 && threadIdx.x == 0) bstart[(g.rows + kCensusRows - 1) / kCensusRows] = n_entries;
+        uint32_t *counts = census + (int64_t)(blockIdx.x % kCensusCopies) * cfeat;
+        for (uint32_t f = threadIdx.x; f < cwords; f += kBlock) {
+            const uint32_t v = s_feat[f];
+            if (v & 0xffffu) atomicAdd(&counts[f], v & 0xffffu);
+            if (v >> 16) atomicAdd(&counts[f + kBins], v >> 16);
+        }
+        uint32_t *bstart = census + (int64_t)kCensusCopies * cfeat;
+        const int64_t seg_rows = (int64_t)kCensusRows * segs;  // a block of the layer's rows in segment rows
+        if (threadIdx.x == 0 && row0 % seg_rows == 0) bstart[row0 / seg_rows] = wo.off;
+        if (blockIdx.x == 0 && threadIdx.x == 0) bstart[(g.rows / segs + kCensusRows - 1) / kCensusRows] = n_entries;
     }
 }
 
@@ -2568,10 +2581,13 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     // padded basis; histograms and max key (contiguous in the layout) cleared in the same launch
     const int64_t n_zero = resid ? (int64_t)((off[WS_MAXKEY] + (size_t)p.g.hcopies * kMaxKeyStride * sizeof(uint32_t) -
                                               off[WS_HIST]) / sizeof(uint32_t)) : 0;
-    // the entry census (bf16 candidate passes without a trim, blocks of whole workgroups, rows not
-    // split into segments, d <= 2048): its counts are cleared here and filled by the emission pass
-    const bool census = a.census && (p.cand || p.cand_rin) && !p.trim && kCensusRows % p.g.rows_per_wg == 0 &&
-                        p.g.d == a.feats && p.g.d <= kBins;
+    // the entry census (bf16 candidate passes without a trim, blocks of whole workgroups): its
+    // counts are cleared here and filled by the emission pass.  Lists from X: rows of <= 2048
+    // features; lists from the stored residual: also rows split into segments (<= 4096 features)
+    const int64_t csegs = p.g.d > 0 && a.feats % p.g.d == 0 ? a.feats / p.g.d : 0;
+    const bool census = a.census && (p.cand || p.cand_rin) && !p.trim && csegs >= 1 &&
+                        (kCensusRows * csegs) % p.g.rows_per_wg == 0 && p.g.rows % csegs == 0 &&
+                        (csegs == 1 ? a.feats <= kBins : p.cand_rin && !p.cand && a.feats <= 2 * kBins);
     const int64_t n_census = census ? (int64_t)kCensusCopies * a.feats : 0;
     stacr_launch("k_prep", s, [&] {
         k_prep<DT><<<grid_for(hmax<int64_t>(hmax<int64_t>(a.feats * p.Rq, n_zero), n_census)), kBlock, 0, s>>>(
@@ -2696,14 +2712,14 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
             uint32_t *cen = census ? a.census : nullptr;
             const uint32_t kt = (uint32_t)a.k_sum;  // the entries emitted (no trim: the chunks' k summed)
             if (cand && hc8)
-                stacr_launch("k_emit", s, [&] { k_emit_cand<R, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt); });
+                stacr_launch("k_emit", s, [&] { k_emit_cand<R, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt, (uint32_t)a.feats); });
             else if (cand)
-                stacr_launch("k_emit", s, [&] { k_emit_cand<R, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt); });
+                stacr_launch("k_emit", s, [&] { k_emit_cand<R, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt, (uint32_t)a.feats); });
             if constexpr (kRin) {  // the lists of the level-1 pass; the fallback reads the stored residual
                 if (cand_rin && hc8)
-                    stacr_launch("k_emit", s, [&] { k_emit_cand<R, kHistCopies, true><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt); });
+                    stacr_launch("k_emit", s, [&] { k_emit_cand<R, kHistCopies, true><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt, (uint32_t)a.feats); });
                 else if (cand_rin)
-                    stacr_launch("k_emit", s, [&] { k_emit_cand<R, 1, true><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt); });
+                    stacr_launch("k_emit", s, [&] { k_emit_cand<R, 1, true><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt, (uint32_t)a.feats); });
             }
             // (written only by an emission that ran: candidate lists from X, or from the stored
             // residual where this type and rank build that pass)

@@ -742,7 +742,7 @@ def test_turbo_step_50_freezes_basis_and_drops_residual(dev, full):
 
 @pytest.mark.parametrize("rows,d_in,d_out,mode,budget,chunk,dtype,expect", [
     (8192, 1024, 4096, "global_topk", 0.005, 512, "bf16", True),    # the north-star layer
-    (8192, 4096, 1024, "global_topk", 0.005, 512, "bf16", False),   # cfg 3 c_proj: rows split in two, no census
+    (8192, 4096, 1024, "global_topk", 0.005, 512, "bf16", True),    # cfg 3 c_proj: rows split into two segments
     (2048, 1024, 512, "global_topk", 0.02, 512, "bf16", True),      # quota past the list: lists from the stored residual
     (2048, 1024, 512, "chunk_topk", 0.01, 256, "bf16", True),
     (64, 1024, 256, "chunk_topk", 0.0001, 1, "bf16", False),         # one entry a row, trimmed to 7: no census
