@@ -168,7 +168,9 @@ def _rel(a, b) -> float:
 
 
 def check_layer(outs, ref):
-    """Save outputs are deterministic (bit-equal); dW sums the sparse term in arrival order."""
+    """Every output of a replay equals the eager result bit for bit: the save is deterministic,
+    and every timed workload's dW runs on the matrix-core tiles kernels, whose sums have a fixed
+    order (a replay reading a stale plan or census would show here)."""
     import torch
 
     for name, a, b in zip(("coeff", "idx", "data", "scale"), outs[:4], ref[:4]):
@@ -179,8 +181,9 @@ def check_layer(outs, ref):
                 first = int(diff.nonzero()[0].item()) if diff.any() else -1
                 detail = f": {int(diff.sum().item())} of {diff.numel()} elements, first at {first}"
             raise RuntimeError(f"graph replay of the save differs from the eager result in {name}{detail}")
-    if _rel(outs[4], ref[4]) > 1e-3:
-        raise RuntimeError("graph replay of the weight gradient differs from the eager result")
+    if not torch.equal(outs[4], ref[4]):
+        raise RuntimeError(f"graph replay of the weight gradient differs from the eager result "
+                           f"(rel-L2 {_rel(outs[4], ref[4]):.3g})")
 
 
 def kernel_breakdown(step, reps: int = 10) -> dict:
@@ -364,7 +367,7 @@ def main() -> int:
             for name, (tot, cnt) in timer.results.items()}
     dominant = max(kern, key=lambda n: kern[n]["per_step_us"])
     ab = algorithmic_bytes(N, D_IN, D_OUT, RANK, k_saved)
-    per_kernel_bytes = {"k_dw_fused": ab["bwd"]}
+    per_kernel_bytes = {"k_tile_grad": ab["bwd"]}
     dom_bytes = per_kernel_bytes.get(dominant)
     avg_s = kern[dominant]["avg_us"] * 1e-6
     achieved = dom_bytes / avg_s / 1e9 if dom_bytes else None

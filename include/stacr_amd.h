@@ -164,12 +164,14 @@ int stacr_weight_grad(const void *g, int dtype, int64_t rows, int64_t d_out, con
                       void *workspace, size_t workspace_bytes, void *stream);
 /* stacr_weight_grad with the census a stacr_save_census call wrote for these entries (same rows,
  * d_in and residual): the matrix-core path takes the counts and block starts from it instead of
- * counting (one launch fewer); the other paths ignore it.  Same results as stacr_weight_grad. */
+ * counting (one launch fewer); the other paths ignore it.  Same results as stacr_weight_grad.
+ * census_bytes is the census buffer's size; a buffer smaller than stacr_save_census_bytes(rows,
+ * d_in) is refused with STACR_ERR_INVALID (a census of another problem would be read past its end). */
 int stacr_weight_grad_census(const void *g, int dtype, int64_t rows, int64_t d_out, const void *coeff, const void *q,
                              int64_t d_in, int rank, const void *idx, int index_bytes, const void *data,
                              const float *scale, int bits, int val_dtype, int64_t nnz, int transposed, void *dw,
-                             int dw_dtype, void *dbias, int dbias_dtype, const void *census, void *workspace,
-                             size_t workspace_bytes, void *stream);
+                             int dw_dtype, void *dbias, int dbias_dtype, const void *census, size_t census_bytes,
+                             void *workspace, size_t workspace_bytes, void *stream);
 
 /*
  * Allocation-free weight gradient.  No counterpart in the reference: it is for callers that cannot

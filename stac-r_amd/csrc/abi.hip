@@ -316,10 +316,15 @@ int stacr_weight_grad(const void *g, int dtype, int64_t rows, int64_t d_out, con
 int stacr_weight_grad_census(const void *g, int dtype, int64_t rows, int64_t d_out, const void *coeff, const void *q,
                              int64_t d_in, int rank, const void *idx, int index_bytes, const void *data,
                              const float *scale, int bits, int val_dtype, int64_t nnz, int transposed, void *dw,
-                             int dw_dtype, void *dbias, int dbias_dtype, const void *census, void *workspace,
-                             size_t workspace_bytes, void *stream)
+                             int dw_dtype, void *dbias, int dbias_dtype, const void *census, size_t census_bytes,
+                             void *workspace, size_t workspace_bytes, void *stream)
 {
     if (!census) return stacr_fail(STACR_ERR_INVALID, "stacr_weight_grad_census: census is NULL");
+    if (rows < 0 || d_in < 1) return stacr_fail(STACR_ERR_INVALID, "stacr_weight_grad_census: bad shape");
+    const size_t need = (size_t)census_words(rows, d_in) * 4;
+    if (census_bytes < need)
+        return stacr_fail(STACR_ERR_INVALID, "stacr_weight_grad_census: census has %zu bytes, this problem's needs %zu",
+                          census_bytes, need);
     return grad_impl(g, dtype, rows, d_out, coeff, q, d_in, rank, idx, index_bytes, data, scale, bits, val_dtype, nnz,
                      transposed, dw, dw_dtype, dbias, dbias_dtype, workspace, workspace_bytes, stream, census);
 }
@@ -705,7 +710,7 @@ int stacr_adaptive_select_block_sparse(const void *x, const void *coeff, const v
     if (index_bytes != p.index_bytes)
         return stacr_fail(STACR_ERR_INVALID, "stacr_adaptive_select_block_sparse: index_bytes must be %d", p.index_bytes);
     if (!count) return stacr_fail(STACR_ERR_INVALID, "stacr_adaptive_select_block_sparse: NULL count");
-    if (!p.k_blocks) return stacr_hip_check(hipMemsetAsync(count, 0, 8, static_cast<hipStream_t>(stream)), "count");
+    if (!p.k_blocks) return stacr_fill_int_launch(count, 8, 1, 0, static_cast<hipStream_t>(stream));
     if (!idx || !values || !workspace)
         return stacr_fail(STACR_ERR_INVALID, "stacr_adaptive_select_block_sparse: NULL pointer argument");
     const size_t need = stacr_adaptive_block_ws(rows, feats, block_size, p.n_cand, p.k_blocks);

@@ -366,6 +366,12 @@ int stacr_aq_quantize_launch(const void *v, int dtype, int64_t n, int bits, void
     return stacr_hip_check(hipGetLastError(), "adaptive quantizer");
 }
 
+int stacr_fill_int_launch(void *p, int bytes, int64_t n, int64_t v, hipStream_t s)
+{
+    if (n > 0) stacr_launch("k_fill_int", s, [&] { k_fill_int<<<blocks_for(n), kBlock, 0, s>>>(p, bytes, n, v); });
+    return stacr_hip_check(hipGetLastError(), "fill");
+}
+
 int stacr_aq_dequantize_launch(const void *data, int bits, const void *scale, int64_t n, void *out, int out_dt,
                                hipStream_t s)
 {

@@ -329,6 +329,9 @@ size_t stacr_tiles_ws_bound(int64_t rows, int64_t d_out, int64_t d_in, int64_t n
 int stacr_tiles_launch(const StacrGradArgs &a);
 
 // ------------------------------------------------------------------ launchers (adaptive.hip)
+// n integers of `bytes` bytes at p set to v by a kernel (no hipMemsetAsync: the callers' launches may
+// be captured into a HIP graph)
+int stacr_fill_int_launch(void *p, int bytes, int64_t n, int64_t v, hipStream_t s);
 int stacr_aq_quantize_launch(const void *v, int dtype, int64_t n, int bits, void *data, void *scale, void *ws,
                              hipStream_t s);
 int stacr_aq_dequantize_launch(const void *data, int bits, const void *scale, int64_t n, void *out, int out_dt,

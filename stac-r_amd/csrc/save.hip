@@ -2543,7 +2543,7 @@ int launch_wide_pass1(const StacrSaveArgs &a, const Plan &p, const typename Act<
         constexpr int R = decltype(r)::value, MV = decltype(mv)::value, NT = decltype(nt)::value;
         if (done || p.Rq != R || p.mvw != MV || p.ntw != NT) return;
         done = true;
-        stacr_launch("k_proj_hist", s, [&] {
+        stacr_launch("k_proj_hist_w", s, [&] {
             k_proj_hist_w<DT, R, MV, NT><<<n, NT, 0, s>>>(p.gw, c_vec, x, qp, coeff, hist, maxkey, do_hist, coeff_in, rout, coarse);
         });
     };
@@ -2628,9 +2628,9 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
                 }
             } else if (fast && cand) {
                 if constexpr (kCandOk)
-                    stacr_launch("k_proj_hist", s, [&] { k_proj_cand<R><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff_out, hist, maxkey, coeff_in, coarse, p.quota, cidx, cval, cmeta); });
+                    stacr_launch("k_proj_cand", s, [&] { k_proj_cand<R><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff_out, hist, maxkey, coeff_in, coarse, p.quota, cidx, cval, cmeta); });
             } else if (fast) {
-                stacr_launch("k_proj_hist", s, [&] { k_proj_hist_b<DT, R, V, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in, rbuf, coarse); });
+                stacr_launch("k_proj_hist_b", s, [&] { k_proj_hist_b<DT, R, V, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff_out, hist, maxkey, resid ? 1 : 0, coeff_in, rbuf, coarse); });
             }
         }
         if (!fast)
@@ -2647,7 +2647,7 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
         if constexpr (kFastOk) {
             if (fast) {
                 auto refine = [&](auto hc, auto level) {
-                    stacr_launch("k_refine_hist", s, [&] {
+                    stacr_launch("k_refine_hist_b", s, [&] {
                         k_refine_hist_b<DT, R, V, decltype(hc)::value, kRin, decltype(level)::value><<<nwg, kBlock, 0, s>>>(
                             p.g, fg, xin, qp, coeff, hist, state, kf, kl, maxkey, fold, p.n_wgs, coarse);
                     });
@@ -2658,14 +2658,14 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
                 using H1 = std::integral_constant<int, 1>;
                 auto refine_cand = [&](auto hc) {
                     if constexpr (kCandOk)
-                        stacr_launch("k_refine_hist", s, [&] {
+                        stacr_launch("k_refine_cand", s, [&] {
                             k_refine_cand<R, decltype(hc)::value><<<nwg, kBlock, 0, s>>>(
                                 p.g, fg, x, qp, coeff, hist, state, kf, kl, maxkey, fold, p.n_wgs, coarse, cval, cmeta);
                         });
                 };
                 auto refine_lists = [&](auto hc) {
                     if constexpr (kCandOk && kRin)
-                        stacr_launch("k_refine_hist", s, [&] {
+                        stacr_launch("k_refine_hist_b", s, [&] {
                             k_refine_hist_b<DT, R, V, decltype(hc)::value, true, 1, true><<<nwg, kBlock, 0, s>>>(
                                 p.g, fg, xin, qp, coeff, hist, state, kf, kl, maxkey, fold, p.n_wgs, coarse, cidx, cval,
                                 cmeta);
@@ -2690,9 +2690,9 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     }
     if constexpr (kFastOk) {
         if (fast && hc8 && !p.fold)
-            stacr_launch("k_count", s, [&] { k_count_b<DT, R, V, kHistCopies, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, hist, state, counts, kf, kl); });
+            stacr_launch("k_count_b", s, [&] { k_count_b<DT, R, V, kHistCopies, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, hist, state, counts, kf, kl); });
         if (fast && !hc8 && !p.fold)
-            stacr_launch("k_count", s, [&] { k_count_b<DT, R, V, 1, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, hist, state, counts, kf, kl); });
+            stacr_launch("k_count_b", s, [&] { k_count_b<DT, R, V, 1, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, hist, state, counts, kf, kl); });
     }
     if (!fast) stacr_launch("k_count", s, [&] { k_count<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, hist, state, counts, kf, kl); });
 
@@ -2712,23 +2712,23 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
             uint32_t *cen = census ? a.census : nullptr;
             const uint32_t kt = (uint32_t)a.k_sum;  // the entries emitted (no trim: the chunks' k summed)
             if (cand && hc8)
-                stacr_launch("k_emit", s, [&] { k_emit_cand<R, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt, (uint32_t)a.feats); });
+                stacr_launch("k_emit_cand", s, [&] { k_emit_cand<R, kHistCopies><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt, (uint32_t)a.feats); });
             else if (cand)
-                stacr_launch("k_emit", s, [&] { k_emit_cand<R, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt, (uint32_t)a.feats); });
+                stacr_launch("k_emit_cand", s, [&] { k_emit_cand<R, 1><<<nwg, kBlock, 0, s>>>(p.g, fg, x, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt, (uint32_t)a.feats); });
             if constexpr (kRin) {  // the lists of the level-1 pass; the fallback reads the stored residual
                 if (cand_rin && hc8)
-                    stacr_launch("k_emit", s, [&] { k_emit_cand<R, kHistCopies, true><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt, (uint32_t)a.feats); });
+                    stacr_launch("k_emit_cand", s, [&] { k_emit_cand<R, kHistCopies, true><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt, (uint32_t)a.feats); });
                 else if (cand_rin)
-                    stacr_launch("k_emit", s, [&] { k_emit_cand<R, 1, true><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt, (uint32_t)a.feats); });
+                    stacr_launch("k_emit_cand", s, [&] { k_emit_cand<R, 1, true><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs, cidx, cval, cmeta, cen, kt, (uint32_t)a.feats); });
             }
             // (written only by an emission that ran: candidate lists from X, or from the stored
             // residual where this type and rank build that pass)
             if (census && a.census_written && (cand || (kRin && cand_rin))) *a.census_written = 1;
         }
         if (!cand && !cand_rin && fast && hc8 && DT == STACR_DTYPE_BF16)
-            stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V, kHistCopies, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs); });
+            stacr_launch("k_emit_b", s, [&] { k_emit_b<DT, R, V, kHistCopies, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs); });
         else if (!cand && !cand_rin && fast)
-            stacr_launch("k_emit", s, [&] { k_emit_b<DT, R, V, 1, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs); });
+            stacr_launch("k_emit_b", s, [&] { k_emit_b<DT, R, V, 1, kRin><<<nwg, kBlock, 0, s>>>(p.g, fg, xin, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0, hist, fold, p.n_wgs); });
     }
     if (!fast) stacr_launch("k_emit", s, [&] { k_emit<DT, R, V, QREG><<<nwg, kBlock, 0, s>>>(p.g, x, qp, coeff, state, counts, kf, maxkey, o, a.scale, p.trim ? 1 : 0); });
 

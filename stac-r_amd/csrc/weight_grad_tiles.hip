@@ -961,7 +961,7 @@ size_t tile_layout(int64_t nnz, int64_t d_in, const TileGeom &g, size_t *off)
 template <int DT, bool SP, bool BT8>
 int launch_tile_grad(const TileArgs &t, int nwg, hipStream_t s)
 {
-    stacr_launch("k_dw_fused", s, [&] { k_tile_grad<DT, SP, BT8><<<nwg, kThreads, 0, s>>>(t); });
+    stacr_launch("k_tile_grad", s, [&] { k_tile_grad<DT, SP, BT8><<<nwg, kThreads, 0, s>>>(t); });
     return stacr_hip_check(hipGetLastError(), "weight_grad matrix-core kernel");
 }
 
@@ -1056,13 +1056,13 @@ int stacr_tiles_launch(const StacrGradArgs &a)
     hipStream_t s = a.stream;
     int rc;
     if (g.sparse && !census) {
-        stacr_launch("k_dw_count", s, [&] { k_tile_count<<<kChunks, kThreads, 0, s>>>(t); });
+        stacr_launch("k_tile_count", s, [&] { k_tile_count<<<kChunks, kThreads, 0, s>>>(t); });
         rc = stacr_hip_check(hipGetLastError(), "weight_grad entry count");
         if (rc) return rc;
     }
     const dim3 pgrid((unsigned)g.n_blocks, g.sparse ? (unsigned)g.n_parts + 1u : 1u);
-    if (g.bt8) stacr_launch("k_dw_plan", s, [&] { k_tile_plan<true><<<pgrid, kThreads, 0, s>>>(t); });
-    else stacr_launch("k_dw_plan", s, [&] { k_tile_plan<false><<<pgrid, kThreads, 0, s>>>(t); });
+    if (g.bt8) stacr_launch("k_tile_plan", s, [&] { k_tile_plan<true><<<pgrid, kThreads, 0, s>>>(t); });
+    else stacr_launch("k_tile_plan", s, [&] { k_tile_plan<false><<<pgrid, kThreads, 0, s>>>(t); });
     rc = stacr_hip_check(hipGetLastError(), "weight_grad plan");
     if (rc) return rc;
     const int nwg = (int)(a.d_out / kOS) * g.n_parts;

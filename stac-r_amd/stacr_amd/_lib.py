@@ -46,7 +46,7 @@ SIGNATURES = {
     "stacr_weight_grad": ([_p, _i32, _i64, _i64, _p, _p, _i64, _i32, _p, _i32, _p, _p, _i32, _i32, _i64, _i32, _p,
                            _i32, _p, _i32, _p, _sz, _p], _i32),
     "stacr_weight_grad_census": ([_p, _i32, _i64, _i64, _p, _p, _i64, _i32, _p, _i32, _p, _p, _i32, _i32, _i64, _i32,
-                                  _p, _i32, _p, _i32, _p, _p, _sz, _p], _i32),
+                                  _p, _i32, _p, _i32, _p, _sz, _p, _sz, _p], _i32),
     "stacr_weight_grad_noalloc": ([_p, _i32, _i64, _i64, _p, _p, _i64, _i32, _p, _i32, _p, _p, _i32, _i32, _i64, _i32,
                                    _p, _i32, _p, _i32, _p], _i32),
     "stacr_adaptive_residual_plan": ([_i64, _i64, _f64, _i64, _P64, _P64, _PI32], _i32),

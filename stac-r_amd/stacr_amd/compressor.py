@@ -1,14 +1,22 @@
-"""Saved-tensor compressor: the storage-only path (interface of stacr/compressor.py:13-140).
+"""Saved-tensor compressor: the storage-only path (interface of stacr/compressor.py:13-140 and
+stacr/residual.py:8-33).
 
 ``stacr_saved_tensors(STACRCompressor(...))`` installs PyTorch saved-tensor hooks.  ``pack``
-replaces an eligible saved activation X (floating point, >= 2 dims, not a parameter or a view of
-one, wide and large enough) by its rank-r coefficients C = X Q, the shared basis Q and the
-top-k residual entries of X - rnd(C Q^T) over the whole tensor; ``unpack`` hands autograd the
-dense tensor rnd(C Q^T) + residual.  Both run in the HIP kernels: the save kernels (projection,
-residual and exact global top-k in one call, stacr/compressor.py:108-119 and
-stacr/residual.py:23-33) and the reconstruction kernels (stacr/compressor.py:127-133,
-stacr/residual.py:13-20).  The basis per (feature size, device) is an OjaBasis whose update is
-the HIP Oja step.  Tensors must be ROCm GPU tensors in fp32, bf16 or fp16; anything else raises.
+replaces an eligible saved activation X by its factors: rank-r coefficients C = X Q on a basis
+kept per (feature size, device), and the top-k entries of the residual X - rnd(C Q^T) over the
+whole tensor; ``unpack`` hands autograd the dense tensor rnd(C Q^T) + residual.
+
+How the pieces are arranged here:
+* eligibility is a table of named gates (`_GATES`); `skip_reason` names the first one a tensor
+  fails, `should_compress` is "no gate failed";
+* the compressor's schedule is a phase computed from the step (`"warmup"`: pass everything
+  through, `"turbo"`: coefficients only, `"full"`: coefficients and residual);
+* bases live in a `_BasisBank` that creates an `OjaBasis` on first use and steps it on the update
+  interval (the step itself is the HIP Oja kernel);
+* a pack is one library call: the save kernels project, form the residual and take the exact
+  global top-k in the same call (chunk = the whole tensor, values kept in the activation dtype);
+  the unpack is the reconstruction kernel (stacr_reconstruct).
+Tensors must be ROCm GPU tensors in fp32, bf16 or fp16; anything else raises.
 
 As in the reference this path rebuilds a dense activation in backward; the factor-native layer
 (STACRLinear via apply_stacr) is the measured method.
@@ -17,7 +25,7 @@ from __future__ import annotations
 
 from contextlib import contextmanager
 from dataclasses import dataclass
-from typing import Any
+from typing import Any, Callable
 
 import torch
 
@@ -27,8 +35,8 @@ from .oja import OjaBasis
 
 @dataclass
 class STACRConfig:
-    """Options of the saved-tensor compressor (stacr/compressor.py:13-25); apply_stacr also takes
-    it (a dataclass config is used as given)."""
+    """Options of the saved-tensor compressor (field names and defaults of stacr/compressor.py:13-25);
+    apply_stacr also takes it (a dataclass config is used as given)."""
 
     rank: int = 8
     residual_budget: float = 0.005
@@ -45,18 +53,31 @@ class STACRConfig:
 
 @dataclass
 class SparseResidual:
-    """Flat indices into a tensor of `shape` and the values kept there (stacr/residual.py:8-20)."""
+    """Entries kept from a residual of `shape`: flat (row-major) indices and their values
+    (stacr/residual.py:8-20)."""
 
     shape: tuple[int, ...]
     indices: torch.Tensor
     values: torch.Tensor
 
+    @property
+    def numel(self) -> int:
+        n = 1
+        for s in self.shape:
+            n *= int(s)
+        return n
+
     def dense(self, *, device: torch.device, dtype: torch.dtype) -> torch.Tensor:
-        out = torch.zeros(self.shape, device=device, dtype=dtype)
-        if self.indices.numel() > 0:
-            out.view(-1)[self.indices.to(device=device, dtype=torch.long)] = self.values.to(device=device,
-                                                                                            dtype=dtype)
-        return out
+        """A zero tensor of `shape` holding the values at their flat indices."""
+        flat = torch.zeros(self.numel, device=device, dtype=dtype)
+        if self.indices.numel():
+            flat.scatter_(0, self.indices.to(device=device, dtype=torch.long), self.values.to(device=device, dtype=dtype))
+        return flat.view(self.shape)
+
+    @classmethod
+    def empty(cls, shape, device, dtype) -> "SparseResidual":
+        return cls(tuple(shape), torch.zeros(0, device=device, dtype=torch.long),
+                   torch.zeros(0, device=device, dtype=dtype))
 
 
 @dataclass
@@ -68,42 +89,96 @@ class PackedActivation:
     residual: SparseResidual | None
 
 
-def _topk_budget(numel: int, budget: float) -> float:
-    """The budget whose global k is the reference's max(1, min(n, round(budget n)))
-    (stacr/residual.py:30); the kernels' global k is round(budget n)."""
-    if numel > 0 and round(float(budget) * numel) < 1:
-        return 1.0 / numel
-    return float(budget)
+def _reference_k_budget(numel: int, budget: float) -> float:
+    """The budget whose global k under the kernels' rule round(budget n) is the reference's
+    max(1, min(n, round(budget n))) (stacr/residual.py:30): only the round-to-zero case differs."""
+    budget = float(budget)
+    return 1.0 / numel if numel and round(budget * numel) == 0 else budget
 
 
-def _empty_residual(shape, device, dtype) -> SparseResidual:
-    return SparseResidual(tuple(shape), torch.empty(0, device=device, dtype=torch.long),
-                          torch.empty(0, device=device, dtype=dtype))
+def _as_rows(t: torch.Tensor) -> torch.Tensor:
+    return t.reshape(1, 1) if t.dim() == 0 else t.reshape(-1, t.shape[-1])
+
+
+def _global_topk(rows: torch.Tensor, basis: torch.Tensor, budget: float):
+    """(coeff, flat indices int64, values) of one save call: the projection on `basis` and the
+    exact top-k of the residual over every element (budget 0: coefficients only)."""
+    coeff, idx, values, _ = kernels.save(rows, basis, mode="global_topk", budget=budget, chunk_rows=rows.shape[0],
+                                         bits=0)
+    if idx is None:
+        return coeff, None, None
+    return coeff, idx.to(torch.long), values
 
 
 def select_topk_residual(residual: torch.Tensor, budget: float) -> SparseResidual:
     """The largest-magnitude entries of `residual` under a fractional budget, over the whole
-    tensor (stacr/residual.py:23-33): the global top-k of the save kernels run on `residual`
-    with a zero basis.  Indices are ascending; ties at the cut go to the lowest index."""
+    tensor (stacr/residual.py:23-33): the save kernels' global top-k on `residual` against a zero
+    basis (so the residual they form is `residual` itself).  Indices ascend; ties at the cut go to
+    the lowest index."""
     residual = residual.detach()
     if budget <= 0 or residual.numel() == 0:
-        return _empty_residual(residual.shape, residual.device, residual.dtype)
-    x2d = residual.reshape(-1, residual.shape[-1]) if residual.dim() > 0 else residual.reshape(1, 1)
-    zero = torch.zeros(x2d.shape[1], 1, device=residual.device, dtype=residual.dtype)
-    _, idx, values, _ = kernels.save(x2d, zero, mode="global_topk", budget=_topk_budget(residual.numel(), budget),
-                                     chunk_rows=x2d.shape[0], bits=0)
-    return SparseResidual(tuple(residual.shape), idx.to(torch.long), values)
+        return SparseResidual.empty(residual.shape, residual.device, residual.dtype)
+    rows = _as_rows(residual)
+    zero_basis = rows.new_zeros(rows.shape[1], 1)
+    _, idx, values = _global_topk(rows, zero_basis, _reference_k_budget(residual.numel(), budget))
+    return SparseResidual(tuple(residual.shape), idx, values)
 
 
-def _basis_dtype(name: str, activation_dtype: torch.dtype) -> torch.dtype:
-    spec = str(name).lower()
-    if spec in ("auto", "activation"):
-        return activation_dtype
-    if spec in ("float16", "fp16", "half"):
-        return torch.float16
-    if spec in ("bfloat16", "bf16"):
-        return torch.bfloat16
-    return torch.float32
+# basis_dtype option -> basis dtype; "auto" / "activation" follow the activation, anything else is fp32
+_BASIS_DTYPE_NAMES = {"float16": torch.float16, "fp16": torch.float16, "half": torch.float16,
+                      "bfloat16": torch.bfloat16, "bf16": torch.bfloat16}
+_FOLLOW_ACTIVATION = ("auto", "activation")
+
+
+def _resolve_basis_dtype(spec: str, activation: torch.dtype) -> torch.dtype:
+    key = str(spec).lower()
+    if key in _FOLLOW_ACTIVATION:
+        return activation
+    return _BASIS_DTYPE_NAMES.get(key, torch.float32)
+
+
+def _is_weight_like(t: torch.Tensor) -> bool:
+    """A parameter, a leaf that requires grad, or a view of either (linear autograd saves the
+    transposed weight): tensors whose compression would make G W approximate."""
+    while t is not None:
+        if isinstance(t, torch.nn.Parameter) or (t.is_leaf and t.requires_grad):
+            return True
+        t = getattr(t, "_base", None)
+    return False
+
+
+# (reason, test that fails the gate): a tensor is compressed only if no gate fails
+_GATES: tuple[tuple[str, Callable[[STACRConfig, torch.Tensor], bool]], ...] = (
+    ("not floating point", lambda cfg, t: not t.is_floating_point()),
+    ("fewer than 2 dimensions", lambda cfg, t: t.dim() < 2),
+    ("parameter or a view of one", lambda cfg, t: _is_weight_like(t)),
+    ("too few features", lambda cfg, t: int(t.shape[-1]) < int(cfg.min_features)),
+    ("too few elements", lambda cfg, t: t.numel() < int(cfg.min_numel)),
+)
+
+
+class _BasisBank:
+    """One OjaBasis per (feature size, device), created on first use in the configured dtype."""
+
+    def __init__(self, config: STACRConfig):
+        self.config = config
+        self.by_key: dict[tuple[int, torch.device], OjaBasis] = {}
+
+    def get(self, x: torch.Tensor) -> OjaBasis:
+        key = (int(x.shape[-1]), x.device)
+        basis = self.by_key.get(key)
+        if basis is None:
+            basis = OjaBasis(key[0], self.config.rank, dtype=_resolve_basis_dtype(self.config.basis_dtype, x.dtype),
+                             device=x.device)
+            self.by_key[key] = basis
+        return basis
+
+    def refreshed(self, x: torch.Tensor, rows: torch.Tensor, step: int) -> OjaBasis:
+        """The basis for `x`, stepped on `rows` when `step` falls on the update interval."""
+        basis = self.get(x)
+        if step % max(1, int(self.config.update_interval)) == 0:
+            basis.update(rows, lr=float(self.config.oja_lr))
+        return basis
 
 
 class STACRCompressor:
@@ -112,78 +187,69 @@ class STACRCompressor:
     def __init__(self, config: STACRConfig | None = None):
         self.config = config or STACRConfig()
         self.step = 0
-        self._bases: dict[tuple[int, torch.device], OjaBasis] = {}
+        self._bank = _BasisBank(self.config)
+
+    @property
+    def _bases(self) -> dict:
+        return self._bank.by_key
 
     def set_step(self, step: int) -> None:
         self.step = int(step)
 
     def advance(self) -> None:
-        self.step += 1
+        self.set_step(self.step + 1)
 
-    def _basis_for(self, tensor: torch.Tensor) -> OjaBasis:
-        features = int(tensor.shape[-1])
-        key = (features, tensor.device)
-        if key not in self._bases:
-            dtype = _basis_dtype(self.config.basis_dtype, tensor.dtype)
-            self._bases[key] = OjaBasis(features, self.config.rank, dtype=dtype, device=tensor.device)
-        return self._bases[key]
+    def phase(self) -> str:
+        """"warmup" before warmup_steps, "turbo" from turbo_after_step on (or with residual mode
+        "none"), else "full"."""
+        cfg = self.config
+        if self.step < int(cfg.warmup_steps):
+            return "warmup"
+        turbo = cfg.turbo_after_step is not None and self.step >= int(cfg.turbo_after_step)
+        return "turbo" if turbo or cfg.residual_mode == "none" else "full"
 
     @staticmethod
     def is_parameter(tensor: torch.Tensor) -> bool:
-        """True for weights and biases (a parameter, a leaf that requires grad, or a view of one:
-        linear autograd saves the transposed weight), which are never compressed."""
-        if isinstance(tensor, torch.nn.Parameter) or (tensor.requires_grad and tensor.is_leaf):
-            return True
-        base = getattr(tensor, "_base", None)
-        return base is not None and STACRCompressor.is_parameter(base)
+        return _is_weight_like(tensor)
+
+    def skip_reason(self, tensor: torch.Tensor) -> str | None:
+        for reason, fails in _GATES:
+            if fails(self.config, tensor):
+                return reason
+        return None
 
     def should_compress(self, tensor: torch.Tensor) -> bool:
-        return (tensor.is_floating_point() and tensor.dim() >= 2 and not self.is_parameter(tensor)
-                and int(tensor.shape[-1]) >= int(self.config.min_features)
-                and tensor.numel() >= int(self.config.min_numel))
-
-    def _effective_residual_mode(self) -> str:
-        if self.config.turbo_after_step is not None and self.step >= int(self.config.turbo_after_step):
-            return "none"
-        return self.config.residual_mode
+        return self.skip_reason(tensor) is None
 
     def pack(self, tensor: torch.Tensor) -> Any:
-        if not self.should_compress(tensor) or self.step < int(self.config.warmup_steps):
+        phase = self.phase()
+        if phase == "warmup" or not self.should_compress(tensor):
             return tensor
         x = tensor.detach()
-        x2d = x.reshape(-1, x.shape[-1])
-        basis_state = self._basis_for(x)
-        if self.step % max(1, int(self.config.update_interval)) == 0:
-            basis_state.update(x2d, lr=float(self.config.oja_lr))
-        basis = basis_state.shared(dtype=x.dtype)
-        residual = None
-        if self._effective_residual_mode() != "none":
-            budget = float(self.config.residual_budget)
-            if budget <= 0:
-                coeff = kernels.save(x2d, basis, mode="global_topk", budget=0.0, chunk_rows=x2d.shape[0], bits=0)[0]
-                residual = _empty_residual(x.shape, x.device, x.dtype)
-            else:
-                coeff, idx, values, _ = kernels.save(x2d, basis, mode="global_topk",
-                                                     budget=_topk_budget(x.numel(), budget),
-                                                     chunk_rows=x2d.shape[0], bits=0)
-                residual = SparseResidual(tuple(x.shape), idx.to(torch.long), values)
+        rows = _as_rows(x)
+        basis = self._bank.refreshed(x, rows, self.step).shared(dtype=x.dtype)
+        budget = float(self.config.residual_budget) if phase == "full" else 0.0
+        coeff, idx, values = _global_topk(rows, basis, _reference_k_budget(x.numel(), budget) if budget > 0 else 0.0)
+        if phase != "full":
+            residual = None
+        elif idx is None:
+            residual = SparseResidual.empty(x.shape, x.device, x.dtype)
         else:
-            coeff = kernels.save(x2d, basis, mode="global_topk", budget=0.0, chunk_rows=x2d.shape[0], bits=0)[0]
+            residual = SparseResidual(tuple(x.shape), idx, values)
         return PackedActivation(tuple(x.shape), x.dtype, coeff, basis, residual)
 
     def unpack(self, packed: Any) -> torch.Tensor:
         if not isinstance(packed, PackedActivation):
             return packed
-        res = None
-        if packed.residual is not None:
-            res = (packed.residual.indices, packed.residual.values)
-        recon = kernels.reconstruct(packed.coeff, packed.basis, res)
-        return recon.reshape(packed.shape).to(dtype=packed.dtype)
+        entries = None if packed.residual is None else (packed.residual.indices, packed.residual.values)
+        dense = kernels.reconstruct(packed.coeff, packed.basis, entries)
+        return dense.reshape(packed.shape).to(dtype=packed.dtype)
 
 
 @contextmanager
 def stacr_saved_tensors(compressor: STACRCompressor):
-    """Context manager for PyTorch saved-tensor hooks (stacr/compressor.py:136-140)."""
+    """Installs `compressor`'s pack / unpack as PyTorch saved-tensor hooks for the block
+    (stacr/compressor.py:136-140)."""
     with torch.autograd.graph.saved_tensors_hooks(compressor.pack, compressor.unpack):
         yield compressor
 

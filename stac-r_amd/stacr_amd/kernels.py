@@ -311,7 +311,8 @@ def weight_grad(g2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, residua
         _lib.check(L.stacr_weight_grad_census(_ptr(g2d), dt, rows, d_out, _ptr(coeff), _ptr(q), d_in, rank, _ptr(idx),
                                               ib, _ptr(data), _ptr(scale), int(bits), vdt, nnz,
                                               1 if transposed else 0, _ptr(dw), dtype_code(out_dtype), _ptr(db),
-                                              dtype_code(bias_dtype) if db is not None else 0, _ptr(census), _ptr(ws),
+                                              dtype_code(bias_dtype) if db is not None else 0, _ptr(census),
+                                              census.numel() * census.element_size(), _ptr(ws),
                                               ws_bytes.value, _stream(device)), "stacr_weight_grad_census")
         return dw, db
     _lib.check(L.stacr_weight_grad(_ptr(g2d), dt, rows, d_out, _ptr(coeff), _ptr(q), d_in, rank, _ptr(idx), ib,

@@ -419,11 +419,45 @@ def test_config4_fifty_steps_refresh_rank_and_parity(dev):
     tokens, int8 coefficients, rank from the sensitivity controller capped at 16, chunk top-k budget
     0.005, fixed-cadence (10 steps) hybrid refresh of a frozen basis, 50 seeded steps with drifting
     activations.  Checks: refresh fires exactly on the layer's scheduled steps (plus any energy
-    triggers, which are recorded as such), the active rank stays in [rank_min, 16], the step-0 save
-    is bit-exact against the oracle, and dW matches the oracle on sampled output features at
-    steps 0, 10, 25 and 49."""
+    triggers, which are recorded as such), the active rank stays in [rank_min, 16], the save is
+    bit-exact against the oracle at step 0 and on the first step after each layer's first scheduled
+    refresh, the basis that refresh installs (a rank-16 Oja step on the layer's own 32768-row X,
+    d_in 2048 and 8192, then QR) matches the fp64 Oja step of the oracle on the same X, prior basis
+    and rate, and dW matches the oracle on sampled output features at steps 0, 10, 25 and 49."""
     from stacr_amd import adaptive
     from stacr_amd.rank_controller import is_fixed_refresh_step
+
+    def check_save(out, x, li, step):
+        announce("cfg4 save parity", li, step)
+        basis = out.grad_fn.basis
+        coeff, idx, values, _ = adaptive.save(x, basis, 0.005)
+        xf, qf, cf = _np(x), _np(basis), _np(coeff)
+        _, oidx, oval = orc.adaptive_save(xf, qf, "bf16", 0.005, 512, coeff=cf)
+        assert np.array_equal(idx.cpu().numpy().astype(np.int64), oidx.astype(np.int64))
+        assert np.array_equal(_np(values), oval)
+        oq, oscale, odt = orc.adaptive_quantize(cf, "bf16", 8)
+        assert np.array_equal(out.grad_fn.saved_tensors[0].cpu().numpy().reshape(-1), oq)
+        assert out.grad_fn.saved_tensors[2].item() == oscale and odt == "bf16"
+
+    def check_refresh(layer, x, prior, li, step):
+        """The installed basis against orthonormalize(oja_step) in fp64 by projector distance.  The
+        layer keeps its basis in bf16, so each entry carries a relative rounding of at most 2^-9:
+        the projector of 16 orthonormal columns (Frobenius norm 4) then moves by at most about
+        2 * 2^-9 * 4, 0.4 % of its norm; the bound is 1 %.  The step must also have moved the basis
+        well beyond that bound (so a refresh on the wrong X, basis or rate would show)."""
+        announce("cfg4 refresh basis", li, step)
+        lr = float(layer.layer_state["last_oja_lr"])
+        _, m64 = orc.oja_step(_np(x), _np(prior), lr)
+        ref = orc.orthonormalize(m64)
+        got = layer.effective_basis.detach().double().cpu().numpy()
+        assert got.shape == ref.shape == (x.shape[1], 16)
+        p_ref = ref @ ref.T
+        dist = np.linalg.norm(got @ got.T - p_ref) / np.linalg.norm(p_ref)
+        q0 = _np(prior).astype(np.float64)
+        moved = np.linalg.norm(q0 @ q0.T - p_ref) / np.linalg.norm(p_ref)
+        print(f"refresh layer {li} step {step}: projector distance {dist:.3g}, prior basis {moved:.3g}", flush=True)
+        assert dist <= 1e-2, dist
+        assert moved >= 5e-2, moved
 
     rows, dims = 16 * 2048, ((2048, 8192), (8192, 2048))
     cfg = _cfg(rank=16, rank_mode="sensitivity", rank_min=4, rank_max=16, rank_adjust_interval=5,
@@ -434,12 +468,14 @@ def test_config4_fifty_steps_refresh_rank_and_parity(dev):
     layers = adaptive.apply_adaptive_stacr(model, cfg, surface="all", min_features=1)
     assert len(layers) == 2 and [lay.layer_index for lay in layers] == [0, 1]
     check_steps = {0, 10, 25, 49}
+    first_refresh = {li: min(s for s in range(1, 50) if is_fixed_refresh_step(s, 0, 10, li, 2)) for li in (0, 1)}
     energy_refresh_steps = {0: [], 1: []}
     for step in range(50):
         adaptive.set_stacr_runtime_state(model, step)
         for li, (layer, (d_in, d_out)) in enumerate(zip(layers, dims)):
             before = layer.layer_state["refresh_count_total"]
             x = _drifting_activation(rows, d_in, step, 11 + li, dev).to(torch.bfloat16)
+            prior = layer.effective_basis.detach().clone() if step == first_refresh[li] else None
             out = layer(x)
             fixed = is_fixed_refresh_step(step, 0, 10, li, 2)
             fired = layer.layer_state["refresh_count_total"] - before
@@ -453,17 +489,10 @@ def test_config4_fifty_steps_refresh_rank_and_parity(dev):
             assert 4 <= active <= 16
             g = torch.randn(rows, d_out, generator=torch.Generator(device=dev).manual_seed(500 + step),
                             device=dev).to(torch.bfloat16)
-            if step == 0:
-                announce("cfg4 save parity", li)
-                basis = out.grad_fn.basis
-                coeff, idx, values, _ = adaptive.save(x, basis, 0.005)
-                xf, qf, cf = _np(x), _np(basis), _np(coeff)
-                _, oidx, oval = orc.adaptive_save(xf, qf, "bf16", 0.005, 512, coeff=cf)
-                assert np.array_equal(idx.cpu().numpy().astype(np.int64), oidx.astype(np.int64))
-                assert np.array_equal(_np(values), oval)
-                oq, oscale, odt = orc.adaptive_quantize(cf, "bf16", 8)
-                assert np.array_equal(out.grad_fn.saved_tensors[0].cpu().numpy().reshape(-1), oq)
-                assert out.grad_fn.saved_tensors[2].item() == oscale and odt == "bf16"
+            if step == first_refresh[li]:
+                check_refresh(layer, x, prior, li, step)
+            if step in (0, first_refresh[li] + 1):
+                check_save(out, x, li, step)
             if step in check_steps:
                 announce("cfg4 dW", li, step)
                 coeff, idx, values = _saved_factors(out, cfg, rows, d_in)

@@ -37,6 +37,9 @@ OJA_CASES = [
     ("onepass_d512_f16_ragged_rows", 1001, 512, 5, "f16", "random"),
     ("onepass_d2048_rank1", 300, 2048, 1, "bf16", "random"),
     ("onepass_fewer_rows_than_a_batch", 3, 1024, 8, "bf16", "random"),
+    # config 4's refresh shapes: 16 x 2048 tokens, rank 16, d_in 2048 and 8192
+    ("cfg4_up_rank16", 32768, 2048, 16, "bf16", "random"),
+    ("cfg4_down_rank16", 32768, 8192, 16, "bf16", "random"),
 ]
 
 

@@ -780,3 +780,21 @@ def test_entry_census_matches_count_and_gives_the_same_weight_gradient(dev, rows
     dw2, _ = kernels.weight_grad(g, coeff, q, res, 8, True, DT[dtype], census=census)
     torch.cuda.synchronize()
     assert torch.equal(dw1, dw2)
+
+
+def test_weight_grad_census_refuses_a_census_too_small_for_the_problem(dev):
+    """stacr_weight_grad_census reads counts for every input feature and a start for every 512-row
+    block: a census buffer sized for another (smaller) problem is refused on the host, before any
+    launch, instead of being read past its end."""
+    from stacr_amd import kernels
+
+    rows, d_in, d_out = 2048, 1024, 512
+    x = make_activation(rows, d_in, lognormal=True).to(dev, torch.bfloat16)
+    q = make_basis(d_in, 8).to(dev, torch.bfloat16)
+    g = make_grad(rows, d_out).to(dev, torch.bfloat16)
+    coeff, idx, data, scale, census = kernels.save_with_census(x, q, mode="global_topk", budget=0.005, chunk_rows=512,
+                                                               bits=8)
+    assert census is not None
+    small = census[: 8 * 512].clone()  # a census of a 512-feature layer
+    with pytest.raises(ValueError, match="census has"):
+        kernels.weight_grad(g, coeff, q, (idx, data, scale), 8, True, torch.bfloat16, census=small)

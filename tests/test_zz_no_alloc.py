@@ -2,9 +2,13 @@
 
 Both run the same kernels; the only difference is where the plan lives (a static per-GPU device
 array instead of a caller workspace).  Two calls in a row, the second on a smaller problem, each
-checked against stacr_weight_grad on the same inputs: dbias bit-equal (fixed summation order); dW
-within what the sparse term's arrival-order fp32 sums allow (fp32: rel-L2 <= 1e-6; bf16: every
-element within one bf16 ulp and rel-L2 <= 4e-3).  An oversized problem is refused on the host.
+checked against stacr_weight_grad on the same inputs, dbias bit-equal in both:
+* the first (bf16 Conv1D 1024 -> 4096, d_out a multiple of 16) runs the matrix-core tiles kernels,
+  whose sums have a fixed order, so dW is bit-equal too (a plan word left over from an earlier call
+  in the shared scratch would show);
+* the second (fp32, d_out = 1000, not a multiple of 16) runs the general kernels, which add the
+  sparse term's pieces in LDS arrival order: dW within rel-L2 1e-6.
+An oversized problem is refused on the host.
 """
 import ctypes
 
@@ -65,13 +69,10 @@ def test_noalloc_matches_workspace_entry_point_twice(dev):
         got_dw, got_db = _noalloc(g, coeff, q, (idx, data, scale), 8, transposed, dtype, dtype)
         torch.cuda.synchronize()
         assert torch.equal(got_db, want_db)
-        if dtype == torch.float32:
+        if d_out % 16 == 0:  # tiles kernels: fixed-order sums
+            assert torch.equal(got_dw, want_dw), f"rel-L2 {_rel(got_dw, want_dw):.3g}"
+        else:  # general kernels: arrival-order fp32 sums of the sparse term
             assert _rel(got_dw, want_dw) <= 1e-6
-        else:
-            w = want_dw.float()
-            ulp = torch.exp2(torch.floor(torch.log2(w.abs().clamp_min(2.0**-126))) - 7)
-            assert bool(((got_dw.float() - w).abs() <= ulp).all())
-            assert _rel(got_dw, want_dw) <= 4e-3
 
 
 def test_noalloc_refuses_problems_above_its_scratch(dev):
