@@ -335,6 +335,19 @@ int stacr_oja_workspace_bytes(int64_t rows, int64_t feats, int rank, size_t *byt
 int stacr_oja_step(const void *x, int dtype, int64_t rows, int64_t feats, const float *q, int rank, float lr,
                    float *update, float *out, void *workspace, size_t workspace_bytes, void *stream);
 
+/*
+ * stacr_oja_step on a Y = X Q the caller already holds (rows x rank fp32, row-major; the adaptive
+ * engine's save computes it in its projection pass, stacr_adaptive_save_y), so X is read once:
+ * X^T Y and Y^T Y, then U and M as stacr_oja_step.  The post-forward Oja refresh of the adaptive
+ * layer, stacr/adaptive.py:3311-3395, with its Y taken from the forward's projection.  Needs bf16
+ * X (16-byte aligned, features a multiple of 8 and <= 8192), rank <= 16, rows > 0 and Y 16-byte
+ * aligned with rows * rank a multiple of 4; otherwise STACR_ERR_UNSUPPORTED (use stacr_oja_step).
+ * Workspace as stacr_oja_workspace_bytes.
+ */
+int stacr_oja_step_given_y(const void *x, int dtype, int64_t rows, int64_t feats, const float *q, int rank,
+                           const float *y, float lr, float *update, float *out, void *workspace,
+                           size_t workspace_bytes, void *stream);
+
 /* ---------------------------------------------------------------- dense reconstruction */
 
 /*

@@ -567,6 +567,29 @@ int stacr_oja_step(const void *x, int dtype, int64_t rows, int64_t feats, const 
     return stacr_oja_launch(x, dtype, rows, feats, q, rank, lr, update, out, workspace, static_cast<hipStream_t>(stream));
 }
 
+int stacr_oja_step_given_y(const void *x, int dtype, int64_t rows, int64_t feats, const float *q, int rank,
+                           const float *y, float lr, float *update, float *out, void *workspace,
+                           size_t workspace_bytes, void *stream)
+{
+    if (!valid_dtype(dtype)) return stacr_fail(STACR_ERR_INVALID, "unsupported activation dtype code %d", dtype);
+    if (rows < 0 || feats < 1) return stacr_fail(STACR_ERR_INVALID, "stacr_oja_step_given_y: bad shape");
+    if (rank < 1 || rank > STACR_MAX_RANK)
+        return stacr_fail(STACR_ERR_UNSUPPORTED, "rank %d outside 1..%d", rank, STACR_MAX_RANK);
+    if (!q || !update || !out || !workspace || (rows > 0 && (!x || !y)))
+        return stacr_fail(STACR_ERR_INVALID, "stacr_oja_step_given_y: NULL pointer argument");
+    if (!isfinite(lr)) return stacr_fail(STACR_ERR_INVALID, "stacr_oja_step_given_y: lr must be finite");
+    if (!stacr_oja_given_y_ok(dtype, rows, feats, rank, x, y))
+        return stacr_fail(STACR_ERR_UNSUPPORTED,
+                          "stacr_oja_step_given_y: needs bf16 X (16-byte aligned, features a multiple of 8, at most "
+                          "8192), rank <= 16, rows > 0, and Y 16-byte aligned with rows * rank a multiple of 4");
+    const size_t need = stacr_oja_ws_bytes(rows, feats, rank);
+    if (workspace_bytes < need)
+        return stacr_fail(STACR_ERR_WORKSPACE, "stacr_oja_step_given_y: workspace has %zu bytes, needs %zu",
+                          workspace_bytes, need);
+    return stacr_oja_given_y_launch(x, rows, feats, q, rank, y, lr, update, out, workspace,
+                                    static_cast<hipStream_t>(stream));
+}
+
 // ------------------------------------------------------------------ uniform / block_sparse / sampled
 namespace {
 

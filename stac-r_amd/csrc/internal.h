@@ -368,6 +368,10 @@ int stacr_threshold_launch(const void *x, const void *coeff, const void *q, int 
 size_t stacr_oja_ws_bytes(int64_t rows, int64_t d, int rank);
 int stacr_oja_launch(const void *x, int dtype, int64_t rows, int64_t d, const float *q, int rank, float lr,
                      float *update, float *out, void *ws, hipStream_t s);
+// the Oja step on a Y = X Q computed elsewhere (rows x rank fp32): one pass over X
+bool stacr_oja_given_y_ok(int dtype, int64_t rows, int64_t d, int rank, const void *x, const void *y);
+int stacr_oja_given_y_launch(const void *x, int64_t rows, int64_t d, const float *q, int rank, const float *y,
+                             float lr, float *update, float *out, void *ws, hipStream_t s);
 size_t stacr_energy_ws();
 int stacr_energy_launch(const void *x, const void *c, int dtype, int64_t rows, int64_t feats, int rank, float *out,
                         void *ws, hipStream_t s);

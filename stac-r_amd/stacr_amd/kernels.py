@@ -276,6 +276,32 @@ def oja_step(x2d: torch.Tensor, q: torch.Tensor, lr: float):
     return update, out
 
 
+def oja_step_given_y(x2d: torch.Tensor, q: torch.Tensor, y: torch.Tensor, lr: float):
+    """oja_step with Y = X Q supplied (rows x rank fp32, e.g. the save's own projection), so X is
+    read once (stacr_oja_step_given_y).  Raises NotImplementedError for shapes the one-pass form
+    does not take (see the header); oja_step serves those."""
+    require_gpu(x2d, "activation")
+    x2d = x2d.contiguous()
+    q32 = q.to(device=x2d.device, dtype=torch.float32).contiguous()
+    rows, feats = x2d.shape
+    rank = q32.shape[1]
+    if q32.shape[0] != feats:
+        raise ValueError(f"basis has {q32.shape[0]} rows, activation has {feats} features")
+    if y.shape != (rows, rank) or y.dtype != torch.float32:
+        raise ValueError(f"Y must be {rows} x {rank} fp32, got {tuple(y.shape)} {y.dtype}")
+    y = y.contiguous()
+    L = _lib.load()
+    ws_bytes = ctypes.c_size_t()
+    _lib.check(L.stacr_oja_workspace_bytes(rows, feats, rank, ctypes.byref(ws_bytes)), "stacr_oja_workspace_bytes")
+    ws = torch.empty(max(1, ws_bytes.value), dtype=torch.uint8, device=x2d.device)
+    update = torch.empty(feats, rank, dtype=torch.float32, device=x2d.device)
+    out = torch.empty_like(update)
+    _lib.check(L.stacr_oja_step_given_y(_ptr(x2d), dtype_code(x2d.dtype), rows, feats, _ptr(q32), rank, _ptr(y),
+                                        float(lr), _ptr(update), _ptr(out), _ptr(ws), ws_bytes.value,
+                                        _stream(x2d.device)), "stacr_oja_step_given_y")
+    return update, out
+
+
 def weight_grad(g2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, residual, bits: int, transposed: bool,
                 out_dtype: torch.dtype, bias_dtype: torch.dtype | None = None, census: torch.Tensor | None = None):
     """dW (and dbias when bias_dtype is given) from the saved factors (stacr/layers.py:172-198).
