@@ -226,6 +226,23 @@ int stacr_adaptive_save(const void *x, const void *q, int dtype, int64_t rows, i
                         void *stream);
 
 /*
+ * stacr_adaptive_save on a basis q of q_cols columns (feats x q_cols, row-major; rank <= q_cols <= 32)
+ * of which the save uses the first `rank` (the active rank, stacr/adaptive.py:3116-3160: the layer
+ * saves on basis[:, :active]).  When y is non-NULL and the projection pass can write it (16-bit X on
+ * the wide projection pass: rank or q_cols 16, or feats > 2048; *y_written = 1), y (rows x q_cols
+ * fp32) receives X q before rounding: the Y = X B of the adaptive layer's post-forward Oja refresh
+ * (:3311-3395), which stacr_oja_step_given_y then finishes in one more pass over X.  The energies
+ * come from the same projection pass where it runs (one read of X), else from a pass of their own.
+ * Workspace: stacr_adaptive_save_y_workspace_bytes.
+ */
+int stacr_adaptive_save_y_workspace_bytes(int64_t rows, int64_t feats, int q_cols, int rank, int dtype,
+                                          double budget, int64_t chunk_rows, size_t *bytes);
+int stacr_adaptive_save_y(const void *x, const void *q, int dtype, int64_t rows, int64_t feats, int q_cols,
+                          int rank, double budget, int64_t chunk_rows, const void *coeff_in, void *coeff,
+                          void *idx, int index_bytes, void *values, float *energy, float *y, int *y_written,
+                          void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * quantize_int8 / quantize_int4 (stacr/adaptive.py:44-120): scale = max|v| / qmax computed and
  * rounded in the input dtype; q = round(v / scale) with the quotient rounded to the input dtype,
  * clamped to [-qmax, qmax] (qmax 127 or 7); int4 stores q + 8 as nibbles, even entry low, odd

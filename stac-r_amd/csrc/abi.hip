@@ -404,41 +404,61 @@ int stacr_adaptive_residual_plan(int64_t rows, int64_t feats, double budget, int
     return STACR_OK;
 }
 
-int stacr_adaptive_save_workspace_bytes(int64_t rows, int64_t feats, int rank, int dtype, double budget,
-                                        int64_t chunk_rows, size_t *bytes)
+namespace {
+
+// Workspace of an adaptive save: the save's own, then the energies' (the separate pass's partials, or
+// the projection pass's per-workgroup partials, whichever is larger).
+int adaptive_ws(const StacrSaveArgs &a, size_t *save, size_t *energy_off, size_t *total)
 {
-    if (!bytes) return stacr_fail(STACR_ERR_INVALID, "bytes is NULL");
-    StacrSaveArgs a;
-    AdaptivePlan p;
-    const int rc = fill_adaptive_args(rows, feats, rank, dtype, budget, chunk_rows, &a, &p);
-    if (rc) return rc;
-    const size_t save = rows * feats ? stacr_save_ws_layout(a, nullptr) : 0;
-    *bytes = ((save + 255) & ~(size_t)255) + stacr_energy_ws();
+    *save = a.rows * a.feats ? stacr_save_ws_layout(a, nullptr) : 0;
+    *energy_off = (*save + 255) & ~(size_t)255;
+    const int64_t slots = a.rows * a.feats ? stacr_save_energy_slots(a) : 0;
+    *total = *energy_off + stacr::hmax(stacr_energy_ws(), (size_t)slots * kEnergyStride * sizeof(float));
     return STACR_OK;
 }
 
-int stacr_adaptive_save(const void *x, const void *q, int dtype, int64_t rows, int64_t feats, int rank, double budget,
-                        int64_t chunk_rows, const void *coeff_in, void *coeff, void *idx, int index_bytes, void *values,
-                        float *energy, void *workspace, size_t workspace_bytes, void *stream)
+int fill_adaptive_y(int64_t rows, int64_t feats, int q_cols, int rank, int dtype, double budget, int64_t chunk_rows,
+                    float *y, StacrSaveArgs *a, AdaptivePlan *p)
 {
+    int rc = fill_adaptive_args(rows, feats, rank, dtype, budget, chunk_rows, a, p);
+    if (rc) return rc;
+    if (q_cols < rank || q_cols > STACR_MAX_RANK)
+        return stacr_fail(STACR_ERR_INVALID, "q_cols %d outside rank..%d", q_cols, STACR_MAX_RANK);
+    a->q_ld = q_cols;
+    a->y_cols = q_cols;
+    a->y_out = y;
+    return STACR_OK;
+}
+
+// a placeholder address marking "Y requested" for the planning queries (never written through)
+float *const kYPlanned = reinterpret_cast<float *>(alignof(float));
+
+int adaptive_save_impl(const void *x, const void *q, int dtype, int64_t rows, int64_t feats, int q_cols, int rank,
+                       double budget, int64_t chunk_rows, const void *coeff_in, void *coeff, void *idx,
+                       int index_bytes, void *values, float *energy, float *y, int *y_written, void *workspace,
+                       size_t workspace_bytes, void *stream, const char *who)
+{
+    if (y_written) *y_written = 0;
     StacrSaveArgs a;
     AdaptivePlan p;
-    int rc = fill_adaptive_args(rows, feats, rank, dtype, budget, chunk_rows, &a, &p);
+    int rc = fill_adaptive_y(rows, feats, q_cols, rank, dtype, budget, chunk_rows, y, &a, &p);
     if (rc) return rc;
     if (rows * feats == 0) return STACR_OK;
     if (!x || !q || (!coeff && !coeff_in) || !workspace)
-        return stacr_fail(STACR_ERR_INVALID, "stacr_adaptive_save: x, q, coeff (or coeff_in) and workspace must be non-NULL");
+        return stacr_fail(STACR_ERR_INVALID, "%s: x, q, coeff (or coeff_in) and workspace must be non-NULL", who);
     if (p.k > 0) {
-        if (!idx || !values) return stacr_fail(STACR_ERR_INVALID, "stacr_adaptive_save: idx and values must be non-NULL");
+        if (!idx || !values) return stacr_fail(STACR_ERR_INVALID, "%s: idx and values must be non-NULL", who);
         if (index_bytes != p.index_bytes)
-            return stacr_fail(STACR_ERR_INVALID, "stacr_adaptive_save: index_bytes must be %d", p.index_bytes);
+            return stacr_fail(STACR_ERR_INVALID, "%s: index_bytes must be %d", who, p.index_bytes);
     }
-    const size_t save = stacr_save_ws_layout(a, nullptr);
-    const size_t off_energy = (save + 255) & ~(size_t)255;
-    if (workspace_bytes < off_energy + stacr_energy_ws())
-        return stacr_fail(STACR_ERR_WORKSPACE, "stacr_adaptive_save: workspace has %zu bytes, needs %zu",
-                          workspace_bytes, off_energy + stacr_energy_ws());
+    size_t save, off_energy, need;
+    adaptive_ws(a, &save, &off_energy, &need);
+    if (workspace_bytes < need)
+        return stacr_fail(STACR_ERR_WORKSPACE, "%s: workspace has %zu bytes, needs %zu", who, workspace_bytes, need);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t slots = energy ? stacr_save_energy_slots(a) : 0;
+    float *epart = reinterpret_cast<float *>(static_cast<char *>(workspace) + off_energy);
+    int energy_fused = 0;
     a.x = x;
     a.q = q;
     a.coeff_in = coeff_in;
@@ -450,12 +470,62 @@ int stacr_adaptive_save(const void *x, const void *q, int dtype, int64_t rows, i
     a.workspace = workspace;
     a.workspace_bytes = save;
     a.stream = s;
+    a.y_written = y_written;
+    a.energy_part = slots ? epart : nullptr;
+    a.energy_written = &energy_fused;
     rc = stacr_save_launch(a);
     if (rc) return rc;
-    if (energy)
-        return stacr_energy_launch(x, coeff_in ? coeff_in : coeff, dtype, rows, feats, rank, energy,
-                                   static_cast<char *>(workspace) + off_energy, s);
+    if (!energy) return STACR_OK;
+    // the projection pass formed the energy partials (one read of X), else a pass of its own
+    if (energy_fused) return stacr_energy_fold_launch(epart, slots, dtype, rows, rank, energy, s);
+    return stacr_energy_launch(x, coeff_in ? coeff_in : coeff, dtype, rows, feats, rank, energy, epart, s);
+}
+
+}  // namespace
+
+int stacr_adaptive_save_workspace_bytes(int64_t rows, int64_t feats, int rank, int dtype, double budget,
+                                        int64_t chunk_rows, size_t *bytes)
+{
+    return stacr_adaptive_save_y_workspace_bytes(rows, feats, rank, rank, dtype, budget, chunk_rows, bytes);
+}
+
+int stacr_adaptive_save_y_workspace_bytes(int64_t rows, int64_t feats, int q_cols, int rank, int dtype, double budget,
+                                          int64_t chunk_rows, size_t *bytes)
+{
+    if (!bytes) return stacr_fail(STACR_ERR_INVALID, "bytes is NULL");
+    StacrSaveArgs a;
+    AdaptivePlan p;
+    size_t save, off, need = 0;
+    // with or without Y the plans can differ (Y over more columns takes the wide pass): the larger
+    for (int with_y = 0; with_y < 2; ++with_y) {
+        const int rc = fill_adaptive_y(rows, feats, q_cols, rank, dtype, budget, chunk_rows,
+                                       with_y ? kYPlanned : nullptr, &a, &p);
+        if (rc) return rc;
+        size_t t;
+        adaptive_ws(a, &save, &off, &t);
+        need = stacr::hmax(need, t);
+    }
+    *bytes = need;
     return STACR_OK;
+}
+
+int stacr_adaptive_save(const void *x, const void *q, int dtype, int64_t rows, int64_t feats, int rank, double budget,
+                        int64_t chunk_rows, const void *coeff_in, void *coeff, void *idx, int index_bytes, void *values,
+                        float *energy, void *workspace, size_t workspace_bytes, void *stream)
+{
+    return adaptive_save_impl(x, q, dtype, rows, feats, rank, rank, budget, chunk_rows, coeff_in, coeff, idx,
+                              index_bytes, values, energy, nullptr, nullptr, workspace, workspace_bytes, stream,
+                              "stacr_adaptive_save");
+}
+
+int stacr_adaptive_save_y(const void *x, const void *q, int dtype, int64_t rows, int64_t feats, int q_cols, int rank,
+                          double budget, int64_t chunk_rows, const void *coeff_in, void *coeff, void *idx,
+                          int index_bytes, void *values, float *energy, float *y, int *y_written, void *workspace,
+                          size_t workspace_bytes, void *stream)
+{
+    return adaptive_save_impl(x, q, dtype, rows, feats, q_cols, rank, budget, chunk_rows, coeff_in, coeff, idx,
+                              index_bytes, values, energy, y, y_written, workspace, workspace_bytes, stream,
+                              "stacr_adaptive_save_y");
 }
 
 int stacr_adaptive_quantize(const void *values, int dtype, int64_t n, int bits, void *data, void *scale,

@@ -348,6 +348,52 @@ __global__ void k_energy_ratio(int dt, float *__restrict__ out)
     out[0] = rnd_dt(dt, __fdiv_rn(num, den));
 }
 
+// The energies from a save's per-workgroup partials ([kEnergyStride] each: sum of rnd(x^2), sum of
+// rnd(c^2), sum of c_j^2 per basis column), with out[] as k_energy_final and k_energy_ratio write it.
+// Thread (value v, stripe st) adds partials st, st + 16, ... in order, 16 loads at a time; the 16
+// stripes are then added in order.
+constexpr int kFoldStripes = 16;
+__global__ __launch_bounds__(1024) void k_energy_fold(const float *__restrict__ part, int64_t n, int dt, int64_t rows,
+                                                      int rank, float *__restrict__ out)
+{
+    __shared__ float s_t[64][kFoldStripes];
+    __shared__ float s_sum[2];
+    const int v = threadIdx.x / kFoldStripes, st = threadIdx.x % kFoldStripes;
+    float t = 0.f;
+    if (v < 2 + rank) {
+        for (int64_t w0 = st; w0 < n; w0 += 16 * kFoldStripes) {
+            float vals[16];
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                const int64_t w = w0 + (int64_t)c * kFoldStripes;
+                vals[c] = w < n ? part[w * kEnergyStride + v] : 0.f;
+            }
+#pragma unroll
+            for (int c = 0; c < 16; ++c) t += vals[c];
+        }
+    }
+    s_t[v][st] = t;
+    __syncthreads();
+    const int k = threadIdx.x;
+    if (k < 2 + rank) {
+        float sum = 0.f;
+        for (int j = 0; j < kFoldStripes; ++j) sum += s_t[k][j];
+        if (k >= 2) out[3 + (k - 2)] = rows ? __fdiv_rn(sum, (float)rows) : 0.f;
+        else s_sum[k] = rnd_dt(dt, sum);
+    }
+    __syncthreads();
+    if (k == 0) {
+        const float x2 = s_sum[0], c2 = s_sum[1];
+        out[1] = x2;
+        out[2] = c2;
+        const float d0 = rnd_dt(dt, x2 - c2);
+        const float diff = isnan(d0) ? d0 : fmaxf(d0, 0.f);  // torch.clamp keeps NaN
+        const float num = rnd_dt(dt, __fsqrt_rn(diff));
+        const float den = rnd_dt(dt, rnd_dt(dt, __fsqrt_rn(x2)) + 1e-8f);
+        out[0] = rnd_dt(dt, __fdiv_rn(num, den));
+    }
+}
+
 int blocks_for(int64_t n) { return (int)hmax<int64_t>(1, hmin<int64_t>((n + kBlock - 1) / kBlock, 4096)); }
 
 }  // namespace
@@ -457,4 +503,10 @@ int stacr_energy_launch(const void *x, const void *c, int dtype, int64_t rows, i
     stacr_launch("k_energy_final", s, [&] { k_energy_final<<<1, 64, 0, s>>>(part, kEnergyWgs, dtype, rows, rank, out); });
     stacr_launch("k_energy_ratio", s, [&] { k_energy_ratio<<<1, 1, 0, s>>>(dtype, out); });
     return stacr_hip_check(hipGetLastError(), "energy");
+}
+
+int stacr_energy_fold_launch(const float *part, int64_t n, int dtype, int64_t rows, int rank, float *out, hipStream_t s)
+{
+    stacr_launch("k_energy_fold", s, [&] { k_energy_fold<<<1, 1024, 0, s>>>(part, n, dtype, rows, rank, out); });
+    return stacr_hip_check(hipGetLastError(), "energy fold");
 }

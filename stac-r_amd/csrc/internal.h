@@ -278,7 +278,22 @@ struct StacrSaveArgs {
     // whether this save filled it
     uint32_t *census = nullptr;
     int *census_written = nullptr;
+    // The basis q has q_ld columns a row (0: rank); the save uses its first `rank`.  Optional outputs
+    // of the projection pass where it can write them (the wide pass; *written (host) tells):
+    //   y_out        rows x y_cols fp32, X q[:, :y_cols] before rounding (rank <= y_cols <= q_ld), for
+    //                an Oja refresh on the same X and basis
+    //   energy_part  per projection workgroup [kEnergyStride]: sum of rnd(x^2), sum of rnd(c^2), and
+    //                sum of c_j^2 per basis column j < rank (fp32, C as saved)
+    int q_ld = 0, y_cols = 0;
+    float *y_out = nullptr;
+    int *y_written = nullptr;
+    float *energy_part = nullptr;
+    int *energy_written = nullptr;
 };
+constexpr int kEnergyStride = 2 + STACR_MAX_RANK;  // floats of one energy partial
+// Projection workgroups whose energy partials stacr_save_launch writes for these arguments (0 when
+// the plan's projection pass does not form them)
+int64_t stacr_save_energy_slots(const StacrSaveArgs &a);
 size_t stacr_save_ws_layout(const StacrSaveArgs &a, size_t *offsets);
 
 // Entry census: what the weight gradient's matrix-core plan needs to know about a save's residual
@@ -375,3 +390,6 @@ int stacr_oja_given_y_launch(const void *x, int64_t rows, int64_t d, const float
 size_t stacr_energy_ws();
 int stacr_energy_launch(const void *x, const void *c, int dtype, int64_t rows, int64_t feats, int rank, float *out,
                         void *ws, hipStream_t s);
+// the energies from a save's per-workgroup partials (n of them, [kEnergyStride] each), added in order
+int stacr_energy_fold_launch(const float *part, int64_t n, int dtype, int64_t rows, int rank, float *out,
+                             hipStream_t s);

@@ -176,10 +176,12 @@ __global__ void k_zero_u32(uint32_t *p, int64_t n)
         p[i] = 0u;
 }
 
-// Set-up of a save: the padded fp32 basis, and the histograms and max key cleared (one launch).
+// Set-up of a save: the padded fp32 basis (its first `rank` columns of rows q_ld apart), and the
+// histograms and max key cleared (one launch).
 template <int DT>
-__global__ void k_prep(const typename Act<DT>::T *__restrict__ q, int64_t d, int rank, int R, float *__restrict__ qp,
-                       uint32_t *__restrict__ zero, int64_t n_zero, uint32_t *__restrict__ zero2, int64_t n_zero2)
+__global__ void k_prep(const typename Act<DT>::T *__restrict__ q, int64_t d, int rank, int q_ld, int R,
+                       float *__restrict__ qp, uint32_t *__restrict__ zero, int64_t n_zero, uint32_t *__restrict__ zero2,
+                       int64_t n_zero2)
 {
     const int64_t n = d * R;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
@@ -190,13 +192,13 @@ __global__ void k_prep(const typename Act<DT>::T *__restrict__ q, int64_t d, int
         {   // padded copy: element i is (row i / R, column i % R)
             const int64_t row = i / R;
             const int j = (int)(i - row * R);
-            qp[i] = j < rank ? Act<DT>::ld(q[row * rank + j]) : 0.f;
+            qp[i] = j < rank ? Act<DT>::ld(q[row * q_ld + j]) : 0.f;
         }
         {   // transposed copies: element i is (column i / d, row i % d), so consecutive threads write
             // consecutive addresses
             const int j = (int)(i / d);
             const int64_t row = i - (int64_t)j * d;
-            const typename Act<DT>::T raw = j < rank ? q[row * rank + j] : (typename Act<DT>::T)0;
+            const typename Act<DT>::T raw = j < rank ? q[row * q_ld + j] : (typename Act<DT>::T)0;
             qpt[i] = j < rank ? Act<DT>::ld(raw) : 0.f;
             if constexpr (sizeof(typename Act<DT>::T) == 2) qph[i] = raw;
         }
@@ -977,12 +979,19 @@ __global__ __launch_bounds__(kBlock) void k_proj_hist_b(SaveGeom g, FastGeom fg,
 // (exact in the activation dtype), the level-0 histogram with its coarse sums, and the max key.
 // The later passes read the stored residual as a matrix of f * rows rows of d / f columns (the
 // same memory, the same flat indices), so they never need the basis or C.
+//
+// Optional outputs (NULL: none): y_out, the fp32 projections before rounding of the basis's first
+// y_cols columns (the basis copy may hold more columns than the rank, g.rank: those are projected
+// for y_out only and take no part in the coefficients or the residual); epart, the workgroup's
+// energy partial [kEnergyStride]: sum of rnd(x^2) over its elements, sum of rnd(c^2) and, per basis
+// column j < g.rank, the sum of c_j^2 over its rows (C as saved; bf16 only).
 template <int DT, int R, int MV, int NT>
 __global__ __launch_bounds__(NT) void k_proj_hist_w(SaveGeom g, int c_vec, const typename Act<DT>::T *__restrict__ x,
                                                     const float *__restrict__ qp, typename Act<DT>::T *__restrict__ coeff,
                                                     uint32_t *__restrict__ hist, uint32_t *__restrict__ maxkey,
                                                     int do_hist, const typename Act<DT>::T *__restrict__ coeff_in,
-                                                    typename Act<DT>::T *__restrict__ rout, uint32_t *__restrict__ coarse)
+                                                    typename Act<DT>::T *__restrict__ rout, uint32_t *__restrict__ coarse,
+                                                    float *__restrict__ y_out, int y_cols, float *__restrict__ epart)
 {
     using T = typename Act<DT>::T;
     static_assert(sizeof(T) == 2, "16-bit activations");
@@ -992,9 +1001,13 @@ __global__ __launch_bounds__(NT) void k_proj_hist_w(SaveGeom g, int c_vec, const
     __shared__ __align__(16) float s_part[W * 64];
     __shared__ __align__(16) float s_c[64];
     __shared__ uint32_t s_wmax[W];
+    __shared__ float s_ex[W];
     int64_t chunk, row0, row_end;
     wg_rows(g, blockIdx.x, chunk, row0, row_end);
-    if (row0 >= row_end) return;  // a trailing workgroup with no rows (uniform)
+    if (row0 >= row_end) {  // a trailing workgroup with no rows (uniform): its energy partial is zero
+        if (epart && threadIdx.x < kEnergyStride) epart[(int64_t)blockIdx.x * kEnergyStride + threadIdx.x] = 0.f;
+        return;
+    }
     const int u = threadIdx.x, lane = u & 63, wave = u >> 6;
     int64_t col[MV], colc[MV];
     bool col_ok[MV];
@@ -1057,10 +1070,11 @@ __global__ __launch_bounds__(NT) void k_proj_hist_w(SaveGeom g, int c_vec, const
         if (wave == 0) {
             float tot = part;
             for (int w = 1; w < W; ++w) tot += s_part[w * 64 + lane];
-            const float cv = Act<DT>::rnd(tot);
-            s_c[lane] = cv;
             const int i = lane / R, j = lane % R;
             const int64_t row = row0 + i;
+            if (y_out && j < y_cols && row < row_end) y_out[row * y_cols + j] = tot;
+            const float cv = j < g.rank ? Act<DT>::rnd(tot) : 0.f;  // (columns past the rank: Y only)
+            s_c[lane] = cv;
             if (j < g.rank && row < row_end) coeff[row * g.rank + j] = Act<DT>::st(cv);
         }
         __syncthreads();
@@ -1070,6 +1084,48 @@ __global__ __launch_bounds__(NT) void k_proj_hist_w(SaveGeom g, int c_vec, const
             const float4 v = src[k];
             c[4 * k] = v.x; c[4 * k + 1] = v.y; c[4 * k + 2] = v.z; c[4 * k + 3] = v.w;
         }
+    }
+    if constexpr (DT == STACR_DTYPE_BF16) {  // (fp16: the energies take a pass of their own)
+    if (epart) {
+        // energies: sum of rnd(x^2) over this thread's elements, then over the workgroup in wave order
+        float ex = 0.f;
+#pragma unroll
+        for (int m = 0; m < MV; ++m)
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const uint4 xr = rows[i] < row_end && col_ok[m] ? raw[i][m] : make_uint4(0u, 0u, 0u, 0u);
+                const uint32_t xw[4] = {xr.x, xr.y, xr.z, xr.w};
+#pragma unroll
+                for (int e = 0; e < V; ++e) {
+                    const float xe = Act<DT>::ld((T)((xw[e >> 1] >> (16 * (e & 1))) & 0xffffu));
+                    ex += Act<DT>::rnd(xe * xe);
+                }
+            }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ex += __shfl_xor(ex, off, 64);
+        if (lane == 0) s_ex[wave] = ex;
+        // C as saved: lane (i, j) of wave 0
+        if (wave == 0) {
+            const int i = lane / R, j = lane % R;
+            const int64_t row = row0 + i;
+            float cv = 0.f;
+            if (j < g.rank && row < row_end) cv = coeff_in ? Act<DT>::ld(coeff_in[row * g.rank + j]) : s_c[lane];
+            float sc = Act<DT>::rnd(cv * cv), cj = cv * cv;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) sc += __shfl_xor(sc, off, 64);
+#pragma unroll
+            for (int off = 32; off >= R; off >>= 1) cj += __shfl_xor(cj, off, 64);  // over the rows i
+            float *ep = epart + (int64_t)blockIdx.x * kEnergyStride;
+            if (lane < g.rank) ep[2 + lane] = cj;
+            if (lane == 0) ep[1] = sc;
+        }
+        __syncthreads();
+        if (u == 0) {
+            float t = s_ex[0];
+            for (int w = 1; w < W; ++w) t += s_ex[w];
+            epart[(int64_t)blockIdx.x * kEnergyStride] = t;
+        }
+    }
     }
     if (!do_hist) return;
     if (coeff_in) __syncthreads();  // the histogram is clear
@@ -2369,6 +2425,7 @@ struct Plan {
     bool cand_rin;
     bool trim;
     int64_t n_list_blocks;
+    int yc;  // basis columns the projection covers (the rank, or the Y columns the wide pass serves)
 };
 
 Plan make_plan_rows(const StacrSaveArgs &a)
@@ -2473,7 +2530,7 @@ Plan make_plan_wide(const StacrSaveArgs &a)
 // quota, four times its mean share of its chunk's k plus 64, fits half the candidate list: a
 // workgroup then needs more than four times its share above the chunk's level-0 bin before it
 // falls back to recomputing.
-Plan make_plan(const StacrSaveArgs &a)
+Plan make_plan_base(const StacrSaveArgs &a)
 {
     Plan p = make_plan_wide(a);
     if (!p.fold || a.k_total <= 0) return p;
@@ -2489,6 +2546,27 @@ Plan make_plan(const StacrSaveArgs &a)
     p.cand = true;
     p.cand_rin = false;
     p.quota = (uint32_t)quota;
+    return p;
+}
+
+// With y_out asked for y_cols > rank basis columns, the plan is made for a rank of y_cols and kept
+// only if it takes the wide projection pass (the one that writes Y), with the coefficients and the
+// residual then formed from the first `rank` columns; otherwise the plan is the rank's own.
+Plan make_plan(const StacrSaveArgs &a)
+{
+    if (a.y_out && a.y_cols > a.rank) {
+        StacrSaveArgs ay = a;
+        ay.rank = a.y_cols;
+        Plan p = make_plan_base(ay);
+        if (p.wide) {
+            p.gw.rank = a.rank;
+            p.g.rank = a.rank < 8 ? a.rank : 8;
+            p.yc = a.y_cols;
+            return p;
+        }
+    }
+    Plan p = make_plan_base(a);
+    p.yc = a.rank;
     return p;
 }
 
@@ -2534,6 +2612,9 @@ int launch_wide_pass1(const StacrSaveArgs &a, const Plan &p, const typename Act<
                       typename Act<DT>::T *coeff, uint32_t *hist, uint32_t *maxkey, int do_hist,
                       const typename Act<DT>::T *coeff_in, typename Act<DT>::T *rout, uint32_t *coarse)
 {
+    // the optional projection outputs (Y only where the pass projects: not on given coefficients)
+    float *y_out = a.y_out && !coeff_in ? a.y_out : nullptr;
+    float *epart = DT == STACR_DTYPE_BF16 ? a.energy_part : nullptr;
     hipStream_t s = a.stream;
     const unsigned n = (unsigned)p.n_wgs_w;
     const void *cp = coeff_in ? (const void *)coeff_in : (const void *)coeff;
@@ -2544,7 +2625,8 @@ int launch_wide_pass1(const StacrSaveArgs &a, const Plan &p, const typename Act<
         if (done || p.Rq != R || p.mvw != MV || p.ntw != NT) return;
         done = true;
         stacr_launch("k_proj_hist_w", s, [&] {
-            k_proj_hist_w<DT, R, MV, NT><<<n, NT, 0, s>>>(p.gw, c_vec, x, qp, coeff, hist, maxkey, do_hist, coeff_in, rout, coarse);
+            k_proj_hist_w<DT, R, MV, NT><<<n, NT, 0, s>>>(p.gw, c_vec, x, qp, coeff, hist, maxkey, do_hist, coeff_in, rout, coarse,
+                                                          y_out, p.yc, epart);
         });
     };
     using I1 = std::integral_constant<int, 1>;
@@ -2558,6 +2640,8 @@ int launch_wide_pass1(const StacrSaveArgs &a, const Plan &p, const typename Act<
     if constexpr (DT == STACR_DTYPE_BF16) go(std::integral_constant<int, 16>{}, I2{}, N512{});
     if (!done)
         return stacr_fail(STACR_ERR_INVALID, "stacr_save: no wide projection kernel for rank %d, %d x %d", p.Rq, p.mvw, p.ntw);
+    if (y_out && a.y_written) *a.y_written = 1;
+    if (epart && a.energy_written) *a.energy_written = 1;
     return STACR_OK;
 }
 
@@ -2591,7 +2675,8 @@ int launch_typed(const StacrSaveArgs &a, const Plan &p, char *ws, const size_t *
     const int64_t n_census = census ? (int64_t)kCensusCopies * a.feats : 0;
     stacr_launch("k_prep", s, [&] {
         k_prep<DT><<<grid_for(hmax<int64_t>(hmax<int64_t>(a.feats * p.Rq, n_zero), n_census)), kBlock, 0, s>>>(
-            static_cast<const T *>(a.q), a.feats, a.rank, p.Rq, qp, hist, n_zero, census ? a.census : nullptr, n_census);
+            static_cast<const T *>(a.q), a.feats, p.yc, a.q_ld > 0 ? a.q_ld : a.rank, p.Rq, qp, hist, n_zero,
+            census ? a.census : nullptr, n_census);
     });
     // batched fast path: one aligned vector per thread per row, basis columns in registers
     constexpr bool kFastOk = QREG && V == Act<DT>::kVec && V * R <= 64;
@@ -2785,6 +2870,12 @@ size_t stacr_save_ws_layout(const StacrSaveArgs &a, size_t *offsets)
     const Plan p = make_plan(a);
     size_t tmp[WS_N];
     return layout(a, p, offsets ? offsets : tmp);
+}
+
+int64_t stacr_save_energy_slots(const StacrSaveArgs &a)
+{
+    const Plan p = make_plan(a);
+    return p.wide && a.dtype == STACR_DTYPE_BF16 ? p.n_wgs_w : 0;
 }
 
 int stacr_save_launch(const StacrSaveArgs &a)

@@ -53,6 +53,9 @@ SIGNATURES = {
     "stacr_adaptive_save_workspace_bytes": ([_i64, _i64, _i32, _i32, _f64, _i64, _PSZ], _i32),
     "stacr_adaptive_save": ([_p, _p, _i32, _i64, _i64, _i32, _f64, _i64, _p, _p, _p, _i32, _p, _p, _p, _sz, _p],
                             _i32),
+    "stacr_adaptive_save_y_workspace_bytes": ([_i64, _i64, _i32, _i32, _i32, _f64, _i64, _PSZ], _i32),
+    "stacr_adaptive_save_y": ([_p, _p, _i32, _i64, _i64, _i32, _i32, _f64, _i64, _p, _p, _p, _i32, _p, _p, _p,
+                               ctypes.POINTER(ctypes.c_int), _p, _sz, _p], _i32),
     "stacr_adaptive_quantize": ([_p, _i32, _i64, _i32, _p, _p, _p, _sz, _p], _i32),
     "stacr_adaptive_dequantize": ([_p, _i32, _p, _i64, _p, _i32, _p], _i32),
     "stacr_csr_encode": ([_p, _i32, _i64, _i64, _i64, _p, _i32, _p, _i32, _p], _i32),

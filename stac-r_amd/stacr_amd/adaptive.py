@@ -32,7 +32,7 @@ from torch import nn
 
 from . import _lib
 from .kernels import _ptr, _stream, dtype_code, require_gpu
-from .rank_controller import BasisRefreshTrigger, select_active_rank, should_update_basis
+from .rank_controller import BasisRefreshTrigger, basis_update_outlook, select_active_rank, should_update_basis
 
 _SCALE_DTYPES = {_lib.DTYPE_F32: torch.float32, _lib.DTYPE_BF16: torch.bfloat16, _lib.DTYPE_F16: torch.float16,
                  _lib.SCALE_F64: torch.float64}
@@ -315,6 +315,36 @@ def save(x2d: torch.Tensor, basis: torch.Tensor, budget: float, chunk_rows: int 
                                      _ptr(coeff), _ptr(out_coeff), _ptr(idx), ib, _ptr(values), _ptr(energy),
                                      _ptr(ws), ws_bytes.value, _stream(device)), "stacr_adaptive_save")
     return (coeff if coeff is not None else out_coeff), (idx if k > 0 else None), (values if k > 0 else None), energy
+
+
+def save_y(x2d: torch.Tensor, full_basis: torch.Tensor, rank: int, budget: float, chunk_rows: int = 512):
+    """save() on the first `rank` columns of `full_basis` (feats x q_cols, the activation dtype), also
+    returning Y = X full_basis (rows x q_cols fp32) when the projection pass could write it, else None
+    (stacr_adaptive_save_y): (coeff, idx, values, energy, Y or None)."""
+    require_gpu(x2d, "activation")
+    x2d = x2d.contiguous()
+    full = full_basis.to(x2d.dtype).contiguous()
+    rows, feats = x2d.shape
+    q_cols = full.shape[1]
+    dt = dtype_code(x2d.dtype)
+    k, k_saved, ib = residual_plan(rows, feats, budget, chunk_rows)
+    device = x2d.device
+    L = _lib.load()
+    ws_bytes = ctypes.c_size_t()
+    _lib.check(L.stacr_adaptive_save_y_workspace_bytes(rows, feats, q_cols, rank, dt, float(budget), int(chunk_rows),
+                                                       ctypes.byref(ws_bytes)), "stacr_adaptive_save_y")
+    ws = torch.empty(max(1, ws_bytes.value), dtype=torch.uint8, device=device)
+    idx = torch.empty(k_saved, dtype={2: torch.int16, 4: torch.int32, 8: torch.int64}[ib], device=device)
+    values = torch.empty(k_saved, dtype=x2d.dtype, device=device)
+    energy = torch.zeros(3 + rank, dtype=torch.float32, device=device)
+    coeff = torch.empty(rows, rank, dtype=x2d.dtype, device=device)
+    y = torch.empty(rows, q_cols, dtype=torch.float32, device=device)
+    written = ctypes.c_int(0)
+    _lib.check(L.stacr_adaptive_save_y(_ptr(x2d), _ptr(full), dt, rows, feats, q_cols, int(rank), float(budget),
+                                       int(chunk_rows), None, _ptr(coeff), _ptr(idx), ib, _ptr(values), _ptr(energy),
+                                       _ptr(y), ctypes.byref(written), _ptr(ws), ws_bytes.value, _stream(device)),
+               "stacr_adaptive_save_y")
+    return coeff, (idx if k > 0 else None), (values if k > 0 else None), energy, (y if written.value else None)
 
 
 def block_sparse_plan(rows: int, feats: int, budget: float, chunk_rows: int = 512, block_size: int = 16):
@@ -793,7 +823,20 @@ class STACRFunction(torch.autograd.Function):
         total = b_flat * in_features
         k_budget = min(int(total * budget), total)  # the k of "topk" and "adaptive_threshold"
         exact_topk = mode == "topk" and not streaming
-        coeff, idx, values, energy = save(x2d, basis_c, budget if exact_topk else 0.0, chunk)
+        # The layer asks for Y = X B over its whole allocated basis when a post-forward Oja refresh may
+        # follow on this X (its refresh then reads X once more instead of twice); the save computes
+        # it in its projection pass.  Y serves the refresh only when B is exact in the activation
+        # dtype (the refresh projects on B itself) and the saved basis is B's leading columns.
+        full = layer_state.pop("_oja_y_request", None) if not recomputing else None
+        y = None
+        # basis_c = full[:, :rank] (a column slice keeps the data pointer and strides, whatever the layout)
+        leading_cols = full is not None and basis_c.data_ptr() == full.data_ptr() and basis_c.stride() == full.stride()
+        if (leading_cols and full.dtype == x2d.dtype and full.shape[0] == in_features
+                and full.shape[1] >= rank):
+            coeff, idx, values, energy, y = save_y(x2d, full, rank, budget if exact_topk else 0.0, chunk)
+            layer_state["_oja_y"] = (y, full, x2d) if y is not None else None
+        else:
+            coeff, idx, values, energy = save(x2d, basis_c, budget if exact_topk else 0.0, chunk)
         # "adaptive_threshold" with k = 0 keeps no residual and computes no energy (it stays 0)
         no_energy = mode == "adaptive_threshold" and k_budget <= 0
         # The host reads of a forward: the energies (the rank controller, refresh triggers and skip
@@ -1410,7 +1453,18 @@ class STACRLinear(nn.Module):
             if rows.dtype not in kernels.DTYPE_CODES:
                 rows = rows.float()
             current = self.effective_basis
-            _, stepped = kernels.oja_step(rows, current, float(lr))
+            # Y = X B from this forward's save, when it was computed on this X and this basis
+            given = st.pop("_oja_y", None)
+            stepped = None
+            if given is not None and given[1] is current and given[2].data_ptr() == rows.data_ptr() \
+                    and given[2].shape == rows.shape:
+                try:
+                    _, stepped = kernels.oja_step_given_y(rows, current, given[0], float(lr))
+                    st["oja_given_y_steps"] = st.get("oja_given_y_steps", 0) + 1
+                except NotImplementedError:
+                    stepped = None
+            if stepped is None:
+                _, stepped = kernels.oja_step(rows, current, float(lr))
             q, r = torch.linalg.qr(stepped)
             if cfg.use_mgs:  # Gram-Schmidt's factor has a positive diagonal: the same Q up to column signs
                 q = q * torch.sign(torch.diagonal(r)).where(torch.diagonal(r) != 0, torch.ones_like(q[0]))
@@ -1481,6 +1535,16 @@ class STACRLinear(nn.Module):
 
         config_dict = cfg.to_dict()
         residual_off = basis is not None and not sparse_only and self._residual_off(schedule_step)
+        st.pop("_oja_y", None)
+        st.pop("_oja_y_request", None)
+        if basis is not None and not recomputing and not residual_off and self.basis_initialized:
+            outlook = basis_update_outlook(config_dict, schedule_step, self._get_microbatch_index(),
+                                           self._get_accum_steps(), self.layer_index, self.num_layers)
+            full = self.effective_basis
+            # Y over more columns than the saved rank moves the save to its wide projection pass
+            # (slower below 2048 features), so that is done only for a certain refresh
+            if outlook == "certain" or (outlook == "maybe" and full.shape[1] == basis.shape[1]):
+                st["_oja_y_request"] = full
         fast = residual_off and cfg.enable_low_rank_only_fast_path
         fn = STACRLowRankOnlyFunction if fast else STACRFunction
         output = fn.apply(x, self.linear.weight, self.linear.bias, basis, config_dict, step_tensor, st)

@@ -195,6 +195,36 @@ def _microbatch_cached(layer_state: MutableMapping[str, Any], cache: bool, micro
     return False
 
 
+def basis_update_outlook(config: Mapping[str, Any], schedule_step: int, microbatch_index: int = 0,
+                         accum_steps: int = 1, layer_index: Optional[int] = None, num_layers: int = 1) -> str:
+    """What should_update_basis can decide after this step's forward, known before it: "never",
+    "certain" (a cadence fires whatever the forward's energy) or "maybe" (it depends on the energy).
+    Reads and writes no layer state."""
+    step = int(schedule_step)
+    cache = bool(_cfg(config, "cache_basis_per_optimizer_step", REFRESH_DEFAULTS) and accum_steps > 1)
+    if cache and microbatch_index > 0:
+        return "never"
+    warmup = _cfg(config, "warmup_steps", REFRESH_DEFAULTS)
+    if _cfg(config, "freeze_basis_after_warmup", REFRESH_DEFAULTS) and step >= warmup:
+        trigger = _cfg(config, "refresh_trigger", REFRESH_DEFAULTS)
+        fixed = is_fixed_refresh_step(step, warmup, max(1, int(_cfg(config, "refresh_period", REFRESH_DEFAULTS))),
+                                      layer_index, num_layers)
+        if trigger in (BasisRefreshTrigger.FIXED.value, BasisRefreshTrigger.HYBRID.value) and fixed:
+            return "certain"
+        if trigger in (BasisRefreshTrigger.RESIDUAL_ENERGY.value, BasisRefreshTrigger.HYBRID.value):
+            return "maybe"
+        return "never"
+    lazy = bool(_cfg(config, "lazy_update_enabled", REFRESH_DEFAULTS))
+    trigger = _cfg(config, "update_trigger", REFRESH_DEFAULTS)
+    interval = _cfg(config, "update_interval", REFRESH_DEFAULTS)
+    on_interval = step > 0 and step % interval == 0
+    if trigger in ("fixed", "hybrid") and on_interval:
+        return "maybe" if lazy else "certain"
+    if trigger in ("adaptive", "hybrid"):
+        return "maybe"
+    return "never"
+
+
 def should_update_basis(config: Mapping[str, Any], layer_state: MutableMapping[str, Any], schedule_step: int,
                         microbatch_index: int = 0, accum_steps: int = 1, layer_index: Optional[int] = None,
                         num_layers: int = 1) -> bool:

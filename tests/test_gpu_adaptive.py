@@ -141,6 +141,45 @@ def test_adaptive_save_matches_oracle(name, rows, d, r, dtype, budget):
     np.testing.assert_allclose(e[3:3 + r], per_rank, rtol=1e-5, atol=1e-7)
 
 
+SAVE_Y_CASES = [
+    # rows, feats, q_cols, rank: the save uses the first `rank` of q_cols basis columns
+    ("d2048_active5_of16", 4096, 2048, 16, 5),   # below the allocated rank: the wide pass for Y
+    ("d8192_rank16", 2048, 8192, 16, 16),
+    ("d3000_active7_of12", 1000, 3000, 12, 7),
+    ("d1024_rank16_cfg4_like", 2048, 1024, 16, 16),
+]
+
+
+@pytest.mark.parametrize("name,rows,d,qc,r", SAVE_Y_CASES)
+def test_adaptive_save_y_matches_oracle(name, rows, d, qc, r):
+    """stacr_adaptive_save_y: Y = X B over all q_cols columns (fp32, within 1e-5 rel-L2 of the fp64
+    product), the coefficients bf16(Y[:, :rank]) bit for bit, the selection on them bit-exact against
+    the oracle, the energies from the same projection pass within the dtype's rounding."""
+    from stacr_amd import adaptive as ad
+
+    dev = _dev()
+    print(f"CASE save_y {name}", flush=True)
+    x = make_activation(rows, d).to(torch.bfloat16)
+    q = make_basis(d, qc).to(torch.bfloat16)
+    coeff, idx, values, energy, y = ad.save_y(x.to(dev), q.to(dev), r, 0.005, 512)
+    assert y is not None and y.shape == (rows, qc)
+    xf, qf = x.float().numpy(), q.float().numpy()
+    exact = xf.astype(np.float64) @ qf.astype(np.float64)
+    yf = y.cpu().numpy().astype(np.float64)
+    assert np.linalg.norm(yf - exact) <= 1e-5 * np.linalg.norm(exact)
+    assert torch.equal(coeff.cpu(), y[:, :r].cpu().to(torch.bfloat16))
+    cf = coeff.float().cpu().numpy()
+    _, idx_ref, val_ref = orc.adaptive_save(xf, qf[:, :r], "bf16", 0.005, 512, coeff=cf)
+    assert np.array_equal(idx.cpu().numpy().astype(np.int64), idx_ref.astype(np.int64))
+    assert np.array_equal(values.float().cpu().numpy(), val_ref)
+    e_ref, x2, c2, per_rank = orc.adaptive_energy(xf, cf, "bf16")
+    e = energy.cpu().numpy()
+    tol = 2 ** -7
+    assert abs(e[1] - x2) <= tol * abs(x2) and abs(e[2] - c2) <= tol * abs(c2)
+    assert abs(e[0] - e_ref) <= 4 * tol * max(abs(e_ref), 1e-3)
+    np.testing.assert_allclose(e[3:3 + r], per_rank, rtol=1e-5, atol=1e-7)
+
+
 # ---------------------------------------------------------------- the adaptive Function
 FUNC_CONFIGS = [
     dict(residual_mode="topk", residual_budget=0.005, quantize_coefficients=True, quantize_residuals=True,

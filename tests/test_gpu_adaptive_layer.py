@@ -513,6 +513,8 @@ def test_config4_fifty_steps_refresh_rank_and_parity(dev):
         assert layer.layer_state["refresh_count_total"] == scheduled + len(energy_refresh_steps[li])
         assert int(layer.step_counter) == 50
         assert layer.layer_state["rank_trajectory"], "the controller never ran"
+        # the scheduled refreshes took Y from their forward's save (X read once more, not twice)
+        assert layer.layer_state.get("oja_given_y_steps", 0) >= scheduled, layer.layer_state.get("oja_given_y_steps")
     print("energy-triggered refreshes:", energy_refresh_steps, flush=True)
 
 
