@@ -16,11 +16,13 @@ grad_input = G W, grad_bias = G.sum(0)); it is not timed, and the time of G.sum(
 beside the line.  K steps are timed as eager launches and replayed from a HIP graph captured
 once (every replay checked against the eager result; a mismatch fails the run); the value is
 the faster of the two and both are reported.  Other configured layers (cfg3 c_proj, cfg2 Turbo)
-and the basis refresh's Oja step are timed the same way and reported under "other_workloads".
-Prints one JSON line.
+and the basis refresh's Oja step are timed the same way and reported under "other_workloads",
+with two whole-layer lines: the drop-in STACRLinear step with its per-step Oja refresh, and
+config 4 (2048 <-> 8192, 32768 tokens) through the adaptive engine.  Prints one JSON line.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20]
-    python bench.py --workload {c_proj,turbo,cfg1,cfg4_up,cfg4_down,oja} [--steps K] [--warmup W]
+    python bench.py --workload {c_proj,turbo,cfg1,cfg4_up,cfg4_down,oja,cfg4_adaptive_up,cfg4_adaptive_down,
+                                drop_in_layer} [--steps K] [--warmup W]
 
 The second form times one other configured shape alone (cfg1's fp32 nn.Linear, cfg4's 2048 <-> 8192
 layers at rank 16 through the projection engine, ...) and prints its own line, for profiling.
@@ -263,6 +265,108 @@ def oja_workload(x, q, steps, warmup):
     return out
 
 
+def adaptive_workload(name, d_in, d_out, steps, warmup):
+    """BASELINE config 4 through the adaptive engine: one Pythia-1.4B MLP layer (bf16, 16 x 2048 tokens),
+    int8 coefficients and residual values, rank from the sensitivity controller capped at 16, chunk
+    top-k 0.005, hybrid refresh every 10 steps (the post-forward Oja step taking Y from the save).
+    A step is the layer's whole forward + backward (the dense X W^T and G W products included, as
+    the layer runs them), with set_stacr_runtime_state advancing the schedule; eager launches (the
+    policy reads the device every step).  Steps cycle through the schedule, so the timed steps
+    include their share of refreshes."""
+    import torch
+    from torch import nn
+
+    from gpu_cases import make_activation, make_grad
+    from stacr_amd import _lib, adaptive
+
+    dev = torch.device("cuda:0")
+    rows = 16 * 2048
+    cfg = adaptive.STACRConfig(rank=16, rank_mode="sensitivity", rank_min=4, rank_max=16, rank_adjust_interval=5,
+                               residual_mode="topk", residual_budget=0.005, quantize_coefficients=True,
+                               quantize_residuals=True, residual_quantize_bits=8, freeze_basis_after_warmup=True,
+                               warmup_steps=0, refresh_trigger="hybrid", refresh_period=10,
+                               refresh_energy_threshold=0.1, basis_dtype="bfloat16")
+    torch.manual_seed(0)
+    model = nn.Sequential(nn.Linear(d_in, d_out)).to(dev, torch.bfloat16)
+    layer = adaptive.apply_adaptive_stacr(model, cfg, surface="all", min_features=1)[0]
+    x = make_activation(rows, d_in).to(dev, torch.bfloat16)
+    g = make_grad(rows, d_out).to(dev, torch.bfloat16)
+    counter = [0]
+
+    def step():
+        adaptive.set_stacr_runtime_state(model, counter[0])
+        counter[0] += 1
+        out = layer(x)
+        out.backward(g)
+        layer.zero_grad(set_to_none=True)
+
+    for _ in range(max(warmup, 1)):
+        step()
+    torch.cuda.synchronize()
+    refreshes0 = layer.layer_state.get("refresh_count_total", 0)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    refreshes = layer.layer_state.get("refresh_count_total", 0) - refreshes0
+    with _lib.KernelTimer(max_launches=64 * 10) as timer:
+        for _ in range(10):
+            step()
+    kern = {n: round(tot / 10 * 1e3, 3) for n, (tot, _c) in timer.results.items()}
+    return {"config": name, "tokens": rows, "d_in": d_in, "d_out": d_out, "ms_per_step": ms,
+            "tokens_per_s": rows / (ms * 1e-3), "refreshes_in_timed_steps": refreshes,
+            "active_rank": layer.layer_state.get("active_rank"),
+            "oja_steps_on_the_save_y": layer.layer_state.get("oja_given_y_steps", 0),
+            "library_kernels_us_per_step": kern,
+            "timing": "eager launches, whole layer step (dense products included)"}
+
+
+def drop_in_layer_workload(steps, warmup):
+    """One training step of the drop-in projection-engine layer as a user runs it: STACRLinear.from_linear
+    on the north-star Conv1D shape (1024 -> 4096, bf16, rank 8, global_topk 0.005, int8), default
+    update_interval 1, so every step refreshes the basis (Oja step + QR) before the save; forward and
+    backward of the layer, dense products included.  Eager launches."""
+    import torch
+
+    from gpu_cases import make_activation, make_grad
+    from stacr_amd import STACRLinear, _lib
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(D_IN, D_OUT).to(dev, torch.bfloat16)
+    layer = STACRLinear.from_linear(lin, rank=RANK, residual_budget=BUDGET, residual_bits=BITS,
+                                    residual_mode=MODE).train()
+    x = make_activation(N, D_IN, lognormal=True).to(dev, torch.bfloat16)
+    g = make_grad(N, D_OUT).to(dev, torch.bfloat16)
+    counter = [0]
+
+    def step():
+        layer.set_step(counter[0])
+        counter[0] += 1
+        y = layer(x)
+        y.backward(g)
+        lin.weight.grad = None
+        lin.bias.grad = None
+
+    for _ in range(max(warmup, 2)):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    with _lib.KernelTimer(max_launches=64 * 10) as timer:
+        for _ in range(10):
+            step()
+    kern = {n: round(tot / 10 * 1e3, 3) for n, (tot, _c) in timer.results.items()}
+    return {"config": "drop-in STACRLinear step, nn.Linear 1024->4096, N=8192, bf16, r=8, global_topk 0.005, int8, "
+                      "Oja refresh every step", "ms_per_step": ms, "tokens_per_s": N / (ms * 1e-3),
+            "library_kernels_us_per_step": kern,
+            "timing": "eager launches, whole layer step (refresh, dense products included)"}
+
+
 # The configured layers besides the headline, by name: (description, N, d_in, d_out, rank, budget,
 # mode, options).  Each runs through the same save + dW calls; `--workload NAME` times and prints
 # one of them alone (a line for profiling, not the contract line).
@@ -312,7 +416,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the other configured workloads")
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["oja"],
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["oja", "cfg4_adaptive_up", "cfg4_adaptive_down",
+                                                                "drop_in_layer"],
                     help="time only this other configured workload and print its line (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -328,6 +433,12 @@ def main() -> int:
         if args.workload == "oja":
             x = make_activation(N, D_IN, lognormal=True).to("cuda:0", torch.bfloat16)
             w = oja_workload(x, make_basis(D_IN, RANK).to("cuda:0", torch.bfloat16), args.steps, args.warmup)
+        elif args.workload.startswith("cfg4_adaptive"):
+            up = args.workload.endswith("up")
+            w = adaptive_workload("cfg4 adaptive engine, " + ("2048->8192" if up else "8192->2048"),
+                                  2048 if up else 8192, 8192 if up else 2048, args.steps, args.warmup)
+        elif args.workload == "drop_in_layer":
+            w = drop_in_layer_workload(args.steps, args.warmup)
         else:
             w = run_workload(args.workload, args.steps, args.warmup)
         print(json.dumps({"workload": args.workload, **w}), flush=True)
@@ -431,9 +542,14 @@ def main() -> int:
         extra_steps, extra_warm = max(10, args.steps // 4), max(3, args.warmup // 4)
         out["other_workloads"] = [run_workload(key, extra_steps, extra_warm) for key in ("c_proj", "turbo")]
         out["other_workloads"].append(oja_workload(x, q, extra_steps, extra_warm))
+        out["other_workloads"].append(drop_in_layer_workload(extra_steps, extra_warm))
+        for up in (True, False):  # config 4 through the adaptive engine (20 steps: two refresh periods)
+            out["other_workloads"].append(adaptive_workload(
+                "cfg4 adaptive engine, " + ("2048->8192" if up else "8192->2048"), 2048 if up else 8192,
+                8192 if up else 2048, 20, 3))
         for w in out["other_workloads"]:
-            print(f"[bench] {w['config']}: {w['ms_per_step'] * 1e3:.1f} us {w['kernels_us_per_step']}",
-                  file=sys.stderr, flush=True)
+            kern = w.get("kernels_us_per_step", w.get("library_kernels_us_per_step"))
+            print(f"[bench] {w['config']}: {w['ms_per_step'] * 1e3:.1f} us {kern}", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(x, q, g)

@@ -413,7 +413,8 @@ int adaptive_ws(const StacrSaveArgs &a, size_t *save, size_t *energy_off, size_t
     *save = a.rows * a.feats ? stacr_save_ws_layout(a, nullptr) : 0;
     *energy_off = (*save + 255) & ~(size_t)255;
     const int64_t slots = a.rows * a.feats ? stacr_save_energy_slots(a) : 0;
-    *total = *energy_off + stacr::hmax(stacr_energy_ws(), (size_t)slots * kEnergyStride * sizeof(float));
+    const size_t parts = ((size_t)slots * kEnergyStride * sizeof(float) + 255) & ~(size_t)255;
+    *total = *energy_off + stacr::hmax(stacr_energy_ws(), parts + stacr_energy_fold_ws());
     return STACR_OK;
 }
 
@@ -477,7 +478,10 @@ int adaptive_save_impl(const void *x, const void *q, int dtype, int64_t rows, in
     if (rc) return rc;
     if (!energy) return STACR_OK;
     // the projection pass formed the energy partials (one read of X), else a pass of its own
-    if (energy_fused) return stacr_energy_fold_launch(epart, slots, dtype, rows, rank, energy, s);
+    if (energy_fused) {
+        char *fold_ws = reinterpret_cast<char *>(epart) + (((size_t)slots * kEnergyStride * sizeof(float) + 255) & ~(size_t)255);
+        return stacr_energy_fold_launch(epart, slots, dtype, rows, rank, energy, fold_ws, s);
+    }
     return stacr_energy_launch(x, coeff_in ? coeff_in : coeff, dtype, rows, feats, rank, energy, epart, s);
 }
 

@@ -73,14 +73,26 @@ __device__ __forceinline__ int quant_one_dt(int dt, const QScale &q, float v, fl
     return (int)t;
 }
 
-__global__ void k_aq_amax(const void *__restrict__ v, int dt, int64_t n, uint32_t *__restrict__ amax)
+// Largest |v| as fp32 bits (NaN sorts above inf, as the integer order of the bits gives): per
+// workgroup, then one device atomic per workgroup (the grid is capped, so few reach one address).
+constexpr int kAmaxWgs = 256;
+__global__ __launch_bounds__(kBlock) void k_aq_amax(const void *__restrict__ v, int dt, int64_t n,
+                                                    uint32_t *__restrict__ amax)
 {
+    __shared__ uint32_t s_m[kWaves];
     uint32_t m = 0u;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
         m = max(m, __float_as_uint(load_any(v, dt, i)) & 0x7fffffffu);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
-    if ((threadIdx.x & 63) == 0 && m) atomicMax(amax, m);
+    if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t b = s_m[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) b = max(b, s_m[w]);
+        if (b) atomicMax(amax, b);
+    }
 }
 
 // bits 8: one int8 per value.  bits 4: (q + 8) nibbles, even entry low, odd length padded with 8.
@@ -353,6 +365,39 @@ __global__ void k_energy_ratio(int dt, float *__restrict__ out)
 // Thread (value v, stripe st) adds partials st, st + 16, ... in order, 16 loads at a time; the 16
 // stripes are then added in order.
 constexpr int kFoldStripes = 16;
+constexpr int kFoldSlices = 64;  // first stage: workgroups, each over a contiguous slice of partials
+
+// First stage: workgroup b adds the partials of its slice (stripes of 16 in order, then the stripes
+// in order) into part2[b] ([kEnergyStride]).
+__global__ __launch_bounds__(1024) void k_energy_fold_slices(const float *__restrict__ part, int64_t n, int rank,
+                                                             float *__restrict__ part2)
+{
+    __shared__ float s_t[kFoldStripes][64];
+    const int v = threadIdx.x & 63, st = threadIdx.x >> 6;
+    const int64_t per = (n + gridDim.x - 1) / gridDim.x;
+    const int64_t w0 = (int64_t)blockIdx.x * per, w1 = w0 + per < n ? w0 + per : n;
+    float t = 0.f;
+    if (v < 2 + rank) {
+        for (int64_t c0 = w0 + st; c0 < w1; c0 += 16 * kFoldStripes) {
+            float vals[16];
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                const int64_t w = c0 + (int64_t)c * kFoldStripes;
+                vals[c] = w < w1 ? part[w * kEnergyStride + v] : 0.f;
+            }
+#pragma unroll
+            for (int c = 0; c < 16; ++c) t += vals[c];
+        }
+    }
+    s_t[st][v] = t;
+    __syncthreads();
+    if (threadIdx.x < kEnergyStride) {
+        float sum = 0.f;
+        for (int j = 0; j < kFoldStripes; ++j) sum += s_t[j][threadIdx.x];
+        part2[(int64_t)blockIdx.x * kEnergyStride + threadIdx.x] = sum;
+    }
+}
+
 __global__ __launch_bounds__(1024) void k_energy_fold(const float *__restrict__ part, int64_t n, int dt, int64_t rows,
                                                       int rank, float *__restrict__ out)
 {
@@ -404,7 +449,10 @@ int stacr_aq_quantize_launch(const void *v, int dtype, int64_t n, int bits, void
 {
     uint32_t *amax = static_cast<uint32_t *>(ws);
     stacr_launch("k_fill_int", s, [&] { k_fill_int<<<1, 64, 0, s>>>(amax, 4, 1, 0); });
-    if (n > 0) stacr_launch("k_aq_amax", s, [&] { k_aq_amax<<<blocks_for(n), kBlock, 0, s>>>(v, dtype, n, amax); });
+    if (n > 0)
+        stacr_launch("k_aq_amax", s, [&] {
+            k_aq_amax<<<hmin(blocks_for(n), kAmaxWgs), kBlock, 0, s>>>(v, dtype, n, amax);
+        });
     const int64_t work = bits == 4 ? (n + 1) / 2 : n;
     stacr_launch("k_aq_quant", s, [&] {
         k_aq_quant<<<blocks_for(work), kBlock, 0, s>>>(v, dtype, n, bits, amax, data, static_cast<ScaleRec *>(scale));
@@ -505,8 +553,19 @@ int stacr_energy_launch(const void *x, const void *c, int dtype, int64_t rows, i
     return stacr_hip_check(hipGetLastError(), "energy");
 }
 
-int stacr_energy_fold_launch(const float *part, int64_t n, int dtype, int64_t rows, int rank, float *out, hipStream_t s)
+size_t stacr_energy_fold_ws() { return (size_t)kFoldSlices * kEnergyStride * sizeof(float); }
+
+int stacr_energy_fold_launch(const float *part, int64_t n, int dtype, int64_t rows, int rank, float *out, void *ws,
+                             hipStream_t s)
 {
+    if (n > 4 * kFoldSlices) {  // many partials: 64 slices in parallel first
+        float *part2 = static_cast<float *>(ws);
+        stacr_launch("k_energy_fold_slices", s, [&] {
+            k_energy_fold_slices<<<kFoldSlices, 1024, 0, s>>>(part, n, rank, part2);
+        });
+        part = part2;
+        n = kFoldSlices;
+    }
     stacr_launch("k_energy_fold", s, [&] { k_energy_fold<<<1, 1024, 0, s>>>(part, n, dtype, rows, rank, out); });
     return stacr_hip_check(hipGetLastError(), "energy fold");
 }

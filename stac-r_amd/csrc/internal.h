@@ -391,5 +391,6 @@ size_t stacr_energy_ws();
 int stacr_energy_launch(const void *x, const void *c, int dtype, int64_t rows, int64_t feats, int rank, float *out,
                         void *ws, hipStream_t s);
 // the energies from a save's per-workgroup partials (n of them, [kEnergyStride] each), added in order
-int stacr_energy_fold_launch(const float *part, int64_t n, int dtype, int64_t rows, int rank, float *out,
+size_t stacr_energy_fold_ws();
+int stacr_energy_fold_launch(const float *part, int64_t n, int dtype, int64_t rows, int rank, float *out, void *ws,
                              hipStream_t s);
