@@ -193,41 +193,50 @@ __global__ __launch_bounds__(kThreads) void k_tile_count(TileArgs a)
 }
 
 // ------------------------------------------------------------------ the plan
-// Bitonic sort / merge of one value per lane across a wave, descending in lane order (lane 0 the
-// largest): compare-exchange with the lane at distance j, keeping the larger value in the lane that
-// comes first in the direction of its run.
-__device__ __forceinline__ uint32_t cmpx(uint32_t v, int lane, int j, bool desc)
+// One level of the column selection: wave 0 finds, from the 256-bin histogram h (counted from the
+// top), the bin holding the need-th largest value and the need left inside it; *res = {bin, need}
+// (bin -1 when the histogram holds fewer than need values).  Every thread calls it.
+__device__ __forceinline__ void select_bin256(const uint32_t *__restrict__ h, uint32_t need, int2 *res)
 {
-    const uint32_t o = (uint32_t)__shfl_xor((int)v, j, 64);
-    const bool first = (lane & j) == 0;
-    const uint32_t hi = v > o ? v : o, lo = v > o ? o : v;
-    return first == desc ? hi : lo;
-}
-
-__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t v, int lane)
-{
+    const int tid = threadIdx.x, lane = tid & 63;
+    if (tid < 64) {
+        // lane l holds bins 255 - 4 l .. 252 - 4 l (from the top); inclusive sums across the lanes
+        uint32_t c[4], t = 0u;
 #pragma unroll
-    for (int k = 2; k <= 64; k <<= 1)
+        for (int i = 0; i < 4; ++i) {
+            c[i] = h[255 - 4 * lane - i];
+            t += c[i];
+        }
+        const uint32_t incl = wave_inclusive_scan(t);
+        const uint32_t before = incl - t;
+        const uint64_t hit = __ballot(incl >= need);
+        const int first = hit ? __ffsll((unsigned long long)hit) - 1 : -1;
+        if (lane == 0 && first < 0) *res = make_int2(-1, 0);
+        if (lane == first) {
+            uint32_t run = before;
 #pragma unroll
-        for (int j = k >> 1; j > 0; j >>= 1) v = cmpx(v, lane, j, (lane & k) == 0 || k == 64);
-    return v;
-}
-
-// a bitonic sequence across the wave -> descending
-__device__ __forceinline__ uint32_t wave_merge_desc(uint32_t v, int lane)
-{
-#pragma unroll
-    for (int j = 32; j > 0; j >>= 1) v = cmpx(v, lane, j, true);
-    return v;
+            for (int i = 0; i < 4; ++i) {
+                if (run + c[i] >= need) {
+                    *res = make_int2(255 - 4 * lane - i, (int)(need - run));
+                    break;
+                }
+                run += c[i];
+            }
+        }
+    }
+    __syncthreads();
 }
 
 template <bool BT8>
 __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
 {
     using BE = typename std::conditional<BT8, uint8_t, uint16_t>::type;  // one column-operand element
-    __shared__ uint32_t s_key[kPartMax];         // selection keys, then light offsets
+    __shared__ uint32_t s_key[kPartMax];         // colmap staging, then light offsets
     __shared__ int32_t s_slot[kPartMax];         // column slot of each feature of the part, or -1
-    __shared__ uint32_t s_mask[kPartMax * 16];   // light rows of each feature (512-bit bitmaps)
+    __shared__ uint32_t s_mask[16 * kPartMax];   // light rows of each feature, word w of feature f at w * kPartMax + f
+    __shared__ uint16_t s_pre[8 * kPartMax];     // light rows of feature f in words below 2 v, at v * kPartMax + f
+    __shared__ uint32_t s_h[256];
+    __shared__ int2 s_sel;
     __shared__ __attribute__((aligned(16))) BE s_bt[kNC * kBtStride];  // the block's column entries [slot][t]
     __shared__ uint32_t s_tot[kWaves];
 
@@ -261,39 +270,43 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         const bool one_round = e_b1 - e_b0 <= (int64_t)kBatch * kThreads;
         if (one_round) load_batch(e_b0);
 
-        // ---- column features: the nc largest of the unique keys count << 16 | (65535 - f) (count
-        // > 0).  Each wave sorts its 64 keys (descending, in registers); then four rounds merge the
-        // sorted lists pairwise, each keeping the 64 largest of the pair, until one list remains:
-        // its nc-th key is the smallest key taken.  The slots then follow the feature order.
-        uint32_t key = 0;
+        // ---- column features: the kNC largest of the unique keys count << 16 | (65535 - f) over the
+        // features with entries (count clamped to 65535): every feature with a clamped count above the
+        // kNC-th largest one's, c64, and the lowest features with count c64 as far as needed.  c64 by
+        // two radix levels of 8 bits (LDS histograms of the counts, the bin found by wave 0); then one
+        // scan over the features gives, packed, the features above c64 and those equal to it below f,
+        // which places every column at its slot in feature order.  (Every workgroup selects the same set.)
+        uint32_t cnt = 0;
         if (tid < pw) {
-            uint32_t cnt = 0;
 #pragma unroll
             for (int c = 0; c < a.n_hist; ++c) cnt += a.hist[(int64_t)c * a.d_in + plo + tid];
-            key = cnt ? ((cnt < 0xffffu ? cnt : 0xffffu) << 16) | (0xffffu - (uint32_t)tid) : 0u;
+            cnt = cnt < 0xffffu ? cnt : 0xffffu;
         }
         s_slot[tid] = -1;
-        const int lane = tid & 63, wave = tid >> 6;
-        uint32_t v = wave_sort_desc(key, lane);
-        for (int width = kWaves / 2; width >= 1; width /= 2) {
-            // wave w < width merges its list with wave w + width's
-            s_key[tid] = v;
+        if (tid < 256) s_h[tid] = 0u;
+        __syncthreads();
+        if (cnt) atomicAdd(&s_h[cnt >> 8], 1u);
+        __syncthreads();
+        select_bin256(s_h, (uint32_t)kNC, &s_sel);
+        const int2 l1 = s_sel;
+        uint32_t c64 = 0u, take_eq = 0u;  // (fewer than kNC features with entries: all of them, c64 = 0)
+        if (l1.x >= 0) {
+            if (tid < 256) s_h[tid] = 0u;
             __syncthreads();
-            if (wave < width) {
-                // a bitonic sequence holding the 64 largest of both lists: own[i] vs other[63 - i]
-                const uint32_t other = s_key[(wave + width) * 64 + 63 - lane];
-                v = wave_merge_desc(v > other ? v : other, lane);
-            }
+            if (cnt && (int)(cnt >> 8) == l1.x) atomicAdd(&s_h[cnt & 0xffu], 1u);
             __syncthreads();
+            select_bin256(s_h, (uint32_t)l1.y, &s_sel);
+            c64 = ((uint32_t)l1.x << 8) | (uint32_t)s_sel.x;
+            take_eq = (uint32_t)s_sel.y;
         }
-        if (tid < 64) s_key[tid] = v;
-        __syncthreads();
-        // the smallest key taken (0 when fewer than nc features have entries: every nonzero key)
-        const uint32_t kth = s_key[kNC - 1];
-        __syncthreads();
-        uint32_t n_col;
-        const uint32_t slot = block_exclusive_scan<kThreads>(key && key >= kth ? 1u : 0u, s_tot, &n_col);
-        const bool is_col = key && key >= kth && slot < (uint32_t)kNC;  // (the first bound always holds)
+        const bool above = l1.x >= 0 ? cnt > c64 : cnt > 0u;
+        const bool tie = l1.x >= 0 && cnt == c64;
+        uint32_t packed_all;
+        const uint32_t packed = block_exclusive_scan<kThreads>((above ? 1u : 0u) | (tie ? 1u << 16 : 0u), s_tot,
+                                                               &packed_all);
+        const uint32_t n_above = packed & 0xffffu, ties_below = packed >> 16;
+        const bool is_col = above || (tie && ties_below < take_eq);
+        const uint32_t slot = n_above + (ties_below < take_eq ? ties_below : take_eq);
         if (is_col) s_slot[tid] = (int32_t)slot;
         if (b == 0 && tid < kNC) s_key[tid] = 0xffffffffu;
         __syncthreads();
@@ -304,8 +317,11 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         }
 
         // ---- this block's entries: the column tile and the light bitmaps
-        for (int i = tid; i < kNC * kBtStride; i += kThreads) s_bt[i] = 0;
-        for (int i = tid; i < kPartMax * 16; i += kThreads) s_mask[i] = 0u;
+        static_assert((kNC * kBtStride * sizeof(BE)) % 16 == 0, "the column tile clears in 16-byte words");
+        for (int i = tid; i < (int)(kNC * kBtStride * sizeof(BE) / 16); i += kThreads)
+            reinterpret_cast<uint4 *>(s_bt)[i] = make_uint4(0u, 0u, 0u, 0u);
+        for (int i = tid; i < 16 * kPartMax / 4; i += kThreads)
+            reinterpret_cast<uint4 *>(s_mask)[i] = make_uint4(0u, 0u, 0u, 0u);
         __syncthreads();
         const int64_t t_base = (int64_t)b * kTB;
         const uint32_t d_in = (uint32_t)a.d_in;
@@ -334,7 +350,7 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
                     if constexpr (BT8) s_bt[s * kBtStride + tl] = (BE)(uint8_t)(int8_t)(int)val[k];
                     else s_bt[s * kBtStride + tl] = (BE)to_g16(val[k], a.g_dt);
                 } else {
-                    atomicOr(&s_mask[f * 16 + (tl >> 5)], 1u << (tl & 31));
+                    atomicOr(&s_mask[(tl >> 5) * kPartMax + f], 1u << (tl & 31));
                 }
             }
         }
@@ -345,7 +361,10 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         uint32_t lcnt = 0;
         if (tid < pw) {
 #pragma unroll
-            for (int w = 0; w < 16; ++w) lcnt += __popc(s_mask[tid * 16 + w]);
+            for (int w = 0; w < 16; ++w) {
+                if (!(w & 1)) s_pre[(w >> 1) * kPartMax + tid] = (uint16_t)lcnt;
+                lcnt += __popc(s_mask[w * kPartMax + tid]);
+            }
         }
         uint32_t n_light;
         const uint32_t off = block_exclusive_scan<kThreads>(lcnt, s_tot, &n_light);
@@ -371,8 +390,9 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
                 int tl;
                 int64_t f;
                 if (!place(fl[k], tl, f) || f < 0 || f >= pw || s_slot[f] >= 0) continue;
-                uint32_t r = __popc(s_mask[f * 16 + (tl >> 5)] & ((1u << (tl & 31)) - 1u));
-                for (int w = 0; w < (tl >> 5); ++w) r += __popc(s_mask[f * 16 + w]);
+                const int w = tl >> 5;
+                uint32_t r = s_pre[(w >> 1) * kPartMax + f] + __popc(s_mask[w * kPartMax + f] & ((1u << (tl & 31)) - 1u));
+                if (w & 1) r += __popc(s_mask[(w - 1) * kPartMax + f]);
                 reg[kOffWords + s_key[f] + r] = (uint32_t)tl | (to_g16(val[k], a.g_dt) << 16);
             }
         }
