@@ -10,14 +10,14 @@
 //     chunk's count of entries per input feature, and the first entry of every block of 512 token
 //     rows (entries are ascending, so block b starts where the block of the entries changes).
 //   k_tile_plan   one workgroup per (block of 512 rows, input part of <= 1024 features):
-//     * the part's column features: the 64 with most entries over the whole problem, ties to the
-//       lowest feature; every workgroup selects the same set;
+//     * (for k_tile_grad) the part's column features: the 64 with most entries over the whole
+//       problem, ties to the lowest feature; every workgroup selects the same set;
 //     * the block's column entries as dense matrix-core operands, in the order in which the lanes
 //       of the streaming kernel load them, zero where no entry was selected: int8 codes for 4 / 8-bit
 //       residuals (converted to G's dtype, exactly, as the streaming kernel loads them), else the
 //       values in G's dtype (rounded as the reference rounds them);
-//     * the block's other ("light") entries of the part as records t | value << 16, grouped by
-//       feature and within a feature by ascending t (each entry's place is its feature's offset
+//     * the block's other ("light") entries of the part as records t | (f mod 16) << 9 | value << 16,
+//       grouped by feature and within a feature by ascending t (each entry's place is its feature's offset
 //       plus the number of that feature's entries in earlier rows, counted from a per-feature row
 //       bitmap), so the order, and so every sum, is the same on every run;
 //     * part 0 also packs the block's coefficients [C | 1] as matrix-core operands.
@@ -32,6 +32,10 @@
 //       entries to 16 fp32 registers;
 //     and at the end reduces the per-wave tiles over the waves (in wave order) and writes
 //     dW[o][f] = sum_j M[o][j] Q[f][j] + scale * (light sum + column sum).
+//   k_tile_wide   in place of k_tile_grad for problems with at least 256 workgroups of 32 outputs
+//     (the plan then selects no column features: every entry is a light record): one workgroup per
+//     (32 output features, part), the same three-buffer stream of G tiles and records, every entry
+//     summed on the matrix cores in chunks of 32 records (see the kernel).
 #include <type_traits>
 
 #include "internal.h"
@@ -90,6 +94,7 @@ struct TileArgs {
     TileHdr *hdr;       // [n_blocks][n_parts]
     int32_t *colmap;    // [n_parts][kNC] feature in the part, or -1
     int sparse;         // nnz > 0: the plan builds the entry structures
+    int columns;        // the plan picks kNC column features per part (0: every entry is a light record)
 };
 
 // Words of the record array: every region's offsets and records (at most nnz records in all), the
@@ -277,7 +282,7 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         // scan over the features gives, packed, the features above c64 and those equal to it below f,
         // which places every column at its slot in feature order.  (Every workgroup selects the same set.)
         uint32_t cnt = 0;
-        if (tid < pw) {
+        if (tid < pw && a.columns) {
 #pragma unroll
             for (int c = 0; c < a.n_hist; ++c) cnt += a.hist[(int64_t)c * a.d_in + plo + tid];
             cnt = cnt < 0xffffu ? cnt : 0xffffu;
@@ -285,6 +290,7 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         s_slot[tid] = -1;
         if (tid < 256) s_h[tid] = 0u;
         __syncthreads();
+        // (without column features every count is 0 here: no feature is selected)
         if (cnt) atomicAdd(&s_h[cnt >> 8], 1u);
         __syncthreads();
         select_bin256(s_h, (uint32_t)kNC, &s_sel);
@@ -310,7 +316,7 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         if (is_col) s_slot[tid] = (int32_t)slot;
         if (b == 0 && tid < kNC) s_key[tid] = 0xffffffffu;
         __syncthreads();
-        if (b == 0) {
+        if (b == 0 && a.columns) {
             if (is_col) s_key[slot] = (uint32_t)tid;
             __syncthreads();
             if (tid < kNC) a.colmap[part * kNC + tid] = tid < kNC ? (int32_t)s_key[tid] : -1;
@@ -393,14 +399,14 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
                 const int w = tl >> 5;
                 uint32_t r = s_pre[(w >> 1) * kPartMax + f] + __popc(s_mask[w * kPartMax + f] & ((1u << (tl & 31)) - 1u));
                 if (w & 1) r += __popc(s_mask[(w - 1) * kPartMax + f]);
-                reg[kOffWords + s_key[f] + r] = (uint32_t)tl | (to_g16(val[k], a.g_dt) << 16);
+                reg[kOffWords + s_key[f] + r] = (uint32_t)tl | ((uint32_t)(f & 15) << 9) | (to_g16(val[k], a.g_dt) << 16);
             }
         }
         // the column operands in lane order: (tile i, wave w, lane l) holds rows 32 w + 8 (l / 16)
         // .. + 7 of column 16 i + l % 16, 8 elements
         using BV = typename std::conditional<BT8, uint2, uint4>::type;  // 8 elements
         BV *bt = static_cast<BV *>(a.bt) + ((int64_t)b * a.n_parts + part) * kNT * kWaves * 64;
-        for (int u = tid; u < kNT * kWaves * 64; u += kThreads) {
+        for (int u = tid; a.columns && u < kNT * kWaves * 64; u += kThreads) {
             const int l = u & 63, w = (u >> 6) & 15, i = u >> 10;
             bt[u] = *reinterpret_cast<const BV *>(s_bt + (16 * i + (l & 15)) * kBtStride + 32 * w + 8 * (l >> 4));
         }
@@ -922,6 +928,311 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
     if (a.dbias && part == 0 && tid < kOS) store_any(a.dbias, a.db_dt, o0 + tid, fin[tid * 16 + a.bias_col]);
 }
 
+// ------------------------------------------------------------------ the wide streaming kernel
+// For problems large enough to fill the chip with 32-output slabs: one workgroup per (32 outputs,
+// part), every entry of the part a light record (the plan selects no column features).  Wave w
+// owns features 64 w .. 64 w + 63 of the part as four 16-feature tiles, whose records of a block
+// are contiguous (grouped by feature, then by row).  The wave takes them 32 at a time as one
+// chunk: the G rows of the 32 records, gathered by two transposing reads per 16 outputs, are the
+// A operand; for each tile the chunk touches, the records of that tile scatter their values into a
+// zeroed [16 features][32 slots] LDS scratch at (feature in the tile, slot), the scratch read in
+// operand order is the B operand (cleared again after the read), and one v_mfma_f32_16x16x32 per
+// 16 outputs adds G[t_k][o] v_k to (o, feature).  So each wave's work is about its entry count / 32
+// matrix instructions, whatever the spread of the entries over the features, and the sums have a
+// fixed order (chunks in record order, blocks in order).
+constexpr int kWOS = 32;         // outputs per workgroup
+constexpr int kWRecBuf = 3584;   // record words of a stream buffer
+constexpr int kWRecCap = kWRecBuf - 32;  // blocks with at most this many records read them from LDS
+                                         // (a chunk reads up to 31 words past its first record)
+
+struct WideLds {
+    static constexpr size_t g = 0;                                  // [kTB][kWOS] G elements
+    static constexpr size_t rec = g + (size_t)kTB * kWOS * 2;       // [kWRecBuf] records
+    static constexpr size_t size = rec + (size_t)kWRecBuf * 4;      // 46 KiB
+    static_assert(size % 1024 == 0, "buffers start on 1 KiB boundaries");
+    static_assert(kWRecBuf % 256 == 0, "records are staged in 1 KiB copies");
+    static_assert(3 * size + kWaves * 1024 + kMaxBlocks * sizeof(TileHdr) <= 160 * 1024, "fits the CU's LDS");
+    static_assert(size >= (size_t)kWaves * 2 * 256 * 4, "every wave's two coefficient tiles fit a buffer");
+    static_assert(size >= (size_t)kPartMax * 16 * 2, "the part's Q rows fit a buffer");
+};
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_tile_wide(TileArgs a)
+{
+    using L = WideLds;
+    __shared__ __attribute__((aligned(1024))) unsigned char lds0[L::size];
+    __shared__ __attribute__((aligned(1024))) unsigned char lds1[L::size];
+    __shared__ __attribute__((aligned(1024))) unsigned char lds2[L::size];
+    __shared__ __attribute__((aligned(16))) uint16_t s_bs[kWaves * 512];  // per wave [16 features][32 slots]
+    __shared__ TileHdr s_hdr[kMaxBlocks];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, grp = lane >> 4;
+
+    // workgroup -> (o-slab, part), consecutive logical ids on one XCD (as k_tile_grad)
+    const int nwg = gridDim.x;
+    int logical = blockIdx.x;
+    if (nwg % 8 == 0) logical = (blockIdx.x % 8) * (nwg / 8) + blockIdx.x / 8;
+    const int part = logical % a.n_parts;
+    const int64_t o0 = (int64_t)(logical / a.n_parts) * kWOS;
+    const int64_t plo = (int64_t)part * a.part_w;
+    const int pw = (int)(a.d_in - plo < a.part_w ? a.d_in - plo : a.part_w);
+    const int nb = a.n_blocks;
+
+    for (int b = tid; b < nb; b += kThreads) s_hdr[b] = a.hdr[b * a.n_parts + part];
+    uint16_t *bs = s_bs + wave * 512;
+    reinterpret_cast<uint4 *>(bs)[lane] = make_uint4(0u, 0u, 0u, 0u);  // 1 KiB: the scratch starts zero
+    __syncthreads();
+
+    const uint32_t row_bytes = (uint32_t)a.d_out * 2;
+    const uint32_t g_lane_row = (uint32_t)tid >> 2;                        // + 256 for the second copy
+    const uint32_t g_lane_col = (uint32_t)o0 * 2 + 16u * (uint32_t)(tid & 3);
+    const uint32_t rec_lane = (256u * wave + 4u * lane) * 4;
+    const uint32_t cp_lane = ((wave * 4u + grp) * a.ncol + n) * 16;
+    const bool has_c = n < a.ncol;
+    const uint32_t regions = (uint32_t)nb * (uint32_t)a.n_parts;
+    const __amdgpu_buffer_rsrc_t r_cp = make_rsrc(a.cp, (uint64_t)nb * kTB * a.ncol * 2);
+    const __amdgpu_buffer_rsrc_t r_light = make_rsrc(a.light, record_words(a.nnz, regions) * 4);
+
+    // a block's header (record region and count) in scalar registers
+    struct Hdr {
+        uint32_t base, count;
+    };
+    auto hdr_of = [&](int blk) {
+        const int b = blk < nb ? blk : nb - 1;
+        return Hdr{(uint32_t)__builtin_amdgcn_readfirstlane(s_hdr[b].light_base),
+                   (uint32_t)__builtin_amdgcn_readfirstlane(s_hdr[b].light_count)};
+    };
+    // a block's records (the 1 KiB chunks it has, up to the cap) into buffer B
+    auto issue_records = [&](Hdr h, unsigned char *B) {
+        const uint32_t lbase = h.base, lcount = h.count;
+#pragma unroll
+        for (int h = 0; h < kWRecBuf / 256; h += kWaves) {
+            const int c = h + wave;
+            if (c < kWRecBuf / 256 && 256u * (uint32_t)c < lcount)
+                copy16(r_light, B + L::rec + (size_t)c * 1024, rec_lane + (uint32_t)h * 1024, (lbase + kOffWords) * 4);
+        }
+    };
+    // block `blk`'s G tile [512 rows][32 outputs] into buffer B: two 16-byte copies a lane
+    auto issue_g = [&](int blk, unsigned char *B) {
+        const uint32_t rows_here = (uint32_t)(a.rows - (int64_t)blk * kTB) < (uint32_t)kTB
+                                       ? (uint32_t)(a.rows - (int64_t)blk * kTB) : (uint32_t)kTB;
+        const __amdgpu_buffer_rsrc_t r_g =
+            make_rsrc(static_cast<const char *>(a.g) + (size_t)blk * kTB * row_bytes, (uint64_t)rows_here * row_bytes);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t row = g_lane_row + 256u * h;
+            const uint32_t r = row < rows_here - 1 ? row : rows_here - 1;
+            copy16(r_g, B + L::g + (size_t)h * 16384 + (size_t)wave * 1024, r * row_bytes + g_lane_col, 0u);
+        }
+    };
+    // this wave's tile bounds of block `blk`: lane i <= 4 loads the offset of feature 64 w + 16 i
+    // (the part's end past pw), clamped to the block's records
+    auto load_bounds = [&](Hdr h) {
+        const uint32_t lbase = h.base, lcount = h.count;
+        const int f = 64 * wave + 16 * (lane < 5 ? lane : 4);
+        const uint32_t fo = (uint32_t)(f < pw ? f : pw);
+        const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(r_light, (int)(fo * 4), (int)(lbase * 4), 0);
+        return v < lcount ? v : lcount;
+    };
+    auto load_c = [&](int blk) {
+        uint4 c = make_uint4(0u, 0u, 0u, 0u);
+        if (has_c) c = load16(r_cp, cp_lane, (uint32_t)blk * kTB * a.ncol * 2);
+        return c;
+    };
+
+    f32x4 acc_m[2], acc[4][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        acc_m[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i][j] = acc_m[j];
+    }
+
+    // the block in buffer B: M = G^T [C | 1] over the wave's 32 rows, then the wave's four tiles
+    auto run_block = [&](Hdr h, const unsigned char *B, uint4 cop, uint32_t bnd) {
+        const uint16_t *gt = reinterpret_cast<const uint16_t *>(B + L::g);
+        {
+            const int kk = 32 * wave + 8 * grp;
+            const uint16_t *pa = gt + (kk + (n >> 2)) * kWOS + (n & 3) * 4;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint2 lo = lds_tr16(pa + 16 * j), hi = lds_tr16(pa + 16 * j + 4 * kWOS);
+                acc_m[j] = mfma16<DT>(make_uint4(lo.x, lo.y, hi.x, hi.y), cop, acc_m[j]);
+            }
+        }
+        const uint32_t *recs = reinterpret_cast<const uint32_t *>(B + L::rec);
+        const uint32_t lcount = h.count, lrec = h.base + kOffWords;
+        // Each chunk is 32 consecutive records of the wave's four tiles (records [b0, b4), grouped by
+        // feature), whatever tiles they belong to.  Lane 16 g + 4 q + h (h = 0, 1) holds the record
+        // of slot 8 g + 4 h + q (lanes with h = 2, 3 repeat h = 0, 1): so the quad's first two lanes
+        // hold slots k1 = 8 g + q and k1 + 4, the rows this lane's transposing reads need, and
+        // every slot < 32 is held once by a lane with h < 2, which scatters its value.
+        const int hq = lane & 1, q = (lane >> 2) & 3;
+        const uint32_t my = 8u * grp + 4u * hq + q;      // the slot this lane holds
+        const bool scatters = (lane & 2) == 0;
+        // the wave's chunks over its four tiles, in order: tile i spans records [b_i, b_i+1) and has
+        // c_i = ceil((b_i+1 - b_i) / 32) chunks (every value here is wave-uniform)
+        const uint32_t b0 = __builtin_amdgcn_readlane(bnd, 0);
+        uint32_t b1 = __builtin_amdgcn_readlane(bnd, 1), b2 = __builtin_amdgcn_readlane(bnd, 2);
+        uint32_t b3 = __builtin_amdgcn_readlane(bnd, 3), b4 = __builtin_amdgcn_readlane(bnd, 4);
+        b1 = b1 > b0 ? b1 : b0;
+        b2 = b2 > b1 ? b2 : b1;
+        b3 = b3 > b2 ? b3 : b2;
+        b4 = b4 > b3 ? b4 : b3;
+        const uint16_t *bsrd = bs + n * 32 + 8 * (grp ^ ((n >> 2) & 3));
+        const uint16_t *ga = gt + (n & 3) * 4;
+        // one chunk at records [e0, e0 + 32) (slots past b4 hold whatever follows: another wave's
+        // record or a stale word of the buffer; they are never scattered, and the G row they
+        // address is in the tile, t & 511): A = the G rows of slots k1 (.. + 3 over the group) and
+        // k1 + 4, per 16 outputs, read once; then for each tile the chunk overlaps, B = the tile's
+        // values at (feature in the tile, slot) of the zeroed scratch (rows of 32 slots, the four
+        // 16-byte groups of a row rotated by the feature's bits 2..3 so that a group's 16 lanes read
+        // distinct banks), cleared again after the read, and one product per 16 outputs
+        auto chunk = [&](uint32_t rec, uint32_t e0) {
+            const uint32_t r1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)rec, 0x00, 0xf, 0xf, false);
+            const uint32_t r2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)rec, 0x55, 0xf, 0xf, false);
+            const uint16_t *p1 = ga + (r1 & 511u) * kWOS;
+            const uint16_t *p2 = ga + (r2 & 511u) * kWOS;
+            const uint2 lo0 = lds_tr16(p1), hi0 = lds_tr16(p2);
+            const uint2 lo1 = lds_tr16(p1 + 16), hi1 = lds_tr16(p2 + 16);
+            const uint4 a0 = make_uint4(lo0.x, lo0.y, hi0.x, hi0.y), a1 = make_uint4(lo1.x, lo1.y, hi1.x, hi1.y);
+            const uint32_t fo = (rec >> 9) & 15u;
+            uint16_t *slot = bs + fo * 32 + 8 * ((my >> 3) ^ ((fo >> 2) & 3u)) + (my & 7);
+            const uint32_t e = e0 + my;
+            const uint32_t bb[5] = {b0, b1, b2, b3, b4};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (bb[i + 1] <= e0 || bb[i] >= e0 + 32) continue;  // (wave-uniform)
+                const bool live = scatters && e >= bb[i] && e < bb[i + 1];
+                if (live) *slot = (uint16_t)(rec >> 16);
+                const uint4 bop = *reinterpret_cast<const uint4 *>(bsrd);
+                if (live) *slot = 0;
+                acc[i][0] = mfma16<DT>(a0, bop, acc[i][0]);
+                acc[i][1] = mfma16<DT>(a1, bop, acc[i][1]);
+            }
+        };
+        // the chunks in order, the next chunk's record fetched before the current one runs; `fetch`
+        // reads staged records from LDS, or (a block with more records than staged) from memory
+        auto stream = [&](auto fetch) {
+            uint32_t nx = fetch(b0);
+            for (uint32_t e0 = b0; e0 < b4; e0 += 32) {
+                const uint32_t cur = nx;
+                nx = fetch(e0 + 32 < b4 ? e0 + 32 : b4);
+                chunk(cur, e0);
+            }
+        };
+        if (lcount <= (uint32_t)kWRecCap) {
+            // (e0 <= the record count <= kWRecCap: every index is inside the buffer)
+            stream([&](uint32_t e0) { return recs[e0 + my]; });
+        } else {
+            stream([&](uint32_t e0) {
+                const uint32_t e = e0 + my;
+                return a.light[lrec + (e < lcount ? e : lcount - 1)];
+            });
+        }
+    };
+
+    // ---- the stream: block blk runs in buffer blk % 3 while block blk + 2 is copied into buffer
+    // (blk + 2) % 3; the operands (C, tile bounds) of block blk + 1 are loaded into registers
+    // (the headers of blocks blk, blk + 1 and blk + 2 are carried in scalar registers; the next one
+    // is read from LDS at the end of a step, where its latency overlaps the barrier)
+    Hdr h0 = hdr_of(0), h1 = hdr_of(1), h2 = hdr_of(2);
+    uint4 cop = load_c(0);
+    uint32_t bnd = load_bounds(h0);
+    issue_records(h0, lds0);
+    issue_g(0, lds0);
+    if (nb > 1) {
+        issue_records(h1, lds1);
+        issue_g(1, lds1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    auto step = [&](int blk, const unsigned char *__restrict__ B, unsigned char *__restrict__ B2) {
+        const uint4 c_here = cop;
+        const uint32_t b_here = bnd;
+        cop = load_c(blk + 1);
+        bnd = load_bounds(h1);
+        if (blk + 2 < nb) issue_records(h2, B2);
+        run_block(h0, B, c_here, b_here);
+        issue_g(blk + 2 < nb ? blk + 2 : nb - 1, B2);
+        const Hdr h3 = hdr_of(blk + 3);
+        __builtin_amdgcn_s_waitcnt(0x0072);  // vmcnt(2) lgkmcnt(0): only the two G copies stay in flight
+        asm volatile("s_barrier" ::: "memory");
+        h0 = h1;
+        h1 = h2;
+        h2 = h3;
+    };
+    int cb = 0;
+    for (int blk = 0; blk + 1 < nb; ++blk, cb = cb == 2 ? 0 : cb + 1) {
+        unsigned char *B = cb == 0 ? lds0 : cb == 1 ? lds1 : lds2;
+        unsigned char *B2 = cb == 0 ? lds2 : cb == 1 ? lds0 : lds1;
+        step(blk, B, B2);
+    }
+    run_block(h0, cb == 0 ? lds0 : cb == 1 ? lds1 : lds2, cop, bnd);
+
+    const float scale = a.bits ? *a.scale : 1.f;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    // ---- M over the waves, in wave order: every wave's two tiles staged in lds0, sums in lds2;
+    // the part's Q rows (16-bit) in lds1
+    float *stage = reinterpret_cast<float *>(lds0);
+    float *fin = reinterpret_cast<float *>(lds2);  // [2][16 o][16 j]
+    uint16_t *sq = reinterpret_cast<uint16_t *>(lds1);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) stage[(wave * 2 + j) * 256 + (4 * grp + r) * 16 + n] = acc_m[j][r];
+    const uint16_t *q = static_cast<const uint16_t *>(a.q);
+    for (int e = tid; e < pw * a.rank; e += kThreads) sq[e] = q[plo * a.rank + e];
+    __syncthreads();
+    if (tid < 512) {
+        float sum = 0.f;
+        for (int w = 0; w < kWaves; ++w) sum += stage[(w * 2 + (tid >> 8)) * 256 + (tid & 255)];
+        fin[tid] = sum;
+    }
+    __syncthreads();
+
+    // ---- dW: lane (n, grp) of wave w holds, per tile i and o-tile j, outputs 16 j + 4 grp .. + 3 of
+    // feature 64 w + 16 i + n
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int fl = 64 * wave + 16 * i + n;
+        if (fl >= pw) continue;
+        const int64_t f = plo + fl;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float out[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) out[r] = scale * acc[i][j][r];
+            for (int c = 0; c < a.rank; ++c) {
+                const float qc = g16_to_f<DT>(sq[fl * a.rank + c]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) out[r] = fmaf(fin[j * 256 + (4 * grp + r) * 16 + c], qc, out[r]);
+            }
+            const int64_t o = o0 + 16 * j + 4 * grp;
+            if (a.transposed) {  // Conv1D: dW is d_in x d_out, four consecutive outputs
+                if (a.dw_dt == STACR_DTYPE_F32) {
+                    *reinterpret_cast<float4 *>(static_cast<float *>(a.dw) + f * a.d_out + o) =
+                        make_float4(out[0], out[1], out[2], out[3]);
+                } else {
+                    const bool bf = a.dw_dt == STACR_DTYPE_BF16;
+                    uint32_t wv[2];
+#pragma unroll
+                    for (int k = 0; k < 2; ++k)
+                        wv[k] = bf ? (f_to_bf16_bits(out[2 * k]) | (f_to_bf16_bits(out[2 * k + 1]) << 16))
+                                   : (f_to_f16_bits(out[2 * k]) | (f_to_f16_bits(out[2 * k + 1]) << 16));
+                    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(a.dw) + f * a.d_out + o) = make_uint2(wv[0], wv[1]);
+                }
+            } else {  // nn.Linear: dW is d_out x d_in
+#pragma unroll
+                for (int r = 0; r < 4; ++r) store_any(a.dw, a.dw_dt, (o + r) * a.d_in + f, out[r]);
+            }
+        }
+    }
+    if (a.dbias && part == 0 && tid < kWOS) store_any(a.dbias, a.db_dt, o0 + tid, fin[(tid >> 4) * 256 + (tid & 15) * 16 + a.bias_col]);
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ host side
@@ -931,7 +1242,12 @@ struct TileGeom {
     int n_blocks, n_parts, part_w, ncol, bias_col;
     int gb;  // bytes of a G / C element
     bool sparse, bt8;
+    bool wide;  // k_tile_wide (every entry a light record, no column operands) in place of k_tile_grad
 };
+
+// Workgroups of the wide kernel that make it the better choice: at least one per CU (256) with
+// 32-output slabs.  Below that the 16-output kernel's twice as many workgroups fill the chip better.
+constexpr int kWideMinWgs = 256;
 
 bool tile_geom(const StacrGradArgs &a, TileGeom *g)
 {
@@ -956,6 +1272,7 @@ bool tile_geom(const StacrGradArgs &a, TileGeom *g)
     g->gb = f32 ? 4 : 2;
     g->sparse = a.nnz > 0;
     g->bt8 = a.bits != 0;
+    g->wide = g->sparse && !f32 && a.d_out % kWOS == 0 && (a.d_out / kWOS) * g->n_parts >= kWideMinWgs;
     return true;
 }
 
@@ -971,7 +1288,7 @@ size_t tile_layout(int64_t nnz, int64_t d_in, const TileGeom &g, size_t *off)
     take(TW_HIST, g.sparse ? (size_t)kChunks * d_in * 4 : 0);
     take(TW_BSTART, g.sparse ? ((size_t)g.n_blocks + 1) * 4 : 0);
     take(TW_CP, (size_t)g.n_blocks * kTB * g.ncol * g.gb);
-    take(TW_BT, g.sparse ? bt_bytes : 0);
+    take(TW_BT, g.sparse && !g.wide ? bt_bytes : 0);
     take(TW_LIGHT, g.sparse ? (size_t)record_words(nnz, regions) * 4 : 0);
     take(TW_HDR, g.sparse ? regions * sizeof(TileHdr) : 0);
     take(TW_COLMAP, g.sparse ? (size_t)g.n_parts * kNC * 4 : 0);
@@ -1019,6 +1336,7 @@ size_t stacr_tiles_ws_bound(int64_t rows, int64_t d_out, int64_t d_in, int64_t n
     g.gb = 4;       // fp32 coefficient operands
     g.sparse = nnz > 0;
     g.bt8 = false;  // the wider column-operand form
+    g.wide = false;  // (with column operands: the larger layout)
     size_t off[TW_N];
     return tile_layout(nnz, d_in, g, off);
 }
@@ -1073,6 +1391,7 @@ int stacr_tiles_launch(const StacrGradArgs &a)
         t.colmap = reinterpret_cast<int32_t *>(ws + off[TW_COLMAP]);
     }
     t.sparse = g.sparse ? 1 : 0;
+    t.columns = g.wide ? 0 : 1;
     hipStream_t s = a.stream;
     int rc;
     if (g.sparse && !census) {
@@ -1085,6 +1404,14 @@ int stacr_tiles_launch(const StacrGradArgs &a)
     else stacr_launch("k_tile_plan", s, [&] { k_tile_plan<false><<<pgrid, kThreads, 0, s>>>(t); });
     rc = stacr_hip_check(hipGetLastError(), "weight_grad plan");
     if (rc) return rc;
+    if (g.wide) {
+        const int nw = (int)(a.d_out / kWOS) * g.n_parts;
+        if (a.dtype == STACR_DTYPE_BF16)
+            stacr_launch("k_tile_wide", s, [&] { k_tile_wide<STACR_DTYPE_BF16><<<nw, kThreads, 0, s>>>(t); });
+        else
+            stacr_launch("k_tile_wide", s, [&] { k_tile_wide<STACR_DTYPE_F16><<<nw, kThreads, 0, s>>>(t); });
+        return stacr_hip_check(hipGetLastError(), "weight_grad wide matrix-core kernel");
+    }
     const int nwg = (int)(a.d_out / kOS) * g.n_parts;
     if (a.dtype == STACR_DTYPE_F32) return launch_tile_grad<STACR_DTYPE_F32, true, true>(t, nwg, s);
     return a.dtype == STACR_DTYPE_BF16 ? launch_tile_grad_dt<STACR_DTYPE_BF16>(t, g, nwg, s)

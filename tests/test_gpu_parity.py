@@ -334,6 +334,11 @@ GRAD_CASES = [
     ("f16_bits4_rank3", 300, 40, 70, 3, "f16", False, 4, "chunk_topk", 0.1, False),
     ("fp32_lowrank_only", 256, 128, 96, 8, "f32", True, 8, "chunk_topk", 0.0, False),
     ("bf16_rank16", 1024, 2048, 512, 16, "bf16", False, 8, "chunk_topk", 0.005, False),
+    # the wide kernel (32-output slabs, every entry through matrix-core chunks): cfg4's two layer
+    # shapes at 4096 rows with stored values and int8 codes, and fp16 with nibbles over parts of 750
+    ("cfg4_up_wide_bf16_values", 4096, 2048, 8192, 16, "bf16", False, 0, "chunk_topk", 0.005, False),
+    ("cfg4_down_wide_bf16_conv1d", 4096, 8192, 2048, 16, "bf16", True, 8, "chunk_topk", 0.005, False),
+    ("wide_f16_bits4_parts750_rank5", 2048, 1500, 8192, 5, "f16", False, 4, "chunk_topk", 0.01, True),
 ]
 
 
@@ -355,10 +360,10 @@ def test_weight_grad_matches_oracle(dev, case):
     else:
         oidx = idx.cpu().numpy().astype(np.int64)
         orc.check_indices(oidx, rows * d_in, ascending=True)
-        raw = data.cpu().numpy()
         if bits == 0:
             ovals = _np(data)
         else:
+            raw = data.cpu().numpy()
             ovals = orc.dequantize(raw.view(np.int8) if bits == 8 else raw, np.float32(scale.item()), bits, oidx.size)
     odw, odb = orc.weight_grad(_np(g), _np(coeff), _np(q), oidx, ovals, d_in)
     got = _np(dw)
@@ -396,6 +401,35 @@ def test_weight_grad_heavy_features_and_many_rounds(dev, dtype, budget, rank):
     odw, odb = orc.weight_grad(_np(g), _np(coeff), _np(q), oidx, ovals, d_in)
     assert rel_l2(_np(dw), odw) <= TOL[dtype]
     assert rel_l2(_np(db), odb) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("budget,bits", [(0.03, 8), (0.2, 0)])
+def test_weight_grad_wide_kernel_heavy_features(dev, budget, bits):
+    """The wide kernel (d_out 8192: 256 workgroups of 32 outputs) with a few features carrying
+    most entries (tiles of many chunks) and, at budget 0.2, more records a block than it stages in
+    LDS (the rest read from memory)."""
+    from stacr_amd import kernels
+
+    announce("grad wide heavy", budget, bits)
+    rows, d_in, d_out, rank = 2048, 1024, 8192, 8
+    x = make_activation(rows, d_in)
+    x[:, 7] *= 60.0
+    x[:, 300] *= 25.0
+    x[:, 1000:1004] *= 10.0
+    x = x.to(dev, torch.bfloat16)
+    q = make_basis(d_in, rank).to(dev, torch.bfloat16)
+    g = make_grad(rows, d_out).to(dev, torch.bfloat16)
+    coeff, idx, data, scale = kernels.save(x, q, mode="chunk_topk", budget=budget, chunk_rows=512, bits=bits)
+    assert idx.numel() // 4 > 3584 or budget < 0.1  # records a block past the staged ones
+    dw, db = kernels.weight_grad(g, coeff, q, (idx, data, scale), bits, False, torch.bfloat16, torch.bfloat16)
+    oidx = idx.cpu().numpy().astype(np.int64)
+    ovals = (_np(data) if bits == 0 else
+             orc.dequantize(data.cpu().numpy().view(np.int8), np.float32(scale.item()), 8, oidx.size))
+    assert np.count_nonzero(oidx % d_in == 7) > 0.8 * rows
+    odw, odb = orc.weight_grad(_np(g), _np(coeff), _np(q), oidx, ovals, d_in)
+    assert rel_l2(_np(dw), odw) <= TOL["bf16"]
+    assert_rounded_once_bf16(_np(dw), odw, what="dW")
+    assert rel_l2(_np(db), odb) <= TOL["bf16"]
 
 
 @pytest.mark.parametrize("where", ["head", "tail", "middle"])
@@ -474,16 +508,17 @@ def test_weight_grad_matrix_core_shapes(dev, rows, d_in, d_out, rank, bias, dtyp
         assert db is None
 
 
-@pytest.mark.parametrize("dtype,transposed", [("bf16", True), ("f16", False), ("f32", False)])
-def test_weight_grad_matrix_core_path_is_deterministic(dev, dtype, transposed):
+@pytest.mark.parametrize("dtype,transposed,d_out", [("bf16", True, 1024), ("f16", False, 1024), ("f32", False, 1024),
+                                                   ("bf16", True, 8192), ("f16", False, 8192)])
+def test_weight_grad_matrix_core_path_is_deterministic(dev, dtype, transposed, d_out):
     """The matrix-core path at rank 8 (16-bit G; fp32 G with int8 codes): every sum of the weight
     gradient has a fixed order (light entries by one owner thread in ascending row order, per-wave
     tiles reduced in wave order), so repeated calls agree bit for bit, with int32 and int64 indices
     alike."""
     from stacr_amd import kernels
 
-    announce("grad determinism", dtype, transposed)
-    rows, d_in, d_out, rank = 4096, 1024, 1024, 8
+    announce("grad determinism", dtype, transposed, d_out)
+    rows, d_in, rank = 4096, 1024, 8  # (d_out 8192: the wide kernel)
     x = make_activation(rows, d_in, lognormal=True).to(dev, DT[dtype])
     q = make_basis(d_in, rank).to(dev, DT[dtype])
     g = make_grad(rows, d_out).to(dev, DT[dtype])
@@ -748,6 +783,7 @@ def test_turbo_step_50_freezes_basis_and_drops_residual(dev, full):
     (64, 1024, 256, "chunk_topk", 0.0001, 1, "bf16", False),         # one entry a row, trimmed to 7: no census
     (1000, 1024, 256, "chunk_topk", 0.005, 100, "bf16", True),       # chunks of 100 rows, 4-row workgroups
     (2048, 1024, 512, "global_topk", 0.005, 512, "f16", False),      # fp16 keeps the stored residual
+    (4096, 1024, 8192, "global_topk", 0.005, 512, "bf16", True),     # the wide weight-gradient kernel
 ])
 def test_entry_census_matches_count_and_gives_the_same_weight_gradient(dev, rows, d_in, d_out, mode, budget, chunk,
                                                                        dtype, expect):
