@@ -993,23 +993,32 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
     const __amdgpu_buffer_rsrc_t r_cp = make_rsrc(a.cp, (uint64_t)nb * kTB * a.ncol * 2);
     const __amdgpu_buffer_rsrc_t r_light = make_rsrc(a.light, record_words(a.nnz, regions) * 4);
 
-    // a block's header (record region and count) in scalar registers
-    struct Hdr {
-        uint32_t base, count;
+    // A block with more records than a buffer stages runs as several windows of kWRecCap records
+    // over the same G tile ("steps"): step = (block, window), in order.  A step's state in scalar
+    // registers: its block, window, record region and count.
+    struct Step {
+        int blk;
+        uint32_t w, base, count;
     };
-    auto hdr_of = [&](int blk) {
+    auto windows = [&](uint32_t count) { return count <= (uint32_t)kWRecCap ? 1u : (count + kWRecCap - 1) / kWRecCap; };
+    auto step_at = [&](int blk, uint32_t w) {
         const int b = blk < nb ? blk : nb - 1;
-        return Hdr{(uint32_t)__builtin_amdgcn_readfirstlane(s_hdr[b].light_base),
-                   (uint32_t)__builtin_amdgcn_readfirstlane(s_hdr[b].light_count)};
+        return Step{blk, w, (uint32_t)__builtin_amdgcn_readfirstlane(s_hdr[b].light_base),
+                    (uint32_t)__builtin_amdgcn_readfirstlane(s_hdr[b].light_count)};
     };
-    // a block's records (the 1 KiB chunks it has, up to the cap) into buffer B
-    auto issue_records = [&](Hdr h, unsigned char *B) {
-        const uint32_t lbase = h.base, lcount = h.count;
+    auto next_step = [&](const Step &st) {
+        return st.w + 1 < windows(st.count) ? Step{st.blk, st.w + 1, st.base, st.count} : step_at(st.blk + 1, 0u);
+    };
+    // the step's records (window w: records [w kWRecCap, ..), the 1 KiB chunks it has) into buffer B
+    auto issue_records = [&](const Step &st, unsigned char *B) {
+        const uint32_t first = st.w * (uint32_t)kWRecCap;
+        const uint32_t left = st.count - first;
 #pragma unroll
         for (int h = 0; h < kWRecBuf / 256; h += kWaves) {
             const int c = h + wave;
-            if (c < kWRecBuf / 256 && 256u * (uint32_t)c < lcount)
-                copy16(r_light, B + L::rec + (size_t)c * 1024, rec_lane + (uint32_t)h * 1024, (lbase + kOffWords) * 4);
+            if (c < kWRecBuf / 256 && 256u * (uint32_t)c < left)
+                copy16(r_light, B + L::rec + (size_t)c * 1024, rec_lane + (uint32_t)h * 1024,
+                       (st.base + kOffWords + first) * 4);
         }
     };
     // block `blk`'s G tile [512 rows][32 outputs] into buffer B: two 16-byte copies a lane
@@ -1025,18 +1034,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
             copy16(r_g, B + L::g + (size_t)h * 16384 + (size_t)wave * 1024, r * row_bytes + g_lane_col, 0u);
         }
     };
-    // this wave's tile bounds of block `blk`: lane i <= 4 loads the offset of feature 64 w + 16 i
-    // (the part's end past pw), clamped to the block's records
-    auto load_bounds = [&](Hdr h) {
-        const uint32_t lbase = h.base, lcount = h.count;
+    // this wave's tile bounds of the step's block: lane i <= 4 loads the offset of feature
+    // 64 w + 16 i (the part's end past pw), clamped to the block's records
+    auto load_bounds = [&](const Step &st) {
         const int f = 64 * wave + 16 * (lane < 5 ? lane : 4);
         const uint32_t fo = (uint32_t)(f < pw ? f : pw);
-        const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(r_light, (int)(fo * 4), (int)(lbase * 4), 0);
-        return v < lcount ? v : lcount;
+        const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(r_light, (int)(fo * 4), (int)(st.base * 4), 0);
+        return v < st.count ? v : st.count;
     };
     auto load_c = [&](int blk) {
         uint4 c = make_uint4(0u, 0u, 0u, 0u);
-        if (has_c) c = load16(r_cp, cp_lane, (uint32_t)blk * kTB * a.ncol * 2);
+        if (has_c) c = load16(r_cp, cp_lane, (uint32_t)(blk < nb ? blk : nb - 1) * kTB * a.ncol * 2);
         return c;
     };
 
@@ -1048,10 +1056,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
         for (int i = 0; i < 4; ++i) acc[i][j] = acc_m[j];
     }
 
-    // the block in buffer B: M = G^T [C | 1] over the wave's 32 rows, then the wave's four tiles
-    auto run_block = [&](Hdr h, const unsigned char *B, uint4 cop, uint32_t bnd) {
+    // Each chunk is 32 consecutive records of the wave's four tiles (records [b0, b4), grouped by
+    // feature), whatever tiles they belong to.  Lane 16 g + 4 q + h (h = 0, 1) holds the record
+    // of slot 8 g + 4 h + q (lanes with h = 2, 3 repeat h = 0, 1): so the quad's first two lanes
+    // hold slots k1 = 8 g + q and k1 + 4, the rows this lane's transposing reads need, and
+    // every slot < 32 is held once by a lane with h < 2, which scatters its value.
+    const uint32_t my = 8u * grp + 4u * (lane & 1) + ((lane >> 2) & 3);  // the slot this lane holds
+    const bool scatters = (lane & 2) == 0;
+    const uint16_t *bsrd_lane = s_bs + wave * 512 + n * 32 + 8 * (grp ^ ((n >> 2) & 3));
+    const uint32_t ga_lane = (n & 3) * 4;
+
+    // the step in buffer B: (window 0) M = G^T [C | 1] over the wave's 32 rows, then the wave's
+    // records of the window as chunks
+    auto run_step = [&](const Step &st, const unsigned char *B, uint4 cop, uint32_t bnd) {
         const uint16_t *gt = reinterpret_cast<const uint16_t *>(B + L::g);
-        {
+        if (st.w == 0) {
             const int kk = 32 * wave + 8 * grp;
             const uint16_t *pa = gt + (kk + (n >> 2)) * kWOS + (n & 3) * 4;
 #pragma unroll
@@ -1061,17 +1080,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
             }
         }
         const uint32_t *recs = reinterpret_cast<const uint32_t *>(B + L::rec);
-        const uint32_t lcount = h.count, lrec = h.base + kOffWords;
-        // Each chunk is 32 consecutive records of the wave's four tiles (records [b0, b4), grouped by
-        // feature), whatever tiles they belong to.  Lane 16 g + 4 q + h (h = 0, 1) holds the record
-        // of slot 8 g + 4 h + q (lanes with h = 2, 3 repeat h = 0, 1): so the quad's first two lanes
-        // hold slots k1 = 8 g + q and k1 + 4, the rows this lane's transposing reads need, and
-        // every slot < 32 is held once by a lane with h < 2, which scatters its value.
-        const int hq = lane & 1, q = (lane >> 2) & 3;
-        const uint32_t my = 8u * grp + 4u * hq + q;      // the slot this lane holds
-        const bool scatters = (lane & 2) == 0;
-        // the wave's chunks over its four tiles, in order: tile i spans records [b_i, b_i+1) and has
-        // c_i = ceil((b_i+1 - b_i) / 32) chunks (every value here is wave-uniform)
+        // tile i spans records [b_i, b_i+1) of the block (every value here is wave-uniform)
         const uint32_t b0 = __builtin_amdgcn_readlane(bnd, 0);
         uint32_t b1 = __builtin_amdgcn_readlane(bnd, 1), b2 = __builtin_amdgcn_readlane(bnd, 2);
         uint32_t b3 = __builtin_amdgcn_readlane(bnd, 3), b4 = __builtin_amdgcn_readlane(bnd, 4);
@@ -1079,15 +1088,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
         b2 = b2 > b1 ? b2 : b1;
         b3 = b3 > b2 ? b3 : b2;
         b4 = b4 > b3 ? b4 : b3;
-        const uint16_t *bsrd = bs + n * 32 + 8 * (grp ^ ((n >> 2) & 3));
-        const uint16_t *ga = gt + (n & 3) * 4;
-        // one chunk at records [e0, e0 + 32) (slots past b4 hold whatever follows: another wave's
-        // record or a stale word of the buffer; they are never scattered, and the G row they
-        // address is in the tile, t & 511): A = the G rows of slots k1 (.. + 3 over the group) and
-        // k1 + 4, per 16 outputs, read once; then for each tile the chunk overlaps, B = the tile's
-        // values at (feature in the tile, slot) of the zeroed scratch (rows of 32 slots, the four
-        // 16-byte groups of a row rotated by the feature's bits 2..3 so that a group's 16 lanes read
-        // distinct banks), cleared again after the read, and one product per 16 outputs
+        const uint32_t bb[5] = {b0, b1, b2, b3, b4};
+        // the window's records [w0, w1) staged from recs[0]; this wave's part of them [lo, hi)
+        const uint32_t w0 = st.w * (uint32_t)kWRecCap;
+        const uint32_t w1 = st.count - w0 < (uint32_t)kWRecCap ? st.count : w0 + kWRecCap;
+        uint16_t *bs = s_bs + wave * 512;
+        const uint16_t *ga = gt + ga_lane;
+        // this wave's records in the window
+        const uint32_t lo = b0 > w0 ? b0 : w0, hi0 = b4 < w1 ? b4 : w1, hi = hi0 > lo ? hi0 : lo;
+        // one chunk at records [e0, e0 + 32) (slots past hi hold whatever follows: another
+        // wave's record or a stale word of the buffer; they are never scattered, and the G row
+        // they address is in the tile, t & 511): A = the G rows of slots k1 (.. + 3 over the group)
+        // and k1 + 4, per 16 outputs, read once; then for each tile the chunk overlaps, B = the
+        // tile's values at (feature in the tile, slot) of the zeroed scratch (rows of 32 slots, the
+        // four 16-byte groups of a row rotated by the feature's bits 2..3 so that a group's 16
+        // lanes read distinct banks), cleared again after the read, and one product per 16 outputs
         auto chunk = [&](uint32_t rec, uint32_t e0) {
             const uint32_t r1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)rec, 0x00, 0xf, 0xf, false);
             const uint32_t r2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)rec, 0x55, 0xf, 0xf, false);
@@ -1099,76 +1114,77 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
             const uint32_t fo = (rec >> 9) & 15u;
             uint16_t *slot = bs + fo * 32 + 8 * ((my >> 3) ^ ((fo >> 2) & 3u)) + (my & 7);
             const uint32_t e = e0 + my;
-            const uint32_t bb[5] = {b0, b1, b2, b3, b4};
+            const uint32_t e_end = e0 + 32 < hi ? e0 + 32 : hi;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                if (bb[i + 1] <= e0 || bb[i] >= e0 + 32) continue;  // (wave-uniform)
-                const bool live = scatters && e >= bb[i] && e < bb[i + 1];
+                if (bb[i + 1] <= e0 || bb[i] >= e_end) continue;  // (wave-uniform)
+                const bool live = scatters && e >= bb[i] && e < bb[i + 1] && e < hi;
+                // The lanes exchange values through the scratch: wavefront-scope fences keep the
+                // compiler from moving one lane's store across another lane's load (a wave's LDS
+                // operations are performed in order, so they cost no wait).
                 if (live) *slot = (uint16_t)(rec >> 16);
-                const uint4 bop = *reinterpret_cast<const uint4 *>(bsrd);
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                const uint4 bop = *reinterpret_cast<const uint4 *>(bsrd_lane);
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
                 if (live) *slot = 0;
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
                 acc[i][0] = mfma16<DT>(a0, bop, acc[i][0]);
                 acc[i][1] = mfma16<DT>(a1, bop, acc[i][1]);
             }
         };
-        // the chunks in order, the next chunk's record fetched before the current one runs; `fetch`
-        // reads staged records from LDS, or (a block with more records than staged) from memory
-        auto stream = [&](auto fetch) {
-            uint32_t nx = fetch(b0);
-            for (uint32_t e0 = b0; e0 < b4; e0 += 32) {
+        // the chunks in order, the next chunk's record read before the current one runs (index
+        // e - w0 + my <= kWRecCap + 31: inside the buffer)
+        if (lo < hi) {
+            uint32_t nx = recs[lo - w0 + my];
+            for (uint32_t e0 = lo; e0 < hi; e0 += 32) {
                 const uint32_t cur = nx;
-                nx = fetch(e0 + 32 < b4 ? e0 + 32 : b4);
+                nx = recs[(e0 + 32 < hi ? e0 + 32 : hi) - w0 + my];
                 chunk(cur, e0);
             }
-        };
-        if (lcount <= (uint32_t)kWRecCap) {
-            // (e0 <= the record count <= kWRecCap: every index is inside the buffer)
-            stream([&](uint32_t e0) { return recs[e0 + my]; });
-        } else {
-            stream([&](uint32_t e0) {
-                const uint32_t e = e0 + my;
-                return a.light[lrec + (e < lcount ? e : lcount - 1)];
-            });
         }
     };
 
-    // ---- the stream: block blk runs in buffer blk % 3 while block blk + 2 is copied into buffer
-    // (blk + 2) % 3; the operands (C, tile bounds) of block blk + 1 are loaded into registers
-    // (the headers of blocks blk, blk + 1 and blk + 2 are carried in scalar registers; the next one
-    // is read from LDS at the end of a step, where its latency overlaps the barrier)
-    Hdr h0 = hdr_of(0), h1 = hdr_of(1), h2 = hdr_of(2);
+    // ---- the stream: step v runs in buffer v % 3 while step v + 2 is copied into buffer
+    // (v + 2) % 3; the operands (C, tile bounds) of step v + 1 are loaded into registers.  (The
+    // states of steps v, v + 1 and v + 2 are carried in scalar registers; a step past the last
+    // repeats the last block's copies into a buffer nothing reads any more.)
+    int n_steps = 0;
+    for (int b = 0; b < nb; ++b) n_steps += (int)windows((uint32_t)__builtin_amdgcn_readfirstlane(s_hdr[b].light_count));
+    Step s0 = step_at(0, 0u);
+    Step s1 = next_step(s0);
+    Step s2 = next_step(s1);
     uint4 cop = load_c(0);
-    uint32_t bnd = load_bounds(h0);
-    issue_records(h0, lds0);
+    uint32_t bnd = load_bounds(s0);
+    issue_records(s0, lds0);
     issue_g(0, lds0);
-    if (nb > 1) {
-        issue_records(h1, lds1);
-        issue_g(1, lds1);
+    if (n_steps > 1) {
+        issue_records(s1, lds1);
+        issue_g(s1.blk < nb ? s1.blk : nb - 1, lds1);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    auto step = [&](int blk, const unsigned char *__restrict__ B, unsigned char *__restrict__ B2) {
+    auto step = [&](int v, const unsigned char *__restrict__ B, unsigned char *__restrict__ B2) {
         const uint4 c_here = cop;
         const uint32_t b_here = bnd;
-        cop = load_c(blk + 1);
-        bnd = load_bounds(h1);
-        if (blk + 2 < nb) issue_records(h2, B2);
-        run_block(h0, B, c_here, b_here);
-        issue_g(blk + 2 < nb ? blk + 2 : nb - 1, B2);
-        const Hdr h3 = hdr_of(blk + 3);
+        cop = load_c(s1.blk);
+        bnd = load_bounds(s1);
+        if (v + 2 < n_steps) issue_records(s2, B2);
+        run_step(s0, B, c_here, b_here);
+        issue_g(s2.blk < nb ? s2.blk : nb - 1, B2);
+        const Step s3 = next_step(s2);
         __builtin_amdgcn_s_waitcnt(0x0072);  // vmcnt(2) lgkmcnt(0): only the two G copies stay in flight
         asm volatile("s_barrier" ::: "memory");
-        h0 = h1;
-        h1 = h2;
-        h2 = h3;
+        s0 = s1;
+        s1 = s2;
+        s2 = s3;
     };
     int cb = 0;
-    for (int blk = 0; blk + 1 < nb; ++blk, cb = cb == 2 ? 0 : cb + 1) {
+    for (int v = 0; v + 1 < n_steps; ++v, cb = cb == 2 ? 0 : cb + 1) {
         unsigned char *B = cb == 0 ? lds0 : cb == 1 ? lds1 : lds2;
         unsigned char *B2 = cb == 0 ? lds2 : cb == 1 ? lds0 : lds1;
-        step(blk, B, B2);
+        step(v, B, B2);
     }
-    run_block(h0, cb == 0 ? lds0 : cb == 1 ? lds1 : lds2, cop, bnd);
+    run_step(s0, cb == 0 ? lds0 : cb == 1 ? lds1 : lds2, cop, bnd);
 
     const float scale = a.bits ? *a.scale : 1.f;
     __builtin_amdgcn_s_waitcnt(0);
