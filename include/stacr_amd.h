@@ -466,8 +466,8 @@ int stacr_dequantize_rows_int8(const void *codes, const void *scales, int64_t ro
  * `sleep_us` device-side sleep so host enqueue gaps are not measured (up to max_launches
  * launches are recorded).  end synchronises the recorded events and returns, per kernel name in
  * first-launch order, the summed milliseconds and launch count (names: 64-byte slots).
- * A session belongs to the thread that began it (thread-local state): it records that thread's
- * launches only.  Do not enable during stream capture.
+ * A session is process wide: it records the launches of every thread (an autograd worker's
+ * included).  Do not enable during stream capture.
  */
 int stacr_profile_begin(int max_launches, double sleep_us);
 int stacr_profile_end(int max_kernels, char *names, double *total_ms, int *launches, int *n_kernels);

@@ -1,10 +1,12 @@
 // Per-kernel timing hook (benchmarking aid).  When enabled, every kernel the library launches is
 // bracketed by a pair of HIP events on its own stream.  A short device-side sleep is enqueued
 // before the start event so the GPU is still busy while the host enqueues start/kernel/stop: the
-// measured interval is then the kernel's execution, not host launch gaps.  The state is per
-// calling thread: a session records only the launches made by the thread that began it, and
-// threads never share it.
+// measured interval is then the kernel's execution, not host launch gaps.  A session is process
+// wide: it records the launches of every thread (a framework may launch from several, such as
+// an autograd worker), each thread's start/stop pair under one lock.
+#include <atomic>
 #include <map>
+#include <mutex>
 #include <string>
 #include <string.h>
 #include <vector>
@@ -19,14 +21,15 @@ struct Rec {
 };
 
 struct Session {
-    bool on = false;
-    bool open = false;
+    std::atomic<bool> on{false};
+    std::mutex mu;
     size_t max = 0;
     uint64_t sleep_ticks = 0;
-    std::vector<Rec> recs;
+    std::vector<Rec> recs;  // capacity reserved at begin: never reallocated while recording
 };
 
-thread_local Session t_session;
+Session g_session;
+thread_local long t_open = -1;  // this thread's record awaiting its stop event
 
 // Sleeps one wave until `ticks` of the constant wall clock have passed; the loop is bounded so it
 // ends even if the clock were to misbehave.
@@ -41,59 +44,65 @@ __global__ void k_gpu_sleep(uint64_t ticks)
 
 }  // namespace
 
-bool stacr_prof_on() { return t_session.on; }
+bool stacr_prof_on() { return g_session.on.load(std::memory_order_acquire); }
 
 void stacr_prof_before(hipStream_t s)
 {
-    t_session.open = false;
-    if (t_session.recs.size() >= t_session.max) return;
+    t_open = -1;
+    std::lock_guard<std::mutex> lock(g_session.mu);
+    if (!g_session.on.load(std::memory_order_relaxed) || g_session.recs.size() >= g_session.max) return;
     Rec r{nullptr, nullptr, nullptr};
     if (hipEventCreate(&r.start) != hipSuccess) return;
     if (hipEventCreate(&r.stop) != hipSuccess) {
         (void)hipEventDestroy(r.start);
         return;
     }
-    if (t_session.sleep_ticks) k_gpu_sleep<<<1, 64, 0, s>>>(t_session.sleep_ticks);
+    if (g_session.sleep_ticks) k_gpu_sleep<<<1, 64, 0, s>>>(g_session.sleep_ticks);
     (void)hipEventRecord(r.start, s);
-    t_session.recs.push_back(r);
-    t_session.open = true;
+    g_session.recs.push_back(r);
+    t_open = (long)g_session.recs.size() - 1;
 }
 
 void stacr_prof_after(const char *name, hipStream_t s)
 {
-    if (!t_session.open) return;
-    t_session.recs.back().name = name;
-    (void)hipEventRecord(t_session.recs.back().stop, s);
-    t_session.open = false;
+    if (t_open < 0) return;
+    std::lock_guard<std::mutex> lock(g_session.mu);
+    if ((size_t)t_open < g_session.recs.size()) {
+        g_session.recs[(size_t)t_open].name = name;
+        (void)hipEventRecord(g_session.recs[(size_t)t_open].stop, s);
+    }
+    t_open = -1;
 }
 
 extern "C" {
 
 int stacr_profile_begin(int max_launches, double sleep_us)
 {
-    if (t_session.on) return stacr_fail(STACR_ERR_INVALID, "profiling already active");
+    std::lock_guard<std::mutex> lock(g_session.mu);
+    if (g_session.on.load(std::memory_order_relaxed)) return stacr_fail(STACR_ERR_INVALID, "profiling already active");
     if (max_launches < 1) return stacr_fail(STACR_ERR_INVALID, "max_launches must be positive");
     int dev = 0, khz = 0;
     int rc = stacr_hip_check(hipGetDevice(&dev), "hipGetDevice");
     if (rc) return rc;
     rc = stacr_hip_check(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev), "wall clock rate");
     if (rc) return rc;
-    t_session.sleep_ticks = sleep_us > 0 ? (uint64_t)(sleep_us * (double)khz / 1000.0) : 0;
-    t_session.max = (size_t)max_launches;
-    t_session.recs.clear();
-    t_session.recs.reserve(t_session.max);
-    t_session.on = true;
+    g_session.sleep_ticks = sleep_us > 0 ? (uint64_t)(sleep_us * (double)khz / 1000.0) : 0;
+    g_session.max = (size_t)max_launches;
+    g_session.recs.clear();
+    g_session.recs.reserve(g_session.max);
+    g_session.on.store(true, std::memory_order_release);
     return STACR_OK;
 }
 
 int stacr_profile_end(int max_kernels, char *names, double *total_ms, int *launches, int *n_kernels)
 {
-    if (!t_session.on) return stacr_fail(STACR_ERR_INVALID, "profiling is not active");
-    t_session.on = false;
+    std::lock_guard<std::mutex> lock(g_session.mu);
+    if (!g_session.on.load(std::memory_order_relaxed)) return stacr_fail(STACR_ERR_INVALID, "profiling is not active");
+    g_session.on.store(false, std::memory_order_release);
     std::map<std::string, std::pair<double, int>> agg;
     std::vector<std::string> order;
     int rc = STACR_OK;
-    for (Rec &r : t_session.recs) {
+    for (Rec &r : g_session.recs) {
         if (!rc) rc = stacr_hip_check(hipEventSynchronize(r.stop), "hipEventSynchronize");
         float ms = 0.f;
         if (!rc && r.name) rc = stacr_hip_check(hipEventElapsedTime(&ms, r.start, r.stop), "hipEventElapsedTime");
@@ -109,7 +118,7 @@ int stacr_profile_end(int max_kernels, char *names, double *total_ms, int *launc
         (void)hipEventDestroy(r.start);
         (void)hipEventDestroy(r.stop);
     }
-    t_session.recs.clear();
+    g_session.recs.clear();
     if (rc) return rc;
     int n = 0;
     for (const std::string &name : order) {
