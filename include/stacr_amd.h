@@ -461,6 +461,17 @@ int stacr_dequantize_rows_int8(const void *codes, const void *scales, int64_t ro
                                int out_dtype, void *stream);
 
 /*
+ * Reduced QR of a tall fp32 matrix: replaces torch.linalg.qr(matrix, mode="reduced") in the basis
+ * re-orthonormalization (stacr/oja.py:8-11 orthonormalize; stacr/adaptive.py:3368 after the
+ * post-forward Oja step).  a: rows x cols, row-major fp32; q: rows x cols (row-major), r: cols x
+ * cols upper triangular (row-major; NULL: not written).  LAPACK's Householder convention (as
+ * torch's QR): R[j][j] = -sign(alpha_j) * norm, a reflector with tau = 0 where the column below the
+ * diagonal is zero; the same result on every run.  One workgroup, the matrix in LDS:
+ * STACR_ERR_UNSUPPORTED unless cols <= 16 and rows * cols <= 32768; cols <= rows.
+ */
+int stacr_qr(const float *a, int64_t rows, int cols, float *q, float *r, void *stream);
+
+/*
  * Kernel timing (benchmarking aid; no counterpart in the reference).  Between begin and end,
  * every kernel this library launches is bracketed by HIP events on its stream, preceded by a
  * `sleep_us` device-side sleep so host enqueue gaps are not measured (up to max_launches

@@ -1465,7 +1465,10 @@ class STACRLinear(nn.Module):
                     stepped = None
             if stepped is None:
                 _, stepped = kernels.oja_step(rows, current, float(lr))
-            q, r = torch.linalg.qr(stepped)
+            try:
+                q, r = kernels.qr(stepped)
+            except NotImplementedError:
+                q, r = torch.linalg.qr(stepped)
             if cfg.use_mgs:  # Gram-Schmidt's factor has a positive diagonal: the same Q up to column signs
                 q = q * torch.sign(torch.diagonal(r)).where(torch.diagonal(r) != 0, torch.ones_like(q[0]))
             self._set_basis(q[:, :current.shape[1]].to(self.basis_dtype))

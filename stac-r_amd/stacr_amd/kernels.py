@@ -302,6 +302,23 @@ def oja_step_given_y(x2d: torch.Tensor, q: torch.Tensor, y: torch.Tensor, lr: fl
     return update, out
 
 
+def qr(a: torch.Tensor):
+    """Reduced QR (Q, R) of a tall GPU matrix in fp32, LAPACK's sign convention (as
+    torch.linalg.qr): one workgroup (stacr_qr).  Raises NotImplementedError for shapes past its
+    limits (more than 16 columns, or more than 32768 elements)."""
+    require_gpu(a, "matrix")
+    if a.dim() != 2:
+        raise ValueError(f"qr takes a matrix, got {a.dim()} dimensions")
+    rows, cols = a.shape
+    if cols > rows:
+        raise ValueError(f"qr takes a tall matrix, got {rows} x {cols}")
+    a32 = a.to(torch.float32).contiguous()
+    q = torch.empty_like(a32)
+    r = torch.empty(cols, cols, dtype=torch.float32, device=a.device)
+    _lib.check(_lib.load().stacr_qr(_ptr(a32), rows, cols, _ptr(q), _ptr(r), _stream(a.device)), "stacr_qr")
+    return q, r
+
+
 def weight_grad(g2d: torch.Tensor, coeff: torch.Tensor, q: torch.Tensor, residual, bits: int, transposed: bool,
                 out_dtype: torch.dtype, bias_dtype: torch.dtype | None = None, census: torch.Tensor | None = None):
     """dW (and dbias when bias_dtype is given) from the saved factors (stacr/layers.py:172-198).
