@@ -250,9 +250,29 @@ class STACRLinear(nn.Module):
         return layer.train(module.training)
 
     # ---------------------------------------------------------------- step and schedule
+    # Host mirrors of the one-element buffers _step, basis_ready and _last_update_step, so a
+    # training step does not read them back from the GPU (each read waits for every queued
+    # kernel): a mirror holds the value, the tensor and its in-place version counter (host
+    # metadata), and is trusted only while both still match, so a write from outside (fill_,
+    # load_state_dict's copy_, a move to another device) forces one fresh read.
+    def _host_value(self, name: str):
+        t = getattr(self, name)
+        cached = self.__dict__.get("_host_" + name)
+        if cached is not None and cached[1] is t and cached[2] == t._version:
+            return cached[0]
+        v = t.item()
+        self.__dict__["_host_" + name] = (v, t, t._version)
+        return v
+
+    def _fill(self, name: str, value) -> None:
+        """Sets the buffer `name` (bool or int64) to `value` and its mirror with it."""
+        t = getattr(self, name)
+        t.fill_(value)
+        self.__dict__["_host_" + name] = (bool(value) if t.dtype == torch.bool else int(value), t, t._version)
+
     @property
     def step(self) -> int:
-        return int(self._step.item())
+        return int(self._host_value("_step"))
 
     @step.setter
     def step(self, value: int) -> None:
@@ -261,7 +281,7 @@ class STACRLinear(nn.Module):
     def set_step(self, step: int) -> None:
         if not _is_int(step) or step < 0:
             raise ValueError("step must be a nonnegative integer")
-        self._step.fill_(int(step))
+        self._fill("_step", int(step))
 
     def _turbo(self) -> bool:
         after = self.turbo_after_step
@@ -269,9 +289,9 @@ class STACRLinear(nn.Module):
 
     def _basis_action(self, step: int) -> str | None:
         """What this step's first training forward does to the basis: "fit", "oja" or None."""
-        if not bool(self.basis_ready):
+        if not bool(self._host_value("basis_ready")):
             return "fit"
-        if int(self._last_update_step.item()) == step:
+        if int(self._host_value("_last_update_step")) == step:
             return None  # already refreshed for this step (micro-batches, recomputation)
         frozen = self.freeze_after_warmup and step >= self.warmup_steps
         if frozen or self._turbo() or step % self.update_interval:
@@ -280,8 +300,8 @@ class STACRLinear(nn.Module):
 
     def _install_basis(self, basis: torch.Tensor, step: int) -> None:
         self.basis = basis.to(self.basis.dtype)  # rebind: an outstanding forward keeps its version
-        self.basis_ready.fill_(True)
-        self._last_update_step.fill_(step)
+        self._fill("basis_ready", True)
+        self._fill("_last_update_step", step)
 
     @torch.no_grad()
     def _refresh_basis(self, x2d: torch.Tensor) -> None:
@@ -323,7 +343,7 @@ class STACRLinear(nn.Module):
             replayed = guard.replay_layer(self)
             if replayed is not None:
                 return replayed
-            if not bool(self.basis_ready):
+            if not bool(self._host_value("basis_ready")):
                 self._refresh_basis(x.reshape(-1, self.in_features))
         else:
             self._refresh_basis(x.reshape(-1, self.in_features))
