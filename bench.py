@@ -18,11 +18,12 @@ once (every replay checked against the eager result; a mismatch fails the run); 
 the faster of the two and both are reported.  Other configured layers (cfg3 c_proj, cfg2 Turbo)
 and the basis refresh's Oja step are timed the same way and reported under "other_workloads",
 with two whole-layer lines: the drop-in STACRLinear step with its per-step Oja refresh, and
-config 4 (2048 <-> 8192, 32768 tokens) through the adaptive engine.  Prints one JSON line.
+config 4 (2048 <-> 8192, 32768 tokens) through the adaptive engine, and a line for the compact
+save outputs (bit-packed index stream, per-row int8 coefficients).  Prints one JSON line.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20]
     python bench.py --workload {c_proj,turbo,cfg1,cfg4_up,cfg4_down,oja,cfg4_adaptive_up,cfg4_adaptive_down,
-                                drop_in_layer} [--steps K] [--warmup W]
+                                drop_in_layer,compact_outputs} [--steps K] [--warmup W]
 
 The second form times one other configured shape alone (cfg1's fp32 nn.Linear, cfg4's 2048 <-> 8192
 layers at rank 16 through the projection engine, ...) and prints its own line, for profiling.
@@ -367,6 +368,57 @@ def drop_in_layer_workload(steps, warmup):
             "timing": "eager launches, whole layer step (refresh, dense products included)"}
 
 
+def compact_outputs_workload(steps, warmup):
+    """The north star's compact save outputs on the north-star save's own results (cfg3 c_fc: 41,943
+    sorted flat indices, 8192 x 8 bf16 coefficients): the bit-packed index stream (encode, and decode
+    back to int32) and the per-row int8 coefficients (quantize, dequantize).  Eager launches; the
+    sizes are the stored bytes of each form."""
+    import torch
+
+    from gpu_cases import make_activation, make_basis
+    from stacr_amd import _lib, kernels
+    from stacr_amd.codecs import IndexStream, RowQuantizedCoefficients
+
+    dev = torch.device("cuda:0")
+    x = make_activation(N, D_IN, lognormal=True).to(dev, torch.bfloat16)
+    q = make_basis(D_IN, RANK).to(dev, torch.bfloat16)
+    coeff, idx, _data, _scale = kernels.save(x, q, mode=MODE, budget=BUDGET, chunk_rows=512, bits=BITS)
+    stream = IndexStream.encode(idx).check()
+    if not torch.equal(stream.decode(idx.dtype), idx):
+        raise RuntimeError("compact outputs: the index stream does not decode to the save's indices")
+
+    def encode():
+        IndexStream.encode(idx)
+        RowQuantizedCoefficients.quantize(coeff)
+
+    rq = RowQuantizedCoefficients.quantize(coeff)
+
+    def decode():
+        stream.decode(idx.dtype)
+        rq.dequantize()
+
+    out = {"config": "compact save outputs (cfg3 c_fc save: bit-packed index stream, per-row int8 C)"}
+    for name, fn in (("encode", encode), ("decode", decode)):
+        for _ in range(max(warmup, 2)):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        out[f"{name}_ms"] = (time.perf_counter() - t0) * 1e3 / steps
+        with _lib.KernelTimer(max_launches=64 * 10) as timer:
+            for _ in range(10):
+                fn()
+        out[f"{name}_kernels_us"] = {n: round(tot / 10 * 1e3, 3) for n, (tot, _c) in timer.results.items()}
+    out.update({"ms_per_step": out["encode_ms"] + out["decode_ms"],
+                "index_bytes_int32": int(idx.numel()) * 4, "index_stream_bytes": stream.nbytes(),
+                "coeff_bytes_bf16": coeff.numel() * 2, "coeff_int8_bytes": rq.nbytes(),
+                "kernels_us_per_step": {**out["encode_kernels_us"], **out["decode_kernels_us"]},
+                "timing": "eager launches; encode = stream + row quantizer, decode = their inverses"})
+    return out
+
+
 # The configured layers besides the headline, by name: (description, N, d_in, d_out, rank, budget,
 # mode, options).  Each runs through the same save + dW calls; `--workload NAME` times and prints
 # one of them alone (a line for profiling, not the contract line).
@@ -417,7 +469,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the other configured workloads")
     ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["oja", "cfg4_adaptive_up", "cfg4_adaptive_down",
-                                                                "drop_in_layer"],
+                                                                "drop_in_layer", "compact_outputs"],
                     help="time only this other configured workload and print its line (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -439,6 +491,8 @@ def main() -> int:
                                   2048 if up else 8192, 8192 if up else 2048, args.steps, args.warmup)
         elif args.workload == "drop_in_layer":
             w = drop_in_layer_workload(args.steps, args.warmup)
+        elif args.workload == "compact_outputs":
+            w = compact_outputs_workload(args.steps, args.warmup)
         else:
             w = run_workload(args.workload, args.steps, args.warmup)
         print(json.dumps({"workload": args.workload, **w}), flush=True)
@@ -543,6 +597,7 @@ def main() -> int:
         out["other_workloads"] = [run_workload(key, extra_steps, extra_warm) for key in ("c_proj", "turbo")]
         out["other_workloads"].append(oja_workload(x, q, extra_steps, extra_warm))
         out["other_workloads"].append(drop_in_layer_workload(extra_steps, extra_warm))
+        out["other_workloads"].append(compact_outputs_workload(extra_steps, extra_warm))
         for up in (True, False):  # config 4 through the adaptive engine (20 steps: two refresh periods)
             out["other_workloads"].append(adaptive_workload(
                 "cfg4 adaptive engine, " + ("2048->8192" if up else "8192->2048"), 2048 if up else 8192,

@@ -21,8 +21,11 @@
 //                  that continues a feature from the previous run goes to a slot instead, and the
 //                  slots are added (in run order) after a barrier;
 //              then reduces M over its threads and writes dW = M Q^T + S for its tile.
-// Within a feature, entries follow the bucket order, which LDS integer atomics fill in arrival
-// order: the last bits of the sparse term may differ from run to run.
+// Within a feature, entries follow the bucket order, which is ascending row order: each entry's
+// place is its feature's bucket start plus the number of the feature's entries in earlier rows of
+// the round, counted from a per-feature row bitmap, so the sparse term is the same bit for bit on
+// every run.  (A round holding the same (row, feature) twice, which no valid input does, falls back
+// to places handed out by an LDS counter in arrival order.)
 #include <type_traits>
 
 #include "internal.h"
@@ -249,6 +252,10 @@ template <int IDX64, int VK>
 __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
 {
     __shared__ uint32_t cnt[kMaxISlab], ccur[kMaxISlab];
+    __shared__ __attribute__((aligned(16))) uint32_t rowbits[16 * kMaxISlab];  // [row / 32][feature]: the round's rows
+    static_assert(GradCfg<STACR_DTYPE_BF16, 4>::TB <= 512 && GradCfg<STACR_DTYPE_F32, 4>::TB <= 512 && kMTB <= 512,
+                  "blocks of at most 512 rows: 16 bitmap words a feature");
+    __shared__ uint32_t s_dup;
     __shared__ uint32_t cstart[kMaxISlab], lstart[kMaxISlab], hstart[kMaxISlab], hidx[kMaxISlab];
     __shared__ uint32_t colh[kMaxISlab];  // 1 + matrix-core column of a feature, 0 for pieces
     __shared__ uint32_t s_tot[2][kPlanThreads / 64];        // scan1 buffers, used alternately
@@ -350,6 +357,9 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
             cnt[c] = 0u;
             ccur[c] = 0u;
         }
+        for (int i = threadIdx.x; i < 16 * kMaxISlab / 4; i += kPlanThreads)
+            reinterpret_cast<uint4 *>(rowbits)[i] = make_uint4(0u, 0u, 0u, 0u);
+        if (threadIdx.x == 0) s_dup = 0u;
         __syncthreads();
         constexpr int EPT = kRoundMax / kPlanThreads;
         uint32_t col[EPT], tl[EPT], val[EPT];
@@ -380,6 +390,9 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
                     col[k] = c - (uint32_t)i0;
                     tl[k] = t;
                     atomicAdd(&cnt[col[k]], 1u);
+                    // (t < tb <= 512 rows: 16 words a feature)
+                    const uint32_t bit = 1u << (t & 31u);
+                    if (atomicOr(&rowbits[(t >> 5) * kMaxISlab + col[k]], bit) & bit) s_dup = 1u;
                 }
             }
         }
@@ -503,10 +516,20 @@ __global__ __launch_bounds__(kPlanThreads) void k_dw_plan(PlanArgs a)
             }
         }
         __syncthreads();
+        const bool dup = s_dup != 0u;  // (set before the count barrier above)
 #pragma unroll
         for (int k = 0; k < EPT; ++k) {
             if (col[k] != 0xffffffffu) {
-                const uint32_t pos = base + cstart[col[k]] + atomicAdd(&ccur[col[k]], 1u);
+                // the feature's entries in earlier rows of the round
+                uint32_t rank = 0u;
+                if (!dup) {
+                    const uint32_t w = tl[k] >> 5;
+                    rank = (uint32_t)__popc(rowbits[w * kMaxISlab + col[k]] & ((1u << (tl[k] & 31u)) - 1u));
+                    for (uint32_t u = 0; u < w; ++u) rank += (uint32_t)__popc(rowbits[u * kMaxISlab + col[k]]);
+                } else {
+                    rank = atomicAdd(&ccur[col[k]], 1u);
+                }
+                const uint32_t pos = base + cstart[col[k]] + rank;
                 const uint32_t v = entry_value<VK>(a, val[k], c0 + threadIdx.x + k * kPlanThreads);
                 if (f32)
                     static_cast<uint2 *>(a.ent)[pos] = make_uint2(tl[k], v);
@@ -1593,7 +1616,7 @@ int launch_grad(const StacrGradArgs &a, const GPlan &p, char *ws, const size_t *
             static_assert(ml <= 160 * 1024, "LDS budget");
             static_assert(GradCfg<DT, R>::TB == kMTB && GradCfg<DT, R>::ROUND == kRoundMax, "plan geometry");
             raise_lds_limit(k_dw_fused_mfma<DT, R>, ml);
-            stacr_launch("k_dw_fused", s, [&] { k_dw_fused_mfma<DT, R><<<nwg, kBwdThreads, ml, s>>>(f); });
+            stacr_launch("k_dw_fused_mfma", s, [&] { k_dw_fused_mfma<DT, R><<<nwg, kBwdThreads, ml, s>>>(f); });
             return stacr_hip_check(hipGetLastError(), "weight_grad kernels");
         }
     }

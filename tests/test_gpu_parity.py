@@ -530,6 +530,42 @@ def test_weight_grad_matrix_core_path_is_deterministic(dev, dtype, transposed, d
         assert torch.equal(again[1], first[1])
 
 
+# problems the matrix-core tiles do not take: (G dtype, rank, bias, bits, d_out)
+GENERAL_SET_CASES = [
+    ("f32", 8, True, 0, 1024),    # fp32 G with unquantized values
+    ("bf16", 16, True, 8, 1024),  # rank 16 and the bias column: 17 coefficient columns
+    ("bf16", 32, False, 8, 512),  # rank 32
+    ("f16", 8, True, 4, 1000),    # d_out not a multiple of 16
+]
+
+
+@pytest.mark.parametrize("dtype,rank,bias,bits,d_out", GENERAL_SET_CASES)
+def test_weight_grad_general_set_is_deterministic(dev, dtype, rank, bias, bits, d_out):
+    """The general kernel set (the problems above): each feature's entries are placed in its bucket
+    in ascending row order (a per-feature row bitmap, not arrival order), so repeated calls agree
+    bit for bit; heavy features (log-normal scales, budget 0.03) make the buckets long and split
+    them over several pieces."""
+    from stacr_amd import _lib, kernels
+
+    announce("general-set determinism", dtype, rank, bias, bits, d_out)
+    rows, d_in = 4096, 1024
+    x = make_activation(rows, d_in, lognormal=True).to(dev, DT[dtype])
+    q = make_basis(d_in, rank).to(dev, DT[dtype])
+    g = make_grad(rows, d_out).to(dev, DT[dtype])
+    coeff, idx, data, scale = kernels.save(x, q, mode="global_topk", budget=0.03, chunk_rows=512, bits=bits)
+    bdt = DT[dtype] if bias else None
+    with _lib.KernelTimer(max_launches=16) as timer:
+        first = kernels.weight_grad(g, coeff, q, (idx, data, scale), bits, False, DT[dtype], bdt)
+        torch.cuda.synchronize()
+    names = set(timer.results)
+    assert names & {"k_dw_fused", "k_dw_fused_mfma"} and not names & {"k_tile_grad", "k_tile_wide"}, names
+    for _ in range(3):
+        again = kernels.weight_grad(g, coeff, q, (idx, data, scale), bits, False, DT[dtype], bdt)
+        assert torch.equal(again[0], first[0])
+        if bias:
+            assert torch.equal(again[1], first[1])
+
+
 # ------------------------------------------------------------------ the drop-in layer on the GPU
 def _lowrank(rows, feats, rank, seed=0):
     g = torch.Generator().manual_seed(seed)
