@@ -43,23 +43,99 @@ __device__ __forceinline__ float qr_lane(float x, int l)
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
 }
 
+// x from this lane's partner within its 16-lane row for exchange distance D, by one DPP move that
+// every lane executes alike (a per-lane choice between two moves is compiled into branches, and a
+// DPP move then reads lanes the branch has switched off): D = 8, row_ror:8 (lane l ^ 8); D = 4,
+// row_half_mirror (lane l ^ 7); D = 2, 1, quad_perm [2 3 0 1] and [1 0 3 2] (lanes l ^ 2, l ^ 1)
+template <int D>
+__device__ __forceinline__ float qr_xor(float x)
+{
+    if constexpr (D == 8) return qr_dpp<0x128>(x);       // row_ror:8
+    else if constexpr (D == 4) return qr_dpp<0x141>(x);  // row_half_mirror
+    else if constexpr (D == 2) return qr_dpp<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+    else return qr_dpp<0xB1>(x);                         // quad_perm [1, 0, 3, 2]
+}
+
+// P values a[0..P-1] (P = 4, 8, 16) summed over the wave's 64 lanes: lane l ends with the total of
+// value l % P.  Within each 16-lane row a butterfly over the partners of distances 8, 4, 2, 1 (lane
+// l ^ 8, l ^ 7, l ^ 2, l ^ 1, which between them reach all 16 lanes once): halving exchanges (a
+// lane keeps the half of the values its lane bit names and adds its partner's share of it) for
+// the bits that index the values, plain sums for the others, ordered so that partners always
+// hold the same values (the sum over the l ^ 7 partner comes before any exchange, or is an
+// exchange itself).  Then rows 0 + 1 and 2 + 3, and the two halves, by v_permlane16_swap /
+// v_permlane32_swap, whose pairs add the lower lane's value to the upper's in every lane; plain
+// sums likewise add lower + upper in both lanes, so every lane holding value c has the same bits.
+template <int P>
+__device__ __forceinline__ float qr_wave_scatter(float (&a)[P])
+{
+    const int lane = threadIdx.x & 63;
+    auto scatter = [&](auto dc) {
+        constexpr int D = decltype(dc)::value;
+        const bool upper = (lane & D) != 0;
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            const float send = upper ? a[k] : a[k + D], keep = upper ? a[k + D] : a[k];
+            a[k] = keep + qr_xor<D>(send);
+        }
+    };
+    auto fold = [&](auto dc, auto nc) {  // a[k] += the partner's a[k], k < N (lower + upper in both lanes)
+        constexpr int D = decltype(dc)::value, N = decltype(nc)::value;
+        const bool upper = (lane & D) != 0;
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const float other = qr_xor<D>(a[k]);
+            a[k] = upper ? other + a[k] : a[k] + other;
+        }
+    };
+    using I8 = std::integral_constant<int, 8>;
+    using I4 = std::integral_constant<int, 4>;
+    using I2 = std::integral_constant<int, 2>;
+    using I1 = std::integral_constant<int, 1>;
+    if constexpr (P == 16) {
+        scatter(I8{});
+        scatter(I4{});
+    } else if constexpr (P == 8) {
+        scatter(I4{});
+    } else {
+        fold(I4{}, I4{});
+    }
+    scatter(I2{});
+    scatter(I1{});
+    if constexpr (P <= 8) fold(I8{}, I1{});
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[0]), __float_as_uint(a[0]), false, false);
+    float x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Sums of C per-thread values over the workgroup, in a fixed order, the same bits in every
-// thread: each 16-lane row by DPP rotations (1, 2, 4, 8), the wave's four row sums (lanes 0, 16,
-// 32, 48) in order, then the waves' sums in order through LDS (two slots, alternated by the
-// caller, so one barrier suffices; lane c of each wave reads value c's).
+// thread: the wave's totals (C >= 4: the reduce-scatter above, lane c holding value c; fewer: each
+// 16-lane row by DPP rotations (1, 2, 4, 8) and the four row sums (lanes 0, 16, 32, 48) in order),
+// then the waves' sums in order through LDS (two slots, alternated by the caller, so one barrier
+// suffices; lane c of each wave reads value c's).
 template <int C>
 __device__ __forceinline__ void qr_sums(float *v, float (*s_part)[kQrMaxCols + 1])
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if constexpr (C >= 4) {
+        constexpr int P = C <= 4 ? 4 : C <= 8 ? 8 : 16;
+        static_assert(C <= 16, "at most 16 values a sum");
+        float a[P];
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-        float x = v[c];
-        x += qr_dpp<0x121>(x);  // row_ror:1
-        x += qr_dpp<0x122>(x);  // row_ror:2
-        x += qr_dpp<0x124>(x);  // row_ror:4
-        x += qr_dpp<0x128>(x);  // row_ror:8
-        const float t = ((qr_lane(x, 0) + qr_lane(x, 16)) + qr_lane(x, 32)) + qr_lane(x, 48);
-        if (lane == 0) s_part[wave][c] = t;
+        for (int c = 0; c < P; ++c) a[c] = c < C ? v[c] : 0.f;
+        const float t = qr_wave_scatter<P>(a);
+        if (lane < C) s_part[wave][lane] = t;
+    } else {
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            float x = v[c];
+            x += qr_dpp<0x121>(x);  // row_ror:1
+            x += qr_dpp<0x122>(x);  // row_ror:2
+            x += qr_dpp<0x124>(x);  // row_ror:4
+            x += qr_dpp<0x128>(x);  // row_ror:8
+            const float t = ((qr_lane(x, 0) + qr_lane(x, 16)) + qr_lane(x, 32)) + qr_lane(x, 48);
+            if (lane == 0) s_part[wave][c] = t;
+        }
     }
     __syncthreads();
     // lane c of every wave adds value c over the waves, in order; the wave then shares the C
