@@ -10,7 +10,7 @@
 //     chunk's count of entries per input feature, and the first entry of every block of 512 token
 //     rows (entries are ascending, so block b starts where the block of the entries changes).
 //   k_tile_plan   one workgroup per (block of 512 rows, input part of <= 1024 features):
-//     * (for k_tile_grad) the part's column features: the 64 with most entries over the whole
+//     * (for k_tile_grad) the part's column features: the 48 with most entries over the whole
 //       problem, ties to the lowest feature; every workgroup selects the same set;
 //     * the block's column entries as dense matrix-core operands, in the order in which the lanes
 //       of the streaming kernel load them, zero where no entry was selected: int8 codes for 4 / 8-bit
@@ -60,7 +60,8 @@ static_assert(kThreads == 2 * kTB, "two G tile rows per lane pair: one 16-byte c
 static_assert(kTB == kCensusRows, "a save's entry census gives the first entry of every block");
 static_assert(kOffWords % 256 == 0, "offsets are staged in whole 1 KiB copies");
 
-constexpr int kNT = 4;               // 16-column matrix-core tiles of column entries per part
+constexpr int kNT = 3;               // 16-column matrix-core tiles of column entries per part (48 columns:
+                                     // fewer light entries than 32, fewer operand bytes than 64; measured)
 constexpr int kNC = 16 * kNT;        // column features per part
 // LDS stride of one column of a block's column entries in the plan (elements): 8 past the block's
 // rows, so that the 16 columns a 16-lane group reads when the tile is written out in lane order
@@ -831,12 +832,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
     __syncthreads();
 
     // ---- reduce the per-wave tiles over the waves, in wave order.  Every wave's tiles are staged
-    // at once (16 KiB a tile: tiles 0, 1 in lds0, 2, 3 in lds1, 4 in lds2); the sums and the part's
+    // at once (16 KiB a tile: tiles 0, 1 in lds0, 2, 3 in lds1, 4 in lds2, as many as there are); the sums and the part's
     // column slots follow the last tile (in lds1 without entries, whose one tile is in lds0)
     constexpr int NTILE = 1 + NT;
     constexpr size_t kTileBytes = (size_t)kWaves * 256 * 4;
     static_assert(L::size >= (SP ? 2 : 1) * kTileBytes, "two tiles (one without entries) fit a buffer");
-    static_assert(!SP || NTILE == 5, "five tiles with entries");
+    static_assert(!SP || NTILE <= 5, "at most five tiles with entries");
     static_assert(!SP || kTileBytes + NTILE * 256 * 4 + kPartMax * 4 <= L::size, "the last tile, sums and slots fit a buffer");
     auto stage_of = [&](int tile) {
         unsigned char *b = tile < 2 ? lds0 : tile < 4 ? lds1 : lds2;
