@@ -151,10 +151,15 @@ def time_steps(step, steps: int, warmup: int, check=None):
     for _ in range(3):
         graph.replay()
         torch.cuda.synchronize()
-        step()  # eager work between replays
+        fresh = step()  # eager work between replays
         torch.cuda.synchronize()
         if check is not None:
-            check(outs, ref)
+            try:
+                check(outs, ref)
+            except RuntimeError as exc:  # name the side a fresh eager step agrees with
+                agree = [name for name, got in (("the replay", outs), ("the first eager step", ref))
+                         if _passes(check, got, fresh)]
+                raise RuntimeError(f"{exc}; a later eager step equals {' and '.join(agree) or 'neither'}") from exc
     for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
@@ -163,6 +168,14 @@ def time_steps(step, steps: int, warmup: int, check=None):
         graph.replay()
     torch.cuda.synchronize()
     return eager_ms, (time.perf_counter() - t0) * 1e3 / steps, None
+
+
+def _passes(check, outs, ref) -> bool:
+    try:
+        check(outs, ref)
+    except RuntimeError:
+        return False
+    return True
 
 
 def _rel(a, b) -> float:
