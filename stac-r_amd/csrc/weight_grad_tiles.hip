@@ -96,7 +96,21 @@ struct TileArgs {
     int32_t *colmap;    // [n_parts][kNC] feature in the part, or -1
     int sparse;         // nnz > 0: the plan builds the entry structures
     int columns;        // the plan picks kNC column features per part (0: every entry is a light record)
+    // division by d_in as a multiply-high and shifts (Granlund and Montgomery, "Division by invariant
+    // integers using multiplication", 1994, figure 4.1): exact for every 32-bit dividend
+    uint32_t div_m;
+    int div_s1, div_s2;
 };
+
+// The magic number and shifts of division by d (1 <= d < 2^32) for TileArgs::div_m / div_s1 / div_s2.
+inline void div_magic(uint32_t d, uint32_t *m, int *s1, int *s2)
+{
+    int l = 0;
+    while ((1ull << l) < d) ++l;  // ceil(log2 d)
+    *m = (uint32_t)((((1ull << 32) * ((1ull << l) - d)) / d) + 1u);
+    *s1 = l > 0 ? 1 : 0;
+    *s2 = l > 0 ? l - 1 : 0;
+}
 
 // Words of the record array: every region's offsets and records (at most nnz records in all), the
 // alignment slack, and the staging copy's overrun past the last region.
@@ -110,13 +124,15 @@ __device__ __forceinline__ int64_t flat_at(const void *idx, int idx64, int64_t k
     return idx64 ? static_cast<const int64_t *>(idx)[k] : (int64_t) static_cast<const int32_t *>(idx)[k];
 }
 
-// (token row, feature) of a flat index; rows * d_in < 2^32 (the host checks), so 32-bit division.
-// An index outside the problem (invalid input) still yields a feature < d_in.
-__device__ __forceinline__ void split_flat(int64_t flat, uint32_t d_in, uint32_t &t, uint32_t &f)
+// (token row, feature) of a flat index; rows * d_in < 2^32 (the host checks), so 32-bit division,
+// by the argument block's multiply-high.  An index outside the problem (invalid input) still yields
+// a feature < d_in.
+__device__ __forceinline__ void split_flat(int64_t flat, const TileArgs &a, uint32_t &t, uint32_t &f)
 {
     const uint32_t x = (uint32_t)flat;
-    t = x / d_in;
-    f = x - t * d_in;
+    const uint32_t h = __umulhi(a.div_m, x);
+    t = (h + ((x - h) >> a.div_s1)) >> a.div_s2;
+    f = x - t * (uint32_t)a.d_in;
 }
 
 // The integer code of entry e (bits 4 / 8).
@@ -179,14 +195,14 @@ __global__ __launch_bounds__(kThreads) void k_tile_count(TileArgs a)
             const int64_t e = r0 + k * kThreads + tid;
             if (e >= e1) continue;
             uint32_t t, f;
-            split_flat(cur[k], d_in, t, f);
+            split_flat(cur[k], a, t, f);
             atomicAdd(&s_h[f], 1u);
             // every block b with block(e - 1) < b <= block(e) starts at e; past the last entry, nnz
             const int64_t bcur = block_of(t);
             int64_t bprev = -1;
             if (e > 0) {
                 uint32_t tp, fp;
-                split_flat(prev[k], d_in, tp, fp);
+                split_flat(prev[k], a, tp, fp);
                 bprev = block_of(tp);
             }
             for (int64_t b = bprev + 1; b <= bcur; ++b) a.bstart[b] = (uint32_t)e;
@@ -199,10 +215,37 @@ __global__ __launch_bounds__(kThreads) void k_tile_count(TileArgs a)
 }
 
 // ------------------------------------------------------------------ the plan
+// Exclusive prefix sums of two values over the workgroup's threads in one exchange (two barriers);
+// the totals in *t0 and *t1.  s_tot2 holds 2 kWaves words.  Every thread must call it.
+__device__ __forceinline__ uint32_t block_exclusive_scan2(uint32_t v0, uint32_t v1, uint32_t *s_tot2, uint32_t *t0,
+                                                          uint32_t *t1)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t x0 = wave_inclusive_scan(v0), x1 = wave_inclusive_scan(v1);
+    if (lane == 63) {
+        s_tot2[wave] = x0;
+        s_tot2[kWaves + wave] = x1;
+    }
+    __syncthreads();
+    uint32_t before = 0, all0 = 0, all1 = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        const uint32_t t = s_tot2[w];
+        before += w < wave ? t : 0u;
+        all0 += t;
+        all1 += s_tot2[kWaves + w];
+    }
+    __syncthreads();
+    *t0 = all0;
+    *t1 = all1;
+    return before + x0 - v0;
+}
+
 // One level of the column selection: wave 0 finds, from the 256-bin histogram h (counted from the
-// top), the bin holding the need-th largest value and the need left inside it; *res = {bin, need}
-// (bin -1 when the histogram holds fewer than need values).  Every thread calls it.
-__device__ __forceinline__ void select_bin256(const uint32_t *__restrict__ h, uint32_t need, int2 *res)
+// top), the bin holding the need-th largest value and the need left inside it, and returns
+// {bin, need} to every thread through *res (bin -1 when the histogram holds fewer than need
+// values).  Every thread calls it (it contains a barrier).
+__device__ __forceinline__ int2 select_bin256(const uint32_t *__restrict__ h, uint32_t need, int2 *res)
 {
     const int tid = threadIdx.x, lane = tid & 63;
     if (tid < 64) {
@@ -231,6 +274,7 @@ __device__ __forceinline__ void select_bin256(const uint32_t *__restrict__ h, ui
         }
     }
     __syncthreads();
+    return *res;
 }
 
 template <bool BT8>
@@ -244,7 +288,7 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
     __shared__ uint32_t s_h[256];
     __shared__ int2 s_sel;
     __shared__ __attribute__((aligned(16))) BE s_bt[kNC * kBtStride];  // the block's column entries [slot][t]
-    __shared__ uint32_t s_tot[kWaves];
+    __shared__ uint32_t s_tot[2 * kWaves];
 
     const int b = blockIdx.x, part = blockIdx.y, tid = threadIdx.x;
     // with entries, the workgroups past the last part pack the coefficient operands, in parallel
@@ -254,6 +298,15 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
     const int pw = (int)(a.d_in - plo < a.part_w ? a.d_in - plo : a.part_w);
 
     if (a.sparse && !pack_c) {
+        // the feature's partial counts (n_hist <= kChunks), issued first and unconditionally (addresses
+        // clamped, values masked where used): they arrive with the block's starts, and the column
+        // selection below does not wait for the block's entries, which are issued after them
+        uint32_t hv[kChunks];
+        {
+            const int64_t fo = plo + (tid < pw ? tid : pw - 1);
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c) hv[c] = a.hist[(int64_t)(c < a.n_hist ? c : a.n_hist - 1) * a.d_in + fo];
+        }
         // ---- entry range of the block (clamped, whatever the starts hold)
         int64_t e_b0 = a.bstart[b], e_b1 = a.bstart[b + 1];
         e_b0 = e_b0 < a.nnz ? e_b0 : a.nnz;
@@ -283,70 +336,71 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         // scan over the features gives, packed, the features above c64 and those equal to it below f,
         // which places every column at its slot in feature order.  (Every workgroup selects the same set.)
         uint32_t cnt = 0;
-        if (tid < pw && a.columns) {
 #pragma unroll
-            for (int c = 0; c < a.n_hist; ++c) cnt += a.hist[(int64_t)c * a.d_in + plo + tid];
-            cnt = cnt < 0xffffu ? cnt : 0xffffu;
-        }
+        for (int c = 0; c < kChunks; ++c) cnt += c < a.n_hist ? hv[c] : 0u;
+        cnt = tid < pw && a.columns ? (cnt < 0xffffu ? cnt : 0xffffu) : 0u;
         s_slot[tid] = -1;
-        if (tid < 256) s_h[tid] = 0u;
-        __syncthreads();
-        // (without column features every count is 0 here: no feature is selected)
-        if (cnt) atomicAdd(&s_h[cnt >> 8], 1u);
-        __syncthreads();
-        select_bin256(s_h, (uint32_t)kNC, &s_sel);
-        const int2 l1 = s_sel;
-        uint32_t c64 = 0u, take_eq = 0u;  // (fewer than kNC features with entries: all of them, c64 = 0)
-        if (l1.x >= 0) {
+        if (a.columns) {  // (uniform; without column features every entry is a light record)
             if (tid < 256) s_h[tid] = 0u;
             __syncthreads();
-            if (cnt && (int)(cnt >> 8) == l1.x) atomicAdd(&s_h[cnt & 0xffu], 1u);
+            if (cnt) atomicAdd(&s_h[cnt >> 8], 1u);
             __syncthreads();
-            select_bin256(s_h, (uint32_t)l1.y, &s_sel);
-            c64 = ((uint32_t)l1.x << 8) | (uint32_t)s_sel.x;
-            take_eq = (uint32_t)s_sel.y;
-        }
-        const bool above = l1.x >= 0 ? cnt > c64 : cnt > 0u;
-        const bool tie = l1.x >= 0 && cnt == c64;
-        uint32_t packed_all;
-        const uint32_t packed = block_exclusive_scan<kThreads>((above ? 1u : 0u) | (tie ? 1u << 16 : 0u), s_tot,
-                                                               &packed_all);
-        const uint32_t n_above = packed & 0xffffu, ties_below = packed >> 16;
-        const bool is_col = above || (tie && ties_below < take_eq);
-        const uint32_t slot = n_above + (ties_below < take_eq ? ties_below : take_eq);
-        if (is_col) s_slot[tid] = (int32_t)slot;
-        if (b == 0 && tid < kNC) s_key[tid] = 0xffffffffu;
-        __syncthreads();
-        if (b == 0 && a.columns) {
-            if (is_col) s_key[slot] = (uint32_t)tid;
+            const int2 l1 = select_bin256(s_h, (uint32_t)kNC, &s_sel);
+            uint32_t c64 = 0u, take_eq = 0u;  // (fewer than kNC features with entries: all of them, c64 = 0)
+            if (l1.x >= 0) {
+                if (tid < 256) s_h[tid] = 0u;
+                __syncthreads();
+                if (cnt && (int)(cnt >> 8) == l1.x) atomicAdd(&s_h[cnt & 0xffu], 1u);
+                __syncthreads();
+                const int2 l2 = select_bin256(s_h, (uint32_t)l1.y, &s_sel);
+                c64 = ((uint32_t)l1.x << 8) | (uint32_t)l2.x;
+                take_eq = (uint32_t)l2.y;
+            }
+            const bool above = l1.x >= 0 ? cnt > c64 : cnt > 0u;
+            const bool tie = l1.x >= 0 && cnt == c64;
+            uint32_t packed_all;
+            const uint32_t packed = block_exclusive_scan<kThreads>((above ? 1u : 0u) | (tie ? 1u << 16 : 0u), s_tot,
+                                                                   &packed_all);
+            const uint32_t n_above = packed & 0xffffu, ties_below = packed >> 16;
+            const bool is_col = above || (tie && ties_below < take_eq);
+            const uint32_t slot = n_above + (ties_below < take_eq ? ties_below : take_eq);
+            if (is_col) s_slot[tid] = (int32_t)slot;
+            if (b == 0 && tid < kNC) s_key[tid] = 0xffffffffu;
             __syncthreads();
-            if (tid < kNC) a.colmap[part * kNC + tid] = tid < kNC ? (int32_t)s_key[tid] : -1;
+            if (b == 0) {
+                if (is_col) s_key[slot] = (uint32_t)tid;
+                __syncthreads();
+                if (tid < kNC) a.colmap[part * kNC + tid] = (int32_t)s_key[tid];
+            }
         }
 
         // ---- this block's entries: the column tile and the light bitmaps
         static_assert((kNC * kBtStride * sizeof(BE)) % 16 == 0, "the column tile clears in 16-byte words");
-        for (int i = tid; i < (int)(kNC * kBtStride * sizeof(BE) / 16); i += kThreads)
+        for (int i = tid; a.columns && i < (int)(kNC * kBtStride * sizeof(BE) / 16); i += kThreads)
             reinterpret_cast<uint4 *>(s_bt)[i] = make_uint4(0u, 0u, 0u, 0u);
         for (int i = tid; i < 16 * kPartMax / 4; i += kThreads)
             reinterpret_cast<uint4 *>(s_mask)[i] = make_uint4(0u, 0u, 0u, 0u);
         __syncthreads();
         const int64_t t_base = (int64_t)b * kTB;
-        const uint32_t d_in = (uint32_t)a.d_in;
         // (row in the block, feature in the part) of a loaded entry; false when it lies outside
         // the block (valid input has no such entry) or, with `in_part`, outside the part
         auto place = [&](int64_t flat, int &tl, int64_t &f) {
             uint32_t t, fg;
-            split_flat(flat, d_in, t, fg);
+            split_flat(flat, a, t, fg);
             const int64_t tl64 = (int64_t)t - t_base;
             f = (int64_t)fg - plo;
             tl = (int)tl64;
             return flat >= 0 && tl64 >= 0 && tl64 < kTB;
         };
         uint32_t before_part = 0;  // entries of this block in lower parts: where the part's records start
+        // (one round: each light entry of the part as row | feature << 9, else ~0, for the second pass)
+        static_assert(kTB == 1 << 9, "a block row in 9 bits");
+        uint32_t pk[kBatch];
         for (int64_t r0 = e_b0; r0 < e_b1; r0 += kBatch * kThreads) {
             if (!one_round) load_batch(r0);
 #pragma unroll
             for (int k = 0; k < kBatch; ++k) {
+                pk[k] = ~0u;
                 int tl;
                 int64_t f;
                 if (!place(fl[k], tl, f)) continue;
@@ -358,13 +412,13 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
                     else s_bt[s * kBtStride + tl] = (BE)to_g16(val[k], a.g_dt);
                 } else {
                     atomicOr(&s_mask[(tl >> 5) * kPartMax + f], 1u << (tl & 31));
+                    pk[k] = (uint32_t)tl | ((uint32_t)f << 9);
                 }
             }
         }
         __syncthreads();
-        uint32_t all_before;
-        (void)block_exclusive_scan<kThreads>(before_part, s_tot, &all_before);
-        // light count of each feature, their offsets
+        // light count of each feature; then, in one exchange, their offsets and the block's entries
+        // in lower parts
         uint32_t lcnt = 0;
         if (tid < pw) {
 #pragma unroll
@@ -373,8 +427,8 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
                 lcnt += __popc(s_mask[w * kPartMax + tid]);
             }
         }
-        uint32_t n_light;
-        const uint32_t off = block_exclusive_scan<kThreads>(lcnt, s_tot, &n_light);
+        uint32_t n_light, all_before;
+        const uint32_t off = block_exclusive_scan2(lcnt, before_part, s_tot, &n_light, &all_before);
         // the region of (block, part): kOffWords words of offsets (feature f's records start at
         // word kOffWords + offset[f]; offset[pw] ends them), then the records.  Regions are ordered
         // by (block, part); region r starts at or after the entries of the earlier regions plus
@@ -396,7 +450,13 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
             for (int k = 0; k < kBatch; ++k) {
                 int tl;
                 int64_t f;
-                if (!place(fl[k], tl, f) || f < 0 || f >= pw || s_slot[f] >= 0) continue;
+                if (one_round) {
+                    if (pk[k] == ~0u) continue;
+                    tl = (int)(pk[k] & (kTB - 1));
+                    f = (int64_t)(pk[k] >> 9);
+                } else if (!place(fl[k], tl, f) || f < 0 || f >= pw || s_slot[f] >= 0) {
+                    continue;
+                }
                 const int w = tl >> 5;
                 uint32_t r = s_pre[(w >> 1) * kPartMax + f] + __popc(s_mask[w * kPartMax + f] & ((1u << (tl & 31)) - 1u));
                 if (w & 1) r += __popc(s_mask[(w - 1) * kPartMax + f]);
@@ -1409,6 +1469,7 @@ int stacr_tiles_launch(const StacrGradArgs &a)
     }
     t.sparse = g.sparse ? 1 : 0;
     t.columns = g.wide ? 0 : 1;
+    div_magic((uint32_t)a.d_in, &t.div_m, &t.div_s1, &t.div_s2);
     hipStream_t s = a.stream;
     int rc;
     if (g.sparse && !census) {
