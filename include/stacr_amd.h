@@ -472,6 +472,20 @@ int stacr_dequantize_rows_int8(const void *codes, const void *scales, int64_t ro
 int stacr_qr(const float *a, int64_t rows, int cols, float *q, float *r, void *stream);
 
 /*
+ * The same reduced QR for any tall matrix of cols <= 16 (rows >= cols), e.g. the 8192 x 16 basis of a
+ * wide layer (stacr_amd's wrapper takes it past 8192 elements, where it is the faster of the two):
+ * replaces torch.linalg.qr(matrix, mode="reduced") at the same call sites (stacr/oja.py:8-11,
+ * stacr/adaptive.py:3368).  Q and R as stacr_qr (LAPACK's signs), by
+ * CholeskyQR in fp64 with the signs recovered from Q's top block; a matrix whose columns are within
+ * 1e-5 of dependent (or whose sign decision is that close) takes LAPACK's Householder QR in one
+ * workgroup instead.  Three launches; the workspace (workspace_bytes from
+ * stacr_qr_tall_workspace_bytes, 8-byte aligned) holds the partial Gram matrices and the product.
+ */
+int stacr_qr_tall_workspace_bytes(int64_t rows, int cols, size_t *bytes);
+int stacr_qr_tall(const float *a, int64_t rows, int cols, float *q, float *r, void *workspace,
+                  size_t workspace_bytes, void *stream);
+
+/*
  * Kernel timing (benchmarking aid; no counterpart in the reference).  Between begin and end,
  * every kernel this library launches is bracketed by HIP events on its stream, preceded by a
  * `sleep_us` device-side sleep so host enqueue gaps are not measured (up to max_launches

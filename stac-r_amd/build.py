@@ -19,7 +19,7 @@ ARCH = os.environ.get("STACR_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["abi.hip", "save.hip", "weight_grad.hip", "adaptive.hip", "oja.hip", "selectors.hip", "profile.hip",
            "noalloc.hip", "weight_grad_tiles.hip", "reconstruct.hip", "codecs.hip",
-           "checkpoint_codec.hip", "qr.hip"]
+           "checkpoint_codec.hip", "qr.hip", "qr_tall.hip"]
 
 FLAGS = [
     f"--offload-arch={ARCH}",

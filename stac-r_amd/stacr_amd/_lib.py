@@ -79,6 +79,8 @@ SIGNATURES = {
     "stacr_oja_step": ([_p, _i32, _i64, _i64, _p, _i32, ctypes.c_float, _p, _p, _p, _sz, _p], _i32),
     "stacr_oja_step_given_y": ([_p, _i32, _i64, _i64, _p, _i32, _p, ctypes.c_float, _p, _p, _p, _sz, _p], _i32),
     "stacr_qr": ([_p, _i64, _i32, _p, _p, _p], _i32),
+    "stacr_qr_tall_workspace_bytes": ([_i64, _i32, _PSZ], _i32),
+    "stacr_qr_tall": ([_p, _i64, _i32, _p, _p, _p, _sz, _p], _i32),
     "stacr_reconstruct": ([_p, _p, _i32, _i64, _i64, _i32, _p, _i32, _p, _i64, _i32, _p, _p], _i32),
     "stacr_index_stream_sizes": ([_i64, _p, _p], _i32),
     "stacr_index_stream_encode": ([_p, _i32, _i64, _p, _p, _p, _p, _p], _i32),

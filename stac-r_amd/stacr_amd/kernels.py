@@ -302,20 +302,36 @@ def oja_step_given_y(x2d: torch.Tensor, q: torch.Tensor, y: torch.Tensor, lr: fl
     return update, out
 
 
+# rows * cols up to which the one-workgroup kernel (stacr_qr, limit 32768) runs; larger matrices take
+# stacr_qr_tall, which is faster from here on (measured: 2048 x 16 in 33 us against 58 us)
+QR_REGISTER_ELEMS = 8192
+
+
 def qr(a: torch.Tensor):
     """Reduced QR (Q, R) of a tall GPU matrix in fp32, LAPACK's sign convention (as
-    torch.linalg.qr): one workgroup (stacr_qr).  Raises NotImplementedError for shapes past its
-    limits (more than 16 columns, or more than 32768 elements)."""
+    torch.linalg.qr): one workgroup (stacr_qr) up to 8192 elements, the tall route (stacr_qr_tall:
+    fp64 CholeskyQR with LAPACK's signs, or LAPACK's Householder QR where that is not exact enough)
+    past it.  Raises NotImplementedError for more than 16 columns."""
     require_gpu(a, "matrix")
     if a.dim() != 2:
         raise ValueError(f"qr takes a matrix, got {a.dim()} dimensions")
     rows, cols = a.shape
     if cols > rows:
         raise ValueError(f"qr takes a tall matrix, got {rows} x {cols}")
+    if cols > 16:
+        raise NotImplementedError(f"qr: {cols} columns (at most 16)")
     a32 = a.to(torch.float32).contiguous()
     q = torch.empty_like(a32)
     r = torch.empty(cols, cols, dtype=torch.float32, device=a.device)
-    _lib.check(_lib.load().stacr_qr(_ptr(a32), rows, cols, _ptr(q), _ptr(r), _stream(a.device)), "stacr_qr")
+    L = _lib.load()
+    if rows * cols <= QR_REGISTER_ELEMS:
+        _lib.check(L.stacr_qr(_ptr(a32), rows, cols, _ptr(q), _ptr(r), _stream(a.device)), "stacr_qr")
+        return q, r
+    wsb = ctypes.c_size_t()
+    _lib.check(L.stacr_qr_tall_workspace_bytes(rows, cols, ctypes.byref(wsb)), "stacr_qr_tall")
+    ws = torch.empty(wsb.value, dtype=torch.uint8, device=a.device)
+    _lib.check(L.stacr_qr_tall(_ptr(a32), rows, cols, _ptr(q), _ptr(r), _ptr(ws), wsb.value, _stream(a.device)),
+               "stacr_qr_tall")
     return q, r
 
 

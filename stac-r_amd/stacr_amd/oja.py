@@ -2,7 +2,7 @@
 
 The Oja step's reductions (Y = XQ, X^T Y, Y^T Y and the stepped basis) run in the HIP kernels
 behind stacr_oja_step, so `OjaBasis.update` needs its basis on a ROCm GPU; the QR after it runs in
-the QR kernel (stacr_qr) within its limits, torch's QR beyond them.  SVD stays a torch call.
+the QR kernels (stacr_qr, stacr_qr_tall) up to 16 columns, torch's QR beyond.  SVD stays a torch call.
 
 The basis is versioned: every change installs a new tensor (never an in-place write) and bumps
 the version, so a tensor handed out by `shared` stays valid for the activations that used it,
@@ -17,8 +17,8 @@ from . import kernels
 
 def orthonormalize(matrix: torch.Tensor) -> torch.Tensor:
     """Orthonormal columns spanning ``matrix``: reduced QR in fp32 (LAPACK's Householder signs),
-    returned in its dtype.  On a ROCm GPU the one-launch QR kernel (stacr_qr) within its limits
-    (<= 16 columns, <= 32768 elements); otherwise torch's QR."""
+    returned in its dtype.  On a ROCm GPU the QR kernels (stacr_qr, or stacr_qr_tall past 8192
+    elements) for up to 16 columns; otherwise torch's QR."""
     m = matrix.to(torch.float32)
     if m.is_cuda and m.dim() == 2 and m.shape[1] <= m.shape[0]:
         try:

@@ -1,6 +1,7 @@
-"""The native reduced QR (stacr_qr) against LAPACK's Householder QR on the CPU in fp64 (torch's
-CPU torch.linalg.qr): the same Q and R, signs included (R[j][j] = -sign(alpha_j) * norm), Q with
-orthonormal columns, Q R = A, bit-identical repeated calls, and the shapes past its limits refused.
+"""The native reduced QR (stacr_qr, and stacr_qr_tall past one workgroup's registers) against
+LAPACK's Householder QR on the CPU in fp64 (torch's CPU torch.linalg.qr): the same Q and R, signs
+included (R[j][j] = -sign(alpha_j) * norm), Q with orthonormal columns, Q R = A, bit-identical
+repeated calls, and more than 16 columns refused.
 The basis refreshes that use it (orthonormalize after an Oja step) are checked in
 test_gpu_oja.py and the layer tests."""
 import numpy as np
@@ -56,6 +57,17 @@ CASES = [
     ("repeated_column", "repeated_column", 300, 7),
     ("zero_below_diagonal", "zero_below_diagonal", 200, 5),
     ("max_elements", "gaussian", 8192, 4),
+    # past 8192 elements (and in several of the cases above) the tall route: fp64 CholeskyQR with
+    # LAPACK's signs, or LAPACK's Householder QR streamed through memory where columns are close to
+    # dependent (the graded, zero and repeated column cases)
+    ("tall_cfg4_down_rank16", "near_orthonormal", 8192, 16),
+    ("tall_cfg4_rank16_32768", "gaussian", 32768, 16),
+    ("tall_odd_rows", "gaussian", 8193, 4),
+    ("tall_single_column", "gaussian", 40000, 1),
+    ("tall_zero_below_diagonal", "zero_below_diagonal", 4096, 9),
+    ("tall_graded_householder", "graded", 8192, 12),
+    ("tall_zero_column_householder", "zero_column", 4096, 9),
+    ("tall_repeated_column_householder", "repeated_column", 3000, 16),
 ]
 
 
@@ -87,14 +99,14 @@ def test_qr_is_deterministic_and_refuses_what_it_does_not_take(dev):
     from stacr_amd import kernels
 
     announce("qr determinism")
-    a = _matrix("gaussian", 2048, 16).to(dev)
-    q1, r1 = kernels.qr(a)
-    q2, r2 = kernels.qr(a)
-    assert torch.equal(q1, q2) and torch.equal(r1, r2)
+    for rows, cols, kind in ((512, 16, "gaussian"), (2048, 16, "gaussian"), (8192, 16, "near_orthonormal"),
+                             (6000, 10, "graded")):
+        a = _matrix(kind, rows, cols).to(dev)
+        q1, r1 = kernels.qr(a)
+        q2, r2 = kernels.qr(a)
+        assert torch.equal(q1, q2) and torch.equal(r1, r2), (rows, cols, kind)
     with pytest.raises(NotImplementedError):
         kernels.qr(torch.randn(100, 17, device=dev))
-    with pytest.raises(NotImplementedError):
-        kernels.qr(torch.randn(8193, 4, device=dev))
     with pytest.raises(ValueError):
         kernels.qr(torch.randn(3, 5, device=dev))
 
