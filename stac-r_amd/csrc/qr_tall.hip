@@ -18,9 +18,11 @@
 //                 the top block of Q+ = A X and its sign-choosing LU: M = X S into the workspace,
 //                 R = S R+ into r.  Where the fp64 route is not exact enough (a Cholesky pivot below
 //                 1e-10 of its column's squared norm, i.e. a column within 1e-5 of the span of the
-//                 earlier ones; a condition estimate above 1e5; or a sign decision |d_j| < 1e-5), the
-//                 same workgroup runs LAPACK's Householder QR itself with the matrix streamed through
-//                 q (sgeqr2, then sorg2r forming Q in place), and flags it.
+//                 earlier ones, a zero column among them; or a condition estimate above 1e5), the same
+//                 workgroup runs LAPACK's Householder QR itself with the matrix streamed through q
+//                 (sgeqr2, then sorg2r forming Q in place), and flags it.  (A sign decision with |d_j|
+//                 near zero stays on the fp64 route: there LAPACK's fp32 alpha has no reliable sign
+//                 either, and a Householder QR summing in another order would not reproduce it.)
 //   k_qrt_apply   P workgroups: Q = A M (fp64 products, rounded once to fp32), unless flagged.
 // Every sum has a fixed order, so the result is the same on every run.
 #include "internal.h"
@@ -71,20 +73,28 @@ __global__ __launch_bounds__(kQtGramThreads) void k_qrt_gram(const float *__rest
     ws[(size_t)blockIdx.x * 256 + e] = ((s_acc[0][e] + s_acc[1][e]) + s_acc[2][e]) + s_acc[3][e];
 }
 
-// ---- one value per thread summed over the workgroup in a fixed order (xor tree within the wave,
-// the waves in order); every thread receives the total.  s_part holds one value a wave.
-template <typename T>
-__device__ __forceinline__ T qt_block_sum(T v, T *s_part)
+// ---- kQtCols values a thread summed over the workgroup in a fixed order (xor tree within the
+// wave, the waves in order), all in one exchange (two barriers); every thread receives the totals.
+// s_part holds kQtCols values a wave.
+__device__ __forceinline__ void qt_block_sums(float (&v)[kQtCols], float *s_part)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    if (lane == 0) s_part[wave] = v;
+    for (int k = 0; k < kQtCols; ++k)
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v[k] += __shfl_xor(v[k], off, 64);
+    if (lane == 0)
+#pragma unroll
+        for (int k = 0; k < kQtCols; ++k) s_part[wave * kQtCols + k] = v[k];
     __syncthreads();
-    T t = s_part[0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) t += s_part[w];
+    const int nw = (int)(blockDim.x >> 6);
+#pragma unroll
+    for (int k = 0; k < kQtCols; ++k) {
+        float t = s_part[k];
+        for (int w = 1; w < nw; ++w) t += s_part[w * kQtCols + k];
+        v[k] = t;
+    }
     __syncthreads();
-    return t;
 }
 
 // LAPACK's sgeqr2 + sorg2r on A (rows x n, row-major in q, fp32), streamed by the workgroup: rows
@@ -113,7 +123,8 @@ __device__ void qt_householder(const float *__restrict__ a, int64_t m, int n, fl
         }
         float sum[kQtCols];
 #pragma unroll
-        for (int k = 0; k < kQtCols; ++k) sum[k] = j + k < n ? qt_block_sum(part[k], s_part) : 0.f;
+        for (int k = 0; k < kQtCols; ++k) sum[k] = part[k];
+        qt_block_sums(sum, s_part);
         const float alpha = q[(int64_t)j * n + j];
         const float xnorm = sqrtf(sum[0]);
         float tau = 0.f, beta = alpha, scale = 0.f;
@@ -160,8 +171,9 @@ __device__ void qt_householder(const float *__restrict__ a, int64_t m, int n, fl
                 for (int k = 1; k < kQtCols; ++k)
                     if (j + k < n) part[k] = fmaf(v, q[i * n + j + k], part[k]);
             }
+            qt_block_sums(part, s_part);
 #pragma unroll
-            for (int k = 1; k < kQtCols; ++k) s_w[k] = j + k < n ? qt_block_sum(part[k], s_part) : 0.f;
+            for (int k = 1; k < kQtCols; ++k) s_w[k] = j + k < n ? part[k] : 0.f;
             for (int64_t i = t0; i < m; i += step) {
                 if (i < j) continue;
                 const float v = i == j ? 1.f : q[i * n + j];
@@ -195,7 +207,7 @@ __global__ __launch_bounds__(kQtFactorThreads) void k_qrt_factor(const float *__
 {
     __shared__ double s_red[2][256];
     __shared__ double s_g[256], s_a[256];
-    __shared__ float s_partf[kQtFactorThreads / 64], s_tau[kQtCols], s_w[kQtCols];
+    __shared__ float s_partf[kQtFactorThreads / 64 * kQtCols], s_tau[kQtCols], s_w[kQtCols];
     __shared__ int s_ok;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = g.cols;
@@ -299,7 +311,6 @@ __global__ __launch_bounds__(kQtFactorThreads) void k_qrt_factor(const float *__
                     sg[j] = d >= 0.0 ? 1.0 : -1.0;
                 } else {
                     sg[j] = d >= 0.0 ? -1.0 : 1.0;
-                    ok = ok && ad >= 1e-5;
                     const double inv_u = 1.0 / (d - sg[j]);
 #pragma unroll
                     for (int i = j + 1; i < kQtCols; ++i)
