@@ -34,6 +34,7 @@ namespace {
 constexpr int kQtCols = 16;
 constexpr int kQtGramThreads = 256;  // 4 waves
 constexpr int kQtFactorThreads = 512;
+constexpr int kQtBatch = 8;        // rows a thread loads together in the Householder route's passes
 constexpr int kQtMaxSlices = 32;  // the factor sums the slices' partials: few of them
 typedef double d4 __attribute__((ext_vector_type(4)));
 
@@ -73,60 +74,65 @@ __global__ __launch_bounds__(kQtGramThreads) void k_qrt_gram(const float *__rest
     ws[(size_t)blockIdx.x * 256 + e] = ((s_acc[0][e] + s_acc[1][e]) + s_acc[2][e]) + s_acc[3][e];
 }
 
-// ---- kQtCols values a thread summed over the workgroup in a fixed order (xor tree within the
-// wave, the waves in order), all in one exchange (two barriers); every thread receives the totals.
-// s_part holds kQtCols values a wave.
-__device__ __forceinline__ void qt_block_sums(float (&v)[kQtCols], float *s_part)
+// One value a thread summed over the threads of the same column (lanes c, c + 16, c + 32, c + 48 of
+// every wave: an xor tree over the wave's four row groups, then the waves in order), in one exchange
+// (two barriers).  Every thread receives its column's total and, in *pivot, column j's.  s_part holds
+// 16 values a wave.
+__device__ __forceinline__ float qt_column_sum(float v, int j, float *pivot, float *s_part)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int k = 0; k < kQtCols; ++k)
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) v[k] += __shfl_xor(v[k], off, 64);
-    if (lane == 0)
-#pragma unroll
-        for (int k = 0; k < kQtCols; ++k) s_part[wave * kQtCols + k] = v[k];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, c = lane & 15;
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    if (lane < 16) s_part[wave * 16 + lane] = v;
     __syncthreads();
     const int nw = (int)(blockDim.x >> 6);
-#pragma unroll
-    for (int k = 0; k < kQtCols; ++k) {
-        float t = s_part[k];
-        for (int w = 1; w < nw; ++w) t += s_part[w * kQtCols + k];
-        v[k] = t;
+    float t = s_part[c], tj = s_part[j];
+    for (int w = 1; w < nw; ++w) {
+        t += s_part[w * 16 + c];
+        tj += s_part[w * 16 + j];
     }
     __syncthreads();
+    *pivot = tj;
+    return t;
 }
 
-// LAPACK's sgeqr2 + sorg2r on A (rows x n, row-major in q, fp32), streamed by the workgroup: rows
-// t, t + 512, ... to thread t in every pass (each thread reads back what it wrote, apart from the
-// pivot row), its sums in that order, then over the workgroup.  R into r (n x n, may be NULL), Q left
-// in q.  (LAPACK's rescaling of a reflector whose beta is below the safe minimum is not made: inputs
-// that small fall outside fp32's normal range.)
+// LAPACK's sgeqr2 + sorg2r on A (rows x n, row-major in q, fp32), streamed by the workgroup: thread t
+// takes column t % 16 of rows t / 16, t / 16 + blockDim / 16, ... in every pass, kQtBatch of them
+// loaded together (sixteen consecutive threads read one row's consecutive words), a row's column-j
+// entry passed along its sixteen lanes;
+// each column's sums over its threads' rows in that order, then over the workgroup.  R into r (n x n,
+// may be NULL), Q left in q.  (LAPACK's rescaling of a reflector whose beta is below the safe minimum
+// is not made: inputs that small fall outside fp32's normal range.)
 __device__ void qt_householder(const float *__restrict__ a, int64_t m, int n, float *__restrict__ q,
-                               float *__restrict__ r, float *s_part, float *s_tau, float *s_w)
+                               float *__restrict__ r, float *s_part, float *s_tau)
 {
-    const int64_t t0 = threadIdx.x, step = blockDim.x;
-    for (int64_t i = t0; i < m * n; i += step) q[i] = a[i];
+    const int lane = threadIdx.x & 63, c = lane & 15, base = lane & 48;
+    const int64_t g0 = threadIdx.x >> 4, gstep = blockDim.x >> 4;
+    const bool col = c < n;
+    for (int64_t i = threadIdx.x; i < m * n; i += blockDim.x) q[i] = a[i];
     __syncthreads();
     for (int j = 0; j < n; ++j) {
-        // squared norm of x = A[j+1:, j] and the dots of x with the columns k > j
-        float part[kQtCols];
+        // the squared norm of x = A[j+1:, j] (column j's threads) and the dots of x with the columns
+        // k > j (column k's threads)
+        float part = 0.f;
+        for (int64_t i0 = g0; i0 < m; i0 += kQtBatch * gstep) {
+            float e[kQtBatch];
 #pragma unroll
-        for (int k = 0; k < kQtCols; ++k) part[k] = 0.f;
-        for (int64_t i = t0; i < m; i += step) {
-            if (i <= j) continue;
-            const float x = q[i * n + j];
-            part[0] = fmaf(x, x, part[0]);
+            for (int u = 0; u < kQtBatch; ++u) {
+                const int64_t i = i0 + u * gstep;
+                e[u] = col && i < m ? q[i * n + c] : 0.f;
+            }
 #pragma unroll
-            for (int k = 1; k < kQtCols; ++k)
-                if (j + k < n) part[k] = fmaf(x, q[i * n + j + k], part[k]);
+            for (int u = 0; u < kQtBatch; ++u) {
+                const int64_t i = i0 + u * gstep;
+                const float x = __shfl(e[u], base + j, 64);
+                if (i > j && i < m) part = fmaf(x, e[u], part);
+            }
         }
-        float sum[kQtCols];
-#pragma unroll
-        for (int k = 0; k < kQtCols; ++k) sum[k] = part[k];
-        qt_block_sums(sum, s_part);
+        float norm2;
+        const float dot = qt_column_sum(part, j, &norm2, s_part);
         const float alpha = q[(int64_t)j * n + j];
-        const float xnorm = sqrtf(sum[0]);
+        const float xnorm = sqrtf(norm2);
         float tau = 0.f, beta = alpha, scale = 0.f;
         if (xnorm != 0.f) {  // slarfg: beta = -sign(alpha) * hypot(alpha, xnorm)
             const float h = hypotf(alpha, xnorm);
@@ -134,56 +140,75 @@ __device__ void qt_householder(const float *__restrict__ a, int64_t m, int n, fl
             tau = (beta - alpha) / beta;
             scale = 1.f / (alpha - beta);
         }
-        // w_k = v^T A[:, k] for k > j (v_j = 1, v_i = scale x_i)
-#pragma unroll
-        for (int k = 1; k < kQtCols; ++k) s_w[k] = j + k < n ? q[(int64_t)j * n + j + k] + scale * sum[k] : 0.f;
+        // w_c = v^T A[:, c] for c > j (v_j = 1, v_i = scale x_i)
+        const float wc = col && c > j ? q[(int64_t)j * n + c] + scale * dot : 0.f;
         if (threadIdx.x == 0) s_tau[j] = tau;
-        __syncthreads();
-        for (int64_t i = t0; i < m; i += step) {
-            if (i < j) continue;
-            const float v = i == j ? 1.f : q[i * n + j] * scale;
-            if (tau != 0.f) {
+        __syncthreads();  // (row j is read above and written below)
+        for (int64_t i0 = g0; i0 < m; i0 += kQtBatch * gstep) {
+            float e[kQtBatch];
 #pragma unroll
-                for (int k = 1; k < kQtCols; ++k)
-                    if (j + k < n) q[i * n + j + k] = fmaf(-tau * s_w[k], v, q[i * n + j + k]);
+            for (int u = 0; u < kQtBatch; ++u) {
+                const int64_t i = i0 + u * gstep;
+                e[u] = col && i < m ? q[i * n + c] : 0.f;
             }
-            q[i * n + j] = i == j ? beta : v;  // R[j][j], then the reflector below
+#pragma unroll
+            for (int u = 0; u < kQtBatch; ++u) {
+                const int64_t i = i0 + u * gstep;
+                const float x = __shfl(e[u], base + j, 64);
+                if (i < j || i >= m || !col) continue;
+                const float v = i == j ? 1.f : x * scale;
+                if (c > j && tau != 0.f) q[i * n + c] = fmaf(-tau * wc, v, e[u]);
+                if (c == j) q[i * n + c] = i == j ? beta : v;  // R[j][j], then the reflector below
+            }
         }
         __syncthreads();
     }
     if (r)
         for (int e = threadIdx.x; e < n * n; e += blockDim.x) {
-            const int i = e / n, c = e % n;
-            r[e] = c >= i ? q[(int64_t)i * n + c] : 0.f;
+            const int i = e / n, k = e % n;
+            r[e] = k >= i ? q[(int64_t)i * n + k] : 0.f;
         }
     __syncthreads();
     // sorg2r: from the last reflector to the first
     for (int j = n - 1; j >= 0; --j) {
         const float tau = s_tau[j];
-        if (tau != 0.f && j + 1 < n) {
-            float part[kQtCols];
+        if (tau != 0.f && j + 1 < n) {  // (uniform) H_j on the columns already formed
+            float part = 0.f;
+            for (int64_t i0 = g0; i0 < m; i0 += kQtBatch * gstep) {
+                float e[kQtBatch];
 #pragma unroll
-            for (int k = 0; k < kQtCols; ++k) part[k] = 0.f;
-            for (int64_t i = t0; i < m; i += step) {
-                if (i < j) continue;
-                const float v = i == j ? 1.f : q[i * n + j];
+                for (int u = 0; u < kQtBatch; ++u) {
+                    const int64_t i = i0 + u * gstep;
+                    e[u] = col && i < m ? q[i * n + c] : 0.f;
+                }
 #pragma unroll
-                for (int k = 1; k < kQtCols; ++k)
-                    if (j + k < n) part[k] = fmaf(v, q[i * n + j + k], part[k]);
+                for (int u = 0; u < kQtBatch; ++u) {
+                    const int64_t i = i0 + u * gstep;
+                    const float x = __shfl(e[u], base + j, 64);
+                    if (i >= j && i < m) part = fmaf(i == j ? 1.f : x, e[u], part);
+                }
             }
-            qt_block_sums(part, s_part);
+            float unused;
+            const float dot = qt_column_sum(part, j, &unused, s_part);
+            const float wc = c > j ? dot : 0.f;
+            for (int64_t i0 = g0; i0 < m; i0 += kQtBatch * gstep) {
+                float e[kQtBatch];
 #pragma unroll
-            for (int k = 1; k < kQtCols; ++k) s_w[k] = j + k < n ? part[k] : 0.f;
-            for (int64_t i = t0; i < m; i += step) {
-                if (i < j) continue;
-                const float v = i == j ? 1.f : q[i * n + j];
+                for (int u = 0; u < kQtBatch; ++u) {
+                    const int64_t i = i0 + u * gstep;
+                    e[u] = col && i < m ? q[i * n + c] : 0.f;
+                }
 #pragma unroll
-                for (int k = 1; k < kQtCols; ++k)
-                    if (j + k < n) q[i * n + j + k] = fmaf(-tau * s_w[k], v, q[i * n + j + k]);
+                for (int u = 0; u < kQtBatch; ++u) {
+                    const int64_t i = i0 + u * gstep;
+                    const float x = __shfl(e[u], base + j, 64);
+                    if (i >= j && i < m && col && c > j) q[i * n + c] = fmaf(-tau * wc, i == j ? 1.f : x, e[u]);
+                }
             }
             __syncthreads();
         }
-        for (int64_t i = t0; i < m; i += step) {
+        for (int64_t i = g0; i < m; i += gstep) {  // column j itself
+            if (c != j) continue;
             const float v = q[i * n + j];
             q[i * n + j] = i < j ? 0.f : i == j ? 1.f - tau : -tau * v;
         }
@@ -207,7 +232,7 @@ __global__ __launch_bounds__(kQtFactorThreads) void k_qrt_factor(const float *__
 {
     __shared__ double s_red[2][256];
     __shared__ double s_g[256], s_a[256];
-    __shared__ float s_partf[kQtFactorThreads / 64 * kQtCols], s_tau[kQtCols], s_w[kQtCols];
+    __shared__ float s_partf[kQtFactorThreads / 64 * 16], s_tau[kQtCols];
     __shared__ int s_ok;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = g.cols;
@@ -335,7 +360,7 @@ __global__ __launch_bounds__(kQtFactorThreads) void k_qrt_factor(const float *__
     }
     __syncthreads();
     if (tid == 0) ws[qt_flag_offset(g.slices)] = s_ok ? 1.0 : 0.0;
-    if (!s_ok) qt_householder(a, g.rows, n, q, r, s_partf, s_tau, s_w);  // (uniform)
+    if (!s_ok) qt_householder(a, g.rows, n, q, r, s_partf, s_tau);  // (uniform)
 }
 
 // ---- Q = A M
