@@ -993,13 +993,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
 // For problems large enough to fill the chip with 32-output slabs: one workgroup per (32 outputs,
 // part), every entry of the part a light record (the plan selects no column features).  Wave w
 // owns features 64 w .. 64 w + 63 of the part as four 16-feature tiles, whose records of a block
-// are contiguous (grouped by feature, then by row).  The wave takes them 32 at a time as one
-// chunk: the G rows of the 32 records, gathered by two transposing reads per 16 outputs, are the
-// A operand; for each tile the chunk touches, the records of that tile scatter their values into a
-// zeroed [16 features][32 slots] LDS scratch at (feature in the tile, slot), the scratch read in
-// operand order is the B operand (cleared again after the read), and one v_mfma_f32_16x16x32 per
-// 16 outputs adds G[t_k][o] v_k to (o, feature).  So each wave's work is about its entry count / 32
-// matrix instructions, whatever the spread of the entries over the features, and the sums have a
+// are contiguous (grouped by feature, then by row).  The wave takes each tile's records 32 at a
+// time as one chunk: the G rows of the 32 records, gathered by two transposing reads per 16
+// outputs, are the A operand; the records scatter their values into a zeroed [16 features][32
+// slots] LDS scratch at (feature in the tile, slot), the scratch read in operand order is the B
+// operand (cleared again after the read), and one v_mfma_f32_16x16x32 per 16 outputs adds
+// G[t_k][o] v_k to (o, feature).  So each wave's work is about its entry count / 32 + 4 matrix
+// instructions a block, whatever the spread of the entries over the features, and the sums have a
 // fixed order (chunks in record order, blocks in order).
 constexpr int kWOS = 32;         // outputs per workgroup
 constexpr int kWRecBuf = 3584;   // record words of a stream buffer
@@ -1012,7 +1012,7 @@ struct WideLds {
     static constexpr size_t size = rec + (size_t)kWRecBuf * 4;      // 46 KiB
     static_assert(size % 1024 == 0, "buffers start on 1 KiB boundaries");
     static_assert(kWRecBuf % 256 == 0, "records are staged in 1 KiB copies");
-    static_assert(3 * size + kWaves * 1024 + kMaxBlocks * sizeof(TileHdr) <= 160 * 1024, "fits the CU's LDS");
+    static_assert(3 * size + kWaves * (1024 + 64) + kMaxBlocks * sizeof(TileHdr) <= 160 * 1024, "fits the CU's LDS");
     static_assert(size >= (size_t)kWaves * 2 * 256 * 4, "every wave's two coefficient tiles fit a buffer");
     static_assert(size >= (size_t)kPartMax * 16 * 2, "the part's Q rows fit a buffer");
 };
@@ -1025,6 +1025,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
     __shared__ __attribute__((aligned(1024))) unsigned char lds1[L::size];
     __shared__ __attribute__((aligned(1024))) unsigned char lds2[L::size];
     __shared__ __attribute__((aligned(16))) uint16_t s_bs[kWaves * 512];  // per wave [16 features][32 slots]
+    __shared__ uint16_t s_spare[kWaves * 32];  // per wave, a word each for the lanes whose stores go nowhere
     __shared__ TileHdr s_hdr[kMaxBlocks];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, grp = lane >> 4;
@@ -1117,13 +1118,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
         for (int i = 0; i < 4; ++i) acc[i][j] = acc_m[j];
     }
 
-    // Each chunk is 32 consecutive records of the wave's four tiles (records [b0, b4), grouped by
-    // feature), whatever tiles they belong to.  Lane 16 g + 4 q + h (h = 0, 1) holds the record
+    // Each chunk is up to 32 consecutive records of one of the wave's four tiles (a tile's records
+    // are grouped by feature, the tiles' ranges follow each other).  Lane 16 g + 4 q + h (h = 0, 1) holds the record
     // of slot 8 g + 4 h + q (lanes with h = 2, 3 repeat h = 0, 1): so the quad's first two lanes
     // hold slots k1 = 8 g + q and k1 + 4, the rows this lane's transposing reads need, and
     // every slot < 32 is held once by a lane with h < 2, which scatters its value.
     const uint32_t my = 8u * grp + 4u * (lane & 1) + ((lane >> 2) & 3);  // the slot this lane holds
     const bool scatters = (lane & 2) == 0;
+    uint16_t *spare = s_spare + wave * 32 + 2 * (lane >> 2) + (lane & 1);
     const uint16_t *bsrd_lane = s_bs + wave * 512 + n * 32 + 8 * (grp ^ ((n >> 2) & 3));
     const uint32_t ga_lane = (n & 3) * 4;
 
@@ -1157,14 +1159,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
         const uint16_t *ga = gt + ga_lane;
         // this wave's records in the window
         const uint32_t lo = b0 > w0 ? b0 : w0, hi0 = b4 < w1 ? b4 : w1, hi = hi0 > lo ? hi0 : lo;
-        // one chunk at records [e0, e0 + 32) (slots past hi hold whatever follows: another
-        // wave's record or a stale word of the buffer; they are never scattered, and the G row
-        // they address is in the tile, t & 511): A = the G rows of slots k1 (.. + 3 over the group)
-        // and k1 + 4, per 16 outputs, read once; then for each tile the chunk overlaps, B = the
-        // tile's values at (feature in the tile, slot) of the zeroed scratch (rows of 32 slots, the
-        // four 16-byte groups of a row rotated by the feature's bits 2..3 so that a group's 16
-        // lanes read distinct banks), cleared again after the read, and one product per 16 outputs
-        auto chunk = [&](uint32_t rec, uint32_t e0) {
+        // one chunk of tile i at records [e0, e0 + 32) (slots at or past t_hi hold whatever follows:
+        // the next tile's records or a stale word of the buffer; their lanes store zero, and the G
+        // row they address is in the tile, t & 511): A = the G rows of slots k1 (.. + 3 over the
+        // group) and k1 + 4, per 16 outputs; B = the tile's values at (feature in the tile, slot) of
+        // the zeroed scratch (rows of 32 slots, the four 16-byte groups of a row rotated by the
+        // feature's bits 2..3 so that a group's 16 lanes read distinct banks), cleared again after
+        // the read; one product per 16 outputs.  Every lane stores unconditionally: a lane past
+        // t_hi stores zero at its own slot, which no other lane of the chunk writes and which is
+        // zero already, and the lanes that repeat another's record store into their spare word.
+        auto chunk = [&](f32x4 (&ac)[2], uint32_t rec, uint32_t e0, uint32_t t_hi) {
             const uint32_t r1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)rec, 0x00, 0xf, 0xf, false);
             const uint32_t r2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)rec, 0x55, 0xf, 0xf, false);
             const uint16_t *p1 = ga + (r1 & 511u) * kWOS;
@@ -1173,34 +1177,36 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
             const uint2 lo1 = lds_tr16(p1 + 16), hi1 = lds_tr16(p2 + 16);
             const uint4 a0 = make_uint4(lo0.x, lo0.y, hi0.x, hi0.y), a1 = make_uint4(lo1.x, lo1.y, hi1.x, hi1.y);
             const uint32_t fo = (rec >> 9) & 15u;
-            uint16_t *slot = bs + fo * 32 + 8 * ((my >> 3) ^ ((fo >> 2) & 3u)) + (my & 7);
-            const uint32_t e = e0 + my;
-            const uint32_t e_end = e0 + 32 < hi ? e0 + 32 : hi;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (bb[i + 1] <= e0 || bb[i] >= e_end) continue;  // (wave-uniform)
-                const bool live = scatters && e >= bb[i] && e < bb[i + 1] && e < hi;
-                // The lanes exchange values through the scratch: wavefront-scope fences keep the
-                // compiler from moving one lane's store across another lane's load (a wave's LDS
-                // operations are performed in order, so they cost no wait).
-                if (live) *slot = (uint16_t)(rec >> 16);
-                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-                const uint4 bop = *reinterpret_cast<const uint4 *>(bsrd_lane);
-                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-                if (live) *slot = 0;
-                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-                acc[i][0] = mfma16<DT>(a0, bop, acc[i][0]);
-                acc[i][1] = mfma16<DT>(a1, bop, acc[i][1]);
-            }
+            uint16_t *slot = scatters ? bs + fo * 32 + 8 * ((my >> 3) ^ ((fo >> 2) & 3u)) + (my & 7) : spare;
+            const uint16_t v = e0 + my < t_hi ? (uint16_t)(rec >> 16) : (uint16_t)0;
+            // The lanes exchange values through the scratch: wavefront-scope fences keep the
+            // compiler from moving one lane's store across another lane's load (a wave's LDS
+            // operations are performed in order, so they cost no wait).
+            *slot = v;
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            const uint4 bop = *reinterpret_cast<const uint4 *>(bsrd_lane);
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            *slot = 0;
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            ac[0] = mfma16<DT>(a0, bop, ac[0]);
+            ac[1] = mfma16<DT>(a1, bop, ac[1]);
         };
-        // the chunks in order, the next chunk's record read before the current one runs (index
-        // e - w0 + my <= kWRecCap + 31: inside the buffer)
+        // tile by tile, the tile's records of the window [max(b_i, lo), min(b_i+1, hi)) in chunks,
+        // each chunk's record read before the previous one runs.  The chunks follow each other in
+        // record order (a tile's first record is where the previous tile's ended), so the next
+        // start is always e0 + 32 or the tile's end; its index, at most hi - w0 + 31 <= kWRecCap +
+        // 31, is inside the buffer.
         if (lo < hi) {
             uint32_t nx = recs[lo - w0 + my];
-            for (uint32_t e0 = lo; e0 < hi; e0 += 32) {
-                const uint32_t cur = nx;
-                nx = recs[(e0 + 32 < hi ? e0 + 32 : hi) - w0 + my];
-                chunk(cur, e0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t t_lo = bb[i] > lo ? bb[i] : lo;
+                const uint32_t t_hi = bb[i + 1] < hi ? bb[i + 1] : hi;
+                for (uint32_t e0 = t_lo; e0 < t_hi; e0 += 32) {
+                    const uint32_t cur = nx;
+                    nx = recs[(e0 + 32 < t_hi ? e0 + 32 : t_hi) - w0 + my];
+                    chunk(acc[i], cur, e0, t_hi);
+                }
             }
         }
     };
