@@ -1126,7 +1126,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
     const uint32_t my = 8u * grp + 4u * (lane & 1) + ((lane >> 2) & 3);  // the slot this lane holds
     const bool scatters = (lane & 2) == 0;
     uint16_t *spare = s_spare + wave * 32 + 2 * (lane >> 2) + (lane & 1);
-    const uint16_t *bsrd_lane = s_bs + wave * 512 + n * 32 + 8 * (grp ^ ((n >> 2) & 3));
+    // the scratch row of feature f keeps its four 16-byte slot groups rotated by rot(f): a 16-byte
+    // read is served eight lanes a cycle over 32 banks, and (f & 1, rot(f)) differ across each eight
+    // consecutive features (a rotation by f's bits 2..3 alone gave every read two cycles of conflicts)
+    // rot(f) = f2 | (f1 ^ f2 ^ f3) << 1, two bits a feature of the constant
+    auto rot = [](uint32_t f) { return (0xf50a5fa0u >> (2u * f)) & 3u; };
+    const uint16_t *bsrd_lane = s_bs + wave * 512 + n * 32 + 8 * (grp ^ rot((uint32_t)n));
     const uint32_t ga_lane = (n & 3) * 4;
 
     // the step in buffer B: (window 0) M = G^T [C | 1] over the wave's 32 rows, then the wave's
@@ -1163,9 +1168,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
         // the next tile's records or a stale word of the buffer; their lanes store zero, and the G
         // row they address is in the tile, t & 511): A = the G rows of slots k1 (.. + 3 over the
         // group) and k1 + 4, per 16 outputs; B = the tile's values at (feature in the tile, slot) of
-        // the zeroed scratch (rows of 32 slots, the four 16-byte groups of a row rotated by the
-        // feature's bits 2..3 so that a group's 16 lanes read distinct banks), cleared again after
-        // the read; one product per 16 outputs.  Every lane stores unconditionally: a lane past
+        // the zeroed scratch (rows of 32 slots, the four 16-byte groups of a row rotated by rot(f)),
+        // cleared again after the read; one product per 16 outputs.  Every lane stores unconditionally: a lane past
         // t_hi stores zero at its own slot, which no other lane of the chunk writes and which is
         // zero already, and the lanes that repeat another's record store into their spare word.
         auto chunk = [&](f32x4 (&ac)[2], uint32_t rec, uint32_t e0, uint32_t t_hi) {
@@ -1177,7 +1181,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
             const uint2 lo1 = lds_tr16(p1 + 16), hi1 = lds_tr16(p2 + 16);
             const uint4 a0 = make_uint4(lo0.x, lo0.y, hi0.x, hi0.y), a1 = make_uint4(lo1.x, lo1.y, hi1.x, hi1.y);
             const uint32_t fo = (rec >> 9) & 15u;
-            uint16_t *slot = scatters ? bs + fo * 32 + 8 * ((my >> 3) ^ ((fo >> 2) & 3u)) + (my & 7) : spare;
+            uint16_t *slot = scatters ? bs + fo * 32 + 8 * ((my >> 3) ^ rot(fo)) + (my & 7) : spare;
             const uint16_t v = e0 + my < t_hi ? (uint16_t)(rec >> 16) : (uint16_t)0;
             // The lanes exchange values through the scratch: wavefront-scope fences keep the
             // compiler from moving one lane's store across another lane's load (a wave's LDS
