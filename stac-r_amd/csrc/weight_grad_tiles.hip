@@ -119,11 +119,6 @@ __host__ __device__ inline uint64_t record_words(int64_t nnz, uint64_t regions)
     return (uint64_t)nnz + regions * (uint64_t)(kOffWords + 3) + 3 + kLightCap;
 }
 
-__device__ __forceinline__ int64_t flat_at(const void *idx, int idx64, int64_t k)
-{
-    return idx64 ? static_cast<const int64_t *>(idx)[k] : (int64_t) static_cast<const int32_t *>(idx)[k];
-}
-
 // (token row, feature) of a flat index; rows * d_in < 2^32 (the host checks), so 32-bit division,
 // by the argument block's multiply-high.  An index outside the problem (invalid input) still yields
 // a feature < d_in.
@@ -135,19 +130,52 @@ __device__ __forceinline__ void split_flat(int64_t flat, const TileArgs &a, uint
     f = x - t * (uint32_t)a.d_in;
 }
 
-// The integer code of entry e (bits 4 / 8).
-__device__ __forceinline__ int entry_code(const TileArgs &a, int64_t e)
+// Batched loads of kBatch entries e[k] (each an existing entry): the flat indices, and the product
+// operands (the integer code for bits 4 / 8, or the stored value for bits 0).  The index width and
+// the value encoding are uniform branches outside the unrolled loads, so a thread's loads are all
+// issued before the first result is used (one memory round trip for the batch, not one per load).
+__device__ __forceinline__ void load_flats(const TileArgs &a, const int64_t (&e)[kBatch], int64_t (&out)[kBatch])
 {
-    if (a.bits == 8) return static_cast<const int8_t *>(a.data)[e];
-    const uint32_t b = static_cast<const uint8_t *>(a.data)[e >> 1];
-    const int n = (int)((e & 1) ? (b >> 4) : (b & 0xfu));
-    return n > 7 ? n - 16 : n;
+    if (a.idx64) {
+        const int64_t *p = static_cast<const int64_t *>(a.idx);
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) out[k] = p[e[k]];
+    } else {
+        const int32_t *p = static_cast<const int32_t *>(a.idx);
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) out[k] = (int64_t)p[e[k]];
+    }
 }
 
-// The product operand of entry e: the integer code for bits 4 / 8, or the stored value for bits 0.
-__device__ __forceinline__ float entry_value(const TileArgs &a, int64_t e)
+__device__ __forceinline__ void load_values(const TileArgs &a, const int64_t (&e)[kBatch], float (&out)[kBatch])
 {
-    return a.bits ? (float)entry_code(a, e) : load_any(a.data, a.val_dt, e);
+    if (a.bits == 8) {
+        const int8_t *p = static_cast<const int8_t *>(a.data);
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) out[k] = (float)(int)p[e[k]];
+    } else if (a.bits == 4) {
+        const uint8_t *p = static_cast<const uint8_t *>(a.data);
+        uint32_t byte[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) byte[k] = p[e[k] >> 1];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int n = (int)((e[k] & 1) ? (byte[k] >> 4) : (byte[k] & 0xfu));
+            out[k] = (float)(n > 7 ? n - 16 : n);
+        }
+    } else if (a.val_dt == STACR_DTYPE_F32) {
+        const float *p = static_cast<const float *>(a.data);
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) out[k] = p[e[k]];
+    } else {
+        const uint16_t *p = static_cast<const uint16_t *>(a.data);
+        uint32_t h[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) h[k] = p[e[k]];
+        const bool bf = a.val_dt == STACR_DTYPE_BF16;
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) out[k] = bf ? bf16_bits_to_f(h[k]) : f16_bits_to_f(h[k]);
+    }
 }
 
 // A light record's 16-bit value: an operand in G's dtype, exact for the integer codes; a stored value
@@ -183,13 +211,17 @@ __global__ __launch_bounds__(kThreads) void k_tile_count(TileArgs a)
     };
     // kBatch entries per thread per round, their loads issued together
     for (int64_t r0 = e0; r0 < e1; r0 += kBatch * kThreads) {
-        int64_t cur[kBatch], prev[kBatch];
+        // lanes past e1 load entry e1 - 1 (r0 < e1, so it exists) and skip it below; prev is used
+        // only for e > 0
+        int64_t cur[kBatch], prev[kBatch], ec[kBatch], ep[kBatch];
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
             const int64_t e = r0 + k * kThreads + tid;
-            cur[k] = e < e1 ? flat_at(a.idx, a.idx64, e) : 0;
-            prev[k] = e < e1 && e > 0 ? flat_at(a.idx, a.idx64, e - 1) : 0;
+            ec[k] = e < e1 ? e : e1 - 1;
+            ep[k] = ec[k] > 0 ? ec[k] - 1 : 0;
         }
+        load_flats(a, ec, cur);
+        load_flats(a, ep, prev);
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
             const int64_t e = r0 + k * kThreads + tid;
@@ -318,12 +350,24 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         // and keeps them in registers for both passes below.
         int64_t fl[kBatch];
         float val[kBatch];
+        // (lanes past the block's entries load an existing entry, e_b1 - 1 or 0 as nnz >= 1 here,
+        // and mark it flat -1, value 0)
         auto load_batch = [&](int64_t r0) {
+            int64_t ec[kBatch];
+            const int64_t e_safe = e_b1 > 0 ? e_b1 - 1 : 0;
 #pragma unroll
             for (int k = 0; k < kBatch; ++k) {
                 const int64_t e = r0 + k * kThreads + tid;
-                fl[k] = e < e_b1 ? flat_at(a.idx, a.idx64, e) : -1;
-                val[k] = e < e_b1 ? entry_value(a, e) : 0.f;
+                ec[k] = e < e_b1 ? e : e_safe;
+            }
+            load_flats(a, ec, fl);
+            load_values(a, ec, val);
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                if (r0 + k * kThreads + tid >= e_b1) {
+                    fl[k] = -1;
+                    val[k] = 0.f;
+                }
             }
         };
         const bool one_round = e_b1 - e_b0 <= (int64_t)kBatch * kThreads;
@@ -474,20 +518,32 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
     }
 
     // ---- the block's coefficient operands [C | 1]: (wave w, row group g, column n) holds rows
-    // 32 w + 8 g .. + 7 of column n
+    // 32 w + 8 g .. + 7 of column n.  ncol <= 16 (the host checks), so a thread packs at most
+    // kTB * 16 / kThreads elements: all their loads are issued before the first store, one memory
+    // round trip in place of one per element.
     if (pack_c) {
         auto pack = [&](auto *cp, const auto *c, auto one) {
+            constexpr int kPer = kTB * 16 / kThreads;
             cp += (int64_t)b * kTB * a.ncol;
-            for (int i = tid; i < kTB * a.ncol; i += kThreads) {
+            const int n_el = kTB * a.ncol;
+            uint32_t v[kPer];  // (a register each: 16-bit values merged into shared registers would wait)
+#pragma unroll
+            for (int u = 0; u < kPer; ++u) {
+                const int i = tid + u * kThreads;
                 const int k = i & 7, n = (i >> 3) % a.ncol, wg = (i >> 3) / a.ncol;  // wg = 4 w + g
                 const int64_t t = (int64_t)b * kTB + 8 * wg + k;
-                decltype(one) v = 0;
-                if (t < a.rows) {
-                    if (n < a.rank) v = c[t * a.rank + n];
-                    else if (n == a.bias_col) v = one;
+                v[u] = 0u;
+                if (i < n_el && t < a.rows) {
+                    if (n < a.rank) v[u] = c[t * a.rank + n];
+                    else if (n == a.bias_col) v[u] = one;
                 }
-                cp[i] = v;
             }
+            // every load has landed before the predicated stores, or each store would wait for the
+            // stores before it (on this ISA the vector memory counter counts stores too)
+            __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+            for (int u = 0; u < kPer; ++u)
+                if (tid + u * kThreads < n_el) cp[tid + u * kThreads] = (decltype(one))v[u];
         };
         if (a.g_dt == STACR_DTYPE_F32)
             pack(static_cast<uint32_t *>(a.cp), static_cast<const uint32_t *>(a.coeff), 0x3f800000u);
