@@ -55,6 +55,7 @@ constexpr int kChunks = 16;          // entry chunks of the feature count
 constexpr int kMaxFeat = 8192;       // input features the count kernel's LDS histogram holds
 constexpr int kMaxBlocks = 256;      // blocks per problem (rows <= 131072): headers held in LDS
 constexpr int kBatch = 8;            // entries per thread whose loads the count and the plan issue together
+constexpr int kRounds = 3;           // rounds of kBatch entries a thread the plan keeps in registers between its passes
 
 static_assert(kThreads == 2 * kTB, "two G tile rows per lane pair: one 16-byte copy per lane");
 static_assert(kTB == kCensusRows, "a save's entry census gives the first entry of every block");
@@ -370,8 +371,10 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
                 }
             }
         };
-        const bool one_round = e_b1 - e_b0 <= (int64_t)kBatch * kThreads;
-        if (one_round) load_batch(e_b0);
+        // the first round is loaded here, so that its latency overlaps the column selection; blocks of
+        // at most kRounds rounds keep their part's light entries in registers for the second pass
+        const bool cached = e_b1 - e_b0 <= (int64_t)kRounds * kBatch * kThreads;
+        load_batch(e_b0);
 
         // ---- column features: the kNC largest of the unique keys count << 16 | (65535 - f) over the
         // features with entries (count clamped to 65535): every feature with a clamped count above the
@@ -387,7 +390,13 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         if (a.columns) {  // (uniform; without column features every entry is a light record)
             if (tid < 256) s_h[tid] = 0u;
             __syncthreads();
-            if (cnt) atomicAdd(&s_h[cnt >> 8], 1u);
+            {   // most features have fewer than 256 entries: bin 0 is added once per wave (a ballot
+                // count), not once per lane, which would serialize about a thousand same-address atomics
+                const bool low = cnt != 0u && (cnt >> 8) == 0u;
+                const uint64_t lowm = __ballot(low);
+                if (cnt != 0u && !low) atomicAdd(&s_h[cnt >> 8], 1u);
+                if ((tid & 63) == 0 && lowm) atomicAdd(&s_h[0], (uint32_t)__popcll(lowm));
+            }
             __syncthreads();
             const int2 l1 = select_bin256(s_h, (uint32_t)kNC, &s_sel);
             uint32_t c64 = 0u, take_eq = 0u;  // (fewer than kNC features with entries: all of them, c64 = 0)
@@ -437,26 +446,52 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
             return flat >= 0 && tl64 >= 0 && tl64 < kTB;
         };
         uint32_t before_part = 0;  // entries of this block in lower parts: where the part's records start
-        // (one round: each light entry of the part as row | feature << 9, else ~0, for the second pass)
+        // entry k of the loaded round: its column operand, or its light-row bit; a light entry of the
+        // part is returned as row | feature << 9 with its record value, else ~0
         static_assert(kTB == 1 << 9, "a block row in 9 bits");
-        uint32_t pk[kBatch];
-        for (int64_t r0 = e_b0; r0 < e_b1; r0 += kBatch * kThreads) {
-            if (!one_round) load_batch(r0);
+        auto first_entry = [&](int k, uint32_t &pko, uint32_t &v16) {
+            pko = ~0u;
+            v16 = 0u;
+            int tl;
+            int64_t f;
+            if (!place(fl[k], tl, f)) return;
+            before_part += f < 0;
+            if (f < 0 || f >= pw) return;
+            const int s = s_slot[f];
+            if (s >= 0) {
+                if constexpr (BT8) s_bt[s * kBtStride + tl] = (BE)(uint8_t)(int8_t)(int)val[k];
+                else s_bt[s * kBtStride + tl] = (BE)to_g16(val[k], a.g_dt);
+            } else {
+                atomicOr(&s_mask[(tl >> 5) * kPartMax + f], 1u << (tl & 31));
+                pko = (uint32_t)tl | ((uint32_t)f << 9);
+                v16 = to_g16(val[k], a.g_dt);
+            }
+        };
+        uint32_t pk[kRounds][kBatch];      // (cached) light entries as row | feature << 9, else ~0
+        uint32_t pv[kRounds][kBatch / 2];  // (cached) their record values, two a word
+        if (cached) {
 #pragma unroll
-            for (int k = 0; k < kBatch; ++k) {
-                pk[k] = ~0u;
-                int tl;
-                int64_t f;
-                if (!place(fl[k], tl, f)) continue;
-                before_part += f < 0;
-                if (f < 0 || f >= pw) continue;
-                const int s = s_slot[f];
-                if (s >= 0) {
-                    if constexpr (BT8) s_bt[s * kBtStride + tl] = (BE)(uint8_t)(int8_t)(int)val[k];
-                    else s_bt[s * kBtStride + tl] = (BE)to_g16(val[k], a.g_dt);
-                } else {
-                    atomicOr(&s_mask[(tl >> 5) * kPartMax + f], 1u << (tl & 31));
-                    pk[k] = (uint32_t)tl | ((uint32_t)f << 9);
+            for (int rr = 0; rr < kRounds; ++rr) {
+                const int64_t r0 = e_b0 + (int64_t)rr * kBatch * kThreads;
+                if (rr > 0 && r0 < e_b1) load_batch(r0);  // (uniform)
+#pragma unroll
+                for (int k = 0; k < kBatch; k += 2) {
+                    uint32_t v0 = 0u, v1 = 0u;
+                    pk[rr][k] = pk[rr][k + 1] = ~0u;
+                    if (r0 < e_b1) {
+                        first_entry(k, pk[rr][k], v0);
+                        first_entry(k + 1, pk[rr][k + 1], v1);
+                    }
+                    pv[rr][k / 2] = v0 | (v1 << 16);
+                }
+            }
+        } else {
+            for (int64_t r0 = e_b0; r0 < e_b1; r0 += kBatch * kThreads) {
+                if (r0 != e_b0) load_batch(r0);
+#pragma unroll
+                for (int k = 0; k < kBatch; ++k) {
+                    uint32_t unused0, unused1;
+                    first_entry(k, unused0, unused1);
                 }
             }
         }
@@ -487,24 +522,33 @@ __global__ __launch_bounds__(kThreads) void k_tile_plan(TileArgs a)
         s_key[tid] = tid < pw ? off : 0u;
         __syncthreads();
         // each light entry at its feature's offset + the feature's light entries in earlier rows
-        // (a block whose entries fit one round has them in registers already)
-        for (int64_t r0 = e_b0; r0 < e_b1; r0 += kBatch * kThreads) {
-            if (!one_round) load_batch(r0);
+        // (blocks of at most kRounds rounds have them in registers already)
+        auto write_record = [&](int tl, int64_t f, uint32_t v16) {
+            const int w = tl >> 5;
+            uint32_t r = s_pre[(w >> 1) * kPartMax + f] + __popc(s_mask[w * kPartMax + f] & ((1u << (tl & 31)) - 1u));
+            if (w & 1) r += __popc(s_mask[(w - 1) * kPartMax + f]);
+            reg[kOffWords + s_key[f] + r] = (uint32_t)tl | ((uint32_t)(f & 15) << 9) | (v16 << 16);
+        };
+        if (cached) {
 #pragma unroll
-            for (int k = 0; k < kBatch; ++k) {
-                int tl;
-                int64_t f;
-                if (one_round) {
-                    if (pk[k] == ~0u) continue;
-                    tl = (int)(pk[k] & (kTB - 1));
-                    f = (int64_t)(pk[k] >> 9);
-                } else if (!place(fl[k], tl, f) || f < 0 || f >= pw || s_slot[f] >= 0) {
-                    continue;
+            for (int rr = 0; rr < kRounds; ++rr) {
+#pragma unroll
+                for (int k = 0; k < kBatch; ++k) {
+                    if (pk[rr][k] == ~0u) continue;
+                    write_record((int)(pk[rr][k] & (kTB - 1)), (int64_t)(pk[rr][k] >> 9),
+                                 (pv[rr][k / 2] >> (16 * (k & 1))) & 0xffffu);
                 }
-                const int w = tl >> 5;
-                uint32_t r = s_pre[(w >> 1) * kPartMax + f] + __popc(s_mask[w * kPartMax + f] & ((1u << (tl & 31)) - 1u));
-                if (w & 1) r += __popc(s_mask[(w - 1) * kPartMax + f]);
-                reg[kOffWords + s_key[f] + r] = (uint32_t)tl | ((uint32_t)(f & 15) << 9) | (to_g16(val[k], a.g_dt) << 16);
+            }
+        } else {
+            for (int64_t r0 = e_b0; r0 < e_b1; r0 += kBatch * kThreads) {
+                load_batch(r0);
+#pragma unroll
+                for (int k = 0; k < kBatch; ++k) {
+                    int tl;
+                    int64_t f;
+                    if (!place(fl[k], tl, f) || f < 0 || f >= pw || s_slot[f] >= 0) continue;
+                    write_record(tl, f, to_g16(val[k], a.g_dt));
+                }
             }
         }
         // the column operands in lane order: (tile i, wave w, lane l) holds rows 32 w + 8 (l / 16)
