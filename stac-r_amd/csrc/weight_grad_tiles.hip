@@ -56,6 +56,8 @@ constexpr int kMaxFeat = 8192;       // input features the count kernel's LDS hi
 constexpr int kMaxBlocks = 256;      // blocks per problem (rows <= 131072): headers held in LDS
 constexpr int kBatch = 8;            // entries per thread whose loads the count and the plan issue together
 constexpr int kRounds = 3;           // rounds of kBatch entries a thread the plan keeps in registers between its passes
+constexpr int kMaxRowSplit = 8;     // (no entries) workgroups over the rows of one o-slab, at most
+constexpr int kSplitTargetWgs = 1024;  // rows are split until this many workgroups: two rounds of two a CU
 
 static_assert(kThreads == 2 * kTB, "two G tile rows per lane pair: one 16-byte copy per lane");
 static_assert(kTB == kCensusRows, "a save's entry census gives the first entry of every block");
@@ -96,6 +98,8 @@ struct TileArgs {
     TileHdr *hdr;       // [n_blocks][n_parts]
     int32_t *colmap;    // [n_parts][kNC] feature in the part, or -1
     int sparse;         // nnz > 0: the plan builds the entry structures
+    int row_split;      // (no entries) workgroups over the rows of one o-slab; above 1 their M tiles go to mpart
+    float *mpart;       // [o-slabs][row_split][256] the row ranges' M tiles (k_tile_lr_finish sums them)
     int columns;        // the plan picks kNC column features per part (0: every entry is a light record)
     // division by d_in as a multiply-high and shifts (Granlund and Montgomery, "Division by invariant
     // integers using multiplication", 1994, figure 4.1): exact for every 32-bit dividend
@@ -704,6 +708,32 @@ struct TileLds {
     static_assert(size >= (size_t)kWaves * 256 * 4, "one tile of every wave fits a buffer (the reduction)");
 };
 
+// dW row i's outputs o0 .. o0 + 15, rounded once to dW's dtype: Conv1D (transposed, dW d_in x d_out)
+// as two 16-byte words, nn.Linear (dW d_out x d_in) one value per output row.
+__device__ __forceinline__ void store_dw_row(const TileArgs &a, int64_t i, int64_t o0, const float (&out)[kOS])
+{
+    if (a.transposed) {  // Conv1D: dW is d_in x d_out, 16 consecutive outputs per thread
+        if (a.dw_dt == STACR_DTYPE_F32) {
+            float4 *dst = reinterpret_cast<float4 *>(static_cast<float *>(a.dw) + i * a.d_out + o0);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) dst[k] = make_float4(out[4 * k], out[4 * k + 1], out[4 * k + 2], out[4 * k + 3]);
+        } else {
+            const bool bf = a.dw_dt == STACR_DTYPE_BF16;
+            uint32_t wv[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                wv[k] = bf ? (f_to_bf16_bits(out[2 * k]) | (f_to_bf16_bits(out[2 * k + 1]) << 16))
+                           : (f_to_f16_bits(out[2 * k]) | (f_to_f16_bits(out[2 * k + 1]) << 16));
+            uint4 *dst = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.dw) + i * a.d_out + o0);
+            dst[0] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+            dst[1] = make_uint4(wv[4], wv[5], wv[6], wv[7]);
+        }
+    } else {  // nn.Linear: dW is d_out x d_in; consecutive threads write consecutive features
+#pragma unroll
+        for (int o = 0; o < kOS; ++o) store_any(a.dw, a.dw_dt, (o0 + o) * a.d_in + i, out[o]);
+    }
+}
+
 // Without entries the buffers are small and two workgroups share a CU: 8 waves per SIMD, so
 // <= 64 VGPRs.  fp32 G (entries with 4 / 8-bit codes only) runs v_mfma_f32_16x16x4_f32: eight
 // products a tile over the same 32 rows a wave takes, row 32 w + 8 (lane / 16) + s in step s, so the
@@ -734,11 +764,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
     const int nwg = gridDim.x;
     int logical = blockIdx.x;
     if (nwg % 8 == 0) logical = (blockIdx.x % 8) * (nwg / 8) + blockIdx.x / 8;
+    // without entries the rows may be split over row_split workgroups per o-slab (slab-major, so
+    // that neighbouring slabs, which read the same G lines, still meet in one L2): this one takes
+    // blocks bb .. bb + nb - 1 and leaves its M tile for k_tile_lr_finish
+    const int split = SP ? 0 : logical / (nwg / a.row_split);
+    if constexpr (!SP) logical -= split * (nwg / a.row_split);
     const int part = logical % a.n_parts;
     const int64_t o0 = (int64_t)(logical / a.n_parts) * kOS;
     const int64_t plo = (int64_t)part * a.part_w;
     const int pw = (int)(a.d_in - plo < a.part_w ? a.d_in - plo : a.part_w);
-    const int nb = a.n_blocks;
+    const int bb = SP ? 0 : (int)((int64_t)split * a.n_blocks / a.row_split);
+    const int nb = SP ? a.n_blocks : (int)((int64_t)(split + 1) * a.n_blocks / a.row_split) - bb;
 
     const int n = lane & 15, grp = lane >> 4;
 
@@ -758,8 +794,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
     const uint32_t cp_lane = ((wave * 4u + grp) * a.ncol + n) * 8 * GB;       // coefficient operand
     const uint32_t bt_lane = (wave * 64u + lane) * sizeof(BW);                // column operand
     const bool has_c = n < a.ncol;
-    const uint32_t regions = (uint32_t)nb * (uint32_t)a.n_parts;
-    const __amdgpu_buffer_rsrc_t r_cp = make_rsrc(a.cp, (uint64_t)nb * kTB * a.ncol * GB);
+    const uint32_t regions = (uint32_t)a.n_blocks * (uint32_t)a.n_parts;
+    const __amdgpu_buffer_rsrc_t r_cp = make_rsrc(a.cp, (uint64_t)a.n_blocks * kTB * a.ncol * GB);  // (every block's)
     // (without entries these three are empty resources that nothing reads)
     const __amdgpu_buffer_rsrc_t r_light = make_rsrc(a.light, SP ? record_words(a.nnz, regions) * 4 : 0);
     const __amdgpu_buffer_rsrc_t r_bt = make_rsrc(a.bt, SP ? (uint64_t)regions * NT * kWaves * 64 * sizeof(BW) : 0);
@@ -779,10 +815,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
     };
     auto issue_g = [&](int blk, unsigned char *B) {
         // rows past the end repeat the last (their operands are zero)
-        const uint32_t rows_here = (uint32_t)(a.rows - (int64_t)blk * kTB) < (uint32_t)kTB
-                                       ? (uint32_t)(a.rows - (int64_t)blk * kTB) : (uint32_t)kTB;
+        const int64_t gb = (int64_t)(blk + bb);  // the block's index in the problem
+        const uint32_t rows_here = (uint32_t)(a.rows - gb * kTB) < (uint32_t)kTB
+                                       ? (uint32_t)(a.rows - gb * kTB) : (uint32_t)kTB;
         const __amdgpu_buffer_rsrc_t r_g =
-            make_rsrc(static_cast<const char *>(a.g) + (size_t)blk * kTB * row_bytes, (uint64_t)rows_here * row_bytes);
+            make_rsrc(static_cast<const char *>(a.g) + (size_t)gb * kTB * row_bytes, (uint64_t)rows_here * row_bytes);
 #pragma unroll
         for (int h = 0; h < GB / 2; ++h) {
             const uint32_t row = g_lane_row + 256u * h;
@@ -800,7 +837,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
 #pragma unroll
         for (int h = 0; h < GB / 2; ++h) {
             r.c[h] = make_uint4(0u, 0u, 0u, 0u);
-            if (has_c) r.c[h] = load16(r_cp, cp_lane + 16u * h, (uint32_t)blk * kTB * a.ncol * GB);
+            if (has_c) r.c[h] = load16(r_cp, cp_lane + 16u * h, (uint32_t)(blk + bb) * kTB * a.ncol * GB);
         }
         if constexpr (SP) {
             const uint32_t base = ((uint32_t)blk * a.n_parts + part) * (uint32_t)(NT * kWaves * 64 * sizeof(BW));
@@ -1029,6 +1066,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
     }
     __syncthreads();
 
+    if constexpr (!SP) {
+        if (a.row_split > 1) {  // (uniform) this row range's M tile, summed over the splits later
+            if (tid < 256) a.mpart[((int64_t)(o0 / kOS) * a.row_split + split) * 256 + tid] = fin[tid];
+            return;
+        }
+    }
+
     // ---- dW tile: M Q^T + scale (light + column sums), one rounding; dbias from M[:, bias_col].
     // With entries a part has <= 1024 features, one per thread (thread f finishes feature f); 16-bit
     // Q rows are in s_q already.  Otherwise the Q rows of a chunk of features are first copied to
@@ -1064,29 +1108,65 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SP ? 4
 #pragma unroll
             for (int o = 0; o < kOS; ++o) out[o] = fmaf(fin[o * 16 + j], qj, out[o]);
         }
-        if (a.transposed) {  // Conv1D: dW is d_in x d_out, 16 consecutive outputs per thread
-            if (a.dw_dt == STACR_DTYPE_F32) {
-                float4 *dst = reinterpret_cast<float4 *>(static_cast<float *>(a.dw) + i * a.d_out + o0);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) dst[k] = make_float4(out[4 * k], out[4 * k + 1], out[4 * k + 2], out[4 * k + 3]);
-            } else {
-                const bool bf = a.dw_dt == STACR_DTYPE_BF16;
-                uint32_t wv[8];
-#pragma unroll
-                for (int k = 0; k < 8; ++k)
-                    wv[k] = bf ? (f_to_bf16_bits(out[2 * k]) | (f_to_bf16_bits(out[2 * k + 1]) << 16))
-                               : (f_to_f16_bits(out[2 * k]) | (f_to_f16_bits(out[2 * k + 1]) << 16));
-                uint4 *dst = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.dw) + i * a.d_out + o0);
-                dst[0] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
-                dst[1] = make_uint4(wv[4], wv[5], wv[6], wv[7]);
-            }
-        } else {  // nn.Linear: dW is d_out x d_in; consecutive threads write consecutive features
-#pragma unroll
-            for (int o = 0; o < kOS; ++o) store_any(a.dw, a.dw_dt, (o0 + o) * a.d_in + i, out[o]);
-        }
+        store_dw_row(a, i, o0, out);
         }
     }
     if (a.dbias && part == 0 && tid < kOS) store_any(a.dbias, a.db_dt, o0 + tid, fin[tid * 16 + a.bias_col]);
+}
+
+// ------------------------------------------------------------------ row-split finish (no entries)
+// Without entries, the rows of an o-slab may be split over row_split workgroups of k_tile_grad,
+// each leaving its M tile (Gᵀ[C | 1] over its rows) in mpart.  One workgroup per (o-slab, 256 input
+// features): M = the tiles summed in row-range order, then dW = M Qᵀ rounded once, as k_tile_grad's
+// epilogue computes it, and dbias from M's bias column.
+template <int DT>
+__global__ __launch_bounds__(256) void k_tile_lr_finish(TileArgs a)
+{
+    __shared__ float s_m[256];
+    const int tid = threadIdx.x;
+    // workgroup -> (o-slab, chunk of 256 features), slabs fastest; consecutive logical ids share an
+    // XCD (ids are dealt to the 8 XCDs round-robin), so the 32-byte pieces neighbouring slabs write
+    // into one Conv1D dW row meet in one L2
+    const int nwg = gridDim.x, n_slabs = (int)(a.d_out / kOS);
+    const int logical = nwg % 8 == 0 ? (blockIdx.x % 8) * (nwg / 8) + blockIdx.x / 8 : blockIdx.x;
+    const int64_t slab = logical % n_slabs, o0 = slab * kOS, chunk = logical / n_slabs;
+    const int64_t i = chunk * 256 + tid;
+    const bool live = i < a.d_in && a.rank > 0;
+    // this thread's Q row (rank < 16 values), loaded first so that its latency overlaps the M
+    // tiles': unconditional loads of the row's own values, index clamped (a branch per load would
+    // make each wait for the one before)
+    const uint16_t *q = static_cast<const uint16_t *>(a.q) + (live ? i : 0) * a.rank;
+    uint32_t qv[16];
+    if (a.rank > 0) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) qv[j] = q[j < a.rank ? j : a.rank - 1];
+    }
+    // M: the slab's row-range tiles summed in range order
+    const float *mp = a.mpart + slab * a.row_split * 256;
+    float v[kMaxRowSplit];
+#pragma unroll
+    for (int r = 0; r < kMaxRowSplit; ++r) v[r] = r < a.row_split ? mp[r * 256 + tid] : 0.f;
+    float m = v[0];
+#pragma unroll
+    for (int r = 1; r < kMaxRowSplit; ++r)
+        if (r < a.row_split) m += v[r];
+    s_m[tid] = m;
+    __syncthreads();
+    if (chunk == 0 && a.dbias && tid < kOS) store_any(a.dbias, a.db_dt, o0 + tid, s_m[tid * 16 + a.bias_col]);
+    if (i >= a.d_in) return;
+    // dW[i][o0 .. o0 + 15] = sum_j M[o][j] Q[i][j] in j order, rounded once
+    float out[kOS];
+#pragma unroll
+    for (int o = 0; o < kOS; ++o) out[o] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        if (j < a.rank) {
+            const float qj = g16_to_f<DT>(qv[j]);
+#pragma unroll
+            for (int o = 0; o < kOS; ++o) out[o] = fmaf(s_m[o * 16 + j], qj, out[o]);
+        }
+    }
+    store_dw_row(a, i, o0, out);
 }
 
 // ------------------------------------------------------------------ the wide streaming kernel
@@ -1430,6 +1510,7 @@ struct TileGeom {
     int gb;  // bytes of a G / C element
     bool sparse, bt8;
     bool wide;  // k_tile_wide (every entry a light record, no column operands) in place of k_tile_grad
+    int row_split;  // (no entries) k_tile_grad workgroups over the rows of one o-slab
 };
 
 // Workgroups of the wide kernel that make it the better choice: at least one per CU (256) with
@@ -1460,12 +1541,19 @@ bool tile_geom(const StacrGradArgs &a, TileGeom *g)
     g->sparse = a.nnz > 0;
     g->bt8 = a.bits != 0;
     g->wide = g->sparse && !f32 && a.d_out % kWOS == 0 && (a.d_out / kWOS) * g->n_parts >= kWideMinWgs;
+    // without entries a workgroup's results are its M tile alone, so the rows of each o-slab are
+    // split (at least two blocks a workgroup) until the launch fills the chip evenly; the tiles are
+    // summed in a fixed order by k_tile_lr_finish
+    g->row_split = 1;
+    while (!g->sparse && g->row_split < kMaxRowSplit && (a.d_out / kOS) * g->row_split < kSplitTargetWgs &&
+           g->n_blocks >= 4 * g->row_split)
+        g->row_split *= 2;
     return true;
 }
 
-enum { TW_HIST, TW_BSTART, TW_CP, TW_BT, TW_LIGHT, TW_HDR, TW_COLMAP, TW_N };
+enum { TW_HIST, TW_BSTART, TW_CP, TW_BT, TW_LIGHT, TW_HDR, TW_COLMAP, TW_MPART, TW_N };
 
-size_t tile_layout(int64_t nnz, int64_t d_in, const TileGeom &g, size_t *off)
+size_t tile_layout(int64_t nnz, int64_t d_in, int64_t d_out, const TileGeom &g, size_t *off)
 {
     size_t cur = 0;
     auto take = [&](int slot, size_t bytes) { off[slot] = cur; cur += (bytes + 255) & ~(size_t)255; };
@@ -1479,6 +1567,7 @@ size_t tile_layout(int64_t nnz, int64_t d_in, const TileGeom &g, size_t *off)
     take(TW_LIGHT, g.sparse ? (size_t)record_words(nnz, regions) * 4 : 0);
     take(TW_HDR, g.sparse ? regions * sizeof(TileHdr) : 0);
     take(TW_COLMAP, g.sparse ? (size_t)g.n_parts * kNC * 4 : 0);
+    take(TW_MPART, g.row_split > 1 ? (size_t)(d_out / kOS) * g.row_split * 256 * 4 : 0);
     return cur;
 }
 
@@ -1508,7 +1597,7 @@ size_t stacr_tiles_ws(const StacrGradArgs &a)
 {
     TileGeom g;
     size_t off[TW_N];
-    return tile_geom(a, &g) ? tile_layout(a.nnz, a.d_in, g, off) : 0;
+    return tile_geom(a, &g) ? tile_layout(a.nnz, a.d_in, a.d_out, g, off) : 0;
 }
 
 size_t stacr_tiles_ws_bound(int64_t rows, int64_t d_out, int64_t d_in, int64_t nnz)
@@ -1524,8 +1613,9 @@ size_t stacr_tiles_ws_bound(int64_t rows, int64_t d_out, int64_t d_in, int64_t n
     g.sparse = nnz > 0;
     g.bt8 = false;  // the wider column-operand form
     g.wide = false;  // (with column operands: the larger layout)
+    g.row_split = nnz > 0 ? 1 : kMaxRowSplit;  // (the most M tiles)
     size_t off[TW_N];
-    return tile_layout(nnz, d_in, g, off);
+    return tile_layout(nnz, d_in, d_out, g, off);
 }
 
 int stacr_tiles_launch(const StacrGradArgs &a)
@@ -1533,7 +1623,7 @@ int stacr_tiles_launch(const StacrGradArgs &a)
     TileGeom g;
     if (!tile_geom(a, &g)) return stacr_fail(STACR_ERR_UNSUPPORTED, "stacr_weight_grad: matrix-core path not applicable");
     size_t off[TW_N];
-    const size_t need = tile_layout(a.nnz, a.d_in, g, off);
+    const size_t need = tile_layout(a.nnz, a.d_in, a.d_out, g, off);
     if (a.workspace_bytes < need)
         return stacr_fail(STACR_ERR_WORKSPACE, "stacr_weight_grad: workspace has %zu bytes, needs %zu", a.workspace_bytes,
                           need);
@@ -1578,6 +1668,8 @@ int stacr_tiles_launch(const StacrGradArgs &a)
         t.colmap = reinterpret_cast<int32_t *>(ws + off[TW_COLMAP]);
     }
     t.sparse = g.sparse ? 1 : 0;
+    t.row_split = g.row_split;
+    t.mpart = reinterpret_cast<float *>(ws + off[TW_MPART]);
     t.columns = g.wide ? 0 : 1;
     div_magic((uint32_t)a.d_in, &t.div_m, &t.div_s1, &t.div_s2);
     hipStream_t s = a.stream;
@@ -1600,8 +1692,15 @@ int stacr_tiles_launch(const StacrGradArgs &a)
             stacr_launch("k_tile_wide", s, [&] { k_tile_wide<STACR_DTYPE_F16><<<nw, kThreads, 0, s>>>(t); });
         return stacr_hip_check(hipGetLastError(), "weight_grad wide matrix-core kernel");
     }
-    const int nwg = (int)(a.d_out / kOS) * g.n_parts;
+    const int nwg = (int)(a.d_out / kOS) * g.n_parts * g.row_split;
     if (a.dtype == STACR_DTYPE_F32) return launch_tile_grad<STACR_DTYPE_F32, true, true>(t, nwg, s);
-    return a.dtype == STACR_DTYPE_BF16 ? launch_tile_grad_dt<STACR_DTYPE_BF16>(t, g, nwg, s)
-                                       : launch_tile_grad_dt<STACR_DTYPE_F16>(t, g, nwg, s);
+    rc = a.dtype == STACR_DTYPE_BF16 ? launch_tile_grad_dt<STACR_DTYPE_BF16>(t, g, nwg, s)
+                                     : launch_tile_grad_dt<STACR_DTYPE_F16>(t, g, nwg, s);
+    if (rc || g.row_split == 1) return rc;
+    const unsigned fgrid = (unsigned)((a.d_out / kOS) * ((a.d_in + 255) / 256));
+    if (a.dtype == STACR_DTYPE_BF16)
+        stacr_launch("k_tile_lr_finish", s, [&] { k_tile_lr_finish<STACR_DTYPE_BF16><<<fgrid, 256, 0, s>>>(t); });
+    else
+        stacr_launch("k_tile_lr_finish", s, [&] { k_tile_lr_finish<STACR_DTYPE_F16><<<fgrid, 256, 0, s>>>(t); });
+    return stacr_hip_check(hipGetLastError(), "weight_grad row-split finish");
 }
