@@ -328,6 +328,10 @@ GRAD_CASES = [
     ("cfg3_cfc_bf16_conv1d_full", 8192, 1024, 4096, 8, "bf16", True, 8, "global_topk", 0.005, True),
     ("cfg3_cproj_bf16_conv1d_full", 8192, 4096, 1024, 8, "bf16", True, 8, "global_topk", 0.005, True),
     ("cfg2_turbo_bf16_full", 8192, 1280, 5120, 8, "bf16", False, 8, "chunk_topk", 0.0, False),
+    # no residual, the rows of each output slab split over two workgroups: 2900 rows are 6 blocks
+    # (3 + 3, the last one partial) over 25 slabs (no XCD remap), 2100 rows 5 blocks (2 + 3)
+    ("turbo_split_ragged_bf16_conv1d", 2900, 300, 400, 5, "bf16", True, 8, "chunk_topk", 0.0, False),
+    ("turbo_split_ragged_f16", 2100, 130, 160, 7, "f16", False, 8, "chunk_topk", 0.0, False),
     ("cfg3_cfc_bf16_conv1d", 2048, 1024, 4096, 8, "bf16", True, 8, "global_topk", 0.005, False),
     ("fp32_bits0", 512, 256, 384, 4, "f32", False, 0, "chunk_topk", 0.02, False),
     ("fp32_bits4_conv1d_rank5", 1100, 300, 160, 5, "f32", True, 4, "chunk_topk", 0.02, True),
